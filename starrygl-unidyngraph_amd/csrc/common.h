@@ -1,0 +1,98 @@
+// Shared helpers for the MI355X (gfx950) CTDG kernels: C-ABI error state,
+// launch checks and wave64 scan primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../../include/starrygl_mi355x.h"
+
+namespace sgl {
+
+// Thread-local last error (read through sgl_last_error()).
+void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+constexpr int kWave = 64;
+
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+
+// Carves aligned sub-buffers out of a caller-provided workspace.
+struct Carver {
+  char *base;
+  size_t used = 0;
+  explicit Carver(void *p) : base(static_cast<char *>(p)) {}
+  template <typename T>
+  T *take(size_t count) {
+    T *p = reinterpret_cast<T *>(base ? base + used : nullptr);
+    used = align_up(used + count * sizeof(T));
+    return p;
+  }
+};
+
+// Inclusive scan across one 64-lane wavefront.
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_scan(T v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    T n = __shfl_up(v, d, kWave);
+    if (lane >= d) v += n;
+  }
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_reduce_sum(T v) {
+#pragma unroll
+  for (int d = kWave / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// Exclusive scan across a block of BLOCK threads (BLOCK a multiple of 64).
+// s_wave must hold BLOCK/64 elements. Returns the exclusive prefix and the
+// block total. Contains two __syncthreads(): call from uniform control flow.
+template <typename T, int BLOCK>
+__device__ __forceinline__ T block_exclusive_scan(T v, T *s_wave, T &total) {
+  static_assert(BLOCK % kWave == 0, "block must be whole waves");
+  constexpr int W = BLOCK / kWave;
+  const T inc = wave_inclusive_scan(v);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int w = threadIdx.x / kWave;
+  if (lane == kWave - 1) s_wave[w] = inc;
+  __syncthreads();
+  T before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < W; ++i) {
+    const T s = s_wave[i];
+    before += (i < w) ? s : T(0);
+    tot += s;
+  }
+  total = tot;
+  __syncthreads();
+  return before + inc - v;
+}
+
+}  // namespace sgl
+
+#define SGL_CHECK_HIP(expr)                                                    \
+  do {                                                                         \
+    hipError_t e_ = (expr);                                                    \
+    if (e_ != hipSuccess) {                                                    \
+      sgl::set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),   \
+                     __FILE__, __LINE__);                                      \
+      return SGL_ERR_HIP;                                                      \
+    }                                                                          \
+  } while (0)
+
+#define SGL_CHECK_LAUNCH() SGL_CHECK_HIP(hipGetLastError())
+
+#define SGL_REQUIRE(cond, ...)                                                 \
+  do {                                                                         \
+    if (!(cond)) {                                                             \
+      sgl::set_error(__VA_ARGS__);                                             \
+      return SGL_ERR_INVALID;                                                  \
+    }                                                                          \
+  } while (0)

@@ -1,0 +1,242 @@
+// Recent-k temporal neighbour sampling over the device CSR (the GPU
+// counterpart of ParallelSampler::neighbor_sample_from_nodes_with_before_layer
+// with policy "recent", vendor/bts_sampler/sampler/include/sampler.h:213-261).
+//
+// Hot path: ONE kernel per hop, HBM/latency bound integer work.
+//   phase 1: one lane per query -- lower_bound over the node's int64
+//            timestamps (the same probe sequence as std::lower_bound) gives
+//            the window [end-k, end) of the node's list;
+//   phase 2: the wavefront copies its 64 windows cooperatively: the wave's
+//            padded output rows [q*k, q*k+k) are contiguous, so lane l of
+//            iteration it owns slot s = it*64 + l, i.e. (query s/k, entry
+//            s%k). Stores are fully contiguous and loads are contiguous
+//            inside each window.
+// The padded layout (row q holds cnt[q] <= k valid entries, oldest first) is
+// what the attention kernels consume. sgl_recent_compact() turns it into the
+// reference's concatenated layout (a block scan of the counts, tile offsets
+// scanned by one workgroup, then a copy).
+#include <climits>
+
+#include "common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kTile = 256;      // queries per compaction tile
+constexpr int kScanBlock = 1024;
+
+template <typename NodeT>
+__global__ __launch_bounds__(kBlock) void k_recent_padded(
+    int64_t nq, const NodeT *__restrict__ q_node, const int64_t *__restrict__ q_ts,
+    const int32_t *__restrict__ q_valid_cnt, int q_stride,
+    const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
+    const int32_t *__restrict__ eid, const int64_t *__restrict__ ts,
+    int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
+    int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
+    float *__restrict__ out_dt, int64_t *__restrict__ out_ts,
+    int32_t *__restrict__ err) {
+  const int lane = threadIdx.x & (sgl::kWave - 1);
+  const int64_t q0 = int64_t(blockIdx.x) * kBlock + (threadIdx.x & ~(sgl::kWave - 1));
+  const int64_t i = q0 + lane;
+  int c = 0;
+  int64_t b = 0, t = 0;
+  if (i < nq) {
+    bool valid = true;
+    if (q_valid_cnt != nullptr) valid = int(i % q_stride) < q_valid_cnt[i / q_stride];
+    if (valid) {
+      const int64_t n = int64_t(q_node[i]);
+      t = q_ts[i];
+      if (n < 0 || n >= num_nodes) {
+        if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
+      } else {
+        const int64_t lo = indptr[n];
+        int64_t len = indptr[n + 1] - lo;
+        int64_t first = lo;
+        while (len > 0) {  // std::lower_bound
+          const int64_t half = len >> 1;
+          const int64_t mid = first + half;
+          if (ts[mid] < t) {
+            first = mid + 1;
+            len -= half + 1;
+          } else {
+            len = half;
+          }
+        }
+        const int64_t end = first - lo;
+        int64_t start = end - k;
+        if (start < 0) start = 0;
+        b = lo + start;
+        c = int(end - start);
+      }
+    }
+    out_cnt[i] = c;
+  }
+  // Cooperative copy of the wave's 64 windows into its contiguous padded rows.
+  const int64_t obase = q0 * k;
+  for (int it = 0; it < k; ++it) {
+    const int s = it * sgl::kWave + lane;
+    const int ql = s / k;
+    const int j = s - ql * k;
+    const int cq = __shfl(c, ql, sgl::kWave);
+    const int64_t bq = __shfl(b, ql, sgl::kWave);
+    const int64_t tq = __shfl(t, ql, sgl::kWave);
+    if (j < cq) {
+      const int64_t src = bq + j;
+      const int64_t o = obase + s;
+      const int64_t tv = ts[src];
+      out_nbr[o] = nbr[src];
+      out_eid[o] = eid[src];
+      out_dt[o] = float(tq - tv);  // int64 -> f32, round to nearest even
+      if (out_ts != nullptr) out_ts[o] = tv;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kTile) void k_tile_sums(int64_t nq, const int32_t *__restrict__ cnt,
+                                                     int64_t *__restrict__ tile_sum) {
+  const int64_t i = int64_t(blockIdx.x) * kTile + threadIdx.x;
+  const int64_t c = i < nq ? cnt[i] : 0;
+  __shared__ int64_t s_w[kTile / sgl::kWave];
+  const int64_t s = sgl::wave_reduce_sum(c);
+  if ((threadIdx.x & (sgl::kWave - 1)) == 0) s_w[threadIdx.x / sgl::kWave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t tot = 0;
+#pragma unroll
+    for (int w = 0; w < kTile / sgl::kWave; ++w) tot += s_w[w];
+    tile_sum[blockIdx.x] = tot;
+  }
+}
+
+// Exclusive scan of n tile totals by one workgroup: each thread owns a
+// contiguous chunk, chunk sums are block-scanned, then chunks are rewritten.
+__global__ __launch_bounds__(kScanBlock) void k_scan_tiles(
+    int64_t n, const int64_t *__restrict__ in, int64_t *__restrict__ out_excl) {
+  __shared__ int64_t s_w[kScanBlock / sgl::kWave];
+  const int64_t per = (n + kScanBlock - 1) / kScanBlock;
+  const int64_t b = int64_t(threadIdx.x) * per;
+  const int64_t e = b + per < n ? b + per : n;
+  int64_t sum = 0;
+  for (int64_t i = b; i < e; ++i) sum += in[i];
+  int64_t total;
+  int64_t run = sgl::block_exclusive_scan<int64_t, kScanBlock>(sum, s_w, total);
+  for (int64_t i = b; i < e; ++i) {
+    const int64_t v = in[i];
+    out_excl[i] = run;
+    run += v;
+  }
+}
+
+__global__ __launch_bounds__(kTile) void k_compact_fill(
+    int64_t nq, int k, const int32_t *__restrict__ cnt,
+    const int64_t *__restrict__ tile_off, const int32_t *__restrict__ pnbr,
+    const int32_t *__restrict__ peid, const float *__restrict__ pdt,
+    const int64_t *__restrict__ pts, int64_t *__restrict__ out_ptr,
+    int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
+    float *__restrict__ out_dt, int64_t *__restrict__ out_ts) {
+  __shared__ int32_t s_off[kTile + 1];
+  __shared__ int32_t s_w[kTile / sgl::kWave];
+  const int tid = threadIdx.x;
+  const int64_t q0 = int64_t(blockIdx.x) * kTile;
+  const int64_t i = q0 + tid;
+  const int c = i < nq ? cnt[i] : 0;
+  int32_t total;
+  const int32_t off = sgl::block_exclusive_scan<int32_t, kTile>(c, s_w, total);
+  s_off[tid] = off;
+  if (tid == 0) s_off[kTile] = total;
+  const int64_t base = tile_off[blockIdx.x];
+  if (i < nq) out_ptr[i] = base + off;
+  if (i == nq - 1) out_ptr[nq] = base + off + c;
+  __syncthreads();
+  for (int j = tid; j < total; j += kTile) {
+    int lo = 0, hi = kTile;  // owner: the largest q with s_off[q] <= j
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_off[mid] <= j) lo = mid; else hi = mid;
+    }
+    const int64_t src = (q0 + lo) * k + (j - s_off[lo]);
+    const int64_t o = base + j;
+    out_nbr[o] = pnbr[src];
+    out_eid[o] = peid[src];
+    out_dt[o] = pdt[src];
+    if (out_ts != nullptr) out_ts[o] = pts[src];
+  }
+}
+
+__global__ void k_write_zero_ptr(int64_t *out_ptr) { out_ptr[0] = 0; }
+
+}  // namespace
+
+extern "C" int sgl_recent_sample(
+    const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
+    const int64_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
+    const int64_t *q_ts, int64_t num_queries, const int32_t *q_valid_cnt,
+    int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
+    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
+    hipStream_t stream) {
+  SGL_REQUIRE(num_queries >= 0, "recent: num_queries < 0");
+  SGL_REQUIRE(fanout >= 0 && fanout <= 4096, "recent: fanout %d outside [0, 4096]", fanout);
+  SGL_REQUIRE(num_nodes >= 0, "recent: num_nodes < 0");
+  if (num_queries == 0) return SGL_OK;
+  SGL_REQUIRE(indptr && q_node && q_ts && out_cnt, "recent: NULL graph, query or count array");
+  SGL_REQUIRE(fanout == 0 || (nbr && eid && ts && out_nbr && out_eid && out_dt), "recent: NULL output array");
+  SGL_REQUIRE(q_valid_cnt == nullptr || q_stride > 0, "recent: q_stride must be > 0 with q_valid_cnt");
+  const int64_t blocks = (num_queries + kBlock - 1) / kBlock;
+  SGL_REQUIRE(blocks < INT_MAX, "recent: too many queries");
+  if (q_node_is_i64) {
+    k_recent_padded<int64_t><<<unsigned(blocks), kBlock, 0, stream>>>(
+        num_queries, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
+        num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+  } else {
+    k_recent_padded<int32_t><<<unsigned(blocks), kBlock, 0, stream>>>(
+        num_queries, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
+        num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+  }
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+extern "C" size_t sgl_compact_workspace_bytes(int64_t num_queries) {
+  if (num_queries < 0) return 0;
+  const size_t tiles = (size_t(num_queries) + kTile - 1) / kTile;
+  return 2 * sgl::align_up(tiles * 8) + 256;
+}
+
+extern "C" int sgl_recent_compact(int64_t num_queries, int32_t fanout,
+                                  const int32_t *cnt, const int32_t *pad_nbr,
+                                  const int32_t *pad_eid, const float *pad_dt,
+                                  const int64_t *pad_ts, int64_t *out_ptr,
+                                  int32_t *out_nbr, int32_t *out_eid,
+                                  float *out_dt, int64_t *out_ts,
+                                  void *workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  SGL_REQUIRE(num_queries >= 0, "compact: num_queries < 0");
+  SGL_REQUIRE(fanout >= 0 && fanout <= 4096, "compact: fanout %d outside [0, 4096]", fanout);
+  SGL_REQUIRE(out_ptr != nullptr, "compact: out_ptr is NULL");
+  if (num_queries == 0) {
+    k_write_zero_ptr<<<1, 1, 0, stream>>>(out_ptr);
+    SGL_CHECK_LAUNCH();
+    return SGL_OK;
+  }
+  SGL_REQUIRE(cnt != nullptr, "compact: cnt is NULL");
+  SGL_REQUIRE(fanout == 0 || (pad_nbr && pad_eid && pad_dt && out_nbr && out_eid && out_dt), "compact: NULL array");
+  SGL_REQUIRE(out_ts == nullptr || pad_ts != nullptr, "compact: out_ts needs pad_ts");
+  const size_t need = sgl_compact_workspace_bytes(num_queries);
+  if (workspace_bytes < need || workspace == nullptr) {
+    sgl::set_error("compact: workspace %zu bytes < required %zu", workspace_bytes, need);
+    return SGL_ERR_WORKSPACE;
+  }
+  const size_t tiles = (size_t(num_queries) + kTile - 1) / kTile;
+  SGL_REQUIRE(tiles < size_t(INT_MAX), "compact: too many queries");
+  sgl::Carver c(workspace);
+  int64_t *tile_sum = c.take<int64_t>(tiles);
+  int64_t *tile_off = c.take<int64_t>(tiles);
+  k_tile_sums<<<unsigned(tiles), kTile, 0, stream>>>(num_queries, cnt, tile_sum);
+  SGL_CHECK_LAUNCH();
+  k_scan_tiles<<<1, kScanBlock, 0, stream>>>(int64_t(tiles), tile_sum, tile_off);
+  SGL_CHECK_LAUNCH();
+  k_compact_fill<<<unsigned(tiles), kTile, 0, stream>>>(num_queries, fanout, cnt, tile_off, pad_nbr, pad_eid,
+                                                        pad_dt, pad_ts, out_ptr, out_nbr, out_eid, out_dt, out_ts);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}

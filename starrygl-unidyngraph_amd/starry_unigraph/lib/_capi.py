@@ -1,0 +1,122 @@
+"""ctypes binding of libstarrygl_mi355x.so (the C ABI in include/starrygl_mi355x.h).
+
+The library is the only compute path: when it is missing, or when no GPU is
+visible, every entry point raises ``RuntimeError``. There is no CPU fallback.
+Device buffers are torch tensors (the caching allocator owns them); work is
+enqueued on torch's current stream for the tensor's device.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # loads the HIP runtime first, so the library binds to the same one
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_NAME = "libstarrygl_mi355x.so"
+LIB_PATH = os.path.join(_HERE, LIB_NAME)
+ABI_VERSION = 1
+
+SGL_DERR_NODE_RANGE = 1
+SGL_DERR_EID_RANGE = 2
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/starrygl_mi355x.h
+SIGNATURES: dict[str, tuple] = {
+    "sgl_abi_version": (ctypes.c_int, []),
+    "sgl_last_error": (ctypes.c_char_p, []),
+    "sgl_tcsr_workspace_bytes": (_sz, [_i64, _i64]),
+    "sgl_tcsr_build": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
+    "sgl_recent_sample": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _i32, _i32,
+                                         _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sgl_compact_workspace_bytes": (_sz, [_i64]),
+    "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                          _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load_library(path: str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the C-ABI library. Raises RuntimeError if absent."""
+    global _lib
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        p = path or LIB_PATH
+        if not os.path.exists(p):
+            raise RuntimeError(
+                f"{LIB_NAME} not found at {p}: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `make -C starrygl-unidyngraph_amd/csrc`")
+        lib = ctypes.CDLL(p)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        v = lib.sgl_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"{LIB_NAME} ABI version {v} != expected {ABI_VERSION}")
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def lib() -> ctypes.CDLL:
+    return _lib if _lib is not None else load_library()
+
+
+def require_gpu(device=None) -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("starry_unigraph MI355X path needs a GPU (torch.cuda.is_available() is False); "
+                           "there is no CPU fallback")
+    if device is None:
+        return torch.device("cuda", torch.cuda.current_device())
+    d = torch.device(device)
+    if d.type != "cuda":
+        raise RuntimeError(f"device {d} is not a GPU; the MI355X path has no CPU fallback")
+    return d if d.index is not None else torch.device("cuda", torch.cuda.current_device())
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().sgl_last_error()
+        raise RuntimeError(f"{what}: {msg.decode() if msg else 'error code %d' % rc}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class ErrorFlag:
+    """A device int32 that kernels OR SGL_DERR_* bits into."""
+
+    def __init__(self, device: torch.device):
+        self.t = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def reset(self) -> None:
+        self.t.zero_()
+
+    def raise_if_set(self, what: str) -> None:
+        v = int(self.t.item())
+        if v:
+            parts = []
+            if v & SGL_DERR_NODE_RANGE:
+                parts.append("node id out of range [0, num_nodes)")
+            if v & SGL_DERR_EID_RANGE:
+                parts.append("edge id out of range [0, 2^31)")
+            self.reset()
+            raise RuntimeError(f"{what}: " + "; ".join(parts))
+
+
+def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
