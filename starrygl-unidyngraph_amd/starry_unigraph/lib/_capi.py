@@ -90,7 +90,14 @@ def check(rc: int, what: str) -> None:
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+    """Device address of a tensor's first element; for an empty view the
+    address inside its (non-empty) storage, so the C side never sees NULL for
+    an array that merely has no elements this call."""
+    if t is None:
+        return None
+    if t.numel() == 0:
+        return t.untyped_storage().data_ptr() + t.storage_offset() * t.element_size()
+    return t.data_ptr()
 
 
 def stream_of(device: torch.device) -> int:

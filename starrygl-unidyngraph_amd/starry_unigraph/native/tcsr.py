@@ -99,9 +99,10 @@ def build_tcsr(num_nodes: int, row, col, eid=None, ts=None, device=None, check: 
     n = int(num_nodes)
     with torch.cuda.device(dev):
         indptr = torch.empty(n + 1, dtype=torch.int64, device=dev)
-        nbr = torch.empty(e, dtype=torch.int32, device=dev)
-        eo = torch.empty(e, dtype=torch.int32, device=dev)
-        to = torch.empty(e, dtype=torch.int64, device=dev)
+        # never-NULL storage (an empty graph still hands valid pointers to kernels)
+        nbr = torch.empty(max(e, 1), dtype=torch.int32, device=dev)[:e]
+        eo = torch.empty(max(e, 1), dtype=torch.int32, device=dev)[:e]
+        to = torch.empty(max(e, 1), dtype=torch.int64, device=dev)[:e]
         ws_bytes = lib.sgl_tcsr_workspace_bytes(n, e)
         ws = _capi.workspace(ws_bytes, dev)
         err = _capi.ErrorFlag(dev)
@@ -191,17 +192,24 @@ class RecentSampler:
             else:
                 ptr.zero_()
                 m = 0
-            nbr = torch.empty(m, dtype=torch.int32, device=dev)
-            eid = torch.empty(m, dtype=torch.int32, device=dev)
-            dt = torch.empty(m, dtype=torch.float32, device=dev)
-            ts = torch.empty(m, dtype=torch.int64, device=dev) if hop.ts is not None else None
+            # at least one element each, so no output pointer is NULL
+            mm = max(m, 1)
+            nbr = torch.empty(mm, dtype=torch.int32, device=dev)
+            eid = torch.empty(mm, dtype=torch.int32, device=dev)
+            dt = torch.empty(mm, dtype=torch.float32, device=dev)
+            ts = torch.empty(mm, dtype=torch.int64, device=dev) if hop.ts is not None else None
+            pad = [hop.nbr, hop.eid, hop.dt, hop.ts]
+            if hop.nbr.numel() == 0:  # fanout 0: nothing to read, but keep pointers valid
+                one = torch.empty(1, dtype=torch.int64, device=dev)
+                pad = [one.view(torch.int32)[:1], one.view(torch.int32)[:1], one.view(torch.float32)[:1],
+                       one if hop.ts is not None else None]
             ws_bytes = _capi.lib().sgl_compact_workspace_bytes(nq)
             ws = _capi.workspace(ws_bytes, dev)
             _capi.check(_capi.lib().sgl_recent_compact(
-                nq, hop.fanout, _capi.ptr(hop.cnt), _capi.ptr(hop.nbr), _capi.ptr(hop.eid), _capi.ptr(hop.dt),
-                _capi.ptr(hop.ts), _capi.ptr(ptr), _capi.ptr(nbr), _capi.ptr(eid), _capi.ptr(dt), _capi.ptr(ts),
+                nq, hop.fanout, _capi.ptr(hop.cnt), _capi.ptr(pad[0]), _capi.ptr(pad[1]), _capi.ptr(pad[2]),
+                _capi.ptr(pad[3]), _capi.ptr(ptr), _capi.ptr(nbr), _capi.ptr(eid), _capi.ptr(dt), _capi.ptr(ts),
                 _capi.ptr(ws), ws_bytes, _capi.stream_of(dev)), "sgl_recent_compact")
-        return SampleHop(ptr, nbr, eid, dt, ts, hop.q_ts)
+        return SampleHop(ptr, nbr[:m], eid[:m], dt[:m], None if ts is None else ts[:m], hop.q_ts)
 
     def sample_hops(self, nodes: torch.Tensor, q_ts: torch.Tensor, fanouts: list[int],
                     want_last_ts: bool = False) -> list[SampleHop]:
