@@ -82,11 +82,15 @@ int sgl_tcsr_build(int64_t num_nodes, int64_t num_edges, const int64_t *row,
  * NULL, query i is sampled only when (i % q_stride) < q_valid_cnt[i / q_stride]
  * (so a padded previous hop can be the query list; q_valid_cnt then holds
  * ceil(num_queries / q_stride) entries); other queries get out_cnt = 0.
+ * If num_queries_dev is not NULL (a device int64), only queries
+ * i < *num_queries_dev are live: launch shapes stay at the capacity
+ * num_queries while the live count is known only on the device.
  * ------------------------------------------------------------------------- */
 int sgl_recent_sample(const int64_t *indptr, const int32_t *nbr,
                       const int32_t *eid, const int64_t *ts, int64_t num_nodes,
                       const void *q_node, int q_node_is_i64,
                       const int64_t *q_ts, int64_t num_queries,
+                      const int64_t *num_queries_dev,
                       const int32_t *q_valid_cnt, int32_t q_stride,
                       int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
                       int32_t *out_eid, float *out_dt, int64_t *out_ts,
@@ -104,6 +108,141 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
                        int64_t *out_ptr, int32_t *out_nbr, int32_t *out_eid,
                        float *out_dt, int64_t *out_ts, void *workspace,
                        size_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (3) Batch preparation.
+ * Replaces CTDGOnlineRuntime._prepare (backends/ctdg/runtime/runtime.py:138-144:
+ * roots = sorted unique(src ∪ dst), query time int(batch.ts.max())) and the
+ * duplicate handling of CTDGMemoryBank._write_slots (memory.py:237-248).
+ *
+ * node_bits (ceil(N/32) words) must be all zero on entry; sgl_memory_commit
+ * clears the words it set. Outputs, all device-resident (no host sync):
+ *   num_roots / num_roots64: U;  roots[0..U) sorted ascending (int64);
+ *   root_ts[0..U) = t_query = trunc(max ts) for every root; ts_max = max ts;
+ *   ridx_src/ridx_dst[e] = root index of src[e]/dst[e]; ridx_neg[e] = root
+ *   index of neg[e] or -1 when neg[e] is not a root (neg may be NULL);
+ *   win_src/win_dst[r] = (order(ts) << 32 | e) of the LAST event in stable
+ *   timestamp order in which root r is the src / dst; cnt_src/cnt_dst[r] =
+ *   how many events root r is src / dst in; any_edges reset to 0.
+ * Arrays indexed by root hold 2*batch entries (the capacity).
+ * ------------------------------------------------------------------------- */
+int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
+                      const int64_t *dst, const int64_t *neg, const float *ts,
+                      uint32_t *node_bits, int32_t *word_prefix,
+                      int32_t *num_roots, int64_t *num_roots64, float *ts_max,
+                      int64_t *t_query, int64_t *roots, int64_t *root_ts,
+                      int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
+                      uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src,
+                      int32_t *cnt_dst, int32_t *any_edges, int32_t *err_flag,
+                      hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (4)+(6) Memory update (GRU) fused with the mailbox write.
+ * Replaces, for the U roots of a batch:
+ *   CTDGMemoryUpdater.forward  backends/ctdg/runtime/models.py:244-254
+ *     (nn.GRU over the K mailbox slots in slot order from h0 = 0, then
+ *      nn.GRUCell(agg, memory); PyTorch weight layouts, gate order r,z,n)
+ *   CTDGMemoryBank.read_mailbox / gather   memory.py:135-168
+ *   CTDGMemoryBank.write_mailbox / _write_slots   memory.py:183-248
+ * new_mem[r] (capacity x D) receives the updated memory of roots[r]; the
+ * memory table itself is not written (see sgl_memory_commit), so the mailbox
+ * messages [mem(self) | mem(other) | efeat[e]] use pre-update memory as the
+ * reference does (runtime.py:270-282). Mailbox slot, ts and next_mail_pos
+ * (int32 here) follow memory.py:237-248: one slot per node and role per
+ * batch, src role first, pointer advanced by the occurrence counts.
+ * Weights: w_ih [3D][2D+F], w_hh [3D][D], wc_ih [3D][D], wc_hh [3D][D].
+ * ------------------------------------------------------------------------- */
+size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F);
+int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
+                      const int32_t *num_roots, const int64_t *roots,
+                      const float *memory, float *mailbox, float *mailbox_ts,
+                      int32_t *next_mail_pos, const float *w_ih,
+                      const float *w_hh, const float *b_ih, const float *b_hh,
+                      const float *wc_ih, const float *wc_hh,
+                      const float *bc_ih, const float *bc_hh,
+                      const int64_t *src, const int64_t *dst,
+                      const float *efeat, const float *ts,
+                      const uint64_t *win_src, const uint64_t *win_dst,
+                      const int32_t *cnt_src, const int32_t *cnt_dst,
+                      float *new_mem, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (5) Memory commit.
+ * Replaces CTDGMemoryBank._apply_memory_update (memory.py:254-269):
+ * memory[roots[r]] = new_mem[r], memory_ts[roots[r]] = ts_max for r < U.
+ * Also clears node_bits for the next batch and sets any_edges = 1 if some
+ * root has sample_cnt[r] > 0 (sample_cnt may be NULL).
+ * ------------------------------------------------------------------------- */
+int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
+                      const int64_t *roots, const float *new_mem,
+                      float *memory, float *memory_ts, const float *ts_max,
+                      uint32_t *node_bits, const int32_t *sample_cnt,
+                      int32_t *any_edges, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (7) Time encoding + temporal attention, forward and backward.
+ * Replaces TemporalTransformerConv.forward (backends/ctdg/runtime/models.py:77-137)
+ * with TimeEncode (runtime/modules/time_encode.py:41-58) over the block of
+ * build_dgl_block (models.py:144-197), one tile of 16 roots per workgroup.
+ * Inputs per root r < U: h_root[r] (its updated memory), its padded hop-0
+ * window (cnt[r], nbr/eid/dt rows of the sampler); neighbour features come
+ * from the committed memory table and efeat [num_edges][F].
+ * Parameters use nn.Linear layouts: w_q [D][D+T], w_k/w_v [D][D+F+T],
+ * w_out [D][2D], ln_g/ln_b [D], te_w/te_b [T]. capacity % 16 == 0.
+ * Forward writes y [capacity][D] plus the saved state the backward needs
+ * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
+ * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows >= U are
+ * zero. If any_edges == 0 the whole output is zero (models.py:88-89).
+ * Backward takes gy and writes gz, gagg [cap][D], G [cap][H][D+F+T],
+ * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
+ * tile partial sums ln_part [cap/16][2][D] (gamma, beta) and
+ * te_part [cap/16][2][T] (time-encoding w, b).
+ * ------------------------------------------------------------------------- */
+int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
+                     int32_t fanout, int64_t capacity,
+                     const int32_t *num_roots, const int32_t *any_edges,
+                     const float *h_root, const float *memory,
+                     const float *efeat, const int32_t *cnt,
+                     const int32_t *nbr, const int32_t *eid, const float *dt,
+                     const float *w_q, const float *b_q, const float *w_k,
+                     const float *b_k, const float *w_v, const float *b_v,
+                     const float *w_out, const float *b_out,
+                     const float *ln_g, const float *ln_b, const float *te_w,
+                     const float *te_b, float *sv_Q, float *sv_qt,
+                     float *sv_xbar, float *sv_score, float *sv_ml,
+                     float *sv_agg, float *sv_z, float *sv_stats, float *y,
+                     hipStream_t stream);
+int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
+                      int32_t fanout, int64_t capacity,
+                      const int32_t *num_roots, const int32_t *any_edges,
+                      const float *memory, const float *efeat,
+                      const int32_t *cnt, const int32_t *nbr,
+                      const int32_t *eid, const float *dt, const float *w_q,
+                      const float *b_q, const float *w_k, const float *b_k,
+                      const float *w_v, const float *b_v, const float *w_out,
+                      const float *b_out, const float *ln_g, const float *ln_b,
+                      const float *te_w, const float *te_b,
+                      const float *sv_Q, const float *sv_qt,
+                      const float *sv_xbar, const float *sv_score,
+                      const float *sv_ml, const float *sv_agg,
+                      const float *sv_z, const float *sv_stats,
+                      const float *gy, float *gz, float *gagg, float *G,
+                      float *sigma, float *gQ, float *ln_part, float *te_part,
+                      hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
+ * optimizer of backends/ctdg/runtime/factory.py:122-128. `step` is a device
+ * float holding the completed step count (read as t-1); sgl_adam_advance
+ * adds one after the segment's update. `active` (device int32, may be NULL)
+ * gates both: 0 leaves parameters, moments and step untouched, as Adam does
+ * for parameters whose grad is None.
+ * ------------------------------------------------------------------------- */
+int sgl_adam_step(int64_t n, float *param, const float *grad, float *exp_avg,
+                  float *exp_avg_sq, const float *step, const int32_t *active,
+                  float lr, float beta1, float beta2, float eps,
+                  float weight_decay, hipStream_t stream);
+int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,8 @@ bench.py's ``cpu_baseline`` leg may import it, and only as the checker or the
 timed CPU baseline; the product path never imports it.
 
 Follows, function by function:
-  TimeEncodeO            runtime/modules/time_encode.py:41-58
+  TimeEncodeO            runtime/modules/time_encode.py:41-58 (argument rounded
+                         as fl(fl(t*w) + b): the GEMM-with-bias-epilogue result)
   TemporalConvO.forward  backends/ctdg/runtime/models.py:77-137 with
                          build_dgl_block models.py:144-197 (DGL edge_softmax
                          restated as a per-destination max-subtracted softmax,
@@ -21,8 +22,7 @@ Follows, function by function:
 Parity pins (tests/test_oracle_step.py): GRU/GRUCell against hand-written
 gate equations; the conv against a per-root brute-force attention loop and
 invariants (single neighbour, no neighbour, empty block, permutation of a
-root's neighbours); mailbox writes against a serial loop of the A10 rules;
-gradients by float64 gradcheck.
+root's neighbours); mailbox writes against a serial loop of the A10 rules.
 """
 from __future__ import annotations
 
@@ -47,9 +47,13 @@ class TimeEncodeO(nn.Module):
         self.w.weight = nn.Parameter((1.0 / 10 ** torch.linspace(0, 9, dim)).reshape(dim, 1))
 
     def forward(self, t: torch.Tensor) -> torch.Tensor:
-        # t.float() in the reference; the parameter dtype here, so a float64
-        # copy of the module can be checked in float64
-        return torch.cos(self.w(t.to(self.w.weight.dtype).reshape(-1, 1))).reshape(*t.shape, self.dim)
+        # The reference evaluates nn.Linear(1, T); a GPU GEMM with a bias
+        # epilogue rounds the product, then adds the bias. CPU BLAS picks a fused
+        # multiply-add for some shapes and not others, so the oracle states the
+        # two-rounding form elementwise. (t.float() in the reference; the
+        # parameter dtype here so that a float64 copy can be checked in float64.)
+        tt = t.to(self.w.weight.dtype).reshape(-1, 1)
+        return torch.cos(tt * self.w.weight.reshape(1, -1) + self.w.bias).reshape(*t.shape, self.dim)
 
 
 class TemporalConvO(nn.Module):

@@ -27,8 +27,8 @@ constexpr int kScanBlock = 1024;
 
 template <typename NodeT>
 __global__ __launch_bounds__(kBlock) void k_recent_padded(
-    int64_t nq, const NodeT *__restrict__ q_node, const int64_t *__restrict__ q_ts,
-    const int32_t *__restrict__ q_valid_cnt, int q_stride,
+    int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
+    const int64_t *__restrict__ q_ts, const int32_t *__restrict__ q_valid_cnt, int q_stride,
     const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, const int64_t *__restrict__ ts,
     int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
@@ -40,9 +40,10 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
   const int64_t i = q0 + lane;
   int c = 0;
   int64_t b = 0, t = 0;
+  const int64_t nq_live = nq_live_dev != nullptr ? min(nq, *nq_live_dev) : nq;
   if (i < nq) {
-    bool valid = true;
-    if (q_valid_cnt != nullptr) valid = int(i % q_stride) < q_valid_cnt[i / q_stride];
+    bool valid = i < nq_live;
+    if (valid && q_valid_cnt != nullptr) valid = int(i % q_stride) < q_valid_cnt[i / q_stride];
     if (valid) {
       const int64_t n = int64_t(q_node[i]);
       t = q_ts[i];
@@ -170,7 +171,7 @@ __global__ void k_write_zero_ptr(int64_t *out_ptr) { out_ptr[0] = 0; }
 extern "C" int sgl_recent_sample(
     const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
     const int64_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
-    const int64_t *q_ts, int64_t num_queries, const int32_t *q_valid_cnt,
+    const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
     int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
     int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
     hipStream_t stream) {
@@ -185,11 +186,11 @@ extern "C" int sgl_recent_sample(
   SGL_REQUIRE(blocks < INT_MAX, "recent: too many queries");
   if (q_node_is_i64) {
     k_recent_padded<int64_t><<<unsigned(blocks), kBlock, 0, stream>>>(
-        num_queries, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
+        num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
         num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   } else {
     k_recent_padded<int32_t><<<unsigned(blocks), kBlock, 0, stream>>>(
-        num_queries, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
+        num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
         num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   }
   SGL_CHECK_LAUNCH();

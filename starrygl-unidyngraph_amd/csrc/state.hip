@@ -1,0 +1,362 @@
+// Per-step node state: batch preparation, the fused GRU memory update +
+// mailbox write, and the memory commit. Counterparts of
+//   CTDGOnlineRuntime._prepare / train_step steps 3-5   backends/ctdg/runtime/runtime.py:138-144,268-282
+//   CTDGMemoryBank.gather/read_mailbox                   backends/ctdg/runtime/memory.py:135-168
+//   CTDGMemoryUpdater.forward (GRU over K slots + GRUCell)  backends/ctdg/runtime/models.py:244-254
+//   CTDGMemoryBank.write_mailbox/_write_slots            memory.py:183-248
+//   CTDGMemoryBank._apply_memory_update                  memory.py:254-269
+//
+// Roots (= sorted unique(src ∪ dst)) come from a node bitmap: mark, scan the
+// word popcounts, then rank(n) = prefix[n/32] + popc(word & below(n)); the
+// rank is the root index and the roots come out sorted without a sort.
+// Capacity-sized arrays (2B roots) plus a device-side root count keep every
+// launch shape static (HIP-graph capturable, no host sync).
+#include <climits>
+
+#include "common.h"
+#include "mfma.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kScanBlock = 1024;
+constexpr int kTileRows = 16;
+
+__device__ __forceinline__ uint32_t ts_order(float x) {
+  // monotone map float -> uint32 (larger float -> larger key)
+  const uint32_t b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ int32_t node_rank(const uint32_t *__restrict__ bits,
+                                             const int32_t *__restrict__ prefix, int64_t n) {
+  const uint32_t w = bits[n >> 5];
+  const uint32_t below = (1u << (n & 31)) - 1u;
+  return prefix[n >> 5] + __popc(w & below);
+}
+
+__global__ __launch_bounds__(kBlock) void k_step_mark(
+    int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ dst, uint32_t *__restrict__ bits,
+    unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
+    int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst,
+    int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
+  const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (e == 0) *any_edges = 0;
+  for (int64_t r = 2 * e; r < 2 * e + 2 && r < cap; ++r) {
+    win_src[r] = 0ull;
+    win_dst[r] = 0ull;
+    cnt_src[r] = 0;
+    cnt_dst[r] = 0;
+  }
+  if (e >= batch) return;
+  const int64_t s = src[e], d = dst[e];
+  if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
+    if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
+    return;
+  }
+  atomicOr(&bits[s >> 5], 1u << (s & 31));
+  atomicOr(&bits[d >> 5], 1u << (d & 31));
+}
+
+// One workgroup: exclusive scan of the bitmap word popcounts (-> root count)
+// and the batch's max timestamp (-> the sampler's query time).
+__global__ __launch_bounds__(kScanBlock) void k_step_scan(
+    int64_t nwords, const uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
+    int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
+    const float *__restrict__ ts, float *__restrict__ ts_max, int64_t *__restrict__ t_query) {
+  __shared__ int32_t s_w[kScanBlock / sgl::kWave];
+  __shared__ float s_m[kScanBlock / sgl::kWave];
+  const int64_t per = (nwords + kScanBlock - 1) / kScanBlock;
+  const int64_t b = int64_t(threadIdx.x) * per;
+  const int64_t e = b + per < nwords ? b + per : nwords;
+  int32_t sum = 0;
+  for (int64_t i = b; i < e; ++i) sum += __popc(bits[i]);
+  int32_t total;
+  int32_t run = sgl::block_exclusive_scan<int32_t, kScanBlock>(sum, s_w, total);
+  for (int64_t i = b; i < e; ++i) {
+    prefix[i] = run;
+    run += __popc(bits[i]);
+  }
+  float m = -INFINITY;
+  for (int64_t i = threadIdx.x; i < batch; i += kScanBlock) m = fmaxf(m, ts[i]);
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, sgl::kWave));
+  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mm = -INFINITY;
+    for (int w = 0; w < kScanBlock / sgl::kWave; ++w) mm = fmaxf(mm, s_m[w]);
+    *num_roots = total;
+    *num_roots64 = total;
+    *ts_max = mm;
+    // int(float max) truncates toward zero (runtime.py:142); the float32 round
+    // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
+    *t_query = batch > 0 ? (long long)truncf(mm) : 0;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_step_index(
+    int64_t batch, int64_t num_nodes, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
+    const float *__restrict__ ts, const uint32_t *__restrict__ bits,
+    const int32_t *__restrict__ prefix, const int64_t *__restrict__ t_query,
+    int64_t *__restrict__ roots, int64_t *__restrict__ root_ts,
+    int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst,
+    int32_t *__restrict__ ridx_neg, unsigned long long *__restrict__ win_src,
+    unsigned long long *__restrict__ win_dst, int32_t *__restrict__ cnt_src,
+    int32_t *__restrict__ cnt_dst) {
+  const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  if (e >= batch) return;
+  const int64_t s = src[e], d = dst[e];
+  if (neg != nullptr) {
+    const int64_t n = neg[e];
+    int32_t rn = -1;
+    if (n >= 0 && n < num_nodes && ((bits[n >> 5] >> (n & 31)) & 1u)) rn = node_rank(bits, prefix, n);
+    ridx_neg[e] = rn;
+  }
+  if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
+    ridx_src[e] = -1;
+    ridx_dst[e] = -1;
+    return;
+  }
+  const int32_t rs = node_rank(bits, prefix, s);
+  const int32_t rd = node_rank(bits, prefix, d);
+  const int64_t tq = *t_query;
+  roots[rs] = s;
+  roots[rd] = d;
+  root_ts[rs] = tq;
+  root_ts[rd] = tq;
+  ridx_src[e] = rs;
+  ridx_dst[e] = rd;
+  // last writer per node and role = the largest (ts, event) pair (stable ts order)
+  const unsigned long long key = (static_cast<unsigned long long>(ts_order(ts[e])) << 32) |
+                                 static_cast<unsigned long long>(e);
+  atomicMax(&win_src[rs], key);
+  atomicMax(&win_dst[rd], key);
+  atomicAdd(&cnt_src[rs], 1);
+  atomicAdd(&cnt_dst[rd], 1);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+
+// GRU gate combination (PyTorch order r, z, n):
+//   r = s(gi_r + gh_r), z = s(gi_z + gh_z), n = tanh(gi_n + r * gh_n),
+//   h' = (1 - z) * n + z * h
+__device__ __forceinline__ float gru_combine(float gir, float giz, float gin, float ghr, float ghz,
+                                             float ghn, float h) {
+  const float r = 1.f / (1.f + expf(-(gir + ghr)));
+  const float z = 1.f / (1.f + expf(-(giz + ghz)));
+  const float n = tanhf(gin + r * ghn);
+  return (1.f - z) * n + z * h;
+}
+
+// One workgroup = 16 roots. LDS: x [16][S], h [16][D], mem [16][D],
+// gi [16][3D], gh [16][3D] (leading dims padded by one float).
+__global__ __launch_bounds__(kBlock) void k_gru_mailbox(
+    int D, int K, int F, const int32_t *__restrict__ num_roots,
+    const int64_t *__restrict__ roots, const float *__restrict__ memory,
+    float *__restrict__ mailbox, float *__restrict__ mailbox_ts,
+    int32_t *__restrict__ next_mail_pos, const float *__restrict__ w_ih,
+    const float *__restrict__ w_hh, const float *__restrict__ b_ih,
+    const float *__restrict__ b_hh, const float *__restrict__ wc_ih,
+    const float *__restrict__ wc_hh, const float *__restrict__ bc_ih,
+    const float *__restrict__ bc_hh, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ dst, const float *__restrict__ efeat,
+    const float *__restrict__ ts, const unsigned long long *__restrict__ win_src,
+    const unsigned long long *__restrict__ win_dst, const int32_t *__restrict__ cnt_src,
+    const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
+  extern __shared__ float lds[];
+  const int S = 2 * D + F;
+  const int G = 3 * D;
+  const int ldx = S + 1, ldh = D + 1, ldg = G + 1;
+  float *xs = lds;
+  float *hs = xs + kTileRows * ldx;
+  float *ms = hs + kTileRows * ldh;
+  float *gi = ms + kTileRows * ldh;
+  float *gh = gi + kTileRows * ldg;
+  const int U = *num_roots;
+  const int r0 = blockIdx.x * kTileRows;
+  if (r0 >= U) return;  // uniform per workgroup
+  const int nrows = min(kTileRows, U - r0);
+  const int tid = threadIdx.x;
+  const int nwaves = kBlock / sgl::kWave;
+
+  for (int idx = tid; idx < kTileRows * D; idx += kBlock) {
+    const int i = idx / D, j = idx - (idx / D) * D;
+    ms[i * ldh + j] = i < nrows ? memory[roots[r0 + i] * D + j] : 0.f;
+    hs[i * ldh + j] = 0.f;
+  }
+  // GRU layer over the K mailbox slots in slot-index order, h0 = 0
+  for (int k = 0; k < K; ++k) {
+    for (int idx = tid; idx < kTileRows * S; idx += kBlock) {
+      const int i = idx / S, j = idx - (idx / S) * S;
+      xs[i * ldx + j] = i < nrows ? mailbox[(roots[r0 + i] * K + k) * S + j] : 0.f;
+    }
+    __syncthreads();
+    sgl::tile_gemm16<sgl::kNT>(xs, ldx, w_ih, S, b_ih, gi, ldg, S, G, nwaves);
+    if (k > 0) sgl::tile_gemm16<sgl::kNT>(hs, ldh, w_hh, D, b_hh, gh, ldg, D, G, nwaves);
+    __syncthreads();
+    for (int idx = tid; idx < kTileRows * D; idx += kBlock) {
+      const int i = idx / D, j = idx - (idx / D) * D;
+      const float *g1 = gi + i * ldg;
+      float ghr, ghz, ghn;
+      if (k > 0) {
+        const float *g2 = gh + i * ldg;
+        ghr = g2[j]; ghz = g2[D + j]; ghn = g2[2 * D + j];
+      } else {  // W_hh h0 = 0
+        ghr = b_hh[j]; ghz = b_hh[D + j]; ghn = b_hh[2 * D + j];
+      }
+      hs[i * ldh + j] = gru_combine(g1[j], g1[D + j], g1[2 * D + j], ghr, ghz, ghn, hs[i * ldh + j]);
+    }
+    __syncthreads();
+  }
+  // GRUCell(agg = h, memory)
+  sgl::tile_gemm16<sgl::kNT>(hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G, nwaves);
+  sgl::tile_gemm16<sgl::kNT>(ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G, nwaves);
+  __syncthreads();
+  for (int idx = tid; idx < nrows * D; idx += kBlock) {
+    const int i = idx / D, j = idx - (idx / D) * D;
+    const float *g1 = gi + i * ldg;
+    const float *g2 = gh + i * ldg;
+    new_mem[size_t(r0 + i) * D + j] =
+        gru_combine(g1[j], g1[D + j], g1[2 * D + j], g2[j], g2[D + j], g2[2 * D + j], ms[i * ldh + j]);
+  }
+
+  // Mailbox write (memory.py:218-248): the src-role message of node u is
+  // [mem(u) || mem(other) || f_e] of its last src event, written to slot p =
+  // next_mail_pos[u]; the dst-role message goes to (p + #src occurrences) % K,
+  // so with one slot the dst role wins. The memory table still holds the
+  // pre-update values here (the commit is a later launch).
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int i = wave; i < nrows; i += nwaves) {
+    const int r = r0 + i;
+    const int64_t u = roots[r];
+    const int cs = cnt_src[r], cd = cnt_dst[r];
+    const int p = next_mail_pos[u];
+    const int p2 = (p + cs) % K;
+    const bool write_src = cs > 0 && !(cd > 0 && p2 == p);
+    for (int role = 0; role < 2; ++role) {
+      if (role == 0 && !write_src) continue;
+      if (role == 1 && cd == 0) continue;
+      const unsigned long long key = role == 0 ? win_src[r] : win_dst[r];
+      const int64_t e = int64_t(key & 0xffffffffull);
+      const int64_t self = role == 0 ? src[e] : dst[e];
+      const int64_t other = role == 0 ? dst[e] : src[e];
+      const int slot = role == 0 ? p : p2;
+      float *out = mailbox + (u * K + slot) * S;
+      for (int j = lane; j < S; j += sgl::kWave) {
+        float v;
+        if (j < D) v = memory[self * D + j];
+        else if (j < 2 * D) v = memory[other * D + (j - D)];
+        else v = efeat[e * F + (j - 2 * D)];
+        out[j] = v;
+      }
+      if (lane == 0) mailbox_ts[u * K + slot] = ts[e];
+    }
+    if (lane == 0) next_mail_pos[u] = int32_t((int64_t(p) + cs + cd) % K);
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_memory_commit(
+    int D, int64_t cap, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ roots,
+    const float *__restrict__ new_mem, float *__restrict__ memory, float *__restrict__ memory_ts,
+    const float *__restrict__ ts_max, uint32_t *__restrict__ bits,
+    const int32_t *__restrict__ sample_cnt, int32_t *__restrict__ any_edges) {
+  const int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t r = idx / D;
+  const int j = int(idx - r * D);
+  if (r >= cap || r >= *num_roots) return;
+  const int64_t u = roots[r];
+  memory[u * D + j] = new_mem[r * D + j];
+  if (j == 0) {
+    memory_ts[u] = *ts_max;
+    bits[u >> 5] = 0u;  // leave the bitmap clear for the next step
+    if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
+  }
+}
+
+}  // namespace
+
+extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
+                                 const int64_t *neg, const float *ts, uint32_t *node_bits,
+                                 int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
+                                 float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
+                                 int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
+                                 uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src, int32_t *cnt_dst,
+                                 int32_t *any_edges, int32_t *err_flag, hipStream_t stream) {
+  SGL_REQUIRE(num_nodes > 0 && num_nodes < INT_MAX, "batch_prepare: num_nodes %lld out of range", (long long)num_nodes);
+  SGL_REQUIRE(batch >= 0 && batch < (INT_MAX / 2), "batch_prepare: batch %lld out of range", (long long)batch);
+  SGL_REQUIRE(node_bits && word_prefix && num_roots && num_roots64 && ts_max && t_query && any_edges,
+              "batch_prepare: NULL state array");
+  SGL_REQUIRE(batch == 0 || (src && dst && ts && roots && root_ts && ridx_src && ridx_dst && win_src && win_dst &&
+                             cnt_src && cnt_dst && (neg == nullptr || ridx_neg)),
+              "batch_prepare: NULL batch array");
+  const int64_t cap = 2 * batch;
+  const int64_t nwords = (num_nodes + 31) / 32;
+  const unsigned grid = unsigned((cap / 2 + kBlock - 1) / kBlock + 1);
+  auto *ws = reinterpret_cast<unsigned long long *>(win_src);
+  auto *wd = reinterpret_cast<unsigned long long *>(win_dst);
+  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, node_bits, ws, wd, cnt_src, cnt_dst,
+                                           any_edges, err_flag);
+  SGL_CHECK_LAUNCH();
+  k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts,
+                                            ts_max, t_query);
+  SGL_CHECK_LAUNCH();
+  if (batch > 0) {
+    k_step_index<<<unsigned((batch + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
+        batch, num_nodes, src, dst, neg, ts, node_bits, word_prefix, t_query, roots, root_ts, ridx_src, ridx_dst,
+        ridx_neg, ws, wd, cnt_src, cnt_dst);
+    SGL_CHECK_LAUNCH();
+  }
+  return SGL_OK;
+}
+
+extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {
+  const size_t S = size_t(2 * D + F), G = size_t(3 * D);
+  return sizeof(float) * kTileRows * ((S + 1) + 2 * (D + 1) + 2 * (G + 1));
+}
+
+extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
+                                 const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
+                                 int32_t *next_mail_pos, const float *w_ih, const float *w_hh, const float *b_ih,
+                                 const float *b_hh, const float *wc_ih, const float *wc_hh, const float *bc_ih,
+                                 const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
+                                 const float *ts, const uint64_t *win_src, const uint64_t *win_dst,
+                                 const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
+                                 hipStream_t stream) {
+  SGL_REQUIRE(D > 0 && K > 0 && F >= 0, "memory_update: bad dims D=%d K=%d F=%d", D, K, F);
+  SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX, "memory_update: capacity out of range");
+  if (capacity == 0) return SGL_OK;
+  SGL_REQUIRE(num_roots && roots && memory && mailbox && mailbox_ts && next_mail_pos && w_ih && w_hh && b_ih &&
+                  b_hh && wc_ih && wc_hh && bc_ih && bc_hh && src && dst && ts && win_src && win_dst &&
+                  cnt_src && cnt_dst && new_mem && (F == 0 || efeat),
+              "memory_update: NULL array");
+  const size_t lds = sgl_memory_update_lds_bytes(D, F);
+  SGL_REQUIRE(lds <= 160 * 1024, "memory_update: D=%d F=%d needs %zu bytes of LDS (> 160 KiB)", D, F, lds);
+  SGL_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gru_mailbox),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  const unsigned grid = unsigned((capacity + kTileRows - 1) / kTileRows);
+  k_gru_mailbox<<<grid, kBlock, lds, stream>>>(
+      D, K, F, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh,
+      bc_ih, bc_hh, src, dst, efeat, ts, reinterpret_cast<const unsigned long long *>(win_src),
+      reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
+                                 const float *new_mem, float *memory, float *memory_ts, const float *ts_max,
+                                 uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges,
+                                 hipStream_t stream) {
+  SGL_REQUIRE(D > 0, "memory_commit: D <= 0");
+  SGL_REQUIRE(capacity >= 0, "memory_commit: capacity < 0");
+  if (capacity == 0) return SGL_OK;
+  SGL_REQUIRE(num_roots && roots && new_mem && memory && memory_ts && ts_max && node_bits && any_edges,
+              "memory_commit: NULL array");
+  const int64_t total = capacity * D;
+  k_memory_commit<<<unsigned((total + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
+      D, capacity, num_roots, roots, new_mem, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}

@@ -1,0 +1,130 @@
+"""CTDG event stream and batching (backends/ctdg/runtime/data.py:22-239 in
+the reference): contiguous time-ordered batches of one split, and the
+per-split sampler graph (every event before the split's end, so it includes
+the current batch -- data.py:196-231)."""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Iterator
+
+import torch
+
+from starry_unigraph.data import RawTemporalEvents, load_raw_temporal_events
+from starry_unigraph.runtime._split import normalize_split_ratio, split_bounds
+
+
+@dataclass
+class CTDGDataBatch:
+    index: int
+    split: str
+    event_ids: torch.Tensor
+    src: torch.Tensor
+    dst: torch.Tensor
+    ts: torch.Tensor
+    edge_feat: torch.Tensor
+    src_node_feat: torch.Tensor | None = None
+    dst_node_feat: torch.Tensor | None = None
+
+    @property
+    def size(self) -> int:
+        return int(self.src.numel())
+
+    @property
+    def is_empty(self) -> bool:
+        return self.size == 0
+
+    @property
+    def start(self) -> int:
+        """First event id when the batch is a contiguous range, else -1."""
+        n = self.event_ids.numel()
+        if n == 0:
+            return 0
+        a, b = int(self.event_ids[0]), int(self.event_ids[-1])
+        return a if b - a + 1 == n else -1
+
+
+class TGTemporalDataset:
+    def __init__(self, root: str | Path, name: str, split_ratio: dict[str, float] | None = None,
+                 config: dict | None = None, events: RawTemporalEvents | None = None):
+        self.root = Path(root).expanduser().resolve() / name
+        cfg = dict(config or {})
+        cfg.setdefault("data", {})
+        cfg["data"] = dict(cfg["data"])
+        cfg["data"]["split_ratio"] = split_ratio or cfg["data"].get("split_ratio")
+        raw = events if events is not None else load_raw_temporal_events(Path(root), name, cfg)
+        self.event_ids = torch.arange(raw.num_edges, dtype=torch.long)
+        self.src = raw.src.long()
+        self.dst = raw.dst.long()
+        self.ts = raw.ts.float()
+        self.num_nodes = int(raw.num_nodes)
+        self.num_edges = int(raw.num_edges)
+        self.edge_feat = raw.edge_feat.float()
+        self.edge_feat_dim = int(self.edge_feat.size(-1))
+        self.node_temporal_features = None
+        self.node_feat_dim = 0
+        self.split_ratio = normalize_split_ratio(cfg["data"].get("split_ratio"))
+        self._split_cache: dict[str, torch.Tensor] = {}
+        self._sampler_cache: dict[str, dict[str, torch.Tensor]] = {}
+        self._device_cache: dict[str, dict[str, torch.Tensor]] = {}
+        self.node_parts = None
+        self.edge_parts = None
+        self.partition_rank = 0
+        self.partition_world_size = 1
+
+    def configure_partition(self, *, node_parts, edge_parts, rank: int, world_size: int) -> None:
+        self.node_parts, self.edge_parts = node_parts, edge_parts
+        self.partition_rank, self.partition_world_size = rank, world_size
+
+    def split_event_ids(self, split: str) -> torch.Tensor:
+        ids = self._split_cache.get(split)
+        if ids is None:
+            a, b = split_bounds(self.num_edges, split, self.split_ratio)
+            ids = self._split_cache[split] = torch.arange(a, b, dtype=torch.long)
+        return ids
+
+    def lookup_node_features(self, node_ids, ts):
+        return None
+
+    def iter_batches(self, split: str, batch_size: int) -> Iterator[CTDGDataBatch]:
+        """data.py:161-194: consecutive slices of the split."""
+        ids = self.split_event_ids(split)
+        step = batch_size * (self.partition_world_size if (self.partition_world_size > 1 and
+                                                            self.edge_parts is not None) else 1)
+        for bi, start in enumerate(range(0, int(ids.numel()), step)):
+            ev = ids[start:start + step]
+            if self.partition_world_size > 1 and self.edge_parts is not None:
+                ev = ev[self.edge_parts[ev] == self.partition_rank]
+            yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[ev], dst=self.dst[ev],
+                                ts=self.ts[ev], edge_feat=self.edge_feat[ev])
+
+    def sampler_graph(self, split: str) -> dict[str, torch.Tensor]:
+        """data.py:196-231: train = [0, train_end); val = [0, val_end);
+        test = [0, test_end); ts is int64 of the float32 times (truncation)."""
+        g = self._sampler_cache.get(split)
+        if g is not None:
+            return g
+        _, train_end = split_bounds(self.num_edges, "train", self.split_ratio)
+        _, val_end = split_bounds(self.num_edges, "val", self.split_ratio)
+        _, test_end = split_bounds(self.num_edges, "test", self.split_ratio)
+        end = {"train": train_end, "val": val_end, "test": test_end}.get(split)
+        if end is None:
+            raise KeyError(f"Unsupported CTDG split: {split}")
+        idx = torch.arange(0, end, dtype=torch.long)
+        g = {"row": self.src[idx], "col": self.dst[idx], "eid": idx, "ts": self.ts[idx].long()}
+        self._sampler_cache[split] = g
+        return g
+
+    def device_arrays(self, device) -> dict[str, torch.Tensor]:
+        """The whole stream resident in HBM (uploaded once)."""
+        key = str(device)
+        d = self._device_cache.get(key)
+        if d is None:
+            d = {"src": self.src.to(device), "dst": self.dst.to(device), "ts": self.ts.to(device),
+                 "edge_feat": self.edge_feat.to(device).contiguous()}
+            self._device_cache[key] = d
+        return d
+
+    def describe(self) -> dict[str, int]:
+        return {"num_nodes": self.num_nodes, "num_edges": self.num_edges, "edge_feat_dim": self.edge_feat_dim,
+                "node_feat_dim": self.node_feat_dim}

@@ -1,0 +1,112 @@
+"""Build a CTDGOnlineRuntime from a session config (backends/ctdg/runtime/factory.py:20-178
+in the reference). Construction order is the reference's -- dataset, sampler,
+memory bank, model, memory updater -- so a seeded run draws the same initial
+weights. The optimizer is a fused HIP Adam over the trainable parameters."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import torch
+
+from starry_unigraph.native.step import FusedAdam
+from starry_unigraph.types import RuntimeBundle, SessionContext
+
+from .data import TGTemporalDataset
+from .memory import CTDGMemoryBank
+from .models import CTDGMemoryUpdater, build_ctdg_model
+from .runtime import CTDGOnlineRuntime
+from .sampler import NativeTemporalSampler
+
+
+class _SingleRankRoute:
+    """The reference's CTDGFeatureRoute is multi-rank only; one GPU needs none."""
+
+    def __init__(self, route_type: str, world_size: int):
+        self.route_type, self.world_size = route_type, world_size
+
+    def describe(self) -> dict:
+        return {"route_type": self.route_type, "world_size": self.world_size}
+
+
+def build_ctdg_runtime(session_ctx: SessionContext, events=None) -> tuple[CTDGOnlineRuntime, RuntimeBundle]:
+    cfg = session_ctx.config
+    root = session_ctx.dataset_path or Path(cfg["data"]["root"]).expanduser().resolve()
+    dataset = TGTemporalDataset(root, cfg["data"]["name"], split_ratio=cfg.get("data", {}).get("split_ratio"),
+                                config=cfg, events=events)
+    device = str(cfg["runtime"]["device"])
+    hidden_dim = int(cfg["model"]["hidden_dim"])
+    c = cfg.get("ctdg", {})
+    mailbox_slots = int(c.get("mailbox_slots", 4))
+    dim_time = int(c.get("dim_time", 100))
+    num_head = int(c.get("num_head", 2))
+    dropout = float(c.get("dropout", 0.1))
+    att_dropout = float(c.get("att_dropout", 0.1))
+    sampler = NativeTemporalSampler(dataset=dataset, fanout=list(cfg["sampling"]["neighbor_limit"]),
+                                    history=int(cfg["sampling"]["history"]),
+                                    strategy=str(cfg["sampling"]["strategy"]),
+                                    workers=max(1, min(4, session_ctx.dist.local_world_size or 1)))
+    edge_feat_dim = max(1, dataset.edge_feat_dim)
+    dataset.configure_partition(node_parts=None, edge_parts=None, rank=session_ctx.dist.rank,
+                                world_size=session_ctx.dist.world_size)
+    memory = CTDGMemoryBank(num_nodes=dataset.num_nodes, hidden_dim=hidden_dim, device=device,
+                            mailbox_slots=mailbox_slots, edge_feat_dim=edge_feat_dim)
+    model = build_ctdg_model(str(cfg["model"]["family"]), num_nodes=dataset.num_nodes, hidden_dim=hidden_dim,
+                             edge_feat_dim=edge_feat_dim, dim_time=dim_time, num_head=num_head, dropout=dropout,
+                             att_dropout=att_dropout).to(device)
+    memory_updater = CTDGMemoryUpdater(hidden_dim=hidden_dim, mailbox_slot_dim=2 * hidden_dim + edge_feat_dim,
+                                       mailbox_slots=mailbox_slots).to(device)
+    optimizer = make_optimizer(model, lr=float(cfg.get("train", {}).get("lr", 1e-3)))
+    runtime = CTDGOnlineRuntime(dataset=dataset, sampler=sampler, memory=memory, model=model, optimizer=optimizer,
+                                route=_SingleRankRoute(str(cfg["graph"]["route"]), session_ctx.dist.world_size),
+                                device=device, dist_ctx=session_ctx.dist, memory_updater=memory_updater,
+                                max_batch=int(cfg["train"]["batch_size"]))
+    optimizer.gate_fn = lambda: runtime.step.buf.any_edges
+    optimizer.inner  # re-seat the parameters in the optimizer's flat buffers before any forward
+    bundle = RuntimeBundle(model=model, optimizer=optimizer,
+                           state={"pipeline": "ctdg_online_native", "dataset": dataset.describe(),
+                                  "memory_state": memory.describe(), "route_state": runtime.route.describe()})
+    return runtime, bundle
+
+
+def make_optimizer(model: torch.nn.Module, lr: float) -> "GatedAdam":
+    return GatedAdam(model, lr)
+
+
+class GatedAdam:
+    """Adam over the link predictor's parameters (factory.py:122-128). The
+    attention's segment is gated by the step's "block has edges" flag (when
+    it is 0 those parameters have no gradient in the reference, and Adam
+    skips them). The memory updater gets no gradients in the reference
+    (runtime.py:279) and is not optimised."""
+
+    def __init__(self, model: torch.nn.Module, lr: float):
+        self.model = model
+        self.lr = lr
+        self._inner: FusedAdam | None = None
+        self.gate_fn = None
+
+    def _build(self) -> FusedAdam:
+        core = self.model.module if hasattr(self.model, "module") else self.model
+        conv = list(core.conv.parameters())
+        conv_ids = {id(p) for p in conv}
+        rest = [p for p in core.parameters() if id(p) not in conv_ids]
+        return FusedAdam([conv, rest], lr=self.lr)
+
+    @property
+    def inner(self) -> FusedAdam:
+        if self._inner is None:
+            self._inner = self._build()
+        return self._inner
+
+    def zero_grad(self, set_to_none: bool = False) -> None:
+        self.inner.zero_grad()
+
+    def step(self) -> None:
+        gate = self.gate_fn() if self.gate_fn is not None else None
+        self.inner.step([gate, None])
+
+    def state_dict(self) -> dict:
+        return self.inner.state_dict()
+
+    def load_state_dict(self, sd: dict) -> None:
+        self.inner.load_state_dict(sd)

@@ -1,0 +1,170 @@
+"""CTDG model components backed by the MI355X kernels.
+
+Module structure, parameter names and construction order follow the
+reference (backends/ctdg/runtime/models.py), so state dicts are
+interchangeable and a seeded construction draws the same initial weights:
+
+* ``TemporalTransformerConv`` (models.py:35-137): TimeEncode, w_q, w_k, w_v,
+  w_out, LayerNorm. Its forward runs the fused HIP attention kernels over a
+  device block (the padded hop-0 sample of the step's roots) instead of a
+  DGL block; backward is the matching HIP kernel plus weight-gradient GEMMs.
+* ``CTDGMemoryUpdater`` (models.py:214-254): nn.GRU(2D+F -> D) over the K
+  mailbox slots, then nn.GRUCell(D, D). Evaluated by the fused GRU kernel;
+  it never receives gradients in the reference (its output is detached,
+  runtime.py:279), so it is forward-only here.
+* ``CTDGLinkPredictor`` (models.py:261-324) and ``build_ctdg_model``
+  (models.py:327-386). The edge predictor (three nn.Linear) and the BCE loss
+  run in torch.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from starry_unigraph.lib import _capi
+from starry_unigraph.native.step import ConvFunction, DeviceStep
+from starry_unigraph.runtime.modules import TimeEncode
+
+
+class TemporalTransformerConv(nn.Module):
+    """Single-layer temporal multi-head attention (models.py:35-137)."""
+
+    def __init__(self, dim_node: int, dim_edge: int, dim_time: int, num_head: int, dim_out: int,
+                 dropout: float = 0.1, att_dropout: float = 0.1) -> None:
+        super().__init__()
+        if dim_time <= 0:
+            raise ValueError("TemporalTransformerConv: the MI355X kernels need dim_time > 0")
+        if dim_out != dim_node:
+            raise ValueError("TemporalTransformerConv: dim_out must equal dim_node (the CTDG path uses hidden_dim)")
+        if dim_out % num_head:
+            raise ValueError("TemporalTransformerConv: dim_out must be divisible by num_head")
+        self.num_head = num_head
+        self.dim_node = dim_node
+        self.dim_edge = dim_edge
+        self.dim_time = dim_time
+        self.dim_out = dim_out
+        self.time_enc = TimeEncode(dim_time)
+        self.w_q = nn.Linear(dim_node + dim_time, dim_out)
+        self.w_k = nn.Linear(dim_node + dim_edge + dim_time, dim_out)
+        self.w_v = nn.Linear(dim_node + dim_edge + dim_time, dim_out)
+        self.w_out = nn.Linear(dim_node + dim_out, dim_out)
+        self.dropout = nn.Dropout(dropout)
+        self.att_dropout = nn.Dropout(att_dropout)
+        self.att_act = nn.LeakyReLU(0.2)
+        self.layer_norm = nn.LayerNorm(dim_out)
+
+    def kernel_params(self) -> list[torch.Tensor]:
+        return [self.time_enc.w.weight, self.time_enc.w.bias, self.w_q.weight, self.w_q.bias, self.w_k.weight,
+                self.w_k.bias, self.w_v.weight, self.w_v.bias, self.w_out.weight, self.w_out.bias,
+                self.layer_norm.weight, self.layer_norm.bias]
+
+    def forward(self, step: DeviceStep, edge_feat_all: torch.Tensor) -> torch.Tensor:
+        """Embeddings [capacity, D] of the step's roots (rows >= the live root
+        count are zero)."""
+        if self.training and (self.dropout.p > 0 or self.att_dropout.p > 0):
+            raise NotImplementedError(
+                "dropout > 0 is not implemented by the MI355X attention kernels; set ctdg.dropout and "
+                "ctdg.att_dropout to 0")
+        return ConvFunction.apply(step, edge_feat_all, *self.kernel_params())
+
+
+@dataclass
+class CTDGModelOutput:
+    pos_logits: torch.Tensor
+    neg_logits: torch.Tensor
+
+
+class CTDGMemoryUpdater(nn.Module):
+    """GRU over the K-slot mailbox, then GRUCell with the memory (models.py:214-254)."""
+
+    def __init__(self, hidden_dim: int, mailbox_slot_dim: int, mailbox_slots: int) -> None:
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.mailbox_slots = mailbox_slots
+        self.mail_aggregator = nn.GRU(input_size=mailbox_slot_dim, hidden_size=hidden_dim, batch_first=True)
+        self.memory_cell = nn.GRUCell(hidden_dim, hidden_dim)
+
+    def kernel_weights(self) -> dict[str, torch.Tensor]:
+        g, c = self.mail_aggregator, self.memory_cell
+        return {"w_ih": g.weight_ih_l0.detach(), "w_hh": g.weight_hh_l0.detach(), "b_ih": g.bias_ih_l0.detach(),
+                "b_hh": g.bias_hh_l0.detach(), "wc_ih": c.weight_ih.detach(), "wc_hh": c.weight_hh.detach(),
+                "bc_ih": c.bias_ih.detach(), "bc_hh": c.bias_hh.detach()}
+
+    @torch.no_grad()
+    def forward(self, mailbox_history: torch.Tensor, current_memory: torch.Tensor) -> torch.Tensor:
+        """mailbox_history [M, K, S], current_memory [M, D] -> [M, D], through
+        the fused GRU kernel (rows addressed by an identity root list)."""
+        M = mailbox_history.size(0)
+        if M == 0:
+            return current_memory.clone()
+        dev = _capi.require_gpu(current_memory.device)
+        D = self.hidden_dim
+        K = mailbox_history.size(1)
+        S = mailbox_history.size(2)
+        Fd = S - 2 * D
+        mail = mailbox_history.to(dev, torch.float32).contiguous()
+        mem = current_memory.to(dev, torch.float32).contiguous()
+        cap = (M + 15) // 16 * 16
+        roots = torch.arange(M, dtype=torch.int64, device=dev)
+        n = torch.tensor([M], dtype=torch.int32, device=dev)
+        zeros_i = torch.zeros(cap, dtype=torch.int32, device=dev)
+        zeros_k = torch.zeros(cap, dtype=torch.int64, device=dev)
+        out = torch.empty(cap, D, dtype=torch.float32, device=dev)
+        w = self.kernel_weights()
+        P = _capi.ptr
+        dummy_i64 = torch.zeros(1, dtype=torch.int64, device=dev)
+        dummy_f = torch.zeros(max(Fd, 1), dtype=torch.float32, device=dev)
+        mts = torch.zeros(M, K, dtype=torch.float32, device=dev)
+        nmp = torch.zeros(M, dtype=torch.int32, device=dev)
+        _capi.check(_capi.lib().sgl_memory_update(
+            D, K, Fd, cap, P(n), P(roots), P(mem), P(mail), P(mts), P(nmp), P(w["w_ih"]), P(w["w_hh"]),
+            P(w["b_ih"]), P(w["b_hh"]), P(w["wc_ih"]), P(w["wc_hh"]), P(w["bc_ih"]), P(w["bc_hh"]), P(dummy_i64),
+            P(dummy_i64), P(dummy_f), P(dummy_f), P(zeros_k), P(zeros_k), P(zeros_i), P(zeros_i), P(out),
+            _capi.stream_of(dev)), "sgl_memory_update")
+        return out[:M]
+
+
+class CTDGLinkPredictor(nn.Module):
+    """Temporal attention + edge predictor (models.py:261-324)."""
+
+    def __init__(self, num_nodes: int, hidden_dim: int, edge_feat_dim: int, dim_time: int = 100, num_head: int = 2,
+                 dropout: float = 0.1, att_dropout: float = 0.1) -> None:
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.conv = TemporalTransformerConv(dim_node=hidden_dim, dim_edge=edge_feat_dim, dim_time=dim_time,
+                                            num_head=num_head, dim_out=hidden_dim, dropout=dropout,
+                                            att_dropout=att_dropout)
+        self.src_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.dst_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.out_fc = nn.Linear(hidden_dim, 1)
+
+    def forward(self, src_conv: torch.Tensor, dst_conv: torch.Tensor, neg_conv: torch.Tensor) -> CTDGModelOutput:
+        h_src = self.src_fc(src_conv)
+        h_dst = self.dst_fc(dst_conv)
+        h_neg = self.dst_fc(neg_conv)
+        pos_logits = self.out_fc(F.relu(h_src + h_dst)).squeeze(-1)
+        neg_logits = self.out_fc(F.relu(h_src + h_neg)).squeeze(-1)
+        return CTDGModelOutput(pos_logits=pos_logits, neg_logits=neg_logits)
+
+
+@dataclass(frozen=True)
+class CTDGModelSpec:
+    model_cls: type[nn.Module]
+
+
+# One implementation serves the CTDG families the reference registers (models.py:332-342).
+CTDG_MODEL_SPECS: dict[str, CTDGModelSpec] = {
+    name: CTDGModelSpec(CTDGLinkPredictor) for name in ("tgn", "jodie", "dyrep", "tgat", "apan")
+}
+
+
+def build_ctdg_model(model_family: str, *, num_nodes: int, hidden_dim: int, edge_feat_dim: int, dim_time: int = 100,
+                     num_head: int = 2, dropout: float = 0.1, att_dropout: float = 0.1) -> nn.Module:
+    spec = CTDG_MODEL_SPECS.get(model_family.lower())
+    if spec is None:
+        raise KeyError(f"Unsupported CTDG model family: {model_family}")
+    return spec.model_cls(num_nodes=num_nodes, hidden_dim=hidden_dim, edge_feat_dim=edge_feat_dim,
+                          dim_time=dim_time, num_head=num_head, dropout=dropout, att_dropout=att_dropout)

@@ -1,0 +1,234 @@
+"""CTDG online runtime (backends/ctdg/runtime/runtime.py:39-391 in the reference).
+
+``train_step`` / ``eval_step`` / ``predict_step`` keep the reference's
+signatures and result dicts. Inside, a step is the device kernel sequence of
+starry_unigraph.native.step over the HBM-resident event stream:
+
+  negatives (CPU generator, runtime.py:124-136) -> sgl_batch_prepare ->
+  sgl_recent_sample (hop 0 of the split's sampler) -> sgl_memory_update ->
+  sgl_memory_commit -> attention forward -> edge predictor + BCE (torch) ->
+  backward -> Adam
+
+Differences by design: the attention runs once per step and its rows are
+selected for src / dst / negatives (the reference runs it three times with
+three dropout masks, runtime.py:193-195 -- identical when dropout is 0, the
+only setting implemented here); no host synchronisation happens inside a step
+unless ``collect_results`` asks for the reference's Python-side result dict.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from typing import Any, Iterable
+
+import torch
+import torch.nn.functional as F
+
+from starry_unigraph.native.step import ConvDims, DeviceStep
+
+from .data import CTDGDataBatch, TGTemporalDataset
+from .memory import CTDGMemoryBank
+from .models import CTDGMemoryUpdater
+from .sampler import NativeTemporalSampler
+
+try:
+    from sklearn.metrics import average_precision_score, roc_auc_score
+except Exception:  # pragma: no cover
+    average_precision_score = None
+    roc_auc_score = None
+
+
+@dataclass
+class StepTensors:
+    """Device results of one step (no host sync)."""
+    loss: torch.Tensor
+    pos_logits: torch.Tensor
+    neg_logits: torch.Tensor
+    batch_size: int
+
+
+class CTDGOnlineRuntime:
+    def __init__(self, dataset: TGTemporalDataset, sampler: NativeTemporalSampler, memory: CTDGMemoryBank,
+                 model: torch.nn.Module, optimizer, route: Any, device: str, dist_ctx: Any,
+                 memory_updater: CTDGMemoryUpdater | None = None, max_batch: int | None = None):
+        self.dataset = dataset
+        self.sampler = sampler
+        self.memory = memory
+        self.model = model
+        self.optimizer = optimizer
+        self.route = route
+        self.device = torch.device(device)
+        self.dist_ctx = dist_ctx
+        self.memory_updater = memory_updater
+        self.collect_results = True
+        self._dst_node_pool: torch.Tensor | None = None
+        self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
+        core = self._core()
+        conv = core.conv
+        self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head,
+                             fanout=int(sampler.fanout[0]) if sampler.fanout else 0)
+        self.step = DeviceStep(memory.state, self.dims, int(max_batch or 1))
+        self._dev = dataset.device_arrays(self.device)
+        self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
+        self._zero_row = torch.zeros(1, memory.hidden_dim, device=self.device)
+
+    def _core(self):
+        return self.model.module if hasattr(self.model, "module") else self.model
+
+    # ------------------------------------------------------------- batching
+    def iter_batches(self, split: str, batch_size: int) -> Iterable[CTDGDataBatch]:
+        yield from self.dataset.iter_batches(split=split, batch_size=batch_size)
+
+    def _dst_pool(self) -> torch.Tensor:
+        if self._dst_node_pool is None:
+            self._dst_node_pool = self.dataset.dst.unique()
+        return self._dst_node_pool
+
+    def _negative_sample(self, batch: CTDGDataBatch) -> torch.Tensor:
+        """runtime.py:124-136: uniform over the sorted unique dst pool (global CPU
+        generator), collisions with the true dst bumped to the next pool entry."""
+        pool = self._dst_pool()
+        idx = torch.randint(low=0, high=pool.numel(), size=batch.dst.shape, dtype=torch.long)
+        neg = pool[idx]
+        col = neg.eq(batch.dst.cpu())
+        if col.any():
+            idx[col] = (idx[col] + 1) % pool.numel()
+            neg = pool[idx]
+        return neg
+
+    def precompute_negatives(self, split: str, batch_size: int) -> None:
+        """Draw the negatives of every batch of ``split`` in one call and keep them
+        in HBM. torch.randint on the CPU generator yields the same numbers in one
+        call as in per-batch calls, so this equals per-step sampling."""
+        pool = self._dst_pool()
+        ids = self.dataset.split_event_ids(split)
+        idx = torch.randint(low=0, high=pool.numel(), size=(ids.numel(),), dtype=torch.long)
+        dst = self.dataset.dst[ids]
+        neg = pool[idx]
+        col = neg.eq(dst)
+        if col.any():
+            idx[col] = (idx[col] + 1) % pool.numel()
+            neg = pool[idx]
+        self._neg_queue[split] = (neg.to(self.device), 0)
+
+    def _negatives(self, batch: CTDGDataBatch) -> torch.Tensor:
+        q = self._neg_queue.get(batch.split)
+        if q is not None:
+            buf, off = q
+            n = batch.size
+            if off + n <= buf.numel():
+                self._neg_queue[batch.split] = (buf, off + n)
+                return buf[off:off + n]
+            del self._neg_queue[batch.split]
+        return self._negative_sample(batch).to(self.device, non_blocking=True)
+
+    def _device_batch(self, batch: CTDGDataBatch):
+        d = self._dev
+        s = batch.start
+        n = batch.size
+        if s >= 0:
+            return (d["src"][s:s + n], d["dst"][s:s + n], d["ts"][s:s + n], d["edge_feat"][s:s + n])
+        ev = batch.event_ids.to(self.device)
+        return d["src"][ev], d["dst"][ev], d["ts"][ev], d["edge_feat"][ev].contiguous()
+
+    # ------------------------------------------------------------- the step
+    def _forward(self, batch: CTDGDataBatch, split: str, train: bool) -> StepTensors:
+        n = batch.size
+        if n > self.step.buf.max_batch:
+            self.step = DeviceStep(self.memory.state, self.dims, n)
+        src, dst, ts, ef = self._device_batch(batch)
+        neg = self._negatives(batch)
+        step = self.step
+        step.prepare(src, dst, neg, ts)
+        step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
+        if self._gru is not None:
+            step.update_memory(self._gru, src, dst, ef, ts)
+            step.commit()
+        core = self._core()
+        with torch.set_grad_enabled(train):
+            y = core.conv(step, self._dev["edge_feat"])
+            b = step.buf
+            rn = b.ridx_neg[:n].long()
+            e_s = y[b.ridx_src[:n].long()]
+            e_d = y[b.ridx_dst[:n].long()]
+            # runtime.py:176-182: a negative that is not a root gets a zero embedding
+            y_ext = torch.cat([y, self._zero_row.to(y.dtype)], dim=0)
+            e_n = y_ext[torch.where(rn >= 0, rn, torch.full_like(rn, y.shape[0]))]
+            out = self.model(src_conv=e_s, dst_conv=e_d, neg_conv=e_n)
+            pos, negl = out.pos_logits, out.neg_logits
+            loss = (F.binary_cross_entropy_with_logits(pos, torch.ones_like(pos))
+                    + F.binary_cross_entropy_with_logits(negl, torch.zeros_like(negl)))
+        if train:
+            self.optimizer.zero_grad(set_to_none=True)
+            loss.backward()
+            self.optimizer.step()
+        return StepTensors(loss.detach(), pos.detach(), negl.detach(), n)
+
+    def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
+        """runtime.py:202-214."""
+        pp = torch.sigmoid(pos_logits).detach().cpu()
+        pn = torch.sigmoid(neg_logits).detach().cpu()
+        scores = torch.cat([pp, pn]).numpy()
+        labels = torch.cat([torch.ones_like(pp), torch.zeros_like(pn)]).numpy()
+        m: dict[str, float] = {}
+        if average_precision_score is not None:
+            m["ap"] = float(average_precision_score(labels, scores))
+        if roc_auc_score is not None:
+            m["auc"] = float(roc_auc_score(labels, scores))
+        m["mrr"] = float((pp.unsqueeze(1) > pn.unsqueeze(0)).float().mean().item())
+        return m
+
+    def _sample_meta(self, n: int) -> dict[str, int]:
+        b = self.step.buf
+        u = int(b.num_roots.item())
+        cnt = b.hop.cnt[:u]
+        k = self.dims.fanout
+        valid = torch.arange(k, device=cnt.device).unsqueeze(0) < cnt.unsqueeze(1)
+        nbr = b.hop.nbr[:u * k].view(u, k)[valid].long() if k > 0 else torch.empty(0, dtype=torch.long,
+                                                                                   device=cnt.device)
+        eid = b.hop.eid[:u * k].view(u, k)[valid] if k > 0 else nbr
+        return {"root_count": u, "sampled_node_count": int(torch.unique(torch.cat([b.roots[:u], nbr])).numel()),
+                "sampled_edge_count": int(torch.unique(eid).numel()), "num_layers": len(self.sampler.fanout[:1])}
+
+    def _empty_result(self, batch: CTDGDataBatch, split: str) -> dict[str, Any]:
+        return {"loss": 0.0, "predictions": [], "targets": [],
+                "meta": {"split": split, "batch_size": 0, "metrics": {}, "memory": self.memory.describe(),
+                         "empty_batch": True}}
+
+    def train_step(self, batch: CTDGDataBatch) -> dict[str, Any]:
+        self.model.train()
+        t0 = time.perf_counter()
+        if batch.is_empty:
+            return self._empty_result(batch, batch.split)
+        st = self._forward(batch, batch.split, train=True)
+        if not self.collect_results:
+            return {"loss": st.loss, "pos_logits": st.pos_logits, "neg_logits": st.neg_logits,
+                    "meta": {"split": batch.split, "batch_size": st.batch_size}}
+        step_ms = (time.perf_counter() - t0) * 1000.0
+        return {"loss": float(st.loss.item()), "predictions": torch.sigmoid(st.pos_logits).cpu().tolist(),
+                "targets": [1] * batch.size,
+                "meta": {"split": batch.split, "batch_size": batch.size, "sample": self._sample_meta(batch.size),
+                         "metrics": self._metric_dict(st.pos_logits, st.neg_logits),
+                         "memory": self.memory.describe(), "sync_wait_ms": 0.0, "sync_submit_ms": 0.0,
+                         "step_ms": step_ms}}
+
+    def eval_step(self, batch: CTDGDataBatch, split: str) -> dict[str, Any]:
+        """runtime.py:330-386: no grad, memory and mailbox still updated."""
+        self.model.eval()
+        if batch.is_empty:
+            return self._empty_result(batch, split)
+        with torch.no_grad():
+            st = self._forward(batch, split, train=False)
+        if not self.collect_results:
+            return {"loss": st.loss, "pos_logits": st.pos_logits, "neg_logits": st.neg_logits,
+                    "meta": {"split": split, "batch_size": st.batch_size}}
+        return {"loss": float(st.loss.item()), "predictions": torch.sigmoid(st.pos_logits).cpu().tolist(),
+                "targets": [1] * batch.size,
+                "meta": {"split": split, "batch_size": batch.size,
+                         "metrics": self._metric_dict(st.pos_logits, st.neg_logits),
+                         "memory": self.memory.describe()}}
+
+    def predict_step(self, batch: CTDGDataBatch) -> dict[str, Any]:
+        r = self.eval_step(batch, split=batch.split)
+        r["meta"]["predict"] = True
+        return r

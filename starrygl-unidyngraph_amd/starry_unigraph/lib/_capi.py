@@ -32,11 +32,19 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_last_error": (ctypes.c_char_p, []),
     "sgl_tcsr_workspace_bytes": (_sz, [_i64, _i64]),
     "sgl_tcsr_build": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
-    "sgl_recent_sample": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _i32, _i32,
+    "sgl_recent_sample": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _vp, _i32, _i32,
                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "sgl_compact_workspace_bytes": (_sz, [_i64]),
     "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),
+    "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 22),
+    "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
+    "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 24),
+    "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 31),
+    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 37),
+    "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
+    "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
 }
 
 _lock = threading.Lock()

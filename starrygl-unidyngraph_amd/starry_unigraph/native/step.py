@@ -1,0 +1,283 @@
+"""Device side of one CTDG step: HBM-resident node state, capacity-sized step
+buffers and the kernel sequence (all through the C ABI, no host syncs).
+
+Kernel order of a training step (reference: CTDGOnlineRuntime.train_step,
+backends/ctdg/runtime/runtime.py:225-297):
+
+  sgl_batch_prepare   roots, query time, per-role last writers     (runtime.py:138-144)
+  sgl_recent_sample   hop-0 recent-k windows of the roots          (sampler.py:93-128)
+  sgl_memory_update   GRU over mailbox + memory, mailbox write     (runtime.py:268-282)
+  sgl_memory_commit   memory/memory_ts scatter                     (memory.py:254-269)
+  sgl_conv_forward    time encoding + temporal attention           (models.py:77-137)
+  (predictor + BCE in torch autograd)                              (models.py:313-324, runtime.py:290-292)
+  sgl_conv_backward   attention backward; weight-gradient GEMMs
+  sgl_adam_step       Adam, the attention segment gated by "block has edges"
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from starry_unigraph.lib import _capi
+from starry_unigraph.native.tcsr import PaddedHop, RecentSampler
+
+TILE = 16
+
+
+def _round_up(x: int, m: int) -> int:
+    return (x + m - 1) // m * m
+
+
+class NodeState:
+    """Per-node memory and K-slot mailbox in HBM (memory.py:98-102):
+    memory [N,D] f32 = 0, mailbox [N,K,2D+F] f32 = 0, mailbox_ts [N,K] = 0,
+    memory_ts [N] = -1, next_mail_pos [N] (int32 here) = 0; plus the node
+    bitmap the batch preparation uses (kept all-zero between steps)."""
+
+    def __init__(self, num_nodes: int, hidden_dim: int, slots: int, edge_dim: int, device):
+        dev = _capi.require_gpu(device)
+        self.device = dev
+        self.N, self.D, self.K, self.F = int(num_nodes), int(hidden_dim), int(slots), int(edge_dim)
+        self.S = 2 * self.D + self.F
+        with torch.cuda.device(dev):
+            self.memory = torch.zeros(self.N, self.D, dtype=torch.float32, device=dev)
+            self.mailbox = torch.zeros(self.N, self.K, self.S, dtype=torch.float32, device=dev)
+            self.mailbox_ts = torch.zeros(self.N, self.K, dtype=torch.float32, device=dev)
+            self.memory_ts = torch.full((self.N,), -1.0, dtype=torch.float32, device=dev)
+            self.next_mail_pos = torch.zeros(self.N, dtype=torch.int32, device=dev)
+            nwords = (self.N + 31) // 32
+            self.node_bits = torch.zeros(nwords, dtype=torch.int32, device=dev)
+            self.word_prefix = torch.zeros(nwords, dtype=torch.int32, device=dev)
+
+    def reset(self) -> None:
+        self.memory.zero_()
+        self.mailbox.zero_()
+        self.mailbox_ts.zero_()
+        self.memory_ts.fill_(-1.0)
+        self.next_mail_pos.zero_()
+        self.node_bits.zero_()
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in
+                   (self.memory, self.mailbox, self.mailbox_ts, self.memory_ts, self.next_mail_pos))
+
+
+@dataclass
+class ConvDims:
+    D: int
+    F: int
+    T: int
+    H: int
+    fanout: int
+
+    @property
+    def C(self) -> int:
+        return self.D + self.F + self.T
+
+
+class StepBuffers:
+    """Scratch for batches of up to ``max_batch`` events; root-indexed arrays
+    hold cap = round_up(2*max_batch, 16) rows (the most roots a batch can
+    have), so launch shapes never depend on the batch."""
+
+    def __init__(self, max_batch: int, dims: ConvDims, device):
+        dev = torch.device(device)
+        self.device = dev
+        self.max_batch = int(max_batch)
+        self.cap = _round_up(max(2 * self.max_batch, TILE), TILE)
+        c, B, D, H, C, k = self.cap, self.max_batch, dims.D, dims.H, dims.C, dims.fanout
+        z = lambda *s, dt=torch.float32: torch.zeros(*s, dtype=dt, device=dev)
+        i32, i64 = torch.int32, torch.int64
+        self.num_roots = z(1, dt=i32)
+        self.num_roots64 = z(1, dt=i64)
+        self.ts_max = z(1)
+        self.t_query = z(1, dt=i64)
+        self.any_edges = z(1, dt=i32)
+        self.err = _capi.ErrorFlag(dev)
+        self.roots = z(c, dt=i64)
+        self.root_ts = z(c, dt=i64)
+        self.ridx_src = z(max(B, 1), dt=i32)
+        self.ridx_dst = z(max(B, 1), dt=i32)
+        self.ridx_neg = z(max(B, 1), dt=i32)
+        self.win_src = z(c, dt=i64)
+        self.win_dst = z(c, dt=i64)
+        self.cnt_src = z(c, dt=i32)
+        self.cnt_dst = z(c, dt=i32)
+        self.new_mem = z(c, D)
+        self.hop = PaddedHop(cnt=z(c, dt=i32), nbr=z(max(c * k, 1), dt=i32), eid=z(max(c * k, 1), dt=i32),
+                             dt=z(max(c * k, 1)), ts=None, q_ts=self.root_ts, fanout=k)
+        # attention saved state and gradients
+        self.Q, self.agg, self.z, self.y = z(c, D), z(c, D), z(c, D), z(c, D)
+        self.qt, self.xbar = z(c, H, C), z(c, H, C)
+        self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
+        self.gz, self.gagg, self.gQ = z(c, D), z(c, D), z(c, D)
+        self.G, self.sigma = z(c, H, C), z(c, H)
+        self.ln_part = z(c // TILE, 2, D)
+        self.te_part = z(c // TILE, 2, max(dims.T, 1))
+
+
+class DeviceStep:
+    """The kernel sequence of one step over a NodeState (no host syncs)."""
+
+    def __init__(self, state: NodeState, dims: ConvDims, max_batch: int):
+        self.state = state
+        self.dims = dims
+        self.buf = StepBuffers(max_batch, dims, state.device)
+        self.dev = state.device
+        self.lib = _capi.lib()
+
+    def _s(self) -> int:
+        return _capi.stream_of(self.dev)
+
+    # -- batch preparation --------------------------------------------------
+    def prepare(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor) -> None:
+        b, st, P = self.buf, self.state, _capi.ptr
+        n = src.numel()
+        if n > b.max_batch:
+            raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
+        _capi.check(self.lib.sgl_batch_prepare(
+            st.N, n, P(src), P(dst), P(neg), P(ts), P(st.node_bits), P(st.word_prefix), P(b.num_roots),
+            P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
+            P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
+            self._s()), "sgl_batch_prepare")
+
+    def sample(self, sampler: RecentSampler) -> PaddedHop:
+        b = self.buf
+        return sampler.sample(b.roots, b.root_ts, self.dims.fanout, out=b.hop, num_live=b.num_roots64)
+
+    # -- memory -------------------------------------------------------------
+    def update_memory(self, gru: dict, src, dst, efeat, ts) -> None:
+        b, st, P = self.buf, self.state, _capi.ptr
+        _capi.check(self.lib.sgl_memory_update(
+            st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
+            P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
+            P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(b.win_src),
+            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), "sgl_memory_update")
+
+    def commit(self) -> None:
+        b, st, P = self.buf, self.state, _capi.ptr
+        _capi.check(self.lib.sgl_memory_commit(
+            st.D, b.cap, P(b.num_roots), P(b.roots), P(b.new_mem), P(st.memory), P(st.memory_ts), P(b.ts_max),
+            P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit")
+
+    # -- attention ----------------------------------------------------------
+    def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
+        b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
+        hop = b.hop
+        _capi.check(self.lib.sgl_conv_forward(
+            d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
+            P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
+            P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
+            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.y), self._s()), "sgl_conv_forward")
+        return b.y
+
+    def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
+        """Returns the 12 parameter gradients (TimeEncode w, b; w_q, b_q, w_k,
+        b_k, w_v, b_v, w_out, b_out, ln weight, ln bias)."""
+        b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
+        hop = b.hop
+        gy = gy.contiguous()
+        _capi.check(self.lib.sgl_conv_backward(
+            d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
+            P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
+            P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
+            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(gy), P(b.gz), P(b.gagg), P(b.G), P(b.sigma), P(b.gQ),
+            P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward")
+        # weight gradients: per-root products reduced over the root rows (rows
+        # past the live roots are zero in gz/gagg/G/sigma/gQ)
+        D, H, C, T = d.D, d.H, d.C, d.T
+        dh = D // H
+        c = b.cap
+        g_w_out = torch.cat([b.gz.t() @ b.agg, b.gz.t() @ b.new_mem], dim=1)
+        g_b_out = b.gz.sum(0)
+        ga = b.gagg.view(c, H, dh).permute(1, 2, 0).contiguous()          # [H, dh, cap]
+        g_w_v = torch.bmm(ga, b.xbar.permute(1, 0, 2).contiguous()).reshape(D, C)
+        g_b_v = b.gagg.sum(0)
+        qh = b.Q.view(c, H, dh)
+        g_w_k = torch.bmm(qh.permute(1, 2, 0).contiguous(), b.G.permute(1, 0, 2).contiguous()).reshape(D, C)
+        g_b_k = (qh * b.sigma.unsqueeze(-1)).sum(0).reshape(D)
+        sq = b.gQ.sum(0)
+        phi0 = torch.cos(te_b)
+        g_w_q = torch.cat([b.gQ.t() @ b.new_mem, torch.outer(sq, phi0)], dim=1)
+        g_b_q = sq
+        g_ln_g = b.ln_part[:, 0].sum(0)
+        g_ln_b = b.ln_part[:, 1].sum(0)
+        te = b.te_part[:, :, :T].sum(0)
+        g_te_w = te[0].reshape(T, 1)
+        g_te_b = te[1] + (w_q[:, D:].t() @ sq) * (-torch.sin(te_b))
+        return [g_te_w, g_te_b, g_w_q, g_b_q, g_w_k, g_b_k, g_w_v, g_b_v, g_w_out, g_b_out, g_ln_g, g_ln_b]
+
+
+class ConvFunction(torch.autograd.Function):
+    """Autograd node for the attention: forward/backward are the HIP kernels."""
+
+    @staticmethod
+    def forward(ctx, step: DeviceStep, efeat_all: torch.Tensor, *params):
+        ctx.step = step
+        ctx.efeat_all = efeat_all
+        ctx.params = params
+        return step.conv_forward(list(params), efeat_all)
+
+    @staticmethod
+    def backward(ctx, gy):
+        grads = ctx.step.conv_backward(list(ctx.params), ctx.efeat_all, gy)
+        return (None, None, *grads)
+
+
+class FusedAdam:
+    """torch.optim.Adam arithmetic over flat HIP segments. Parameters are
+    re-seated as views of one flat buffer and their .grad as views of one flat
+    gradient buffer; each segment may carry a device gate (see sgl_adam_step)."""
+
+    def __init__(self, segments: list[list[torch.nn.Parameter]], lr: float = 1e-3,
+                 betas=(0.9, 0.999), eps: float = 1e-8, weight_decay: float = 0.0):
+        self.lr, self.betas, self.eps, self.wd = float(lr), betas, float(eps), float(weight_decay)
+        params = [p for seg in segments for p in seg]
+        if not params:
+            raise ValueError("FusedAdam: no parameters")
+        dev = params[0].device
+        n = sum(p.numel() for p in params)
+        self.flat = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.flat_grad = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.exp_avg = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.exp_avg_sq = torch.zeros(n, dtype=torch.float32, device=dev)
+        self.segments = []
+        off = 0
+        for seg in segments:
+            start = off
+            for p in seg:
+                k = p.numel()
+                self.flat[off:off + k].copy_(p.data.reshape(-1))
+                p.data = self.flat[off:off + k].view_as(p)
+                p.grad = self.flat_grad[off:off + k].view_as(p)
+                off += k
+            self.segments.append((start, off - start, torch.zeros(1, dtype=torch.float32, device=dev)))
+        self.params = params
+
+    def zero_grad(self, set_to_none: bool = False) -> None:
+        self.flat_grad.zero_()
+
+    def step(self, gates: list[torch.Tensor | None] | None = None) -> None:
+        """``gates[i]``: device int32 gating segment i (None = always update)."""
+        lib, P = _capi.lib(), _capi.ptr
+        s = _capi.stream_of(self.flat.device)
+        b1, b2 = self.betas
+        gates = gates or [None] * len(self.segments)
+        for (start, n, stepc), gate in zip(self.segments, gates):
+            _capi.check(lib.sgl_adam_step(n, P(self.flat[start:start + n]), P(self.flat_grad[start:start + n]),
+                                          P(self.exp_avg[start:start + n]), P(self.exp_avg_sq[start:start + n]),
+                                          P(stepc), P(gate), self.lr, b1, b2, self.eps, self.wd, s), "sgl_adam_step")
+            _capi.check(lib.sgl_adam_advance(P(stepc), P(gate), s), "sgl_adam_advance")
+
+    def state_dict(self) -> dict:
+        return {"exp_avg": self.exp_avg.clone(), "exp_avg_sq": self.exp_avg_sq.clone(),
+                "steps": [seg[2].clone() for seg in self.segments], "lr": self.lr}
+
+    def load_state_dict(self, sd: dict) -> None:
+        self.exp_avg.copy_(sd["exp_avg"])
+        self.exp_avg_sq.copy_(sd["exp_avg_sq"])
+        for seg, st in zip(self.segments, sd["steps"]):
+            seg[2].copy_(st)

@@ -125,9 +125,10 @@ class RecentSampler:
 
     def sample(self, nodes: torch.Tensor, q_ts: torch.Tensor, fanout: int, want_ts: bool = False,
                valid_cnt: torch.Tensor | None = None, stride: int = 0,
-               out: PaddedHop | None = None) -> PaddedHop:
+               out: PaddedHop | None = None, num_live: torch.Tensor | None = None) -> PaddedHop:
         """One hop, padded layout, no host synchronisation. With ``valid_cnt``,
-        query i is live only if ``i % stride < valid_cnt[i // stride]``."""
+        query i is live only if ``i % stride < valid_cnt[i // stride]``; with
+        ``num_live`` (a device int64 scalar) only queries i < num_live are."""
         dev = self.dev
         if nodes.device != dev or nodes.dtype not in (torch.int64, torch.int32):
             nodes = nodes.to(device=dev, dtype=torch.int64)
@@ -160,7 +161,7 @@ class RecentSampler:
             _capi.check(_capi.lib().sgl_recent_sample(
                 _capi.ptr(g.indptr), _capi.ptr(g.nbr), _capi.ptr(g.eid), _capi.ptr(g.ts), g.num_nodes,
                 _capi.ptr(nodes), 1 if nodes.dtype == torch.int64 else 0, _capi.ptr(q_ts), nq,
-                _capi.ptr(valid_cnt), int(stride), fanout,
+                _capi.ptr(num_live), _capi.ptr(valid_cnt), int(stride), fanout,
                 _capi.ptr(hop.cnt), _capi.ptr(hop.nbr), _capi.ptr(hop.eid), _capi.ptr(hop.dt),
                 _capi.ptr(hop.ts), _capi.ptr(self.err.t), _capi.stream_of(dev)), "sgl_recent_sample")
         return hop

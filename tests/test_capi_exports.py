@@ -49,7 +49,7 @@ def test_host_side_queries_need_no_gpu():
 def test_argument_errors_are_reported_without_a_gpu():
     from starry_unigraph.lib import _capi
     lib = _capi.load_library()
-    rc = lib.sgl_recent_sample(None, None, None, None, 10, None, 1, None, 5, None, 0, -3,
+    rc = lib.sgl_recent_sample(None, None, None, None, 10, None, 1, None, 5, None, None, 0, -3,
                                None, None, None, None, None, None, None)
     assert rc == 1
     assert b"fanout" in lib.sgl_last_error()

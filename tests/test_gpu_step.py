@@ -1,0 +1,330 @@
+"""GPU parity of the CTDG step kernels against the CPU oracle.
+
+Tolerances (fp32 path): rtol 1e-3 on memory, embeddings, loss and gradients
+(atol scaled to the quantity's magnitude); integer outputs (roots, indices,
+slot pointers) and mailbox contents given identical pre-step memory are
+bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import ctdg_oracle as co
+import sampler_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-3
+
+
+def _close(got, want, rtol=RTOL, atol=1e-5, msg=""):
+    torch.testing.assert_close(got.detach().cpu().double(), want.detach().cpu().double(), rtol=rtol, atol=atol,
+                               msg=msg)
+
+
+@pytest.mark.parametrize("K,D,F", [(1, 100, 16), (3, 32, 5), (4, 172, 16)])
+def test_gru_kernel_matches_torch(gpu, K, D, F):
+    from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
+    torch.manual_seed(K)
+    S = 2 * D + F
+    up = CTDGMemoryUpdater(D, S, K).to(gpu)
+    ref = co.MemoryUpdaterO(D, S, K)
+    ref.load_state_dict({k: v.cpu() for k, v in up.state_dict().items()})
+    M = 203
+    mail = torch.randn(M, K, S)
+    mem = torch.randn(M, D)
+    got = up(mail.to(gpu), mem.to(gpu))
+    with torch.no_grad():
+        want = ref(mail, mem)
+    _close(got, want, atol=2e-5)
+
+
+def _small_batch(rng, n_nodes, B):
+    src = rng.integers(0, n_nodes, B)
+    dst = rng.integers(0, n_nodes, B)
+    ts = np.sort(rng.integers(0, 50, B)).astype(np.float32)   # ties on purpose
+    neg = rng.integers(0, n_nodes, B)
+    return src, dst, ts, neg
+
+
+def test_batch_prepare_matches_numpy(gpu):
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    rng = np.random.default_rng(0)
+    N, B = 5000, 600
+    st = NodeState(N, 8, 2, 4, gpu)
+    step = DeviceStep(st, ConvDims(8, 4, 8, 2, 5), B)
+    for _ in range(3):
+        src, dst, ts, neg = _small_batch(rng, N, B)
+        T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
+        step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
+        b = step.buf
+        U = int(b.num_roots.item())
+        roots = np.unique(np.concatenate([src, dst]))
+        assert U == len(roots)
+        np.testing.assert_array_equal(b.roots[:U].cpu().numpy(), roots)
+        np.testing.assert_array_equal(b.ridx_src[:B].cpu().numpy(), np.searchsorted(roots, src))
+        np.testing.assert_array_equal(b.ridx_dst[:B].cpu().numpy(), np.searchsorted(roots, dst))
+        isin = np.isin(neg, roots)
+        want_neg = np.where(isin, np.searchsorted(roots, neg), -1)
+        np.testing.assert_array_equal(b.ridx_neg[:B].cpu().numpy(), want_neg)
+        assert int(b.t_query.item()) == int(np.float32(ts.max()))
+        np.testing.assert_array_equal(b.root_ts[:U].cpu().numpy(), np.full(U, int(ts.max())))
+        for role, ids, cnt, win in (("src", src, b.cnt_src, b.win_src), ("dst", dst, b.cnt_dst, b.win_dst)):
+            c = np.zeros(U, dtype=np.int64)
+            np.add.at(c, np.searchsorted(roots, ids), 1)
+            np.testing.assert_array_equal(cnt[:U].cpu().numpy(), c, err_msg=role)
+            order = np.argsort(ts, kind="stable")
+            last = {}
+            for e in order:
+                last[ids[e]] = e
+            got = (win[:U].cpu().numpy().view(np.uint64) & np.uint64(0xffffffff)).astype(np.int64)
+            for r, node in enumerate(roots):
+                if c[r]:
+                    assert got[r] == last[node], (role, node)
+        # leave the bitmap clear as the commit would
+        st.node_bits.zero_()
+
+
+def _state_pair(gpu, N, D, K, F, seed):
+    from starry_unigraph.native.step import NodeState
+    torch.manual_seed(seed)
+    st = NodeState(N, D, K, F, gpu)
+    ref = co.MemoryO(N, D, K, F)
+    ref.memory = torch.randn(N, D)
+    ref.mailbox = torch.randn(N, K, 2 * D + F)
+    ref.mailbox_ts = torch.rand(N, K) * 10
+    ref.next_mail_pos = torch.randint(0, K, (N,))
+    st.memory.copy_(ref.memory)
+    st.mailbox.copy_(ref.mailbox)
+    st.mailbox_ts.copy_(ref.mailbox_ts)
+    st.next_mail_pos.copy_(ref.next_mail_pos.to(torch.int32))
+    return st, ref
+
+
+@pytest.mark.parametrize("K", [1, 2, 4])
+def test_memory_update_and_mailbox_teacher_forced(gpu, K):
+    """Each step starts from identical state: mailbox/ts/slot pointers bit-exact,
+    memory within rtol 1e-3."""
+    from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
+    from starry_unigraph.native.step import ConvDims, DeviceStep
+    rng = np.random.default_rng(K)
+    N, D, F, B = 700, 32, 6, 300
+    st, ref = _state_pair(gpu, N, D, K, F, seed=K)
+    up = CTDGMemoryUpdater(D, 2 * D + F, K).to(gpu)
+    up_ref = co.MemoryUpdaterO(D, 2 * D + F, K)
+    up_ref.load_state_dict({k: v.cpu() for k, v in up.state_dict().items()})
+    step = DeviceStep(st, ConvDims(D, F, 8, 2, 4), B)
+    gru = up.kernel_weights()
+    for it in range(4):
+        src, dst, ts, neg = _small_batch(rng, N, B)
+        ef = rng.standard_normal((B, F)).astype(np.float32)
+        T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
+        s_d, d_d, t_d, e_d = T(src), T(dst), T(ts, torch.float32), T(ef, torch.float32)
+        step.prepare(s_d, d_d, T(neg), t_d)
+        step.update_memory(gru, s_d, d_d, e_d, t_d)
+        step.commit()
+        co.memory_phase(ref, up_ref, torch.as_tensor(src), torch.as_tensor(dst), torch.as_tensor(ts),
+                        torch.as_tensor(ef))
+        assert torch.equal(st.mailbox.cpu(), ref.mailbox), f"mailbox step {it}"
+        assert torch.equal(st.mailbox_ts.cpu(), ref.mailbox_ts)
+        assert torch.equal(st.next_mail_pos.cpu().long(), ref.next_mail_pos)
+        assert torch.equal(st.memory_ts.cpu(), ref.memory_ts)
+        _close(st.memory, ref.memory, atol=2e-5, msg=f"memory step {it}")
+        assert int(st.node_bits.abs().sum().item()) == 0
+        st.memory.copy_(ref.memory)            # teacher forcing
+
+
+def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
+    rng = np.random.default_rng(seed)
+    row = rng.integers(0, N, E)
+    col = np.minimum(rng.zipf(1.3, E) - 1, N - 1)
+    ts = np.sort(rng.integers(0, 10 ** 6, E))
+    roots = np.sort(rng.choice(N, R, replace=False))
+    tq = np.full(R, 10 ** 6 // 2, dtype=np.int64)
+    mem = torch.randn(N, D)
+    ef = torch.randn(E, F)
+    return rng, row, col, ts, roots, tq, mem, ef
+
+
+@pytest.mark.parametrize("H,k,seed", [(2, 10, 0), (4, 20, 1), (1, 3, 2)])
+def test_conv_forward_backward_matches_oracle(gpu, H, k, seed):
+    from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    D, F, T = 32, 6, 16
+    rng, row, col, ts, roots, tq, mem, ef = _conv_inputs(gpu, seed, D=D, F=F, T=T, H=H, k=k)
+    N, R = mem.shape[0], len(roots)
+    torch.manual_seed(seed)
+    conv = TemporalTransformerConv(D, F, T, H, D, dropout=0.0, att_dropout=0.0).to(gpu)
+    with torch.no_grad():   # non-trivial time-encoding bias and LayerNorm affine
+        conv.time_enc.w.bias.uniform_(-1, 1)
+        conv.layer_norm.weight.uniform_(0.5, 1.5)
+        conv.layer_norm.bias.uniform_(-0.2, 0.2)
+    ref = co.TemporalConvO(D, F, T, H, D)
+    ref.load_state_dict({kk: v.cpu() for kk, v in conv.state_dict().items()})
+    # device step with the roots injected directly
+    st = NodeState(N, D, 1, F, gpu)
+    st.memory.copy_(mem)
+    step = DeviceStep(st, ConvDims(D, F, T, H, k), R)
+    b = step.buf
+    b.roots[:R] = torch.as_tensor(roots, device=gpu)
+    b.root_ts[:R] = torch.as_tensor(tq, device=gpu)
+    b.num_roots.fill_(R)
+    b.num_roots64.fill_(R)
+    b.new_mem[:R] = mem[roots].to(gpu)
+    g = build_tcsr(N, torch.as_tensor(row), torch.as_tensor(col), None, torch.as_tensor(ts))
+    step.sample(RecentSampler(g))
+    b.any_edges.fill_(int(int(b.hop.cnt[:R].sum().item()) > 0))
+    efd = ef.to(gpu)
+    y = conv(step, efd)
+    gy = torch.randn(R, D)
+    loss = (y[:R] * gy.to(gpu)).sum()
+    loss.backward()
+    # oracle
+    og = so.build_tcsr(N, row, col, np.arange(len(row)), ts)
+    blk = co.block_from_oracle_sampler(og, torch.as_tensor(roots), torch.as_tensor(tq), k)
+    yr = co.conv_all(_Wrap(ref), mem, torch.as_tensor(roots), blk, ef)
+    (yr * gy).sum().backward()
+    _close(y[:R], yr, atol=2e-4, msg="embedding")
+    assert torch.count_nonzero(y[R:]) == 0
+    for (name, p), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
+        scale = float(pr.grad.abs().max()) + 1e-6
+        _close(p.grad, pr.grad, rtol=2e-3, atol=2e-4 * scale, msg=f"grad {name}")
+
+
+class _Wrap:
+    """conv_all expects the predictor-shaped object with .conv/.hidden_dim."""
+
+    def __init__(self, conv):
+        self.conv = conv
+        self.hidden_dim = conv.dim_out
+
+
+def test_conv_empty_block_is_zero(gpu):
+    from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    D, F, T, H, k, R = 16, 3, 8, 2, 4, 20
+    conv = TemporalTransformerConv(D, F, T, H, D, dropout=0.0, att_dropout=0.0).to(gpu)
+    st = NodeState(50, D, 1, F, gpu)
+    st.memory.normal_()
+    step = DeviceStep(st, ConvDims(D, F, T, H, k), R)
+    b = step.buf
+    b.num_roots.fill_(R)
+    b.new_mem[:R] = st.memory[:R]
+    b.hop.cnt.zero_()
+    b.any_edges.zero_()
+    y = conv(step, torch.zeros(1, F, device=gpu))
+    assert torch.count_nonzero(y) == 0
+    y.sum().backward()
+    assert all(torch.count_nonzero(p.grad) == 0 for p in conv.parameters())
+
+
+def _runtime_pair(gpu, K, seed=0, D=32, T=16, H=2, k=10, B=200, n_events=4000, lr=1e-3):
+    """A product runtime and the oracle with identical weights, state and stream."""
+    from starry_unigraph import SchedulerSession, synth
+    from starry_unigraph.data import from_stream
+    s = synth.bipartite_stream(num_src=300, num_dst=60, num_events=n_events, edge_dim=16, seed=seed)
+    cfg = {"model": {"family": "tgn", "hidden_dim": D}, "data": {"name": f"t{seed}", "format": "synthetic"},
+           "train": {"batch_size": B, "lr": lr}, "runtime": {"device": "cuda"},
+           "ctdg": {"mailbox_slots": K, "dim_time": T, "num_head": H, "dropout": 0.0, "att_dropout": 0.0},
+           "sampling": {"neighbor_limit": [k], "history": 1, "strategy": "recent"}}
+    torch.manual_seed(seed)
+    sess = SchedulerSession.from_config(cfg).with_events(from_stream(s))
+    sess.build_runtime()
+    rt = sess.ctdg_session.online_runtime
+    model, updater = co.build_models(D, 16, T, H, K, seed=seed)
+    model.load_state_dict({kk: v.cpu() for kk, v in rt.model.state_dict().items()})
+    updater.load_state_dict({kk: v.cpu() for kk, v in rt.memory_updater.state_dict().items()})
+    opt = torch.optim.Adam(list(model.parameters()) + list(updater.parameters()), lr=lr)
+    mem = co.MemoryO(rt.dataset.num_nodes, D, K, 16)
+    g = rt.dataset.sampler_graph("train")
+    og = so.build_tcsr(rt.dataset.num_nodes, g["row"].numpy(), g["col"].numpy(), g["eid"].numpy(), g["ts"].numpy())
+    return sess, rt, model, updater, opt, mem, og, s
+
+
+def test_initialisation_matches_reference_order(gpu):
+    """Seeded construction in the reference's order gives the oracle's weights."""
+    sess, rt, model, updater, *_ = _runtime_pair(gpu, K=1)
+    m2, u2 = co.build_models(32, 16, 16, 2, 1, seed=0)
+    for (n, p), (_, q) in zip(rt.model.state_dict().items(), m2.state_dict().items()):
+        assert torch.equal(p.cpu(), q), n
+    for (n, p), (_, q) in zip(rt.memory_updater.state_dict().items(), u2.state_dict().items()):
+        assert torch.equal(p.cpu(), q), n
+
+
+def _teacher_force(rt, model, mem):
+    """Copy the oracle's parameters and node state into the GPU runtime."""
+    with torch.no_grad():
+        for p, q in zip(rt.model.parameters(), model.parameters()):
+            p.copy_(q)
+    st = rt.memory.state
+    st.memory.copy_(mem.memory)
+    st.mailbox.copy_(mem.mailbox)
+    st.mailbox_ts.copy_(mem.mailbox_ts)
+    st.memory_ts.copy_(mem.memory_ts)
+    st.next_mail_pos.copy_(mem.next_mail_pos.to(torch.int32))
+
+
+@pytest.mark.parametrize("K", [1, 2])
+def test_train_steps_match_oracle_teacher_forced(gpu, K):
+    """Per step from identical parameters and node state (the learnable time
+    encoding makes free-running fp32 trajectories decorrelate within a few
+    Adam steps): loss, logits, memory, mailbox and this step's gradients
+    match the oracle; mailbox, timestamps and slot pointers bit-exactly."""
+    sess, rt, model, updater, opt, mem, og, s = _runtime_pair(gpu, K=K, seed=K)
+    fan = 10
+    batches = list(rt.iter_batches("train", 200))[:10]
+    gen = torch.Generator().manual_seed(123)
+    pool = rt.dataset.dst.unique()
+    for i, batch in enumerate(batches):
+        neg = co.negative_sample(pool, batch.dst, gen)
+        _teacher_force(rt, model, mem)
+        mem_before = mem.clone()
+        rt._neg_queue["train"] = (neg.to(gpu), 0)
+        out = rt.train_step(batch)
+        ref = co.train_step(model, updater, opt, mem, lambda r, t: co.block_from_oracle_sampler(og, r, t, fan),
+                            batch.src, batch.dst, batch.ts, batch.edge_feat, neg, rt.dataset.edge_feat)
+        rl = float(ref["loss"])
+        assert abs(out["loss"] - rl) <= RTOL * abs(rl) + 1e-6, (i, out["loss"], rl)
+        np.testing.assert_allclose(out["predictions"], torch.sigmoid(ref["pos"]).numpy(), rtol=RTOL, atol=1e-6)
+        st = rt.memory.state
+        _close(st.memory, mem.memory, atol=1e-5, msg=f"memory step {i}")
+        assert torch.equal(st.mailbox.cpu(), mem.mailbox), f"mailbox step {i}"
+        assert torch.equal(st.mailbox_ts.cpu(), mem.mailbox_ts)
+        assert torch.equal(st.memory_ts.cpu(), mem.memory_ts)
+        assert torch.equal(st.next_mail_pos.cpu().long(), mem.next_mail_pos)
+        any_edges = int(rt.step.buf.any_edges.item())
+        assert any_edges == int(ref["block"].nbr.numel() > 0)
+        for (n, p), (_, q) in zip(rt.model.named_parameters(), model.named_parameters()):
+            if q.grad is None:        # the reference's Adam skips it; ours is gated off
+                assert n.startswith("conv.") and any_edges == 0, n
+                continue
+            scale = float(q.grad.abs().max()) + 1e-12
+            _close(p.grad, q.grad, rtol=2e-3, atol=1e-3 * scale, msg=f"grad {n} step {i}")
+        del mem_before
+
+
+def test_fused_adam_matches_torch_adam(gpu):
+    """FusedAdam vs torch.optim.Adam, a gated segment skipped like a None grad."""
+    from starry_unigraph.native.step import FusedAdam
+    torch.manual_seed(0)
+    shapes = [(7, 3), (5,), (11, 2), (4,)]
+    ref_p = [torch.nn.Parameter(torch.randn(s)) for s in shapes]
+    gpu_p = [torch.nn.Parameter(p.detach().clone().to(gpu)) for p in ref_p]
+    opt_r = torch.optim.Adam(ref_p, lr=3e-3)
+    opt_g = FusedAdam([gpu_p[:2], gpu_p[2:]], lr=3e-3)
+    gate = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for it, on in enumerate([1, 0, 1, 1, 0, 1]):
+        grads = [torch.randn(s) * (10.0 ** (it % 3 - 1)) for s in shapes]
+        opt_r.zero_grad(set_to_none=True)
+        for i, (p, g) in enumerate(zip(ref_p, grads)):
+            if i < 2 and not on:
+                continue
+            p.grad = g.clone()
+        opt_r.step()
+        opt_g.zero_grad()
+        for p, g in zip(gpu_p, grads):
+            p.grad.copy_(g)
+        gate.fill_(on)
+        opt_g.step([gate, None])
+        for a, b in zip(gpu_p, ref_p):
+            _close(a, b, rtol=1e-5, atol=1e-6, msg=f"step {it}")
