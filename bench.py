@@ -1,19 +1,31 @@
-"""Benchmark of the MI355X-native CTDG training-step path (one GPU).
+"""Benchmark of the MI355X-native CTDG training step (one GPU).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload sampler]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
-Prints ONE JSON line. Workloads:
-  sampler  -- config 3: temporal sampler microbench (1e7 nodes, 1e8 edges,
-              4e6 degree-weighted queries); a step is one recent-k pass over
-              all queries (k=10, 1 hop); the other cases (k=20, 2 hops) are
-              reported under "cases".
-Inputs are generated (seeded) and resident in HBM before the timed region.
+Prints ONE JSON line. Workloads (BASELINE.json configs):
+  tgn-large  (default) config 4: TGN, 1,140,149 nodes, 7,833,140 events
+             (Zipf 1.5), 16-d edge features, D = T = 100, 2 heads, k = 10,
+             1 mailbox slot, batch 600. A step is one training batch.
+  tgn-small  config 1: bipartite 8,227 + 1,000 nodes, 157,474 events, F = 172, B = 200.
+  jodie      config 2: the same stream with the "jodie" family (the reference
+             builds the same model for it, models.py:337-338).
+  tgn-stress config 5: the config-4 stream, D = 172, 4 heads, k = 20,
+             2 sampled hops, 4 mailbox slots, batch 4,000.
+  sampler    config 3 alone (temporal sampler microbench).
+The default run also measures config 3 and reports it under "sampler".
+
+Timed region: W untimed warm-up steps, then K steps bracketed by
+torch.cuda.synchronize(); value = events / s over the K steps. Inputs (event
+stream, node state, negatives) are resident in HBM before the timed region.
+The node state and optimizer are then restored and the same K steps are
+replayed with HIP events around every library call (per-kernel breakdown and
+the algorithmic work of the dominant kernel); the dominant kernel's events are
+also recorded inside the timed region itself.
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import platform
 import sys
@@ -23,7 +35,19 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "starrygl-unidyngraph_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
 METRIC = "TGN train events/sec on 1 MI355X; sampler Mqueries/s; % HBM roofline"
+
+WORKLOADS = {
+    "tgn-large": dict(config="cfg4", stream="unipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=600,
+                      history=1),
+    "tgn-small": dict(config="cfg1", stream="bipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=200,
+                      history=1),
+    "jodie": dict(config="cfg2", stream="bipartite", family="jodie", D=100, T=100, H=2, k=10, K=1, B=200,
+                  history=1),
+    "tgn-stress": dict(config="cfg5", stream="unipartite", family="tgn", D=172, T=100, H=4, k=20, K=4, B=4000,
+                       history=2),
+}
 
 
 def log(msg: str) -> None:
@@ -48,20 +72,19 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
-# --------------------------------------------------------------------------- sampler
-def sampler_bytes(deg_q, cnt):
-    """Algorithmic bytes of the recent-k kernel per query (summed):
+# --------------------------------------------------------------------------- sampler (config 3)
+def sampler_bytes(deg_q, cnt) -> float:
+    """Algorithmic bytes of the recent-k kernel, summed over queries:
     12 (node + t) + 16 (two row offsets) + 8*ceil(log2(deg+1)) (probes)
-    + 16*k_eff (nbr i32 + eid i32 + ts i64 read) + 12*k_eff (nbr, eid, dt written)
-    + 4 (count written)."""
+    + 16*k_eff (nbr i32 + eid i32 + ts i64 read) + 12*k_eff (nbr, eid, dt
+    written) + 4 (count written)."""
     import torch
     probes = torch.ceil(torch.log2(deg_q.double() + 1.0))
     k = cnt.double()
     return float((12 + 16 + 8 * probes + 28 * k + 4).sum().item())
 
 
-def run_sampler(args) -> dict:
-    import numpy as np
+def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -> dict:
     import torch
 
     from starry_unigraph import synth
@@ -71,91 +94,82 @@ def run_sampler(args) -> dict:
     t0 = time.time()
     g_np = synth.powerlaw_sampler_graph(seed=0)
     nodes_np, qt_np = synth.degree_weighted_queries(g_np, seed=1)
-    log(f"generated config-3 graph in {time.time() - t0:.1f}s")
+    log(f"config-3 graph generated in {time.time() - t0:.1f}s")
     g = build_tcsr(g_np.num_nodes, torch.from_numpy(g_np.row), torch.from_numpy(g_np.col), None,
                    torch.from_numpy(g_np.ts), device=dev)
     nodes = torch.from_numpy(nodes_np).to(dev)
     qt = torch.from_numpy(qt_np).to(dev)
     torch.cuda.synchronize()
-    log(f"device CSR built ({g.nbytes() / 1e9:.2f} GB)")
     s = RecentSampler(g)
     deg = g.deg
-
     stream = torch.cuda.current_stream(dev)
     nq = nodes.numel()
-
-    # headline: 1 hop, k=10; each step is one kernel launch, timed with events
-    # recorded on the stream the kernel is launched on
     head = s.sample(nodes, qt, 10)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         s.sample(nodes, qt, 10, out=head)
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    wall0 = time.perf_counter()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    w0 = time.perf_counter()
     for a, b in evs:
         a.record(stream)
         s.sample(nodes, qt, 10, out=head)
         b.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
+    wall = time.perf_counter() - w0
     avg_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    out = {
-        "value": nq * args.steps / wall / 1e6,
-        "unit": "Mqueries/s",
-        "ms_per_step": wall * 1000.0 / args.steps,
-        "kernel": "k_recent_padded",
-        "kernel_avg_ms": avg_ms,
-        "alg_bytes": sampler_bytes(deg[nodes], head.cnt),
-    }
+    alg = sampler_bytes(deg[nodes], head.cnt)
+    out = {"value": nq * steps / wall / 1e6, "unit": "Mqueries/s", "ms_per_pass": wall * 1e3 / steps,
+           "workload": "cfg3: 1e7 nodes, 1e8 edges, 4e6 degree-weighted queries, recent k=10, 1 hop",
+           "roofline": {"bound": "hbm", "kernel": "k_recent_padded", "kernel_avg_ms": avg_ms,
+                        "alg_bytes_per_launch": alg, "achieved": alg / (avg_ms * 1e-3) / 1e9,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": alg / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}}
     del head
-    log(f"headline k=10 1-hop: {avg_ms:.3f} ms/launch")
-
-    # the other config-3 cases: k in {10, 20} x {1, 2} hops, each hop timed
-    cases = {}
-    for k in (10, 20):
-        for hops in (1, 2):
-            q_nodes, q_t, valid, stride = nodes, qt, None, 0
-            per_hop = []
-            for h in range(hops):
-                want_ts = h < hops - 1
-                ph = s.sample(q_nodes, q_t, k, want_ts=want_ts, valid_cnt=valid, stride=stride)
-                s.sample(q_nodes, q_t, k, want_ts=want_ts, valid_cnt=valid, stride=stride, out=ph)
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                reps = 3
-                a.record(stream)
-                for _ in range(reps):
-                    s.sample(q_nodes, q_t, k, want_ts=want_ts, valid_cnt=valid, stride=stride, out=ph)
-                b.record(stream)
-                torch.cuda.synchronize()
-                ms = a.elapsed_time(b) / reps
-                if valid is None:
-                    dq, cnt, live = deg[q_nodes], ph.cnt, q_nodes.numel()
-                else:
-                    mask = (torch.arange(q_nodes.numel(), device=dev) % stride) < valid.long().repeat_interleave(stride)
-                    dq, cnt, live = deg[q_nodes[mask].long()], ph.cnt[mask], int(mask.sum().item())
-                alg_h = sampler_bytes(dq, cnt) + 4 * (q_nodes.numel() - live)
-                per_hop.append({"queries": live, "ms": ms, "alg_GBs": alg_h / ms / 1e6,
-                                "entries": int(ph.cnt.sum().item())})
-                q_nodes, q_t, valid, stride = ph.nbr, ph.ts, ph.cnt, k
-            tot_ms = sum(p["ms"] for p in per_hop)
-            cases[f"k{k}_hop{hops}"] = {"ms": tot_ms, "Mqueries_per_s_roots": nq / tot_ms / 1e3, "hops": per_hop}
-            log(f"case k={k} hops={hops}: {tot_ms:.3f} ms")
-            del ph, q_nodes, q_t, valid
-            torch.cuda.empty_cache()
-    out["cases"] = cases
-    out["cpu_baseline"] = sampler_cpu_baseline(g_np, nodes_np, qt_np)
+    if cases:
+        res = {}
+        for k in (10, 20):
+            for hops in (1, 2):
+                q_nodes, q_t, valid, stride = nodes, qt, None, 0
+                per_hop = []
+                for h in range(hops):
+                    want_ts = h < hops - 1
+                    ph = s.sample(q_nodes, q_t, k, want_ts=want_ts, valid_cnt=valid, stride=stride)
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    for _ in range(3):
+                        s.sample(q_nodes, q_t, k, want_ts=want_ts, valid_cnt=valid, stride=stride, out=ph)
+                    b.record(stream)
+                    torch.cuda.synchronize()
+                    ms = a.elapsed_time(b) / 3
+                    if valid is None:
+                        dq, cnt, live = deg[q_nodes], ph.cnt, q_nodes.numel()
+                    else:
+                        mask = (torch.arange(q_nodes.numel(), device=dev) % stride) < \
+                            valid.long().repeat_interleave(stride)
+                        dq, cnt, live = deg[q_nodes[mask].long()], ph.cnt[mask], int(mask.sum().item())
+                    alg_h = sampler_bytes(dq, cnt) + 4 * (q_nodes.numel() - live)
+                    per_hop.append({"queries": live, "ms": round(ms, 4), "alg_GBs": round(alg_h / ms / 1e6, 1),
+                                    "entries": int(ph.cnt.sum().item())})
+                    q_nodes, q_t, valid, stride = ph.nbr, ph.ts, ph.cnt, k
+                tot = sum(p["ms"] for p in per_hop)
+                res[f"k{k}_hop{hops}"] = {"ms": round(tot, 4), "Mqueries_per_s": round(nq / tot / 1e3, 1),
+                                          "hops": per_hop}
+                del ph, q_nodes, q_t, valid
+                torch.cuda.empty_cache()
+        out["cases"] = res
+    if cpu:
+        out["cpu_baseline"] = sampler_cpu_baseline(g_np, nodes_np, qt_np)
+    del g, s, nodes, qt
+    torch.cuda.empty_cache()
     return out
 
 
 def sampler_cpu_baseline(g_np, nodes_np, qt_np) -> dict:
-    """The reference's own C++ sampler (compiled from its sources into
-    oracle/_ref) when loadable, else the C oracle, on a bounded sample: the
-    first 1e6 queries of the 1-hop k=10 case, all host threads."""
+    """The C oracle (OpenMP over all host threads) on a bounded sample: the
+    first 1e6 of the 4e6 queries, 1 hop, k = 10."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import numpy as np
     cores = host_cores()
-    sample_q = 1_000_000
-    nq = min(sample_q, len(nodes_np))
+    nq = min(1_000_000, len(nodes_np))
     try:
         import sampler_oracle as so
         so.set_threads(cores)
@@ -164,53 +178,272 @@ def sampler_cpu_baseline(g_np, nodes_np, qt_np) -> dict:
         t0 = time.perf_counter()
         so.sample_layer(og, nodes_np[:nq], qt_np[:nq], 10)
         dt = time.perf_counter() - t0
-        del og
         return {"value": nq / dt / 1e6, "unit": "Mqueries/s", "cores": cores, "kind": "port",
-                "sample": f"1-hop k=10 recent over the first {nq} of the 4e6 config-3 queries, C oracle (OpenMP)",
+                "sample": f"1-hop k=10 recent over the first {nq} config-3 queries (C oracle, OpenMP)",
                 "cpu_model": cpu_model()}
-    except Exception as e:  # the baseline is reported, never required
+    except Exception as e:  # reported, never required
         return {"value": None, "unit": "Mqueries/s", "cores": cores, "kind": "port", "sample": f"failed: {e}"}
+
+
+# --------------------------------------------------------------------------- TGN end to end
+def make_stream(wl: dict):
+    from starry_unigraph import synth
+    if wl["stream"] == "bipartite":
+        return synth.bipartite_stream(seed=0)
+    return synth.unipartite_stream(seed=0)
+
+
+def build_session(wl: dict, stream):
+    import torch
+
+    from starry_unigraph import SchedulerSession
+    from starry_unigraph.data import from_stream
+    cfg = {"model": {"family": wl["family"], "hidden_dim": wl["D"]},
+           "data": {"name": f"bench_{wl['config']}", "format": "synthetic"},
+           "train": {"batch_size": wl["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
+           "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"], "dropout": 0.0,
+                    "att_dropout": 0.0},
+           "sampling": {"neighbor_limit": [wl["k"]] * wl["history"], "history": wl["history"],
+                        "strategy": "recent"}}
+    torch.manual_seed(0)
+    sess = SchedulerSession.from_config(cfg).with_events(from_stream(stream))
+    sess.build_runtime()
+    return sess
+
+
+class Epochs:
+    """Training batches in order, epoch after epoch (memory is never reset
+    between epochs, as in the reference); negatives drawn per epoch."""
+
+    def __init__(self, rt, B):
+        self.rt, self.B = rt, B
+        self._it = None
+
+    def next(self):
+        while True:
+            if self._it is None:
+                self.rt.precompute_negatives("train", self.B)
+                self._it = iter(self.rt.iter_batches("train", self.B))
+            try:
+                return next(self._it)
+            except StopIteration:
+                self._it = None
+
+
+def _snapshot(rt):
+    st = rt.memory.state
+    opt = rt.optimizer.inner
+    return ([t.clone() for t in (st.memory, st.mailbox, st.mailbox_ts, st.memory_ts, st.next_mail_pos)],
+            [t.clone() for t in (opt.flat, opt.exp_avg, opt.exp_avg_sq)] + [seg[2].clone() for seg in opt.segments])
+
+
+def _restore(rt, snap):
+    st = rt.memory.state
+    opt = rt.optimizer.inner
+    for dst, src in zip((st.memory, st.mailbox, st.mailbox_ts, st.memory_ts, st.next_mail_pos), snap[0]):
+        dst.copy_(src)
+    for dst, src in zip([opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments], snap[1]):
+        dst.copy_(src)
+
+
+def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float]:
+    """Algorithmic work of one launch: ("hbm", bytes) or ("mfma", flops)."""
+    D, F, T, H, k, K = wl["D"], dims.F, wl["T"], wl["H"], wl["k"], wl["K"]
+    C = D + F + T
+    S = 2 * D + F
+    if name == "memory_update":
+        # GRU over K slots + GRUCell per updated root
+        return "mfma", float(U) * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
+    if name == "conv_forward":
+        # Q (2D*D), qt (2D*C), per edge 4HC (scores + weighted sum), agg (2CD), z (4D*D)
+        return "mfma", float(U) * (2 * D * D + 2 * D * C + 2 * C * D + 4 * D * D) + float(E) * 4 * H * C
+    if name == "conv_backward":
+        # gagg (2D*D), gxbar (2D*C), per edge 8HC, gQ (2CD)
+        return "mfma", float(U) * (2 * D * D + 2 * D * C + 2 * C * D) + float(E) * 8 * H * C
+    if name == "memory_commit":
+        return "hbm", float(U) * (8 + 4 * D * 2 + 4)
+    if name == "recent_sample":
+        return "hbm", float(U) * (12 + 16 + 8 * 8 + 4) + float(E) * 28
+    if name == "batch_prepare":
+        return "hbm", float(B) * (8 + 8 + 8 + 4) + float(U) * 8
+    return "hbm", 0.0
+
+
+def run_tgn(args, wl: dict) -> dict:
+    import torch
+
+    t0 = time.time()
+    stream = make_stream(wl)
+    log(f"{wl['config']} stream generated in {time.time() - t0:.1f}s ({stream.num_events} events)")
+    sess = build_session(wl, stream)
+    rt = sess.ctdg_session.online_runtime
+    rt.collect_results = False
+    ep = Epochs(rt, wl["B"])
+    dev = torch.device("cuda:0")
+    for _ in range(args.warmup):
+        out = rt.train_step(ep.next())
+    torch.cuda.synchronize()
+    log(f"warm-up done ({args.warmup} steps)")
+
+    batches = [ep.next() for _ in range(args.steps)]
+    snap = _snapshot(rt)
+    neg_state = dict(rt._neg_queue)
+    dom = args.roofline_kernel
+    timer: list = []
+    rt.step.timer, rt.step.timed = timer, {dom}
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    losses = []
+    for b in batches:
+        out = rt.train_step(b)
+        losses.append(out["loss"])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    events = sum(b.size for b in batches)
+    dom_ms = [a.elapsed_time(b) for _, a, b in timer]
+    final_loss = float(torch.stack(losses).mean().item())
+    log(f"timed {args.steps} steps: {wall * 1e3 / args.steps:.3f} ms/step, {events / wall:.0f} events/s")
+
+    # replay the same steps with every library call timed + per-step counts
+    _restore(rt, snap)
+    rt._neg_queue = dict(neg_state)
+    rt.step.timed = None
+    timer.clear()
+    per_step = []
+    for b in batches:
+        n0 = len(timer)
+        rt.train_step(b)
+        buf = rt.step.buf
+        U = int(buf.num_roots.item())
+        E = int(buf.hop.cnt[:U].sum().item())
+        per_step.append((n0, len(timer), U, E, b.size))
+    torch.cuda.synchronize()
+    agg: dict[str, list] = {}
+    work: dict[str, list] = {}
+    for n0, n1, U, E, B in per_step:
+        for name, a, b in timer[n0:n1]:
+            agg.setdefault(name, []).append(a.elapsed_time(b))
+            work.setdefault(name, []).append(kernel_work(name, wl, U, E, B, rt.dims)[1])
+    breakdown = {}
+    for name, ms in agg.items():
+        avg = sum(ms) / len(ms)
+        bound = kernel_work(name, wl, 1, 1, 1, rt.dims)[0]
+        wavg = sum(work[name]) / len(work[name])
+        if bound == "mfma":
+            ach, peak, unit = wavg / (avg * 1e-3) / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+        else:
+            ach, peak, unit = wavg / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        breakdown[name] = {"avg_us": round(avg * 1e3, 2), "calls": len(ms), "bound": bound,
+                           "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5)}
+    mean_U = sum(p[2] for p in per_step) / len(per_step)
+    mean_E = sum(p[3] for p in per_step) / len(per_step)
+    dom_avg = sum(dom_ms) / max(1, len(dom_ms))
+    bound = kernel_work(dom, wl, 1, 1, 1, rt.dims)[0]
+    dwork = sum(work[dom]) / len(work[dom])
+    if bound == "mfma":
+        ach, peak, unit = dwork / (dom_avg * 1e-3) / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        ach, peak, unit = dwork / (dom_avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+    res = {
+        "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
+        "mean_train_loss": final_loss,
+        "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
+                     "frac": ach / peak, "traffic": None, "kernel_avg_ms": dom_avg,
+                     "work_per_launch": dwork},
+        "kernels": breakdown,
+        "step_shape": {"mean_roots": round(mean_U, 1), "mean_sampled_edges": round(mean_E, 1)},
+    }
+    rt.step.timer = None
+    if not args.no_cpu:
+        res["cpu_baseline"] = tgn_cpu_baseline(wl, stream, rt)
+    return res
+
+
+def tgn_cpu_baseline(wl: dict, stream, rt) -> dict:
+    """The torch-CPU oracle step (C oracle sampler + memory/GRU + attention +
+    predictor + Adam), all host threads, on a bounded prefix of the training
+    stream: the first N batches from zero memory."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import numpy as np
+    import torch
+    cores = host_cores()
+    nsteps = 200 if wl["B"] <= 1000 else 20
+    try:
+        import ctdg_oracle as co
+        import sampler_oracle as so
+        torch.set_num_threads(cores)
+        so.set_threads(cores)
+        ds = rt.dataset
+        model, updater = co.build_models(wl["D"], ds.edge_feat_dim, wl["T"], wl["H"], wl["K"], seed=0)
+        opt = torch.optim.Adam(list(model.parameters()) + list(updater.parameters()), lr=1e-3)
+        mem = co.MemoryO(ds.num_nodes, wl["D"], wl["K"], ds.edge_feat_dim)
+        g = ds.sampler_graph("train")
+        og = so.build_tcsr(ds.num_nodes, g["row"].numpy(), g["col"].numpy(), g["eid"].numpy(), g["ts"].numpy())
+        pool = ds.dst.unique()
+        gen = torch.Generator().manual_seed(0)
+        it = ds.iter_batches("train", wl["B"])
+        k = wl["k"]
+        fn = lambda r, t: co.block_from_oracle_sampler(og, r, t, k)
+        b = next(it)
+        neg = co.negative_sample(pool, b.dst, gen)
+        co.train_step(model, updater, opt, mem, fn, b.src, b.dst, b.ts, b.edge_feat, neg, ds.edge_feat)
+        t0 = time.perf_counter()
+        n = 0
+        for _ in range(nsteps):
+            b = next(it)
+            neg = co.negative_sample(pool, b.dst, gen)
+            co.train_step(model, updater, opt, mem, fn, b.src, b.dst, b.ts, b.edge_feat, neg, ds.edge_feat)
+            n += b.size
+        dt = time.perf_counter() - t0
+        return {"value": n / dt, "unit": "events/s", "cores": cores, "kind": "port",
+                "sample": f"{nsteps} training steps (batches 2..{nsteps + 1} of the epoch, B={wl['B']}) of the "
+                          f"torch-CPU oracle step incl. the C oracle sampler; {dt:.1f}s",
+                "cpu_model": cpu_model()}
+    except Exception as e:  # reported, never required
+        return {"value": None, "unit": "events/s", "cores": cores, "kind": "port", "sample": f"failed: {e!r}"}
 
 
 # --------------------------------------------------------------------------- main
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="sampler", choices=["sampler"])
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="tgn-large", choices=sorted(list(WORKLOADS) + ["sampler"]))
+    ap.add_argument("--roofline-kernel", default="conv_backward",
+                    choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "conv_forward",
+                             "conv_backward"])
+    ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only; multi-GPU sharding is a design note "
-                                   "(the GPU boxes here have one GPU)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build measures one GPU (the GPU boxes here have one); multi-GPU "
+                                   "sharding is a design note, not a measured path", "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
-    res = run_sampler(args)
-    ach = res["alg_bytes"] / (res["kernel_avg_ms"] * 1e-3) / 1e9
-    line = {
-        "metric": METRIC,
-        "value": res["value"],
-        "unit": res["unit"],
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": res["ms_per_step"],
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int64",
-        "data": "synthetic (seeded PCG64 generators, starry_unigraph.synth)",
-        "config": {"workload": "cfg3 temporal sampler microbench: 1e7 nodes, 1e8 edges, 4e6 queries, k=10, 1 hop",
-                   "global_batch": 4_000_000, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": ach / HBM_PEAK_GBS, "traffic": None, "kernel": res["kernel"],
-                     "kernel_avg_ms": res["kernel_avg_ms"]},
-        "cpu_baseline": res["cpu_baseline"],
-        "cases": res.get("cases"),
-    }
+    base = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded PCG64 generators, starry_unigraph.synth)"}
+    if args.workload == "sampler":
+        r = run_sampler(args.steps, args.warmup, cpu=not args.no_cpu)
+        line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_pass"], dtype="int64",
+                    config={"workload": r["workload"], "global_batch": 4_000_000, "parallelism": "single GPU"},
+                    roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), cases=r.get("cases"))
+        print(json.dumps(line), flush=True)
+        return
+    wl = WORKLOADS[args.workload]
+    r = run_tgn(args, wl)
+    line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"], dtype="fp32",
+                config={"workload": f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
+                                    f"H={wl['H']} k={wl['k']} hops={wl['history']} K={wl['K']} B={wl['B']}, "
+                                    "dropout 0",
+                        "global_batch": wl["B"], "parallelism": "single GPU"},
+                roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
+                step_shape=r["step_shape"], mean_train_loss=r["mean_train_loss"])
+    if args.workload == "tgn-large" and not args.no_sampler:
+        line["sampler"] = run_sampler(20, 3, cases=False, cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

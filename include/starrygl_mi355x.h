@@ -231,6 +231,26 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Edge predictor + BCE, forward and (train != 0) backward.
+ * Replaces CTDGLinkPredictor.forward (backends/ctdg/runtime/models.py:313-324)
+ * on the root rows selected as in runtime.py:176-183, and the loss of
+ * runtime.py:290-292. y [capacity][D] are the attention outputs of the
+ * roots; ridx_* (from sgl_batch_prepare) pick each event's rows, -1 meaning
+ * a zero embedding. Weights in nn.Linear layout: w_s, w_d [D][D], w_o [1][D].
+ * Writes pos/neg logits [batch] and loss (mean BCE, pos label 1, neg 0).
+ * With train: zeroes gy [capacity][D] then adds dloss/dy into it, and ADDS
+ * the parameter gradients into g_* (callers zero them once per step).
+ * ------------------------------------------------------------------------- */
+int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
+                  const float *y, const int32_t *ridx_src,
+                  const int32_t *ridx_dst, const int32_t *ridx_neg,
+                  const float *w_s, const float *b_s, const float *w_d,
+                  const float *b_d, const float *w_o, const float *b_o,
+                  float *pos_logits, float *neg_logits, float *loss,
+                  float *gy, float *g_ws, float *g_bs, float *g_wd,
+                  float *g_bd, float *g_wo, float *g_bo, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
  * optimizer of backends/ctdg/runtime/factory.py:122-128. `step` is a device
  * float holding the completed step count (read as t-1); sgl_adam_advance

@@ -91,12 +91,18 @@ class TGTemporalDataset:
         ids = self.split_event_ids(split)
         step = batch_size * (self.partition_world_size if (self.partition_world_size > 1 and
                                                             self.edge_parts is not None) else 1)
+        sharded = self.partition_world_size > 1 and self.edge_parts is not None
+        base = int(ids[0]) if ids.numel() else 0
         for bi, start in enumerate(range(0, int(ids.numel()), step)):
             ev = ids[start:start + step]
-            if self.partition_world_size > 1 and self.edge_parts is not None:
+            if sharded:
                 ev = ev[self.edge_parts[ev] == self.partition_rank]
-            yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[ev], dst=self.dst[ev],
-                                ts=self.ts[ev], edge_feat=self.edge_feat[ev])
+                yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[ev], dst=self.dst[ev],
+                                    ts=self.ts[ev], edge_feat=self.edge_feat[ev])
+            else:  # splits are contiguous event ranges: views, no copies
+                a, b = base + start, base + start + ev.numel()
+                yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[a:b], dst=self.dst[a:b],
+                                    ts=self.ts[a:b], edge_feat=self.edge_feat[a:b])
 
     def sampler_graph(self, split: str) -> dict[str, torch.Tensor]:
         """data.py:196-231: train = [0, train_end); val = [0, val_end);

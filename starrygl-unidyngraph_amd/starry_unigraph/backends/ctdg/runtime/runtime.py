@@ -145,24 +145,30 @@ class CTDGOnlineRuntime:
             step.update_memory(self._gru, src, dst, ef, ts)
             step.commit()
         core = self._core()
-        with torch.set_grad_enabled(train):
-            y = core.conv(step, self._dev["edge_feat"])
-            b = step.buf
-            rn = b.ridx_neg[:n].long()
-            e_s = y[b.ridx_src[:n].long()]
-            e_d = y[b.ridx_dst[:n].long()]
-            # runtime.py:176-182: a negative that is not a root gets a zero embedding
-            y_ext = torch.cat([y, self._zero_row.to(y.dtype)], dim=0)
-            e_n = y_ext[torch.where(rn >= 0, rn, torch.full_like(rn, y.shape[0]))]
-            out = self.model(src_conv=e_s, dst_conv=e_d, neg_conv=e_n)
-            pos, negl = out.pos_logits, out.neg_logits
-            loss = (F.binary_cross_entropy_with_logits(pos, torch.ones_like(pos))
-                    + F.binary_cross_entropy_with_logits(negl, torch.zeros_like(negl)))
+        conv = core.conv
+        if train and (conv.dropout.p > 0 or conv.att_dropout.p > 0):
+            raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
+                                      "ctdg.dropout and ctdg.att_dropout to 0")
+        efeat_all = self._dev["edge_feat"]
+        cparams = [p.detach() for p in conv.kernel_params()]
+        pparams = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
+                   core.out_fc.bias]
         if train:
+            # gradients are views of the optimizer's flat buffer: zero it, then the
+            # kernels add into it (no torch autograd on this path)
             self.optimizer.zero_grad(set_to_none=True)
-            loss.backward()
+            pgrads = [p.grad for p in pparams]
+            if any(g is None for g in pgrads):
+                raise RuntimeError("the fused step needs the runtime's optimizer (gradient buffers missing)")
+        else:
+            pgrads = None
+        step.conv_forward(cparams, efeat_all)
+        pos, negl, loss = step.predictor(n, train, [p.detach() for p in pparams], pgrads)
+        if train:
+            grads = step.conv_backward(cparams, efeat_all, step.buf.gy)
+            torch._foreach_add_([p.grad for p in conv.kernel_params()], grads)
             self.optimizer.step()
-        return StepTensors(loss.detach(), pos.detach(), negl.detach(), n)
+        return StepTensors(loss[0], pos, negl, n)
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
         """runtime.py:202-214."""

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
     "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 31),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 37),
+    "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 21),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
 }

@@ -111,6 +111,10 @@ class StepBuffers:
         self.Q, self.agg, self.z, self.y = z(c, D), z(c, D), z(c, D), z(c, D)
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
+        self.gy = z(c, D)
+        self.pos = z(max(B, 1))
+        self.neg = z(max(B, 1))
+        self.loss = z(1)
         self.gz, self.gagg, self.gQ = z(c, D), z(c, D), z(c, D)
         self.G, self.sigma = z(c, H, C), z(c, H)
         self.ln_part = z(c // TILE, 2, D)
@@ -126,9 +130,26 @@ class DeviceStep:
         self.buf = StepBuffers(max_batch, dims, state.device)
         self.dev = state.device
         self.lib = _capi.lib()
+        # optional per-launch timing: a list that receives (name, start, end)
+        # HIP events around each library call, or None
+        self.timer: list | None = None
+        self.timed: set[str] | None = None   # names to time (None = all)
 
     def _s(self) -> int:
         return _capi.stream_of(self.dev)
+
+    def _call(self, name: str, fn):
+        t = self.timer
+        if t is None or (self.timed is not None and name not in self.timed):
+            return fn()
+        stream = torch.cuda.current_stream(self.dev)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        r = fn()
+        b.record(stream)
+        t.append((name, a, b))
+        return r
 
     # -- batch preparation --------------------------------------------------
     def prepare(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor) -> None:
@@ -136,42 +157,56 @@ class DeviceStep:
         n = src.numel()
         if n > b.max_batch:
             raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
-        _capi.check(self.lib.sgl_batch_prepare(
+        self._call("batch_prepare", lambda: _capi.check(self.lib.sgl_batch_prepare(
             st.N, n, P(src), P(dst), P(neg), P(ts), P(st.node_bits), P(st.word_prefix), P(b.num_roots),
             P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
             P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
-            self._s()), "sgl_batch_prepare")
+            self._s()), "sgl_batch_prepare"))
 
     def sample(self, sampler: RecentSampler) -> PaddedHop:
         b = self.buf
-        return sampler.sample(b.roots, b.root_ts, self.dims.fanout, out=b.hop, num_live=b.num_roots64)
+        return self._call("recent_sample", lambda: sampler.sample(b.roots, b.root_ts, self.dims.fanout, out=b.hop,
+                                                                   num_live=b.num_roots64))
 
     # -- memory -------------------------------------------------------------
     def update_memory(self, gru: dict, src, dst, efeat, ts) -> None:
         b, st, P = self.buf, self.state, _capi.ptr
-        _capi.check(self.lib.sgl_memory_update(
+        self._call("memory_update", lambda: _capi.check(self.lib.sgl_memory_update(
             st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
             P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
             P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(b.win_src),
-            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), "sgl_memory_update")
+            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), "sgl_memory_update"))
 
     def commit(self) -> None:
         b, st, P = self.buf, self.state, _capi.ptr
-        _capi.check(self.lib.sgl_memory_commit(
+        self._call("memory_commit", lambda: _capi.check(self.lib.sgl_memory_commit(
             st.D, b.cap, P(b.num_roots), P(b.roots), P(b.new_mem), P(st.memory), P(st.memory_ts), P(b.ts_max),
-            P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit")
+            P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
 
     # -- attention ----------------------------------------------------------
     def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
-        _capi.check(self.lib.sgl_conv_forward(
+        self._call("conv_forward", lambda: _capi.check(self.lib.sgl_conv_forward(
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
             P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
             P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
-            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.y), self._s()), "sgl_conv_forward")
+            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.y), self._s()), "sgl_conv_forward"))
         return b.y
+
+    def predictor(self, n: int, train: bool, pred: list[torch.Tensor], grads: list[torch.Tensor] | None):
+        """Edge predictor + BCE over the step's roots (sgl_predictor). ``pred``:
+        src_fc.weight, src_fc.bias, dst_fc.weight, dst_fc.bias, out_fc.weight,
+        out_fc.bias; ``grads``: their gradient buffers (added into)."""
+        b, P = self.buf, _capi.ptr
+        g = grads if (train and grads is not None) else [None] * 6
+        self._call("predictor", lambda: _capi.check(self.lib.sgl_predictor(
+            n, self.dims.D, b.cap, 1 if train else 0, P(b.y), P(b.ridx_src), P(b.ridx_dst), P(b.ridx_neg),
+            P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]), P(b.pos), P(b.neg),
+            P(b.loss), P(b.gy) if train else None, P(g[0]), P(g[1]), P(g[2]), P(g[3]), P(g[4]), P(g[5]),
+            self._s()), "sgl_predictor"))
+        return b.pos[:n], b.neg[:n], b.loss
 
     def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
         """Returns the 12 parameter gradients (TimeEncode w, b; w_q, b_q, w_k,
@@ -180,12 +215,12 @@ class DeviceStep:
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
         gy = gy.contiguous()
-        _capi.check(self.lib.sgl_conv_backward(
+        self._call("conv_backward", lambda: _capi.check(self.lib.sgl_conv_backward(
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
             P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
             P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
             P(b.ml), P(b.agg), P(b.z), P(b.stats), P(gy), P(b.gz), P(b.gagg), P(b.G), P(b.sigma), P(b.gQ),
-            P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward")
+            P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
         # weight gradients: per-root products reduced over the root rows (rows
         # past the live roots are zero in gz/gagg/G/sigma/gQ)
         D, H, C, T = d.D, d.H, d.C, d.T
