@@ -125,10 +125,15 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
  *   timestamp order in which root r is the src / dst; cnt_src/cnt_dst[r] =
  *   how many events root r is src / dst in; any_edges reset to 0.
  * Arrays indexed by root hold 2*batch entries (the capacity).
+ * event_offset (device int64, may be NULL): when given, src/dst/ts are the
+ * whole event stream and the batch is events [*event_offset, +batch) of it
+ * (so a captured HIP graph can replay the step for every batch); neg always
+ * holds the batch's own `batch` entries. Event indices e above are relative
+ * to the batch start.
  * ------------------------------------------------------------------------- */
 int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
                       const int64_t *dst, const int64_t *neg, const float *ts,
-                      uint32_t *node_bits, int32_t *word_prefix,
+                      const int64_t *event_offset, uint32_t *node_bits, int32_t *word_prefix,
                       int32_t *num_roots, int64_t *num_roots64, float *ts_max,
                       int64_t *t_query, int64_t *roots, int64_t *root_ts,
                       int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
@@ -151,6 +156,8 @@ int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
  * (int32 here) follow memory.py:237-248: one slot per node and role per
  * batch, src role first, pointer advanced by the occurrence counts.
  * Weights: w_ih [3D][2D+F], w_hh [3D][D], wc_ih [3D][D], wc_hh [3D][D].
+ * event_offset as in sgl_batch_prepare (src/dst/efeat/ts then span the
+ * whole stream).
  * ------------------------------------------------------------------------- */
 size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F);
 int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
@@ -162,6 +169,7 @@ int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
                       const float *bc_ih, const float *bc_hh,
                       const int64_t *src, const int64_t *dst,
                       const float *efeat, const float *ts,
+                      const int64_t *event_offset,
                       const uint64_t *win_src, const uint64_t *win_dst,
                       const int32_t *cnt_src, const int32_t *cnt_dst,
                       float *new_mem, hipStream_t stream);

@@ -1,5 +1,5 @@
 // TGN temporal attention (TimeEncode + TemporalTransformerConv), forward and
-// backward, one workgroup per tile of 16 roots.
+// backward, one workgroup (8 or 16 waves) per tile of 16 roots.
 //
 // Reference: TemporalTransformerConv.forward  backends/ctdg/runtime/models.py:77-137,
 //            build_dgl_block                  models.py:144-197,
@@ -16,8 +16,14 @@
 //          block has no edges (models.py:88-89, runtime.py:168-169)
 // The re-association moves the K/V projections from per-edge to per-root
 // GEMMs (qt and the W_v product), so per edge only a gather, T cosines and
-// 2H dot/axpy passes over C floats remain. The edge loop is one wavefront per
-// root with an online (running max / running sum) softmax.
+// 2H dot/axpy passes over C floats remain.
+//
+// Latency structure (a step has a few hundred roots, so a launch is ~U/16
+// workgroups and every phase is a chain of L2 round trips): the GEMMs issue
+// all weight loads of a block at once (mfma.h), and in the edge phase each
+// wave owns one root, reads its whole window's (nbr, eid, dt) with one load
+// per lane, then gathers the X rows of 4 edges per round trip. The softmax
+// runs online (running max / running sum) over the window.
 //
 // No 1/sqrt(d) scaling (models.py:125). The time-encoding argument is
 // fl(fl(dt * w) + b), then cos.
@@ -28,11 +34,16 @@
 
 namespace {
 
-constexpr int kBlock = 256;
 constexpr int kRows = 16;
-constexpr int kWaves = kBlock / 64;
+constexpr int kEC = 4;      // edges gathered per round trip
 constexpr int kMaxH = 4;
-constexpr int kMaxJ = 8;  // C <= 512
+constexpr int kMaxJ = 8;    // C <= 512
+constexpr int kMaxWaves = 16;
+
+// Waves per workgroup for a (heads, column slots) instance: 16 (one root per
+// wave, 128 VGPRs each) while the edge loop's per-lane [H][J] arrays fit,
+// else 8 (two roots per wave, 256 VGPRs each).
+constexpr int waves_for(int hm, int jm) { return hm * jm <= 6 || (hm == 2 && jm == 4) ? 16 : 8; }
 
 struct Dims {
   int D, F, T, H, C, dh, k;
@@ -56,20 +67,21 @@ __device__ __forceinline__ float te_arg(float dt, float w, float b) {
   return prod + b;
 }
 
-// lane's slice of X_e: c = lane + 64*j
+// This lane's slice of X_e: c = lane + 64*j. te_w / te_b are the time
+// encoding's parameters staged in LDS.
+template <int JM>
 __device__ __forceinline__ void load_x(const Dims &d, const float *__restrict__ memory,
-                                       const float *__restrict__ efeat,
-                                       const float *__restrict__ te_w,
-                                       const float *__restrict__ te_b, int64_t nb, int64_t ei,
-                                       float dtv, int lane, float (&x)[kMaxJ]) {
+                                       const float *__restrict__ efeat, const float *__restrict__ te_w,
+                                       const float *__restrict__ te_b, int nb, int ei, float dtv, int lane,
+                                       float (&x)[JM]) {
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
+  for (int j = 0; j < JM; ++j) {
     const int c = lane + 64 * j;
     float v = 0.f;
     if (c < d.D) {
-      v = memory[nb * d.D + c];
+      v = memory[size_t(nb) * d.D + c];
     } else if (c < d.D + d.F) {
-      v = efeat[ei * d.F + (c - d.D)];
+      v = efeat[size_t(ei) * d.F + (c - d.D)];
     } else if (c < d.C) {
       const int t = c - d.D - d.F;
       v = cosf(te_arg(dtv, te_w[t], te_b[t]));
@@ -93,23 +105,45 @@ struct ConvSaved {
   float *stats;  // [cap][2]     LayerNorm mean, rstd
 };
 
-__global__ __launch_bounds__(kBlock) void k_conv_fwd(
+struct FwdLds {
+  int ldh, ldr, lda, ldq;
+  float *HT;  // [16][ldh]  [h | cos(b)]
+  float *Qs;  // [16][ldr]
+  float *AH;  // [16][lda]  [agg | h]
+  float *Zs;  // [16][ldr]
+  float *QT;  // [16][ldq]  qt, then xbar
+  float *qb;  // [16][H]
+  float *TW, *TB;  // [T] time-encoding weight / bias
+};
+
+__host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base) {
+  FwdLds L;
+  L.ldh = d.D + d.T + 1;
+  L.ldr = d.D + 1;
+  L.lda = 2 * d.D + 1;
+  L.ldq = d.H * d.C + 1;
+  L.HT = base;
+  L.Qs = L.HT + kRows * L.ldh;
+  L.AH = L.Qs + kRows * L.ldr;
+  L.Zs = L.AH + kRows * L.lda;
+  L.QT = L.Zs + kRows * L.ldr;
+  L.qb = L.QT + kRows * L.ldq;
+  L.TW = L.qb + kRows * d.H;
+  L.TB = L.TW + d.T;
+  return L;
+}
+
+template <int HM, int JM, int NW = waves_for(HM, JM)>
+__global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ h_root, const float *__restrict__ memory,
     const float *__restrict__ efeat, const int32_t *__restrict__ cnt,
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ eid,
     const float *__restrict__ dt, ConvParams p, ConvSaved sv, float *__restrict__ y) {
+  constexpr int kWaves = NW, kBlock = NW * 64;
   extern __shared__ float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const int ldr = D + 1, ldq = H * C + 1;
-  float *Hd = lds;
-  float *Qs = Hd + kRows * ldr;
-  float *Ag = Qs + kRows * ldr;
-  float *Zs = Ag + kRows * ldr;
-  float *QT = Zs + kRows * ldr;
-  float *cq = QT + kRows * ldq;
-  float *phi0 = cq + D;
-  float *qb = phi0 + T;
+  const FwdLds L = fwd_lds(d, lds);
   __shared__ int s_cnt[kRows];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -132,90 +166,114 @@ __global__ __launch_bounds__(kBlock) void k_conv_fwd(
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
+  for (int t = tid; t < T; t += kBlock) {
+    L.TW[t] = p.te_w[t];
+    L.TB[t] = p.te_b[t];
+  }
+  // HT = [h | cos(b)] (TimeEncode(0) = cos(0*w + b)); AH[:, D:] = h
+  for (int idx = tid; idx < kRows * (D + T); idx += kBlock) {
+    const int i = idx / (D + T), j = idx - i * (D + T);
+    float v;
+    if (j < D) {
+      v = i < nrows ? h_root[size_t(r0 + i) * D + j] : 0.f;
+      L.AH[i * L.lda + D + j] = v;
+    } else {
+      v = cosf(p.te_b[j - D]);
+    }
+    L.HT[i * L.ldh + j] = v;
+  }
+  __syncthreads();
+  // Q = W_q [h | cos(b)] + b_q
+  sgl::tile_gemm16<sgl::kNT>(L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D, kWaves);
+  __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
-    Hd[i * ldr + j] = i < nrows ? h_root[size_t(r0 + i) * D + j] : 0.f;
-  }
-  for (int t = tid; t < T; t += kBlock) phi0[t] = cosf(p.te_b[t]);  // TimeEncode(0) = cos(0*w + b)
-  __syncthreads();
-  for (int n = tid; n < D; n += kBlock) {
-    float acc = p.b_q[n];
-    const float *wr = p.w_q + size_t(n) * (D + T) + D;
-    for (int t = 0; t < T; ++t) acc += wr[t] * phi0[t];
-    cq[n] = acc;
-  }
-  __syncthreads();
-  // Q = W_q[:, :D] h + (W_q[:, D:] cos(b) + b_q)
-  sgl::tile_gemm16<sgl::kNT>(Hd, ldr, p.w_q, D + T, cq, Qs, ldr, D, D, kWaves);
-  __syncthreads();
-  for (int idx = tid; idx < kRows * D; idx += kBlock) {
-    const int i = idx / D, j = idx - i * D;
-    sv.Q[size_t(r0 + i) * D + j] = Qs[i * ldr + j];
+    sv.Q[size_t(r0 + i) * D + j] = L.Qs[i * L.ldr + j];
   }
   if (tid < kRows * H) {
     const int i = tid / H, h = tid - (tid / H) * H;
     float acc = 0.f;
-    for (int j = 0; j < dh; ++j) acc += Qs[i * ldr + h * dh + j] * p.b_k[h * dh + j];
-    qb[i * H + h] = acc;
+    for (int j = 0; j < dh; ++j) acc += L.Qs[i * L.ldr + h * dh + j] * p.b_k[h * dh + j];
+    L.qb[i * H + h] = acc;
   }
   // qt_h = Q_h W_k[h rows, :]  (kNN: rows of W_k are the reduction index)
   for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNN>(Qs + h * dh, ldr, p.w_k + size_t(h) * dh * C, C, nullptr, QT + h * C, ldq, dh,
-                               C, kWaves);
+    sgl::tile_gemm16<sgl::kNN>(L.Qs + h * dh, L.ldr, p.w_k + size_t(h) * dh * C, C, nullptr, L.QT + h * C, L.ldq,
+                               dh, C, kWaves);
   __syncthreads();
-  for (int idx = tid; idx < kRows * H * C; idx += kBlock) {
-    const int i = idx / (H * C), hc = idx - i * (H * C);
-    sv.qt[size_t(r0 + i) * H * C + hc] = QT[i * ldq + hc];
-  }
 
-  // edge pass: one wave per root, online softmax, xbar overwrites qt in LDS
+  // edge phase: a wave owns roots wave, wave + NW, ...; xbar overwrites qt in
+  // the root's LDS row
   for (int i = wave; i < kRows; i += kWaves) {
     const int r = r0 + i;
     const int ne = s_cnt[i];
-    float q[kMaxH][kMaxJ], acc[kMaxH][kMaxJ], m[kMaxH], l[kMaxH];
+    float q[HM][JM], acc[HM][JM], m[HM], l[HM], qbh[HM];
 #pragma unroll
-    for (int h = 0; h < kMaxH; ++h) {
+    for (int h = 0; h < HM; ++h) {
       m[h] = -INFINITY;
       l[h] = 0.f;
+      qbh[h] = h < H ? L.qb[i * H + h] : 0.f;
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
+      for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
-        q[h][j] = (h < H && c < C) ? QT[i * ldq + h * C + c] : 0.f;
+        const bool ok = h < H && c < C;
+        q[h][j] = ok ? L.QT[i * L.ldq + h * C + c] : 0.f;
+        if (ok) sv.qt[size_t(r) * H * C + h * C + c] = q[h][j];
         acc[h][j] = 0.f;
       }
     }
-    for (int e = 0; e < ne; ++e) {
-      const size_t idx = size_t(r) * K + e;
-      float x[kMaxJ];
-      load_x(d, memory, efeat, p.te_w, p.te_b, nbr[idx], eid[idx], dt[idx], lane, x);
+    const size_t base = size_t(r) * K;
+    for (int e0 = 0; e0 < ne; e0 += 64) {
+      const int mwin = min(64, ne - e0);
+      int my_nb = 0, my_ei = 0;
+      float my_dt = 0.f;
+      if (lane < mwin) {
+        my_nb = nbr[base + e0 + lane];
+        my_ei = eid[base + e0 + lane];
+        my_dt = dt[base + e0 + lane];
+      }
+      for (int c0 = 0; c0 < mwin; c0 += kEC) {
+        float x[kEC][JM];
 #pragma unroll
-      for (int h = 0; h < kMaxH; ++h) {
-        if (h >= H) continue;
-        float part = 0.f;
+        for (int u = 0; u < kEC; ++u) {
+          const int e = min(c0 + u, mwin - 1);
+          load_x<JM>(d, memory, efeat, L.TW, L.TB, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
+                     __shfl(my_dt, e, 64), lane, x[u]);
+        }
 #pragma unroll
-        for (int j = 0; j < kMaxJ; ++j) part += q[h][j] * x[j];
-        const float s = wave_sum(part) + qb[i * H + h];
-        const float a = s > 0.f ? s : 0.2f * s;
-        const float mn = fmaxf(m[h], a);
-        const float sc = __expf(m[h] - mn);
-        const float pe = __expf(a - mn);
-        l[h] = l[h] * sc + pe;
+        for (int u = 0; u < kEC; ++u) {
+          if (c0 + u >= mwin) break;
+          const size_t idx = base + e0 + c0 + u;
 #pragma unroll
-        for (int j = 0; j < kMaxJ; ++j) acc[h][j] = acc[h][j] * sc + pe * x[j];
-        m[h] = mn;
-        if (lane == 0) sv.score[idx * H + h] = a;
+          for (int h = 0; h < HM; ++h) {
+            if (h >= H) continue;
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
+            const float s = wave_sum(part) + qbh[h];
+            const float a = s > 0.f ? s : 0.2f * s;
+            const float mn = fmaxf(m[h], a);
+            const float sc = __expf(m[h] - mn);
+            const float pe = __expf(a - mn);
+            l[h] = l[h] * sc + pe;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * sc + pe * x[u][j];
+            m[h] = mn;
+            if (lane == 0) sv.score[idx * H + h] = a;
+          }
+        }
       }
     }
 #pragma unroll
-    for (int h = 0; h < kMaxH; ++h) {
+    for (int h = 0; h < HM; ++h) {
       if (h >= H) continue;
       const float inv = ne > 0 ? 1.f / l[h] : 0.f;
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
+      for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
         if (c < C) {
           const float v = acc[h][j] * inv;
-          QT[i * ldq + h * C + c] = v;
+          L.QT[i * L.ldq + h * C + c] = v;
           sv.xbar[size_t(r) * H * C + h * C + c] = v;
         }
       }
@@ -226,39 +284,43 @@ __global__ __launch_bounds__(kBlock) void k_conv_fwd(
     }
   }
   __syncthreads();
-  // agg_h = W_v[h rows] xbar_h + b_v[h]
-  for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNT>(QT + h * C, ldq, p.w_v + size_t(h) * dh * C, C, p.b_v + h * dh, Ag + h * dh,
-                               ldr, C, dh, kWaves);
+  // agg_h = W_v[h rows] xbar_h + b_v[h]  -> AH[:, :D]
+  {
+    sgl::GemmJob jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.QT + h * C, L.ldq, p.w_v + size_t(h) * dh * C, C, p.b_v + h * dh, L.AH + h * dh, L.lda, C,
+                 h < H ? dh : 0};
+    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+  }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
-    if (s_cnt[i] == 0) Ag[i * ldr + j] = 0.f;  // no in-edges: the sum aggregator gives 0
-    sv.agg[size_t(r0 + i) * D + j] = Ag[i * ldr + j];
+    if (s_cnt[i] == 0) L.AH[i * L.lda + j] = 0.f;  // no in-edges: the sum aggregator gives 0
+    sv.agg[size_t(r0 + i) * D + j] = L.AH[i * L.lda + j];
   }
   __syncthreads();
-  // z = W_out[:, :D] agg + W_out[:, D:] h + b_out
-  sgl::tile_gemm16<sgl::kNT>(Ag, ldr, p.w_out, 2 * D, p.b_out, Zs, ldr, D, D, kWaves);
-  sgl::tile_gemm16<sgl::kNT, true>(Hd, ldr, p.w_out + D, 2 * D, nullptr, Zs, ldr, D, D, kWaves);
+  // z = W_out [agg | h] + b_out
+  sgl::tile_gemm16<sgl::kNT>(L.AH, L.lda, p.w_out, 2 * D, p.b_out, L.Zs, L.ldr, 2 * D, D, kWaves);
   __syncthreads();
-  // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance
+  // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance; one wave per row
   for (int i = wave; i < kRows; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
     float s1 = 0.f;
     for (int j = lane; j < D; j += 64) {
-      const float zz = Zs[i * ldr + j];
+      const float zz = L.Zs[i * L.ldr + j];
       sv.z[ro + j] = i < nrows ? zz : 0.f;
       s1 += fmaxf(zz, 0.f);
     }
     const float mean = wave_sum(s1) / D;
     float s2 = 0.f;
     for (int j = lane; j < D; j += 64) {
-      const float dv = fmaxf(Zs[i * ldr + j], 0.f) - mean;
+      const float dv = fmaxf(L.Zs[i * L.ldr + j], 0.f) - mean;
       s2 += dv * dv;
     }
     const float rstd = 1.f / sqrtf(wave_sum(s2) / D + 1e-5f);
     for (int j = lane; j < D; j += 64) {
-      const float xh = (fmaxf(Zs[i * ldr + j], 0.f) - mean) * rstd;
+      const float xh = (fmaxf(L.Zs[i * L.ldr + j], 0.f) - mean) * rstd;
       y[ro + j] = i < nrows ? xh * p.ln_g[j] + p.ln_b[j] : 0.f;
     }
     if (lane == 0) {
@@ -278,20 +340,41 @@ struct ConvGrads {
   float *te_part;  // [tiles][2][T]  per-tile time-encoding weight / bias grads
 };
 
-__global__ __launch_bounds__(kBlock) void k_conv_bwd(
+struct BwdLds {
+  int ldr, ldq;
+  float *GZ, *GA, *GQ, *XH, *GY;  // [16][ldr]
+  float *GX;                      // [16][ldq]  g_xbar, then G
+  float *tep;                     // [waves][2][T]
+  float *TW, *TB;                 // [T] time-encoding weight / bias
+};
+
+__host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base) {
+  BwdLds L;
+  L.ldr = d.D + 1;
+  L.ldq = d.H * d.C + 1;
+  L.GZ = base;
+  L.GA = L.GZ + kRows * L.ldr;
+  L.GQ = L.GA + kRows * L.ldr;
+  L.XH = L.GQ + kRows * L.ldr;
+  L.GY = L.XH + kRows * L.ldr;
+  L.GX = L.GY + kRows * L.ldr;
+  L.tep = L.GX + kRows * L.ldq;
+  L.TW = L.tep + kMaxWaves * 2 * d.T;
+  L.TB = L.TW + d.T;
+  return L;
+}
+
+template <int HM, int JM, int NW = waves_for(HM, JM)>
+__global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ memory, const float *__restrict__ efeat,
     const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, const float *__restrict__ dt, ConvParams p,
     ConvSaved sv, const float *__restrict__ gy, ConvGrads g) {
+  constexpr int kWaves = NW, kBlock = NW * 64;
   extern __shared__ float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const int ldr = D + 1, ldq = H * C + 1;
-  float *GZ = lds;
-  float *GA = GZ + kRows * ldr;
-  float *GQ = GA + kRows * ldr;
-  float *GX = GQ + kRows * ldr;      // g_xbar, then G
-  float *tep = GX + kRows * ldq;     // [kWaves][2][T]
+  const BwdLds L = bwd_lds(d, lds);
   __shared__ int s_cnt[kRows];
   __shared__ float s_sig[kRows][kMaxH];
 
@@ -312,140 +395,174 @@ __global__ __launch_bounds__(kBlock) void k_conv_bwd(
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
-  __syncthreads();
-  // LayerNorm + ReLU backward, one wave per row
+  for (int t = tid; t < T; t += kBlock) {
+    L.TW[t] = p.te_w[t];
+    L.TB[t] = p.te_b[t];
+  }
+  // LayerNorm + ReLU backward; one wave per row
   for (int i = wave; i < kRows; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
     if (i >= nrows) {
-      for (int j = lane; j < D; j += 64) GZ[i * ldr + j] = 0.f;
-      continue;
-    }
-    const float mean = sv.stats[size_t(r0 + i) * 2], rstd = sv.stats[size_t(r0 + i) * 2 + 1];
-    float a1 = 0.f, a2 = 0.f;
-    for (int j = lane; j < D; j += 64) {
-      const float xh = (fmaxf(sv.z[ro + j], 0.f) - mean) * rstd;
-      const float gxh = gy[ro + j] * p.ln_g[j];
-      a1 += gxh;
-      a2 += gxh * xh;
-    }
-    a1 = wave_sum(a1) / D;
-    a2 = wave_sum(a2) / D;
-    for (int j = lane; j < D; j += 64) {
-      const float zz = sv.z[ro + j];
-      const float xh = (fmaxf(zz, 0.f) - mean) * rstd;
-      const float gx = rstd * (gy[ro + j] * p.ln_g[j] - a1 - xh * a2);
-      GZ[i * ldr + j] = zz > 0.f ? gx : 0.f;
+      for (int j = lane; j < D; j += 64) {
+        L.GZ[i * L.ldr + j] = 0.f;
+        L.XH[i * L.ldr + j] = 0.f;
+        L.GY[i * L.ldr + j] = 0.f;
+      }
+    } else {
+      const float mean = sv.stats[size_t(r0 + i) * 2], rstd = sv.stats[size_t(r0 + i) * 2 + 1];
+      float a1 = 0.f, a2 = 0.f;
+      for (int j = lane; j < D; j += 64) {
+        const float zz = sv.z[ro + j], gv = gy[ro + j];
+        const float xh = (fmaxf(zz, 0.f) - mean) * rstd;
+        const float gxh = gv * p.ln_g[j];
+        L.XH[i * L.ldr + j] = xh;
+        L.GY[i * L.ldr + j] = gv;
+        L.GZ[i * L.ldr + j] = zz;
+        a1 += gxh;
+        a2 += gxh * xh;
+      }
+      a1 = wave_sum(a1) / D;
+      a2 = wave_sum(a2) / D;
+      for (int j = lane; j < D; j += 64) {
+        const float zz = L.GZ[i * L.ldr + j];
+        const float xh = L.XH[i * L.ldr + j];
+        const float gx = rstd * (L.GY[i * L.ldr + j] * p.ln_g[j] - a1 - xh * a2);
+        L.GZ[i * L.ldr + j] = zz > 0.f ? gx : 0.f;
+      }
     }
   }
-  // per-tile LayerNorm parameter grads
+  __syncthreads();
+  // per-tile LayerNorm parameter grads; gz out
   for (int j = tid; j < D; j += kBlock) {
     float sg = 0.f, sb = 0.f;
-    for (int i = 0; i < nrows; ++i) {
-      const size_t ro = size_t(r0 + i) * D;
-      const float mean = sv.stats[size_t(r0 + i) * 2], rstd = sv.stats[size_t(r0 + i) * 2 + 1];
-      const float xh = (fmaxf(sv.z[ro + j], 0.f) - mean) * rstd;
-      sg += gy[ro + j] * xh;
-      sb += gy[ro + j];
+#pragma unroll 4
+    for (int i = 0; i < kRows; ++i) {
+      sg += L.GY[i * L.ldr + j] * L.XH[i * L.ldr + j];
+      sb += L.GY[i * L.ldr + j];
     }
     g.ln_part[size_t(blockIdx.x) * 2 * D + j] = sg;
     g.ln_part[size_t(blockIdx.x) * 2 * D + D + j] = sb;
   }
-  __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
-    g.gz[size_t(r0 + i) * D + j] = GZ[i * ldr + j];
+    g.gz[size_t(r0 + i) * D + j] = L.GZ[i * L.ldr + j];
   }
   // g_agg = gz W_out[:, :D]
-  sgl::tile_gemm16<sgl::kNN>(GZ, ldr, p.w_out, 2 * D, nullptr, GA, ldr, D, D, kWaves);
+  sgl::tile_gemm16<sgl::kNN>(L.GZ, L.ldr, p.w_out, 2 * D, nullptr, L.GA, L.ldr, D, D, kWaves);
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
-    if (s_cnt[i] == 0) GA[i * ldr + j] = 0.f;  // agg was the constant 0
-    g.gagg[size_t(r0 + i) * D + j] = GA[i * ldr + j];
+    if (s_cnt[i] == 0) L.GA[i * L.ldr + j] = 0.f;  // agg was the constant 0
+    g.gagg[size_t(r0 + i) * D + j] = L.GA[i * L.ldr + j];
   }
   __syncthreads();
   // g_xbar_h = g_agg_h W_v[h rows, :]
   for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNN>(GA + h * dh, ldr, p.w_v + size_t(h) * dh * C, C, nullptr, GX + h * C, ldq, dh, C,
-                               kWaves);
+    sgl::tile_gemm16<sgl::kNN>(L.GA + h * dh, L.ldr, p.w_v + size_t(h) * dh * C, C, nullptr, L.GX + h * C, L.ldq,
+                               dh, C, kWaves);
   __syncthreads();
 
-  // edge backward pass: one wave per root
-  float tw[kMaxJ], tb[kMaxJ];
+  // edge backward phase: a wave owns roots wave, wave + NW, ...
+  float twp[JM], tbp[JM];  // this lane's time-encoding weight / bias partials
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) { tw[j] = 0.f; tb[j] = 0.f; }
+  for (int j = 0; j < JM; ++j) { twp[j] = 0.f; tbp[j] = 0.f; }
   for (int i = wave; i < kRows; i += kWaves) {
     const int r = r0 + i;
     const int ne = s_cnt[i];
-    float q[kMaxH][kMaxJ], xb[kMaxH][kMaxJ], gx[kMaxH][kMaxJ], G[kMaxH][kMaxJ];
-    float dot[kMaxH], sig[kMaxH], mh[kMaxH], lh[kMaxH];
+    float q[HM][JM], gx[HM][JM], G[HM][JM];
+    float dot[HM], sig[HM], mh[HM], lh[HM];
 #pragma unroll
-    for (int h = 0; h < kMaxH; ++h) {
+    for (int h = 0; h < HM; ++h) {
       float pd = 0.f;
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
+      for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
         const bool ok = h < H && c < C;
         q[h][j] = ok ? sv.qt[size_t(r) * H * C + h * C + c] : 0.f;
-        xb[h][j] = ok ? sv.xbar[size_t(r) * H * C + h * C + c] : 0.f;
-        gx[h][j] = ok ? GX[i * ldq + h * C + c] : 0.f;
+        const float xb = ok ? sv.xbar[size_t(r) * H * C + h * C + c] : 0.f;
+        gx[h][j] = ok ? L.GX[i * L.ldq + h * C + c] : 0.f;
         G[h][j] = 0.f;
-        pd += gx[h][j] * xb[h][j];
+        pd += gx[h][j] * xb;
       }
       dot[h] = wave_sum(pd);
       sig[h] = 0.f;
       mh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2] : 0.f;
       lh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2 + 1] : 1.f;
     }
-    for (int e = 0; e < ne; ++e) {
-      const size_t idx = size_t(r) * K + e;
-      const float dtv = dt[idx];
-      float x[kMaxJ];
-      load_x(d, memory, efeat, p.te_w, p.te_b, nbr[idx], eid[idx], dtv, lane, x);
-      float gsv[kMaxH], al[kMaxH];
+    const size_t base = size_t(r) * K;
+    for (int e0 = 0; e0 < ne; e0 += 64) {
+      const int mwin = min(64, ne - e0);
+      int my_nb = 0, my_ei = 0;
+      float my_dt = 0.f, my_sc[HM];
 #pragma unroll
-      for (int h = 0; h < kMaxH; ++h) {
-        gsv[h] = 0.f;
-        al[h] = 0.f;
-        if (h >= H) continue;
-        float part = 0.f;
+      for (int h = 0; h < HM; ++h) my_sc[h] = 0.f;
+      if (lane < mwin) {
+        my_nb = nbr[base + e0 + lane];
+        my_ei = eid[base + e0 + lane];
+        my_dt = dt[base + e0 + lane];
 #pragma unroll
-        for (int j = 0; j < kMaxJ; ++j) part += gx[h][j] * x[j];
-        const float t = wave_sum(part);
-        const float a = sv.score[idx * H + h];
-        const float alpha = __expf(a - mh[h]) / lh[h];
-        const float ga = alpha * (t - dot[h]);  // softmax backward
-        const float gs = ga * (a > 0.f ? 1.f : 0.2f);
-        gsv[h] = gs;
-        al[h] = alpha;
-        sig[h] += gs;
-#pragma unroll
-        for (int j = 0; j < kMaxJ; ++j) G[h][j] += gs * x[j];
+        for (int h = 0; h < HM; ++h)
+          if (h < H) my_sc[h] = sv.score[(base + e0 + lane) * H + h];
       }
-      // time-encoding gradients for this edge's T columns
+      for (int c0 = 0; c0 < mwin; c0 += kEC) {
+        float x[kEC][JM];
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
-        const int c = lane + 64 * j;
-        if (c >= d.D + d.F && c < C) {
-          float gphi = 0.f;
+        for (int u = 0; u < kEC; ++u) {
+          const int e = min(c0 + u, mwin - 1);
+          load_x<JM>(d, memory, efeat, L.TW, L.TB, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
+                     __shfl(my_dt, e, 64), lane, x[u]);
+        }
 #pragma unroll
-          for (int h = 0; h < kMaxH; ++h)
-            if (h < H) gphi += gsv[h] * q[h][j] + al[h] * gx[h][j];
-          const int t = c - d.D - d.F;
-          const float ds = -sinf(te_arg(dtv, p.te_w[t], p.te_b[t])) * gphi;
-          tw[j] += ds * dtv;
-          tb[j] += ds;
+        for (int u = 0; u < kEC; ++u) {
+          if (c0 + u >= mwin) break;
+          const int e = c0 + u;
+          const float dtv = __shfl(my_dt, e, 64);
+          float gsv[HM], al[HM];
+#pragma unroll
+          for (int h = 0; h < HM; ++h) {
+            gsv[h] = 0.f;
+            al[h] = 0.f;
+            if (h >= H) continue;
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) part += gx[h][j] * x[u][j];
+            const float t = wave_sum(part);
+            const float a = __shfl(my_sc[h], e, 64);
+            const float alpha = __expf(a - mh[h]) / lh[h];
+            const float ga = alpha * (t - dot[h]);  // softmax backward
+            const float gs = ga * (a > 0.f ? 1.f : 0.2f);
+            gsv[h] = gs;
+            al[h] = alpha;
+            sig[h] += gs;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) G[h][j] += gs * x[u][j];
+          }
+          // time-encoding gradients for this edge's T columns
+#pragma unroll
+          for (int j = 0; j < JM; ++j) {
+            const int c = lane + 64 * j;
+            if (c >= D + d.F && c < C) {
+              float gphi = 0.f;
+#pragma unroll
+              for (int h = 0; h < HM; ++h)
+                if (h < H) gphi += gsv[h] * q[h][j] + al[h] * gx[h][j];
+              const int t = c - D - d.F;
+              const float ds = -sinf(te_arg(dtv, L.TW[t], L.TB[t])) * gphi;
+              twp[j] += ds * dtv;
+              tbp[j] += ds;
+            }
+          }
         }
       }
     }
 #pragma unroll
-    for (int h = 0; h < kMaxH; ++h) {
+    for (int h = 0; h < HM; ++h) {
       if (h >= H) continue;
 #pragma unroll
-      for (int j = 0; j < kMaxJ; ++j) {
+      for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
         if (c < C) {
-          GX[i * ldq + h * C + c] = G[h][j];
+          L.GX[i * L.ldq + h * C + c] = G[h][j];
           g.G[size_t(r) * H * C + h * C + c] = G[h][j];
         }
       }
@@ -457,40 +574,50 @@ __global__ __launch_bounds__(kBlock) void k_conv_bwd(
   }
   // reduce the waves' time-encoding partials
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
+  for (int j = 0; j < JM; ++j) {
     const int c = lane + 64 * j;
-    if (c >= d.D + d.F && c < C) {
-      const int t = c - d.D - d.F;
-      tep[(wave * 2 + 0) * T + t] = tw[j];
-      tep[(wave * 2 + 1) * T + t] = tb[j];
+    if (c >= D + d.F && c < C) {
+      const int t = c - D - d.F;
+      L.tep[(wave * 2 + 0) * T + t] = twp[j];
+      L.tep[(wave * 2 + 1) * T + t] = tbp[j];
     }
   }
   __syncthreads();
   for (int t = tid; t < T; t += kBlock) {
     float a = 0.f, b = 0.f;
-    for (int w = 0; w < kWaves; ++w) { a += tep[(w * 2) * T + t]; b += tep[(w * 2 + 1) * T + t]; }
+    for (int w = 0; w < kWaves; ++w) { a += L.tep[(w * 2) * T + t]; b += L.tep[(w * 2 + 1) * T + t]; }
     g.te_part[size_t(blockIdx.x) * 2 * T + t] = a;
     g.te_part[size_t(blockIdx.x) * 2 * T + T + t] = b;
   }
   // gQ_h = W_k[h rows] G_h + b_k[h] sigma_h
-  for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNT>(GX + h * C, ldq, p.w_k + size_t(h) * dh * C, C, nullptr, GQ + h * dh, ldr, C, dh,
-                               kWaves);
+  {
+    sgl::GemmJob jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.GX + h * C, L.ldq, p.w_k + size_t(h) * dh * C, C, nullptr, L.GQ + h * dh, L.ldr, C,
+                 h < H ? dh : 0};
+    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+  }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     const int h = j / dh;
-    const float v = i < nrows ? GQ[i * ldr + j] + p.b_k[j] * s_sig[i][h] : 0.f;
+    const float v = i < nrows ? L.GQ[i * L.ldr + j] + p.b_k[j] * s_sig[i][h] : 0.f;
     g.gQ[size_t(r0 + i) * D + j] = v;
   }
 }
 
+// LDS sizes from the same carving as the kernels (on a dummy base address)
 size_t fwd_lds_bytes(const Dims &d) {
-  return sizeof(float) * (size_t(kRows) * (4 * (d.D + 1) + d.H * d.C + 1) + d.D + d.T + kRows * d.H);
+  float *base = reinterpret_cast<float *>(uintptr_t(4096));
+  const FwdLds L = fwd_lds(d, base);
+  return sizeof(float) * size_t(L.TB + d.T - base);
 }
 
 size_t bwd_lds_bytes(const Dims &d) {
-  return sizeof(float) * (size_t(kRows) * (3 * (d.D + 1) + d.H * d.C + 1) + size_t(kWaves) * 2 * d.T);
+  float *base = reinterpret_cast<float *>(uintptr_t(4096));
+  const BwdLds L = bwd_lds(d, base);
+  return sizeof(float) * size_t(L.TB + d.T - base);
 }
 
 int check_dims(const Dims &d) {
@@ -500,6 +627,39 @@ int check_dims(const Dims &d) {
   SGL_REQUIRE(d.k >= 0 && d.k <= 4096, "conv: fanout %d out of range", d.k);
   return SGL_OK;
 }
+
+// Kernel instance for (H, C): register arrays sized to the next supported
+// head count (1, 2, 4) and column-slot count (2, 4, 6, 8 slots of 64).
+template <typename Fn>
+struct Instance {
+  Fn fn;
+  int waves;
+};
+
+template <template <int, int> class Pick>
+auto pick_instance(const Dims &d) -> decltype(Pick<1, 2>::get()) {
+  const int j = (d.C + 63) / 64;
+  const int jm = j <= 2 ? 2 : j <= 4 ? 4 : j <= 6 ? 6 : 8;
+  const int hm = d.H <= 1 ? 1 : d.H <= 2 ? 2 : 4;
+#define SGL_PICK(HH, JJ) \
+  if (hm == HH && jm == JJ) return Pick<HH, JJ>::get();
+  SGL_PICK(1, 2) SGL_PICK(1, 4) SGL_PICK(1, 6) SGL_PICK(1, 8)
+  SGL_PICK(2, 2) SGL_PICK(2, 4) SGL_PICK(2, 6) SGL_PICK(2, 8)
+  SGL_PICK(4, 2) SGL_PICK(4, 4) SGL_PICK(4, 6) SGL_PICK(4, 8)
+#undef SGL_PICK
+  return {nullptr, 0};
+}
+
+using FwdFn = decltype(&k_conv_fwd<1, 2>);
+using BwdFn = decltype(&k_conv_bwd<1, 2>);
+template <int HM, int JM>
+struct FwdPick {
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM>, waves_for(HM, JM)}; }
+};
+template <int HM, int JM>
+struct BwdPick {
+  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM>, waves_for(HM, JM)}; }
+};
 
 }  // namespace
 
@@ -523,12 +683,13 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
               "conv_forward: NULL array");
   const size_t lds = fwd_lds_bytes(d);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
-  SGL_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_conv_fwd),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  const auto inst = pick_instance<FwdPick>(d);
+  SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats};
-  k_conv_fwd<<<unsigned(capacity / kRows), kBlock, lds, stream>>>(d, num_roots, any_edges, h_root, memory, efeat,
-                                                                   cnt, nbr, eid, dt, p, sv, y);
+  inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
+      d, num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -554,15 +715,16 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
               "conv_backward: NULL array");
   const size_t lds = bwd_lds_bytes(d);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
-  SGL_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_conv_bwd),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  const auto inst = pick_instance<BwdPick>(d);
+  SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
                const_cast<float *>(sv_z), const_cast<float *>(sv_stats)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
-  k_conv_bwd<<<unsigned(capacity / kRows), kBlock, lds, stream>>>(d, num_roots, any_edges, memory, efeat, cnt, nbr,
-                                                                  eid, dt, p, sv, gy, g);
+  inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
+      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -17,6 +17,11 @@ void clear_error();
 
 constexpr int kWave = 64;
 
+// Raises a kernel's dynamic-LDS limit to at least `bytes` (the first call per
+// kernel and size only; thread-safe). Keeps hipFuncSetAttribute out of the
+// steady state, and so out of captured HIP graphs once a step has run.
+hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes);
+
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 
 // Carves aligned sub-buffers out of a caller-provided workspace.

@@ -1,6 +1,8 @@
-// C-ABI error state and version query.
+// C-ABI error state, version query and the once-per-kernel LDS attribute.
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -16,6 +18,17 @@ void set_error(const char *fmt, ...) {
 }
 
 void clear_error() { g_last_error[0] = 0; }
+
+hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes) {
+  static std::mutex mu;
+  static std::unordered_map<const void *, size_t> done;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = done.find(kernel);
+  if (it != done.end() && it->second >= bytes) return hipSuccess;
+  const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+  if (e == hipSuccess) done[kernel] = bytes;
+  return e;
+}
 
 }  // namespace sgl
 

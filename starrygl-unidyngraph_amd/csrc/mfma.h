@@ -1,16 +1,28 @@
 // Row-tile GEMM primitives on CDNA MFMA for the fused per-root kernels.
 //
-// A workgroup owns a tile of 16 rows (roots / nodes) whose activations sit in
+// A workgroup owns a tile of 16 rows (roots / events) whose activations sit in
 // LDS; weights stream from global memory (L2-resident: every weight matrix on
 // this path is < 1 MB). A wave computes 16x16 output blocks with
 // v_mfma_f32_16x16x4_f32 (fp32 in, fp32 accumulate).
 //
-// Lane layout of v_mfma_f32_16x16x4_f32 (one block, K = 4):
-//   A[i][k] comes from lane i + 16*k, B[k][j] from lane j + 16*k,
+// Lane layout of v_mfma_f32_16x16x4_f32 (one block, K = 4 per instruction):
+//   A[i][k] comes from lane i + 16*q, B[k][j] from lane j + 16*q (q = 0..3
+//   picks which of the instruction's 4 k values the lane supplies),
 //   D[i][j] lands in lane j + 16*(i/4), accumulator element i%4.
+// Which actual k a (lane, instruction) pair supplies is free as long as A and
+// B agree. Here lane q supplies k = 16g + 4q + s in instruction s of group g,
+// so each lane reads four consecutive k values of its row: one 16-byte load
+// from global memory (weights) and one from LDS (activations).
+//
+// The blocks are latency-bound (16 rows, a few hundred k), so the weight loads
+// of a whole 64-k chunk are issued before its MFMAs, and the next chunk's
+// loads before the current chunk's MFMAs (two register buffers). Weight
+// matrices are < 4 GiB, so element offsets are 32-bit.
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <cstdint>
 
 namespace sgl {
 
@@ -20,6 +32,90 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 //   kNT: W is [N][ldw] row-major and OUT[i][n] = sum_k A[i][k] * W[n][k]   (nn.Linear weight)
 //   kNN: W is [K][ldw] row-major and OUT[i][n] = sum_k A[i][k] * W[k][n]
 enum WLayout { kNT = 0, kNN = 1 };
+
+constexpr int kChunkGroups = 4;  // 4 groups of 16 k = 64 k per chunk
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Weight reads go through a raw buffer resource whose range is exactly the
+// operand's span: elements past it read as 0 without a branch or a fault, so
+// the loads of a chunk issue back to back. The whole byte offset is in the
+// VGPR operand (the range check does not cover the scalar offset).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const float *p, uint32_t nfloats) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, int(nfloats * 4u), 0x00020000);
+}
+
+__device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(elem * 4u), 0, 0));
+}
+
+__device__ __forceinline__ f32x4 buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, int(elem * 4u), 0, 0);
+  f32x4 f;
+  f[0] = __uint_as_float(v[0]); f[1] = __uint_as_float(v[1]);
+  f[2] = __uint_as_float(v[2]); f[3] = __uint_as_float(v[3]);
+  return f;
+}
+
+__device__ __forceinline__ bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// b[g][s] = op(W)[k][n] for k = kb + 16g + 4q + s. Positions past the
+// operand's span read 0; positions inside it but outside k < kd or
+// n < n_total read neighbouring (finite) weights, which meet a zero A element
+// (k) or land in a discarded output column (n).
+template <int LAYOUT>
+__device__ __forceinline__ void load_w_chunk(float (&b)[kChunkGroups][4], __amdgpu_buffer_rsrc_t W, int ldw, int n,
+                                             int kb, int q, bool vec) {
+  if (LAYOUT == kNT && vec) {
+    // ldw % 4 == 0, kd % 4 == 0, 16-byte aligned base: one 16-byte load per group
+    const uint32_t row = uint32_t(n) * uint32_t(ldw) + uint32_t(kb + 4 * q);
+#pragma unroll
+    for (int g = 0; g < kChunkGroups; ++g) {
+      const f32x4 v = buf_load4(W, row + 16u * g);
+      b[g][0] = v[0]; b[g][1] = v[1]; b[g][2] = v[2]; b[g][3] = v[3];
+    }
+  } else if (LAYOUT == kNT) {
+    const uint32_t row = uint32_t(n) * uint32_t(ldw) + uint32_t(kb + 4 * q);
+#pragma unroll
+    for (int g = 0; g < kChunkGroups; ++g)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[g][s] = buf_load(W, row + uint32_t(16 * g + s));
+  } else {
+    const uint32_t col = uint32_t(kb + 4 * q) * uint32_t(ldw) + uint32_t(n);
+#pragma unroll
+    for (int g = 0; g < kChunkGroups; ++g)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[g][s] = buf_load(W, col + uint32_t(16 * g + s) * uint32_t(ldw));
+  }
+}
+
+// acc += A[rows][kb .. kb+64) * b, A read from LDS (0 for k >= kd)
+__device__ __forceinline__ void mfma_chunk(f32x4 &acc, const float (&b)[kChunkGroups][4],
+                                           const float *__restrict__ A, int lda, int i, int kb, int kd, int q,
+                                           bool avec) {
+  const float *arow = A + i * lda;
+#pragma unroll
+  for (int g = 0; g < kChunkGroups; ++g) {
+    const int k = kb + 16 * g + 4 * q;
+    if (kb + 16 * g >= kd) break;  // uniform across the wave
+    float a[4];
+    if (avec) {
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(arow + min(k, kd - 4));
+      const bool ok = k < kd;
+      a[0] = ok ? v[0] : 0.f; a[1] = ok ? v[1] : 0.f; a[2] = ok ? v[2] : 0.f; a[3] = ok ? v[3] : 0.f;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float v = arow[min(k + s, kd - 1)];
+        a[s] = (k + s < kd) ? v : 0.f;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[g][s], acc, 0, 0, 0);
+  }
+}
 
 // One 16x16 output block: rows 0..15 of A (LDS, leading dim lda), columns
 // n0..n0+15 of op(W), reduction over k in [0, kd). Out-of-range k or n read
@@ -31,33 +127,26 @@ __device__ __forceinline__ f32x4 mfma_block16(const float *__restrict__ A, int l
                                               int n0, int kd, int n_total) {
   const int lane = threadIdx.x & 63;
   const int i = lane & 15;
-  const int kq = lane >> 4;
+  const int q = lane >> 4;
   const int n = n0 + i;
-  const bool n_ok = n < n_total;
+  // the operand's span: rows of op(W)^T up to the last used element
+  const uint32_t span = LAYOUT == kNT ? uint32_t(n_total - 1) * uint32_t(ldw) + uint32_t(kd)
+                                      : uint32_t(kd - 1) * uint32_t(ldw) + uint32_t(n_total);
+  const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, span);
+  // 16-byte loads: aligned, and never straddling the span end (kd % 4 == 0)
+  const bool wvec = LAYOUT == kNT && (kd & 3) == 0 && (ldw & 3) == 0 && aligned16(W);
+  const bool avec = (kd & 3) == 0 && (lda & 3) == 0 && aligned16(A);
+  constexpr int kc = 16 * kChunkGroups;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int k0 = 0;
-  // main loop: 4 k-steps (16 values) per iteration, loads issued before MFMAs
-  for (; k0 + 16 <= kd; k0 += 16) {
-    float a[4], b[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int k = k0 + 4 * s + kq;
-      a[s] = A[i * lda + k];
-      if (LAYOUT == kNT)
-        b[s] = n_ok ? W[size_t(n) * ldw + k] : 0.f;
-      else
-        b[s] = n_ok ? W[size_t(k) * ldw + n] : 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
-  }
-  for (; k0 < kd; k0 += 4) {
-    const int k = k0 + kq;
-    const bool k_ok = k < kd;
-    const float a = k_ok ? A[i * lda + k] : 0.f;
-    float b = 0.f;
-    if (k_ok && n_ok) b = (LAYOUT == kNT) ? W[size_t(n) * ldw + k] : W[size_t(k) * ldw + n];
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+  float b0[kChunkGroups][4], b1[kChunkGroups][4];
+  load_w_chunk<LAYOUT>(b0, wr, ldw, n, 0, q, wvec);
+  for (int kb = 0; kb < kd; kb += 2 * kc) {
+    const bool more = kb + kc < kd;
+    if (more) load_w_chunk<LAYOUT>(b1, wr, ldw, n, kb + kc, q, wvec);
+    mfma_chunk(acc, b0, A, lda, i, kb, kd, q, avec);
+    if (!more) break;
+    if (kb + 2 * kc < kd) load_w_chunk<LAYOUT>(b0, wr, ldw, n, kb + 2 * kc, q, wvec);
+    mfma_chunk(acc, b1, A, lda, i, kb + kc, kd, q, avec);
   }
   return acc;
 }
@@ -87,6 +176,52 @@ __device__ __forceinline__ void tile_gemm16(const float *__restrict__ A, int lda
         if (ACC) o += OUT[row * ldo + col];
         OUT[row * ldo + col] = o;
       }
+    }
+  }
+}
+
+// Several independent OUT = A * op(W) + bias products of one layout, their
+// 16x16 blocks dealt over the workgroup's waves together (so a wave is not
+// idle in one product while another has blocks left). No barrier inside.
+struct GemmJob {
+  const float *A;
+  int lda;
+  const float *W;
+  int ldw;
+  const float *bias;  // may be NULL
+  float *OUT;
+  int ldo;
+  int kd, n_total;
+};
+
+template <int LAYOUT, int NJOBS>
+__device__ __forceinline__ void tile_gemm16_jobs(const GemmJob (&jobs)[NJOBS], int nwaves) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < NJOBS; ++j) total += (jobs[j].n_total + 15) >> 4;
+  for (int blk = wave; blk < total; blk += nwaves) {
+    // find the job of this block with unrolled selects (no dynamic indexing
+    // of the local array, which would go through scratch memory)
+    GemmJob jb = jobs[0];
+    int nb = blk, first = 0;
+#pragma unroll
+    for (int j = 0; j < NJOBS; ++j) {
+      const int nbj = (jobs[j].n_total + 15) >> 4;
+      if (blk >= first && blk < first + nbj) {
+        jb = jobs[j];
+        nb = blk - first;
+      }
+      first += nbj;
+    }
+    const int n0 = nb * 16;
+    f32x4 acc = mfma_block16<LAYOUT>(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
+    const int col = n0 + (lane & 15);
+    if (col < jb.n_total) {
+      const float bv = jb.bias != nullptr ? jb.bias[col] : 0.f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;
     }
   }
 }

@@ -1,5 +1,5 @@
-// Edge predictor + BCE loss, forward and backward, one workgroup per 16
-// events. Reference: CTDGLinkPredictor.forward (backends/ctdg/runtime/models.py:313-324),
+// Edge predictor + BCE loss, forward and backward, one workgroup (16 waves)
+// per 16 events. Reference: CTDGLinkPredictor.forward (backends/ctdg/runtime/models.py:313-324),
 // the root-row selection of _conv_output (runtime.py:176-183) and the loss of
 // train_step (runtime.py:290-292):
 //   e_s = y[rs], e_d = y[rd], e_n = y[rn] (0 when the negative is not a root)
@@ -16,9 +16,9 @@
 
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 1024;
 constexpr int kRows = 16;
-constexpr int kWaves = kBlock / 64;
+constexpr int kWaves = kBlock / 64;  // one event per wave for the logits
 
 __device__ __forceinline__ float softplus(float x) {
   // log(1 + exp(x)), stable: max(x, 0) + log1p(exp(-|x|))
@@ -27,9 +27,9 @@ __device__ __forceinline__ float softplus(float x) {
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
-__global__ __launch_bounds__(kBlock) void k_zero(float *__restrict__ a, int64_t n, float *__restrict__ b,
+__global__ __launch_bounds__(256) void k_zero(float *__restrict__ a, int64_t n, float *__restrict__ b,
                                                  int64_t m) {
-  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) a[i] = 0.f;
   if (i < m) b[i] = 0.f;
 }
@@ -72,9 +72,11 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     En[i * ld + j] = c >= 0 ? y[size_t(c) * D + j] : 0.f;
   }
   __syncthreads();
-  sgl::tile_gemm16<sgl::kNT>(Es, ld, w_s, D, b_s, Hs, ld, D, D, kWaves);
-  sgl::tile_gemm16<sgl::kNT>(Ed, ld, w_d, D, b_d, Hd, ld, D, D, kWaves);
-  sgl::tile_gemm16<sgl::kNT>(En, ld, w_d, D, b_d, Hn, ld, D, D, kWaves);
+  {
+    sgl::GemmJob jobs[3] = {{Es, ld, w_s, D, b_s, Hs, ld, D, D}, {Ed, ld, w_d, D, b_d, Hd, ld, D, D},
+                            {En, ld, w_d, D, b_d, Hn, ld, D, D}};
+    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+  }
   __syncthreads();
   // logits, loss, logit gradients: one wave per event
   for (int i = wave; i < kRows; i += kWaves) {
@@ -179,14 +181,13 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
               "predictor: NULL array");
   SGL_REQUIRE(!train || (gy && g_ws && g_bs && g_wd && g_bd && g_wo && g_bo), "predictor: NULL gradient array");
   const int64_t nz = train ? capacity * D : 0;
-  const int64_t zb = ((nz > 1 ? nz : 1) + kBlock - 1) / kBlock;
-  k_zero<<<unsigned(zb), kBlock, 0, stream>>>(gy, nz, loss, 1);
+  const int64_t zb = ((nz > 1 ? nz : 1) + 255) / 256;
+  k_zero<<<unsigned(zb), 256, 0, stream>>>(gy, nz, loss, 1);
   SGL_CHECK_LAUNCH();
   if (batch == 0) return SGL_OK;
   const size_t lds = sizeof(float) * size_t(kRows) * 7 * (D + 1);
   SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
-  SGL_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_predictor),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
   k_predictor<<<unsigned((batch + kRows - 1) / kRows), kBlock, lds, stream>>>(
       batch, D, train, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
       gy, g_ws, g_bs, g_wd, g_bd, g_wo, g_bo);

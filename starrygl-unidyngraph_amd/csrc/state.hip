@@ -37,7 +37,7 @@ __device__ __forceinline__ int32_t node_rank(const uint32_t *__restrict__ bits,
 
 __global__ __launch_bounds__(kBlock) void k_step_mark(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
-    const int64_t *__restrict__ dst, uint32_t *__restrict__ bits,
+    const int64_t *__restrict__ dst, const int64_t *__restrict__ event_offset, uint32_t *__restrict__ bits,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst,
     int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
@@ -50,7 +50,8 @@ __global__ __launch_bounds__(kBlock) void k_step_mark(
     cnt_dst[r] = 0;
   }
   if (e >= batch) return;
-  const int64_t s = src[e], d = dst[e];
+  const int64_t off = event_offset != nullptr ? *event_offset : 0;
+  const int64_t s = src[off + e], d = dst[off + e];
   if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
     if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
     return;
@@ -64,7 +65,9 @@ __global__ __launch_bounds__(kBlock) void k_step_mark(
 __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     int64_t nwords, const uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
-    const float *__restrict__ ts, float *__restrict__ ts_max, int64_t *__restrict__ t_query) {
+    const float *__restrict__ ts, const int64_t *__restrict__ event_offset, float *__restrict__ ts_max,
+    int64_t *__restrict__ t_query) {
+  if (event_offset != nullptr) ts += *event_offset;
   __shared__ int32_t s_w[kScanBlock / sgl::kWave];
   __shared__ float s_m[kScanBlock / sgl::kWave];
   const int64_t per = (nwords + kScanBlock - 1) / kScanBlock;
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
 __global__ __launch_bounds__(kBlock) void k_step_index(
     int64_t batch, int64_t num_nodes, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
-    const float *__restrict__ ts, const uint32_t *__restrict__ bits,
+    const float *__restrict__ ts, const int64_t *__restrict__ event_offset, const uint32_t *__restrict__ bits,
     const int32_t *__restrict__ prefix, const int64_t *__restrict__ t_query,
     int64_t *__restrict__ roots, int64_t *__restrict__ root_ts,
     int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst,
@@ -108,6 +111,12 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
     int32_t *__restrict__ cnt_dst) {
   const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (e >= batch) return;
+  if (event_offset != nullptr) {
+    const int64_t off = *event_offset;
+    src += off;
+    dst += off;
+    ts += off;
+  }
   const int64_t s = src[e], d = dst[e];
   if (neg != nullptr) {
     const int64_t n = neg[e];
@@ -151,9 +160,18 @@ __device__ __forceinline__ float gru_combine(float gir, float giz, float gin, fl
   return (1.f - z) * n + z * h;
 }
 
-// One workgroup = 16 roots. LDS: x [16][S], h [16][D], mem [16][D],
-// gi [16][3D], gh [16][3D] (leading dims padded by one float).
-__global__ __launch_bounds__(kBlock) void k_gru_mailbox(
+constexpr int kGruBlock = 1024;
+constexpr int kGruWaves = kGruBlock / sgl::kWave;
+constexpr int kMaxMsgSlots = 8;  // S = 2D + F <= 512
+static_assert(kGruWaves == kTileRows, "the mailbox phase maps wave w to root w");
+
+// One workgroup of 16 waves = 16 roots. LDS: x [16][S], h [16][D],
+// mem [16][D], gi [16][3D], gh [16][3D] (leading dims padded by one float).
+// Wave i also assembles root i's outgoing messages: their foreign parts (the
+// other endpoint's memory row and the edge's features) are loaded into
+// registers before the GEMMs and stored after them, so the loads overlap
+// the GRU arithmetic.
+__global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     int D, int K, int F, const int32_t *__restrict__ num_roots,
     const int64_t *__restrict__ roots, const float *__restrict__ memory,
     float *__restrict__ mailbox, float *__restrict__ mailbox_ts,
@@ -163,7 +181,8 @@ __global__ __launch_bounds__(kBlock) void k_gru_mailbox(
     const float *__restrict__ wc_hh, const float *__restrict__ bc_ih,
     const float *__restrict__ bc_hh, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const float *__restrict__ efeat,
-    const float *__restrict__ ts, const unsigned long long *__restrict__ win_src,
+    const float *__restrict__ ts, const int64_t *__restrict__ event_offset,
+    const unsigned long long *__restrict__ win_src,
     const unsigned long long *__restrict__ win_dst, const int32_t *__restrict__ cnt_src,
     const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
   extern __shared__ float lds[];
@@ -175,29 +194,76 @@ __global__ __launch_bounds__(kBlock) void k_gru_mailbox(
   float *ms = hs + kTileRows * ldh;
   float *gi = ms + kTileRows * ldh;
   float *gh = gi + kTileRows * ldg;
+  __shared__ int64_t s_root[kTileRows], s_e[2][kTileRows];
+  __shared__ int32_t s_cnt[2][kTileRows];
   const int U = *num_roots;
   const int r0 = blockIdx.x * kTileRows;
   if (r0 >= U) return;  // uniform per workgroup
   const int nrows = min(kTileRows, U - r0);
-  const int tid = threadIdx.x;
-  const int nwaves = kBlock / sgl::kWave;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  for (int idx = tid; idx < kTileRows * D; idx += kBlock) {
-    const int i = idx / D, j = idx - (idx / D) * D;
-    ms[i * ldh + j] = i < nrows ? memory[roots[r0 + i] * D + j] : 0.f;
+  if (event_offset != nullptr) {  // event arrays are the whole stream
+    const int64_t off = *event_offset;
+    src += off;
+    dst += off;
+    ts += off;
+    efeat += off * F;
+  }
+  if (tid < kTileRows) {
+    const bool ok = tid < nrows;
+    s_root[tid] = ok ? roots[r0 + tid] : 0;
+    s_cnt[0][tid] = ok ? cnt_src[r0 + tid] : 0;
+    s_cnt[1][tid] = ok ? cnt_dst[r0 + tid] : 0;
+    s_e[0][tid] = ok ? int64_t(win_src[r0 + tid] & 0xffffffffull) : 0;
+    s_e[1][tid] = ok ? int64_t(win_dst[r0 + tid] & 0xffffffffull) : 0;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
+    const int i = idx / D, j = idx - i * D;
+    ms[i * ldh + j] = i < nrows ? memory[s_root[i] * D + j] : 0.f;
     hs[i * ldh + j] = 0.f;
+  }
+  // Mailbox messages (memory.py:218-248): the src-role message of node u is
+  // [mem(u) || mem(other) || f_e] of its last src event e, the dst-role one
+  // the same for its last dst event. Prefetch the foreign parts.
+  const int i_msg = wave;
+  const bool msg_row = i_msg < nrows;
+  float part[2][kMaxMsgSlots];
+  float ts_e[2] = {0.f, 0.f};
+  int p_slot = 0;
+  if (msg_row) {
+    const int64_t u = s_root[i_msg];
+    p_slot = next_mail_pos[u];
+#pragma unroll
+    for (int role = 0; role < 2; ++role) {
+      const bool has = s_cnt[role][i_msg] > 0;
+      const int64_t e = s_e[role][i_msg];
+      const int64_t other = has ? (role == 0 ? dst[e] : src[e]) : 0;
+      if (has) ts_e[role] = ts[e];
+#pragma unroll
+      for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
+        const int c = lane + 64 * jj;
+        float v = 0.f;
+        if (has && c >= D && c < 2 * D) v = memory[other * D + (c - D)];
+        else if (has && c >= 2 * D && c < S) v = efeat[e * F + (c - 2 * D)];
+        part[role][jj] = v;
+      }
+    }
   }
   // GRU layer over the K mailbox slots in slot-index order, h0 = 0
   for (int k = 0; k < K; ++k) {
-    for (int idx = tid; idx < kTileRows * S; idx += kBlock) {
+    for (int idx = tid; idx < kTileRows * S; idx += kGruBlock) {
       const int i = idx / S, j = idx - (idx / S) * S;
-      xs[i * ldx + j] = i < nrows ? mailbox[(roots[r0 + i] * K + k) * S + j] : 0.f;
+      xs[i * ldx + j] = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
     }
     __syncthreads();
-    sgl::tile_gemm16<sgl::kNT>(xs, ldx, w_ih, S, b_ih, gi, ldg, S, G, nwaves);
-    if (k > 0) sgl::tile_gemm16<sgl::kNT>(hs, ldh, w_hh, D, b_hh, gh, ldg, D, G, nwaves);
+    {
+      sgl::GemmJob jobs[2] = {{xs, ldx, w_ih, S, b_ih, gi, ldg, S, G},
+                              {hs, ldh, w_hh, D, b_hh, gh, ldg, D, k > 0 ? G : 0}};
+      sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
+    }
     __syncthreads();
-    for (int idx = tid; idx < kTileRows * D; idx += kBlock) {
+    for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
       const int i = idx / D, j = idx - (idx / D) * D;
       const float *g1 = gi + i * ldg;
       float ghr, ghz, ghn;
@@ -212,10 +278,12 @@ __global__ __launch_bounds__(kBlock) void k_gru_mailbox(
     __syncthreads();
   }
   // GRUCell(agg = h, memory)
-  sgl::tile_gemm16<sgl::kNT>(hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G, nwaves);
-  sgl::tile_gemm16<sgl::kNT>(ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G, nwaves);
+  {
+    sgl::GemmJob jobs[2] = {{hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G}, {ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G}};
+    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
+  }
   __syncthreads();
-  for (int idx = tid; idx < nrows * D; idx += kBlock) {
+  for (int idx = tid; idx < nrows * D; idx += kGruBlock) {
     const int i = idx / D, j = idx - (idx / D) * D;
     const float *g1 = gi + i * ldg;
     const float *g2 = gh + i * ldg;
@@ -223,38 +291,30 @@ __global__ __launch_bounds__(kBlock) void k_gru_mailbox(
         gru_combine(g1[j], g1[D + j], g1[2 * D + j], g2[j], g2[D + j], g2[2 * D + j], ms[i * ldh + j]);
   }
 
-  // Mailbox write (memory.py:218-248): the src-role message of node u is
-  // [mem(u) || mem(other) || f_e] of its last src event, written to slot p =
-  // next_mail_pos[u]; the dst-role message goes to (p + #src occurrences) % K,
-  // so with one slot the dst role wins. The memory table still holds the
-  // pre-update values here (the commit is a later launch).
-  const int wave = tid >> 6, lane = tid & 63;
-  for (int i = wave; i < nrows; i += nwaves) {
-    const int r = r0 + i;
-    const int64_t u = roots[r];
-    const int cs = cnt_src[r], cd = cnt_dst[r];
-    const int p = next_mail_pos[u];
-    const int p2 = (p + cs) % K;
-    const bool write_src = cs > 0 && !(cd > 0 && p2 == p);
+  // Mailbox write: the src-role message goes to slot p = next_mail_pos[u],
+  // the dst-role one to (p + #src occurrences) % K, so with one slot the dst
+  // role wins; the pointer advances by both counts. Every read of this
+  // root's mailbox rows happened before the barriers above.
+  if (msg_row) {
+    const int64_t u = s_root[i_msg];
+    const int cs = s_cnt[0][i_msg], cd = s_cnt[1][i_msg];
+    const int p2 = (p_slot + cs) % K;
+    const bool write_src = cs > 0 && !(cd > 0 && p2 == p_slot);
+#pragma unroll
     for (int role = 0; role < 2; ++role) {
       if (role == 0 && !write_src) continue;
       if (role == 1 && cd == 0) continue;
-      const unsigned long long key = role == 0 ? win_src[r] : win_dst[r];
-      const int64_t e = int64_t(key & 0xffffffffull);
-      const int64_t self = role == 0 ? src[e] : dst[e];
-      const int64_t other = role == 0 ? dst[e] : src[e];
-      const int slot = role == 0 ? p : p2;
+      const int slot = role == 0 ? p_slot : p2;
       float *out = mailbox + (u * K + slot) * S;
-      for (int j = lane; j < S; j += sgl::kWave) {
-        float v;
-        if (j < D) v = memory[self * D + j];
-        else if (j < 2 * D) v = memory[other * D + (j - D)];
-        else v = efeat[e * F + (j - 2 * D)];
-        out[j] = v;
+#pragma unroll
+      for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
+        const int c = lane + 64 * jj;
+        if (c < D) out[c] = ms[i_msg * ldh + c];
+        else if (c < S) out[c] = part[role][jj];
       }
-      if (lane == 0) mailbox_ts[u * K + slot] = ts[e];
+      if (lane == 0) mailbox_ts[u * K + slot] = ts_e[role];
     }
-    if (lane == 0) next_mail_pos[u] = int32_t((int64_t(p) + cs + cd) % K);
+    if (lane == 0) next_mail_pos[u] = int32_t((int64_t(p_slot) + cs + cd) % K);
   }
 }
 
@@ -279,7 +339,8 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
 }  // namespace
 
 extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
-                                 const int64_t *neg, const float *ts, uint32_t *node_bits,
+                                 const int64_t *neg, const float *ts, const int64_t *event_offset,
+                                 uint32_t *node_bits,
                                  int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
                                  float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
                                  int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
@@ -297,16 +358,16 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   const unsigned grid = unsigned((cap / 2 + kBlock - 1) / kBlock + 1);
   auto *ws = reinterpret_cast<unsigned long long *>(win_src);
   auto *wd = reinterpret_cast<unsigned long long *>(win_dst);
-  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, node_bits, ws, wd, cnt_src, cnt_dst,
-                                           any_edges, err_flag);
+  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, event_offset, node_bits, ws, wd,
+                                           cnt_src, cnt_dst, any_edges, err_flag);
   SGL_CHECK_LAUNCH();
   k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts,
-                                            ts_max, t_query);
+                                            event_offset, ts_max, t_query);
   SGL_CHECK_LAUNCH();
   if (batch > 0) {
     k_step_index<<<unsigned((batch + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
-        batch, num_nodes, src, dst, neg, ts, node_bits, word_prefix, t_query, roots, root_ts, ridx_src, ridx_dst,
-        ridx_neg, ws, wd, cnt_src, cnt_dst);
+        batch, num_nodes, src, dst, neg, ts, event_offset, node_bits, word_prefix, t_query, roots, root_ts,
+        ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
     SGL_CHECK_LAUNCH();
   }
   return SGL_OK;
@@ -322,7 +383,8 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
                                  int32_t *next_mail_pos, const float *w_ih, const float *w_hh, const float *b_ih,
                                  const float *b_hh, const float *wc_ih, const float *wc_hh, const float *bc_ih,
                                  const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
-                                 const float *ts, const uint64_t *win_src, const uint64_t *win_dst,
+                                 const float *ts, const int64_t *event_offset, const uint64_t *win_src,
+                                 const uint64_t *win_dst,
                                  const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
                                  hipStream_t stream) {
   SGL_REQUIRE(D > 0 && K > 0 && F >= 0, "memory_update: bad dims D=%d K=%d F=%d", D, K, F);
@@ -334,12 +396,13 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
               "memory_update: NULL array");
   const size_t lds = sgl_memory_update_lds_bytes(D, F);
   SGL_REQUIRE(lds <= 160 * 1024, "memory_update: D=%d F=%d needs %zu bytes of LDS (> 160 KiB)", D, F, lds);
-  SGL_CHECK_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&k_gru_mailbox),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
+              64 * kMaxMsgSlots);
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox), lds));
   const unsigned grid = unsigned((capacity + kTileRows - 1) / kTileRows);
-  k_gru_mailbox<<<grid, kBlock, lds, stream>>>(
+  k_gru_mailbox<<<grid, kGruBlock, lds, stream>>>(
       D, K, F, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh,
-      bc_ih, bc_hh, src, dst, efeat, ts, reinterpret_cast<const unsigned long long *>(win_src),
+      bc_ih, bc_hh, src, dst, efeat, ts, event_offset, reinterpret_cast<const unsigned long long *>(win_src),
       reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

@@ -122,7 +122,7 @@ class CTDGMemoryUpdater(nn.Module):
         _capi.check(_capi.lib().sgl_memory_update(
             D, K, Fd, cap, P(n), P(roots), P(mem), P(mail), P(mts), P(nmp), P(w["w_ih"]), P(w["w_hh"]),
             P(w["b_ih"]), P(w["b_hh"]), P(w["wc_ih"]), P(w["wc_hh"]), P(w["bc_ih"]), P(w["bc_hh"]), P(dummy_i64),
-            P(dummy_i64), P(dummy_f), P(dummy_f), P(zeros_k), P(zeros_k), P(zeros_i), P(zeros_i), P(out),
+            P(dummy_i64), P(dummy_f), P(dummy_f), None, P(zeros_k), P(zeros_k), P(zeros_i), P(zeros_i), P(out),
             _capi.stream_of(dev)), "sgl_memory_update")
         return out[:M]
 

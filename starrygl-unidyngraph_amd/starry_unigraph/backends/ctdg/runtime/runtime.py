@@ -61,6 +61,13 @@ class CTDGOnlineRuntime:
         self.dist_ctx = dist_ctx
         self.memory_updater = memory_updater
         self.collect_results = True
+        # Full-size batches of a contiguous split run as one captured HIP graph
+        # per (split, train/eval); the graph reads the events at a device-side
+        # cursor and the negatives from a staging buffer, so one capture
+        # replays for every batch. The first full batch of a kind runs eagerly.
+        self.use_graphs = True
+        self._graphs: dict[tuple[str, bool], torch.cuda.CUDAGraph] = {}
+        self._graph_seen: set[tuple[str, bool]] = set()
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
         core = self._core()
@@ -70,7 +77,8 @@ class CTDGOnlineRuntime:
         self.step = DeviceStep(memory.state, self.dims, int(max_batch or 1))
         self._dev = dataset.device_arrays(self.device)
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
-        self._zero_row = torch.zeros(1, memory.hidden_dim, device=self.device)
+        self._cursor = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self._neg_stage = torch.zeros(self.step.buf.max_batch, dtype=torch.int64, device=self.device)
 
     def _core(self):
         return self.model.module if hasattr(self.model, "module") else self.model
@@ -136,19 +144,53 @@ class CTDGOnlineRuntime:
         n = batch.size
         if n > self.step.buf.max_batch:
             self.step = DeviceStep(self.memory.state, self.dims, n)
-        src, dst, ts, ef = self._device_batch(batch)
-        neg = self._negatives(batch)
-        step = self.step
-        step.prepare(src, dst, neg, ts)
-        step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
-        if self._gru is not None:
-            step.update_memory(self._gru, src, dst, ef, ts)
-            step.commit()
-        core = self._core()
-        conv = core.conv
+            self._neg_stage = torch.zeros(n, dtype=torch.int64, device=self.device)
+            self.reset_graphs()
+        conv = self._core().conv
         if train and (conv.dropout.p > 0 or conv.att_dropout.p > 0):
             raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
                                       "ctdg.dropout and ctdg.att_dropout to 0")
+        neg = self._negatives(batch)
+        b = self.step.buf
+        graphable = (self.use_graphs and n == b.max_batch and batch.start >= 0 and self.step.timer is None)
+        if not graphable:
+            src, dst, ts, ef = self._device_batch(batch)
+            self._step_body(split, train, n, src, dst, neg, ts, ef, None)
+        else:
+            d = self._dev
+            self._neg_stage[:n].copy_(neg)
+            self._cursor.fill_(batch.start)
+            key = ("test" if split == "predict" else split, bool(train))
+            args = (split, train, n, d["src"], d["dst"], self._neg_stage[:n], d["ts"], d["edge_feat"], self._cursor)
+            g = self._graphs.get(key)
+            if g is None and key in self._graph_seen:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._step_body(*args)
+                self._graphs[key] = g
+            if g is not None:
+                g.replay()
+            else:
+                self._graph_seen.add(key)
+                self._step_body(*args)
+        return StepTensors(b.loss[0], b.pos[:n], b.neg[:n], n)
+
+    def reset_graphs(self) -> None:
+        """Drop captured step graphs (after buffers they reference change)."""
+        self._graphs.clear()
+        self._graph_seen.clear()
+
+    def _step_body(self, split: str, train: bool, n: int, src, dst, neg, ts, ef, offset) -> None:
+        """The device work of one step. With ``offset`` (device int64 [1]) the
+        event arrays are the whole stream and the batch starts at the offset."""
+        step = self.step
+        step.prepare(src, dst, neg, ts, n=n, event_offset=offset)
+        step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
+        if self._gru is not None:
+            step.update_memory(self._gru, src, dst, ef, ts, event_offset=offset)
+            step.commit()
+        core = self._core()
+        conv = core.conv
         efeat_all = self._dev["edge_feat"]
         cparams = [p.detach() for p in conv.kernel_params()]
         pparams = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
@@ -163,12 +205,11 @@ class CTDGOnlineRuntime:
         else:
             pgrads = None
         step.conv_forward(cparams, efeat_all)
-        pos, negl, loss = step.predictor(n, train, [p.detach() for p in pparams], pgrads)
+        step.predictor(n, train, [p.detach() for p in pparams], pgrads)
         if train:
             grads = step.conv_backward(cparams, efeat_all, step.buf.gy)
             torch._foreach_add_([p.grad for p in conv.kernel_params()], grads)
             self.optimizer.step()
-        return StepTensors(loss[0], pos, negl, n)
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
         """runtime.py:202-214."""

@@ -37,9 +37,9 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_compact_workspace_bytes": (_sz, [_i64]),
     "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),
-    "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 22),
+    "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 23),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
-    "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 24),
+    "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
     "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 31),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 37),

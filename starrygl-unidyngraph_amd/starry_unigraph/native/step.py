@@ -152,13 +152,17 @@ class DeviceStep:
         return r
 
     # -- batch preparation --------------------------------------------------
-    def prepare(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor) -> None:
+    def prepare(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor,
+                n: int | None = None, event_offset: torch.Tensor | None = None) -> None:
+        """Batch preparation. With ``event_offset`` (device int64 [1]) src/dst/ts
+        are the whole stream and the batch is its ``n`` events from the offset."""
         b, st, P = self.buf, self.state, _capi.ptr
-        n = src.numel()
+        n = src.numel() if n is None else int(n)
         if n > b.max_batch:
             raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
         self._call("batch_prepare", lambda: _capi.check(self.lib.sgl_batch_prepare(
-            st.N, n, P(src), P(dst), P(neg), P(ts), P(st.node_bits), P(st.word_prefix), P(b.num_roots),
+            st.N, n, P(src), P(dst), P(neg), P(ts), P(event_offset), P(st.node_bits), P(st.word_prefix),
+            P(b.num_roots),
             P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
             P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
             self._s()), "sgl_batch_prepare"))
@@ -169,12 +173,13 @@ class DeviceStep:
                                                                    num_live=b.num_roots64))
 
     # -- memory -------------------------------------------------------------
-    def update_memory(self, gru: dict, src, dst, efeat, ts) -> None:
+    def update_memory(self, gru: dict, src, dst, efeat, ts, event_offset: torch.Tensor | None = None) -> None:
         b, st, P = self.buf, self.state, _capi.ptr
         self._call("memory_update", lambda: _capi.check(self.lib.sgl_memory_update(
             st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
             P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
-            P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(b.win_src),
+            P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(event_offset),
+            P(b.win_src),
             P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), "sgl_memory_update"))
 
     def commit(self) -> None:

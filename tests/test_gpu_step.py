@@ -328,3 +328,44 @@ def test_fused_adam_matches_torch_adam(gpu):
         opt_g.step([gate, None])
         for a, b in zip(gpu_p, ref_p):
             _close(a, b, rtol=1e-5, atol=1e-6, msg=f"step {it}")
+
+
+def _step_state(rt):
+    st, opt = rt.memory.state, rt.optimizer.inner
+    return ([st.memory, st.mailbox, st.mailbox_ts, st.memory_ts, st.next_mail_pos] +
+            [opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments])
+
+
+def test_graph_replay_matches_eager(gpu):
+    """The captured-graph step (event cursor, staged negatives) against the
+    eager step, each batch from identical state (train, then eval): mailbox,
+    timestamps and slot pointers bit-exact; loss, logits and memory within
+    1e-5; the Adam-updated parameters within 3 lr (the gradient scatter uses
+    float atomics, and Adam maps a near-zero gradient's sign to +-lr)."""
+    lr = 1e-3
+    _, rt_e, *_ = _runtime_pair(gpu, K=1, seed=5, lr=lr)
+    _, rt_g, *_ = _runtime_pair(gpu, K=1, seed=5, lr=lr)
+    rt_e.use_graphs, rt_g.use_graphs = False, True
+    gen = torch.Generator().manual_seed(9)
+    pool = rt_e.dataset.dst.unique()
+    for split, train in (("train", True), ("val", False)):
+        for i, (be, bg) in enumerate(zip(list(rt_e.iter_batches(split, 200))[:5],
+                                         list(rt_g.iter_batches(split, 200))[:5])):
+            with torch.no_grad():
+                for d, s_ in zip(_step_state(rt_g), _step_state(rt_e)):
+                    d.copy_(s_)
+            neg = co.negative_sample(pool, be.dst, gen).to(gpu)
+            outs = []
+            for rt, b in ((rt_e, be), (rt_g, bg)):
+                rt._neg_queue[split] = (neg, 0)
+                outs.append(rt.train_step(b) if train else rt.eval_step(b, split))
+            (re_, rg) = outs
+            msg = f"{split} batch {i}"
+            assert abs(re_["loss"] - rg["loss"]) <= 1e-5 * abs(re_["loss"]) + 1e-7, msg
+            np.testing.assert_allclose(rg["predictions"], re_["predictions"], rtol=1e-5, atol=1e-7, err_msg=msg)
+            se, sg = rt_e.memory.state, rt_g.memory.state
+            for name in ("mailbox", "mailbox_ts", "memory_ts", "next_mail_pos"):
+                assert torch.equal(getattr(se, name), getattr(sg, name)), (name, msg)
+            _close(sg.memory, se.memory, rtol=1e-5, atol=1e-6, msg=f"memory {msg}")
+            _close(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat, rtol=0, atol=3 * lr, msg=f"params {msg}")
+    assert len(rt_g._graphs) == 2 and not rt_e._graphs
