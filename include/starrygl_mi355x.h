@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 1
+#define SGL_ABI_VERSION 2
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -201,10 +201,12 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
  * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows >= U are
  * zero. If any_edges == 0 the whole output is zero (models.py:88-89).
+ * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding.
  * Backward takes gy and writes gz, gagg [cap][D], G [cap][H][D+F+T],
  * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
  * tile partial sums ln_part [cap/16][2][D] (gamma, beta) and
- * te_part [cap/16][2][T] (time-encoding w, b).
+ * te_part [cap/16][2][T] (time-encoding w, b; the b part includes the
+ * query's cos(b) term through w_q).
  * ------------------------------------------------------------------------- */
 int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      int32_t fanout, int64_t capacity,
@@ -218,8 +220,8 @@ int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      const float *ln_g, const float *ln_b, const float *te_w,
                      const float *te_b, float *sv_Q, float *sv_qt,
                      float *sv_xbar, float *sv_score, float *sv_ml,
-                     float *sv_agg, float *sv_z, float *sv_stats, float *y,
-                     hipStream_t stream);
+                     float *sv_agg, float *sv_z, float *sv_stats,
+                     float *sv_phi0, float *y, hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
@@ -271,6 +273,49 @@ int sgl_adam_step(int64_t n, float *param, const float *grad, float *exp_avg,
                   float lr, float beta1, float beta2, float eps,
                   float weight_decay, hipStream_t stream);
 int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused weight gradients + Adam for one training step.
+ * Replaces the backward weight-gradient products of TemporalTransformerConv's
+ * nn.Linear / LayerNorm / TimeEncode parameters (autograd of models.py:77-137)
+ * and the optimizer.step() of runtime.py:294-296 (torch.optim.Adam of
+ * factory.py:122-128), for parameters kept in one flat fp32 buffer with
+ * moments exp_avg / exp_avg_sq at the same offsets.
+ *
+ * A job (device array) is one of:
+ *   kind 0: a gradient block G[a][b] = sum_{r<R} x1[r*s1 + a] * x2[r*s2 + b]
+ *           for a < rows, b < cols, stored at grad[off + a*ldo + b]; R is
+ *           r_fixed, or *num_roots when r_fixed < 0. s1 >= rows (s2 may be 0:
+ *           a broadcast row). Tiles: ceil(rows/16) * ceil(cols/16), tiles_b =
+ *           ceil(cols/16).
+ *   kind 1: rows*cols contiguous elements from off whose gradient is already
+ *           in grad (Adam only). Tiles: ceil(rows*cols/256).
+ * tile0 is the job's first tile; tile_job[t] the job of tile t (device).
+ * Each gradient element is written once, then Adam-updated if its segment
+ * `seg` is active this step (coef from sgl_adam_prepare).
+ * sgl_adam_prepare: for each segment s < nseg (<= SGL_MAX_ADAM_SEGMENTS):
+ * if gates[s] is NULL or *gates[s] != 0, *steps[s] += 1 and coef[4s..4s+2] =
+ * {lr / (1 - beta1^t), sqrt(1 - beta2^t), 1}; else coef[4s+2] = 0. steps and
+ * gates are host arrays of device pointers. torch.optim.Adam arithmetic.
+ * ------------------------------------------------------------------------- */
+#define SGL_MAX_ADAM_SEGMENTS 8
+
+typedef struct sgl_grad_job {
+  const float *x1;
+  const float *x2;
+  int64_t s1, s2;
+  int64_t off;
+  int32_t ldo, rows, cols, kind, seg, r_fixed, tiles_b, tile0;
+} sgl_grad_job;
+
+int sgl_adam_prepare(int32_t nseg, float *const *steps,
+                     const int32_t *const *gates, float lr, float beta1,
+                     float beta2, float *coef, hipStream_t stream);
+int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
+                  int32_t num_tiles, const int32_t *num_roots, float *param,
+                  float *grad, float *exp_avg, float *exp_avg_sq,
+                  const float *coef, float beta1, float beta2, float eps,
+                  float weight_decay, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -103,6 +103,7 @@ struct ConvSaved {
   float *agg;    // [cap][D]
   float *z;      // [cap][D]     pre-ReLU output projection
   float *stats;  // [cap][2]     LayerNorm mean, rstd
+  float *phi0;   // [T]          cos(b): the query's time encoding (may be NULL)
 };
 
 struct FwdLds {
@@ -179,6 +180,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       L.AH[i * L.lda + D + j] = v;
     } else {
       v = cosf(p.te_b[j - D]);
+      if (i == 0 && blockIdx.x == 0 && sv.phi0 != nullptr) sv.phi0[j - D] = v;
     }
     L.HT[i * L.ldh + j] = v;
   }
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       }
     }
   }
-  // reduce the waves' time-encoding partials
+  // the waves' time-encoding partials (reduced at the end)
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
     const int c = lane + 64 * j;
@@ -583,12 +585,6 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     }
   }
   __syncthreads();
-  for (int t = tid; t < T; t += kBlock) {
-    float a = 0.f, b = 0.f;
-    for (int w = 0; w < kWaves; ++w) { a += L.tep[(w * 2) * T + t]; b += L.tep[(w * 2 + 1) * T + t]; }
-    g.te_part[size_t(blockIdx.x) * 2 * T + t] = a;
-    g.te_part[size_t(blockIdx.x) * 2 * T + T + t] = b;
-  }
   // gQ_h = W_k[h rows] G_h + b_k[h] sigma_h
   {
     sgl::GemmJob jobs[HM];
@@ -603,7 +599,27 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     const int i = idx / D, j = idx - i * D;
     const int h = j / dh;
     const float v = i < nrows ? L.GQ[i * L.ldr + j] + p.b_k[j] * s_sig[i][h] : 0.f;
+    L.GQ[i * L.ldr + j] = v;
     g.gQ[size_t(r0 + i) * D + j] = v;
+  }
+  __syncthreads();
+  // column sums of this tile's gQ (GA row 0 is free by now)
+  for (int j = tid; j < D; j += kBlock) {
+    float sq = 0.f;
+    for (int i = 0; i < kRows; ++i) sq += L.GQ[i * L.ldr + j];
+    L.GA[j] = sq;
+  }
+  __syncthreads();
+  // per-tile time-encoding gradients: the edges' terms, plus for the bias the
+  // query's cos(b) term -sin(b_t) * sum_j W_q[j][D+t] * sum_rows gQ[.][j]
+  for (int t = tid; t < T; t += kBlock) {
+    float a = 0.f, b = 0.f;
+    for (int w = 0; w < kWaves; ++w) { a += L.tep[(w * 2) * T + t]; b += L.tep[(w * 2 + 1) * T + t]; }
+    float qterm = 0.f;
+    for (int j = 0; j < D; ++j) qterm += p.w_q[size_t(j) * (D + T) + D + t] * L.GA[j];
+    b += -sinf(L.TB[t]) * qterm;
+    g.te_part[size_t(blockIdx.x) * 2 * T + t] = a;
+    g.te_part[size_t(blockIdx.x) * 2 * T + T + t] = b;
   }
 }
 
@@ -671,7 +687,7 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                                 const float *w_out, const float *b_out, const float *ln_g, const float *ln_b,
                                 const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
                                 float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
-                                float *y, hipStream_t stream) {
+                                float *sv_phi0, float *y, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
@@ -687,7 +703,7 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
-  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats};
+  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0};
   inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
       d, num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
   SGL_CHECK_LAUNCH();
@@ -721,7 +737,7 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
-               const_cast<float *>(sv_z), const_cast<float *>(sv_stats)};
+               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
   inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
       d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g);

@@ -24,7 +24,7 @@ from typing import Any, Iterable
 import torch
 import torch.nn.functional as F
 
-from starry_unigraph.native.step import ConvDims, DeviceStep
+from starry_unigraph.native.step import ConvDims, DeviceStep, FusedAdam, StepParamUpdate
 
 from .data import CTDGDataBatch, TGTemporalDataset
 from .memory import CTDGMemoryBank
@@ -79,6 +79,7 @@ class CTDGOnlineRuntime:
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
         self._cursor = torch.zeros(1, dtype=torch.int64, device=self.device)
         self._neg_stage = torch.zeros(self.step.buf.max_batch, dtype=torch.int64, device=self.device)
+        self._update: StepParamUpdate | None = None
 
     def _core(self):
         return self.model.module if hasattr(self.model, "module") else self.model
@@ -196,20 +197,33 @@ class CTDGOnlineRuntime:
         pparams = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
                    core.out_fc.bias]
         if train:
-            # gradients are views of the optimizer's flat buffer: zero it, then the
-            # kernels add into it (no torch autograd on this path)
-            self.optimizer.zero_grad(set_to_none=True)
+            # gradients are views of the optimizer's flat buffer (no torch
+            # autograd on this path): the predictor kernel adds into its
+            # segment, the fused update writes the attention's
+            upd = self._param_update()
+            start, count, _ = upd.opt.segments[1]
+            upd.opt.flat_grad[start:start + count].zero_()
             pgrads = [p.grad for p in pparams]
-            if any(g is None for g in pgrads):
-                raise RuntimeError("the fused step needs the runtime's optimizer (gradient buffers missing)")
         else:
             pgrads = None
         step.conv_forward(cparams, efeat_all)
         step.predictor(n, train, [p.detach() for p in pparams], pgrads)
         if train:
-            grads = step.conv_backward(cparams, efeat_all, step.buf.gy)
-            torch._foreach_add_([p.grad for p in conv.kernel_params()], grads)
-            self.optimizer.step()
+            step.conv_backward_kernel(cparams, efeat_all, step.buf.gy)
+            upd.run()
+
+    def _param_update(self) -> StepParamUpdate:
+        """The fused weight-gradient + Adam launches for the current step
+        buffers and the runtime's optimizer (rebuilt if either changed)."""
+        inner = getattr(self.optimizer, "inner", None)
+        if not isinstance(inner, FusedAdam):
+            raise RuntimeError("the fused step needs the runtime's optimizer (GatedAdam over a FusedAdam)")
+        upd = self._update
+        if upd is None or upd.step is not self.step or upd.opt is not inner:
+            upd = StepParamUpdate(self.step, inner, self._core().conv.kernel_params(),
+                                  [self.step.buf.any_edges, None])
+            self._update = upd
+        return upd
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
         """runtime.py:202-214."""

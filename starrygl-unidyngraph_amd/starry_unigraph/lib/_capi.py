@@ -16,7 +16,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -41,11 +41,13 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
-    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 31),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 32),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 37),
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 21),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
+    "sgl_adam_prepare": (ctypes.c_int, [_i32, _vp, _vp] + [ctypes.c_float] * 3 + [_vp, _vp]),
+    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 6 + [ctypes.c_float] * 4 + [_vp]),
 }
 
 _lock = threading.Lock()
@@ -111,6 +113,13 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class GradJob(ctypes.Structure):
+    """struct sgl_grad_job of include/starrygl_mi355x.h."""
+    _fields_ = [("x1", _vp), ("x2", _vp), ("s1", _i64), ("s2", _i64), ("off", _i64),
+                ("ldo", _i32), ("rows", _i32), ("cols", _i32), ("kind", _i32), ("seg", _i32),
+                ("r_fixed", _i32), ("tiles_b", _i32), ("tile0", _i32)]
 
 
 class ErrorFlag:

@@ -15,6 +15,7 @@ backends/ctdg/runtime/runtime.py:225-297):
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -111,6 +112,7 @@ class StepBuffers:
         self.Q, self.agg, self.z, self.y = z(c, D), z(c, D), z(c, D), z(c, D)
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
+        self.phi0 = z(max(dims.T, 1))
         self.gy = z(c, D)
         self.pos = z(max(B, 1))
         self.neg = z(max(B, 1))
@@ -197,7 +199,7 @@ class DeviceStep:
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
             P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
             P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
-            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.y), self._s()), "sgl_conv_forward"))
+            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.phi0), P(b.y), self._s()), "sgl_conv_forward"))
         return b.y
 
     def predictor(self, n: int, train: bool, pred: list[torch.Tensor], grads: list[torch.Tensor] | None):
@@ -213,9 +215,9 @@ class DeviceStep:
             self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
-    def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
-        """Returns the 12 parameter gradients (TimeEncode w, b; w_q, b_q, w_k,
-        b_k, w_v, b_v, w_out, b_out, ln weight, ln bias)."""
+    def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor) -> None:
+        """sgl_conv_backward only: per-root gradient rows and per-tile partials
+        in the step buffers (the weight gradients are StepParamUpdate's)."""
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
@@ -226,6 +228,14 @@ class DeviceStep:
             P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
             P(b.ml), P(b.agg), P(b.z), P(b.stats), P(gy), P(b.gz), P(b.gagg), P(b.G), P(b.sigma), P(b.gQ),
             P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
+
+    def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
+        """The backward kernel plus the weight gradients as torch products (the
+        autograd path). Returns the 12 parameter gradients (TimeEncode w, b;
+        w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln weight, ln bias)."""
+        self.conv_backward_kernel(params, efeat_all, gy)
+        b, d = self.buf, self.dims
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         # weight gradients: per-root products reduced over the root rows (rows
         # past the live roots are zero in gz/gagg/G/sigma/gQ)
         D, H, C, T = d.D, d.H, d.C, d.T
@@ -247,8 +257,100 @@ class DeviceStep:
         g_ln_b = b.ln_part[:, 1].sum(0)
         te = b.te_part[:, :, :T].sum(0)
         g_te_w = te[0].reshape(T, 1)
-        g_te_b = te[1] + (w_q[:, D:].t() @ sq) * (-torch.sin(te_b))
+        g_te_b = te[1]   # includes the query's cos(b) term (folded in by the kernel)
         return [g_te_w, g_te_b, g_w_q, g_b_q, g_w_k, g_b_k, g_w_v, g_b_v, g_w_out, g_b_out, g_ln_g, g_ln_b]
+
+
+class StepParamUpdate:
+    """Weight gradients of the attention and Adam over the whole model in two
+    launches (sgl_adam_prepare, sgl_grad_adam). The job table points at the
+    step buffers and at the optimizer's flat buffers, so it is rebuilt when
+    either is re-created. Segment 0 (the attention) is gated by the step's
+    "block has edges" flag; segment 1 (the edge predictor) takes its
+    gradients from sgl_predictor (Adam-only jobs)."""
+
+    def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
+                 gates: list[torch.Tensor | None]):
+        if len(opt.segments) != 2:
+            raise ValueError("StepParamUpdate expects the attention and predictor segments")
+        self.step, self.opt = step, opt
+        self.lib = _capi.lib()
+        dev = opt.flat.device
+        self.one = torch.ones(1, dtype=torch.float32, device=dev)
+        self.coef = torch.zeros(4 * len(opt.segments), dtype=torch.float32, device=dev)
+        jobs, tiles = self._jobs(conv_params)
+        arr = (_capi.GradJob * len(jobs))(*jobs)
+        raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
+        self.jobs = raw.to(dev)
+        self.tile_job = torch.as_tensor(tiles, dtype=torch.int32, device=dev)
+        self.num_tiles = len(tiles)
+        P = _capi.ptr
+        self._steps = (ctypes.c_void_p * len(opt.segments))(*[P(seg[2]) for seg in opt.segments])
+        self._gates = (ctypes.c_void_p * len(opt.segments))(*[P(g) for g in gates])
+
+    def _jobs(self, conv_params):
+        b, d, opt = self.step.buf, self.step.dims, self.opt
+        D, T, H, C = d.D, d.T, d.H, d.C
+        dh = D // H
+        ntiles = b.cap // TILE
+        base = opt.flat.data_ptr()
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
+
+        def off(p):
+            o = p.data_ptr() - base
+            if o < 0 or o % 4 or p.data_ptr() + 4 * p.numel() > base + 4 * opt.flat.numel():
+                raise RuntimeError("StepParamUpdate: parameter outside the optimizer's flat buffer")
+            return o // 4
+
+        def at(t, k=0):
+            return t.data_ptr() + 4 * k
+
+        jobs, tiles = [], []
+
+        def add(job, ntile):
+            job.tile0 = len(tiles)
+            tiles.extend([len(jobs)] * ntile)
+            jobs.append(job)
+
+        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1):
+            assert s1 >= rows
+            tb = (cols + 15) // 16
+            add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ldo=ldo, rows=rows, cols=cols, kind=0, seg=0,
+                              r_fixed=r_fixed, tiles_b=tb), ((rows + 15) // 16) * tb)
+
+        one = at(self.one)
+        gemm(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, ntiles)
+        gemm(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, ntiles)
+        gemm(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D)
+        gemm(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T)
+        gemm(at(b.gQ), D, one, 0, off(b_q), 1, D, 1)
+        for h in range(H):
+            gemm(at(b.Q, h * dh), D, at(b.G, h * C), H * C, off(w_k) + h * dh * C, C, dh, C)
+            gemm(at(b.Q, h * dh), D, at(b.sigma, h), H, off(b_k) + h * dh, 1, dh, 1)
+            gemm(at(b.gagg, h * dh), D, at(b.xbar, h * C), H * C, off(w_v) + h * dh * C, C, dh, C)
+        gemm(at(b.gagg), D, one, 0, off(b_v), 1, D, 1)
+        gemm(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D)
+        gemm(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D)
+        gemm(at(b.gz), D, one, 0, off(b_out), 1, D, 1)
+        gemm(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, ntiles)
+        gemm(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, ntiles)
+        start, n, _ = opt.segments[1]
+        add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=start, ldo=1, rows=n, cols=1, kind=1, seg=1,
+                          r_fixed=0, tiles_b=1), (n + 255) // 256)
+        covered = sum(p.numel() for p in conv_params)
+        if covered != opt.segments[0][1]:
+            raise RuntimeError("StepParamUpdate: the attention segment holds parameters the jobs do not cover")
+        return jobs, tiles
+
+    def run(self) -> None:
+        """Advance the gated step counts, then gradients + Adam."""
+        opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
+        b1, b2 = opt.betas
+        _capi.check(self.lib.sgl_adam_prepare(len(opt.segments), self._steps, self._gates, opt.lr, b1, b2,
+                                              P(self.coef), s), "sgl_adam_prepare")
+        _capi.check(self.lib.sgl_grad_adam(P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots),
+                                           P(opt.flat), P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq),
+                                           P(self.coef), b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam")
 
 
 class ConvFunction(torch.autograd.Function):

@@ -66,3 +66,22 @@ def test_product_path_fails_loudly_without_gpu():
     assert is_bts_sampler_available() is False
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         build_tcsr(3, [0], [1], None, [1])
+
+
+def test_grad_job_struct_layout_matches_header(tmp_path):
+    """ctypes' GradJob has the size and field offsets of struct sgl_grad_job
+    (host compiler on the header)."""
+    import ctypes
+    from starry_unigraph.lib import _capi
+    fields = [f for f, _ in _capi.GradJob._fields_]
+    src = tmp_path / "layout.cpp"
+    src.write_text(
+        '#include <cstdio>\n#include <cstddef>\n#include "starrygl_mi355x.h"\nint main() {\n'
+        '  printf("%zu", sizeof(sgl_grad_job));\n'
+        + "".join(f'  printf(" %zu", offsetof(sgl_grad_job, {f}));\n' for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(_capi.GradJob)] + [getattr(_capi.GradJob, f).offset for f in fields]
+    assert got == want

@@ -369,3 +369,33 @@ def test_graph_replay_matches_eager(gpu):
             _close(sg.memory, se.memory, rtol=1e-5, atol=1e-6, msg=f"memory {msg}")
             _close(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat, rtol=0, atol=3 * lr, msg=f"params {msg}")
     assert len(rt_g._graphs) == 2 and not rt_e._graphs
+
+
+def test_fused_update_matches_torch_adam(gpu):
+    """sgl_adam_prepare + sgl_grad_adam: the parameters after a runtime train
+    step equal torch.optim.Adam applied (in fp32 on the CPU) to the parameters,
+    moments and step count before it with the gradients the kernel wrote; the
+    attention segment is skipped when the block has no edges."""
+    _, rt, *_ = _runtime_pair(gpu, K=1, seed=11)
+    opt = rt.optimizer.inner
+    gen = torch.Generator().manual_seed(3)
+    pool = rt.dataset.dst.unique()
+    for i, batch in enumerate(list(rt.iter_batches("train", 200))[:4]):
+        before = [t.detach().cpu().clone() for t in (opt.flat, opt.exp_avg, opt.exp_avg_sq)]
+        steps = [float(seg[2].item()) for seg in opt.segments]
+        rt._neg_queue["train"] = (co.negative_sample(pool, batch.dst, gen).to(gpu), 0)
+        rt.train_step(batch)
+        grad = opt.flat_grad.detach().cpu()
+        after = opt.flat.detach().cpu()
+        active = [int(rt.step.buf.any_edges.item()) == 1, True]
+        for (start, n, stepc), st0, act in zip(opt.segments, steps, active):
+            sl = slice(start, start + n)
+            p = torch.nn.Parameter(before[0][sl].clone())
+            ref = torch.optim.Adam([p], lr=opt.lr, betas=opt.betas, eps=opt.eps)
+            if act:
+                p.grad = grad[sl].clone()
+                ref.state[p] = {"step": torch.tensor(st0), "exp_avg": before[1][sl].clone(),
+                                "exp_avg_sq": before[2][sl].clone()}
+                ref.step()
+            torch.testing.assert_close(after[sl], p.detach(), rtol=1e-6, atol=1e-8, msg=f"step {i}")
+            assert float(stepc.item()) == st0 + (1 if act else 0)
