@@ -115,8 +115,10 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
  * roots = sorted unique(src ∪ dst), query time int(batch.ts.max())) and the
  * duplicate handling of CTDGMemoryBank._write_slots (memory.py:237-248).
  *
- * node_bits (ceil(N/32) words) must be all zero on entry; sgl_memory_commit
- * clears the words it set. Outputs, all device-resident (no host sync):
+ * node_bits and word_prefix hold ceil(N/32) words rounded up to a multiple of
+ * 4 (node_bits 16-byte aligned); node_bits must be all zero on entry and is
+ * left zero (batches of up to 2048 events clear it themselves, larger ones
+ * through sgl_memory_commit). Outputs, all device-resident (no host sync):
  *   num_roots / num_roots64: U;  roots[0..U) sorted ascending (int64);
  *   root_ts[0..U) = t_query = trunc(max ts) for every root; ts_max = max ts;
  *   ridx_src/ridx_dst[e] = root index of src[e]/dst[e]; ridx_neg[e] = root

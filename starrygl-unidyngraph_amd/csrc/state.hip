@@ -9,6 +9,8 @@
 // Roots (= sorted unique(src ∪ dst)) come from a node bitmap: mark, scan the
 // word popcounts, then rank(n) = prefix[n/32] + popc(word & below(n)); the
 // rank is the root index and the roots come out sorted without a sort.
+// Batches of up to 2048 events do all of it in one workgroup (one launch);
+// larger ones use three grid-wide launches.
 // Capacity-sized arrays (2B roots) plus a device-side root count keep every
 // launch shape static (HIP-graph capturable, no host sync).
 #include <climits>
@@ -145,6 +147,158 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
   atomicMax(&win_dst[rd], key);
   atomicAdd(&cnt_src[rs], 1);
   atomicAdd(&cnt_dst[rd], 1);
+}
+
+// One-workgroup batch preparation for batches of up to kPrepMaxBatch events.
+// The node bitmap gives the roots in ascending order without a sort: mark the
+// endpoints' bits, scan the popcounts of all bitmap words (16-byte loads, all
+// of a thread's issued at once), then rank(n) = prefix[n / 32] +
+// popc(word & below(n)). Per-(root, role) counts and last writers are LDS
+// atomics (64-bit max of order(ts) << 32 | e: the last event in stable
+// timestamp order); negatives need one bit test. The workgroup clears the
+// bits it set before it ends, leaving the bitmap zero.
+constexpr int kPrepBlock = 1024;
+constexpr int kPrepMaxBatch = 2048;
+constexpr int kPrepPer = kPrepMaxBatch / kPrepBlock;
+
+__global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
+    int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
+    const int64_t *__restrict__ dst, const int64_t *__restrict__ neg, const float *__restrict__ ts,
+    const int64_t *__restrict__ event_offset, uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
+    int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, float *__restrict__ ts_max,
+    int64_t *__restrict__ t_query, int64_t *__restrict__ roots, int64_t *__restrict__ root_ts,
+    int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst, int32_t *__restrict__ ridx_neg,
+    unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
+    int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst, int32_t *__restrict__ any_edges,
+    int32_t *__restrict__ err) {
+  extern __shared__ unsigned long long l_win[];                      // [2][cap]
+  int32_t *l_cnt = reinterpret_cast<int32_t *>(l_win + 2 * cap);     // [2][cap]
+  __shared__ int32_t s_scan[kPrepBlock / sgl::kWave];
+  __shared__ float s_max[kPrepBlock / sgl::kWave];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (event_offset != nullptr) {
+    const int64_t off = *event_offset;
+    src += off;
+    dst += off;
+    ts += off;
+  }
+  for (int r = tid; r < 2 * cap; r += kPrepBlock) {
+    l_win[r] = 0ull;
+    l_cnt[r] = 0;
+  }
+  // endpoints of events e = tid + c * kPrepBlock; mark their bits
+  int64_t es[kPrepPer], ed[kPrepPer];
+  bool ok[kPrepPer];
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kPrepPer; ++c) {
+    const int e = tid + c * kPrepBlock;
+    ok[c] = false;
+    es[c] = ed[c] = 0;
+    if (e < batch) {
+      es[c] = src[e];
+      ed[c] = dst[e];
+      ok[c] = es[c] >= 0 && es[c] < num_nodes && ed[c] >= 0 && ed[c] < num_nodes;
+      m = fmaxf(m, ts[e]);
+      if (ok[c]) {
+        atomicOr(&bits[es[c] >> 5], 1u << (es[c] & 31));
+        atomicOr(&bits[ed[c] >> 5], 1u << (ed[c] & 31));
+      } else {
+        if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
+        ridx_src[e] = -1;
+        ridx_dst[e] = -1;
+      }
+    }
+  }
+#pragma unroll
+  for (int dd = 32; dd > 0; dd >>= 1) m = fmaxf(m, __shfl_xor(m, dd, sgl::kWave));
+  if (lane == 0) s_max[wave] = m;
+  __syncthreads();
+  float mm = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kPrepBlock / sgl::kWave; ++w) mm = fmaxf(mm, s_max[w]);
+  // int(float max) truncates toward zero (runtime.py:142); the float32 round
+  // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
+  const int64_t tq = batch > 0 ? (long long)truncf(mm) : 0;
+
+  // exclusive scan of the word popcounts; thread t owns words [w0, w0 + cw)
+  const int64_t nwords = (num_nodes + 31) / 32;
+  const int64_t nvec = (nwords + 3) / 4;  // 16-byte groups (the bitmap is padded to a multiple of 4 words)
+  const int64_t cv = (nvec + kPrepBlock - 1) / kPrepBlock;
+  const int64_t v0 = int64_t(tid) * cv;
+  const uint4 *bv = reinterpret_cast<const uint4 *>(bits);
+  int32_t cnt_here = 0;
+  for (int64_t g = v0; g < v0 + cv && g < nvec; g += 8) {
+    uint4 q[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) q[u] = (g + u < v0 + cv && g + u < nvec) ? bv[g + u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cnt_here += __popc(q[u].x) + __popc(q[u].y) + __popc(q[u].z) + __popc(q[u].w);
+  }
+  int32_t U;
+  int32_t run = sgl::block_exclusive_scan<int32_t, kPrepBlock>(cnt_here, s_scan, U);
+  for (int64_t g = v0; g < v0 + cv && g < nvec; ++g) {
+    const uint4 q = bv[g];
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (w4[u] != 0u) prefix[4 * g + u] = run;
+      run += __popc(w4[u]);
+    }
+  }
+  __syncthreads();
+
+  // ranks, roots, counts and last writers
+#pragma unroll
+  for (int c = 0; c < kPrepPer; ++c) {
+    const int e = tid + c * kPrepBlock;
+    if (e >= batch || !ok[c]) continue;
+    const unsigned long long wkey =
+        (static_cast<unsigned long long>(ts_order(ts[e])) << 32) | static_cast<unsigned long long>(e);
+#pragma unroll
+    for (int role = 0; role < 2; ++role) {
+      const int64_t n = role ? ed[c] : es[c];
+      const int32_t rank = node_rank(bits, prefix, n);
+      (role ? ridx_dst : ridx_src)[e] = rank;
+      roots[rank] = n;
+      root_ts[rank] = tq;
+      atomicAdd(&l_cnt[role * cap + rank], 1);
+      atomicMax(&l_win[role * cap + rank], wkey);
+    }
+  }
+  if (neg != nullptr) {
+#pragma unroll
+    for (int c = 0; c < kPrepPer; ++c) {
+      const int e = tid + c * kPrepBlock;
+      if (e >= batch) continue;
+      const int64_t n = neg[e];
+      int32_t rn = -1;
+      if (n >= 0 && n < num_nodes && ((bits[n >> 5] >> (n & 31)) & 1u)) rn = node_rank(bits, prefix, n);
+      ridx_neg[e] = rn;
+    }
+  }
+  __syncthreads();
+  for (int r = tid; r < cap; r += kPrepBlock) {
+    cnt_src[r] = l_cnt[r];
+    cnt_dst[r] = l_cnt[cap + r];
+    win_src[r] = l_win[r];
+    win_dst[r] = l_win[cap + r];
+  }
+  // leave the bitmap zero (every read of it is behind the barrier above)
+#pragma unroll
+  for (int c = 0; c < kPrepPer; ++c) {
+    const int e = tid + c * kPrepBlock;
+    if (e >= batch || !ok[c]) continue;
+    bits[es[c] >> 5] = 0u;
+    bits[ed[c] >> 5] = 0u;
+  }
+  if (tid == 0) {
+    *num_roots = U;
+    *num_roots64 = U;
+    *ts_max = mm;
+    *t_query = tq;
+    *any_edges = 0;
+  }
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
@@ -350,10 +504,22 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   SGL_REQUIRE(batch >= 0 && batch < (INT_MAX / 2), "batch_prepare: batch %lld out of range", (long long)batch);
   SGL_REQUIRE(node_bits && word_prefix && num_roots && num_roots64 && ts_max && t_query && any_edges,
               "batch_prepare: NULL state array");
+  SGL_REQUIRE((reinterpret_cast<uintptr_t>(node_bits) & 15u) == 0, "batch_prepare: node_bits not 16-byte aligned");
   SGL_REQUIRE(batch == 0 || (src && dst && ts && roots && root_ts && ridx_src && ridx_dst && win_src && win_dst &&
                              cnt_src && cnt_dst && (neg == nullptr || ridx_neg)),
               "batch_prepare: NULL batch array");
   const int64_t cap = 2 * batch;
+  if (batch <= kPrepMaxBatch) {
+    const size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
+    SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_step_prepare_wg), lds));
+    k_step_prepare_wg<<<1, kPrepBlock, lds, stream>>>(
+        batch, num_nodes, cap, src, dst, neg, ts, event_offset, node_bits, word_prefix, num_roots, num_roots64,
+        ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg,
+        reinterpret_cast<unsigned long long *>(win_src), reinterpret_cast<unsigned long long *>(win_dst), cnt_src,
+        cnt_dst, any_edges, err_flag);
+    SGL_CHECK_LAUNCH();
+    return SGL_OK;
+  }
   const int64_t nwords = (num_nodes + 31) / 32;
   const unsigned grid = unsigned((cap / 2 + kBlock - 1) / kBlock + 1);
   auto *ws = reinterpret_cast<unsigned long long *>(win_src);

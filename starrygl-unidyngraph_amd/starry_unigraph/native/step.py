@@ -47,7 +47,7 @@ class NodeState:
             self.mailbox_ts = torch.zeros(self.N, self.K, dtype=torch.float32, device=dev)
             self.memory_ts = torch.full((self.N,), -1.0, dtype=torch.float32, device=dev)
             self.next_mail_pos = torch.zeros(self.N, dtype=torch.int32, device=dev)
-            nwords = (self.N + 31) // 32
+            nwords = (self.N + 31) // 32 + 3 & ~3   # padded to 16-byte groups
             self.node_bits = torch.zeros(nwords, dtype=torch.int32, device=dev)
             self.word_prefix = torch.zeros(nwords, dtype=torch.int32, device=dev)
 

@@ -38,22 +38,28 @@ def test_gru_kernel_matches_torch(gpu, K, D, F):
     _close(got, want, atol=2e-5)
 
 
-def _small_batch(rng, n_nodes, B):
+def _small_batch(rng, n_nodes, B, sorted_ts=True):
     src = rng.integers(0, n_nodes, B)
     dst = rng.integers(0, n_nodes, B)
-    ts = np.sort(rng.integers(0, 50, B)).astype(np.float32)   # ties on purpose
+    ts = rng.integers(0, 50, B).astype(np.float32)   # ties on purpose
+    if sorted_ts:
+        ts = np.sort(ts)
     neg = rng.integers(0, n_nodes, B)
     return src, dst, ts, neg
 
 
-def test_batch_prepare_matches_numpy(gpu):
+@pytest.mark.parametrize("B,sorted_ts", [(600, True), (600, False), (4096, True), (5000, False)])
+def test_batch_prepare_matches_numpy(gpu, B, sorted_ts):
+    """Roots, root indices, query time, per-role counts and last writers (in
+    stable timestamp order) against numpy: one-workgroup sort path (2B <=
+    8192) with sorted and unsorted timestamps, and the bitmap path."""
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
-    rng = np.random.default_rng(0)
-    N, B = 5000, 600
+    rng = np.random.default_rng(B)
+    N = 5000
     st = NodeState(N, 8, 2, 4, gpu)
     step = DeviceStep(st, ConvDims(8, 4, 8, 2, 5), B)
     for _ in range(3):
-        src, dst, ts, neg = _small_batch(rng, N, B)
+        src, dst, ts, neg = _small_batch(rng, N, B, sorted_ts)
         T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
         step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
         b = step.buf
