@@ -258,8 +258,12 @@ def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str,
         # Q (2D*D), qt (2D*C), per edge 4HC (scores + weighted sum), agg (2CD), z (4D*D)
         return "mfma", float(U) * (2 * D * D + 2 * D * C + 2 * C * D + 4 * D * D) + float(E) * 4 * H * C
     if name == "conv_backward":
-        # gagg (2D*D), gxbar (2D*C), per edge 8HC, gQ (2CD)
-        return "mfma", float(U) * (2 * D * D + 2 * D * C + 2 * C * D) + float(E) * 8 * H * C
+        # dL/dy from the predictor rows (4D*D), gagg (2D*D), gxbar (2D*C), per edge 8HC, gQ (2CD)
+        return "mfma", float(U) * (4 * D * D + 2 * D * D + 2 * D * C + 2 * C * D) + float(E) * 8 * H * C
+    if name == "param_update":
+        # weight-gradient reductions over the roots: w_q (D x (D+T)), w_k, w_v (D x C), w_out (D x 2D),
+        # src_fc / dst_fc (D x D over U + 1 rows); 2 flops per multiply-add
+        return "mfma", float(U) * 2 * (D * (D + T) + 2 * D * C + 2 * D * D) + float(U + 1) * 2 * 2 * D * D
     if name == "memory_commit":
         return "hbm", float(U) * (8 + 4 * D * 2 + 4)
     if name == "recent_sample":
@@ -299,8 +303,10 @@ def run_tgn(args, wl: dict) -> dict:
     for b in batches:
         out = rt.train_step(b)
         losses.append(out["loss"])
+    host = time.perf_counter() - w0
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
+    log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]
     final_loss = float(torch.stack(losses).mean().item())

@@ -115,10 +115,12 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
  * roots = sorted unique(src ∪ dst), query time int(batch.ts.max())) and the
  * duplicate handling of CTDGMemoryBank._write_slots (memory.py:237-248).
  *
- * node_bits and word_prefix hold ceil(N/32) words rounded up to a multiple of
- * 4 (node_bits 16-byte aligned); node_bits must be all zero on entry and is
- * left zero (batches of up to 2048 events clear it themselves, larger ones
- * through sgl_memory_commit). Outputs, all device-resident (no host sync):
+ * node_bits holds W = ceil(N/32) rounded up to a multiple of 4 bitmap words
+ * followed by ceil(W/32) rounded up to a multiple of 4 summary words
+ * (sgl_node_bits_words(N) in all, 16-byte aligned); word_prefix holds W
+ * words. node_bits must be all zero on entry and is left zero (batches of up
+ * to 2048 events clear it themselves, larger ones through sgl_memory_commit).
+ * Outputs, all device-resident (no host sync):
  *   num_roots / num_roots64: U;  roots[0..U) sorted ascending (int64);
  *   root_ts[0..U) = t_query = trunc(max ts) for every root; ts_max = max ts;
  *   ridx_src/ridx_dst[e] = root index of src[e]/dst[e]; ridx_neg[e] = root
@@ -127,15 +129,17 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
  *   timestamp order in which root r is the src / dst; cnt_src/cnt_dst[r] =
  *   how many events root r is src / dst in; any_edges reset to 0.
  * Arrays indexed by root hold 2*batch entries (the capacity).
- * event_offset (device int64, may be NULL): when given, src/dst/ts are the
- * whole event stream and the batch is events [*event_offset, +batch) of it
- * (so a captured HIP graph can replay the step for every batch); neg always
- * holds the batch's own `batch` entries. Event indices e above are relative
- * to the batch start.
+ * cursor (device int64, may be NULL): when given, src/dst/ts/neg span the
+ * whole event stream and the batch is events [*cursor, *cursor + batch);
+ * batch_start (device int64) then receives *cursor and *cursor advances by
+ * `batch` (so one captured HIP graph replays the step for consecutive
+ * batches). Without a cursor the arrays hold the batch's own events. Event
+ * indices e above are relative to the batch start.
  * ------------------------------------------------------------------------- */
+int64_t sgl_node_bits_words(int64_t num_nodes);
 int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
                       const int64_t *dst, const int64_t *neg, const float *ts,
-                      const int64_t *event_offset, uint32_t *node_bits, int32_t *word_prefix,
+                      int64_t *cursor, int64_t *batch_start, uint32_t *node_bits, int32_t *word_prefix,
                       int32_t *num_roots, int64_t *num_roots64, float *ts_max,
                       int64_t *t_query, int64_t *roots, int64_t *root_ts,
                       int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
@@ -158,8 +162,8 @@ int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
  * (int32 here) follow memory.py:237-248: one slot per node and role per
  * batch, src role first, pointer advanced by the occurrence counts.
  * Weights: w_ih [3D][2D+F], w_hh [3D][D], wc_ih [3D][D], wc_hh [3D][D].
- * event_offset as in sgl_batch_prepare (src/dst/efeat/ts then span the
- * whole stream).
+ * batch_start (may be NULL): sgl_batch_prepare's output when it ran with a
+ * cursor; src/dst/efeat/ts then span the whole stream.
  * ------------------------------------------------------------------------- */
 size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F);
 int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
@@ -171,7 +175,7 @@ int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
                       const float *bc_ih, const float *bc_hh,
                       const int64_t *src, const int64_t *dst,
                       const float *efeat, const float *ts,
-                      const int64_t *event_offset,
+                      const int64_t *batch_start,
                       const uint64_t *win_src, const uint64_t *win_dst,
                       const int32_t *cnt_src, const int32_t *cnt_dst,
                       float *new_mem, hipStream_t stream);
@@ -203,8 +207,12 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
  * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows >= U are
  * zero. If any_edges == 0 the whole output is zero (models.py:88-89).
- * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding.
- * Backward takes gy and writes gz, gagg [cap][D], G [cap][H][D+F+T],
+ * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding;
+ * sv_trig [cap][fanout][2][T] each sampled edge's time encoding cos and sin
+ * (may be NULL in a forward without backward); the backward reads it.
+ * Backward takes dL/dy as gy [cap][D], or (gy NULL) as W_s^T g_src + W_d^T
+ * g_dst from sgl_predictor's per-root rows and the predictor's src_fc /
+ * dst_fc weights w_s, w_d [D][D], and writes gz, gagg [cap][D], G [cap][H][D+F+T],
  * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
  * tile partial sums ln_part [cap/16][2][D] (gamma, beta) and
  * te_part [cap/16][2][T] (time-encoding w, b; the b part includes the
@@ -223,7 +231,8 @@ int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      const float *te_b, float *sv_Q, float *sv_qt,
                      float *sv_xbar, float *sv_score, float *sv_ml,
                      float *sv_agg, float *sv_z, float *sv_stats,
-                     float *sv_phi0, float *y, hipStream_t stream);
+                     float *sv_phi0, float *sv_trig, float *y,
+                     hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
@@ -238,7 +247,10 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       const float *sv_xbar, const float *sv_score,
                       const float *sv_ml, const float *sv_agg,
                       const float *sv_z, const float *sv_stats,
-                      const float *gy, float *gz, float *gagg, float *G,
+                      const float *sv_trig,
+                      const float *gy, const float *g_src, const float *g_dst,
+                      const float *w_s, const float *w_d,
+                      float *gz, float *gagg, float *G,
                       float *sigma, float *gQ, float *ln_part, float *te_part,
                       hipStream_t stream);
 
@@ -250,17 +262,22 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
  * roots; ridx_* (from sgl_batch_prepare) pick each event's rows, -1 meaning
  * a zero embedding. Weights in nn.Linear layout: w_s, w_d [D][D], w_o [1][D].
  * Writes pos/neg logits [batch] and loss (mean BCE, pos label 1, neg 0).
- * With train: zeroes gy [capacity][D] then adds dloss/dy into it, and ADDS
- * the parameter gradients into g_* (callers zero them once per step).
+ * With train it also writes (after zeroing them) the out_fc gradients
+ * g_wo [D] and g_bo (= g_wo + D) and the per-root sums of the hidden-layer
+ * gradients: g_src[r] = sum over events with root r as src of dL/dh_s,
+ * g_dst[r] = the same for dst (dL/dh_d) and negatives (dL/dh_n); negatives
+ * that are not roots add into row U = *num_roots. g_src / g_dst hold
+ * capacity + 1 rows. The src_fc / dst_fc gradients follow as reductions over
+ * rows 0..U (sgl_grad_adam jobs) and dL/dy through sgl_conv_backward.
  * ------------------------------------------------------------------------- */
 int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
-                  const float *y, const int32_t *ridx_src,
-                  const int32_t *ridx_dst, const int32_t *ridx_neg,
-                  const float *w_s, const float *b_s, const float *w_d,
-                  const float *b_d, const float *w_o, const float *b_o,
-                  float *pos_logits, float *neg_logits, float *loss,
-                  float *gy, float *g_ws, float *g_bs, float *g_wd,
-                  float *g_bd, float *g_wo, float *g_bo, hipStream_t stream);
+                  const int32_t *num_roots, const float *y,
+                  const int32_t *ridx_src, const int32_t *ridx_dst,
+                  const int32_t *ridx_neg, const float *w_s, const float *b_s,
+                  const float *w_d, const float *b_d, const float *w_o,
+                  const float *b_o, float *pos_logits, float *neg_logits,
+                  float *loss, float *g_src, float *g_dst, float *g_wo,
+                  float *g_bo, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
@@ -287,18 +304,19 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * A job (device array) is one of:
  *   kind 0: a gradient block G[a][b] = sum_{r<R} x1[r*s1 + a] * x2[r*s2 + b]
  *           for a < rows, b < cols, stored at grad[off + a*ldo + b]; R is
- *           r_fixed, or *num_roots when r_fixed < 0. s1 >= rows (s2 may be 0:
+ *           r_fixed, or *num_roots + r_extra when r_fixed < 0. s1 >= rows (s2 may be 0:
  *           a broadcast row). Tiles: ceil(rows/16) * ceil(cols/16), tiles_b =
  *           ceil(cols/16).
  *   kind 1: rows*cols contiguous elements from off whose gradient is already
  *           in grad (Adam only). Tiles: ceil(rows*cols/256).
  * tile0 is the job's first tile; tile_job[t] the job of tile t (device).
- * Each gradient element is written once, then Adam-updated if its segment
- * `seg` is active this step (coef from sgl_adam_prepare).
- * sgl_adam_prepare: for each segment s < nseg (<= SGL_MAX_ADAM_SEGMENTS):
- * if gates[s] is NULL or *gates[s] != 0, *steps[s] += 1 and coef[4s..4s+2] =
- * {lr / (1 - beta1^t), sqrt(1 - beta2^t), 1}; else coef[4s+2] = 0. steps and
- * gates are host arrays of device pointers. torch.optim.Adam arithmetic.
+ * Each gradient element is written once, then Adam-updated (torch.optim.Adam
+ * arithmetic) if its segment `seg` is active: gates[seg] NULL or
+ * *gates[seg] != 0. steps[s] (device float) holds segment s's completed step
+ * count; the launch uses t = steps[s] + 1 for the bias corrections and
+ * advances the active segments' counts when its last workgroup finishes
+ * (done: a device int32 completion counter, zero between launches). steps
+ * and gates are host arrays of nseg <= SGL_MAX_ADAM_SEGMENTS device pointers.
  * ------------------------------------------------------------------------- */
 #define SGL_MAX_ADAM_SEGMENTS 8
 
@@ -307,17 +325,15 @@ typedef struct sgl_grad_job {
   const float *x2;
   int64_t s1, s2;
   int64_t off;
-  int32_t ldo, rows, cols, kind, seg, r_fixed, tiles_b, tile0;
+  int32_t ldo, rows, cols, kind, seg, r_fixed, r_extra, tiles_b, tile0;
 } sgl_grad_job;
 
-int sgl_adam_prepare(int32_t nseg, float *const *steps,
-                     const int32_t *const *gates, float lr, float beta1,
-                     float beta2, float *coef, hipStream_t stream);
 int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   int32_t num_tiles, const int32_t *num_roots, float *param,
-                  float *grad, float *exp_avg, float *exp_avg_sq,
-                  const float *coef, float beta1, float beta2, float eps,
-                  float weight_decay, hipStream_t stream);
+                  float *grad, float *exp_avg, float *exp_avg_sq, int32_t nseg,
+                  float *const *steps, const int32_t *const *gates,
+                  int32_t *done, float lr, float beta1, float beta2,
+                  float eps, float weight_decay, hipStream_t stream);
 
 #ifdef __cplusplus
 }

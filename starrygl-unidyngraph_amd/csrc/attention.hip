@@ -26,7 +26,8 @@
 // runs online (running max / running sum) over the window.
 //
 // No 1/sqrt(d) scaling (models.py:125). The time-encoding argument is
-// fl(fl(dt * w) + b), then cos.
+// fl(fl(dt * w) + b), then cos. The forward saves each edge's cos and sin;
+// the backward reads them instead of recomputing.
 #include <climits>
 
 #include "common.h"
@@ -49,11 +50,7 @@ struct Dims {
   int D, F, T, H, C, dh, k;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return sgl::wave_sum_dpp(v); }
 
 // Argument of the time encoding: the product rounded, then the bias added
 // (a GEMM with a bias epilogue, as nn.Linear(1, T) runs on the GPU). The
@@ -67,26 +64,64 @@ __device__ __forceinline__ float te_arg(float dt, float w, float b) {
   return prod + b;
 }
 
-// This lane's slice of X_e: c = lane + 64*j. te_w / te_b are the time
-// encoding's parameters staged in LDS.
-template <int JM>
+// sin and cos of an fp32 time-encoding argument. Cody-Waite reduction by
+// pi/2 in double precision with a three-part split of pi/2 (26-, 23- and
+// 53-bit pieces, so k*P1 and k*P2 are exact for |k| < 2^27), then fp32
+// polynomials on |r| <= pi/4 with the Cephes sinf/cosf coefficients
+// (S. Moshier, Cephes Math Library); about 1.3 ulp against a float64 libm.
+// Arguments beyond 1.5e8 (k near 2^27) take the library sincosf.
+__device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
+  if (fabsf(x) > 1.5e8f) {
+    sincosf(x, &sn, &cs);
+    return;
+  }
+  const double xd = x;
+  const double k = rint(xd * 0.63661977236758134308);
+  double r = fma(-k, 1.5707963407039642, xd);
+  r = fma(-k, -1.3909067675399456e-08, r);
+  r = fma(-k, 6.123233995736766e-17, r);
+  const float rf = float(r), z = rf * rf;
+  const float sp = fmaf(fmaf(fmaf(-1.9515295891e-4f, z, 8.3321608736e-3f), z, -1.6666654611e-1f), z * rf, rf);
+  const float cp =
+      fmaf(fmaf(fmaf(2.443315711809948e-5f, z, -1.388731625493765e-3f), z, 4.166664568298827e-2f), z * z,
+           fmaf(-0.5f, z, 1.f));
+  const int q = int(k) & 3;  // quadrant (two's complement keeps it right for k < 0)
+  sn = q == 0 ? sp : q == 1 ? cp : q == 2 ? -sp : -cp;
+  cs = q == 0 ? cp : q == 1 ? -sp : q == 2 ? -cp : sp;
+}
+
+// This lane's slice of X_e: c = lane + 64*j, and of the time columns' sines.
+// te_w / te_b are the time encoding's parameters staged in LDS. With
+// LOAD_TRIG the time columns come from `trig` (the edge's saved [cos | sin]
+// rows); otherwise they are computed, and stored to `trig` if it is given.
+template <int JM, bool LOAD_TRIG>
 __device__ __forceinline__ void load_x(const Dims &d, const float *__restrict__ memory,
                                        const float *__restrict__ efeat, const float *__restrict__ te_w,
-                                       const float *__restrict__ te_b, int nb, int ei, float dtv, int lane,
-                                       float (&x)[JM]) {
+                                       const float *__restrict__ te_b, float *__restrict__ trig, int nb, int ei,
+                                       float dtv, int lane, float (&x)[JM], float (&sn)[JM]) {
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
     const int c = lane + 64 * j;
-    float v = 0.f;
+    float v = 0.f, w = 0.f;
     if (c < d.D) {
       v = memory[size_t(nb) * d.D + c];
     } else if (c < d.D + d.F) {
       v = efeat[size_t(ei) * d.F + (c - d.D)];
     } else if (c < d.C) {
       const int t = c - d.D - d.F;
-      v = cosf(te_arg(dtv, te_w[t], te_b[t]));
+      if (LOAD_TRIG) {
+        v = trig[t];
+        w = trig[d.T + t];
+      } else {
+        te_sincos(te_arg(dtv, te_w[t], te_b[t]), w, v);
+        if (trig != nullptr) {
+          trig[t] = v;
+          trig[d.T + t] = w;
+        }
+      }
     }
     x[j] = v;
+    sn[j] = w;
   }
 }
 
@@ -104,6 +139,7 @@ struct ConvSaved {
   float *z;      // [cap][D]     pre-ReLU output projection
   float *stats;  // [cap][2]     LayerNorm mean, rstd
   float *phi0;   // [T]          cos(b): the query's time encoding (may be NULL)
+  float *trig;   // [cap][k][2][T] each edge's time encoding cos and sin (may be NULL)
 };
 
 struct FwdLds {
@@ -239,9 +275,24 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
           const int e = min(c0 + u, mwin - 1);
-          load_x<JM>(d, memory, efeat, L.TW, L.TB, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
-                     __shfl(my_dt, e, 64), lane, x[u]);
+          float sn_unused[JM];
+          float *trig = (sv.trig != nullptr && c0 + u < mwin) ? sv.trig + (base + e0 + e) * size_t(2 * d.T)
+                                                                : nullptr;
+          load_x<JM, false>(d, memory, efeat, L.TW, L.TB, trig, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
+                            __shfl(my_dt, e, 64), lane, x[u], sn_unused);
         }
+        // the chunk's scores first (independent reductions), then the
+        // online-softmax updates in edge order
+        float sc[kEC][HM];
+#pragma unroll
+        for (int u = 0; u < kEC; ++u)
+#pragma unroll
+          for (int h = 0; h < HM; ++h) {
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
+            sc[u][h] = wave_sum(part) + qbh[h];
+          }
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
           if (c0 + u >= mwin) break;
@@ -249,10 +300,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
 #pragma unroll
           for (int h = 0; h < HM; ++h) {
             if (h >= H) continue;
-            float part = 0.f;
-#pragma unroll
-            for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
-            const float s = wave_sum(part) + qbh[h];
+            const float s = sc[u][h];
             const float a = s > 0.f ? s : 0.2f * s;
             const float mn = fmaxf(m[h], a);
             const float sc = __expf(m[h] - mn);
@@ -372,7 +420,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     const float *__restrict__ memory, const float *__restrict__ efeat,
     const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, const float *__restrict__ dt, ConvParams p,
-    ConvSaved sv, const float *__restrict__ gy, ConvGrads g) {
+    ConvSaved sv, const float *__restrict__ gy, const float *__restrict__ g_src,
+    const float *__restrict__ g_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
+    ConvGrads g) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   extern __shared__ float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
@@ -401,6 +451,25 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     L.TW[t] = p.te_w[t];
     L.TB[t] = p.te_b[t];
   }
+  // dL/dy of the tile: given, or W_s^T g_src + W_d^T g_dst from the edge
+  // predictor's per-root rows (GA / GQ are free until later phases)
+  if (gy != nullptr) {
+    for (int idx = tid; idx < kRows * D; idx += kBlock) {
+      const int i = idx / D, j = idx - i * D;
+      L.GY[i * L.ldr + j] = i < nrows ? gy[size_t(r0 + i) * D + j] : 0.f;
+    }
+    __syncthreads();
+  } else {
+    for (int idx = tid; idx < kRows * D; idx += kBlock) {
+      const int i = idx / D, j = idx - i * D;
+      L.GA[i * L.ldr + j] = i < nrows ? g_src[size_t(r0 + i) * D + j] : 0.f;
+      L.GQ[i * L.ldr + j] = i < nrows ? g_dst[size_t(r0 + i) * D + j] : 0.f;
+    }
+    __syncthreads();
+    sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves);
+    sgl::tile_gemm16<sgl::kNN, true>(L.GQ, L.ldr, w_d, D, nullptr, L.GY, L.ldr, D, D, kWaves);
+    __syncthreads();
+  }
   // LayerNorm + ReLU backward; one wave per row
   for (int i = wave; i < kRows; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
@@ -414,11 +483,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       const float mean = sv.stats[size_t(r0 + i) * 2], rstd = sv.stats[size_t(r0 + i) * 2 + 1];
       float a1 = 0.f, a2 = 0.f;
       for (int j = lane; j < D; j += 64) {
-        const float zz = sv.z[ro + j], gv = gy[ro + j];
+        const float zz = sv.z[ro + j], gv = L.GY[i * L.ldr + j];
         const float xh = (fmaxf(zz, 0.f) - mean) * rstd;
         const float gxh = gv * p.ln_g[j];
         L.XH[i * L.ldr + j] = xh;
-        L.GY[i * L.ldr + j] = gv;
         L.GZ[i * L.ldr + j] = zz;
         a1 += gxh;
         a2 += gxh * xh;
@@ -507,13 +575,23 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
           if (h < H) my_sc[h] = sv.score[(base + e0 + lane) * H + h];
       }
       for (int c0 = 0; c0 < mwin; c0 += kEC) {
-        float x[kEC][JM];
+        float x[kEC][JM], sn[kEC][JM];
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
           const int e = min(c0 + u, mwin - 1);
-          load_x<JM>(d, memory, efeat, L.TW, L.TB, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
-                     __shfl(my_dt, e, 64), lane, x[u]);
+          load_x<JM, true>(d, memory, efeat, L.TW, L.TB, sv.trig + (base + e0 + e) * size_t(2 * d.T),
+                           __shfl(my_nb, e, 64), __shfl(my_ei, e, 64), 0.f, lane, x[u], sn[u]);
         }
+        float tg[kEC][HM];  // <g_xbar_h, X_e> for the chunk's edges
+#pragma unroll
+        for (int u = 0; u < kEC; ++u)
+#pragma unroll
+          for (int h = 0; h < HM; ++h) {
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < JM; ++j) part += gx[h][j] * x[u][j];
+            tg[u][h] = wave_sum(part);
+          }
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
           if (c0 + u >= mwin) break;
@@ -525,10 +603,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
             gsv[h] = 0.f;
             al[h] = 0.f;
             if (h >= H) continue;
-            float part = 0.f;
-#pragma unroll
-            for (int j = 0; j < JM; ++j) part += gx[h][j] * x[u][j];
-            const float t = wave_sum(part);
+            const float t = tg[u][h];
             const float a = __shfl(my_sc[h], e, 64);
             const float alpha = __expf(a - mh[h]) / lh[h];
             const float ga = alpha * (t - dot[h]);  // softmax backward
@@ -548,8 +623,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
 #pragma unroll
               for (int h = 0; h < HM; ++h)
                 if (h < H) gphi += gsv[h] * q[h][j] + al[h] * gx[h][j];
-              const int t = c - D - d.F;
-              const float ds = -sinf(te_arg(dtv, L.TW[t], L.TB[t])) * gphi;
+              const float ds = -sn[u][j] * gphi;
               twp[j] += ds * dtv;
               tbp[j] += ds;
             }
@@ -687,7 +761,7 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                                 const float *w_out, const float *b_out, const float *ln_g, const float *ln_b,
                                 const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
                                 float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
-                                float *sv_phi0, float *y, hipStream_t stream) {
+                                float *sv_phi0, float *sv_trig, float *y, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
@@ -703,7 +777,7 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
-  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0};
+  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_trig};
   inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
       d, num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
   SGL_CHECK_LAUNCH();
@@ -718,7 +792,9 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                                  const float *b_out, const float *ln_g, const float *ln_b, const float *te_w,
                                  const float *te_b, const float *sv_Q, const float *sv_qt, const float *sv_xbar,
                                  const float *sv_score, const float *sv_ml, const float *sv_agg, const float *sv_z,
-                                 const float *sv_stats, const float *gy, float *gz, float *gagg, float *G,
+                                 const float *sv_stats, const float *sv_trig, const float *gy, const float *g_src,
+                                 const float *g_dst,
+                                 const float *w_s, const float *w_d, float *gz, float *gagg, float *G,
                                  float *sigma, float *gQ, float *ln_part, float *te_part, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
@@ -726,8 +802,9 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
   SGL_REQUIRE(num_roots && any_edges && memory && cnt && w_q && w_k && b_k && w_v && w_out && ln_g && te_w && te_b &&
-                  sv_qt && sv_xbar && sv_ml && sv_z && sv_stats && gy && gz && gagg && G && sigma && gQ && ln_part &&
-                  te_part && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score)),
+                  sv_qt && sv_xbar && sv_ml && sv_z && sv_stats && (gy || (g_src && g_dst && w_s && w_d)) && gz &&
+                  gagg && G && sigma && gQ && ln_part &&
+                  te_part && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score && sv_trig)),
               "conv_backward: NULL array");
   const size_t lds = bwd_lds_bytes(d);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
@@ -737,10 +814,10 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
-               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr};
+               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr, const_cast<float *>(sv_trig)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
   inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
-      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g);
+      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g_src, g_dst, w_s, w_d, g);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

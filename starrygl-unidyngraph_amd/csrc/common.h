@@ -6,6 +6,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "../../include/starrygl_mi355x.h"
 
@@ -47,6 +48,23 @@ __device__ __forceinline__ T wave_inclusive_scan(T v) {
     if (lane >= d) v += n;
   }
   return v;
+}
+
+// Sum over the 64 lanes of a wavefront, returned to every lane, through lane
+// permutes that stay in the VALU: DPP quad_perm (xor 1, xor 2), DPP row_ror
+// 4 and 8 (a 16-lane row sums to every lane of the row), ds_swizzle xor 16
+// (32-lane halves), then the two halves' sums read from lanes 0 and 32.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  auto mov = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, true));
+  };
+  v += mov(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  v += mov(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  v += mov(v, std::integral_constant<int, 0x124>{});  // row_ror:4
+  v += mov(v, std::integral_constant<int, 0x128>{});  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16 within 32 lanes
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+         __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
 template <typename T>

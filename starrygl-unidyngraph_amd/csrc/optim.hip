@@ -79,55 +79,45 @@ extern "C" int sgl_adam_advance(float *step, const int32_t *active, hipStream_t 
 // gradient is already in place. Either way each thread then owns one
 // gradient element: it stores the gradient and, if its segment is active
 // this step, applies the Adam update to the parameter and moments.
-// The bias corrections come from sgl_adam_prepare (launched before), which
-// also advances the segment's step count: no thread here reads a value
-// another workgroup of this launch writes.
+// Every workgroup derives the bias corrections from the segment's completed
+// step count t-1 (unchanged during the launch); the last workgroup to finish
+// (an atomic completion counter, reset by it) advances the active segments'
+// counts, so no separate launch is needed and no workgroup reads a value
+// another one of this launch writes.
 namespace {
 
 constexpr int kGaBlock = 256;
 constexpr int kGaChunk = 16;  // MFMA row groups per wave per load batch
 
-struct AdamPrepArgs {
+struct AdamSegs {
   float *step[SGL_MAX_ADAM_SEGMENTS];
   const int32_t *gate[SGL_MAX_ADAM_SEGMENTS];
 };
-
-__global__ void k_adam_prepare(int nseg, AdamPrepArgs a, float lr, float b1, float b2, float *coef) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  for (int s = 0; s < nseg; ++s) {
-    const bool active = a.gate[s] == nullptr || *a.gate[s] != 0;
-    float *c = coef + 4 * s;
-    if (!active) {
-      c[2] = 0.f;
-      continue;
-    }
-    const float t = *a.step[s] + 1.f;
-    *a.step[s] = t;
-    const double bc1 = 1.0 - pow(double(b1), double(t));
-    const double bc2 = 1.0 - pow(double(b2), double(t));
-    c[0] = float(double(lr) / bc1);
-    c[1] = float(sqrt(bc2));
-    c[2] = 1.f;
-    c[3] = 0.f;
-  }
-}
 
 __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__restrict__ jobs,
                                                        const int32_t *__restrict__ tile_job,
                                                        const int32_t *__restrict__ num_roots, float *__restrict__ p,
                                                        float *__restrict__ g, float *__restrict__ m,
-                                                       float *__restrict__ v, const float *__restrict__ coef,
-                                                       float b1, float b2, float eps, float wd) {
+                                                       float *__restrict__ v, int nseg, AdamSegs segs,
+                                                       int32_t *__restrict__ done, float lr, float b1, float b2,
+                                                       float eps, float wd) {
   __shared__ float red[4][16][17];
+  __shared__ float s_coef[3];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t = blockIdx.x;
   const sgl_grad_job jb = jobs[tile_job[t]];
   const int local = t - jb.tile0;
-  const float *cf = coef + 4 * jb.seg;
-  const bool active = cf[2] != 0.f;
+  if (tid == 0) {
+    const bool act = segs.gate[jb.seg] == nullptr || *segs.gate[jb.seg] != 0;
+    const double st = double(*segs.step[jb.seg]) + 1.0;
+    s_coef[0] = float(double(lr) / (1.0 - pow(double(b1), st)));
+    s_coef[1] = float(sqrt(1.0 - pow(double(b2), st)));
+    s_coef[2] = act ? 1.f : 0.f;
+  }
 
-  int64_t idx;
-  bool valid;
+  int64_t idx = 0;
+  bool valid = false;
+  float gv = 0.f, pv = 0.f, mv = 0.f, vv = 0.f;
   if (jb.kind == 0) {
     const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
     const int a0 = 16 * ta, b0 = 16 * tb;
@@ -135,13 +125,12 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
     valid = a0 + oa < jb.rows && b0 + ob < jb.cols;
     idx = jb.off + int64_t(a0 + oa) * jb.ldo + (b0 + ob);
     // this thread's Adam operands, loaded while the tile is reduced
-    float pv = 0.f, mv = 0.f, vv = 0.f;
-    if (valid && active) {
+    if (valid) {
       pv = p[idx];
       mv = m[idx];
       vv = v[idx];
     }
-    const int R = jb.r_fixed >= 0 ? jb.r_fixed : *num_roots;
+    const int R = jb.r_fixed >= 0 ? jb.r_fixed : *num_roots + jb.r_extra;
     const int i16 = lane & 15, q = lane >> 4;
     sgl::f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (R > 0) {
@@ -167,62 +156,61 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[wave][4 * (lane >> 4) + e][lane & 15] = acc[e];
     __syncthreads();
-    const float gv = red[0][oa][ob] + red[1][oa][ob] + red[2][oa][ob] + red[3][oa][ob];
-    if (!valid) return;
-    g[idx] = gv;
-    if (!active) return;
+    gv = red[0][oa][ob] + red[1][oa][ob] + red[2][oa][ob] + red[3][oa][ob];
+    if (valid) g[idx] = gv;
+  } else {
+    // kind 1: Adam over contiguous elements whose gradient is in place
+    const int64_t e = int64_t(local) * kGaBlock + tid;
+    valid = e < int64_t(jb.rows) * jb.cols;
+    idx = jb.off + e;
+    if (valid) {
+      gv = g[idx];
+      pv = p[idx];
+      mv = m[idx];
+      vv = v[idx];
+    }
+    __syncthreads();
+  }
+  if (valid && s_coef[2] != 0.f) {
     float gi = gv;
     if (wd != 0.f) gi = gi + wd * pv;
     mv = mv + (1.f - b1) * (gi - mv);
     vv = vv * b2 + (1.f - b2) * gi * gi;
     m[idx] = mv;
     v[idx] = vv;
-    const float denom = sqrtf(vv) / cf[1] + eps;
-    p[idx] = pv - cf[0] * (mv / denom);
-    return;
+    const float denom = sqrtf(vv) / s_coef[1] + eps;
+    p[idx] = pv - s_coef[0] * (mv / denom);
   }
-  // kind 1: Adam over contiguous elements whose gradient is in place
-  const int64_t e = int64_t(local) * kGaBlock + tid;
-  valid = e < int64_t(jb.rows) * jb.cols;
-  if (!valid || !active) return;
-  idx = jb.off + e;
-  const float pv = p[idx];
-  float gi = g[idx];
-  if (wd != 0.f) gi = gi + wd * pv;
-  const float mv = m[idx] + (1.f - b1) * (gi - m[idx]);
-  const float vv = v[idx] * b2 + (1.f - b2) * gi * gi;
-  m[idx] = mv;
-  v[idx] = vv;
-  const float denom = sqrtf(vv) / cf[1] + eps;
-  p[idx] = pv - cf[0] * (mv / denom);
+  // the last workgroup advances the active segments' step counts
+  if (tid == 0) {
+    __threadfence();
+    if (atomicAdd(done, 1) == int(gridDim.x) - 1) {
+      for (int s = 0; s < nseg; ++s)
+        if (segs.gate[s] == nullptr || *segs.gate[s] != 0) *segs.step[s] += 1.f;
+      *done = 0;
+    }
+  }
 }
 
 }  // namespace
 
-extern "C" int sgl_adam_prepare(int32_t nseg, float *const *steps, const int32_t *const *gates, float lr,
-                                float beta1, float beta2, float *coef, hipStream_t stream) {
-  SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "adam_prepare: nseg %d out of range", nseg);
-  SGL_REQUIRE(steps && coef, "adam_prepare: NULL array");
-  AdamPrepArgs a{};
-  for (int s = 0; s < nseg; ++s) {
-    SGL_REQUIRE(steps[s] != nullptr, "adam_prepare: NULL step counter %d", s);
-    a.step[s] = steps[s];
-    a.gate[s] = gates != nullptr ? gates[s] : nullptr;
-  }
-  k_adam_prepare<<<1, 64, 0, stream>>>(nseg, a, lr, beta1, beta2, coef);
-  SGL_CHECK_LAUNCH();
-  return SGL_OK;
-}
-
 extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, int32_t num_tiles,
                              const int32_t *num_roots, float *param, float *grad, float *exp_avg, float *exp_avg_sq,
-                             const float *coef, float beta1, float beta2, float eps, float weight_decay,
-                             hipStream_t stream) {
+                             int32_t nseg, float *const *steps, const int32_t *const *gates, int32_t *done, float lr,
+                             float beta1, float beta2, float eps, float weight_decay, hipStream_t stream) {
   SGL_REQUIRE(num_tiles >= 0, "grad_adam: num_tiles < 0");
+  SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "grad_adam: nseg %d out of range", nseg);
   if (num_tiles == 0) return SGL_OK;
-  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && coef, "grad_adam: NULL array");
+  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && steps && done, "grad_adam: NULL array");
+  AdamSegs segs{};
+  for (int s = 0; s < nseg; ++s) {
+    SGL_REQUIRE(steps[s] != nullptr, "grad_adam: NULL step counter %d", s);
+    segs.step[s] = steps[s];
+    segs.gate[s] = gates != nullptr ? gates[s] : nullptr;
+  }
   k_grad_adam<<<unsigned(num_tiles), kGaBlock, 0, stream>>>(jobs, tile_job, num_roots, param, grad, exp_avg,
-                                                            exp_avg_sq, coef, beta1, beta2, eps, weight_decay);
+                                                            exp_avg_sq, nseg, segs, done, lr, beta1, beta2, eps,
+                                                            weight_decay);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

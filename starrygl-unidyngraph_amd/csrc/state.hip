@@ -39,7 +39,8 @@ __device__ __forceinline__ int32_t node_rank(const uint32_t *__restrict__ bits,
 
 __global__ __launch_bounds__(kBlock) void k_step_mark(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
-    const int64_t *__restrict__ dst, const int64_t *__restrict__ event_offset, uint32_t *__restrict__ bits,
+    const int64_t *__restrict__ dst, const int64_t *__restrict__ cursor, int64_t *__restrict__ batch_start,
+    uint32_t *__restrict__ bits,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst,
     int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
@@ -51,8 +52,9 @@ __global__ __launch_bounds__(kBlock) void k_step_mark(
     cnt_src[r] = 0;
     cnt_dst[r] = 0;
   }
+  const int64_t off = cursor != nullptr ? *cursor : 0;
+  if (cursor != nullptr && e == 0) *batch_start = off;
   if (e >= batch) return;
-  const int64_t off = event_offset != nullptr ? *event_offset : 0;
   const int64_t s = src[off + e], d = dst[off + e];
   if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
     if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
@@ -67,9 +69,10 @@ __global__ __launch_bounds__(kBlock) void k_step_mark(
 __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     int64_t nwords, const uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
-    const float *__restrict__ ts, const int64_t *__restrict__ event_offset, float *__restrict__ ts_max,
+    const float *__restrict__ ts, int64_t *__restrict__ cursor, const int64_t *__restrict__ batch_start,
+    float *__restrict__ ts_max,
     int64_t *__restrict__ t_query) {
-  if (event_offset != nullptr) ts += *event_offset;
+  if (cursor != nullptr) ts += *batch_start;
   __shared__ int32_t s_w[kScanBlock / sgl::kWave];
   __shared__ float s_m[kScanBlock / sgl::kWave];
   const int64_t per = (nwords + kScanBlock - 1) / kScanBlock;
@@ -98,13 +101,14 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     // int(float max) truncates toward zero (runtime.py:142); the float32 round
     // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
     *t_query = batch > 0 ? (long long)truncf(mm) : 0;
+    if (cursor != nullptr) *cursor = *batch_start + batch;
   }
 }
 
 __global__ __launch_bounds__(kBlock) void k_step_index(
     int64_t batch, int64_t num_nodes, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
-    const float *__restrict__ ts, const int64_t *__restrict__ event_offset, const uint32_t *__restrict__ bits,
+    const float *__restrict__ ts, const int64_t *__restrict__ batch_start, const uint32_t *__restrict__ bits,
     const int32_t *__restrict__ prefix, const int64_t *__restrict__ t_query,
     int64_t *__restrict__ roots, int64_t *__restrict__ root_ts,
     int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst,
@@ -113,11 +117,12 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
     int32_t *__restrict__ cnt_dst) {
   const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
   if (e >= batch) return;
-  if (event_offset != nullptr) {
-    const int64_t off = *event_offset;
+  if (batch_start != nullptr) {
+    const int64_t off = *batch_start;
     src += off;
     dst += off;
     ts += off;
+    if (neg != nullptr) neg += off;
   }
   const int64_t s = src[e], d = dst[e];
   if (neg != nullptr) {
@@ -150,21 +155,28 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
 }
 
 // One-workgroup batch preparation for batches of up to kPrepMaxBatch events.
-// The node bitmap gives the roots in ascending order without a sort: mark the
-// endpoints' bits, scan the popcounts of all bitmap words (16-byte loads, all
-// of a thread's issued at once), then rank(n) = prefix[n / 32] +
+// The node bitmap gives the roots in ascending order without a sort. Marking
+// also sets a summary bitmap (bit w: word w of the node bitmap is nonzero),
+// so the popcount prefix only visits the nonzero words: scan the summary,
+// popcount the flagged words, block-scan, and rank(n) = prefix[n / 32] +
 // popc(word & below(n)). Per-(root, role) counts and last writers are LDS
 // atomics (64-bit max of order(ts) << 32 | e: the last event in stable
 // timestamp order); negatives need one bit test. The workgroup clears the
-// bits it set before it ends, leaving the bitmap zero.
+// bits it set, leaving both bitmaps zero.
 constexpr int kPrepBlock = 1024;
 constexpr int kPrepMaxBatch = 2048;
 constexpr int kPrepPer = kPrepMaxBatch / kPrepBlock;
 
+__host__ __device__ inline int64_t bitmap_words(int64_t num_nodes) { return ((num_nodes + 31) / 32 + 3) & ~int64_t(3); }
+__host__ __device__ inline int64_t summary_words(int64_t num_nodes) {
+  return ((bitmap_words(num_nodes) + 31) / 32 + 3) & ~int64_t(3);
+}
+
 __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg, const float *__restrict__ ts,
-    const int64_t *__restrict__ event_offset, uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
+    int64_t *__restrict__ cursor, int64_t *__restrict__ batch_start, uint32_t *__restrict__ bits,
+    int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, float *__restrict__ ts_max,
     int64_t *__restrict__ t_query, int64_t *__restrict__ roots, int64_t *__restrict__ root_ts,
     int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst, int32_t *__restrict__ ridx_neg,
@@ -176,12 +188,12 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   __shared__ int32_t s_scan[kPrepBlock / sgl::kWave];
   __shared__ float s_max[kPrepBlock / sgl::kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (event_offset != nullptr) {
-    const int64_t off = *event_offset;
-    src += off;
-    dst += off;
-    ts += off;
-  }
+  uint32_t *summary = bits + bitmap_words(num_nodes);
+  const int64_t off = cursor != nullptr ? *cursor : 0;
+  src += off;
+  dst += off;
+  ts += off;
+  if (neg != nullptr) neg += off;
   for (int r = tid; r < 2 * cap; r += kPrepBlock) {
     l_win[r] = 0ull;
     l_cnt[r] = 0;
@@ -203,6 +215,8 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
       if (ok[c]) {
         atomicOr(&bits[es[c] >> 5], 1u << (es[c] & 31));
         atomicOr(&bits[ed[c] >> 5], 1u << (ed[c] & 31));
+        atomicOr(&summary[es[c] >> 10], 1u << ((es[c] >> 5) & 31));
+        atomicOr(&summary[ed[c] >> 10], 1u << ((ed[c] >> 5) & 31));
       } else {
         if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
         ridx_src[e] = -1;
@@ -221,29 +235,31 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
   const int64_t tq = batch > 0 ? (long long)truncf(mm) : 0;
 
-  // exclusive scan of the word popcounts; thread t owns words [w0, w0 + cw)
-  const int64_t nwords = (num_nodes + 31) / 32;
-  const int64_t nvec = (nwords + 3) / 4;  // 16-byte groups (the bitmap is padded to a multiple of 4 words)
-  const int64_t cv = (nvec + kPrepBlock - 1) / kPrepBlock;
-  const int64_t v0 = int64_t(tid) * cv;
-  const uint4 *bv = reinterpret_cast<const uint4 *>(bits);
+  // popcount prefix over the nonzero words, in word order: thread t owns
+  // summary words [s0, s0 + cs)
+  const int64_t nsum = (bitmap_words(num_nodes) + 31) / 32;
+  const int64_t cs = (nsum + kPrepBlock - 1) / kPrepBlock;
+  const int64_t s0 = int64_t(tid) * cs;
+  const int64_t s1 = s0 + cs < nsum ? s0 + cs : nsum;
   int32_t cnt_here = 0;
-  for (int64_t g = v0; g < v0 + cv && g < nvec; g += 8) {
-    uint4 q[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) q[u] = (g + u < v0 + cv && g + u < nvec) ? bv[g + u] : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) cnt_here += __popc(q[u].x) + __popc(q[u].y) + __popc(q[u].z) + __popc(q[u].w);
+  for (int64_t sw = s0; sw < s1; ++sw) {
+    uint32_t f = summary[sw];
+    while (f != 0u) {
+      const int b = __ffs(f) - 1;
+      f &= f - 1u;
+      cnt_here += __popc(bits[(sw << 5) + b]);
+    }
   }
   int32_t U;
   int32_t run = sgl::block_exclusive_scan<int32_t, kPrepBlock>(cnt_here, s_scan, U);
-  for (int64_t g = v0; g < v0 + cv && g < nvec; ++g) {
-    const uint4 q = bv[g];
-    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (w4[u] != 0u) prefix[4 * g + u] = run;
-      run += __popc(w4[u]);
+  for (int64_t sw = s0; sw < s1; ++sw) {
+    uint32_t f = summary[sw];
+    while (f != 0u) {
+      const int b = __ffs(f) - 1;
+      f &= f - 1u;
+      const int64_t w = (sw << 5) + b;
+      prefix[w] = run;
+      run += __popc(bits[w]);
     }
   }
   __syncthreads();
@@ -284,13 +300,15 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     win_src[r] = l_win[r];
     win_dst[r] = l_win[cap + r];
   }
-  // leave the bitmap zero (every read of it is behind the barrier above)
+  // leave both bitmaps zero (every read of them is behind the barrier above)
 #pragma unroll
   for (int c = 0; c < kPrepPer; ++c) {
     const int e = tid + c * kPrepBlock;
     if (e >= batch || !ok[c]) continue;
     bits[es[c] >> 5] = 0u;
     bits[ed[c] >> 5] = 0u;
+    summary[es[c] >> 10] = 0u;
+    summary[ed[c] >> 10] = 0u;
   }
   if (tid == 0) {
     *num_roots = U;
@@ -298,6 +316,10 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     *ts_max = mm;
     *t_query = tq;
     *any_edges = 0;
+    if (cursor != nullptr) {  // every read of *cursor is behind the barriers above
+      *batch_start = off;
+      *cursor = off + batch;
+    }
   }
 }
 
@@ -335,7 +357,7 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     const float *__restrict__ wc_hh, const float *__restrict__ bc_ih,
     const float *__restrict__ bc_hh, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const float *__restrict__ efeat,
-    const float *__restrict__ ts, const int64_t *__restrict__ event_offset,
+    const float *__restrict__ ts, const int64_t *__restrict__ batch_start,
     const unsigned long long *__restrict__ win_src,
     const unsigned long long *__restrict__ win_dst, const int32_t *__restrict__ cnt_src,
     const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
@@ -356,8 +378,8 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
   const int nrows = min(kTileRows, U - r0);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
-  if (event_offset != nullptr) {  // event arrays are the whole stream
-    const int64_t off = *event_offset;
+  if (batch_start != nullptr) {  // event arrays are the whole stream
+    const int64_t off = *batch_start;
     src += off;
     dst += off;
     ts += off;
@@ -492,8 +514,12 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
 
 }  // namespace
 
+extern "C" int64_t sgl_node_bits_words(int64_t num_nodes) {
+  return num_nodes > 0 ? bitmap_words(num_nodes) + summary_words(num_nodes) : 0;
+}
+
 extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
-                                 const int64_t *neg, const float *ts, const int64_t *event_offset,
+                                 const int64_t *neg, const float *ts, int64_t *cursor, int64_t *batch_start,
                                  uint32_t *node_bits,
                                  int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
                                  float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
@@ -504,6 +530,7 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   SGL_REQUIRE(batch >= 0 && batch < (INT_MAX / 2), "batch_prepare: batch %lld out of range", (long long)batch);
   SGL_REQUIRE(node_bits && word_prefix && num_roots && num_roots64 && ts_max && t_query && any_edges,
               "batch_prepare: NULL state array");
+  SGL_REQUIRE(cursor == nullptr || batch_start != nullptr, "batch_prepare: cursor without batch_start");
   SGL_REQUIRE((reinterpret_cast<uintptr_t>(node_bits) & 15u) == 0, "batch_prepare: node_bits not 16-byte aligned");
   SGL_REQUIRE(batch == 0 || (src && dst && ts && roots && root_ts && ridx_src && ridx_dst && win_src && win_dst &&
                              cnt_src && cnt_dst && (neg == nullptr || ridx_neg)),
@@ -513,7 +540,7 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
     const size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
     SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_step_prepare_wg), lds));
     k_step_prepare_wg<<<1, kPrepBlock, lds, stream>>>(
-        batch, num_nodes, cap, src, dst, neg, ts, event_offset, node_bits, word_prefix, num_roots, num_roots64,
+        batch, num_nodes, cap, src, dst, neg, ts, cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64,
         ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg,
         reinterpret_cast<unsigned long long *>(win_src), reinterpret_cast<unsigned long long *>(win_dst), cnt_src,
         cnt_dst, any_edges, err_flag);
@@ -524,15 +551,16 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   const unsigned grid = unsigned((cap / 2 + kBlock - 1) / kBlock + 1);
   auto *ws = reinterpret_cast<unsigned long long *>(win_src);
   auto *wd = reinterpret_cast<unsigned long long *>(win_dst);
-  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, event_offset, node_bits, ws, wd,
+  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, cursor, batch_start, node_bits, ws, wd,
                                            cnt_src, cnt_dst, any_edges, err_flag);
   SGL_CHECK_LAUNCH();
   k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts,
-                                            event_offset, ts_max, t_query);
+                                            cursor, batch_start, ts_max, t_query);
   SGL_CHECK_LAUNCH();
   if (batch > 0) {
     k_step_index<<<unsigned((batch + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
-        batch, num_nodes, src, dst, neg, ts, event_offset, node_bits, word_prefix, t_query, roots, root_ts,
+        batch, num_nodes, src, dst, neg, ts, cursor != nullptr ? batch_start : nullptr, node_bits, word_prefix,
+        t_query, roots, root_ts,
         ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
     SGL_CHECK_LAUNCH();
   }
@@ -549,7 +577,7 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
                                  int32_t *next_mail_pos, const float *w_ih, const float *w_hh, const float *b_ih,
                                  const float *b_hh, const float *wc_ih, const float *wc_hh, const float *bc_ih,
                                  const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
-                                 const float *ts, const int64_t *event_offset, const uint64_t *win_src,
+                                 const float *ts, const int64_t *batch_start, const uint64_t *win_src,
                                  const uint64_t *win_dst,
                                  const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
                                  hipStream_t stream) {
@@ -568,7 +596,7 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
   const unsigned grid = unsigned((capacity + kTileRows - 1) / kTileRows);
   k_gru_mailbox<<<grid, kGruBlock, lds, stream>>>(
       D, K, F, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh,
-      bc_ih, bc_hh, src, dst, efeat, ts, event_offset, reinterpret_cast<const unsigned long long *>(win_src),
+      bc_ih, bc_hh, src, dst, efeat, ts, batch_start, reinterpret_cast<const unsigned long long *>(win_src),
       reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

@@ -36,12 +36,18 @@ class CTDGDataBatch:
 
     @property
     def start(self) -> int:
-        """First event id when the batch is a contiguous range, else -1."""
-        n = self.event_ids.numel()
-        if n == 0:
-            return 0
-        a, b = int(self.event_ids[0]), int(self.event_ids[-1])
-        return a if b - a + 1 == n else -1
+        """First event id when the batch is a contiguous range, else -1
+        (computed once: batches are immutable)."""
+        st = self.__dict__.get("_start")
+        if st is None:
+            n = self.event_ids.numel()
+            if n == 0:
+                st = 0
+            else:
+                a, b = int(self.event_ids[0]), int(self.event_ids[-1])
+                st = a if b - a + 1 == n else -1
+            self.__dict__["_start"] = st
+        return st
 
 
 class TGTemporalDataset:

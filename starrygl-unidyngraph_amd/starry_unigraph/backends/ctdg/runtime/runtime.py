@@ -77,8 +77,12 @@ class CTDGOnlineRuntime:
         self.step = DeviceStep(memory.state, self.dims, int(max_batch or 1))
         self._dev = dataset.device_arrays(self.device)
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
+        # graph replays read events and negatives at a device cursor that the
+        # batch preparation advances; _cursor_host mirrors its value (None:
+        # unknown) so it is only rewritten when batches are not consecutive
         self._cursor = torch.zeros(1, dtype=torch.int64, device=self.device)
-        self._neg_stage = torch.zeros(self.step.buf.max_batch, dtype=torch.int64, device=self.device)
+        self._cursor_host: int | None = None
+        self._neg_all = torch.zeros(max(int(dataset.src.numel()), 1), dtype=torch.int64, device=self.device)
         self._update: StepParamUpdate | None = None
 
     def _core(self):
@@ -118,7 +122,13 @@ class CTDGOnlineRuntime:
         if col.any():
             idx[col] = (idx[col] + 1) % pool.numel()
             neg = pool[idx]
-        self._neg_queue[split] = (neg.to(self.device), 0)
+        lo = int(ids[0]) if ids.numel() else 0
+        if ids.numel() and int(ids[-1]) - lo + 1 == ids.numel():   # contiguous split: in place
+            view = self._neg_all[lo:lo + ids.numel()]
+            view.copy_(neg)
+            self._neg_queue[split] = (view, 0)
+        else:
+            self._neg_queue[split] = (neg.to(self.device), 0)
 
     def _negatives(self, batch: CTDGDataBatch) -> torch.Tensor:
         q = self._neg_queue.get(batch.split)
@@ -145,7 +155,6 @@ class CTDGOnlineRuntime:
         n = batch.size
         if n > self.step.buf.max_batch:
             self.step = DeviceStep(self.memory.state, self.dims, n)
-            self._neg_stage = torch.zeros(n, dtype=torch.int64, device=self.device)
             self.reset_graphs()
         conv = self._core().conv
         if train and (conv.dropout.p > 0 or conv.att_dropout.p > 0):
@@ -159,10 +168,14 @@ class CTDGOnlineRuntime:
             self._step_body(split, train, n, src, dst, neg, ts, ef, None)
         else:
             d = self._dev
-            self._neg_stage[:n].copy_(neg)
-            self._cursor.fill_(batch.start)
+            at = self._neg_all[batch.start:batch.start + n]
+            if neg.data_ptr() != at.data_ptr():
+                at.copy_(neg)
+            if self._cursor_host != batch.start:
+                self._cursor.fill_(batch.start)
+            self._cursor_host = batch.start + n
             key = ("test" if split == "predict" else split, bool(train))
-            args = (split, train, n, d["src"], d["dst"], self._neg_stage[:n], d["ts"], d["edge_feat"], self._cursor)
+            args = (split, train, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"], self._cursor)
             g = self._graphs.get(key)
             if g is None and key in self._graph_seen:
                 g = torch.cuda.CUDAGraph()
@@ -181,14 +194,15 @@ class CTDGOnlineRuntime:
         self._graphs.clear()
         self._graph_seen.clear()
 
-    def _step_body(self, split: str, train: bool, n: int, src, dst, neg, ts, ef, offset) -> None:
-        """The device work of one step. With ``offset`` (device int64 [1]) the
-        event arrays are the whole stream and the batch starts at the offset."""
+    def _step_body(self, split: str, train: bool, n: int, src, dst, neg, ts, ef, cursor) -> None:
+        """The device work of one step. With ``cursor`` (device int64 [1]) the
+        event and negative arrays are the whole stream and the batch starts at
+        the cursor (which the step advances)."""
         step = self.step
-        step.prepare(src, dst, neg, ts, n=n, event_offset=offset)
+        step.prepare(src, dst, neg, ts, n=n, cursor=cursor)
         step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
         if self._gru is not None:
-            step.update_memory(self._gru, src, dst, ef, ts, event_offset=offset)
+            step.update_memory(self._gru, src, dst, ef, ts, from_cursor=cursor is not None)
             step.commit()
         core = self._core()
         conv = core.conv
@@ -198,18 +212,17 @@ class CTDGOnlineRuntime:
                    core.out_fc.bias]
         if train:
             # gradients are views of the optimizer's flat buffer (no torch
-            # autograd on this path): the predictor kernel adds into its
-            # segment, the fused update writes the attention's
+            # autograd on this path): sgl_predictor writes out_fc's, the fused
+            # update every other parameter's
             upd = self._param_update()
-            start, count, _ = upd.opt.segments[1]
-            upd.opt.flat_grad[start:start + count].zero_()
-            pgrads = [p.grad for p in pparams]
+            out_grads = [core.out_fc.weight.grad, core.out_fc.bias.grad]
         else:
-            pgrads = None
+            out_grads = None
+        pdet = [p.detach() for p in pparams]
         step.conv_forward(cparams, efeat_all)
-        step.predictor(n, train, [p.detach() for p in pparams], pgrads)
+        step.predictor(n, train, pdet, out_grads)
         if train:
-            step.conv_backward_kernel(cparams, efeat_all, step.buf.gy)
+            step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]))
             upd.run()
 
     def _param_update(self) -> StepParamUpdate:
@@ -220,8 +233,10 @@ class CTDGOnlineRuntime:
             raise RuntimeError("the fused step needs the runtime's optimizer (GatedAdam over a FusedAdam)")
         upd = self._update
         if upd is None or upd.step is not self.step or upd.opt is not inner:
-            upd = StepParamUpdate(self.step, inner, self._core().conv.kernel_params(),
-                                  [self.step.buf.any_edges, None])
+            core = self._core()
+            pred = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
+                    core.out_fc.bias]
+            upd = StepParamUpdate(self.step, inner, core.conv.kernel_params(), pred, [self.step.buf.any_edges, None])
             self._update = upd
         return upd
 
@@ -257,7 +272,8 @@ class CTDGOnlineRuntime:
                          "empty_batch": True}}
 
     def train_step(self, batch: CTDGDataBatch) -> dict[str, Any]:
-        self.model.train()
+        if not self.model.training:   # Module.train() walks every submodule
+            self.model.train()
         t0 = time.perf_counter()
         if batch.is_empty:
             return self._empty_result(batch, batch.split)
@@ -275,7 +291,8 @@ class CTDGOnlineRuntime:
 
     def eval_step(self, batch: CTDGDataBatch, split: str) -> dict[str, Any]:
         """runtime.py:330-386: no grad, memory and mailbox still updated."""
-        self.model.eval()
+        if self.model.training:
+            self.model.eval()
         if batch.is_empty:
             return self._empty_result(batch, split)
         with torch.no_grad():

@@ -37,17 +37,17 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_compact_workspace_bytes": (_sz, [_i64]),
     "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),
-    "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 23),
+    "sgl_node_bits_words": (_i64, [_i64]),
+    "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 24),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
-    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 32),
-    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 37),
-    "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 21),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 33),
+    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 42),
+    "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 19),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
-    "sgl_adam_prepare": (ctypes.c_int, [_i32, _vp, _vp] + [ctypes.c_float] * 3 + [_vp, _vp]),
-    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 6 + [ctypes.c_float] * 4 + [_vp]),
+    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 3 + [ctypes.c_float] * 5 + [_vp]),
 }
 
 _lock = threading.Lock()
@@ -119,7 +119,7 @@ class GradJob(ctypes.Structure):
     """struct sgl_grad_job of include/starrygl_mi355x.h."""
     _fields_ = [("x1", _vp), ("x2", _vp), ("s1", _i64), ("s2", _i64), ("off", _i64),
                 ("ldo", _i32), ("rows", _i32), ("cols", _i32), ("kind", _i32), ("seg", _i32),
-                ("r_fixed", _i32), ("tiles_b", _i32), ("tile0", _i32)]
+                ("r_fixed", _i32), ("r_extra", _i32), ("tiles_b", _i32), ("tile0", _i32)]
 
 
 class ErrorFlag:

@@ -47,9 +47,9 @@ class NodeState:
             self.mailbox_ts = torch.zeros(self.N, self.K, dtype=torch.float32, device=dev)
             self.memory_ts = torch.full((self.N,), -1.0, dtype=torch.float32, device=dev)
             self.next_mail_pos = torch.zeros(self.N, dtype=torch.int32, device=dev)
-            nwords = (self.N + 31) // 32 + 3 & ~3   # padded to 16-byte groups
-            self.node_bits = torch.zeros(nwords, dtype=torch.int32, device=dev)
-            self.word_prefix = torch.zeros(nwords, dtype=torch.int32, device=dev)
+            # node bitmap + its summary (layout owned by the library)
+            self.node_bits = torch.zeros(int(_capi.lib().sgl_node_bits_words(self.N)), dtype=torch.int32, device=dev)
+            self.word_prefix = torch.zeros((self.N + 31) // 32 + 3 & ~3, dtype=torch.int32, device=dev)
 
     def reset(self) -> None:
         self.memory.zero_()
@@ -92,6 +92,7 @@ class StepBuffers:
         i32, i64 = torch.int32, torch.int64
         self.num_roots = z(1, dt=i32)
         self.num_roots64 = z(1, dt=i64)
+        self.batch_start = z(1, dt=i64)
         self.ts_max = z(1)
         self.t_query = z(1, dt=i64)
         self.any_edges = z(1, dt=i32)
@@ -109,11 +110,16 @@ class StepBuffers:
         self.hop = PaddedHop(cnt=z(c, dt=i32), nbr=z(max(c * k, 1), dt=i32), eid=z(max(c * k, 1), dt=i32),
                              dt=z(max(c * k, 1)), ts=None, q_ts=self.root_ts, fanout=k)
         # attention saved state and gradients
-        self.Q, self.agg, self.z, self.y = z(c, D), z(c, D), z(c, D), z(c, D)
+        self.Q, self.agg, self.z = z(c, D), z(c, D), z(c, D)
+        self.y = z(c + TILE, D)          # rows >= cap stay zero (row U is read by the predictor's reductions)
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
         self.phi0 = z(max(dims.T, 1))
+        self.trig = z(max(c * k * 2 * dims.T, 1))   # each sampled edge's time-encoding cos, sin
         self.gy = z(c, D)
+        # per-root sums of the predictor's hidden-layer gradients (+ the
+        # non-root-negatives row U)
+        self.g_src, self.g_dst = z(c + 1, D), z(c + 1, D)
         self.pos = z(max(B, 1))
         self.neg = z(max(B, 1))
         self.loss = z(1)
@@ -155,16 +161,17 @@ class DeviceStep:
 
     # -- batch preparation --------------------------------------------------
     def prepare(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor,
-                n: int | None = None, event_offset: torch.Tensor | None = None) -> None:
-        """Batch preparation. With ``event_offset`` (device int64 [1]) src/dst/ts
-        are the whole stream and the batch is its ``n`` events from the offset."""
+                n: int | None = None, cursor: torch.Tensor | None = None) -> None:
+        """Batch preparation. With ``cursor`` (device int64 [1]) src/dst/neg/ts
+        are the whole stream, the batch is its ``n`` events from the cursor,
+        buf.batch_start receives the cursor and the cursor advances by n."""
         b, st, P = self.buf, self.state, _capi.ptr
         n = src.numel() if n is None else int(n)
         if n > b.max_batch:
             raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
         self._call("batch_prepare", lambda: _capi.check(self.lib.sgl_batch_prepare(
-            st.N, n, P(src), P(dst), P(neg), P(ts), P(event_offset), P(st.node_bits), P(st.word_prefix),
-            P(b.num_roots),
+            st.N, n, P(src), P(dst), P(neg), P(ts), P(cursor), P(b.batch_start) if cursor is not None else None,
+            P(st.node_bits), P(st.word_prefix), P(b.num_roots),
             P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
             P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
             self._s()), "sgl_batch_prepare"))
@@ -175,7 +182,10 @@ class DeviceStep:
                                                                    num_live=b.num_roots64))
 
     # -- memory -------------------------------------------------------------
-    def update_memory(self, gru: dict, src, dst, efeat, ts, event_offset: torch.Tensor | None = None) -> None:
+    def update_memory(self, gru: dict, src, dst, efeat, ts, from_cursor: bool = False) -> None:
+        """GRU + mailbox (sgl_memory_update); ``from_cursor``: the event arrays
+        span the stream and the batch starts at buf.batch_start."""
+        event_offset = self.buf.batch_start if from_cursor else None
         b, st, P = self.buf, self.state, _capi.ptr
         self._call("memory_update", lambda: _capi.check(self.lib.sgl_memory_update(
             st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
@@ -199,34 +209,47 @@ class DeviceStep:
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
             P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
             P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
-            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.phi0), P(b.y), self._s()), "sgl_conv_forward"))
+            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.phi0), P(b.trig), P(b.y), self._s()),
+            "sgl_conv_forward"))
         return b.y
 
-    def predictor(self, n: int, train: bool, pred: list[torch.Tensor], grads: list[torch.Tensor] | None):
+    def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None):
         """Edge predictor + BCE over the step's roots (sgl_predictor). ``pred``:
         src_fc.weight, src_fc.bias, dst_fc.weight, dst_fc.bias, out_fc.weight,
-        out_fc.bias; ``grads``: their gradient buffers (added into)."""
+        out_fc.bias; ``out_grads``: the out_fc weight / bias gradient buffers
+        (contiguous; overwritten). In training the per-root rows g_src / g_dst
+        are written for the attention backward and the weight reductions."""
         b, P = self.buf, _capi.ptr
-        g = grads if (train and grads is not None) else [None] * 6
+        g = out_grads if (train and out_grads is not None) else [None, None]
         self._call("predictor", lambda: _capi.check(self.lib.sgl_predictor(
-            n, self.dims.D, b.cap, 1 if train else 0, P(b.y), P(b.ridx_src), P(b.ridx_dst), P(b.ridx_neg),
-            P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]), P(b.pos), P(b.neg),
-            P(b.loss), P(b.gy) if train else None, P(g[0]), P(g[1]), P(g[2]), P(g[3]), P(g[4]), P(g[5]),
+            n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src), P(b.ridx_dst),
+            P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]), P(b.pos),
+            P(b.neg), P(b.loss), P(b.g_src) if train else None, P(b.g_dst) if train else None, P(g[0]), P(g[1]),
             self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
-    def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor) -> None:
+    def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor,
+                             gy: torch.Tensor | None = None, pred_w: tuple | None = None) -> None:
         """sgl_conv_backward only: per-root gradient rows and per-tile partials
-        in the step buffers (the weight gradients are StepParamUpdate's)."""
+        in the step buffers (the weight gradients are StepParamUpdate's).
+        dL/dy is ``gy``, or (gy None) comes from the predictor's per-root rows
+        with ``pred_w`` = (src_fc.weight, dst_fc.weight)."""
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
-        gy = gy.contiguous()
+        if gy is not None:
+            gy = gy.contiguous()
+            g_src = g_dst = w_s = w_d = None
+        else:
+            g_src, g_dst = b.g_src, b.g_dst
+            w_s, w_d = pred_w
         self._call("conv_backward", lambda: _capi.check(self.lib.sgl_conv_backward(
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
             P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
             P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
-            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(gy), P(b.gz), P(b.gagg), P(b.G), P(b.sigma), P(b.gQ),
+            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.trig), P(gy), P(g_src), P(g_dst), P(w_s), P(w_d), P(b.gz),
+            P(b.gagg),
+            P(b.G), P(b.sigma), P(b.gQ),
             P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
 
     def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
@@ -270,15 +293,15 @@ class StepParamUpdate:
     gradients from sgl_predictor (Adam-only jobs)."""
 
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
-                 gates: list[torch.Tensor | None]):
+                 pred_params: list[torch.Tensor], gates: list[torch.Tensor | None]):
         if len(opt.segments) != 2:
             raise ValueError("StepParamUpdate expects the attention and predictor segments")
         self.step, self.opt = step, opt
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
-        self.coef = torch.zeros(4 * len(opt.segments), dtype=torch.float32, device=dev)
-        jobs, tiles = self._jobs(conv_params)
+        self.done = torch.zeros(1, dtype=torch.int32, device=dev)
+        jobs, tiles = self._jobs(conv_params, pred_params)
         arr = (_capi.GradJob * len(jobs))(*jobs)
         raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
         self.jobs = raw.to(dev)
@@ -288,7 +311,7 @@ class StepParamUpdate:
         self._steps = (ctypes.c_void_p * len(opt.segments))(*[P(seg[2]) for seg in opt.segments])
         self._gates = (ctypes.c_void_p * len(opt.segments))(*[P(g) for g in gates])
 
-    def _jobs(self, conv_params):
+    def _jobs(self, conv_params, pred_params):
         b, d, opt = self.step.buf, self.step.dims, self.opt
         D, T, H, C = d.D, d.T, d.H, d.C
         dh = D // H
@@ -312,11 +335,11 @@ class StepParamUpdate:
             tiles.extend([len(jobs)] * ntile)
             jobs.append(job)
 
-        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1):
+        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0):
             assert s1 >= rows
             tb = (cols + 15) // 16
-            add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ldo=ldo, rows=rows, cols=cols, kind=0, seg=0,
-                              r_fixed=r_fixed, tiles_b=tb), ((rows + 15) // 16) * tb)
+            add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ldo=ldo, rows=rows, cols=cols, kind=0, seg=seg,
+                              r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb), ((rows + 15) // 16) * tb)
 
         one = at(self.one)
         gemm(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, ntiles)
@@ -334,23 +357,32 @@ class StepParamUpdate:
         gemm(at(b.gz), D, one, 0, off(b_out), 1, D, 1)
         gemm(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, ntiles)
         gemm(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, ntiles)
-        start, n, _ = opt.segments[1]
-        add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=start, ldo=1, rows=n, cols=1, kind=1, seg=1,
-                          r_fixed=0, tiles_b=1), (n + 255) // 256)
-        covered = sum(p.numel() for p in conv_params)
-        if covered != opt.segments[0][1]:
+        # edge predictor: src_fc / dst_fc as reductions over roots 0..U (row U
+        # of g_dst holds the non-root negatives; y's row U is zero); out_fc's
+        # gradients come from sgl_predictor (Adam only)
+        w_s, b_s, w_d, b_d, w_o, b_o = pred_params
+        gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, seg=1, r_extra=1)
+        gemm(at(b.g_src), D, one, 0, off(b_s), 1, D, 1, seg=1, r_extra=1)
+        gemm(at(b.g_dst), D, at(b.y), D, off(w_d), D, D, D, seg=1, r_extra=1)
+        gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, seg=1, r_extra=1)
+        if off(b_o) != off(w_o) + D:
+            raise RuntimeError("StepParamUpdate: out_fc weight and bias are not contiguous in the flat buffer")
+        add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=off(w_o), ldo=1, rows=D + 1, cols=1, kind=1, seg=1,
+                          r_fixed=0, tiles_b=1), (D + 1 + 255) // 256)
+        if sum(p.numel() for p in conv_params) != opt.segments[0][1]:
             raise RuntimeError("StepParamUpdate: the attention segment holds parameters the jobs do not cover")
+        if sum(p.numel() for p in pred_params) != opt.segments[1][1]:
+            raise RuntimeError("StepParamUpdate: the predictor segment holds parameters the jobs do not cover")
         return jobs, tiles
 
     def run(self) -> None:
-        """Advance the gated step counts, then gradients + Adam."""
+        """Gradients + Adam (the gated step counts advance in the same launch)."""
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
         b1, b2 = opt.betas
-        _capi.check(self.lib.sgl_adam_prepare(len(opt.segments), self._steps, self._gates, opt.lr, b1, b2,
-                                              P(self.coef), s), "sgl_adam_prepare")
-        _capi.check(self.lib.sgl_grad_adam(P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots),
-                                           P(opt.flat), P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq),
-                                           P(self.coef), b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam")
+        self.step._call("param_update", lambda: _capi.check(self.lib.sgl_grad_adam(
+            P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots), P(opt.flat),
+            P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._steps, self._gates,
+            P(self.done), opt.lr, b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
 
 
 class ConvFunction(torch.autograd.Function):
