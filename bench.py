@@ -25,6 +25,7 @@ also recorded inside the timed region itself.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import platform
@@ -244,6 +245,7 @@ def _restore(rt, snap):
         dst.copy_(src)
     for dst, src in zip([opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments], snap[1]):
         dst.copy_(src)
+    opt.mark_state_changed()
 
 
 def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float]:
@@ -298,6 +300,8 @@ def run_tgn(args, wl: dict) -> dict:
     if args.no_graphs:   # eager steps: time the dominant kernel inside the timed region
         rt.step.timer, rt.step.timed = timer, {dom}
     torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()   # no collector pauses on the host inside the timed region
     w0 = time.perf_counter()
     losses = []
     for b in batches:
@@ -306,6 +310,7 @@ def run_tgn(args, wl: dict) -> dict:
     host = time.perf_counter() - w0
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
+    gc.enable()
     log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]

@@ -313,10 +313,12 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * Each gradient element is written once, then Adam-updated (torch.optim.Adam
  * arithmetic) if its segment `seg` is active: gates[seg] NULL or
  * *gates[seg] != 0. steps[s] (device float) holds segment s's completed step
- * count; the launch uses t = steps[s] + 1 for the bias corrections and
- * advances the active segments' counts when its last workgroup finishes
- * (done: a device int32 completion counter, zero between launches). steps
- * and gates are host arrays of nseg <= SGL_MAX_ADAM_SEGMENTS device pointers.
+ * count t-1; coef[2s], coef[2s+1] (device) hold lr / (1 - beta1^t) and
+ * sqrt(1 - beta2^t) for that t (the caller writes them before the first
+ * launch). The launch's last workgroup to finish advances the active
+ * segments' counts and writes coef for the next launch (done: a device
+ * int32 completion counter, zero between launches). steps and gates are
+ * host arrays of nseg <= SGL_MAX_ADAM_SEGMENTS device pointers.
  * ------------------------------------------------------------------------- */
 #define SGL_MAX_ADAM_SEGMENTS 8
 
@@ -332,7 +334,7 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   int32_t num_tiles, const int32_t *num_roots, float *param,
                   float *grad, float *exp_avg, float *exp_avg_sq, int32_t nseg,
                   float *const *steps, const int32_t *const *gates,
-                  int32_t *done, float lr, float beta1, float beta2,
+                  float *coef, int32_t *done, float lr, float beta1, float beta2,
                   float eps, float weight_decay, hipStream_t stream);
 
 #ifdef __cplusplus

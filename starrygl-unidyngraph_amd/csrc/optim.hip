@@ -79,11 +79,12 @@ extern "C" int sgl_adam_advance(float *step, const int32_t *active, hipStream_t 
 // gradient is already in place. Either way each thread then owns one
 // gradient element: it stores the gradient and, if its segment is active
 // this step, applies the Adam update to the parameter and moments.
-// Every workgroup derives the bias corrections from the segment's completed
-// step count t-1 (unchanged during the launch); the last workgroup to finish
-// (an atomic completion counter, reset by it) advances the active segments'
-// counts, so no separate launch is needed and no workgroup reads a value
-// another one of this launch writes.
+// The bias corrections for this launch's t = steps[s] + 1 are read from
+// coef (written by the previous launch, or by the caller for the first);
+// the last workgroup to finish (an atomic completion counter, reset by it)
+// advances the active segments' step counts and writes the corrections for
+// the next launch. No workgroup reads a value another one of this launch
+// writes, so no separate launch or fence is needed.
 namespace {
 
 constexpr int kGaBlock = 256;
@@ -99,21 +100,15 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
                                                        const int32_t *__restrict__ num_roots, float *__restrict__ p,
                                                        float *__restrict__ g, float *__restrict__ m,
                                                        float *__restrict__ v, int nseg, AdamSegs segs,
-                                                       int32_t *__restrict__ done, float lr, float b1, float b2,
-                                                       float eps, float wd) {
+                                                       float *__restrict__ coef, int32_t *__restrict__ done,
+                                                       float lr, float b1, float b2, float eps, float wd) {
   __shared__ float red[4][16][17];
-  __shared__ float s_coef[3];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t = blockIdx.x;
   const sgl_grad_job jb = jobs[tile_job[t]];
   const int local = t - jb.tile0;
-  if (tid == 0) {
-    const bool act = segs.gate[jb.seg] == nullptr || *segs.gate[jb.seg] != 0;
-    const double st = double(*segs.step[jb.seg]) + 1.0;
-    s_coef[0] = float(double(lr) / (1.0 - pow(double(b1), st)));
-    s_coef[1] = float(sqrt(1.0 - pow(double(b2), st)));
-    s_coef[2] = act ? 1.f : 0.f;
-  }
+  const bool active = segs.gate[jb.seg] == nullptr || *segs.gate[jb.seg] != 0;
+  const float step_size = coef[2 * jb.seg], bc2_sqrt = coef[2 * jb.seg + 1];
 
   int64_t idx = 0;
   bool valid = false;
@@ -171,24 +166,31 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
     }
     __syncthreads();
   }
-  if (valid && s_coef[2] != 0.f) {
+  if (valid && active) {
     float gi = gv;
     if (wd != 0.f) gi = gi + wd * pv;
     mv = mv + (1.f - b1) * (gi - mv);
     vv = vv * b2 + (1.f - b2) * gi * gi;
     m[idx] = mv;
     v[idx] = vv;
-    const float denom = sqrtf(vv) / s_coef[1] + eps;
-    p[idx] = pv - s_coef[0] * (mv / denom);
+    const float denom = sqrtf(vv) / bc2_sqrt + eps;
+    p[idx] = pv - step_size * (mv / denom);
   }
-  // the last workgroup advances the active segments' step counts
-  if (tid == 0) {
-    __threadfence();
-    if (atomicAdd(done, 1) == int(gridDim.x) - 1) {
-      for (int s = 0; s < nseg; ++s)
-        if (segs.gate[s] == nullptr || *segs.gate[s] != 0) *segs.step[s] += 1.f;
-      *done = 0;
+  // the last workgroup advances the active segments' step counts and writes
+  // the next launch's bias corrections (torch.optim.Adam: lr / (1 - b1^t),
+  // sqrt(1 - b2^t), in double)
+  if (tid == 0 && atomicAdd(done, 1) == int(gridDim.x) - 1) {
+    for (int s = 0; s < nseg; ++s) {
+      float st = *segs.step[s];
+      if (segs.gate[s] == nullptr || *segs.gate[s] != 0) {
+        st += 1.f;
+        *segs.step[s] = st;
+      }
+      const double tn = double(st) + 1.0;
+      coef[2 * s] = float(double(lr) / (1.0 - pow(double(b1), tn)));
+      coef[2 * s + 1] = float(sqrt(1.0 - pow(double(b2), tn)));
     }
+    *done = 0;
   }
 }
 
@@ -196,12 +198,14 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
 
 extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, int32_t num_tiles,
                              const int32_t *num_roots, float *param, float *grad, float *exp_avg, float *exp_avg_sq,
-                             int32_t nseg, float *const *steps, const int32_t *const *gates, int32_t *done, float lr,
-                             float beta1, float beta2, float eps, float weight_decay, hipStream_t stream) {
+                             int32_t nseg, float *const *steps, const int32_t *const *gates, float *coef,
+                             int32_t *done, float lr, float beta1, float beta2, float eps, float weight_decay,
+                             hipStream_t stream) {
   SGL_REQUIRE(num_tiles >= 0, "grad_adam: num_tiles < 0");
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "grad_adam: nseg %d out of range", nseg);
   if (num_tiles == 0) return SGL_OK;
-  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && steps && done, "grad_adam: NULL array");
+  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && steps && coef && done,
+              "grad_adam: NULL array");
   AdamSegs segs{};
   for (int s = 0; s < nseg; ++s) {
     SGL_REQUIRE(steps[s] != nullptr, "grad_adam: NULL step counter %d", s);
@@ -209,8 +213,8 @@ extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, 
     segs.gate[s] = gates != nullptr ? gates[s] : nullptr;
   }
   k_grad_adam<<<unsigned(num_tiles), kGaBlock, 0, stream>>>(jobs, tile_job, num_roots, param, grad, exp_avg,
-                                                            exp_avg_sq, nseg, segs, done, lr, beta1, beta2, eps,
-                                                            weight_decay);
+                                                            exp_avg_sq, nseg, segs, coef, done, lr, beta1, beta2,
+                                                            eps, weight_decay);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -83,6 +83,8 @@ class CTDGOnlineRuntime:
         self._cursor = torch.zeros(1, dtype=torch.int64, device=self.device)
         self._cursor_host: int | None = None
         self._neg_all = torch.zeros(max(int(dataset.src.numel()), 1), dtype=torch.int64, device=self.device)
+        self._neg_all_ptr = self._neg_all.data_ptr()
+        self._views: dict[int, tuple] = {}
         self._update: StepParamUpdate | None = None
 
     def _core(self):
@@ -131,15 +133,21 @@ class CTDGOnlineRuntime:
             self._neg_queue[split] = (neg.to(self.device), 0)
 
     def _negatives(self, batch: CTDGDataBatch) -> torch.Tensor:
+        buf, off = self._negatives_at(batch)
+        return buf[off:off + batch.size] if off >= 0 else buf
+
+    def _negatives_at(self, batch: CTDGDataBatch) -> tuple[torch.Tensor, int]:
+        """(buffer, offset) of the batch's negatives (offset -1: the buffer is
+        exactly the batch's negatives); consumes the split's precomputed queue."""
         q = self._neg_queue.get(batch.split)
         if q is not None:
             buf, off = q
             n = batch.size
             if off + n <= buf.numel():
                 self._neg_queue[batch.split] = (buf, off + n)
-                return buf[off:off + n]
+                return buf, off
             del self._neg_queue[batch.split]
-        return self._negative_sample(batch).to(self.device, non_blocking=True)
+        return self._negative_sample(batch).to(self.device, non_blocking=True), -1
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev
@@ -156,24 +164,26 @@ class CTDGOnlineRuntime:
         if n > self.step.buf.max_batch:
             self.step = DeviceStep(self.memory.state, self.dims, n)
             self.reset_graphs()
-        conv = self._core().conv
-        if train and (conv.dropout.p > 0 or conv.att_dropout.p > 0):
-            raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
-                                      "ctdg.dropout and ctdg.att_dropout to 0")
-        neg = self._negatives(batch)
+        if train:
+            conv = self._core().conv
+            if conv.dropout.p > 0 or conv.att_dropout.p > 0:
+                raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
+                                          "ctdg.dropout and ctdg.att_dropout to 0")
+        buf, off = self._negatives_at(batch)
         b = self.step.buf
-        graphable = (self.use_graphs and n == b.max_batch and batch.start >= 0 and self.step.timer is None)
+        start = batch.start
+        graphable = (self.use_graphs and n == b.max_batch and start >= 0 and self.step.timer is None)
         if not graphable:
             src, dst, ts, ef = self._device_batch(batch)
-            self._step_body(split, train, n, src, dst, neg, ts, ef, None)
+            self._step_body(split, train, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
         else:
             d = self._dev
-            at = self._neg_all[batch.start:batch.start + n]
-            if neg.data_ptr() != at.data_ptr():
-                at.copy_(neg)
-            if self._cursor_host != batch.start:
-                self._cursor.fill_(batch.start)
-            self._cursor_host = batch.start + n
+            # the negatives must sit at the batch's place in the stream-wide array
+            if off < 0 or buf.data_ptr() + 8 * off != self._neg_all_ptr + 8 * start:
+                self._neg_all[start:start + n].copy_(buf[off:off + n] if off >= 0 else buf)
+            if self._cursor_host != start:
+                self._cursor.fill_(start)
+            self._cursor_host = start + n
             key = ("test" if split == "predict" else split, bool(train))
             args = (split, train, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"], self._cursor)
             g = self._graphs.get(key)
@@ -187,7 +197,11 @@ class CTDGOnlineRuntime:
             else:
                 self._graph_seen.add(key)
                 self._step_body(*args)
-        return StepTensors(b.loss[0], b.pos[:n], b.neg[:n], n)
+        views = self._views.get(n)
+        if views is None or views[0] is not b:
+            views = (b, b.loss[0], b.pos[:n], b.neg[:n])
+            self._views[n] = views
+        return StepTensors(views[1], views[2], views[3], n)
 
     def reset_graphs(self) -> None:
         """Drop captured step graphs (after buffers they reference change)."""
@@ -238,6 +252,8 @@ class CTDGOnlineRuntime:
                     core.out_fc.bias]
             upd = StepParamUpdate(self.step, inner, core.conv.kernel_params(), pred, [self.step.buf.any_edges, None])
             self._update = upd
+        elif upd.version != inner.state_version:
+            upd.sync()
         return upd
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:

@@ -16,6 +16,7 @@ backends/ctdg/runtime/runtime.py:225-297):
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 
 import torch
@@ -301,6 +302,10 @@ class StepParamUpdate:
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
         self.done = torch.zeros(1, dtype=torch.int32, device=dev)
+        # bias corrections for each segment's next step (then kept current by
+        # the kernel): torch.optim.Adam's lr / (1 - b1^t), sqrt(1 - b2^t)
+        self.coef = torch.zeros(2 * len(opt.segments), dtype=torch.float32, device=dev)
+        self.sync()
         jobs, tiles = self._jobs(conv_params, pred_params)
         arr = (_capi.GradJob * len(jobs))(*jobs)
         raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
@@ -375,6 +380,17 @@ class StepParamUpdate:
             raise RuntimeError("StepParamUpdate: the predictor segment holds parameters the jobs do not cover")
         return jobs, tiles
 
+    def sync(self) -> None:
+        """Recompute the bias corrections from the step counts (in place, so
+        captured graphs stay valid); needed after the counts are restored."""
+        b1, b2 = self.opt.betas
+        coef = []
+        for _, _, stepc in self.opt.segments:
+            t = float(stepc.item()) + 1.0
+            coef += [self.opt.lr / (1.0 - b1 ** t), math.sqrt(1.0 - b2 ** t)]
+        self.coef.copy_(torch.tensor(coef, dtype=torch.float32))
+        self.version = self.opt.state_version
+
     def run(self) -> None:
         """Gradients + Adam (the gated step counts advance in the same launch)."""
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
@@ -382,7 +398,7 @@ class StepParamUpdate:
         self.step._call("param_update", lambda: _capi.check(self.lib.sgl_grad_adam(
             P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots), P(opt.flat),
             P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._steps, self._gates,
-            P(self.done), opt.lr, b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
+            P(self.coef), P(self.done), opt.lr, b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
 
 
 class ConvFunction(torch.autograd.Function):
@@ -430,6 +446,10 @@ class FusedAdam:
                 off += k
             self.segments.append((start, off - start, torch.zeros(1, dtype=torch.float32, device=dev)))
         self.params = params
+        self.state_version = 0   # bumped when the step counts are restored
+
+    def mark_state_changed(self) -> None:
+        self.state_version += 1
 
     def zero_grad(self, set_to_none: bool = False) -> None:
         self.flat_grad.zero_()
@@ -455,3 +475,4 @@ class FusedAdam:
         self.exp_avg_sq.copy_(sd["exp_avg_sq"])
         for seg, st in zip(self.segments, sd["steps"]):
             seg[2].copy_(st)
+        self.mark_state_changed()
