@@ -2,7 +2,9 @@
 // counterpart of ParallelSampler::neighbor_sample_from_nodes_with_before_layer
 // with policy "recent", vendor/bts_sampler/sampler/include/sampler.h:213-261).
 //
-// Hot path: ONE kernel per hop, HBM/latency bound integer work.
+// Hot path: ONE kernel per hop, HBM/latency bound integer work. Up to 32768
+// queries (a training step) take k_recent_wave, one wavefront per query;
+// more take k_recent_padded:
 //   phase 1: one lane per query -- lower_bound over the node's int64
 //            timestamps (the same probe sequence as std::lower_bound) gives
 //            the window [end-k, end) of the node's list;
@@ -24,6 +26,7 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kTile = 256;      // queries per compaction tile
 constexpr int kScanBlock = 1024;
+constexpr int64_t kWaveModeMaxQueries = 1 << 15;  // below: one wavefront per query
 
 template <typename NodeT>
 __global__ __launch_bounds__(kBlock) void k_recent_padded(
@@ -90,6 +93,91 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
       out_dt[o] = float(tq - tv);  // int64 -> f32, round to nearest even
       if (out_ts != nullptr) out_ts[o] = tv;
     }
+  }
+}
+
+// Latency variant for small query counts (a training step's few hundred
+// roots): one wavefront per query, following std::lower_bound's decision
+// tree exactly (so unsorted timestamp lists give the reference's result
+// too), six levels per memory round trip: lane h-1 evaluates node h of the
+// next six levels' complete binary subtree (its (first, len) follows from
+// the path bits of h), a ballot collects the 63 comparisons, and the wave
+// then walks the six levels. A 100k-entry list takes 3 round trips instead
+// of 17 dependent probes. The window is then copied by the wave's lanes.
+constexpr int kWaveQueriesPerBlock = kBlock / sgl::kWave;
+
+template <typename NodeT>
+__global__ __launch_bounds__(kBlock) void k_recent_wave(
+    int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
+    const int64_t *__restrict__ q_ts, const int32_t *__restrict__ q_valid_cnt, int q_stride,
+    const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
+    const int32_t *__restrict__ eid, const int64_t *__restrict__ ts,
+    int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
+    int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
+    float *__restrict__ out_dt, int64_t *__restrict__ out_ts,
+    int32_t *__restrict__ err) {
+  const int lane = threadIdx.x & (sgl::kWave - 1);
+  const int64_t i = int64_t(blockIdx.x) * kWaveQueriesPerBlock + (threadIdx.x >> 6);
+  if (i >= nq) return;  // uniform per wave
+  const int64_t nq_live = nq_live_dev != nullptr ? min(nq, *nq_live_dev) : nq;
+  bool valid = i < nq_live;
+  if (valid && q_valid_cnt != nullptr) valid = int(i % q_stride) < q_valid_cnt[i / q_stride];
+  int c = 0;
+  int64_t b = 0, t = 0;
+  if (valid) {
+    const int64_t n = int64_t(q_node[i]);
+    t = q_ts[i];
+    if (n < 0 || n >= num_nodes) {
+      if (err != nullptr && lane == 0) atomicOr(err, SGL_DERR_NODE_RANGE);
+    } else {
+      const int64_t lo = indptr[n];
+      int64_t first = lo, len = indptr[n + 1] - lo;
+      const int h = lane + 1;  // heap index of this lane's node (1..63; lane 63 idle)
+      const int depth = 31 - __clz(h);
+      while (len > 0) {
+        int64_t fh = first, lh = len;
+        for (int d = depth - 1; d >= 0; --d) {
+          const int64_t half = lh >> 1;
+          if ((h >> d) & 1) {
+            fh += half + 1;
+            lh -= half + 1;
+          } else {
+            lh = half;
+          }
+        }
+        const bool below = h < sgl::kWave && lh > 0 && ts[fh + (lh >> 1)] < t;
+        const unsigned long long res = __ballot(below);
+        int node = 1;
+#pragma unroll
+        for (int lev = 0; lev < 6; ++lev) {
+          if (len == 0) break;
+          const int64_t half = len >> 1;
+          const bool r = (res >> (node - 1)) & 1ull;
+          if (r) {
+            first += half + 1;
+            len -= half + 1;
+          } else {
+            len = half;
+          }
+          node = 2 * node + (r ? 1 : 0);
+        }
+      }
+      const int64_t end = first - lo;
+      int64_t start = end - k;
+      if (start < 0) start = 0;
+      b = lo + start;
+      c = int(end - start);
+    }
+  }
+  if (lane == 0) out_cnt[i] = c;
+  const int64_t obase = i * k;
+  for (int j = lane; j < c; j += sgl::kWave) {
+    const int64_t src = b + j;
+    const int64_t tv = ts[src];
+    out_nbr[obase + j] = nbr[src];
+    out_eid[obase + j] = eid[src];
+    out_dt[obase + j] = float(t - tv);  // int64 -> f32, round to nearest even
+    if (out_ts != nullptr) out_ts[obase + j] = tv;
   }
 }
 
@@ -184,6 +272,19 @@ extern "C" int sgl_recent_sample(
   SGL_REQUIRE(q_valid_cnt == nullptr || q_stride > 0, "recent: q_stride must be > 0 with q_valid_cnt");
   const int64_t blocks = (num_queries + kBlock - 1) / kBlock;
   SGL_REQUIRE(blocks < INT_MAX, "recent: too many queries");
+  if (num_queries <= kWaveModeMaxQueries) {  // latency: one wavefront per query
+    const unsigned wblocks = unsigned((num_queries + kWaveQueriesPerBlock - 1) / kWaveQueriesPerBlock);
+    if (q_node_is_i64)
+      k_recent_wave<int64_t><<<wblocks, kBlock, 0, stream>>>(
+          num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
+          nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+    else
+      k_recent_wave<int32_t><<<wblocks, kBlock, 0, stream>>>(
+          num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
+          nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+    SGL_CHECK_LAUNCH();
+    return SGL_OK;
+  }
   if (q_node_is_i64) {
     k_recent_padded<int64_t><<<unsigned(blocks), kBlock, 0, stream>>>(
         num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
