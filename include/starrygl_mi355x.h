@@ -197,7 +197,8 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * (7) Time encoding + temporal attention, forward and backward.
  * Replaces TemporalTransformerConv.forward (backends/ctdg/runtime/models.py:77-137)
  * with TimeEncode (runtime/modules/time_encode.py:41-58) over the block of
- * build_dgl_block (models.py:144-197), one tile of 16 roots per workgroup.
+ * build_dgl_block (models.py:144-197), one tile of sgl_conv_tile_rows()
+ * roots per workgroup.
  * Inputs per root r < U: h_root[r] (its updated memory), its padded hop-0
  * window (cnt[r], nbr/eid/dt rows of the sampler); neighbour features come
  * from the committed memory table and efeat [num_edges][F].
@@ -214,10 +215,14 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * g_dst from sgl_predictor's per-root rows and the predictor's src_fc /
  * dst_fc weights w_s, w_d [D][D], and writes gz, gagg [cap][D], G [cap][H][D+F+T],
  * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
- * tile partial sums ln_part [cap/16][2][D] (gamma, beta) and
- * te_part [cap/16][2][T] (time-encoding w, b; the b part includes the
- * query's cos(b) term through w_q).
+ * tile partial sums ln_part [cap/R][2][D] (gamma, beta) and
+ * te_part [cap/R][2][T] (time-encoding w, b; the b part includes the
+ * query's cos(b) term through w_q), R = sgl_conv_tile_rows(D, F, T, H).
  * ------------------------------------------------------------------------- */
+/* Roots per attention workgroup for these dimensions (4 or 8; a divisor of
+ * 16), i.e. the row count of one ln_part / te_part tile; 0 if the
+ * dimensions are unsupported. */
+int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
 int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      int32_t fanout, int64_t capacity,
                      const int32_t *num_roots, const int32_t *any_edges,

@@ -1,5 +1,5 @@
 // TGN temporal attention (TimeEncode + TemporalTransformerConv), forward and
-// backward, one workgroup (8 or 16 waves) per tile of 16 roots.
+// backward, one workgroup (8 or 16 waves) per tile of 4 or 8 roots.
 //
 // Reference: TemporalTransformerConv.forward  backends/ctdg/runtime/models.py:77-137,
 //            build_dgl_block                  models.py:144-197,
@@ -18,12 +18,16 @@
 // GEMMs (qt and the W_v product), so per edge only a gather, T cosines and
 // 2H dot/axpy passes over C floats remain.
 //
-// Latency structure (a step has a few hundred roots, so a launch is ~U/16
-// workgroups and every phase is a chain of L2 round trips): the GEMMs issue
-// all weight loads of a block at once (mfma.h), and in the edge phase each
-// wave owns one root, reads its whole window's (nbr, eid, dt) with one load
-// per lane, then gathers the X rows of 4 edges per round trip. The softmax
-// runs online (running max / running sum) over the window.
+// Latency structure: a step has a few hundred roots, and every phase is a
+// chain of L2 round trips. A workgroup takes few roots (RPW = 4 or 8; the
+// MFMA tiles keep 16 rows, zero-padded), so a launch spreads over U/RPW
+// workgroups. The GEMMs issue all weight loads of a block at once (mfma.h).
+// In the edge phase WPR = waves / RPW waves share a root: each takes a
+// contiguous slice of the window, reads its slice's (nbr, eid, dt) with one
+// load per lane and gathers the X rows of 4 edges per round trip, with its own
+// online softmax (running max, running sum); the slices are merged through
+// LDS (global max, rescaled sums). The backward splits the window the same
+// way and sums the slices' gradient partials.
 //
 // No 1/sqrt(d) scaling (models.py:125). The time-encoding argument is
 // fl(fl(dt * w) + b), then cos. The forward saves each edge's cos and sin;
@@ -35,16 +39,18 @@
 
 namespace {
 
-constexpr int kRows = 16;
+constexpr int kRows = 16;   // MFMA tile rows
 constexpr int kEC = 4;      // edges gathered per round trip
 constexpr int kMaxH = 4;
 constexpr int kMaxJ = 8;    // C <= 512
 constexpr int kMaxWaves = 16;
 
-// Waves per workgroup for a (heads, column slots) instance: 16 (one root per
-// wave, 128 VGPRs each) while the edge loop's per-lane [H][J] arrays fit,
-// else 8 (two roots per wave, 256 VGPRs each).
+// Waves per workgroup for a (heads, column slots) instance: 16 (128 VGPRs
+// each) while the edge loop's per-lane [H][J] arrays fit, else 8 (256 VGPRs).
 constexpr int waves_for(int hm, int jm) { return hm * jm <= 6 || (hm == 2 && jm == 4) ? 16 : 8; }
+// Roots per workgroup: 16 waves share 4 roots (4 waves a root, merged
+// through LDS); 8 waves take 8 roots (one wave each, no merge).
+constexpr int rows_for(int nw) { return nw == 16 ? 4 : 8; }
 
 struct Dims {
   int D, F, T, H, C, dh, k;
@@ -125,6 +131,13 @@ __device__ __forceinline__ void load_x(const Dims &d, const float *__restrict__ 
   }
 }
 
+// The slice [lo, hi) of a window of ne edges that slice `sub` of `nsub` takes.
+__device__ __forceinline__ void window_slice(int ne, int sub, int nsub, int &lo, int &hi) {
+  const int per = (ne + nsub - 1) / nsub;
+  lo = min(ne, sub * per);
+  hi = min(ne, lo + per);
+}
+
 struct ConvParams {
   const float *w_q, *b_q, *w_k, *b_k, *w_v, *b_v, *w_out, *b_out, *ln_g, *ln_b, *te_w, *te_b;
 };
@@ -144,16 +157,18 @@ struct ConvSaved {
 
 struct FwdLds {
   int ldh, ldr, lda, ldq;
-  float *HT;  // [16][ldh]  [h | cos(b)]
-  float *Qs;  // [16][ldr]
-  float *AH;  // [16][lda]  [agg | h]
-  float *Zs;  // [16][ldr]
-  float *QT;  // [16][ldq]  qt, then xbar
-  float *qb;  // [16][H]
+  float *HT;    // [16][ldh]  [h | cos(b)]
+  float *Qs;    // [16][ldr]
+  float *AH;    // [16][lda]  [agg | h]
+  float *Zs;    // [16][ldr]
+  float *QT;    // [16][ldq]  qt, then xbar
+  float *qb;    // [16][H]
   float *TW, *TB;  // [T] time-encoding weight / bias
+  float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
+  float *pml;   // [NW][H][2] a slice's running max and sum (slices only)
 };
 
-__host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base) {
+__host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bool slices) {
   FwdLds L;
   L.ldh = d.D + d.T + 1;
   L.ldr = d.D + 1;
@@ -167,10 +182,18 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base) {
   L.qb = L.QT + kRows * L.ldq;
   L.TW = L.qb + kRows * d.H;
   L.TB = L.TW + d.T;
+  L.part = L.TB + d.T;
+  L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   return L;
 }
 
-template <int HM, int JM, int NW = waves_for(HM, JM)>
+inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices) {
+  float *base = reinterpret_cast<float *>(uintptr_t(4096));
+  const FwdLds L = fwd_lds(d, base, nw, slices);
+  return size_t(L.pml + (slices ? nw * d.H * 2 : 0) - base);
+}
+
+template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ h_root, const float *__restrict__ memory,
@@ -178,28 +201,30 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     const int32_t *__restrict__ nbr, const int32_t *__restrict__ eid,
     const float *__restrict__ dt, ConvParams p, ConvSaved sv, float *__restrict__ y) {
   constexpr int kWaves = NW, kBlock = NW * 64;
+  constexpr int WPR = NW / RPW;  // waves per root in the edge phase
+  static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
   extern __shared__ float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const FwdLds L = fwd_lds(d, lds);
+  const FwdLds L = fwd_lds(d, lds, NW, WPR > 1);
   __shared__ int s_cnt[kRows];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = *num_roots;
-  const int r0 = blockIdx.x * kRows;
-  const int nrows = max(0, min(kRows, U - r0));
+  const int r0 = blockIdx.x * RPW;
+  const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
   if (nrows == 0 || !live) {
     // rows outside the live set, or a block without edges: zero output and
     // zero saved state (the backward then produces zero gradients)
-    for (int idx = tid; idx < kRows * D; idx += kBlock) {
+    for (int idx = tid; idx < RPW * D; idx += kBlock) {
       const size_t o = size_t(r0) * D + idx;
       y[o] = 0.f; sv.Q[o] = 0.f; sv.agg[o] = 0.f; sv.z[o] = 0.f;
     }
-    for (int idx = tid; idx < kRows * H * C; idx += kBlock) {
+    for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
       sv.qt[size_t(r0) * H * C + idx] = 0.f;
       sv.xbar[size_t(r0) * H * C + idx] = 0.f;
     }
-    for (int idx = tid; idx < kRows * 2; idx += kBlock) sv.stats[size_t(r0) * 2 + idx] = 0.f;
+    for (int idx = tid; idx < RPW * 2; idx += kBlock) sv.stats[size_t(r0) * 2 + idx] = 0.f;
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
@@ -224,9 +249,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   // Q = W_q [h | cos(b)] + b_q
   sgl::tile_gemm16<sgl::kNT>(L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D, kWaves);
   __syncthreads();
-  for (int idx = tid; idx < kRows * D; idx += kBlock) {
+  for (int idx = tid; idx < RPW * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
-    sv.Q[size_t(r0 + i) * D + j] = L.Qs[i * L.ldr + j];
+    sv.Q[size_t(r0 + i) * D + j] = i < nrows ? L.Qs[i * L.ldr + j] : 0.f;
   }
   if (tid < kRows * H) {
     const int i = tid / H, h = tid - (tid / H) * H;
@@ -240,11 +265,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
                                dh, C, kWaves);
   __syncthreads();
 
-  // edge phase: a wave owns roots wave, wave + NW, ...; xbar overwrites qt in
-  // the root's LDS row
-  for (int i = wave; i < kRows; i += kWaves) {
+  // edge phase: wave w takes slice w % WPR of root w / WPR's window
+  {
+    const int i = wave / WPR, sub = wave % WPR;
     const int r = r0 + i;
     const int ne = s_cnt[i];
+    int elo, ehi;
+    window_slice(ne, sub, WPR, elo, ehi);
     float q[HM][JM], acc[HM][JM], m[HM], l[HM], qbh[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h) {
@@ -256,13 +283,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
         const int c = lane + 64 * j;
         const bool ok = h < H && c < C;
         q[h][j] = ok ? L.QT[i * L.ldq + h * C + c] : 0.f;
-        if (ok) sv.qt[size_t(r) * H * C + h * C + c] = q[h][j];
+        if (ok && sub == 0) sv.qt[size_t(r) * H * C + h * C + c] = i < nrows ? q[h][j] : 0.f;
         acc[h][j] = 0.f;
       }
     }
     const size_t base = size_t(r) * K;
-    for (int e0 = 0; e0 < ne; e0 += 64) {
-      const int mwin = min(64, ne - e0);
+    for (int e0 = elo; e0 < ehi; e0 += 64) {
+      const int mwin = min(64, ehi - e0);
       int my_nb = 0, my_ei = 0;
       float my_dt = 0.f;
       if (lane < mwin) {
@@ -303,37 +330,85 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
             const float s = sc[u][h];
             const float a = s > 0.f ? s : 0.2f * s;
             const float mn = fmaxf(m[h], a);
-            const float sc = __expf(m[h] - mn);
+            const float scale = __expf(m[h] - mn);
             const float pe = __expf(a - mn);
-            l[h] = l[h] * sc + pe;
+            l[h] = l[h] * scale + pe;
 #pragma unroll
-            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * sc + pe * x[u][j];
+            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
             m[h] = mn;
             if (lane == 0) sv.score[idx * H + h] = a;
           }
         }
       }
     }
+    if (WPR == 1) {
+      // the wave owns its root: xbar overwrites qt in the root's LDS row
+      // (only this wave reads that row)
 #pragma unroll
-    for (int h = 0; h < HM; ++h) {
-      if (h >= H) continue;
-      const float inv = ne > 0 ? 1.f / l[h] : 0.f;
+      for (int h = 0; h < HM; ++h) {
+        if (h >= H) continue;
+        const float inv = ne > 0 ? 1.f / l[h] : 0.f;
 #pragma unroll
-      for (int j = 0; j < JM; ++j) {
-        const int c = lane + 64 * j;
-        if (c < C) {
-          const float v = acc[h][j] * inv;
-          L.QT[i * L.ldq + h * C + c] = v;
-          sv.xbar[size_t(r) * H * C + h * C + c] = v;
+        for (int j = 0; j < JM; ++j) {
+          const int c = lane + 64 * j;
+          if (c < C) {
+            const float v = acc[h][j] * inv;
+            L.QT[i * L.ldq + h * C + c] = v;
+            sv.xbar[size_t(r) * H * C + h * C + c] = v;
+          }
+        }
+        if (lane == 0) {
+          sv.ml[(size_t(r) * H + h) * 2 + 0] = ne > 0 ? m[h] : 0.f;
+          sv.ml[(size_t(r) * H + h) * 2 + 1] = ne > 0 ? l[h] : 1.f;
         }
       }
-      if (lane == 0) {
-        sv.ml[(size_t(r) * H + h) * 2 + 0] = ne > 0 ? m[h] : 0.f;
-        sv.ml[(size_t(r) * H + h) * 2 + 1] = ne > 0 ? l[h] : 1.f;
+    } else {
+      // publish this slice's state for the merge (an empty slice has
+      // m = -inf, l = 0, acc = 0 and drops out with weight e^-inf = 0)
+#pragma unroll
+      for (int h = 0; h < HM; ++h) {
+        if (h >= H) continue;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+          const int c = lane + 64 * j;
+          if (c < C) L.part[(wave * H + h) * C + c] = acc[h][j];
+        }
+        if (lane == 0) {
+          L.pml[(wave * H + h) * 2 + 0] = m[h];
+          L.pml[(wave * H + h) * 2 + 1] = l[h];
+        }
       }
     }
   }
   __syncthreads();
+  if (WPR > 1) {
+    // merge the slices: M = max_s m_s, Lsum = sum_s l_s e^(m_s - M),
+    // xbar = sum_s acc_s e^(m_s - M) / Lsum (the whole window's softmax)
+    for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
+      const int i = idx / (H * C), hc = idx - i * (H * C), h = hc / C, c = hc - h * C;
+      const int r = r0 + i;
+      float v = 0.f, M = -INFINITY, Ls = 0.f;
+      if (s_cnt[i] > 0) {
+#pragma unroll
+        for (int s = 0; s < WPR; ++s) M = fmaxf(M, L.pml[((i * WPR + s) * H + h) * 2]);
+#pragma unroll
+        for (int s = 0; s < WPR; ++s) {
+          const int w = i * WPR + s;
+          const float f = __expf(L.pml[(w * H + h) * 2] - M);
+          Ls += L.pml[(w * H + h) * 2 + 1] * f;
+          v += L.part[(w * H + h) * C + c] * f;
+        }
+        v /= Ls;
+      }
+      L.QT[i * L.ldq + hc] = v;
+      sv.xbar[size_t(r) * H * C + hc] = v;
+      if (c == 0) {
+        sv.ml[(size_t(r) * H + h) * 2 + 0] = s_cnt[i] > 0 ? M : 0.f;
+        sv.ml[(size_t(r) * H + h) * 2 + 1] = s_cnt[i] > 0 ? Ls : 1.f;
+      }
+    }
+    __syncthreads();
+  }
   // agg_h = W_v[h rows] xbar_h + b_v[h]  -> AH[:, :D]
   {
     sgl::GemmJob jobs[HM];
@@ -347,14 +422,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     if (s_cnt[i] == 0) L.AH[i * L.lda + j] = 0.f;  // no in-edges: the sum aggregator gives 0
-    sv.agg[size_t(r0 + i) * D + j] = L.AH[i * L.lda + j];
+    if (i < RPW) sv.agg[size_t(r0 + i) * D + j] = L.AH[i * L.lda + j];
   }
   __syncthreads();
   // z = W_out [agg | h] + b_out
   sgl::tile_gemm16<sgl::kNT>(L.AH, L.lda, p.w_out, 2 * D, p.b_out, L.Zs, L.ldr, 2 * D, D, kWaves);
   __syncthreads();
   // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance; one wave per row
-  for (int i = wave; i < kRows; i += kWaves) {
+  for (int i = wave; i < RPW; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
     float s1 = 0.f;
     for (int j = lane; j < D; j += 64) {
@@ -374,8 +449,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       y[ro + j] = i < nrows ? xh * p.ln_g[j] + p.ln_b[j] : 0.f;
     }
     if (lane == 0) {
-      sv.stats[size_t(r0 + i) * 2 + 0] = mean;
-      sv.stats[size_t(r0 + i) * 2 + 1] = rstd;
+      sv.stats[size_t(r0 + i) * 2 + 0] = i < nrows ? mean : 0.f;
+      sv.stats[size_t(r0 + i) * 2 + 1] = i < nrows ? rstd : 0.f;
     }
   }
 }
@@ -396,9 +471,11 @@ struct BwdLds {
   float *GX;                      // [16][ldq]  g_xbar, then G
   float *tep;                     // [waves][2][T]
   float *TW, *TB;                 // [T] time-encoding weight / bias
+  float *part;                    // [NW][H*C]  a slice's G partial (slices only)
+  float *psig;                    // [NW][H]    a slice's sigma partial (slices only)
 };
 
-__host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base) {
+__host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bool slices) {
   BwdLds L;
   L.ldr = d.D + 1;
   L.ldq = d.H * d.C + 1;
@@ -409,12 +486,20 @@ __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base) {
   L.GY = L.XH + kRows * L.ldr;
   L.GX = L.GY + kRows * L.ldr;
   L.tep = L.GX + kRows * L.ldq;
-  L.TW = L.tep + kMaxWaves * 2 * d.T;
+  L.TW = L.tep + nw * 2 * d.T;
   L.TB = L.TW + d.T;
+  L.part = L.TB + d.T;
+  L.psig = L.part + (slices ? nw * d.H * d.C : 0);
   return L;
 }
 
-template <int HM, int JM, int NW = waves_for(HM, JM)>
+inline size_t bwd_lds_floats(const Dims &d, int nw, bool slices) {
+  float *base = reinterpret_cast<float *>(uintptr_t(4096));
+  const BwdLds L = bwd_lds(d, base, nw, slices);
+  return size_t(L.psig + (slices ? nw * d.H : 0) - base);
+}
+
+template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ memory, const float *__restrict__ efeat,
@@ -424,24 +509,26 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     const float *__restrict__ g_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
     ConvGrads g) {
   constexpr int kWaves = NW, kBlock = NW * 64;
+  constexpr int WPR = NW / RPW;
+  static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
   extern __shared__ float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const BwdLds L = bwd_lds(d, lds);
+  const BwdLds L = bwd_lds(d, lds, NW, WPR > 1);
   __shared__ int s_cnt[kRows];
   __shared__ float s_sig[kRows][kMaxH];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = *num_roots;
-  const int r0 = blockIdx.x * kRows;
-  const int nrows = max(0, min(kRows, U - r0));
+  const int r0 = blockIdx.x * RPW;
+  const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
   if (nrows == 0 || !live) {
-    for (int idx = tid; idx < kRows * D; idx += kBlock) {
+    for (int idx = tid; idx < RPW * D; idx += kBlock) {
       const size_t o = size_t(r0) * D + idx;
       g.gz[o] = 0.f; g.gagg[o] = 0.f; g.gQ[o] = 0.f;
     }
-    for (int idx = tid; idx < kRows * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
-    for (int idx = tid; idx < kRows * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
+    for (int idx = tid; idx < RPW * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
+    for (int idx = tid; idx < RPW * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
     for (int idx = tid; idx < 2 * D; idx += kBlock) g.ln_part[size_t(blockIdx.x) * 2 * D + idx] = 0.f;
     for (int idx = tid; idx < 2 * T; idx += kBlock) g.te_part[size_t(blockIdx.x) * 2 * T + idx] = 0.f;
     return;
@@ -470,7 +557,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     sgl::tile_gemm16<sgl::kNN, true>(L.GQ, L.ldr, w_d, D, nullptr, L.GY, L.ldr, D, D, kWaves);
     __syncthreads();
   }
-  // LayerNorm + ReLU backward; one wave per row
+  // LayerNorm + ReLU backward; one wave per row (rows past the tile zeroed)
   for (int i = wave; i < kRows; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
     if (i >= nrows) {
@@ -505,15 +592,15 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   // per-tile LayerNorm parameter grads; gz out
   for (int j = tid; j < D; j += kBlock) {
     float sg = 0.f, sb = 0.f;
-#pragma unroll 4
-    for (int i = 0; i < kRows; ++i) {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
       sg += L.GY[i * L.ldr + j] * L.XH[i * L.ldr + j];
       sb += L.GY[i * L.ldr + j];
     }
     g.ln_part[size_t(blockIdx.x) * 2 * D + j] = sg;
     g.ln_part[size_t(blockIdx.x) * 2 * D + D + j] = sb;
   }
-  for (int idx = tid; idx < kRows * D; idx += kBlock) {
+  for (int idx = tid; idx < RPW * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     g.gz[size_t(r0 + i) * D + j] = L.GZ[i * L.ldr + j];
   }
@@ -523,7 +610,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     if (s_cnt[i] == 0) L.GA[i * L.ldr + j] = 0.f;  // agg was the constant 0
-    g.gagg[size_t(r0 + i) * D + j] = L.GA[i * L.ldr + j];
+    if (i < RPW) g.gagg[size_t(r0 + i) * D + j] = L.GA[i * L.ldr + j];
   }
   __syncthreads();
   // g_xbar_h = g_agg_h W_v[h rows, :]
@@ -532,13 +619,16 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
                                dh, C, kWaves);
   __syncthreads();
 
-  // edge backward phase: a wave owns roots wave, wave + NW, ...
+  // edge backward phase: wave w takes slice w % WPR of root w / WPR's window
   float twp[JM], tbp[JM];  // this lane's time-encoding weight / bias partials
 #pragma unroll
   for (int j = 0; j < JM; ++j) { twp[j] = 0.f; tbp[j] = 0.f; }
-  for (int i = wave; i < kRows; i += kWaves) {
+  {
+    const int i = wave / WPR, sub = wave % WPR;
     const int r = r0 + i;
     const int ne = s_cnt[i];
+    int elo, ehi;
+    window_slice(ne, sub, WPR, elo, ehi);
     float q[HM][JM], gx[HM][JM], G[HM][JM];
     float dot[HM], sig[HM], mh[HM], lh[HM];
 #pragma unroll
@@ -560,8 +650,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       lh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2 + 1] : 1.f;
     }
     const size_t base = size_t(r) * K;
-    for (int e0 = 0; e0 < ne; e0 += 64) {
-      const int mwin = min(64, ne - e0);
+    for (int e0 = elo; e0 < ehi; e0 += 64) {
+      const int mwin = min(64, ehi - e0);
       int my_nb = 0, my_ei = 0;
       float my_dt = 0.f, my_sc[HM];
 #pragma unroll
@@ -631,20 +721,35 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         }
       }
     }
+    if (WPR == 1) {
+      // the wave owns its root: G overwrites g_xbar in the root's LDS row
+      // (only this wave reads that row)
 #pragma unroll
-    for (int h = 0; h < HM; ++h) {
-      if (h >= H) continue;
+      for (int h = 0; h < HM; ++h) {
+        if (h >= H) continue;
 #pragma unroll
-      for (int j = 0; j < JM; ++j) {
-        const int c = lane + 64 * j;
-        if (c < C) {
-          L.GX[i * L.ldq + h * C + c] = G[h][j];
-          g.G[size_t(r) * H * C + h * C + c] = G[h][j];
+        for (int j = 0; j < JM; ++j) {
+          const int c = lane + 64 * j;
+          if (c < C) {
+            L.GX[i * L.ldq + h * C + c] = G[h][j];
+            g.G[size_t(r) * H * C + h * C + c] = G[h][j];
+          }
+        }
+        if (lane == 0) {
+          g.sigma[size_t(r) * H + h] = sig[h];
+          s_sig[i][h] = sig[h];
         }
       }
-      if (lane == 0) {
-        g.sigma[size_t(r) * H + h] = sig[h];
-        s_sig[i][h] = sig[h];
+    } else {
+#pragma unroll
+      for (int h = 0; h < HM; ++h) {
+        if (h >= H) continue;
+#pragma unroll
+        for (int j = 0; j < JM; ++j) {
+          const int c = lane + 64 * j;
+          if (c < C) L.part[(wave * H + h) * C + c] = G[h][j];
+        }
+        if (lane == 0) L.psig[wave * H + h] = sig[h];
       }
     }
   }
@@ -659,6 +764,27 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     }
   }
   __syncthreads();
+  if (WPR > 1) {
+    // sum the slices' partials into the root's row (every read of g_xbar is
+    // behind the barrier above)
+    for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
+      const int i = idx / (H * C), hc = idx - i * (H * C), h = hc / C, c = hc - h * C;
+      float v = 0.f;
+#pragma unroll
+      for (int s = 0; s < WPR; ++s) v += L.part[((i * WPR + s) * H + h) * C + c];
+      L.GX[i * L.ldq + hc] = v;
+      g.G[size_t(r0 + i) * H * C + hc] = v;
+    }
+    for (int idx = tid; idx < RPW * H; idx += kBlock) {
+      const int i = idx / H, h = idx - (idx / H) * H;
+      float v = 0.f;
+#pragma unroll
+      for (int s = 0; s < WPR; ++s) v += L.psig[(i * WPR + s) * H + h];
+      g.sigma[size_t(r0 + i) * H + h] = v;
+      s_sig[i][h] = v;
+    }
+    __syncthreads();
+  }
   // gQ_h = W_k[h rows] G_h + b_k[h] sigma_h
   {
     sgl::GemmJob jobs[HM];
@@ -669,7 +795,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
   }
   __syncthreads();
-  for (int idx = tid; idx < kRows * D; idx += kBlock) {
+  for (int idx = tid; idx < RPW * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     const int h = j / dh;
     const float v = i < nrows ? L.GQ[i * L.ldr + j] + p.b_k[j] * s_sig[i][h] : 0.f;
@@ -680,7 +806,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   // column sums of this tile's gQ (GA row 0 is free by now)
   for (int j = tid; j < D; j += kBlock) {
     float sq = 0.f;
-    for (int i = 0; i < kRows; ++i) sq += L.GQ[i * L.ldr + j];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) sq += L.GQ[i * L.ldr + j];
     L.GA[j] = sq;
   }
   __syncthreads();
@@ -697,19 +824,6 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
 }
 
-// LDS sizes from the same carving as the kernels (on a dummy base address)
-size_t fwd_lds_bytes(const Dims &d) {
-  float *base = reinterpret_cast<float *>(uintptr_t(4096));
-  const FwdLds L = fwd_lds(d, base);
-  return sizeof(float) * size_t(L.TB + d.T - base);
-}
-
-size_t bwd_lds_bytes(const Dims &d) {
-  float *base = reinterpret_cast<float *>(uintptr_t(4096));
-  const BwdLds L = bwd_lds(d, base);
-  return sizeof(float) * size_t(L.TB + d.T - base);
-}
-
 int check_dims(const Dims &d) {
   SGL_REQUIRE(d.D > 0 && d.H > 0 && d.H <= kMaxH && d.D % d.H == 0, "conv: need 0 < H <= %d and D %% H == 0 (D=%d H=%d)",
               kMaxH, d.D, d.H);
@@ -724,34 +838,48 @@ template <typename Fn>
 struct Instance {
   Fn fn;
   int waves;
+  int rows;  // roots per workgroup
 };
+
+inline void instance_shape(const Dims &d, int &hm, int &jm) {
+  const int j = (d.C + 63) / 64;
+  jm = j <= 2 ? 2 : j <= 4 ? 4 : j <= 6 ? 6 : 8;
+  hm = d.H <= 1 ? 1 : d.H <= 2 ? 2 : 4;
+}
 
 template <template <int, int> class Pick>
 auto pick_instance(const Dims &d) -> decltype(Pick<1, 2>::get()) {
-  const int j = (d.C + 63) / 64;
-  const int jm = j <= 2 ? 2 : j <= 4 ? 4 : j <= 6 ? 6 : 8;
-  const int hm = d.H <= 1 ? 1 : d.H <= 2 ? 2 : 4;
+  int hm, jm;
+  instance_shape(d, hm, jm);
 #define SGL_PICK(HH, JJ) \
   if (hm == HH && jm == JJ) return Pick<HH, JJ>::get();
   SGL_PICK(1, 2) SGL_PICK(1, 4) SGL_PICK(1, 6) SGL_PICK(1, 8)
   SGL_PICK(2, 2) SGL_PICK(2, 4) SGL_PICK(2, 6) SGL_PICK(2, 8)
   SGL_PICK(4, 2) SGL_PICK(4, 4) SGL_PICK(4, 6) SGL_PICK(4, 8)
 #undef SGL_PICK
-  return {nullptr, 0};
+  return {nullptr, 0, 0};
 }
 
 using FwdFn = decltype(&k_conv_fwd<1, 2>);
 using BwdFn = decltype(&k_conv_bwd<1, 2>);
 template <int HM, int JM>
 struct FwdPick {
-  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM>, waves_for(HM, JM)}; }
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
 template <int HM, int JM>
 struct BwdPick {
-  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM>, waves_for(HM, JM)}; }
+  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
 
 }  // namespace
+
+extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H) {
+  const Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, 0};
+  if (check_dims(d) != SGL_OK) return 0;
+  int hm, jm;
+  instance_shape(d, hm, jm);
+  return rows_for(waves_for(hm, jm));
+}
 
 extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int32_t fanout, int64_t capacity,
                                 const int32_t *num_roots, const int32_t *any_edges, const float *h_root,
@@ -771,14 +899,14 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                   b_out && ln_g && ln_b && te_w && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z &&
                   sv_stats && y && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score)),
               "conv_forward: NULL array");
-  const size_t lds = fwd_lds_bytes(d);
-  SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   const auto inst = pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
+  const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
+  SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_trig};
-  inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
+  inst.fn<<<unsigned(capacity / inst.rows), unsigned(inst.waves * 64), lds, stream>>>(
       d, num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
@@ -806,17 +934,17 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                   gagg && G && sigma && gQ && ln_part &&
                   te_part && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score && sv_trig)),
               "conv_backward: NULL array");
-  const size_t lds = bwd_lds_bytes(d);
-  SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   const auto inst = pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
+  const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
+  SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
                const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr, const_cast<float *>(sv_trig)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
-  inst.fn<<<unsigned(capacity / kRows), unsigned(inst.waves * 64), lds, stream>>>(
+  inst.fn<<<unsigned(capacity / inst.rows), unsigned(inst.waves * 64), lds, stream>>>(
       d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g_src, g_dst, w_s, w_d, g);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

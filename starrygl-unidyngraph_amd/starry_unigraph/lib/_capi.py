@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
+    "sgl_conv_tile_rows": (_i32, [_i32] * 4),
     "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 33),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 42),
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 19),

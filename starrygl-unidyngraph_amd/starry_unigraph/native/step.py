@@ -126,8 +126,13 @@ class StepBuffers:
         self.loss = z(1)
         self.gz, self.gagg, self.gQ = z(c, D), z(c, D), z(c, D)
         self.G, self.sigma = z(c, H, C), z(c, H)
-        self.ln_part = z(c // TILE, 2, D)
-        self.te_part = z(c // TILE, 2, max(dims.T, 1))
+        # per-workgroup partial sums of the attention backward: one tile per
+        # conv_rows roots
+        self.conv_rows = int(_capi.lib().sgl_conv_tile_rows(D, dims.F, dims.T, H))
+        if self.conv_rows <= 0 or TILE % self.conv_rows:
+            raise RuntimeError(f"sgl_conv_tile_rows: unsupported attention dimensions {dims}")
+        self.ln_part = z(c // self.conv_rows, 2, D)
+        self.te_part = z(c // self.conv_rows, 2, max(dims.T, 1))
 
 
 class DeviceStep:
@@ -320,7 +325,7 @@ class StepParamUpdate:
         b, d, opt = self.step.buf, self.step.dims, self.opt
         D, T, H, C = d.D, d.T, d.H, d.C
         dh = D // H
-        ntiles = b.cap // TILE
+        ntiles = b.cap // b.conv_rows
         base = opt.flat.data_ptr()
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
 

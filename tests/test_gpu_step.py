@@ -151,12 +151,16 @@ def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
     return rng, row, col, ts, roots, tq, mem, ef
 
 
-@pytest.mark.parametrize("H,k,seed", [(2, 10, 0), (4, 20, 1), (1, 3, 2)])
-def test_conv_forward_backward_matches_oracle(gpu, H, k, seed):
+# (D, F, T, H) cover both attention tile shapes: 16 waves sharing 4 roots
+# (slices of a window merged through LDS; k=3 leaves a slice empty) and 8
+# waves with one root each (H=4, or C = D+F+T above 256 with H=2); the last
+# two rows are the shapes of the benchmark configurations.
+@pytest.mark.parametrize("H,k,seed,D,F,T", [(2, 10, 0, 32, 6, 16), (4, 20, 1, 32, 6, 16), (1, 3, 2, 32, 6, 16),
+                                            (2, 10, 3, 100, 16, 100), (2, 10, 4, 100, 172, 100)])
+def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T):
     from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
     from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
-    D, F, T = 32, 6, 16
     rng, row, col, ts, roots, tq, mem, ef = _conv_inputs(gpu, seed, D=D, F=F, T=T, H=H, k=k)
     N, R = mem.shape[0], len(roots)
     torch.manual_seed(seed)
