@@ -246,6 +246,7 @@ def _restore(rt, snap):
     for dst, src in zip([opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments], snap[1]):
         dst.copy_(src)
     opt.mark_state_changed()
+    rt.fence()
 
 
 def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float]:
@@ -298,15 +299,15 @@ def run_tgn(args, wl: dict) -> dict:
     dom = args.roofline_kernel
     timer: list = []
     if args.no_graphs:   # eager steps: time the dominant kernel inside the timed region
-        rt.step.timer, rt.step.timed = timer, {dom}
+        for st in rt.steps:
+            st.timer, st.timed = timer, {dom}
     torch.cuda.synchronize()
     gc.collect()
     gc.disable()   # no collector pauses on the host inside the timed region
     w0 = time.perf_counter()
-    losses = []
+    out = None
     for b in batches:
         out = rt.train_step(b)
-        losses.append(out["loss"])
     host = time.perf_counter() - w0
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
@@ -314,13 +315,15 @@ def run_tgn(args, wl: dict) -> dict:
     log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]
-    final_loss = float(torch.stack(losses).mean().item())
+    # the step's loss is a view of a reused step buffer: read the last one
+    final_loss = float(out["loss"].item()) if out is not None else float("nan")
     log(f"timed {args.steps} steps: {wall * 1e3 / args.steps:.3f} ms/step, {events / wall:.0f} events/s")
 
     # replay the same steps eagerly with every library call timed + per-step counts
     _restore(rt, snap)
     rt._neg_queue = dict(neg_state)
-    rt.step.timer, rt.step.timed = timer, None
+    for st in rt.steps:
+        st.timer, st.timed = timer, None
     timer.clear()
     per_step = []
     for b in batches:
@@ -361,14 +364,15 @@ def run_tgn(args, wl: dict) -> dict:
         ach, peak, unit = dwork / (dom_avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
     res = {
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
-        "mean_train_loss": final_loss,
+        "final_train_loss": final_loss,
         "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
                      "frac": ach / peak, "traffic": None, "kernel_avg_ms": dom_avg,
                      "work_per_launch": dwork},
         "kernels": breakdown,
         "step_shape": {"mean_roots": round(mean_U, 1), "mean_sampled_edges": round(mean_E, 1)},
     }
-    rt.step.timer = None
+    for st in rt.steps:
+        st.timer = None
     if not args.no_cpu:
         res["cpu_baseline"] = tgn_cpu_baseline(wl, stream, rt)
     return res
@@ -457,7 +461,7 @@ def main() -> None:
                                     "dropout 0",
                         "global_batch": wl["B"], "parallelism": "single GPU"},
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
-                step_shape=r["step_shape"], mean_train_loss=r["mean_train_loss"])
+                step_shape=r["step_shape"], final_train_loss=r["final_train_loss"])
     if args.workload == "tgn-large" and not args.no_sampler:
         line["sampler"] = run_sampler(20, 3, cases=False, cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)

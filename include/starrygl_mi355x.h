@@ -342,6 +342,27 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   float *coef, int32_t *done, float lr, float beta1, float beta2,
                   float eps, float weight_decay, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Two-stream submission of a training step from captured graphs. Replaces
+ * the reference's per-step call sequence in CTDGOnlineRuntime.train_step
+ * (backends/ctdg/runtime/runtime.py:225-328, which runs the stages one after
+ * another on one stream) for consecutive full batches; no reference
+ * counterpart exists for the overlap itself.
+ * front_exec: batch preparation + sampling + GRU memory update of step t;
+ * commit_exec: sgl_memory_commit of step t; back_exec: attention forward,
+ * predictor, backward and sgl_grad_adam of step t (hipGraphExec_t handles).
+ * Enqueues, without blocking the host:
+ *   front: wait(committed), front_exec, record(fronted)
+ *   back:  wait(fronted), commit_exec, record(committed), back_exec
+ * so step t+1's front part overlaps step t's back part. Consecutive calls
+ * must use graphs over different step buffers (ping-pong), and work queued
+ * on the back stream between calls that the next front part depends on must
+ * be published by recording `committed` on the back stream.
+ * ------------------------------------------------------------------------- */
+int sgl_graph_pipeline(void *front_exec, void *commit_exec, void *back_exec,
+                       hipStream_t front, hipStream_t back,
+                       hipEvent_t committed, hipEvent_t fronted);
+
 #ifdef __cplusplus
 }
 #endif

@@ -107,6 +107,7 @@ class CTDGMemoryBank:
     def _write_slots(self, ids: torch.Tensor, vals: torch.Tensor, ts: torch.Tensor) -> None:
         if ids.numel() == 0:
             return
+        self.state.touched()
         K = self.mailbox_slots
         order = torch.argsort(ts, stable=True)
         ids_o, vals_o, ts_o = ids[order], vals[order], ts[order]
@@ -123,6 +124,7 @@ class CTDGMemoryBank:
         if node_ids.numel() == 0:
             return
         ids = self._ids(node_ids)
+        self.state.touched()
         ts = timestamps.to(ids.device).float()
         order = torch.argsort(ts, stable=True)
         self.state.memory[ids[order]] = values.to(ids.device).float()[order]

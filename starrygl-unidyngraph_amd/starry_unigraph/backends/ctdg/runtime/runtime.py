@@ -24,6 +24,7 @@ from typing import Any, Iterable
 import torch
 import torch.nn.functional as F
 
+from starry_unigraph.lib import _capi
 from starry_unigraph.native.step import ConvDims, DeviceStep, FusedAdam, StepParamUpdate
 
 from .data import CTDGDataBatch, TGTemporalDataset
@@ -61,20 +62,25 @@ class CTDGOnlineRuntime:
         self.dist_ctx = dist_ctx
         self.memory_updater = memory_updater
         self.collect_results = True
-        # Full-size batches of a contiguous split run as one captured HIP graph
-        # per (split, train/eval); the graph reads the events at a device-side
-        # cursor and the negatives from a staging buffer, so one capture
-        # replays for every batch. The first full batch of a kind runs eagerly.
+        # Full-size batches of a contiguous split run as captured HIP graphs
+        # per (split, train/eval, step buffer); the graphs read the events at a
+        # device-side cursor and the negatives from a stream-wide array, so one
+        # capture replays for every batch. The first full batch of a kind runs
+        # eagerly. With a memory updater a step is three graphs (front part,
+        # memory commit, back part) submitted over two streams so that the
+        # next step's front part overlaps this step's back part
+        # (sgl_graph_pipeline); consecutive steps alternate between two sets
+        # of step buffers.
         self.use_graphs = True
-        self._graphs: dict[tuple[str, bool], torch.cuda.CUDAGraph] = {}
-        self._graph_seen: set[tuple[str, bool]] = set()
+        self._graphs: dict[tuple[str, bool, int], tuple] = {}
+        self._graph_seen: set[tuple[str, bool, int]] = set()
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
         core = self._core()
         conv = core.conv
         self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head,
                              fanout=int(sampler.fanout[0]) if sampler.fanout else 0)
-        self.step = DeviceStep(memory.state, self.dims, int(max_batch or 1))
+        self._make_steps(int(max_batch or 1))
         self._dev = dataset.device_arrays(self.device)
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
         # graph replays read events and negatives at a device cursor that the
@@ -84,8 +90,43 @@ class CTDGOnlineRuntime:
         self._cursor_host: int | None = None
         self._neg_all = torch.zeros(max(int(dataset.src.numel()), 1), dtype=torch.int64, device=self.device)
         self._neg_all_ptr = self._neg_all.data_ptr()
-        self._views: dict[int, tuple] = {}
-        self._update: StepParamUpdate | None = None
+        self._views: dict[tuple[int, int], tuple] = {}
+        self._updates: dict[int, StepParamUpdate] = {}
+        # two-stream submission: the front stream runs batch preparation,
+        # sampling and the GRU; the caller's current stream the rest.
+        # _ev_commit marks what the next front part must wait for (the last
+        # commit, or everything queued before a fence), _ev_front the end of
+        # the last front part.
+        self._front_stream: torch.cuda.Stream | None = None
+        self._ev_commit: torch.cuda.Event | None = None
+        self._ev_front: torch.cuda.Event | None = None
+        self._state_writes = memory.state.writes
+
+    def _make_steps(self, max_batch: int) -> None:
+        self.steps = [DeviceStep(self.memory.state, self.dims, max_batch) for _ in range(2)]
+        self._parity = 0
+        self.step = self.steps[0]   # the step buffers of the latest step
+
+    def fence(self) -> None:
+        """Order the next step after all work queued so far on the current
+        stream. With ``collect_results`` False consecutive steps overlap, and
+        a caller that writes state the step reads (memory, mailbox, GRU
+        weights, event arrays) with tensor code between steps calls this
+        before the next step; the memory bank's own writers are tracked
+        without it. With ``collect_results`` every step is fenced."""
+        if self._ev_commit is not None:
+            self._ev_commit.record(torch.cuda.current_stream(self.device))
+        self._state_writes = self.memory.state.writes
+
+    def _pipeline_streams(self):
+        if self._front_stream is None:
+            self._front_stream = torch.cuda.Stream(self.device)
+            self._ev_commit = torch.cuda.Event()
+            self._ev_front = torch.cuda.Event()
+            cur = torch.cuda.current_stream(self.device)
+            self._ev_commit.record(cur)   # materialise both events
+            self._ev_front.record(cur)
+        return self._front_stream
 
     def _core(self):
         return self.model.module if hasattr(self.model, "module") else self.model
@@ -131,6 +172,7 @@ class CTDGOnlineRuntime:
             self._neg_queue[split] = (view, 0)
         else:
             self._neg_queue[split] = (neg.to(self.device), 0)
+        self.fence()   # the next batch preparation reads them
 
     def _negatives(self, batch: CTDGDataBatch) -> torch.Tensor:
         buf, off = self._negatives_at(batch)
@@ -161,63 +203,113 @@ class CTDGOnlineRuntime:
     # ------------------------------------------------------------- the step
     def _forward(self, batch: CTDGDataBatch, split: str, train: bool) -> StepTensors:
         n = batch.size
-        if n > self.step.buf.max_batch:
-            self.step = DeviceStep(self.memory.state, self.dims, n)
+        if n > self.steps[0].buf.max_batch:
+            self._make_steps(n)
             self.reset_graphs()
         if train:
             conv = self._core().conv
             if conv.dropout.p > 0 or conv.att_dropout.p > 0:
                 raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
                                           "ctdg.dropout and ctdg.att_dropout to 0")
+        q = self._parity
+        self._parity = q ^ 1
+        step = self.steps[q]
+        self.step = step
         buf, off = self._negatives_at(batch)
-        b = self.step.buf
+        b = step.buf
         start = batch.start
-        graphable = (self.use_graphs and n == b.max_batch and start >= 0 and self.step.timer is None)
+        graphable = (self.use_graphs and n == b.max_batch and start >= 0 and step.timer is None)
         if not graphable:
             src, dst, ts, ef = self._device_batch(batch)
-            self._step_body(split, train, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
+            self._front_body(step, split, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
+            self._commit_body(step)
+            self._back_body(step, train, n)
+            self.fence()
         else:
             d = self._dev
             # the negatives must sit at the batch's place in the stream-wide array
             if off < 0 or buf.data_ptr() + 8 * off != self._neg_all_ptr + 8 * start:
                 self._neg_all[start:start + n].copy_(buf[off:off + n] if off >= 0 else buf)
+                self.fence()
             if self._cursor_host != start:
                 self._cursor.fill_(start)
+                self.fence()
             self._cursor_host = start + n
-            key = ("test" if split == "predict" else split, bool(train))
-            args = (split, train, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"], self._cursor)
+            # overlap across steps only in the asynchronous mode: a caller
+            # that reads each step's results on the host may also write state
+            # between steps, so its steps start after everything queued before
+            if self.collect_results or self._state_writes != self.memory.state.writes:
+                self.fence()
+            key = ("test" if split == "predict" else split, bool(train), q)
+            args = (step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"], self._cursor)
             g = self._graphs.get(key)
             if g is None and key in self._graph_seen:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    self._step_body(*args)
+                g = self._capture(args, train)
                 self._graphs[key] = g
-            if g is not None:
-                g.replay()
-            else:
+            if g is None:
                 self._graph_seen.add(key)
-                self._step_body(*args)
-        views = self._views.get(n)
+                self._front_body(*args)
+                self._commit_body(step)
+                self._back_body(step, train, n)
+                self.fence()
+            elif len(g) == 4:   # (front, commit, back) executables + the graphs that own them
+                front = self._pipeline_streams()
+                _capi.check(_capi.lib().sgl_graph_pipeline(
+                    g[0], g[1], g[2], front.cuda_stream, torch.cuda.current_stream(self.device).cuda_stream,
+                    self._ev_commit.cuda_event, self._ev_front.cuda_event), "sgl_graph_pipeline")
+            else:
+                g[0].replay()
+        views = self._views.get((n, q))
         if views is None or views[0] is not b:
             views = (b, b.loss[0], b.pos[:n], b.neg[:n])
-            self._views[n] = views
+            self._views[(n, q)] = views
         return StepTensors(views[1], views[2], views[3], n)
+
+    def _capture(self, args, train: bool) -> tuple:
+        """Capture a full step: (front, commit, back) graph executables plus
+        the graphs, or (graph,) when there is no memory updater to split at."""
+        step = args[0]
+        if train:
+            self._param_update(step)   # any rebuild or host-side sync happens before the capture
+        if self._gru is None:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._front_body(*args)
+                self._back_body(step, train, args[2])
+            return (g,)
+        gs = [torch.cuda.CUDAGraph() for _ in range(3)]
+        with torch.cuda.graph(gs[0]):
+            self._front_body(*args)
+        with torch.cuda.graph(gs[1]):
+            self._commit_body(step)
+        with torch.cuda.graph(gs[2]):
+            self._back_body(step, train, args[2])
+        return tuple(int(x.raw_cuda_graph_exec()) for x in gs) + (gs,)
 
     def reset_graphs(self) -> None:
         """Drop captured step graphs (after buffers they reference change)."""
+        if self._ev_commit is not None:
+            torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
         self._graphs.clear()
         self._graph_seen.clear()
 
-    def _step_body(self, split: str, train: bool, n: int, src, dst, neg, ts, ef, cursor) -> None:
-        """The device work of one step. With ``cursor`` (device int64 [1]) the
-        event and negative arrays are the whole stream and the batch starts at
-        the cursor (which the step advances)."""
-        step = self.step
+    def _front_body(self, step: DeviceStep, split: str, n: int, src, dst, neg, ts, ef, cursor) -> None:
+        """Batch preparation, sampling and the GRU memory update of one step.
+        With ``cursor`` (device int64 [1]) the event and negative arrays are
+        the whole stream and the batch starts at the cursor (which the step
+        advances)."""
         step.prepare(src, dst, neg, ts, n=n, cursor=cursor)
         step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
         if self._gru is not None:
             step.update_memory(self._gru, src, dst, ef, ts, from_cursor=cursor is not None)
+
+    def _commit_body(self, step: DeviceStep) -> None:
+        if self._gru is not None:
             step.commit()
+
+    def _back_body(self, step: DeviceStep, train: bool, n: int) -> None:
+        """Attention forward, edge predictor + BCE and, in training, the
+        backward and the fused weight-gradient + Adam update."""
         core = self._core()
         conv = core.conv
         efeat_all = self._dev["edge_feat"]
@@ -228,7 +320,7 @@ class CTDGOnlineRuntime:
             # gradients are views of the optimizer's flat buffer (no torch
             # autograd on this path): sgl_predictor writes out_fc's, the fused
             # update every other parameter's
-            upd = self._param_update()
+            upd = self._param_update(step)
             out_grads = [core.out_fc.weight.grad, core.out_fc.bias.grad]
         else:
             out_grads = None
@@ -239,19 +331,20 @@ class CTDGOnlineRuntime:
             step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]))
             upd.run()
 
-    def _param_update(self) -> StepParamUpdate:
-        """The fused weight-gradient + Adam launches for the current step
-        buffers and the runtime's optimizer (rebuilt if either changed)."""
+    def _param_update(self, step: DeviceStep) -> StepParamUpdate:
+        """The fused weight-gradient + Adam launch for a step's buffers and the
+        runtime's optimizer (rebuilt if either changed)."""
         inner = getattr(self.optimizer, "inner", None)
         if not isinstance(inner, FusedAdam):
             raise RuntimeError("the fused step needs the runtime's optimizer (GatedAdam over a FusedAdam)")
-        upd = self._update
-        if upd is None or upd.step is not self.step or upd.opt is not inner:
+        upd = self._updates.get(id(step))
+        if upd is None or upd.step is not step or upd.opt is not inner:
             core = self._core()
             pred = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
                     core.out_fc.bias]
-            upd = StepParamUpdate(self.step, inner, core.conv.kernel_params(), pred, [self.step.buf.any_edges, None])
-            self._update = upd
+            upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None])
+            self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
+            self._updates[id(step)] = upd
         elif upd.version != inner.state_version:
             upd.sync()
         return upd

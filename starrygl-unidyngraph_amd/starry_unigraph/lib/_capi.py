@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 19),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
+    "sgl_graph_pipeline": (ctypes.c_int, [_vp] * 7),
     "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 4 + [ctypes.c_float] * 5 + [_vp]),
 }
 

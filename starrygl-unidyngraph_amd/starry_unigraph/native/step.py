@@ -51,8 +51,16 @@ class NodeState:
             # node bitmap + its summary (layout owned by the library)
             self.node_bits = torch.zeros(int(_capi.lib().sgl_node_bits_words(self.N)), dtype=torch.int32, device=dev)
             self.word_prefix = torch.zeros((self.N + 31) // 32 + 3 & ~3, dtype=torch.int32, device=dev)
+        # count of writes queued by tensor code outside the fused step (a
+        # pipelined step orders itself after them when the count changes)
+        self.writes = 0
+
+    def touched(self) -> None:
+        """Record that tensor code queued writes to the state on the current stream."""
+        self.writes += 1
 
     def reset(self) -> None:
+        self.touched()
         self.memory.zero_()
         self.mailbox.zero_()
         self.mailbox_ts.zero_()
@@ -291,8 +299,8 @@ class DeviceStep:
 
 
 class StepParamUpdate:
-    """Weight gradients of the attention and Adam over the whole model in two
-    launches (sgl_adam_prepare, sgl_grad_adam). The job table points at the
+    """Weight gradients of the attention and Adam over the whole model in one
+    launch (sgl_grad_adam). The job table points at the
     step buffers and at the optimizer's flat buffers, so it is rebuilt when
     either is re-created. Segment 0 (the attention) is gated by the step's
     "block has edges" flag; segment 1 (the edge predictor) takes its
@@ -306,10 +314,10 @@ class StepParamUpdate:
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
-        self.done = torch.zeros(1, dtype=torch.int32, device=dev)
-        # bias corrections for each segment's next step (then kept current by
-        # the kernel): torch.optim.Adam's lr / (1 - b1^t), sqrt(1 - b2^t)
-        self.coef = torch.zeros(2 * len(opt.segments), dtype=torch.float32, device=dev)
+        # the completion counter and the bias corrections belong to the
+        # optimizer: every update over its segments (one per step buffer)
+        # advances the same step counts
+        self.done, self.coef = opt.done, opt.coef
         self.sync()
         jobs, tiles = self._jobs(conv_params, pred_params)
         arr = (_capi.GradJob * len(jobs))(*jobs)
@@ -452,6 +460,11 @@ class FusedAdam:
             self.segments.append((start, off - start, torch.zeros(1, dtype=torch.float32, device=dev)))
         self.params = params
         self.state_version = 0   # bumped when the step counts are restored
+        # fused-update state (sgl_grad_adam): a completion counter and, per
+        # segment, the bias corrections of its next step, torch.optim.Adam's
+        # lr / (1 - b1^t) and sqrt(1 - b2^t) (kept current by the kernel)
+        self.done = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.coef = torch.zeros(2 * len(self.segments), dtype=torch.float32, device=dev)
 
     def mark_state_changed(self) -> None:
         self.state_version += 1
@@ -470,6 +483,7 @@ class FusedAdam:
                                           P(self.exp_avg[start:start + n]), P(self.exp_avg_sq[start:start + n]),
                                           P(stepc), P(gate), self.lr, b1, b2, self.eps, self.wd, s), "sgl_adam_step")
             _capi.check(lib.sgl_adam_advance(P(stepc), P(gate), s), "sgl_adam_advance")
+        self.mark_state_changed()   # the fused update's bias corrections follow the new counts
 
     def state_dict(self) -> dict:
         return {"exp_avg": self.exp_avg.clone(), "exp_avg_sq": self.exp_avg_sq.clone(),

@@ -378,7 +378,53 @@ def test_graph_replay_matches_eager(gpu):
                 assert torch.equal(getattr(se, name), getattr(sg, name)), (name, msg)
             _close(sg.memory, se.memory, rtol=1e-5, atol=1e-6, msg=f"memory {msg}")
             _close(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat, rtol=0, atol=3 * lr, msg=f"params {msg}")
-    assert len(rt_g._graphs) == 2 and not rt_e._graphs
+    # per (split, train/eval, step buffer), captured on the key's second use:
+    # both training buffers, and the eval buffer that saw three batches
+    assert set(rt_g._graphs) == {("train", True, 0), ("train", True, 1), ("val", False, 1)}, set(rt_g._graphs)
+    assert not rt_e._graphs
+
+
+def test_pipelined_steps_match_eager(gpu):
+    """Consecutive graph steps in the asynchronous mode (collect_results off:
+    each step's front part, batch preparation + sampling + GRU, runs on a
+    second stream beside the previous step's back part) against eager steps
+    on the same batches and negatives, train then eval. The learning rate is
+    0, so both runs keep identical weights (with a nonzero rate the float
+    atomics of the gradient scatter make two runs drift apart, eager or not)
+    and every step is comparable: memory after each step, logits and, at the
+    end, mailbox, timestamps and slot pointers bit-exact; the loss (a float
+    atomic sum) within 1e-5; each step's gradients within 1e-5 of their
+    largest magnitude."""
+    _, rt_e, *_ = _runtime_pair(gpu, K=1, seed=7, lr=0.0, n_events=8000)
+    _, rt_g, *_ = _runtime_pair(gpu, K=1, seed=7, lr=0.0, n_events=8000)
+    rt_e.use_graphs, rt_g.use_graphs = False, True
+    rt_e.collect_results = rt_g.collect_results = False
+    for split, train in (("train", True), ("val", False)):
+        for rt in (rt_e, rt_g):
+            torch.manual_seed(21)
+            rt.precompute_negatives(split, 200)
+        res = {id(rt_e): [], id(rt_g): []}
+        for be, bg in zip(list(rt_e.iter_batches(split, 200)), list(rt_g.iter_batches(split, 200))):
+            for rt, b in ((rt_e, be), (rt_g, bg)):
+                out = rt.train_step(b) if train else rt.eval_step(b, split)
+                # clones on the step's stream: ordered after its commit and back part
+                res[id(rt)].append((out["loss"].clone(), out["pos_logits"].clone(), out["neg_logits"].clone(),
+                                    rt.memory.state.memory.clone(), rt.optimizer.inner.flat_grad.clone()))
+        torch.cuda.synchronize()
+        assert len(res[id(rt_g)]) >= 5 and rt_g._front_stream is not None
+        for i, (e, g) in enumerate(zip(res[id(rt_e)], res[id(rt_g)])):
+            msg = f"{split} batch {i}"
+            assert torch.equal(g[3], e[3]), f"memory {msg}"
+            assert torch.equal(g[1], e[1]) and torch.equal(g[2], e[2]), f"logits {msg}"
+            torch.testing.assert_close(g[0], e[0], rtol=1e-5, atol=1e-7, msg=f"loss {msg}")
+            if train:
+                scale = float(e[4].abs().max())
+                torch.testing.assert_close(g[4], e[4], rtol=0, atol=1e-5 * scale, msg=f"gradients {msg}")
+        se, sg = rt_e.memory.state, rt_g.memory.state
+        for name in ("mailbox", "mailbox_ts", "memory_ts", "next_mail_pos"):
+            assert torch.equal(getattr(se, name), getattr(sg, name)), (name, split)
+    assert torch.equal(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat)
+    assert {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)} <= set(rt_g._graphs)
 
 
 def test_fused_update_matches_torch_adam(gpu):
