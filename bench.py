@@ -249,6 +249,13 @@ def _restore(rt, snap):
     rt.fence()
 
 
+# step stage name -> the C-ABI entry point that launches it
+ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
+                "memory_update": "sgl_memory_update", "memory_commit": "sgl_memory_commit",
+                "conv_forward": "sgl_conv_forward", "predictor": "sgl_predictor",
+                "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam"}
+
+
 def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float]:
     """Algorithmic work of one launch: ("hbm", bytes) or ("mfma", flops)."""
     D, F, T, H, k, K = wl["D"], dims.F, wl["T"], wl["H"], wl["k"], wl["K"]
@@ -285,7 +292,7 @@ def run_tgn(args, wl: dict) -> dict:
     sess = build_session(wl, stream)
     rt = sess.ctdg_session.online_runtime
     rt.collect_results = False
-    rt.use_graphs = not args.no_graphs
+    rt.use_plans = not args.no_plans
     ep = Epochs(rt, wl["B"])
     dev = torch.device("cuda:0")
     for _ in range(args.warmup):
@@ -298,9 +305,27 @@ def run_tgn(args, wl: dict) -> dict:
     neg_state = dict(rt._neg_queue)
     dom = args.roofline_kernel
     timer: list = []
-    if args.no_graphs:   # eager steps: time the dominant kernel inside the timed region
+    if args.no_plans:   # eager steps: time the dominant kernel inside the timed region
         for st in rt.steps:
             st.timer, st.timed = timer, {dom}
+    else:   # planned steps: HIP events around the dominant kernel's launch in every 8th step
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range((args.steps + 7) // 8)]
+        for a, b in pairs:   # torch creates the HIP event at its first record
+            a.record()
+            b.record()
+        count = [0]
+
+        def next_pair():
+            i = count[0]
+            count[0] += 1
+            if i % 8:
+                return None
+            p = pairs[i // 8]
+            timer.append((dom, p[0], p[1]))
+            return p
+
+        rt.plan_timer = (ENTRY_POINTS[dom], next_pair)
     torch.cuda.synchronize()
     gc.collect()
     gc.disable()   # no collector pauses on the host inside the timed region
@@ -312,6 +337,7 @@ def run_tgn(args, wl: dict) -> dict:
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     gc.enable()
+    rt.plan_timer = None
     log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]
@@ -353,7 +379,7 @@ def run_tgn(args, wl: dict) -> dict:
                            "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5)}
     mean_U = sum(p[2] for p in per_step) / len(per_step)
     mean_E = sum(p[3] for p in per_step) / len(per_step)
-    if not dom_ms:   # graph-replayed timed region: the eager replay's launches of the same kernel
+    if not dom_ms:   # no timed launches in the timed region: the eager replay's
         dom_ms = agg[dom]
     dom_avg = sum(dom_ms) / max(1, len(dom_ms))
     bound = kernel_work(dom, wl, 1, 1, 1, rt.dims)[0]
@@ -428,7 +454,8 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--no-graphs", action="store_true", help="run steps eagerly instead of HIP-graph replays")
+    ap.add_argument("--no-plans", action="store_true",
+                    help="run steps eagerly (one library call at a time) instead of as recorded launch plans")
     ap.add_argument("--workload", default="tgn-large", choices=sorted(list(WORKLOADS) + ["sampler"]))
     ap.add_argument("--roofline-kernel", default="conv_backward",
                     choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "conv_forward",

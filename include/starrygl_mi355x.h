@@ -343,25 +343,46 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   float eps, float weight_decay, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
- * Two-stream submission of a training step from captured graphs. Replaces
- * the reference's per-step call sequence in CTDGOnlineRuntime.train_step
- * (backends/ctdg/runtime/runtime.py:225-328, which runs the stages one after
- * another on one stream) for consecutive full batches; no reference
- * counterpart exists for the overlap itself.
- * front_exec: batch preparation + sampling + GRU memory update of step t;
- * commit_exec: sgl_memory_commit of step t; back_exec: attention forward,
- * predictor, backward and sgl_grad_adam of step t (hipGraphExec_t handles).
- * Enqueues, without blocking the host:
- *   front: wait(committed), front_exec, record(fronted)
- *   back:  wait(fronted), commit_exec, record(committed), back_exec
- * so step t+1's front part overlaps step t's back part. Consecutive calls
- * must use graphs over different step buffers (ping-pong), and work queued
- * on the back stream between calls that the next front part depends on must
- * be published by recording `committed` on the back stream.
+ * Launch plans: a training step's calls of the entry points above, recorded
+ * once and replayed by one host call. Replaces the reference's per-step call
+ * sequence in CTDGOnlineRuntime.train_step / eval_step
+ * (backends/ctdg/runtime/runtime.py:225-386, the stages one after another on
+ * one stream) for consecutive full batches; the overlap of steps has no
+ * reference counterpart.
+ * An op is one call: kind = sgl_plan_op_kind(entry point name), nargs its
+ * argument count without the trailing stream, a[i] argument i (pointers and
+ * integers as their value, floats as their bit pattern in the low 32 bits).
+ * sgl_plan_run enqueues, without blocking the host, ops [0, n_front) (the
+ * step's front part: batch preparation, sampling, GRU), then n_commit ops
+ * (the memory commit), then n_back ops (attention, predictor, backward,
+ * Adam):
+ *   front stream: wait(committed), front ops, record(fronted)
+ *   back stream:  wait(fronted), commit ops, record(committed), back ops
+ * so step t+1's front part overlaps step t's back part. Consecutive runs must
+ * use different step buffers (ping-pong), and work queued on the back stream
+ * between runs that the next front part depends on is published by recording
+ * `committed` on the back stream. With n_commit == 0 every op runs in order on
+ * the back stream (front, committed and fronted are unused). An op's own
+ * checks run when it is replayed; the first failing op's error is returned
+ * (ops before it are already enqueued). timed_op >= 0 records t_start and
+ * t_end on that op's stream around it (-1: no timing).
  * ------------------------------------------------------------------------- */
-int sgl_graph_pipeline(void *front_exec, void *commit_exec, void *back_exec,
-                       hipStream_t front, hipStream_t back,
-                       hipEvent_t committed, hipEvent_t fronted);
+#define SGL_OP_MAX_ARGS 48
+
+typedef struct sgl_op {
+  int32_t kind;
+  int32_t nargs;
+  uint64_t a[SGL_OP_MAX_ARGS];
+} sgl_op;
+
+/* Kind of a plannable entry point ("sgl_conv_forward", ...), -1 if the name
+ * is not one; *nargs (may be NULL) receives its argument count without the
+ * stream. */
+int32_t sgl_plan_op_kind(const char *name, int32_t *nargs);
+int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit,
+                 int32_t n_back, hipStream_t front, hipStream_t back,
+                 hipEvent_t committed, hipEvent_t fronted, int32_t timed_op,
+                 hipEvent_t t_start, hipEvent_t t_end);
 
 #ifdef __cplusplus
 }

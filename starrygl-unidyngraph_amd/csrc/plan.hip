@@ -1,0 +1,135 @@
+// Launch plans: a training step's library calls recorded once (their
+// arguments are fixed device pointers and sizes: events are read at a device
+// cursor) and replayed with plain kernel launches by one host call.
+//
+// A plan is three runs of ops: the front part of a step (batch preparation,
+// sampling, GRU memory update), the memory commit, and the back part
+// (attention forward, edge predictor, backward, fused Adam). Step t+1's front
+// part only needs step t's commit (the memory table, the node bitmap) and,
+// with consecutive steps on different step buffers, reads nothing the back
+// part writes, so it runs on a second stream beside step t's back part:
+//
+//   front stream:  wait(committed) -> front ops -> record(fronted)
+//   back stream:   wait(fronted) -> commit ops -> record(committed) -> back ops
+//
+// Everything queued on the back stream before the commit (the previous back
+// part included) precedes the commit, so a front part never overlaps the back
+// part that still reads the buffers it is about to fill. Plain launches cost
+// the GPU well under a microsecond between kernels; the same kernels replayed
+// as graphs cost several, and more at graph boundaries.
+#include <cstring>
+#include <type_traits>
+#include <utility>
+
+#include "common.h"
+
+namespace {
+
+template <typename T>
+T from_slot(uint64_t v) {
+  if constexpr (std::is_pointer_v<T>) {
+    return reinterpret_cast<T>(static_cast<uintptr_t>(v));
+  } else if constexpr (std::is_same_v<T, float>) {
+    const uint32_t u = static_cast<uint32_t>(v);
+    float f;
+    std::memcpy(&f, &u, sizeof f);
+    return f;
+  } else {
+    static_assert(std::is_integral_v<T>, "plan slots hold pointers, integers and floats");
+    return static_cast<T>(v);
+  }
+}
+
+template <typename T, size_t I, size_t N>
+T arg_at(const uint64_t *a, hipStream_t s) {
+  if constexpr (I + 1 == N) {
+    static_assert(std::is_same_v<T, hipStream_t>, "a planned entry point takes the stream last");
+    return s;
+  } else {
+    return from_slot<T>(a[I]);
+  }
+}
+
+template <typename... Args, size_t... I>
+int invoke(int (*fn)(Args...), const uint64_t *a, hipStream_t s, std::index_sequence<I...>) {
+  return fn(arg_at<Args, I, sizeof...(Args)>(a, s)...);
+}
+
+template <typename... Args>
+constexpr int slots_of(int (*)(Args...)) {
+  return int(sizeof...(Args)) - 1;
+}
+
+template <auto Fn>
+int run_op(const uint64_t *a, hipStream_t s) {
+  return invoke(Fn, a, s, std::make_index_sequence<size_t(slots_of(Fn) + 1)>{});
+}
+
+struct OpEntry {
+  const char *name;
+  int (*run)(const uint64_t *, hipStream_t);
+  int slots;
+};
+
+#define SGL_OP(fn) {#fn, &run_op<&fn>, slots_of(&fn)}
+const OpEntry kOps[] = {
+    SGL_OP(sgl_batch_prepare), SGL_OP(sgl_recent_sample), SGL_OP(sgl_memory_update), SGL_OP(sgl_memory_commit),
+    SGL_OP(sgl_conv_forward),  SGL_OP(sgl_predictor),     SGL_OP(sgl_conv_backward), SGL_OP(sgl_grad_adam),
+};
+#undef SGL_OP
+constexpr int kNumOps = int(sizeof(kOps) / sizeof(kOps[0]));
+static_assert(kNumOps > 0, "op table");
+
+// Optional timing of one op: events recorded on its stream around it.
+struct OpTimer {
+  int op;
+  hipEvent_t start, end;
+};
+
+int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t) {
+  for (int i = 0; i < n; ++i) {
+    const sgl_op &op = ops[i];
+    SGL_REQUIRE(op.kind >= 0 && op.kind < kNumOps, "plan op %d: unknown kind %d", base + i, op.kind);
+    const OpEntry &e = kOps[op.kind];
+    SGL_REQUIRE(op.nargs == e.slots, "plan op %d (%s): %d arguments recorded, %d expected", base + i, e.name,
+                op.nargs, e.slots);
+    const bool timed = base + i == t.op;
+    if (timed) SGL_CHECK_HIP(hipEventRecord(t.start, s));
+    if (int rc = e.run(op.a, s)) return rc;
+    if (timed) SGL_CHECK_HIP(hipEventRecord(t.end, s));
+  }
+  return SGL_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
+  if (name == nullptr) return -1;
+  for (int k = 0; k < kNumOps; ++k)
+    if (std::strcmp(kOps[k].name, name) == 0) {
+      if (nargs != nullptr) *nargs = kOps[k].slots;
+      return k;
+    }
+  return -1;
+}
+
+extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit, int32_t n_back,
+                            hipStream_t front, hipStream_t back, hipEvent_t committed, hipEvent_t fronted,
+                            int32_t timed_op, hipEvent_t t_start, hipEvent_t t_end) {
+  SGL_REQUIRE(ops != nullptr || n_front + n_commit + n_back == 0, "plan_run: NULL ops");
+  SGL_REQUIRE(n_front >= 0 && n_commit >= 0 && n_back >= 0, "plan_run: negative op count");
+  SGL_REQUIRE(timed_op < 0 || (t_start && t_end), "plan_run: NULL timing event");
+  const OpTimer t{timed_op, t_start, t_end};
+  if (n_commit == 0) {  // no split point: everything in order on the back stream
+    return run_ops(ops, n_front + n_back, back, 0, t);
+  }
+  SGL_REQUIRE(committed && fronted, "plan_run: NULL event");
+  SGL_REQUIRE(front != back, "plan_run: the front and back streams must differ");
+  SGL_CHECK_HIP(hipStreamWaitEvent(front, committed, 0));
+  if (int rc = run_ops(ops, n_front, front, 0, t)) return rc;
+  SGL_CHECK_HIP(hipEventRecord(fronted, front));
+  SGL_CHECK_HIP(hipStreamWaitEvent(back, fronted, 0));
+  if (int rc = run_ops(ops + n_front, n_commit, back, n_front, t)) return rc;
+  SGL_CHECK_HIP(hipEventRecord(committed, back));
+  return run_ops(ops + n_front + n_commit, n_back, back, n_front + n_commit, t);
+}

@@ -62,18 +62,20 @@ class CTDGOnlineRuntime:
         self.dist_ctx = dist_ctx
         self.memory_updater = memory_updater
         self.collect_results = True
-        # Full-size batches of a contiguous split run as captured HIP graphs
-        # per (split, train/eval, step buffer); the graphs read the events at a
-        # device-side cursor and the negatives from a stream-wide array, so one
-        # capture replays for every batch. The first full batch of a kind runs
-        # eagerly. With a memory updater a step is three graphs (front part,
-        # memory commit, back part) submitted over two streams so that the
-        # next step's front part overlaps this step's back part
-        # (sgl_graph_pipeline); consecutive steps alternate between two sets
-        # of step buffers.
-        self.use_graphs = True
-        self._graphs: dict[tuple[str, bool, int], tuple] = {}
-        self._graph_seen: set[tuple[str, bool, int]] = set()
+        # Full-size batches of a contiguous split run as launch plans per
+        # (split, train/eval, step buffer): the step's library calls recorded
+        # once and replayed by one host call (sgl_plan_run). Plans read the
+        # events at a device-side cursor and the negatives from a stream-wide
+        # array, so one recording serves every batch. With a memory updater
+        # the next step's front part (batch preparation, sampling, GRU) runs on
+        # a second stream beside this step's back part (attention, predictor,
+        # backward, Adam); consecutive steps alternate between two sets of
+        # step buffers.
+        self.use_plans = True
+        self._plans: dict[tuple[str, bool, int], tuple] = {}
+        # optional per-op timing of planned steps: (entry point name, callable
+        # returning this step's (start, end) torch.cuda.Event pair or None)
+        self.plan_timer = None
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
         core = self._core()
@@ -83,7 +85,7 @@ class CTDGOnlineRuntime:
         self._make_steps(int(max_batch or 1))
         self._dev = dataset.device_arrays(self.device)
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
-        # graph replays read events and negatives at a device cursor that the
+        # planned steps read events and negatives at a device cursor that the
         # batch preparation advances; _cursor_host mirrors its value (None:
         # unknown) so it is only rewritten when batches are not consecutive
         self._cursor = torch.zeros(1, dtype=torch.int64, device=self.device)
@@ -205,7 +207,7 @@ class CTDGOnlineRuntime:
         n = batch.size
         if n > self.steps[0].buf.max_batch:
             self._make_steps(n)
-            self.reset_graphs()
+            self.reset_plans()
         if train:
             conv = self._core().conv
             if conv.dropout.p > 0 or conv.att_dropout.p > 0:
@@ -218,15 +220,14 @@ class CTDGOnlineRuntime:
         buf, off = self._negatives_at(batch)
         b = step.buf
         start = batch.start
-        graphable = (self.use_graphs and n == b.max_batch and start >= 0 and step.timer is None)
-        if not graphable:
+        planned = self.use_plans and n == b.max_batch and start >= 0 and step.timer is None
+        if not planned:
             src, dst, ts, ef = self._device_batch(batch)
             self._front_body(step, split, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
             self._commit_body(step)
             self._back_body(step, train, n)
             self.fence()
         else:
-            d = self._dev
             # the negatives must sit at the batch's place in the stream-wide array
             if off < 0 or buf.data_ptr() + 8 * off != self._neg_all_ptr + 8 * start:
                 self._neg_all[start:start + n].copy_(buf[off:off + n] if off >= 0 else buf)
@@ -241,57 +242,50 @@ class CTDGOnlineRuntime:
             if self.collect_results or self._state_writes != self.memory.state.writes:
                 self.fence()
             key = ("test" if split == "predict" else split, bool(train), q)
-            args = (step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"], self._cursor)
-            g = self._graphs.get(key)
-            if g is None and key in self._graph_seen:
-                g = self._capture(args, train)
-                self._graphs[key] = g
-            if g is None:
-                self._graph_seen.add(key)
-                self._front_body(*args)
-                self._commit_body(step)
-                self._back_body(step, train, n)
-                self.fence()
-            elif len(g) == 4:   # (front, commit, back) executables + the graphs that own them
-                front = self._pipeline_streams()
-                _capi.check(_capi.lib().sgl_graph_pipeline(
-                    g[0], g[1], g[2], front.cuda_stream, torch.cuda.current_stream(self.device).cuda_stream,
-                    self._ev_commit.cuda_event, self._ev_front.cuda_event), "sgl_graph_pipeline")
-            else:
-                g[0].replay()
+            plan = self._plans.get(key)
+            if plan is None:
+                plan = self._record(step, split, train, n)
+                self._plans[key] = plan
+                self.fence()   # state built on first use (a split's sampler graph) is queued here
+            front = self._pipeline_streams()
+            top, t0, t1 = -1, None, None
+            if self.plan_timer is not None:   # (entry point name, callback giving this step's event pair or None)
+                evs = self.plan_timer[1]()
+                if evs is not None:
+                    top = plan[4].index(self.plan_timer[0])
+                    t0, t1 = evs[0].cuda_event, evs[1].cuda_event
+            _capi.check(_capi.lib().sgl_plan_run(
+                plan[0], plan[1], plan[2], plan[3], front.cuda_stream,
+                torch.cuda.current_stream(self.device).cuda_stream, self._ev_commit.cuda_event,
+                self._ev_front.cuda_event, top, t0, t1), "sgl_plan_run")
         views = self._views.get((n, q))
         if views is None or views[0] is not b:
             views = (b, b.loss[0], b.pos[:n], b.neg[:n])
             self._views[(n, q)] = views
         return StepTensors(views[1], views[2], views[3], n)
 
-    def _capture(self, args, train: bool) -> tuple:
-        """Capture a full step: (front, commit, back) graph executables plus
-        the graphs, or (graph,) when there is no memory updater to split at."""
-        step = args[0]
+    def _record(self, step: DeviceStep, split: str, train: bool, n: int) -> tuple:
+        """Record a full step on ``step``'s buffers as a launch plan: (ops,
+        #front, #commit, #back, entry point names, recorded calls). Without a memory updater the
+        plan has no commit and runs in order on one stream."""
+        d = self._dev
         if train:
-            self._param_update(step)   # any rebuild or host-side sync happens before the capture
-        if self._gru is None:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                self._front_body(*args)
-                self._back_body(step, train, args[2])
-            return (g,)
-        gs = [torch.cuda.CUDAGraph() for _ in range(3)]
-        with torch.cuda.graph(gs[0]):
-            self._front_body(*args)
-        with torch.cuda.graph(gs[1]):
+            self._param_update(step)   # any rebuild or host-side sync happens outside the recording
+        with _capi.record() as front:
+            self._front_body(step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"],
+                             self._cursor)
+        with _capi.record() as commit:
             self._commit_body(step)
-        with torch.cuda.graph(gs[2]):
-            self._back_body(step, train, args[2])
-        return tuple(int(x.raw_cuda_graph_exec()) for x in gs) + (gs,)
+        with _capi.record() as back:
+            self._back_body(step, train, n)
+        calls = front + commit + back
+        return (_capi.pack_ops(calls), len(front), len(commit), len(back), [c[0] for c in calls], calls)
 
-    def reset_graphs(self) -> None:
-        """Drop captured step graphs (after buffers they reference change)."""
-        if self._ev_commit is not None:
+    def reset_plans(self) -> None:
+        """Drop recorded plans (after buffers they reference change)."""
+        if self._front_stream is not None:
             torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
-        self._graphs.clear()
-        self._graph_seen.clear()
+        self._plans.clear()
 
     def _front_body(self, step: DeviceStep, split: str, n: int, src, dst, neg, ts, ef, cursor) -> None:
         """Batch preparation, sampling and the GRU memory update of one step.

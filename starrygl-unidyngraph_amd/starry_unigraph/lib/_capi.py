@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 
 import torch  # loads the HIP runtime first, so the library binds to the same one
@@ -48,7 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 19),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
-    "sgl_graph_pipeline": (ctypes.c_int, [_vp] * 7),
+    "sgl_plan_op_kind": (_i32, [ctypes.c_char_p, _vp]),
+    "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp, _vp]),
     "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 4 + [ctypes.c_float] * 5 + [_vp]),
 }
 
@@ -122,6 +124,77 @@ class GradJob(ctypes.Structure):
     _fields_ = [("x1", _vp), ("x2", _vp), ("s1", _i64), ("s2", _i64), ("off", _i64),
                 ("ldo", _i32), ("rows", _i32), ("cols", _i32), ("kind", _i32), ("seg", _i32),
                 ("r_fixed", _i32), ("r_extra", _i32), ("tiles_b", _i32), ("tile0", _i32)]
+
+
+SGL_OP_MAX_ARGS = 48
+
+
+class Op(ctypes.Structure):
+    """struct sgl_op of include/starrygl_mi355x.h (one recorded call)."""
+    _fields_ = [("kind", _i32), ("nargs", _i32), ("a", ctypes.c_uint64 * SGL_OP_MAX_ARGS)]
+
+
+_recording: list | None = None
+
+
+class record:
+    """Within ``with record() as calls:``, :func:`call` appends (name, args
+    without the stream) to ``calls`` instead of launching."""
+
+    def __enter__(self) -> list:
+        global _recording
+        if _recording is not None:
+            raise RuntimeError("launch recordings do not nest")
+        _recording = []
+        return _recording
+
+    def __exit__(self, *exc) -> None:
+        global _recording
+        _recording = None
+
+
+def call(name: str, *args) -> int:
+    """Call entry point ``name`` (its arguments end with the stream), or
+    record the call when a recording is active (then 0 is returned; the
+    entry point's checks run when the plan is replayed)."""
+    rec = _recording
+    if rec is not None:
+        rec.append((name, args[:-1]))
+        return 0
+    return getattr(lib(), name)(*args)
+
+
+def _slot(v, t) -> int:
+    if v is None:
+        return 0
+    if t is ctypes.c_float:
+        return struct.unpack("<I", struct.pack("<f", float(v)))[0]
+    if t is _vp:
+        if isinstance(v, ctypes.Array):
+            return ctypes.addressof(v)
+        if isinstance(v, ctypes.c_void_p):
+            return v.value or 0
+        return int(v) & 0xFFFFFFFFFFFFFFFF
+    return int(v) & 0xFFFFFFFFFFFFFFFF
+
+
+def pack_ops(calls: list) -> ctypes.Array:
+    """Recorded calls -> an sgl_op array for sgl_plan_run (the recorded
+    arguments must stay alive, e.g. host pointer arrays, as long as it is
+    replayed)."""
+    L = lib()
+    ops = (Op * max(len(calls), 1))()
+    for i, (name, args) in enumerate(calls):
+        n = _i32(0)
+        kind = L.sgl_plan_op_kind(name.encode(), ctypes.byref(n))
+        argtypes = SIGNATURES[name][1][:-1]
+        if kind < 0 or n.value != len(argtypes) or len(args) != len(argtypes):
+            raise RuntimeError(f"{name}: not a plannable call ({len(args)} arguments recorded)")
+        ops[i].kind = kind
+        ops[i].nargs = n.value
+        for j, (v, t) in enumerate(zip(args, argtypes)):
+            ops[i].a[j] = _slot(v, t)
+    return ops
 
 
 class ErrorFlag:

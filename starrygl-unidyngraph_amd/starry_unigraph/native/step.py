@@ -183,7 +183,7 @@ class DeviceStep:
         n = src.numel() if n is None else int(n)
         if n > b.max_batch:
             raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
-        self._call("batch_prepare", lambda: _capi.check(self.lib.sgl_batch_prepare(
+        self._call("batch_prepare", lambda: _capi.check(_capi.call("sgl_batch_prepare", 
             st.N, n, P(src), P(dst), P(neg), P(ts), P(cursor), P(b.batch_start) if cursor is not None else None,
             P(st.node_bits), P(st.word_prefix), P(b.num_roots),
             P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
@@ -201,7 +201,7 @@ class DeviceStep:
         span the stream and the batch starts at buf.batch_start."""
         event_offset = self.buf.batch_start if from_cursor else None
         b, st, P = self.buf, self.state, _capi.ptr
-        self._call("memory_update", lambda: _capi.check(self.lib.sgl_memory_update(
+        self._call("memory_update", lambda: _capi.check(_capi.call("sgl_memory_update", 
             st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
             P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
             P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(event_offset),
@@ -210,7 +210,7 @@ class DeviceStep:
 
     def commit(self) -> None:
         b, st, P = self.buf, self.state, _capi.ptr
-        self._call("memory_commit", lambda: _capi.check(self.lib.sgl_memory_commit(
+        self._call("memory_commit", lambda: _capi.check(_capi.call("sgl_memory_commit", 
             st.D, b.cap, P(b.num_roots), P(b.roots), P(b.new_mem), P(st.memory), P(st.memory_ts), P(b.ts_max),
             P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
 
@@ -219,7 +219,7 @@ class DeviceStep:
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
-        self._call("conv_forward", lambda: _capi.check(self.lib.sgl_conv_forward(
+        self._call("conv_forward", lambda: _capi.check(_capi.call("sgl_conv_forward", 
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
             P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
             P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
@@ -235,7 +235,7 @@ class DeviceStep:
         are written for the attention backward and the weight reductions."""
         b, P = self.buf, _capi.ptr
         g = out_grads if (train and out_grads is not None) else [None, None]
-        self._call("predictor", lambda: _capi.check(self.lib.sgl_predictor(
+        self._call("predictor", lambda: _capi.check(_capi.call("sgl_predictor", 
             n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src), P(b.ridx_dst),
             P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]), P(b.pos),
             P(b.neg), P(b.loss), P(b.g_src) if train else None, P(b.g_dst) if train else None, P(g[0]), P(g[1]),
@@ -257,7 +257,7 @@ class DeviceStep:
         else:
             g_src, g_dst = b.g_src, b.g_dst
             w_s, w_d = pred_w
-        self._call("conv_backward", lambda: _capi.check(self.lib.sgl_conv_backward(
+        self._call("conv_backward", lambda: _capi.check(_capi.call("sgl_conv_backward", 
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
             P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
             P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
@@ -408,7 +408,7 @@ class StepParamUpdate:
         """Gradients + Adam (the gated step counts advance in the same launch)."""
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
         b1, b2 = opt.betas
-        self.step._call("param_update", lambda: _capi.check(self.lib.sgl_grad_adam(
+        self.step._call("param_update", lambda: _capi.check(_capi.call("sgl_grad_adam", 
             P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots), P(opt.flat),
             P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._steps, self._gates,
             P(self.coef), P(self.done), opt.lr, b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))

@@ -158,7 +158,7 @@ class RecentSampler:
                 q_ts=q_ts, fanout=fanout)
         g = self.g
         with torch.cuda.device(dev):
-            _capi.check(_capi.lib().sgl_recent_sample(
+            _capi.check(_capi.call("sgl_recent_sample", 
                 _capi.ptr(g.indptr), _capi.ptr(g.nbr), _capi.ptr(g.eid), _capi.ptr(g.ts), g.num_nodes,
                 _capi.ptr(nodes), 1 if nodes.dtype == torch.int64 else 0, _capi.ptr(q_ts), nq,
                 _capi.ptr(num_live), _capi.ptr(valid_cnt), int(stride), fanout,

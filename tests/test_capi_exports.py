@@ -85,3 +85,72 @@ def test_grad_job_struct_layout_matches_header(tmp_path):
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [ctypes.sizeof(_capi.GradJob)] + [getattr(_capi.GradJob, f).offset for f in fields]
     assert got == want
+
+
+def test_plan_op_struct_layout_matches_header(tmp_path):
+    """ctypes' Op has the size and field offsets of struct sgl_op."""
+    import ctypes
+    from starry_unigraph.lib import _capi
+    fields = [f for f, _ in _capi.Op._fields_]
+    src = tmp_path / "layout.cpp"
+    src.write_text(
+        '#include <cstdio>\n#include <cstddef>\n#include "starrygl_mi355x.h"\nint main() {\n'
+        '  printf("%zu %d", sizeof(sgl_op), SGL_OP_MAX_ARGS);\n'
+        + "".join(f'  printf(" %zu", offsetof(sgl_op, {f}));\n' for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(_capi.Op), _capi.SGL_OP_MAX_ARGS] + [getattr(_capi.Op, f).offset for f in fields]
+    assert got == want
+
+
+def test_plan_recording_and_packing():
+    """Recorded calls pack into sgl_op slots as the library's op table expects
+    (no launch: a recording intercepts the calls): every plannable entry point
+    is known to the library with the binding's argument count, pointers and
+    integers keep their value (negative integers in two's complement), floats
+    their bit pattern, host pointer arrays their address; unknown names are
+    rejected."""
+    import ctypes
+    import struct
+    from starry_unigraph.lib import _capi
+    L = _capi.lib()
+    plannable = ["sgl_batch_prepare", "sgl_recent_sample", "sgl_memory_update", "sgl_memory_commit",
+                 "sgl_conv_forward", "sgl_predictor", "sgl_conv_backward", "sgl_grad_adam"]
+    for name in plannable:
+        n = ctypes.c_int32(-1)
+        assert L.sgl_plan_op_kind(name.encode(), ctypes.byref(n)) >= 0, name
+        assert n.value == len(_capi.SIGNATURES[name][1]) - 1 <= _capi.SGL_OP_MAX_ARGS, name
+    assert L.sgl_plan_op_kind(b"sgl_tcsr_build", None) == -1
+    host_arr = (ctypes.c_void_p * 2)(0x1000, 0x2000)
+    types = _capi.SIGNATURES["sgl_grad_adam"][1]
+    args = []
+    for t in types[:-1]:
+        if t is ctypes.c_float:
+            args.append(0.125)
+        elif t is ctypes.c_int32:
+            args.append(-3)
+        else:
+            args.append(0xABC0)
+    args[9] = host_arr          # steps: a host array of device pointers
+    args[3] = None              # a NULL pointer
+    with _capi.record() as calls:
+        assert _capi.call("sgl_grad_adam", *args, 0xDEAD) == 0
+    assert len(calls) == 1 and calls[0][0] == "sgl_grad_adam" and len(calls[0][1]) == len(types) - 1
+    ops = _capi.pack_ops(calls)
+    op = ops[0]
+    assert op.kind == L.sgl_plan_op_kind(b"sgl_grad_adam", None) and op.nargs == len(types) - 1
+    for j, t in enumerate(types[:-1]):
+        if j == 9:
+            assert op.a[j] == ctypes.addressof(host_arr)
+        elif j == 3:
+            assert op.a[j] == 0
+        elif t is ctypes.c_float:
+            assert op.a[j] == struct.unpack("<I", struct.pack("<f", 0.125))[0]
+        elif t is ctypes.c_int32:
+            assert op.a[j] == (-3) & 0xFFFFFFFFFFFFFFFF
+        else:
+            assert op.a[j] == 0xABC0
+    with pytest.raises(RuntimeError):
+        _capi.pack_ops([("sgl_tcsr_build", (1, 2))])

@@ -346,8 +346,8 @@ def _step_state(rt):
             [opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments])
 
 
-def test_graph_replay_matches_eager(gpu):
-    """The captured-graph step (event cursor, staged negatives) against the
+def test_planned_steps_match_eager(gpu):
+    """The launch-plan step (event cursor, stream-wide negatives) against the
     eager step, each batch from identical state (train, then eval): mailbox,
     timestamps and slot pointers bit-exact; loss, logits and memory within
     1e-5; the Adam-updated parameters within 3 lr (the gradient scatter uses
@@ -355,7 +355,7 @@ def test_graph_replay_matches_eager(gpu):
     lr = 1e-3
     _, rt_e, *_ = _runtime_pair(gpu, K=1, seed=5, lr=lr)
     _, rt_g, *_ = _runtime_pair(gpu, K=1, seed=5, lr=lr)
-    rt_e.use_graphs, rt_g.use_graphs = False, True
+    rt_e.use_plans, rt_g.use_plans = False, True
     gen = torch.Generator().manual_seed(9)
     pool = rt_e.dataset.dst.unique()
     for split, train in (("train", True), ("val", False)):
@@ -378,10 +378,9 @@ def test_graph_replay_matches_eager(gpu):
                 assert torch.equal(getattr(se, name), getattr(sg, name)), (name, msg)
             _close(sg.memory, se.memory, rtol=1e-5, atol=1e-6, msg=f"memory {msg}")
             _close(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat, rtol=0, atol=3 * lr, msg=f"params {msg}")
-    # per (split, train/eval, step buffer), captured on the key's second use:
-    # both training buffers, and the eval buffer that saw three batches
-    assert set(rt_g._graphs) == {("train", True, 0), ("train", True, 1), ("val", False, 1)}, set(rt_g._graphs)
-    assert not rt_e._graphs
+    # one plan per (split, train/eval, step buffer)
+    assert set(rt_g._plans) == {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)}
+    assert not rt_e._plans
 
 
 def test_pipelined_steps_match_eager(gpu):
@@ -397,7 +396,7 @@ def test_pipelined_steps_match_eager(gpu):
     largest magnitude."""
     _, rt_e, *_ = _runtime_pair(gpu, K=1, seed=7, lr=0.0, n_events=8000)
     _, rt_g, *_ = _runtime_pair(gpu, K=1, seed=7, lr=0.0, n_events=8000)
-    rt_e.use_graphs, rt_g.use_graphs = False, True
+    rt_e.use_plans, rt_g.use_plans = False, True
     rt_e.collect_results = rt_g.collect_results = False
     for split, train in (("train", True), ("val", False)):
         for rt in (rt_e, rt_g):
@@ -424,7 +423,7 @@ def test_pipelined_steps_match_eager(gpu):
         for name in ("mailbox", "mailbox_ts", "memory_ts", "next_mail_pos"):
             assert torch.equal(getattr(se, name), getattr(sg, name)), (name, split)
     assert torch.equal(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat)
-    assert {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)} <= set(rt_g._graphs)
+    assert {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)} <= set(rt_g._plans)
 
 
 def test_fused_update_matches_torch_adam(gpu):
