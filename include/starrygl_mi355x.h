@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 2
+#define SGL_ABI_VERSION 3
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -213,7 +213,10 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * (may be NULL in a forward without backward); the backward reads it.
  * Backward takes dL/dy as gy [cap][D], or (gy NULL) as W_s^T g_src + W_d^T
  * g_dst from sgl_predictor's per-root rows and the predictor's src_fc /
- * dst_fc weights w_s, w_d [D][D], and writes gz, gagg [cap][D], G [cap][H][D+F+T],
+ * dst_fc weights w_s, w_d [D][D]: it reads the fixed-point accumulators
+ * acc_src / acc_dst [cap+1][D], writes their rows as floats to g_src / g_dst
+ * [cap+1][D] (for the src_fc / dst_fc weight reductions) and clears them for
+ * the next step. It writes gz, gagg [cap][D], G [cap][H][D+F+T],
  * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
  * tile partial sums ln_part [cap/R][2][D] (gamma, beta) and
  * te_part [cap/R][2][T] (time-encoding w, b; the b part includes the
@@ -252,12 +255,18 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       const float *sv_xbar, const float *sv_score,
                       const float *sv_ml, const float *sv_agg,
                       const float *sv_z, const float *sv_stats,
-                      const float *sv_trig,
-                      const float *gy, const float *g_src, const float *g_dst,
+                      const float *sv_trig, const float *gy,
+                      int64_t *acc_src, int64_t *acc_dst,
                       const float *w_s, const float *w_d,
+                      float *g_src, float *g_dst,
                       float *gz, float *gagg, float *G,
                       float *sigma, float *gQ, float *ln_part, float *te_part,
                       hipStream_t stream);
+
+/* Fractional bits of the fixed-point int64 accumulators (value = v * 2^-40)
+ * that sgl_predictor scatters into and sgl_conv_backward consumes: integer
+ * atomics make the sums independent of the order of the additions. */
+#define SGL_FIXED_SHIFT 40
 
 /* ---------------------------------------------------------------------------
  * Edge predictor + BCE, forward and (train != 0) backward.
@@ -267,13 +276,18 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
  * roots; ridx_* (from sgl_batch_prepare) pick each event's rows, -1 meaning
  * a zero embedding. Weights in nn.Linear layout: w_s, w_d [D][D], w_o [1][D].
  * Writes pos/neg logits [batch] and loss (mean BCE, pos label 1, neg 0).
- * With train it also writes (after zeroing them) the out_fc gradients
- * g_wo [D] and g_bo (= g_wo + D) and the per-root sums of the hidden-layer
- * gradients: g_src[r] = sum over events with root r as src of dL/dh_s,
- * g_dst[r] = the same for dst (dL/dh_d) and negatives (dL/dh_n); negatives
- * that are not roots add into row U = *num_roots. g_src / g_dst hold
- * capacity + 1 rows. The src_fc / dst_fc gradients follow as reductions over
- * rows 0..U (sgl_grad_adam jobs) and dL/dy through sgl_conv_backward.
+ * With train it also writes the out_fc gradients g_wo [D], g_bo [1] and adds
+ * the per-root sums of the hidden-layer gradients into the fixed-point
+ * accumulators acc_src / acc_dst [capacity+1][D] (SGL_FIXED_SHIFT; zero at
+ * entry, e.g. allocated zeroed and cleared by sgl_conv_backward, which
+ * consumes them): acc_src[r] = sum over events with root r as src of dL/dh_s,
+ * acc_dst[r] = the same for dst (dL/dh_d) and negatives (dL/dh_n); negatives
+ * that are not roots add into row U = *num_roots. The src_fc / dst_fc
+ * gradients follow as reductions over rows 0..U (sgl_grad_adam jobs) and
+ * dL/dy through sgl_conv_backward. acc_out (int64 [D+2]) and done (int32)
+ * are the launch's own accumulator and completion counter: zero before the
+ * first call, left zero by every call. All sums over events are exact integer
+ * sums, so results do not depend on the order of the workgroups.
  * ------------------------------------------------------------------------- */
 int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   const int32_t *num_roots, const float *y,
@@ -281,8 +295,9 @@ int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   const int32_t *ridx_neg, const float *w_s, const float *b_s,
                   const float *w_d, const float *b_d, const float *w_o,
                   const float *b_o, float *pos_logits, float *neg_logits,
-                  float *loss, float *g_src, float *g_dst, float *g_wo,
-                  float *g_bo, hipStream_t stream);
+                  float *loss, int64_t *acc_src, int64_t *acc_dst,
+                  float *g_wo, float *g_bo, int64_t *acc_out, int32_t *done,
+                  hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
@@ -367,7 +382,7 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
  * (ops before it are already enqueued). timed_op >= 0 records t_start and
  * t_end on that op's stream around it (-1: no timing).
  * ------------------------------------------------------------------------- */
-#define SGL_OP_MAX_ARGS 48
+#define SGL_OP_MAX_ARGS 64
 
 typedef struct sgl_op {
   int32_t kind;

@@ -499,15 +499,30 @@ inline size_t bwd_lds_floats(const Dims &d, int nw, bool slices) {
   return size_t(L.psig + (slices ? nw * d.H : 0) - base);
 }
 
+// The edge predictor's per-root gradient rows r0 .. r0+nrows-1 (fixed-point
+// accumulators): returned as floats in g_src / g_dst and cleared for the
+// next step.
+__device__ __forceinline__ void consume_rows(long long *__restrict__ acc_src, long long *__restrict__ acc_dst,
+                                             float *__restrict__ g_src, float *__restrict__ g_dst, int r0,
+                                             int nrows, int D, int tid, int nthreads) {
+  for (int idx = tid; idx < nrows * D; idx += nthreads) {
+    const size_t o = size_t(r0) * D + idx;
+    g_src[o] = sgl::from_fixed(acc_src[o]);
+    g_dst[o] = sgl::from_fixed(acc_dst[o]);
+    acc_src[o] = 0;
+    acc_dst[o] = 0;
+  }
+}
+
 template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ memory, const float *__restrict__ efeat,
     const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, const float *__restrict__ dt, ConvParams p,
-    ConvSaved sv, const float *__restrict__ gy, const float *__restrict__ g_src,
-    const float *__restrict__ g_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
-    ConvGrads g) {
+    ConvSaved sv, const float *__restrict__ gy, long long *__restrict__ acc_src,
+    long long *__restrict__ acc_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
+    float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;
   static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
@@ -522,11 +537,16 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   const int r0 = blockIdx.x * RPW;
   const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
+  // the accumulators' extra row (capacity: the non-root negatives when every
+  // row is a root) belongs to the last workgroup
+  if (gy == nullptr && blockIdx.x == gridDim.x - 1)
+    consume_rows(acc_src, acc_dst, g_src, g_dst, int(gridDim.x) * RPW, 1, D, tid, kBlock);
   if (nrows == 0 || !live) {
     for (int idx = tid; idx < RPW * D; idx += kBlock) {
       const size_t o = size_t(r0) * D + idx;
       g.gz[o] = 0.f; g.gagg[o] = 0.f; g.gQ[o] = 0.f;
     }
+    if (gy == nullptr) consume_rows(acc_src, acc_dst, g_src, g_dst, r0, RPW, D, tid, kBlock);
     for (int idx = tid; idx < RPW * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
     for (int idx = tid; idx < RPW * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
     for (int idx = tid; idx < 2 * D; idx += kBlock) g.ln_part[size_t(blockIdx.x) * 2 * D + idx] = 0.f;
@@ -549,8 +569,18 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   } else {
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
-      L.GA[i * L.ldr + j] = i < nrows ? g_src[size_t(r0 + i) * D + j] : 0.f;
-      L.GQ[i * L.ldr + j] = i < nrows ? g_dst[size_t(r0 + i) * D + j] : 0.f;
+      float vs = 0.f, vd = 0.f;
+      if (i < RPW) {  // the tile's rows (row U of the non-root negatives among them)
+        const size_t o = size_t(r0 + i) * D + j;
+        vs = sgl::from_fixed(acc_src[o]);
+        vd = sgl::from_fixed(acc_dst[o]);
+        acc_src[o] = 0;
+        acc_dst[o] = 0;
+        g_src[o] = vs;
+        g_dst[o] = vd;
+      }
+      L.GA[i * L.ldr + j] = i < nrows ? vs : 0.f;
+      L.GQ[i * L.ldr + j] = i < nrows ? vd : 0.f;
     }
     __syncthreads();
     sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves);
@@ -920,17 +950,18 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                                  const float *b_out, const float *ln_g, const float *ln_b, const float *te_w,
                                  const float *te_b, const float *sv_Q, const float *sv_qt, const float *sv_xbar,
                                  const float *sv_score, const float *sv_ml, const float *sv_agg, const float *sv_z,
-                                 const float *sv_stats, const float *sv_trig, const float *gy, const float *g_src,
-                                 const float *g_dst,
-                                 const float *w_s, const float *w_d, float *gz, float *gagg, float *G,
-                                 float *sigma, float *gQ, float *ln_part, float *te_part, hipStream_t stream) {
+                                 const float *sv_stats, const float *sv_trig, const float *gy, int64_t *acc_src,
+                                 int64_t *acc_dst, const float *w_s, const float *w_d, float *g_src, float *g_dst,
+                                 float *gz, float *gagg, float *G, float *sigma, float *gQ, float *ln_part,
+                                 float *te_part, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
   SGL_REQUIRE(num_roots && any_edges && memory && cnt && w_q && w_k && b_k && w_v && w_out && ln_g && te_w && te_b &&
-                  sv_qt && sv_xbar && sv_ml && sv_z && sv_stats && (gy || (g_src && g_dst && w_s && w_d)) && gz &&
+                  sv_qt && sv_xbar && sv_ml && sv_z && sv_stats &&
+                  (gy || (acc_src && acc_dst && w_s && w_d && g_src && g_dst)) && gz &&
                   gagg && G && sigma && gQ && ln_part &&
                   te_part && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score && sv_trig)),
               "conv_backward: NULL array");
@@ -945,7 +976,8 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr, const_cast<float *>(sv_trig)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
   inst.fn<<<unsigned(capacity / inst.rows), unsigned(inst.waves * 64), lds, stream>>>(
-      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, g_src, g_dst, w_s, w_d, g);
+      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, reinterpret_cast<long long *>(acc_src),
+      reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst, g);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

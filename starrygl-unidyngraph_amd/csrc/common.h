@@ -67,6 +67,20 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
          __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
 }
 
+// Fixed-point accumulation (SGL_FIXED_SHIFT fractional bits in an int64):
+// integer atomics are exact, so sums scattered by many workgroups do not
+// depend on the order the additions happen in. Values are clamped to the
+// int64 range; magnitudes stay far below it for the gradients summed here.
+__device__ __forceinline__ long long to_fixed(float x) {
+  const float s = x * 0x1p40f;
+  return static_cast<long long>(rintf(fminf(fmaxf(s, -9.0e18f), 9.0e18f)));
+}
+__device__ __forceinline__ float from_fixed(long long v) { return float(double(v) * 0x1p-40); }
+__device__ __forceinline__ void atomic_add_fixed(long long *p, long long v) {
+  atomicAdd(reinterpret_cast<unsigned long long *>(p), static_cast<unsigned long long>(v));
+}
+static_assert(SGL_FIXED_SHIFT == 40, "to_fixed / from_fixed scale");
+
 template <typename T>
 __device__ __forceinline__ T wave_reduce_sum(T v) {
 #pragma unroll

@@ -7,14 +7,19 @@
 //   h_s = W_s e_s + b_s, h_d = W_d e_d + b_d, h_n = W_d e_n + b_d
 //   pos = w_o . relu(h_s + h_d) + b_o,  neg = w_o . relu(h_s + h_n) + b_o
 //   loss = mean softplus(-pos) + mean softplus(neg)  (BCE with logits, labels 1 / 0)
-// In training mode the launch also produces the out_fc gradients (atomics
-// into caller buffers) and, per root r, the summed hidden-layer gradients
+// In training mode the launch also produces the out_fc gradients and, per
+// root r, the summed hidden-layer gradients
 //   g_src[r] = sum_{e: rs[e] = r} dL/dh_s[e]
 //   g_dst[r] = sum_{e: rd[e] = r} dL/dh_d[e] + sum_{e: rn[e] = r} dL/dh_n[e]
 // with the negatives that are not roots summed into row U of g_dst. From
 // these rows the attention backward gets dL/dy = W_s^T g_src + W_d^T g_dst,
 // and the src_fc / dst_fc gradients are reductions over the roots
 // (dW_s = sum_r g_src[r] y[r]^T, db_d = sum_{r <= U} g_dst[r], ...).
+// Every sum over events is accumulated in fixed point with integer atomics
+// (exact, so independent of the workgroups' order): the per-root rows in the
+// caller's accumulators (consumed and cleared by the attention backward), the
+// loss and out_fc gradients in a small accumulator that the last workgroup to
+// finish converts into the float outputs and clears.
 #include <climits>
 
 #include "common.h"
@@ -51,18 +56,20 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     const float *__restrict__ w_s, const float *__restrict__ b_s, const float *__restrict__ w_d,
     const float *__restrict__ b_d, const float *__restrict__ w_o, const float *__restrict__ b_o,
     float *__restrict__ pos_out, float *__restrict__ neg_out, float *__restrict__ loss,
-    float *__restrict__ g_src, float *__restrict__ g_dst, float *__restrict__ g_wo, float *__restrict__ g_bo) {
-  extern __shared__ float lds[];
+    long long *__restrict__ acc_src, long long *__restrict__ acc_dst, float *__restrict__ g_wo,
+    float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done) {
+  extern __shared__ __align__(16) float lds[];
   const int ld = D + 1;
-  float *Es = lds;
+  long long *Nul = reinterpret_cast<long long *>(lds);  // [D] dL/dh_n of the tile's non-root negatives
+  float *Es = lds + 2 * ((D + 1) & ~1);
   float *Ed = Es + kRows * ld;
   float *En = Ed + kRows * ld;
   float *Hs = En + kRows * ld;   // h_s
   float *Hd = Hs + kRows * ld;   // h_d -> a_p
   float *Hn = Hd + kRows * ld;   // h_n -> a_n
-  float *Nul = Hn + kRows * ld;  // [D] dL/dh_n of the tile's non-root negatives
-  __shared__ float s_gp[kRows], s_gn[kRows];
+  __shared__ float s_gp[kRows], s_gn[kRows], s_sp[kRows];
   __shared__ int s_idx[3][kRows];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t e0 = int64_t(blockIdx.x) * kRows;
@@ -73,7 +80,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     s_idx[1][tid] = ok ? rd[e0 + tid] : -1;
     s_idx[2][tid] = ok ? rn[e0 + tid] : -1;
   }
-  for (int j = tid; j < D; j += kBlock) Nul[j] = 0.f;
+  for (int j = tid; j < D; j += kBlock) Nul[j] = 0;
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
@@ -89,7 +96,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
   }
   __syncthreads();
-  // logits, loss, logit gradients: one wave per event
+  // logits, loss terms, logit gradients: one wave per event
   for (int i = wave; i < kRows; i += kWaves) {
     float pp = 0.f, pn = 0.f;
     for (int j = lane; j < D; j += 64) {
@@ -104,48 +111,78 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     pp = sgl::wave_sum_dpp(pp);
     pn = sgl::wave_sum_dpp(pn);
     if (lane == 0) {
-      float gp = 0.f, gn = 0.f;
+      float gp = 0.f, gn = 0.f, sp = 0.f;
       if (i < nrows) {
         const float p = pp + b_o[0], n = pn + b_o[0];
         pos_out[e0 + i] = p;
         neg_out[e0 + i] = n;
-        atomicAdd(loss, (softplus(-p) + softplus(n)) / float(batch));
+        sp = softplus(-p) + softplus(n);
         gp = (sigmoid(p) - 1.f) / float(batch);
         gn = sigmoid(n) / float(batch);
       }
       s_gp[i] = gp;
       s_gn[i] = gn;
+      s_sp[i] = sp;
     }
   }
-  if (!train) return;  // uniform
   __syncthreads();
-  // out_fc gradients
-  for (int j = tid; j < D; j += kBlock) {
-    float gw = 0.f;
-    for (int i = 0; i < kRows; ++i) gw += s_gp[i] * Hd[i * ld + j] + s_gn[i] * Hn[i * ld + j];
-    atomicAdd(&g_wo[j], gw);
+  if (tid == 0) {
+    float sp = 0.f;
+    for (int i = 0; i < kRows; ++i) sp += s_sp[i];
+    sgl::atomic_add_fixed(&acc_out[D + 1], sgl::to_fixed(sp));
+  }
+  if (train) {  // uniform
+    // out_fc gradients: this tile's sums
+    for (int j = tid; j < D; j += kBlock) {
+      float gw = 0.f;
+      for (int i = 0; i < kRows; ++i) gw += s_gp[i] * Hd[i * ld + j] + s_gn[i] * Hn[i * ld + j];
+      sgl::atomic_add_fixed(&acc_out[j], sgl::to_fixed(gw));
+    }
+    if (tid == 64) {
+      float gb = 0.f;
+      for (int i = 0; i < kRows; ++i) gb += s_gp[i] + s_gn[i];
+      sgl::atomic_add_fixed(&acc_out[D], sgl::to_fixed(gb));
+    }
+    // hidden-layer gradients, summed into their roots' rows
+    const int U = *num_roots;
+    for (int idx = tid; idx < kRows * D; idx += kBlock) {
+      const int i = idx / D, j = idx - i * D;
+      if (i >= nrows) continue;
+      const float ghp = Hd[i * ld + j] > 0.f ? s_gp[i] * w_o[j] : 0.f;
+      const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * w_o[j] : 0.f;
+      const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
+      const long long fp = sgl::to_fixed(ghp), fn = sgl::to_fixed(ghn);
+      if (a >= 0) sgl::atomic_add_fixed(&acc_src[size_t(a) * D + j], fp + fn);
+      if (b >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(b) * D + j], fp);
+      if (c >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(c) * D + j], fn);
+      else if (fn != 0) atomicAdd(reinterpret_cast<unsigned long long *>(&Nul[j]), static_cast<unsigned long long>(fn));
+    }
+    __syncthreads();
+    for (int j = tid; j < D; j += kBlock)
+      if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_dst[size_t(U) * D + j], Nul[j]);
+  }
+  // the last workgroup to finish turns the accumulated sums into the outputs
+  // and clears the accumulator and the counter for the next launch. The sums
+  // only ever change by atomics, which are performed at the device's
+  // coherence point: a workgroup waits for its own atomics to complete
+  // before it counts itself done, and the last one reads the sums with
+  // atomics too, so no cache writeback is needed.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) s_last = atomicAdd(done, 1) == int(gridDim.x) - 1;
+  __syncthreads();
+  if (!s_last) return;
+  auto take = [&](int k) {
+    return sgl::from_fixed(static_cast<long long>(atomicExch(reinterpret_cast<unsigned long long *>(&acc_out[k]), 0ull)));
+  };
+  if (train) {
+    for (int j = tid; j < D; j += kBlock) g_wo[j] = take(j);
+    if (tid == 64) g_bo[0] = take(D);
   }
   if (tid == 0) {
-    float gb = 0.f;
-    for (int i = 0; i < kRows; ++i) gb += s_gp[i] + s_gn[i];
-    atomicAdd(g_bo, gb);
+    *loss = float(double(take(D + 1)) / double(batch));
+    atomicExch(done, 0);
   }
-  // hidden-layer gradients, summed into their roots' rows
-  const int U = *num_roots;
-  for (int idx = tid; idx < kRows * D; idx += kBlock) {
-    const int i = idx / D, j = idx - i * D;
-    if (i >= nrows) continue;
-    const float ghp = Hd[i * ld + j] > 0.f ? s_gp[i] * w_o[j] : 0.f;
-    const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * w_o[j] : 0.f;
-    const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
-    if (a >= 0) atomicAdd(&g_src[size_t(a) * D + j], ghp + ghn);
-    if (b >= 0) atomicAdd(&g_dst[size_t(b) * D + j], ghp);
-    if (c >= 0) atomicAdd(&g_dst[size_t(c) * D + j], ghn);
-    else atomicAdd(&Nul[j], ghn);
-  }
-  __syncthreads();
-  for (int j = tid; j < D; j += kBlock)
-    if (Nul[j] != 0.f) atomicAdd(&g_dst[size_t(U) * D + j], Nul[j]);
 }
 
 }  // namespace
@@ -154,27 +191,26 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
                              const float *y, const int32_t *ridx_src, const int32_t *ridx_dst, const int32_t *ridx_neg,
                              const float *w_s, const float *b_s, const float *w_d, const float *b_d,
                              const float *w_o, const float *b_o, float *pos_logits, float *neg_logits, float *loss,
-                             float *g_src, float *g_dst, float *g_wo, float *g_bo, hipStream_t stream) {
+                             int64_t *acc_src, int64_t *acc_dst, float *g_wo, float *g_bo, int64_t *acc_out,
+                             int32_t *done, hipStream_t stream) {
   SGL_REQUIRE(batch >= 0 && batch < INT_MAX && D > 0 && capacity >= 0, "predictor: bad sizes");
   SGL_REQUIRE(num_roots && y && ridx_src && ridx_dst && ridx_neg && w_s && b_s && w_d && b_d && w_o && b_o &&
-                  pos_logits && neg_logits && loss,
+                  pos_logits && neg_logits && loss && acc_out && done,
               "predictor: NULL array");
-  SGL_REQUIRE(!train || (g_src && g_dst && g_wo && g_bo), "predictor: NULL gradient array");
-  SGL_REQUIRE(!train || g_bo == g_wo + D, "predictor: g_bo must follow g_wo (out_fc weight, then bias)");
-  // g_src / g_dst hold capacity + 1 rows (row U <= capacity collects the
-  // non-root negatives); g_wo, g_bo are D + 1 contiguous floats
-  const int64_t nz = train ? (capacity + 1) * D : 0;
-  const ZeroSpans z{{g_src, g_dst, g_wo, loss}, {nz, nz, train ? D + 1 : 0, 1}};
-  const int64_t nb = nz > D + 1 ? nz : D + 1;
-  k_zero<<<unsigned((nb + 255) / 256), 256, 0, stream>>>(z);
-  SGL_CHECK_LAUNCH();
-  if (batch == 0) return SGL_OK;
-  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + D);
+  SGL_REQUIRE(!train || (acc_src && acc_dst && g_wo && g_bo), "predictor: NULL gradient array");
+  if (batch == 0) {  // no events: zero loss and out_fc gradients
+    const ZeroSpans z{{loss, train ? g_wo : nullptr, train ? g_bo : nullptr, nullptr}, {1, train ? D : 0, train, 0}};
+    k_zero<<<unsigned((D + 255) / 256), 256, 0, stream>>>(z);
+    SGL_CHECK_LAUNCH();
+    return SGL_OK;
+  }
+  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + 2 * ((D + 1) & ~1));
   SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
   k_predictor<<<unsigned((batch + kRows - 1) / kRows), kBlock, lds, stream>>>(
       batch, D, train, num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits,
-      neg_logits, loss, g_src, g_dst, g_wo, g_bo);
+      neg_logits, loss, reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
+      reinterpret_cast<long long *>(acc_out), done);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

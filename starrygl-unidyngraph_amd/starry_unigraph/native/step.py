@@ -9,9 +9,13 @@ backends/ctdg/runtime/runtime.py:225-297):
   sgl_memory_update   GRU over mailbox + memory, mailbox write     (runtime.py:268-282)
   sgl_memory_commit   memory/memory_ts scatter                     (memory.py:254-269)
   sgl_conv_forward    time encoding + temporal attention           (models.py:77-137)
-  (predictor + BCE in torch autograd)                              (models.py:313-324, runtime.py:290-292)
-  sgl_conv_backward   attention backward; weight-gradient GEMMs
-  sgl_adam_step       Adam, the attention segment gated by "block has edges"
+  sgl_predictor       edge predictor + BCE, per-root gradient sums (models.py:313-324, runtime.py:290-292)
+  sgl_conv_backward   attention backward                           (loss.backward(), runtime.py:296)
+  sgl_grad_adam       weight gradients + Adam, the attention segment
+                      gated by "block has edges"                   (optimizer.step(), runtime.py:297)
+
+The first three are a step's front part, the memory commit its split point,
+the rest its back part (see the runtime's launch plans).
 """
 from __future__ import annotations
 
@@ -127,8 +131,13 @@ class StepBuffers:
         self.trig = z(max(c * k * 2 * dims.T, 1))   # each sampled edge's time-encoding cos, sin
         self.gy = z(c, D)
         # per-root sums of the predictor's hidden-layer gradients (+ the
-        # non-root-negatives row U)
+        # non-root-negatives row U): fixed-point accumulators the predictor
+        # adds into and the attention backward clears (zero between steps),
+        # and their float values for the weight reductions
+        self.acc_src, self.acc_dst = z(c + 1, D, dt=i64), z(c + 1, D, dt=i64)
         self.g_src, self.g_dst = z(c + 1, D), z(c + 1, D)
+        self.acc_out = z(D + 2, dt=i64)      # the predictor's loss / out_fc accumulator
+        self.pred_done = z(1, dt=i32)        # and its completion counter
         self.pos = z(max(B, 1))
         self.neg = z(max(B, 1))
         self.loss = z(1)
@@ -231,15 +240,16 @@ class DeviceStep:
         """Edge predictor + BCE over the step's roots (sgl_predictor). ``pred``:
         src_fc.weight, src_fc.bias, dst_fc.weight, dst_fc.bias, out_fc.weight,
         out_fc.bias; ``out_grads``: the out_fc weight / bias gradient buffers
-        (contiguous; overwritten). In training the per-root rows g_src / g_dst
-        are written for the attention backward and the weight reductions."""
+        (overwritten). In training the per-root gradient sums are added into
+        the step's fixed-point accumulators, which the attention backward
+        (conv_backward_kernel) consumes and clears."""
         b, P = self.buf, _capi.ptr
         g = out_grads if (train and out_grads is not None) else [None, None]
-        self._call("predictor", lambda: _capi.check(_capi.call("sgl_predictor", 
-            n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src), P(b.ridx_dst),
-            P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]), P(b.pos),
-            P(b.neg), P(b.loss), P(b.g_src) if train else None, P(b.g_dst) if train else None, P(g[0]), P(g[1]),
-            self._s()), "sgl_predictor"))
+        self._call("predictor", lambda: _capi.check(_capi.call(
+            "sgl_predictor", n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src),
+            P(b.ridx_dst), P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]),
+            P(b.pos), P(b.neg), P(b.loss), P(b.acc_src) if train else None, P(b.acc_dst) if train else None,
+            P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
     def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor,
@@ -253,16 +263,16 @@ class DeviceStep:
         hop = b.hop
         if gy is not None:
             gy = gy.contiguous()
-            g_src = g_dst = w_s = w_d = None
+            acc_src = acc_dst = g_src = g_dst = w_s = w_d = None
         else:
-            g_src, g_dst = b.g_src, b.g_dst
+            acc_src, acc_dst, g_src, g_dst = b.acc_src, b.acc_dst, b.g_src, b.g_dst
             w_s, w_d = pred_w
         self._call("conv_backward", lambda: _capi.check(_capi.call("sgl_conv_backward", 
             d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
             P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
             P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
-            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.trig), P(gy), P(g_src), P(g_dst), P(w_s), P(w_d), P(b.gz),
-            P(b.gagg),
+            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.trig), P(gy), P(acc_src), P(acc_dst), P(w_s), P(w_d),
+            P(g_src), P(g_dst), P(b.gz), P(b.gagg),
             P(b.G), P(b.sigma), P(b.gQ),
             P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
 
