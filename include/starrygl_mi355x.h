@@ -370,17 +370,22 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
  * sgl_plan_run enqueues, without blocking the host, ops [0, n_front) (the
  * step's front part: batch preparation, sampling, GRU), then n_commit ops
  * (the memory commit), then n_back ops (attention, predictor, backward,
- * Adam):
- *   front stream: wait(committed), front ops, record(fronted)
- *   back stream:  wait(fronted), commit ops, record(committed), back ops
- * so step t+1's front part overlaps step t's back part. Consecutive runs must
- * use different step buffers (ping-pong), and work queued on the back stream
- * between runs that the next front part depends on is published by recording
- * `committed` on the back stream. With n_commit == 0 every op runs in order on
- * the back stream (front, committed and fronted are unused). An op's own
- * checks run when it is replayed; the first failing op's error is returned
- * (ops before it are already enqueued). timed_op >= 0 records t_start and
- * t_end on that op's stream around it (-1: no timing).
+ * Adam), ordering the two streams through the device words sync[0] (last
+ * commit) and sync[16] (last front part), uint32 in device memory, zero
+ * before the first run:
+ *   front stream: wait until sync[0] >= seq-1, front ops, write sync[16] = seq
+ *   back stream:  wait until sync[16] >= seq, commit ops, write sync[0] = seq,
+ *                 back ops
+ * so step t+1's front part overlaps step t's back part. seq increases by one
+ * per run (from 1); consecutive runs must use different step buffers
+ * (ping-pong). Work queued on the back stream between runs that the next
+ * front part depends on is published by writing sync[0] = seq on the back
+ * stream after it and running the next plan with seq + 1 (a fence). With
+ * n_commit == 0 every op runs in order on the back stream (front, sync and
+ * seq are unused). An op's own checks run when it is replayed; the first
+ * failing op's error is returned (ops before it are already enqueued).
+ * timed_op >= 0 records t_start and t_end on that op's stream around it
+ * (-1: no timing).
  * ------------------------------------------------------------------------- */
 #define SGL_OP_MAX_ARGS 64
 
@@ -396,7 +401,7 @@ typedef struct sgl_op {
 int32_t sgl_plan_op_kind(const char *name, int32_t *nargs);
 int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit,
                  int32_t n_back, hipStream_t front, hipStream_t back,
-                 hipEvent_t committed, hipEvent_t fronted, int32_t timed_op,
+                 uint32_t *sync, uint32_t seq, int32_t timed_op,
                  hipEvent_t t_start, hipEvent_t t_end);
 
 #ifdef __cplusplus

@@ -7,16 +7,20 @@
 // (attention forward, edge predictor, backward, fused Adam). Step t+1's front
 // part only needs step t's commit (the memory table, the node bitmap) and,
 // with consecutive steps on different step buffers, reads nothing the back
-// part writes, so it runs on a second stream beside step t's back part:
+// part writes, so it runs on a second stream beside step t's back part. The
+// two streams order themselves through two device words (stream memory
+// operations: a write after the stream's prior work, a wait that holds the
+// stream until the word reaches a value):
 //
-//   front stream:  wait(committed) -> front ops -> record(fronted)
-//   back stream:   wait(fronted) -> commit ops -> record(committed) -> back ops
+//   front stream:  wait(sync[0] >= seq-1) -> front ops -> write(sync[16] = seq)
+//   back stream:   wait(sync[16] >= seq) -> commit ops -> write(sync[0] = seq) -> back ops
 //
 // Everything queued on the back stream before the commit (the previous back
 // part included) precedes the commit, so a front part never overlaps the back
 // part that still reads the buffers it is about to fill. Plain launches cost
 // the GPU well under a microsecond between kernels; the same kernels replayed
-// as graphs cost several, and more at graph boundaries.
+// as graphs cost several, and more at graph boundaries; stream memory
+// operations resolve faster than events between streams.
 #include <cstring>
 #include <type_traits>
 #include <utility>
@@ -114,8 +118,8 @@ extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
 }
 
 extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit, int32_t n_back,
-                            hipStream_t front, hipStream_t back, hipEvent_t committed, hipEvent_t fronted,
-                            int32_t timed_op, hipEvent_t t_start, hipEvent_t t_end) {
+                            hipStream_t front, hipStream_t back, uint32_t *sync, uint32_t seq, int32_t timed_op,
+                            hipEvent_t t_start, hipEvent_t t_end) {
   SGL_REQUIRE(ops != nullptr || n_front + n_commit + n_back == 0, "plan_run: NULL ops");
   SGL_REQUIRE(n_front >= 0 && n_commit >= 0 && n_back >= 0, "plan_run: negative op count");
   SGL_REQUIRE(timed_op < 0 || (t_start && t_end), "plan_run: NULL timing event");
@@ -123,13 +127,14 @@ extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit
   if (n_commit == 0) {  // no split point: everything in order on the back stream
     return run_ops(ops, n_front + n_back, back, 0, t);
   }
-  SGL_REQUIRE(committed && fronted, "plan_run: NULL event");
+  SGL_REQUIRE(sync != nullptr && seq > 0, "plan_run: NULL sync words or sequence number 0");
   SGL_REQUIRE(front != back, "plan_run: the front and back streams must differ");
-  SGL_CHECK_HIP(hipStreamWaitEvent(front, committed, 0));
+  uint32_t *committed = sync, *fronted = sync + 16;  // separate 64-byte lines
+  SGL_CHECK_HIP(hipStreamWaitValue32(front, committed, seq - 1, hipStreamWaitValueGte, 0xffffffffu));
   if (int rc = run_ops(ops, n_front, front, 0, t)) return rc;
-  SGL_CHECK_HIP(hipEventRecord(fronted, front));
-  SGL_CHECK_HIP(hipStreamWaitEvent(back, fronted, 0));
+  SGL_CHECK_HIP(hipStreamWriteValue32(front, fronted, seq, 0));
+  SGL_CHECK_HIP(hipStreamWaitValue32(back, fronted, seq, hipStreamWaitValueGte, 0xffffffffu));
   if (int rc = run_ops(ops + n_front, n_commit, back, n_front, t)) return rc;
-  SGL_CHECK_HIP(hipEventRecord(committed, back));
+  SGL_CHECK_HIP(hipStreamWriteValue32(back, committed, seq, 0));
   return run_ops(ops + n_front + n_commit, n_back, back, n_front + n_commit, t);
 }

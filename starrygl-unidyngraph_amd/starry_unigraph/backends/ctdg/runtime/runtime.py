@@ -95,13 +95,15 @@ class CTDGOnlineRuntime:
         self._views: dict[tuple[int, int], tuple] = {}
         self._updates: dict[int, StepParamUpdate] = {}
         # two-stream submission: the front stream runs batch preparation,
-        # sampling and the GRU; the caller's current stream the rest.
-        # _ev_commit marks what the next front part must wait for (the last
-        # commit, or everything queued before a fence), _ev_front the end of
-        # the last front part.
+        # sampling and the GRU; the caller's current stream the rest. The
+        # streams order themselves through two device words (sgl_plan_run):
+        # _sync[0] holds the sequence number of the last commit or fence,
+        # _sync[16] that of the last front part; _seq is the last number used.
         self._front_stream: torch.cuda.Stream | None = None
-        self._ev_commit: torch.cuda.Event | None = None
-        self._ev_front: torch.cuda.Event | None = None
+        self._sync = torch.zeros(32, dtype=torch.int32, device=self.device)
+        self._sync_ptr = self._sync.data_ptr()
+        self._sync_committed = self._sync[0:1]
+        self._seq = 0
         self._state_writes = memory.state.writes
 
     def _make_steps(self, max_batch: int) -> None:
@@ -116,18 +118,19 @@ class CTDGOnlineRuntime:
         weights, event arrays) with tensor code between steps calls this
         before the next step; the memory bank's own writers are tracked
         without it. With ``collect_results`` every step is fenced."""
-        if self._ev_commit is not None:
-            self._ev_commit.record(torch.cuda.current_stream(self.device))
+        if self._front_stream is not None:
+            self._seq += 1
+            self._sync_committed.fill_(self._seq)   # on the current stream, after the work queued so far
         self._state_writes = self.memory.state.writes
 
     def _pipeline_streams(self):
         if self._front_stream is None:
             self._front_stream = torch.cuda.Stream(self.device)
-            self._ev_commit = torch.cuda.Event()
-            self._ev_front = torch.cuda.Event()
-            cur = torch.cuda.current_stream(self.device)
-            self._ev_commit.record(cur)   # materialise both events
-            self._ev_front.record(cur)
+            self.fence()
+        elif self._seq >= 0x7FFFFFF0:   # keep the sequence numbers in int32 range
+            torch.cuda.synchronize(self.device)
+            self._sync.zero_()
+            self._seq = 0
         return self._front_stream
 
     def _core(self):
@@ -248,6 +251,7 @@ class CTDGOnlineRuntime:
                 self._plans[key] = plan
                 self.fence()   # state built on first use (a split's sampler graph) is queued here
             front = self._pipeline_streams()
+            seq = self._seq + 1
             top, t0, t1 = -1, None, None
             if self.plan_timer is not None:   # (entry point name, callback giving this step's event pair or None)
                 evs = self.plan_timer[1]()
@@ -256,8 +260,9 @@ class CTDGOnlineRuntime:
                     t0, t1 = evs[0].cuda_event, evs[1].cuda_event
             _capi.check(_capi.lib().sgl_plan_run(
                 plan[0], plan[1], plan[2], plan[3], front.cuda_stream,
-                torch.cuda.current_stream(self.device).cuda_stream, self._ev_commit.cuda_event,
-                self._ev_front.cuda_event, top, t0, t1), "sgl_plan_run")
+                torch.cuda.current_stream(self.device).cuda_stream, self._sync_ptr, seq, top, t0, t1),
+                "sgl_plan_run")
+            self._seq = seq
         views = self._views.get((n, q))
         if views is None or views[0] is not b:
             views = (b, b.loss[0], b.pos[:n], b.neg[:n])
