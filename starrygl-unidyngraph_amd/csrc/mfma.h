@@ -41,9 +41,18 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // operand's span: elements past it read as 0 without a branch or a fault, so
 // the loads of a chunk issue back to back. The whole byte offset is in the
 // VGPR operand (the range check does not cover the scalar offset).
+// The operand pointer and span are wave-uniform; readfirstlane states it, so
+// the descriptor lives in scalar registers (a descriptor the compiler has to
+// treat as per-lane turns every load into a waterfall loop).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const float *p, uint32_t nfloats) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), (short)0, int(nfloats * 4u), 0x00020000);
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  const uint32_t bytes = __builtin_amdgcn_readfirstlane(nfloats * 4u);
+  float *u = reinterpret_cast<float *>((uint64_t(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, int(bytes), 0x00020000);
 }
+
 
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t r, uint32_t elem) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, int(elem * 4u), 0, 0));
@@ -91,29 +100,55 @@ __device__ __forceinline__ void load_w_chunk(float (&b)[kChunkGroups][4], __amdg
   }
 }
 
-// acc += A[rows][kb .. kb+64) * b, A read from LDS (0 for k >= kd)
-__device__ __forceinline__ void mfma_chunk(f32x4 &acc, const float (&b)[kChunkGroups][4],
-                                           const float *__restrict__ A, int lda, int i, int kb, int kd, int q,
-                                           bool avec) {
-  const float *arow = A + i * lda;
+// acc += A[rows][kb .. kb+64) * b, A read from LDS. A chunk that lies
+// wholly inside k < kd (FULL) reads A without bounds logic: 16-byte reads
+// when AVEC (lda % 4 == 0, 16-byte aligned A), else 4-byte reads. The last,
+// partial chunk clamps its reads in bounds, zeroes k >= kd and skips the
+// groups past kd. Group g+1's reads are issued before group g's MFMAs, and the
+// MFMAs alternate between two accumulators: a single dependent MFMA chain
+// issues at about half the rate of two interleaved ones.
+template <bool FULL, bool AVEC>
+__device__ __forceinline__ void load_a_group(float (&a)[4], const float *__restrict__ arow, int k, int kd) {
+  if (FULL && AVEC) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(arow + k);
+    a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
+  } else if (FULL) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[s] = arow[k + s];
+  } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float v = arow[min(k + s, kd - 1)];
+      a[s] = (k + s < kd) ? v : 0.f;
+    }
+  }
+}
+
+template <bool FULL, bool AVEC>
+__device__ __forceinline__ void mfma_chunk(f32x4 &acc0, f32x4 &acc1, const float (&b)[kChunkGroups][4],
+                                           const float *__restrict__ arow, int kb, int kd, int q) {
+  float a0[4], a1[4];
+  load_a_group<FULL, AVEC>(a0, arow, kb + 4 * q, kd);
 #pragma unroll
   for (int g = 0; g < kChunkGroups; ++g) {
-    const int k = kb + 16 * g + 4 * q;
-    if (kb + 16 * g >= kd) break;  // uniform across the wave
-    float a[4];
-    if (avec) {
-      const f32x4 v = *reinterpret_cast<const f32x4 *>(arow + min(k, kd - 4));
-      const bool ok = k < kd;
-      a[0] = ok ? v[0] : 0.f; a[1] = ok ? v[1] : 0.f; a[2] = ok ? v[2] : 0.f; a[3] = ok ? v[3] : 0.f;
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const float v = arow[min(k + s, kd - 1)];
-        a[s] = (k + s < kd) ? v : 0.f;
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[g][s], acc, 0, 0, 0);
+    if (!FULL && kb + 16 * g >= kd) break;  // uniform across the wave
+    float (&cur)[4] = (g & 1) ? a1 : a0;
+    float (&nxt)[4] = (g & 1) ? a0 : a1;
+    if (g + 1 < kChunkGroups) load_a_group<FULL, AVEC>(nxt, arow, kb + 16 * (g + 1) + 4 * q, kd);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[0], b[g][0], acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[1], b[g][1], acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[2], b[g][2], acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(cur[3], b[g][3], acc1, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void mfma_chunk_any(f32x4 &acc0, f32x4 &acc1, const float (&b)[kChunkGroups][4],
+                                               const float *__restrict__ arow, int kb, int kd, int q, bool avec) {
+  if (kb + 16 * kChunkGroups <= kd) {  // uniform
+    if (avec) mfma_chunk<true, true>(acc0, acc1, b, arow, kb, kd, q);
+    else mfma_chunk<true, false>(acc0, acc1, b, arow, kb, kd, q);
+  } else {
+    mfma_chunk<false, false>(acc0, acc1, b, arow, kb, kd, q);
   }
 }
 
@@ -135,20 +170,21 @@ __device__ __forceinline__ f32x4 mfma_block16(const float *__restrict__ A, int l
   const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, span);
   // 16-byte loads: aligned, and never straddling the span end (kd % 4 == 0)
   const bool wvec = LAYOUT == kNT && (kd & 3) == 0 && (ldw & 3) == 0 && aligned16(W);
-  const bool avec = (kd & 3) == 0 && (lda & 3) == 0 && aligned16(A);
+  const bool avec = (lda & 3) == 0 && aligned16(A);
+  const float *arow = A + i * lda;
   constexpr int kc = 16 * kChunkGroups;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
   float b0[kChunkGroups][4], b1[kChunkGroups][4];
   load_w_chunk<LAYOUT>(b0, wr, ldw, n, 0, q, wvec);
   for (int kb = 0; kb < kd; kb += 2 * kc) {
     const bool more = kb + kc < kd;
     if (more) load_w_chunk<LAYOUT>(b1, wr, ldw, n, kb + kc, q, wvec);
-    mfma_chunk(acc, b0, A, lda, i, kb, kd, q, avec);
+    mfma_chunk_any(acc0, acc1, b0, arow, kb, kd, q, avec);
     if (!more) break;
     if (kb + 2 * kc < kd) load_w_chunk<LAYOUT>(b0, wr, ldw, n, kb + 2 * kc, q, wvec);
-    mfma_chunk(acc, b1, A, lda, i, kb + kc, kd, q, avec);
+    mfma_chunk_any(acc0, acc1, b1, arow, kb + kc, kd, q, avec);
   }
-  return acc;
+  return acc0 + acc1;
 }
 
 // OUT (LDS, 16 x n_total, leading dim ldo) = A * op(W) + bias (bias may be
