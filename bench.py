@@ -462,6 +462,9 @@ def main() -> None:
                              "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="first run 3 device-to-device copies of this many MiB (a known-size kernel for "
+                         "calibrating FETCH_SIZE / WRITE_SIZE counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU (the GPU boxes here have one); multi-GPU "
@@ -471,6 +474,14 @@ def main() -> None:
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
         sys.exit(1)
+    if args.copy_probe_mb > 0:
+        src = torch.ones(args.copy_probe_mb * (1 << 18), device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)   # an elementwise kernel: reads and writes the size once
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 device copies of {args.copy_probe_mb} MiB")
+        del src, dst
     base = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded PCG64 generators, starry_unigraph.synth)"}
     if args.workload == "sampler":

@@ -384,9 +384,17 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
  * n_commit == 0 every op runs in order on the back stream (front, sync and
  * seq are unused). An op's own checks run when it is replayed; the first
  * failing op's error is returned (ops before it are already enqueued).
- * timed_op >= 0 records t_start and t_end on that op's stream around it
- * (-1: no timing).
+ * timed_op >= 0 has that op's kernel record t_start and t_end at its own
+ * start and end (see sgl_time_next_launch; -1: no timing).
  * ------------------------------------------------------------------------- */
+/* Has the next kernel that the calling host thread launches through one of
+ * the step entry points (batch_prepare, recent_sample, memory_update,
+ * memory_commit, conv_forward/backward, predictor, grad_adam: their main
+ * kernel) record `start` and `stop` (hipEvent_t, timing enabled) at the
+ * dispatch's own start and end (hipExtLaunchKernel), so the interval is the
+ * kernel alone. NULL, NULL cancels. No reference counterpart (measurement). */
+int sgl_time_next_launch(hipEvent_t start, hipEvent_t stop);
+
 #define SGL_OP_MAX_ARGS 64
 
 typedef struct sgl_op {

@@ -936,8 +936,8 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_trig};
-  inst.fn<<<unsigned(capacity / inst.rows), unsigned(inst.waves * 64), lds, stream>>>(
-      d, num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
+  sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
+              num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -975,9 +975,10 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
                const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr, const_cast<float *>(sv_trig)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
-  inst.fn<<<unsigned(capacity / inst.rows), unsigned(inst.waves * 64), lds, stream>>>(
-      d, num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy, reinterpret_cast<long long *>(acc_src),
-      reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst, g);
+  sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
+              num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy,
+              reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst,
+              g);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -2,6 +2,7 @@
 // launch checks and wave64 scan primitives.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -22,6 +23,27 @@ constexpr int kWave = 64;
 // kernel and size only; thread-safe). Keeps hipFuncSetAttribute out of the
 // steady state, and so out of captured HIP graphs once a step has run.
 hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes);
+
+// Timing of the next kernel launch on this host thread (sgl_time_next_launch,
+// a plan's timed op): the launch records the two events itself, from the
+// dispatch's own start and end (hipExtLaunchKernel), so nothing else is
+// queued between them.
+struct LaunchTimer {
+  hipEvent_t start, stop;
+};
+LaunchTimer &pending_timer();
+
+template <typename F, typename... Args>
+inline void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+  LaunchTimer &t = pending_timer();
+  if (t.start != nullptr) {
+    const LaunchTimer u = t;
+    t = LaunchTimer{nullptr, nullptr};
+    hipExtLaunchKernelGGL(kernel, grid, block, uint32_t(lds), stream, u.start, u.stop, 0u, args...);
+  } else {
+    kernel<<<grid, block, lds, stream>>>(args...);
+  }
+}
 
 inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
 

@@ -30,8 +30,19 @@ hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes) {
   return e;
 }
 
+LaunchTimer &pending_timer() {
+  static thread_local LaunchTimer t{nullptr, nullptr};
+  return t;
+}
+
 }  // namespace sgl
 
 extern "C" int sgl_abi_version(void) { return SGL_ABI_VERSION; }
+
+extern "C" int sgl_time_next_launch(hipEvent_t start, hipEvent_t stop) {
+  SGL_REQUIRE((start == nullptr) == (stop == nullptr), "time_next_launch: give both events or neither");
+  sgl::pending_timer() = sgl::LaunchTimer{start, stop};
+  return SGL_OK;
+}
 
 extern "C" const char *sgl_last_error(void) { return sgl::g_last_error; }

@@ -212,9 +212,8 @@ extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, 
     segs.step[s] = steps[s];
     segs.gate[s] = gates != nullptr ? gates[s] : nullptr;
   }
-  k_grad_adam<<<unsigned(num_tiles), kGaBlock, 0, stream>>>(jobs, tile_job, num_roots, param, grad, exp_avg,
-                                                            exp_avg_sq, nseg, segs, coef, done, lr, beta1, beta2,
-                                                            eps, weight_decay);
+  sgl::launch(&k_grad_adam, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, num_roots, param,
+              grad, exp_avg, exp_avg_sq, nseg, segs, coef, done, lr, beta1, beta2, eps, weight_decay);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

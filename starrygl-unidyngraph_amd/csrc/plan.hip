@@ -84,7 +84,7 @@ const OpEntry kOps[] = {
 constexpr int kNumOps = int(sizeof(kOps) / sizeof(kOps[0]));
 static_assert(kNumOps > 0, "op table");
 
-// Optional timing of one op: events recorded on its stream around it.
+// Optional timing of one op: its kernel's dispatch records the two events.
 struct OpTimer {
   int op;
   hipEvent_t start, end;
@@ -98,9 +98,10 @@ int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t)
     SGL_REQUIRE(op.nargs == e.slots, "plan op %d (%s): %d arguments recorded, %d expected", base + i, e.name,
                 op.nargs, e.slots);
     const bool timed = base + i == t.op;
-    if (timed) SGL_CHECK_HIP(hipEventRecord(t.start, s));
-    if (int rc = e.run(op.a, s)) return rc;
-    if (timed) SGL_CHECK_HIP(hipEventRecord(t.end, s));
+    if (timed) sgl::pending_timer() = sgl::LaunchTimer{t.start, t.end};  // the op's (first) kernel records them
+    const int rc = e.run(op.a, s);
+    if (timed) sgl::pending_timer() = sgl::LaunchTimer{nullptr, nullptr};
+    if (rc) return rc;
   }
   return SGL_OK;
 }

@@ -207,10 +207,10 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
   const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + 2 * ((D + 1) & ~1));
   SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
-  k_predictor<<<unsigned((batch + kRows - 1) / kRows), kBlock, lds, stream>>>(
-      batch, D, train, num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits,
-      neg_logits, loss, reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
-      reinterpret_cast<long long *>(acc_out), done);
+  sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
+              num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
+              reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
+              reinterpret_cast<long long *>(acc_out), done);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

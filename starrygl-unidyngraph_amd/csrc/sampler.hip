@@ -275,13 +275,13 @@ extern "C" int sgl_recent_sample(
   if (num_queries <= kWaveModeMaxQueries) {  // latency: one wavefront per query
     const unsigned wblocks = unsigned((num_queries + kWaveQueriesPerBlock - 1) / kWaveQueriesPerBlock);
     if (q_node_is_i64)
-      k_recent_wave<int64_t><<<wblocks, kBlock, 0, stream>>>(
-          num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
-          nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+      sgl::launch(&k_recent_wave<int64_t>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries, num_queries_dev,
+                  static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts, num_nodes,
+                  fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
     else
-      k_recent_wave<int32_t><<<wblocks, kBlock, 0, stream>>>(
-          num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
-          nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+      sgl::launch(&k_recent_wave<int32_t>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries, num_queries_dev,
+                  static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts, num_nodes,
+                  fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }

@@ -539,11 +539,10 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   if (batch <= kPrepMaxBatch) {
     const size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
     SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_step_prepare_wg), lds));
-    k_step_prepare_wg<<<1, kPrepBlock, lds, stream>>>(
-        batch, num_nodes, cap, src, dst, neg, ts, cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64,
-        ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg,
-        reinterpret_cast<unsigned long long *>(win_src), reinterpret_cast<unsigned long long *>(win_dst), cnt_src,
-        cnt_dst, any_edges, err_flag);
+    sgl::launch(&k_step_prepare_wg, dim3(1), dim3(kPrepBlock), lds, stream, batch, num_nodes, cap, src, dst, neg, ts,
+                cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64, ts_max, t_query, roots, root_ts,
+                ridx_src, ridx_dst, ridx_neg, reinterpret_cast<unsigned long long *>(win_src),
+                reinterpret_cast<unsigned long long *>(win_dst), cnt_src, cnt_dst, any_edges, err_flag);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
@@ -594,10 +593,10 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
               64 * kMaxMsgSlots);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox), lds));
   const unsigned grid = unsigned((capacity + kTileRows - 1) / kTileRows);
-  k_gru_mailbox<<<grid, kGruBlock, lds, stream>>>(
-      D, K, F, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh,
-      bc_ih, bc_hh, src, dst, efeat, ts, batch_start, reinterpret_cast<const unsigned long long *>(win_src),
-      reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
+  sgl::launch(&k_gru_mailbox, dim3(grid), dim3(kGruBlock), lds, stream, D, K, F, num_roots, roots, memory, mailbox,
+              mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts,
+              batch_start, reinterpret_cast<const unsigned long long *>(win_src),
+              reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -612,8 +611,8 @@ extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num
   SGL_REQUIRE(num_roots && roots && new_mem && memory && memory_ts && ts_max && node_bits && any_edges,
               "memory_commit: NULL array");
   const int64_t total = capacity * D;
-  k_memory_commit<<<unsigned((total + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
-      D, capacity, num_roots, roots, new_mem, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
+  sgl::launch(&k_memory_commit, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, D, capacity,
+              num_roots, roots, new_mem, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -173,12 +173,18 @@ class DeviceStep:
         t = self.timer
         if t is None or (self.timed is not None and name not in self.timed):
             return fn()
+        # the call's kernel records the events at its own start and end
+        # (sgl_time_next_launch), so launch gaps are not counted
         stream = torch.cuda.current_stream(self.dev)
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        r = fn()
+        a.record(stream)   # torch creates the HIP events at their first record
         b.record(stream)
+        _capi.check(self.lib.sgl_time_next_launch(a.cuda_event, b.cuda_event), "sgl_time_next_launch")
+        try:
+            r = fn()
+        finally:
+            self.lib.sgl_time_next_launch(None, None)
         t.append((name, a, b))
         return r
 
