@@ -206,8 +206,9 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * w_out [D][2D], ln_g/ln_b [D], te_w/te_b [T]. capacity % 16 == 0.
  * Forward writes y [capacity][D] plus the saved state the backward needs
  * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
- * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows >= U are
- * zero. If any_edges == 0 the whole output is zero (models.py:88-89).
+ * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows of y
+ * >= U are zero, rows of the saved state >= U are left unwritten. If
+ * any_edges == 0 the whole output and saved state are zero (models.py:88-89).
  * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding;
  * sv_trig [cap][fanout][2][T] each sampled edge's time encoding cos and sin
  * (may be NULL in a forward without backward); the backward reads it.
@@ -217,7 +218,8 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * acc_src / acc_dst [cap+1][D], writes their rows as floats to g_src / g_dst
  * [cap+1][D] (for the src_fc / dst_fc weight reductions) and clears them for
  * the next step. It writes gz, gagg [cap][D], G [cap][H][D+F+T],
- * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs), and per
+ * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs; rows
+ * >= U unwritten, all zero if any_edges == 0), and per
  * tile partial sums ln_part [cap/R][2][D] (gamma, beta) and
  * te_part [cap/R][2][T] (time-encoding w, b; the b part includes the
  * query's cos(b) term through w_q), R = sgl_conv_tile_rows(D, F, T, H).

@@ -214,11 +214,15 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
   if (nrows == 0 || !live) {
-    // rows outside the live set, or a block without edges: zero output and
-    // zero saved state (the backward then produces zero gradients)
+    // rows outside the live set: zero output (y's row U is the null
+    // embedding the predictor's reductions read); a block without edges:
+    // zero output and zero saved state (the backward then produces zero
+    // gradients). Saved state of rows past the live set is never read.
+    for (int idx = tid; idx < RPW * D; idx += kBlock) y[size_t(r0) * D + idx] = 0.f;
+    if (live) return;
     for (int idx = tid; idx < RPW * D; idx += kBlock) {
       const size_t o = size_t(r0) * D + idx;
-      y[o] = 0.f; sv.Q[o] = 0.f; sv.agg[o] = 0.f; sv.z[o] = 0.f;
+      sv.Q[o] = 0.f; sv.agg[o] = 0.f; sv.z[o] = 0.f;
     }
     for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
       sv.qt[size_t(r0) * H * C + idx] = 0.f;
@@ -537,18 +541,23 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   const int r0 = blockIdx.x * RPW;
   const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
-  // the accumulators' extra row (capacity: the non-root negatives when every
-  // row is a root) belongs to the last workgroup
-  if (gy == nullptr && blockIdx.x == gridDim.x - 1)
-    consume_rows(acc_src, acc_dst, g_src, g_dst, int(gridDim.x) * RPW, 1, D, tid, kBlock);
+  // row U of the accumulators (the non-root negatives; row capacity when
+  // every row is a root) belongs to the workgroup whose tile holds it, or
+  // to the last one; the rows past U are never written by the predictor
+  if (gy == nullptr && ((U >= r0 && U < r0 + RPW) || (U == int(gridDim.x) * RPW && blockIdx.x == gridDim.x - 1)))
+    consume_rows(acc_src, acc_dst, g_src, g_dst, U, 1, D, tid, kBlock);
   if (nrows == 0 || !live) {
-    for (int idx = tid; idx < RPW * D; idx += kBlock) {
-      const size_t o = size_t(r0) * D + idx;
-      g.gz[o] = 0.f; g.gagg[o] = 0.f; g.gQ[o] = 0.f;
+    // rows outside the live set are never read; a block without edges has
+    // zero gradients in its live rows
+    if (gy == nullptr) consume_rows(acc_src, acc_dst, g_src, g_dst, r0, nrows, D, tid, kBlock);
+    if (!live) {
+      for (int idx = tid; idx < RPW * D; idx += kBlock) {
+        const size_t o = size_t(r0) * D + idx;
+        g.gz[o] = 0.f; g.gagg[o] = 0.f; g.gQ[o] = 0.f;
+      }
+      for (int idx = tid; idx < RPW * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
+      for (int idx = tid; idx < RPW * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
     }
-    if (gy == nullptr) consume_rows(acc_src, acc_dst, g_src, g_dst, r0, RPW, D, tid, kBlock);
-    for (int idx = tid; idx < RPW * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
-    for (int idx = tid; idx < RPW * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
     for (int idx = tid; idx < 2 * D; idx += kBlock) g.ln_part[size_t(blockIdx.x) * 2 * D + idx] = 0.f;
     for (int idx = tid; idx < 2 * T; idx += kBlock) g.te_part[size_t(blockIdx.x) * 2 * T + idx] = 0.f;
     return;
@@ -570,7 +579,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
       float vs = 0.f, vd = 0.f;
-      if (i < RPW) {  // the tile's rows (row U of the non-root negatives among them)
+      if (i < nrows) {  // the tile's live rows (row U is consumed above)
         const size_t o = size_t(r0 + i) * D + j;
         vs = sgl::from_fixed(acc_src[o]);
         vd = sgl::from_fixed(acc_dst[o]);
@@ -579,8 +588,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         g_src[o] = vs;
         g_dst[o] = vd;
       }
-      L.GA[i * L.ldr + j] = i < nrows ? vs : 0.f;
-      L.GQ[i * L.ldr + j] = i < nrows ? vd : 0.f;
+      L.GA[i * L.ldr + j] = vs;
+      L.GQ[i * L.ldr + j] = vd;
     }
     __syncthreads();
     sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves);

@@ -289,22 +289,23 @@ class DeviceStep:
         self.conv_backward_kernel(params, efeat_all, gy)
         b, d = self.buf, self.dims
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
-        # weight gradients: per-root products reduced over the root rows (rows
-        # past the live roots are zero in gz/gagg/G/sigma/gQ)
+        # weight gradients: per-root products reduced over the live root rows
+        # (the kernels leave the rows past them unwritten)
         D, H, C, T = d.D, d.H, d.C, d.T
         dh = D // H
-        c = b.cap
-        g_w_out = torch.cat([b.gz.t() @ b.agg, b.gz.t() @ b.new_mem], dim=1)
-        g_b_out = b.gz.sum(0)
-        ga = b.gagg.view(c, H, dh).permute(1, 2, 0).contiguous()          # [H, dh, cap]
-        g_w_v = torch.bmm(ga, b.xbar.permute(1, 0, 2).contiguous()).reshape(D, C)
-        g_b_v = b.gagg.sum(0)
-        qh = b.Q.view(c, H, dh)
-        g_w_k = torch.bmm(qh.permute(1, 2, 0).contiguous(), b.G.permute(1, 0, 2).contiguous()).reshape(D, C)
-        g_b_k = (qh * b.sigma.unsqueeze(-1)).sum(0).reshape(D)
-        sq = b.gQ.sum(0)
+        c = int(b.num_roots.item())
+        gz, gagg, gQ, new_mem = b.gz[:c], b.gagg[:c], b.gQ[:c], b.new_mem[:c]
+        g_w_out = torch.cat([gz.t() @ b.agg[:c], gz.t() @ new_mem], dim=1)
+        g_b_out = gz.sum(0)
+        ga = gagg.reshape(c, H, dh).permute(1, 2, 0).contiguous()          # [H, dh, U]
+        g_w_v = torch.bmm(ga, b.xbar[:c].permute(1, 0, 2).contiguous()).reshape(D, C)
+        g_b_v = gagg.sum(0)
+        qh = b.Q[:c].reshape(c, H, dh)
+        g_w_k = torch.bmm(qh.permute(1, 2, 0).contiguous(), b.G[:c].permute(1, 0, 2).contiguous()).reshape(D, C)
+        g_b_k = (qh * b.sigma[:c].unsqueeze(-1)).sum(0).reshape(D)
+        sq = gQ.sum(0)
         phi0 = torch.cos(te_b)
-        g_w_q = torch.cat([b.gQ.t() @ b.new_mem, torch.outer(sq, phi0)], dim=1)
+        g_w_q = torch.cat([gQ.t() @ new_mem, torch.outer(sq, phi0)], dim=1)
         g_b_q = sq
         g_ln_g = b.ln_part[:, 0].sum(0)
         g_ln_b = b.ln_part[:, 1].sum(0)
