@@ -249,6 +249,12 @@ def _restore(rt, snap):
     rt.fence()
 
 
+# HBM bytes per launch (read + written) of a kernel on a workload, from the
+# rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
+# profiles/conv_backward_cfg4_hbm_traffic.md (counters scaled by a copy
+# kernel of known size); None where no counter run was made.
+HBM_TRAFFIC = {("cfg4", "conv_backward"): (2334 + 1801) * 1024}
+
 # step stage name -> the C-ABI entry point that launches it
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
                 "memory_update": "sgl_memory_update", "memory_commit": "sgl_memory_commit",
@@ -392,7 +398,7 @@ def run_tgn(args, wl: dict) -> dict:
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
         "final_train_loss": final_loss,
         "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "traffic": None, "kernel_avg_ms": dom_avg,
+                     "frac": ach / peak, "traffic": HBM_TRAFFIC.get((wl["config"], dom)), "kernel_avg_ms": dom_avg,
                      "work_per_launch": dwork},
         "kernels": breakdown,
         "step_shape": {"mean_roots": round(mean_U, 1), "mean_sampled_edges": round(mean_E, 1)},
