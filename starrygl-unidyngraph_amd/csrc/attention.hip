@@ -569,10 +569,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
   // dL/dy of the tile: given, or W_s^T g_src + W_d^T g_dst from the edge
   // predictor's per-root rows (GA / GQ are free until later phases)
+  // (the two products land in GY and XH in parallel; the LayerNorm pass
+  // adds them)
   if (gy != nullptr) {
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
       L.GY[i * L.ldr + j] = i < nrows ? gy[size_t(r0 + i) * D + j] : 0.f;
+      L.XH[i * L.ldr + j] = 0.f;
     }
     __syncthreads();
   } else {
@@ -592,8 +595,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       L.GQ[i * L.ldr + j] = vd;
     }
     __syncthreads();
-    sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves);
-    sgl::tile_gemm16<sgl::kNN, true>(L.GQ, L.ldr, w_d, D, nullptr, L.GY, L.ldr, D, D, kWaves);
+    sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves / 2);
+    sgl::tile_gemm16<sgl::kNN>(L.GQ, L.ldr, w_d, D, nullptr, L.XH, L.ldr, D, D, kWaves / 2, kWaves / 2);
     __syncthreads();
   }
   // LayerNorm + ReLU backward; one wave per row (rows past the tile zeroed)
@@ -609,9 +612,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       const float mean = sv.stats[size_t(r0 + i) * 2], rstd = sv.stats[size_t(r0 + i) * 2 + 1];
       float a1 = 0.f, a2 = 0.f;
       for (int j = lane; j < D; j += 64) {
-        const float zz = sv.z[ro + j], gv = L.GY[i * L.ldr + j];
+        const float zz = sv.z[ro + j], gv = L.GY[i * L.ldr + j] + L.XH[i * L.ldr + j];
         const float xh = (fmaxf(zz, 0.f) - mean) * rstd;
         const float gxh = gv * p.ln_g[j];
+        L.GY[i * L.ldr + j] = gv;
         L.XH[i * L.ldr + j] = xh;
         L.GZ[i * L.ldr + j] = zz;
         a1 += gxh;
@@ -850,13 +854,27 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     L.GA[j] = sq;
   }
   __syncthreads();
-  // per-tile time-encoding gradients: the edges' terms, plus for the bias the
-  // query's cos(b) term -sin(b_t) * sum_j W_q[j][D+t] * sum_rows gQ[.][j]
+  // the query's cos(b) term of the time-encoding bias gradient,
+  // -sin(b_t) * sum_j W_q[j][D+t] * colsum[j]: the j range split over the
+  // waves, partial sums in GX (free by now), added in wave order
+  {
+    const int per = (D + kWaves - 1) / kWaves;
+    const int j0 = wave * per, j1 = min(D, j0 + per);
+    for (int t = lane; t < T; t += 64) {
+      float acc = 0.f;
+      for (int j = j0; j < j1; ++j) acc += p.w_q[size_t(j) * (D + T) + D + t] * L.GA[j];
+      L.GX[wave * T + t] = acc;
+    }
+  }
+  __syncthreads();
+  // per-tile time-encoding gradients: the edges' terms and the query's term
   for (int t = tid; t < T; t += kBlock) {
-    float a = 0.f, b = 0.f;
-    for (int w = 0; w < kWaves; ++w) { a += L.tep[(w * 2) * T + t]; b += L.tep[(w * 2 + 1) * T + t]; }
-    float qterm = 0.f;
-    for (int j = 0; j < D; ++j) qterm += p.w_q[size_t(j) * (D + T) + D + t] * L.GA[j];
+    float a = 0.f, b = 0.f, qterm = 0.f;
+    for (int w = 0; w < kWaves; ++w) {
+      a += L.tep[(w * 2) * T + t];
+      b += L.tep[(w * 2 + 1) * T + t];
+      qterm += L.GX[w * T + t];
+    }
     b += -sinf(L.TB[t]) * qterm;
     g.te_part[size_t(blockIdx.x) * 2 * T + t] = a;
     g.te_part[size_t(blockIdx.x) * 2 * T + T + t] = b;

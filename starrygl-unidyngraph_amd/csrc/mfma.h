@@ -190,13 +190,16 @@ __device__ __forceinline__ f32x4 mfma_block16(const float *__restrict__ A, int l
 // OUT (LDS, 16 x n_total, leading dim ldo) = A * op(W) + bias (bias may be
 // NULL), the n-blocks split over the workgroup's waves. No barrier inside;
 // the caller synchronises before reading OUT. If ACC, adds to OUT.
+// Waves [wave0, wave0 + nwaves) take part (two products can run side by
+// side on disjoint wave ranges).
 template <int LAYOUT, bool ACC = false>
 __device__ __forceinline__ void tile_gemm16(const float *__restrict__ A, int lda,
                                             const float *__restrict__ W, int ldw,
                                             const float *__restrict__ bias,
                                             float *__restrict__ OUT, int ldo,
-                                            int kd, int n_total, int nwaves) {
-  const int wave = threadIdx.x >> 6;
+                                            int kd, int n_total, int nwaves, int wave0 = 0) {
+  const int wave = int(threadIdx.x >> 6) - wave0;
+  if (wave < 0) return;
   const int lane = threadIdx.x & 63;
   const int nblocks = (n_total + 15) >> 4;
   for (int nb = wave; nb < nblocks; nb += nwaves) {
