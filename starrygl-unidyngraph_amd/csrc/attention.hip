@@ -302,15 +302,21 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
         my_dt = dt[base + e0 + lane];
       }
       for (int c0 = 0; c0 < mwin; c0 += kEC) {
+        // the chunk's edges past the window (uniform) skip their gathers,
+        // time encodings and reductions
         float x[kEC][JM];
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
-          const int e = min(c0 + u, mwin - 1);
-          float sn_unused[JM];
-          float *trig = (sv.trig != nullptr && c0 + u < mwin) ? sv.trig + (base + e0 + e) * size_t(2 * d.T)
-                                                                : nullptr;
-          load_x<JM, false>(d, memory, efeat, L.TW, L.TB, trig, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
-                            __shfl(my_dt, e, 64), lane, x[u], sn_unused);
+          if (c0 + u < mwin) {
+            const int e = c0 + u;
+            float sn_unused[JM];
+            float *trig = sv.trig != nullptr ? sv.trig + (base + e0 + e) * size_t(2 * d.T) : nullptr;
+            load_x<JM, false>(d, memory, efeat, L.TW, L.TB, trig, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
+                              __shfl(my_dt, e, 64), lane, x[u], sn_unused);
+          } else {
+#pragma unroll
+            for (int j = 0; j < JM; ++j) x[u][j] = 0.f;
+          }
         }
         // the chunk's scores first (independent reductions), then the
         // online-softmax updates in edge order
@@ -322,7 +328,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
             float part = 0.f;
 #pragma unroll
             for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
-            sc[u][h] = wave_sum(part) + qbh[h];
+            sc[u][h] = c0 + u < mwin ? wave_sum(part) + qbh[h] : 0.f;
           }
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
