@@ -187,6 +187,40 @@ __device__ __forceinline__ f32x4 mfma_block16(const float *__restrict__ A, int l
   return acc0 + acc1;
 }
 
+// Two 16-row tiles A0, A1 against the same op(W) block: the weight loads are
+// shared and the two tiles' MFMA chains are independent.
+template <int LAYOUT>
+__device__ __forceinline__ void mfma_block16_pair(const float *__restrict__ A0, const float *__restrict__ A1,
+                                                  int lda, const float *__restrict__ W, int ldw, int n0, int kd,
+                                                  int n_total, f32x4 &out0, f32x4 &out1) {
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15;
+  const int q = lane >> 4;
+  const int n = n0 + i;
+  const uint32_t span = LAYOUT == kNT ? uint32_t(n_total - 1) * uint32_t(ldw) + uint32_t(kd)
+                                      : uint32_t(kd - 1) * uint32_t(ldw) + uint32_t(n_total);
+  const __amdgpu_buffer_rsrc_t wr = weight_rsrc(W, span);
+  const bool wvec = LAYOUT == kNT && (kd & 3) == 0 && (ldw & 3) == 0 && aligned16(W);
+  const bool avec = (lda & 3) == 0 && aligned16(A0) && aligned16(A1);
+  const float *arow0 = A0 + i * lda, *arow1 = A1 + i * lda;
+  constexpr int kc = 16 * kChunkGroups;
+  f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = p0, r0 = p0, r1 = p0;
+  float b0[kChunkGroups][4], b1[kChunkGroups][4];
+  load_w_chunk<LAYOUT>(b0, wr, ldw, n, 0, q, wvec);
+  for (int kb = 0; kb < kd; kb += 2 * kc) {
+    const bool more = kb + kc < kd;
+    if (more) load_w_chunk<LAYOUT>(b1, wr, ldw, n, kb + kc, q, wvec);
+    mfma_chunk_any(p0, p1, b0, arow0, kb, kd, q, avec);
+    mfma_chunk_any(r0, r1, b0, arow1, kb, kd, q, avec);
+    if (!more) break;
+    if (kb + 2 * kc < kd) load_w_chunk<LAYOUT>(b0, wr, ldw, n, kb + 2 * kc, q, wvec);
+    mfma_chunk_any(p0, p1, b1, arow0, kb + kc, kd, q, avec);
+    mfma_chunk_any(r0, r1, b1, arow1, kb + kc, kd, q, avec);
+  }
+  out0 = p0 + p1;
+  out1 = r0 + r1;
+}
+
 // OUT (LDS, 16 x n_total, leading dim ldo) = A * op(W) + bias (bias may be
 // NULL), the n-blocks split over the workgroup's waves. No barrier inside;
 // the caller synchronises before reading OUT. If ACC, adds to OUT.

@@ -67,6 +67,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   float *Hs = En + kRows * ld;   // h_s
   float *Hd = Hs + kRows * ld;   // h_d -> a_p
   float *Hn = Hd + kRows * ld;   // h_n -> a_n
+  float *Wo = Hn + kRows * ld;   // [D] out_fc weight
   __shared__ float s_gp[kRows], s_gn[kRows], s_sp[kRows];
   __shared__ int s_idx[3][kRows];
   __shared__ int s_last;
@@ -80,7 +81,10 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     s_idx[1][tid] = ok ? rd[e0 + tid] : -1;
     s_idx[2][tid] = ok ? rn[e0 + tid] : -1;
   }
-  for (int j = tid; j < D; j += kBlock) Nul[j] = 0;
+  for (int j = tid; j < D; j += kBlock) {
+    Nul[j] = 0;
+    Wo[j] = w_o[j];
+  }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
@@ -91,9 +95,31 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   }
   __syncthreads();
   {
-    sgl::GemmJob jobs[3] = {{Es, ld, w_s, D, b_s, Hs, ld, D, D}, {Ed, ld, w_d, D, b_d, Hd, ld, D, D},
-                            {En, ld, w_d, D, b_d, Hn, ld, D, D}};
-    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+    // h_s = W_s e_s + b_s on one set of waves; h_d and h_n (both W_d) on
+    // another, each block's W_d loads shared by the two tiles
+    const int nblk = (D + 15) >> 4;
+    for (int u = wave; u < 2 * nblk; u += kWaves) {
+      const int nb = u < nblk ? u : u - nblk, n0 = nb * 16, col = n0 + (lane & 15);
+      if (u < nblk) {
+        const sgl::f32x4 acc = sgl::mfma_block16<sgl::kNT>(Es, ld, w_s, D, n0, D, D);
+        if (col < D) {
+          const float bv = b_s[col];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) Hs[(4 * (lane >> 4) + v) * ld + col] = acc[v] + bv;
+        }
+      } else {
+        sgl::f32x4 ad, an;
+        sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
+        if (col < D) {
+          const float bv = b_d[col];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            Hd[(4 * (lane >> 4) + v) * ld + col] = ad[v] + bv;
+            Hn[(4 * (lane >> 4) + v) * ld + col] = an[v] + bv;
+          }
+        }
+      }
+    }
   }
   __syncthreads();
   // logits, loss terms, logit gradients: one wave per event
@@ -105,8 +131,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       const float an = fmaxf(hs + Hn[i * ld + j], 0.f);
       Hd[i * ld + j] = ap;
       Hn[i * ld + j] = an;
-      pp += w_o[j] * ap;
-      pn += w_o[j] * an;
+      pp += Wo[j] * ap;
+      pn += Wo[j] * an;
     }
     pp = sgl::wave_sum_dpp(pp);
     pn = sgl::wave_sum_dpp(pn);
@@ -148,8 +174,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
       if (i >= nrows) continue;
-      const float ghp = Hd[i * ld + j] > 0.f ? s_gp[i] * w_o[j] : 0.f;
-      const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * w_o[j] : 0.f;
+      const float ghp = Hd[i * ld + j] > 0.f ? s_gp[i] * Wo[j] : 0.f;
+      const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * Wo[j] : 0.f;
       const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
       const long long fp = sgl::to_fixed(ghp), fn = sgl::to_fixed(ghn);
       if (a >= 0) sgl::atomic_add_fixed(&acc_src[size_t(a) * D + j], fp + fn);
@@ -204,7 +230,7 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
-  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + 2 * ((D + 1) & ~1));
+  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + 2 * ((D + 1) & ~1) + D);
   SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
   sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
