@@ -344,6 +344,7 @@ def run_tgn(args, wl: dict) -> dict:
     wall = time.perf_counter() - w0
     gc.enable()
     rt.plan_timer = None
+    rt.check_sync()
     log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]

@@ -370,24 +370,34 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
  * argument count without the trailing stream, a[i] argument i (pointers and
  * integers as their value, floats as their bit pattern in the low 32 bits).
  * sgl_plan_run enqueues, without blocking the host, ops [0, n_front) (the
- * step's front part: batch preparation, sampling, GRU), then n_commit ops
- * (the memory commit), then n_back ops (attention, predictor, backward,
- * Adam), ordering the two streams through the device words sync[0] (last
- * commit) and sync[16] (last front part), uint32 in device memory, zero
- * before the first run:
- *   front stream: wait until sync[0] >= seq-1, front ops, write sync[16] = seq
- *   back stream:  wait until sync[16] >= seq, commit ops, write sync[0] = seq,
- *                 back ops
- * so step t+1's front part overlaps step t's back part. seq increases by one
- * per run (from 1); consecutive runs must use different step buffers
- * (ping-pong). Work queued on the back stream between runs that the next
- * front part depends on is published by writing sync[0] = seq on the back
- * stream after it and running the next plan with seq + 1 (a fence). With
- * n_commit == 0 every op runs in order on the back stream (front, sync and
- * seq are unused). An op's own checks run when it is replayed; the first
- * failing op's error is returned (ops before it are already enqueued).
- * timed_op >= 0 has that op's kernel record t_start and t_end at its own
- * start and end (see sgl_time_next_launch; -1: no timing).
+ * step's front part: batch preparation, sampling, GRU), n_commit ops (the
+ * memory commit), n_back ops (attention forward, predictor, backward) and
+ * n_tail ops (the fused Adam), ordering the two streams through uint32
+ * words in device memory (64 words, zero before the first run): sync[0] =
+ * back (last back part done), sync[16] = fronted (last front part incl.
+ * commit), sync[32] = bwd (last backward done), sync[48] = timeout. A write
+ * is a one-lane kernel that stores the number once the stream's earlier
+ * kernels are done; a wait is a one-lane kernel that polls the word and ends
+ * when it reaches the value, or after about two seconds, setting timeout to
+ * 1 (the ordering is then lost; the host checks that word):
+ *   front stream: wait until back >= need_back, front ops,
+ *                 wait until bwd >= need_bwd, commit ops, write fronted = seq
+ *   back stream:  wait until fronted >= seq, back ops, write bwd = seq,
+ *                 tail ops, write back = seq
+ * With two step-buffer sets used alternately, need_back is the sequence
+ * number of the step before the previous one (its back part read this
+ * step's buffers) and need_bwd that of the previous step (its backward
+ * is the last reader of the memory table the commit writes): step t+1's
+ * front part overlaps step t's back part and its commit step t's Adam.
+ * Sequence numbers increase (from 1, need_* < seq). Work queued on the back
+ * stream between runs that the next front part depends on is published by
+ * writing a fresh number v to sync[0] and sync[32] on the back stream after
+ * it and passing need_back = need_bwd = v (a fence). With n_commit == 0 every
+ * op runs in order on the back stream (front, sync, seq, need_* unused).
+ * An op's own checks run when it is replayed; the first failing op's error
+ * is returned (ops before it are already enqueued). timed_op >= 0 has that
+ * op's kernel record t_start and t_end at its own start and end (see
+ * sgl_time_next_launch; -1: no timing).
  * ------------------------------------------------------------------------- */
 /* Has the next kernel that the calling host thread launches through one of
  * the step entry points (batch_prepare, recent_sample, memory_update,
@@ -410,8 +420,9 @@ typedef struct sgl_op {
  * stream. */
 int32_t sgl_plan_op_kind(const char *name, int32_t *nargs);
 int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit,
-                 int32_t n_back, hipStream_t front, hipStream_t back,
-                 uint32_t *sync, uint32_t seq, int32_t timed_op,
+                 int32_t n_back, int32_t n_tail, hipStream_t front,
+                 hipStream_t back, uint32_t *sync, uint32_t seq,
+                 uint32_t need_back, uint32_t need_bwd, int32_t timed_op,
                  hipEvent_t t_start, hipEvent_t t_end);
 
 #ifdef __cplusplus

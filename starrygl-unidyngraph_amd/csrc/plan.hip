@@ -2,25 +2,26 @@
 // arguments are fixed device pointers and sizes: events are read at a device
 // cursor) and replayed with plain kernel launches by one host call.
 //
-// A plan is three runs of ops: the front part of a step (batch preparation,
-// sampling, GRU memory update), the memory commit, and the back part
-// (attention forward, edge predictor, backward, fused Adam). Step t+1's front
-// part only needs step t's commit (the memory table, the node bitmap) and,
-// with consecutive steps on different step buffers, reads nothing the back
-// part writes, so it runs on a second stream beside step t's back part. The
-// two streams order themselves through two device words (stream memory
-// operations: a write after the stream's prior work, a wait that holds the
-// stream until the word reaches a value):
+// A plan is four runs of ops: the front part of a step (batch preparation,
+// sampling, GRU memory update), the memory commit, and the back part split
+// after the backward (attention forward, edge predictor, backward | fused
+// Adam). Consecutive steps use different step buffers. Step t's front part
+// only needs the buffers that step t-2's back part read to be free, and its
+// commit only needs step t-1's backward (the last reader of the memory
+// table) to be done, so the front stream runs ahead, and the commit of step
+// t runs beside step t-1's Adam. The streams order themselves through three
+// device words (stream memory operations: a write after the stream's prior
+// work, a wait that holds the stream until the word reaches a value):
 //
-//   front stream:  wait(sync[0] >= seq-1) -> front ops -> write(sync[16] = seq)
-//   back stream:   wait(sync[16] >= seq) -> commit ops -> write(sync[0] = seq) -> back ops
+//   front:  wait(back >= need_back) -> front ops -> wait(bwd >= need_bwd)
+//           -> commit -> write(fronted = seq)
+//   back:   wait(fronted >= seq) -> fwd, predictor, bwd -> write(bwd = seq)
+//           -> Adam -> write(back = seq)
 //
-// Everything queued on the back stream before the commit (the previous back
-// part included) precedes the commit, so a front part never overlaps the back
-// part that still reads the buffers it is about to fill. Plain launches cost
-// the GPU well under a microsecond between kernels; the same kernels replayed
-// as graphs cost several, and more at graph boundaries; stream memory
-// operations resolve faster than events between streams.
+// Plain launches cost the GPU well under a microsecond between kernels; the
+// same kernels replayed as graphs cost several, and more at graph
+// boundaries; stream memory operations resolve faster than events between
+// streams.
 #include <cstring>
 #include <type_traits>
 #include <utility>
@@ -106,6 +107,39 @@ int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t)
   return SGL_OK;
 }
 
+// Cross-stream ordering: a one-lane kernel that stores a sequence number
+// (release: the stream's earlier kernels have completed, their writes are
+// visible to the device) and one that waits until a word reaches a value
+// (acquire), polling with s_sleep and giving up after about two seconds
+// (then it sets the timeout word, which the host checks).
+__global__ void k_signal(uint32_t *word, uint32_t value) {
+  if (threadIdx.x == 0) __hip_atomic_store(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ void k_gate(const uint32_t *word, uint32_t value, uint32_t *timeout) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();  // 100 MHz
+  while (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < value) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {
+      __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+int signal(uint32_t *word, uint32_t value, hipStream_t s) {
+  k_signal<<<1, 64, 0, s>>>(word, value);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+int gate(const uint32_t *word, uint32_t value, uint32_t *timeout, hipStream_t s) {
+  k_gate<<<1, 64, 0, s>>>(word, value, timeout);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
 }  // namespace
 
 extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
@@ -119,23 +153,30 @@ extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
 }
 
 extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit, int32_t n_back,
-                            hipStream_t front, hipStream_t back, uint32_t *sync, uint32_t seq, int32_t timed_op,
-                            hipEvent_t t_start, hipEvent_t t_end) {
-  SGL_REQUIRE(ops != nullptr || n_front + n_commit + n_back == 0, "plan_run: NULL ops");
-  SGL_REQUIRE(n_front >= 0 && n_commit >= 0 && n_back >= 0, "plan_run: negative op count");
+                            int32_t n_tail, hipStream_t front, hipStream_t back, uint32_t *sync, uint32_t seq,
+                            uint32_t need_back, uint32_t need_bwd, int32_t timed_op, hipEvent_t t_start,
+                            hipEvent_t t_end) {
+  SGL_REQUIRE(ops != nullptr || n_front + n_commit + n_back + n_tail == 0, "plan_run: NULL ops");
+  SGL_REQUIRE(n_front >= 0 && n_commit >= 0 && n_back >= 0 && n_tail >= 0, "plan_run: negative op count");
   SGL_REQUIRE(timed_op < 0 || (t_start && t_end), "plan_run: NULL timing event");
   const OpTimer t{timed_op, t_start, t_end};
   if (n_commit == 0) {  // no split point: everything in order on the back stream
-    return run_ops(ops, n_front + n_back, back, 0, t);
+    return run_ops(ops, n_front + n_back + n_tail, back, 0, t);
   }
-  SGL_REQUIRE(sync != nullptr && seq > 0, "plan_run: NULL sync words or sequence number 0");
+  SGL_REQUIRE(sync != nullptr && seq > 0 && need_back < seq && need_bwd < seq,
+              "plan_run: NULL sync words or inconsistent sequence numbers");
   SGL_REQUIRE(front != back, "plan_run: the front and back streams must differ");
-  uint32_t *committed = sync, *fronted = sync + 16;  // separate 64-byte lines
-  SGL_CHECK_HIP(hipStreamWaitValue32(front, committed, seq - 1, hipStreamWaitValueGte, 0xffffffffu));
+  // separate 64-byte lines; sync[48] is the gates' timeout word
+  uint32_t *w_back = sync, *w_front = sync + 16, *w_bwd = sync + 32, *timeout = sync + 48;
+  if (int rc = gate(w_back, need_back, timeout, front)) return rc;
   if (int rc = run_ops(ops, n_front, front, 0, t)) return rc;
-  SGL_CHECK_HIP(hipStreamWriteValue32(front, fronted, seq, 0));
-  SGL_CHECK_HIP(hipStreamWaitValue32(back, fronted, seq, hipStreamWaitValueGte, 0xffffffffu));
-  if (int rc = run_ops(ops + n_front, n_commit, back, n_front, t)) return rc;
-  SGL_CHECK_HIP(hipStreamWriteValue32(back, committed, seq, 0));
-  return run_ops(ops + n_front + n_commit, n_back, back, n_front + n_commit, t);
+  if (int rc = gate(w_bwd, need_bwd, timeout, front)) return rc;
+  if (int rc = run_ops(ops + n_front, n_commit, front, n_front, t)) return rc;
+  if (int rc = signal(w_front, seq, front)) return rc;
+  if (int rc = gate(w_front, seq, timeout, back)) return rc;
+  const int b0 = n_front + n_commit;
+  if (int rc = run_ops(ops + b0, n_back, back, b0, t)) return rc;
+  if (int rc = signal(w_bwd, seq, back)) return rc;
+  if (int rc = run_ops(ops + b0 + n_back, n_tail, back, b0 + n_back, t)) return rc;
+  return signal(w_back, seq, back);
 }

@@ -95,15 +95,18 @@ class CTDGOnlineRuntime:
         self._views: dict[tuple[int, int], tuple] = {}
         self._updates: dict[int, StepParamUpdate] = {}
         # two-stream submission: the front stream runs batch preparation,
-        # sampling and the GRU; the caller's current stream the rest. The
-        # streams order themselves through two device words (sgl_plan_run):
-        # _sync[0] holds the sequence number of the last commit or fence,
-        # _sync[16] that of the last front part; _seq is the last number used.
+        # sampling, the GRU and the memory commit; the caller's current stream
+        # the attention, predictor, backward and Adam. The streams order
+        # themselves through three device words (sgl_plan_run): _sync[0] the
+        # number of the last back part (or fence), _sync[16] of the last front
+        # part, _sync[32] of the last backward (or fence). _seq is the last
+        # number used; _need_back / _need_bwd what the next front part waits for.
         self._front_stream: torch.cuda.Stream | None = None
-        self._sync = torch.zeros(32, dtype=torch.int32, device=self.device)
+        self._sync = torch.zeros(64, dtype=torch.int32, device=self.device)
         self._sync_ptr = self._sync.data_ptr()
-        self._sync_committed = self._sync[0:1]
+        self._sync_back, self._sync_bwd = self._sync[0:1], self._sync[32:33]
         self._seq = 0
+        self._need_back = self._need_bwd = self._prev_seq = 0
         self._state_writes = memory.state.writes
 
     def _make_steps(self, max_batch: int) -> None:
@@ -120,8 +123,19 @@ class CTDGOnlineRuntime:
         without it. With ``collect_results`` every step is fenced."""
         if self._front_stream is not None:
             self._seq += 1
-            self._sync_committed.fill_(self._seq)   # on the current stream, after the work queued so far
+            # on the current stream, after the work queued so far
+            self._sync_back.fill_(self._seq)
+            self._sync_bwd.fill_(self._seq)
+            self._need_back = self._need_bwd = self._prev_seq = self._seq
         self._state_writes = self.memory.state.writes
+
+    def check_sync(self) -> None:
+        """Raise if a cross-stream wait of a planned step gave up (after about
+        two seconds) instead of seeing its predecessor finish; results from
+        then on are unordered. Synchronizes the device."""
+        if self._front_stream is not None and int(self._sync[48].item()):
+            raise RuntimeError("sgl_plan_run: a cross-stream wait timed out; the steps since the last check "
+                               "ran out of order")
 
     def _pipeline_streams(self):
         if self._front_stream is None:
@@ -130,7 +144,7 @@ class CTDGOnlineRuntime:
         elif self._seq >= 0x7FFFFFF0:   # keep the sequence numbers in int32 range
             torch.cuda.synchronize(self.device)
             self._sync.zero_()
-            self._seq = 0
+            self._seq = self._need_back = self._need_bwd = self._prev_seq = 0
         return self._front_stream
 
     def _core(self):
@@ -256,12 +270,15 @@ class CTDGOnlineRuntime:
             if self.plan_timer is not None:   # (entry point name, callback giving this step's event pair or None)
                 evs = self.plan_timer[1]()
                 if evs is not None:
-                    top = plan[4].index(self.plan_timer[0])
+                    top = plan[5].index(self.plan_timer[0])
                     t0, t1 = evs[0].cuda_event, evs[1].cuda_event
             _capi.check(_capi.lib().sgl_plan_run(
-                plan[0], plan[1], plan[2], plan[3], front.cuda_stream,
-                torch.cuda.current_stream(self.device).cuda_stream, self._sync_ptr, seq, top, t0, t1),
-                "sgl_plan_run")
+                plan[0], plan[1], plan[2], plan[3], plan[4], front.cuda_stream,
+                torch.cuda.current_stream(self.device).cuda_stream, self._sync_ptr, seq, self._need_back,
+                self._need_bwd, top, t0, t1), "sgl_plan_run")
+            # the next step's front part refills the buffers this step's
+            # predecessor read; its commit follows this step's backward
+            self._need_back, self._need_bwd, self._prev_seq = self._prev_seq, seq, seq
             self._seq = seq
         views = self._views.get((n, q))
         if views is None or views[0] is not b:
@@ -271,8 +288,9 @@ class CTDGOnlineRuntime:
 
     def _record(self, step: DeviceStep, split: str, train: bool, n: int) -> tuple:
         """Record a full step on ``step``'s buffers as a launch plan: (ops,
-        #front, #commit, #back, entry point names, recorded calls). Without a memory updater the
-        plan has no commit and runs in order on one stream."""
+        #front, #commit, #back, #tail, entry point names, recorded calls); the
+        tail is the fused Adam. Without a memory updater the plan has no
+        commit and runs in order on one stream."""
         d = self._dev
         if train:
             self._param_update(step)   # any rebuild or host-side sync happens outside the recording
@@ -282,9 +300,13 @@ class CTDGOnlineRuntime:
         with _capi.record() as commit:
             self._commit_body(step)
         with _capi.record() as back:
-            self._back_body(step, train, n)
-        calls = front + commit + back
-        return (_capi.pack_ops(calls), len(front), len(commit), len(back), [c[0] for c in calls], calls)
+            self._back_body(step, train, n, update=False)
+        with _capi.record() as tail:
+            if train:
+                self._param_update(step).run()
+        calls = front + commit + back + tail
+        return (_capi.pack_ops(calls), len(front), len(commit), len(back), len(tail), [c[0] for c in calls],
+                calls)
 
     def reset_plans(self) -> None:
         """Drop recorded plans (after buffers they reference change)."""
@@ -306,9 +328,10 @@ class CTDGOnlineRuntime:
         if self._gru is not None:
             step.commit()
 
-    def _back_body(self, step: DeviceStep, train: bool, n: int) -> None:
+    def _back_body(self, step: DeviceStep, train: bool, n: int, update: bool = True) -> None:
         """Attention forward, edge predictor + BCE and, in training, the
-        backward and the fused weight-gradient + Adam update."""
+        backward and (with ``update``) the fused weight-gradient + Adam
+        update."""
         core = self._core()
         conv = core.conv
         efeat_all = self._dev["edge_feat"]
@@ -328,7 +351,8 @@ class CTDGOnlineRuntime:
         step.predictor(n, train, pdet, out_grads)
         if train:
             step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]))
-            upd.run()
+            if update:
+                upd.run()
 
     def _param_update(self, step: DeviceStep) -> StepParamUpdate:
         """The fused weight-gradient + Adam launch for a step's buffers and the

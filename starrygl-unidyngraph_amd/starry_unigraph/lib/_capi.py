@@ -51,7 +51,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
     "sgl_time_next_launch": (ctypes.c_int, [_vp, _vp]),
     "sgl_plan_op_kind": (_i32, [ctypes.c_char_p, _vp]),
-    "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _vp, _vp, ctypes.c_uint32, _i32, _vp, _vp]),
+    "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp] + [ctypes.c_uint32] * 3
+                     + [_i32, _vp, _vp]),
     "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 4 + [ctypes.c_float] * 5 + [_vp]),
 }
 

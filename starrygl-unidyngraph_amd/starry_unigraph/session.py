@@ -92,6 +92,7 @@ class SchedulerSession:
             else:
                 outputs.append(self.ctdg_session.eval_step(batch))
         elapsed = time.perf_counter() - t0
+        self.ctdg_session.online_runtime.check_sync()
         if split == "train":
             self.current_epoch += 1
         losses = [float(o["loss"]) for o in outputs if "loss" in o]
