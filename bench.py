@@ -245,7 +245,6 @@ def _restore(rt, snap):
         dst.copy_(src)
     for dst, src in zip([opt.flat, opt.exp_avg, opt.exp_avg_sq] + [seg[2] for seg in opt.segments], snap[1]):
         dst.copy_(src)
-    opt.mark_state_changed()
     rt.fence()
 
 

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 3
+#define SGL_ABI_VERSION 4
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -270,6 +270,11 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
  * atomics make the sums independent of the order of the additions. */
 #define SGL_FIXED_SHIFT 40
 
+/* Size in int32 words of sgl_predictor's completion counter (`done`): 16
+ * group words and a top word, 64 words apart, so that the workgroups of a
+ * large launch do not all count themselves on one word. */
+#define SGL_DONE_WORDS 1088
+
 /* ---------------------------------------------------------------------------
  * Edge predictor + BCE, forward and (train != 0) backward.
  * Replaces CTDGLinkPredictor.forward (backends/ctdg/runtime/models.py:313-324)
@@ -286,9 +291,9 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
  * acc_dst[r] = the same for dst (dL/dh_d) and negatives (dL/dh_n); negatives
  * that are not roots add into row U = *num_roots. The src_fc / dst_fc
  * gradients follow as reductions over rows 0..U (sgl_grad_adam jobs) and
- * dL/dy through sgl_conv_backward. acc_out (int64 [D+2]) and done (int32)
- * are the launch's own accumulator and completion counter: zero before the
- * first call, left zero by every call. All sums over events are exact integer
+ * dL/dy through sgl_conv_backward. acc_out (int64 [D+2]) and done (int32
+ * [SGL_DONE_WORDS]) are the launch's own accumulator and completion counter:
+ * zero before the first call, left zero by every call. All sums over events are exact integer
  * sums, so results do not depend on the order of the workgroups.
  * ------------------------------------------------------------------------- */
 int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
@@ -334,13 +339,10 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * tile0 is the job's first tile; tile_job[t] the job of tile t (device).
  * Each gradient element is written once, then Adam-updated (torch.optim.Adam
  * arithmetic) if its segment `seg` is active: gates[seg] NULL or
- * *gates[seg] != 0. steps[s] (device float) holds segment s's completed step
- * count t-1; coef[2s], coef[2s+1] (device) hold lr / (1 - beta1^t) and
- * sqrt(1 - beta2^t) for that t (the caller writes them before the first
- * launch). The launch's last workgroup to finish advances the active
- * segments' counts and writes coef for the next launch (done: a device
- * int32 completion counter, zero between launches). steps and gates are
- * host arrays of nseg <= SGL_MAX_ADAM_SEGMENTS device pointers.
+ * *gates[seg] != 0, with the bias corrections coef[2*seg] = lr / (1 -
+ * beta1^t) and coef[2*seg+1] = sqrt(1 - beta2^t) of the segment's step t
+ * (device floats, written by sgl_adam_coef). gates is a host array of
+ * nseg <= SGL_MAX_ADAM_SEGMENTS device pointers (NULL: every segment open).
  * ------------------------------------------------------------------------- */
 #define SGL_MAX_ADAM_SEGMENTS 8
 
@@ -355,9 +357,23 @@ typedef struct sgl_grad_job {
 int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   int32_t num_tiles, const int32_t *num_roots, float *param,
                   float *grad, float *exp_avg, float *exp_avg_sq, int32_t nseg,
-                  float *const *steps, const int32_t *const *gates,
-                  float *coef, int32_t *done, float lr, float beta1, float beta2,
-                  float eps, float weight_decay, hipStream_t stream);
+                  const int32_t *const *gates, const float *coef, float beta1,
+                  float beta2, float eps, float weight_decay,
+                  hipStream_t stream);
+
+/* Step counts and bias corrections for one sgl_grad_adam launch. Replaces
+ * torch.optim.Adam's per-step `step += 1` and bias corrections (the
+ * optimizer of backends/ctdg/runtime/factory.py:122-128). For each segment
+ * s < nseg whose gate is open (gates NULL, gates[s] NULL or *gates[s] != 0)
+ * the completed-step count *steps[s] (device float) advances by one; coef[2s]
+ * and coef[2s+1] become lr / (1 - beta1^t) and sqrt(1 - beta2^t) for t =
+ * the count after the advance (a closed segment: the count plus one), in
+ * double as torch computes them. One lane. Enqueue it after the gates are
+ * written and after the sgl_grad_adam launch that last read this coef;
+ * steps and gates are host arrays of device pointers. */
+int sgl_adam_coef(int32_t nseg, float *const *steps,
+                  const int32_t *const *gates, float *coef, float lr,
+                  float beta1, float beta2, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Launch plans: a training step's calls of the entry points above, recorded

@@ -103,6 +103,33 @@ __device__ __forceinline__ void atomic_add_fixed(long long *p, long long v) {
 }
 static_assert(SGL_FIXED_SHIFT == 40, "to_fixed / from_fixed scale");
 
+// "The last workgroup of a launch does X". Same-word atomics serialize
+// (~20 ns each) and every atomic is a round trip (~1.5 us), so a small grid
+// counts on one word and a large one on two levels: block b counts itself
+// into group b % kDoneGroups's word, the last of a group into the top word,
+// the last of those is the launch's last block. done holds SGL_DONE_WORDS
+// int32 (the group words kDoneStride apart, the top word after them), zero
+// between launches; each word is cleared by the block that completes it.
+// Call from one thread per block, after the block's own global writes and
+// atomics have completed; one-dimensional grids.
+constexpr int kDoneGroups = 16, kDoneStride = 64, kDoneFlat = 64;
+static_assert((kDoneGroups + 1) * kDoneStride == SGL_DONE_WORDS, "completion counter size");
+__device__ inline bool last_block(int32_t *done) {
+  const unsigned g = gridDim.x, b = blockIdx.x;
+  int32_t *top = done + kDoneGroups * kDoneStride;
+  int arrivals = int(g);
+  if (g > unsigned(kDoneFlat)) {
+    const unsigned grp = b % kDoneGroups;
+    int32_t *w = done + grp * kDoneStride;
+    if (atomicAdd(w, 1) != int((g - grp + kDoneGroups - 1) / kDoneGroups) - 1) return false;
+    __hip_atomic_store(w, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrivals = kDoneGroups;
+  }
+  if (atomicAdd(top, 1) != arrivals - 1) return false;
+  __hip_atomic_store(top, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_reduce_sum(T v) {
 #pragma unroll

@@ -78,13 +78,10 @@ extern "C" int sgl_adam_advance(float *step, const int32_t *active, hipStream_t 
 // then summed through LDS. A kind-1 job covers 256 contiguous elements whose
 // gradient is already in place. Either way each thread then owns one
 // gradient element: it stores the gradient and, if its segment is active
-// this step, applies the Adam update to the parameter and moments.
-// The bias corrections for this launch's t = steps[s] + 1 are read from
-// coef (written by the previous launch, or by the caller for the first);
-// the last workgroup to finish (an atomic completion counter, reset by it)
-// advances the active segments' step counts and writes the corrections for
-// the next launch. No workgroup reads a value another one of this launch
-// writes, so no separate launch or fence is needed.
+// this step, applies the Adam update to the parameter and moments with the
+// bias corrections in coef (k_adam_coef, enqueued earlier). No workgroup
+// reads a value another one of this launch writes, and none counts
+// completions: the step counts advance in k_adam_coef.
 namespace {
 
 constexpr int kGaBlock = 256;
@@ -99,9 +96,9 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
                                                        const int32_t *__restrict__ tile_job,
                                                        const int32_t *__restrict__ num_roots, float *__restrict__ p,
                                                        float *__restrict__ g, float *__restrict__ m,
-                                                       float *__restrict__ v, int nseg, AdamSegs segs,
-                                                       float *__restrict__ coef, int32_t *__restrict__ done,
-                                                       float lr, float b1, float b2, float eps, float wd) {
+                                                       float *__restrict__ v, AdamSegs segs,
+                                                       const float *__restrict__ coef, float b1, float b2, float eps,
+                                                       float wd) {
   __shared__ float red[4][16][17];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t = blockIdx.x;
@@ -164,7 +161,6 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
       mv = m[idx];
       vv = v[idx];
     }
-    __syncthreads();
   }
   if (valid && active) {
     float gi = gv;
@@ -176,44 +172,56 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
     const float denom = sqrtf(vv) / bc2_sqrt + eps;
     p[idx] = pv - step_size * (mv / denom);
   }
-  // the last workgroup advances the active segments' step counts and writes
-  // the next launch's bias corrections (torch.optim.Adam: lr / (1 - b1^t),
-  // sqrt(1 - b2^t), in double)
-  if (tid == 0 && atomicAdd(done, 1) == int(gridDim.x) - 1) {
-    for (int s = 0; s < nseg; ++s) {
-      float st = *segs.step[s];
-      if (segs.gate[s] == nullptr || *segs.gate[s] != 0) {
-        st += 1.f;
-        *segs.step[s] = st;
-      }
-      const double tn = double(st) + 1.0;
-      coef[2 * s] = float(double(lr) / (1.0 - pow(double(b1), tn)));
-      coef[2 * s + 1] = float(sqrt(1.0 - pow(double(b2), tn)));
-    }
-    *done = 0;
+}
+
+// One lane: advance the open segments' step counts and write the bias
+// corrections of the step they are now at (torch.optim.Adam: the count is
+// incremented first, then lr / (1 - b1^t) and sqrt(1 - b2^t) in double).
+// A closed segment keeps its count; its coef (for the next count) is unused.
+__global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, float lr, float b1, float b2) {
+  if (threadIdx.x != 0) return;
+  for (int s = 0; s < nseg; ++s) {
+    const float st = *segs.step[s];
+    const bool open = segs.gate[s] == nullptr || *segs.gate[s] != 0;
+    if (open) *segs.step[s] = st + 1.f;
+    const double t = double(st) + 1.0;
+    coef[2 * s] = float(double(lr) / (1.0 - pow(double(b1), t)));
+    coef[2 * s + 1] = float(sqrt(1.0 - pow(double(b2), t)));
   }
+}
+
+AdamSegs make_segs(int nseg, float *const *steps, const int32_t *const *gates) {
+  AdamSegs segs{};
+  for (int s = 0; s < nseg; ++s) {
+    segs.step[s] = steps != nullptr ? steps[s] : nullptr;
+    segs.gate[s] = gates != nullptr ? gates[s] : nullptr;
+  }
+  return segs;
 }
 
 }  // namespace
 
 extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, int32_t num_tiles,
                              const int32_t *num_roots, float *param, float *grad, float *exp_avg, float *exp_avg_sq,
-                             int32_t nseg, float *const *steps, const int32_t *const *gates, float *coef,
-                             int32_t *done, float lr, float beta1, float beta2, float eps, float weight_decay,
-                             hipStream_t stream) {
+                             int32_t nseg, const int32_t *const *gates, const float *coef, float beta1, float beta2,
+                             float eps, float weight_decay, hipStream_t stream) {
   SGL_REQUIRE(num_tiles >= 0, "grad_adam: num_tiles < 0");
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "grad_adam: nseg %d out of range", nseg);
   if (num_tiles == 0) return SGL_OK;
-  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && steps && coef && done,
-              "grad_adam: NULL array");
-  AdamSegs segs{};
-  for (int s = 0; s < nseg; ++s) {
-    SGL_REQUIRE(steps[s] != nullptr, "grad_adam: NULL step counter %d", s);
-    segs.step[s] = steps[s];
-    segs.gate[s] = gates != nullptr ? gates[s] : nullptr;
-  }
+  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && coef, "grad_adam: NULL array");
   sgl::launch(&k_grad_adam, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, num_roots, param,
-              grad, exp_avg, exp_avg_sq, nseg, segs, coef, done, lr, beta1, beta2, eps, weight_decay);
+              grad, exp_avg, exp_avg_sq, make_segs(nseg, nullptr, gates), coef, beta1, beta2, eps, weight_decay);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+extern "C" int sgl_adam_coef(int32_t nseg, float *const *steps, const int32_t *const *gates, float *coef, float lr,
+                             float beta1, float beta2, hipStream_t stream) {
+  SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "adam_coef: nseg %d out of range", nseg);
+  SGL_REQUIRE(steps != nullptr && coef != nullptr, "adam_coef: NULL array");
+  for (int s = 0; s < nseg; ++s) SGL_REQUIRE(steps[s] != nullptr, "adam_coef: NULL step counter %d", s);
+  sgl::launch(&k_adam_coef, dim3(1), dim3(64), 0, stream, int(nseg), make_segs(nseg, steps, gates), coef, lr, beta1,
+              beta2);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -10,8 +10,9 @@
 // commit only needs step t-1's backward (the last reader of the memory
 // table) to be done, so the front stream runs ahead, and the commit of step
 // t runs beside step t-1's Adam. The streams order themselves through three
-// device words (stream memory operations: a write after the stream's prior
-// work, a wait that holds the stream until the word reaches a value):
+// device words (a one-lane signal kernel stores a number once the stream's
+// earlier kernels are done; a one-lane wait kernel holds the stream until
+// the word reaches a value):
 //
 //   front:  wait(back >= need_back) -> front ops -> wait(bwd >= need_bwd)
 //           -> commit -> write(fronted = seq)
@@ -20,8 +21,8 @@
 //
 // Plain launches cost the GPU well under a microsecond between kernels; the
 // same kernels replayed as graphs cost several, and more at graph
-// boundaries; stream memory operations resolve faster than events between
-// streams.
+// boundaries; the signal / wait kernels cost less than ROCm's stream memory
+// operations or events between streams.
 #include <cstring>
 #include <type_traits>
 #include <utility>
@@ -80,6 +81,7 @@ struct OpEntry {
 const OpEntry kOps[] = {
     SGL_OP(sgl_batch_prepare), SGL_OP(sgl_recent_sample), SGL_OP(sgl_memory_update), SGL_OP(sgl_memory_commit),
     SGL_OP(sgl_conv_forward),  SGL_OP(sgl_predictor),     SGL_OP(sgl_conv_backward), SGL_OP(sgl_grad_adam),
+    SGL_OP(sgl_adam_coef),
 };
 #undef SGL_OP
 constexpr int kNumOps = int(sizeof(kOps) / sizeof(kOps[0]));

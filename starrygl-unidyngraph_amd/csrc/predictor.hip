@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   // atomics too, so no cache writeback is needed.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) s_last = atomicAdd(done, 1) == int(gridDim.x) - 1;
+  if (tid == 0) s_last = sgl::last_block(done);
   __syncthreads();
   if (!s_last) return;
   auto take = [&](int k) {
@@ -205,10 +205,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     for (int j = tid; j < D; j += kBlock) g_wo[j] = take(j);
     if (tid == 64) g_bo[0] = take(D);
   }
-  if (tid == 0) {
-    *loss = float(double(take(D + 1)) / double(batch));
-    atomicExch(done, 0);
-  }
+  if (tid == 0) *loss = float(double(take(D + 1)) / double(batch));
 }
 
 }  // namespace

@@ -241,7 +241,7 @@ class CTDGOnlineRuntime:
         if not planned:
             src, dst, ts, ef = self._device_batch(batch)
             self._front_body(step, split, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
-            self._commit_body(step)
+            self._commit_body(step, train)
             self._back_body(step, train, n)
             self.fence()
         else:
@@ -288,9 +288,11 @@ class CTDGOnlineRuntime:
 
     def _record(self, step: DeviceStep, split: str, train: bool, n: int) -> tuple:
         """Record a full step on ``step``'s buffers as a launch plan: (ops,
-        #front, #commit, #back, #tail, entry point names, recorded calls); the
-        tail is the fused Adam. Without a memory updater the plan has no
-        commit and runs in order on one stream."""
+        #front, #commit, #back, #tail, entry point names, recorded calls); in
+        training the commit part ends with the step's Adam count advance, the
+        tail is the fused gradient + Adam update. A plan with an empty commit
+        part (evaluation without a memory updater) runs in order on one
+        stream."""
         d = self._dev
         if train:
             self._param_update(step)   # any rebuild or host-side sync happens outside the recording
@@ -298,7 +300,7 @@ class CTDGOnlineRuntime:
             self._front_body(step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"],
                              self._cursor)
         with _capi.record() as commit:
-            self._commit_body(step)
+            self._commit_body(step, train)
         with _capi.record() as back:
             self._back_body(step, train, n, update=False)
         with _capi.record() as tail:
@@ -324,9 +326,14 @@ class CTDGOnlineRuntime:
         if self._gru is not None:
             step.update_memory(self._gru, src, dst, ef, ts, from_cursor=cursor is not None)
 
-    def _commit_body(self, step: DeviceStep) -> None:
+    def _commit_body(self, step: DeviceStep, train: bool) -> None:
+        """The memory commit (which also sets the step's "block has edges"
+        gate) and, in training, the Adam step-count advance and bias
+        corrections that the step's fused update reads."""
         if self._gru is not None:
             step.commit()
+        if train:
+            self._param_update(step).advance()
 
     def _back_body(self, step: DeviceStep, train: bool, n: int, update: bool = True) -> None:
         """Attention forward, edge predictor + BCE and, in training, the
@@ -368,8 +375,6 @@ class CTDGOnlineRuntime:
             upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None])
             self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
             self._updates[id(step)] = upd
-        elif upd.version != inner.state_version:
-            upd.sync()
         return upd
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:

@@ -17,10 +17,12 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
+SGL_FIXED_SHIFT = 40    # fractional bits of the predictor's int64 gradient accumulators
+SGL_DONE_WORDS = 1088   # int32 words of sgl_predictor's completion counter
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -53,7 +55,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_plan_op_kind": (_i32, [ctypes.c_char_p, _vp]),
     "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp] + [ctypes.c_uint32] * 3
                      + [_i32, _vp, _vp]),
-    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 4 + [ctypes.c_float] * 5 + [_vp]),
+    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 2 + [ctypes.c_float] * 4 + [_vp]),
+    "sgl_adam_coef": (ctypes.c_int, [_i32] + [_vp] * 3 + [ctypes.c_float] * 3 + [_vp]),
 }
 
 _lock = threading.Lock()

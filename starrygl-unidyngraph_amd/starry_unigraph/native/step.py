@@ -20,7 +20,6 @@ the rest its back part (see the runtime's launch plans).
 from __future__ import annotations
 
 import ctypes
-import math
 from dataclasses import dataclass
 
 import torch
@@ -137,7 +136,7 @@ class StepBuffers:
         self.acc_src, self.acc_dst = z(c + 1, D, dt=i64), z(c + 1, D, dt=i64)
         self.g_src, self.g_dst = z(c + 1, D), z(c + 1, D)
         self.acc_out = z(D + 2, dt=i64)      # the predictor's loss / out_fc accumulator
-        self.pred_done = z(1, dt=i32)        # and its completion counter
+        self.pred_done = z(_capi.SGL_DONE_WORDS, dt=i32)   # and its completion counter
         self.pos = z(max(B, 1))
         self.neg = z(max(B, 1))
         self.loss = z(1)
@@ -317,11 +316,14 @@ class DeviceStep:
 
 class StepParamUpdate:
     """Weight gradients of the attention and Adam over the whole model in one
-    launch (sgl_grad_adam). The job table points at the
-    step buffers and at the optimizer's flat buffers, so it is rebuilt when
-    either is re-created. Segment 0 (the attention) is gated by the step's
-    "block has edges" flag; segment 1 (the edge predictor) takes its
-    gradients from sgl_predictor (Adam-only jobs)."""
+    launch (sgl_grad_adam), preceded by the step-count advance and bias
+    corrections (sgl_adam_coef). The job table points at the step buffers and
+    at the optimizer's flat buffers, so it is rebuilt when either is
+    re-created. Segment 0 (the attention) is gated by the step's "block has
+    edges" flag; segment 1 (the edge predictor) takes its gradients from
+    sgl_predictor (Adam-only jobs). Each step-buffer set has its own bias
+    corrections, so one step's advance may run while the previous step's
+    update still reads its own."""
 
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
                  pred_params: list[torch.Tensor], gates: list[torch.Tensor | None]):
@@ -331,11 +333,7 @@ class StepParamUpdate:
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
-        # the completion counter and the bias corrections belong to the
-        # optimizer: every update over its segments (one per step buffer)
-        # advances the same step counts
-        self.done, self.coef = opt.done, opt.coef
-        self.sync()
+        self.coef = torch.zeros(2 * len(opt.segments), dtype=torch.float32, device=dev)
         jobs, tiles = self._jobs(conv_params, pred_params)
         arr = (_capi.GradJob * len(jobs))(*jobs)
         raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
@@ -410,25 +408,22 @@ class StepParamUpdate:
             raise RuntimeError("StepParamUpdate: the predictor segment holds parameters the jobs do not cover")
         return jobs, tiles
 
-    def sync(self) -> None:
-        """Recompute the bias corrections from the step counts (in place, so
-        captured graphs stay valid); needed after the counts are restored."""
-        b1, b2 = self.opt.betas
-        coef = []
-        for _, _, stepc in self.opt.segments:
-            t = float(stepc.item()) + 1.0
-            coef += [self.opt.lr / (1.0 - b1 ** t), math.sqrt(1.0 - b2 ** t)]
-        self.coef.copy_(torch.tensor(coef, dtype=torch.float32))
-        self.version = self.opt.state_version
-
-    def run(self) -> None:
-        """Gradients + Adam (the gated step counts advance in the same launch)."""
+    def advance(self) -> None:
+        """Advance the open segments' step counts and write this step's bias
+        corrections (after the step's gates are written)."""
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
         b1, b2 = opt.betas
-        self.step._call("param_update", lambda: _capi.check(_capi.call("sgl_grad_adam", 
-            P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots), P(opt.flat),
-            P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._steps, self._gates,
-            P(self.coef), P(self.done), opt.lr, b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
+        _capi.check(_capi.call("sgl_adam_coef", len(opt.segments), self._steps, self._gates, P(self.coef), opt.lr,
+                               b1, b2, s), "sgl_adam_coef")
+
+    def run(self) -> None:
+        """Gradients + Adam with the bias corrections of the last advance()."""
+        opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
+        b1, b2 = opt.betas
+        self.step._call("param_update", lambda: _capi.check(_capi.call(
+            "sgl_grad_adam", P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots),
+            P(opt.flat), P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._gates,
+            P(self.coef), b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
 
 
 class ConvFunction(torch.autograd.Function):
@@ -476,15 +471,6 @@ class FusedAdam:
                 off += k
             self.segments.append((start, off - start, torch.zeros(1, dtype=torch.float32, device=dev)))
         self.params = params
-        self.state_version = 0   # bumped when the step counts are restored
-        # fused-update state (sgl_grad_adam): a completion counter and, per
-        # segment, the bias corrections of its next step, torch.optim.Adam's
-        # lr / (1 - b1^t) and sqrt(1 - b2^t) (kept current by the kernel)
-        self.done = torch.zeros(1, dtype=torch.int32, device=dev)
-        self.coef = torch.zeros(2 * len(self.segments), dtype=torch.float32, device=dev)
-
-    def mark_state_changed(self) -> None:
-        self.state_version += 1
 
     def zero_grad(self, set_to_none: bool = False) -> None:
         self.flat_grad.zero_()
@@ -500,7 +486,6 @@ class FusedAdam:
                                           P(self.exp_avg[start:start + n]), P(self.exp_avg_sq[start:start + n]),
                                           P(stepc), P(gate), self.lr, b1, b2, self.eps, self.wd, s), "sgl_adam_step")
             _capi.check(lib.sgl_adam_advance(P(stepc), P(gate), s), "sgl_adam_advance")
-        self.mark_state_changed()   # the fused update's bias corrections follow the new counts
 
     def state_dict(self) -> dict:
         return {"exp_avg": self.exp_avg.clone(), "exp_avg_sq": self.exp_avg_sq.clone(),
@@ -511,4 +496,3 @@ class FusedAdam:
         self.exp_avg_sq.copy_(sd["exp_avg_sq"])
         for seg, st in zip(self.segments, sd["steps"]):
             seg[2].copy_(st)
-        self.mark_state_changed()

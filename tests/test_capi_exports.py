@@ -105,6 +105,24 @@ def test_plan_op_struct_layout_matches_header(tmp_path):
     assert got == want
 
 
+def test_header_constants_match_binding(tmp_path):
+    """The binding's copies of the header's constants (ABI version, device
+    error bits, fixed-point scale, completion-counter size) are the header's."""
+    from starry_unigraph.lib import _capi
+    names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
+             "SGL_OP_MAX_ARGS"]
+    src = tmp_path / "consts.cpp"
+    src.write_text('#include <cstdio>\n#include "starrygl_mi355x.h"\nint main() {\n'
+                   + "".join(f'  printf("%d ", int({n}));\n' for n in names) + "  return 0;\n}\n")
+    exe = tmp_path / "consts"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_FIXED_SHIFT,
+            _capi.SGL_DONE_WORDS, _capi.SGL_OP_MAX_ARGS]
+    assert got == want
+
+
 def test_plan_recording_and_packing():
     """Recorded calls pack into sgl_op slots as the library's op table expects
     (no launch: a recording intercepts the calls): every plannable entry point
@@ -117,7 +135,7 @@ def test_plan_recording_and_packing():
     from starry_unigraph.lib import _capi
     L = _capi.lib()
     plannable = ["sgl_batch_prepare", "sgl_recent_sample", "sgl_memory_update", "sgl_memory_commit",
-                 "sgl_conv_forward", "sgl_predictor", "sgl_conv_backward", "sgl_grad_adam"]
+                 "sgl_conv_forward", "sgl_predictor", "sgl_conv_backward", "sgl_grad_adam", "sgl_adam_coef"]
     for name in plannable:
         n = ctypes.c_int32(-1)
         assert L.sgl_plan_op_kind(name.encode(), ctypes.byref(n)) >= 0, name
@@ -133,7 +151,7 @@ def test_plan_recording_and_packing():
             args.append(-3)
         else:
             args.append(0xABC0)
-    args[9] = host_arr          # steps: a host array of device pointers
+    args[9] = host_arr          # gates: a host array of device pointers
     args[3] = None              # a NULL pointer
     with _capi.record() as calls:
         assert _capi.call("sgl_grad_adam", *args, 0xDEAD) == 0

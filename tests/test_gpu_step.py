@@ -420,7 +420,7 @@ def test_pipelined_steps_match_eager(gpu):
 
 
 def test_fused_update_matches_torch_adam(gpu):
-    """sgl_adam_prepare + sgl_grad_adam: the parameters after a runtime train
+    """sgl_adam_coef + sgl_grad_adam: the parameters after a runtime train
     step equal torch.optim.Adam applied (in fp32 on the CPU) to the parameters,
     moments and step count before it with the gradients the kernel wrote; the
     attention segment is skipped when the block has no edges."""
