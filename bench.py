@@ -257,7 +257,7 @@ HBM_TRAFFIC = {("cfg4", "conv_backward"): (2334 + 1801) * 1024}
 # step stage name -> the C-ABI entry point that launches it
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
                 "memory_update": "sgl_memory_update", "memory_commit": "sgl_memory_commit",
-                "conv_forward": "sgl_conv_forward", "predictor": "sgl_predictor",
+                "edge_rows": "sgl_edge_rows", "conv_forward": "sgl_conv_forward", "predictor": "sgl_predictor",
                 "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam"}
 
 
@@ -281,6 +281,10 @@ def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str,
         return "mfma", float(U) * 2 * (D * (D + T) + 2 * D * C + 2 * D * D) + float(U + 1) * 2 * 2 * D * D
     if name == "memory_commit":
         return "hbm", float(U) * (8 + 4 * D * 2 + 4)
+    if name == "edge_rows":
+        # per sampled edge: nbr, eid, dt read, the memory row and edge feature gathered, X row and sines
+        # written; per root its count
+        return "hbm", float(E) * (12 + 4 * D + 4 * F + 4 * C + 4 * T) + float(U) * 4
     if name == "recent_sample":
         return "hbm", float(U) * (12 + 16 + 8 * 8 + 4) + float(E) * 28
     if name == "batch_prepare":
@@ -464,8 +468,8 @@ def main() -> None:
                     help="run steps eagerly (one library call at a time) instead of as recorded launch plans")
     ap.add_argument("--workload", default="tgn-large", choices=sorted(list(WORKLOADS) + ["sampler"]))
     ap.add_argument("--roofline-kernel", default="conv_backward",
-                    choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "conv_forward",
-                             "conv_backward"])
+                    choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "edge_rows",
+                             "conv_forward", "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--copy-probe-mb", type=int, default=0,

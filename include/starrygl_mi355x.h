@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 4
+#define SGL_ABI_VERSION 5
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -200,18 +200,18 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * build_dgl_block (models.py:144-197), one tile of sgl_conv_tile_rows()
  * roots per workgroup.
  * Inputs per root r < U: h_root[r] (its updated memory), its padded hop-0
- * window (cnt[r], nbr/eid/dt rows of the sampler); neighbour features come
- * from the committed memory table and efeat [num_edges][F].
+ * window (cnt[r] sampled slots of fanout) and that window's edge rows from
+ * sgl_edge_rows: X [cap][fanout][D+F+T] = [memory[nbr] | efeat[eid] |
+ * cos(te_w * dt + te_b)] and (backward) S [cap][fanout][T] = the sines;
+ * the backward also reads the sampler's dt rows [cap][fanout].
  * Parameters use nn.Linear layouts: w_q [D][D+T], w_k/w_v [D][D+F+T],
- * w_out [D][2D], ln_g/ln_b [D], te_w/te_b [T]. capacity % 16 == 0.
+ * w_out [D][2D], ln_g/ln_b [D], te_b [T]. capacity % 16 == 0.
  * Forward writes y [capacity][D] plus the saved state the backward needs
  * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
  * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows of y
  * >= U are zero, rows of the saved state >= U are left unwritten. If
  * any_edges == 0 the whole output and saved state are zero (models.py:88-89).
- * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding;
- * sv_trig [cap][fanout][2][T] each sampled edge's time encoding cos and sin
- * (may be NULL in a forward without backward); the backward reads it.
+ * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding.
  * Backward takes dL/dy as gy [cap][D], or (gy NULL) as W_s^T g_src + W_d^T
  * g_dst from sgl_predictor's per-root rows and the predictor's src_fc /
  * dst_fc weights w_s, w_d [D][D]: it reads the fixed-point accumulators
@@ -224,6 +224,22 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * te_part [cap/R][2][T] (time-encoding w, b; the b part includes the
  * query's cos(b) term through w_q), R = sgl_conv_tile_rows(D, F, T, H).
  * ------------------------------------------------------------------------- */
+/* Edge rows of the attention's neighbour windows, built once per step after
+ * the memory commit: for every root r < U (device) and sampled slot e <
+ * cnt[r], row r*fanout + e of X [capacity*fanout][D+F+T] becomes
+ * [memory[nbr] | efeat[eid] | cos(te_w * dt + te_b)] and the same row of
+ * S [capacity*fanout][T] sin(te_w * dt + te_b) (the argument rounded as
+ * fl(fl(dt * w) + b), TimeEncode of runtime/modules/time_encode.py:41-58);
+ * nbr, eid, dt are the sampler's padded rows. Padding slots are not
+ * written. Replaces the per-edge feature assembly of
+ * TemporalTransformerConv.forward (models.py:77-137 over the block of
+ * models.py:144-197). */
+int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
+                  int64_t capacity, const int32_t *num_roots,
+                  const float *memory, const float *efeat,
+                  const int32_t *cnt, const int32_t *nbr, const int32_t *eid,
+                  const float *dt, const float *te_w, const float *te_b,
+                  float *X, float *S, hipStream_t stream);
 /* Roots per attention workgroup for these dimensions (4 or 8; a divisor of
  * 16), i.e. the row count of one ln_part / te_part tile; 0 if the
  * dimensions are unsupported. */
@@ -231,34 +247,28 @@ int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
 int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      int32_t fanout, int64_t capacity,
                      const int32_t *num_roots, const int32_t *any_edges,
-                     const float *h_root, const float *memory,
-                     const float *efeat, const int32_t *cnt,
-                     const int32_t *nbr, const int32_t *eid, const float *dt,
+                     const float *h_root, const int32_t *cnt, const float *X,
                      const float *w_q, const float *b_q, const float *w_k,
                      const float *b_k, const float *w_v, const float *b_v,
                      const float *w_out, const float *b_out,
-                     const float *ln_g, const float *ln_b, const float *te_w,
-                     const float *te_b, float *sv_Q, float *sv_qt,
-                     float *sv_xbar, float *sv_score, float *sv_ml,
-                     float *sv_agg, float *sv_z, float *sv_stats,
-                     float *sv_phi0, float *sv_trig, float *y,
+                     const float *ln_g, const float *ln_b, const float *te_b,
+                     float *sv_Q, float *sv_qt, float *sv_xbar,
+                     float *sv_score, float *sv_ml, float *sv_agg,
+                     float *sv_z, float *sv_stats, float *sv_phi0, float *y,
                      hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
-                      const float *memory, const float *efeat,
-                      const int32_t *cnt, const int32_t *nbr,
-                      const int32_t *eid, const float *dt, const float *w_q,
-                      const float *b_q, const float *w_k, const float *b_k,
-                      const float *w_v, const float *b_v, const float *w_out,
-                      const float *b_out, const float *ln_g, const float *ln_b,
-                      const float *te_w, const float *te_b,
+                      const int32_t *cnt, const float *X, const float *S,
+                      const float *dt, const float *w_q, const float *b_q,
+                      const float *w_k, const float *b_k, const float *w_v,
+                      const float *b_v, const float *w_out, const float *b_out,
+                      const float *ln_g, const float *ln_b, const float *te_b,
                       const float *sv_Q, const float *sv_qt,
                       const float *sv_xbar, const float *sv_score,
                       const float *sv_ml, const float *sv_agg,
                       const float *sv_z, const float *sv_stats,
-                      const float *sv_trig, const float *gy,
-                      int64_t *acc_src, int64_t *acc_dst,
+                      const float *gy, int64_t *acc_src, int64_t *acc_dst,
                       const float *w_s, const float *w_d,
                       float *g_src, float *g_dst,
                       float *gz, float *gagg, float *G,

@@ -19,19 +19,21 @@
 // 2H dot/axpy passes over C floats remain.
 //
 // Latency structure: a step has a few hundred roots, and every phase is a
-// chain of L2 round trips. A workgroup takes few roots (RPW = 4 or 8; the
-// MFMA tiles keep 16 rows, zero-padded), so a launch spreads over U/RPW
+// chain of L2 round trips. The edge rows X_e (and the sines of their time
+// encodings, for the backward) are built beforehand by k_edge_rows, one wave
+// per sampled edge, in the padded sampler layout [root][slot], so the
+// attention kernels read each edge's row contiguously instead of chasing
+// (nbr, eid) to the memory table. A workgroup takes few roots (RPW = 4 or 8;
+// the MFMA tiles keep 16 rows, zero-padded), so a launch spreads over U/RPW
 // workgroups. The GEMMs issue all weight loads of a block at once (mfma.h).
 // In the edge phase WPR = waves / RPW waves share a root: each takes a
-// contiguous slice of the window, reads its slice's (nbr, eid, dt) with one
-// load per lane and gathers the X rows of 4 edges per round trip, with its own
-// online softmax (running max, running sum); the slices are merged through
-// LDS (global max, rescaled sums). The backward splits the window the same
-// way and sums the slices' gradient partials.
+// contiguous slice of the window and reads the rows of 4 edges per round
+// trip, with its own online softmax (running max, running sum); the slices
+// are merged through LDS (global max, rescaled sums). The backward splits the
+// window the same way and sums the slices' gradient partials.
 //
 // No 1/sqrt(d) scaling (models.py:125). The time-encoding argument is
-// fl(fl(dt * w) + b), then cos. The forward saves each edge's cos and sin;
-// the backward reads them instead of recomputing.
+// fl(fl(dt * w) + b), then cos.
 #include <climits>
 
 #include "common.h"
@@ -96,38 +98,59 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
   cs = q == 0 ? cp : q == 1 ? -sp : q == 2 ? -cp : sp;
 }
 
-// This lane's slice of X_e: c = lane + 64*j, and of the time columns' sines.
-// te_w / te_b are the time encoding's parameters staged in LDS. With
-// LOAD_TRIG the time columns come from `trig` (the edge's saved [cos | sin]
-// rows); otherwise they are computed, and stored to `trig` if it is given.
-template <int JM, bool LOAD_TRIG>
-__device__ __forceinline__ void load_x(const Dims &d, const float *__restrict__ memory,
-                                       const float *__restrict__ efeat, const float *__restrict__ te_w,
-                                       const float *__restrict__ te_b, float *__restrict__ trig, int nb, int ei,
-                                       float dtv, int lane, float (&x)[JM], float (&sn)[JM]) {
+// Edge rows: X[r*K + e] = [memory[nbr] | efeat[eid] | cos(w dt + b)] (C
+// floats) and S[r*K + e] = sin(w dt + b) (T floats) for every live root r <
+// U and sampled slot e < cnt[r]; padding slots are not written. One wave per
+// row, four rows per workgroup; the row's loads are issued together.
+constexpr int kRowsPerBlock = 4;
+
+__global__ __launch_bounds__(64 * kRowsPerBlock) void k_edge_rows(
+    Dims d, int64_t nrows_total, const int32_t *__restrict__ num_roots, const float *__restrict__ memory,
+    const float *__restrict__ efeat, const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
+    const int32_t *__restrict__ eid, const float *__restrict__ dt, const float *__restrict__ te_w,
+    const float *__restrict__ te_b, float *__restrict__ X, float *__restrict__ S) {
+  const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= nrows_total) return;
+  const int64_t r = row / d.k;
+  const int e = int(row - r * d.k);
+  // issued together: the live-row test and the row's sampler entries
+  const int U = *num_roots, ne = cnt[r];
+  const int nb = nbr[row], ei = eid[row];
+  const float dtv = dt[row];
+  if (r >= U || e >= ne) return;
+  float v[kMaxJ];
+#pragma unroll
+  for (int j = 0; j < kMaxJ; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = 0.f;
+    if (c < d.D) {
+      v[j] = memory[size_t(nb) * d.D + c];
+    } else if (c < d.D + d.F) {
+      v[j] = efeat[size_t(ei) * d.F + (c - d.D)];
+    } else if (c < d.C) {
+      const int t = c - d.D - d.F;
+      float sn, cs;
+      te_sincos(te_arg(dtv, te_w[t], te_b[t]), sn, cs);
+      v[j] = cs;
+      S[size_t(row) * d.T + t] = sn;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxJ; ++j) {
+    const int c = lane + 64 * j;
+    if (c < d.C) X[size_t(row) * d.C + c] = v[j];
+  }
+}
+
+// This lane's slice of edge row `row` of X (c = lane + 64*j; zero past C).
+template <int JM>
+__device__ __forceinline__ void load_row(const Dims &d, const float *__restrict__ X, size_t row, int lane,
+                                         float (&x)[JM]) {
 #pragma unroll
   for (int j = 0; j < JM; ++j) {
     const int c = lane + 64 * j;
-    float v = 0.f, w = 0.f;
-    if (c < d.D) {
-      v = memory[size_t(nb) * d.D + c];
-    } else if (c < d.D + d.F) {
-      v = efeat[size_t(ei) * d.F + (c - d.D)];
-    } else if (c < d.C) {
-      const int t = c - d.D - d.F;
-      if (LOAD_TRIG) {
-        v = trig[t];
-        w = trig[d.T + t];
-      } else {
-        te_sincos(te_arg(dtv, te_w[t], te_b[t]), w, v);
-        if (trig != nullptr) {
-          trig[t] = v;
-          trig[d.T + t] = w;
-        }
-      }
-    }
-    x[j] = v;
-    sn[j] = w;
+    x[j] = c < d.C ? X[row * d.C + c] : 0.f;
   }
 }
 
@@ -152,7 +175,6 @@ struct ConvSaved {
   float *z;      // [cap][D]     pre-ReLU output projection
   float *stats;  // [cap][2]     LayerNorm mean, rstd
   float *phi0;   // [T]          cos(b): the query's time encoding (may be NULL)
-  float *trig;   // [cap][k][2][T] each edge's time encoding cos and sin (may be NULL)
 };
 
 struct FwdLds {
@@ -163,7 +185,6 @@ struct FwdLds {
   float *Zs;    // [16][ldr]
   float *QT;    // [16][ldq]  qt, then xbar
   float *qb;    // [16][H]
-  float *TW, *TB;  // [T] time-encoding weight / bias
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][2] a slice's running max and sum (slices only)
 };
@@ -180,9 +201,7 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.Zs = L.AH + kRows * L.lda;
   L.QT = L.Zs + kRows * L.ldr;
   L.qb = L.QT + kRows * L.ldq;
-  L.TW = L.qb + kRows * d.H;
-  L.TB = L.TW + d.T;
-  L.part = L.TB + d.T;
+  L.part = L.qb + kRows * d.H;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   return L;
 }
@@ -196,10 +215,8 @@ inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices) {
 template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
-    const float *__restrict__ h_root, const float *__restrict__ memory,
-    const float *__restrict__ efeat, const int32_t *__restrict__ cnt,
-    const int32_t *__restrict__ nbr, const int32_t *__restrict__ eid,
-    const float *__restrict__ dt, ConvParams p, ConvSaved sv, float *__restrict__ y) {
+    const float *__restrict__ h_root, const int32_t *__restrict__ cnt, const float *__restrict__ X,
+    ConvParams p, ConvSaved sv, float *__restrict__ y) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
@@ -232,10 +249,6 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
-  for (int t = tid; t < T; t += kBlock) {
-    L.TW[t] = p.te_w[t];
-    L.TB[t] = p.te_b[t];
-  }
   // HT = [h | cos(b)] (TimeEncode(0) = cos(0*w + b)); AH[:, D:] = h
   for (int idx = tid; idx < kRows * (D + T); idx += kBlock) {
     const int i = idx / (D + T), j = idx - i * (D + T);
@@ -292,27 +305,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       }
     }
     const size_t base = size_t(r) * K;
-    for (int e0 = elo; e0 < ehi; e0 += 64) {
-      const int mwin = min(64, ehi - e0);
-      int my_nb = 0, my_ei = 0;
-      float my_dt = 0.f;
-      if (lane < mwin) {
-        my_nb = nbr[base + e0 + lane];
-        my_ei = eid[base + e0 + lane];
-        my_dt = dt[base + e0 + lane];
-      }
-      for (int c0 = 0; c0 < mwin; c0 += kEC) {
-        // the chunk's edges past the window (uniform) skip their gathers,
-        // time encodings and reductions
+    {
+      for (int c0 = elo; c0 < ehi; c0 += kEC) {
+        // the chunk's rows past the window (uniform) are skipped
         float x[kEC][JM];
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
-          if (c0 + u < mwin) {
-            const int e = c0 + u;
-            float sn_unused[JM];
-            float *trig = sv.trig != nullptr ? sv.trig + (base + e0 + e) * size_t(2 * d.T) : nullptr;
-            load_x<JM, false>(d, memory, efeat, L.TW, L.TB, trig, __shfl(my_nb, e, 64), __shfl(my_ei, e, 64),
-                              __shfl(my_dt, e, 64), lane, x[u], sn_unused);
+          if (c0 + u < ehi) {
+            load_row<JM>(d, X, base + c0 + u, lane, x[u]);
           } else {
 #pragma unroll
             for (int j = 0; j < JM; ++j) x[u][j] = 0.f;
@@ -328,12 +328,12 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
             float part = 0.f;
 #pragma unroll
             for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
-            sc[u][h] = c0 + u < mwin ? wave_sum(part) + qbh[h] : 0.f;
+            sc[u][h] = c0 + u < ehi ? wave_sum(part) + qbh[h] : 0.f;
           }
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
-          if (c0 + u >= mwin) break;
-          const size_t idx = base + e0 + c0 + u;
+          if (c0 + u >= ehi) break;
+          const size_t idx = base + c0 + u;
 #pragma unroll
           for (int h = 0; h < HM; ++h) {
             if (h >= H) continue;
@@ -480,7 +480,7 @@ struct BwdLds {
   float *GZ, *GA, *GQ, *XH, *GY;  // [16][ldr]
   float *GX;                      // [16][ldq]  g_xbar, then G
   float *tep;                     // [waves][2][T]
-  float *TW, *TB;                 // [T] time-encoding weight / bias
+  float *TB;                      // [T] time-encoding bias
   float *part;                    // [NW][H*C]  a slice's G partial (slices only)
   float *psig;                    // [NW][H]    a slice's sigma partial (slices only)
 };
@@ -496,8 +496,7 @@ __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bo
   L.GY = L.XH + kRows * L.ldr;
   L.GX = L.GY + kRows * L.ldr;
   L.tep = L.GX + kRows * L.ldq;
-  L.TW = L.tep + nw * 2 * d.T;
-  L.TB = L.TW + d.T;
+  L.TB = L.tep + nw * 2 * d.T;
   L.part = L.TB + d.T;
   L.psig = L.part + (slices ? nw * d.H * d.C : 0);
   return L;
@@ -527,9 +526,8 @@ __device__ __forceinline__ void consume_rows(long long *__restrict__ acc_src, lo
 template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
-    const float *__restrict__ memory, const float *__restrict__ efeat,
-    const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
-    const int32_t *__restrict__ eid, const float *__restrict__ dt, ConvParams p,
+    const int32_t *__restrict__ cnt, const float *__restrict__ X, const float *__restrict__ S,
+    const float *__restrict__ dt, ConvParams p,
     ConvSaved sv, const float *__restrict__ gy, long long *__restrict__ acc_src,
     long long *__restrict__ acc_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
     float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g) {
@@ -569,10 +567,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
-  for (int t = tid; t < T; t += kBlock) {
-    L.TW[t] = p.te_w[t];
-    L.TB[t] = p.te_b[t];
-  }
+  for (int t = tid; t < T; t += kBlock) L.TB[t] = p.te_b[t];
   // dL/dy of the tile: given, or W_s^T g_src + W_d^T g_dst from the edge
   // predictor's per-root rows (GA / GQ are free until later phases)
   // (the two products land in GY and XH in parallel; the LayerNorm pass
@@ -701,13 +696,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     const size_t base = size_t(r) * K;
     for (int e0 = elo; e0 < ehi; e0 += 64) {
       const int mwin = min(64, ehi - e0);
-      int my_nb = 0, my_ei = 0;
       float my_dt = 0.f, my_sc[HM];
 #pragma unroll
       for (int h = 0; h < HM; ++h) my_sc[h] = 0.f;
       if (lane < mwin) {
-        my_nb = nbr[base + e0 + lane];
-        my_ei = eid[base + e0 + lane];
         my_dt = dt[base + e0 + lane];
 #pragma unroll
         for (int h = 0; h < HM; ++h)
@@ -717,9 +709,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         float x[kEC][JM], sn[kEC][JM];
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
-          const int e = min(c0 + u, mwin - 1);
-          load_x<JM, true>(d, memory, efeat, L.TW, L.TB, sv.trig + (base + e0 + e) * size_t(2 * d.T),
-                           __shfl(my_nb, e, 64), __shfl(my_ei, e, 64), 0.f, lane, x[u], sn[u]);
+          const size_t row = base + e0 + min(c0 + u, mwin - 1);
+          load_row<JM>(d, X, row, lane, x[u]);
+#pragma unroll
+          for (int j = 0; j < JM; ++j) {
+            const int t = lane + 64 * j - d.D - d.F;
+            sn[u][j] = t >= 0 && t < d.T ? S[row * d.T + t] : 0.f;
+          }
         }
         float tg[kEC][HM];  // <g_xbar_h, X_e> for the chunk's edges
 #pragma unroll
@@ -944,46 +940,65 @@ extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H
   return rows_for(waves_for(hm, jm));
 }
 
+extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, int64_t capacity,
+                             const int32_t *num_roots, const float *memory, const float *efeat, const int32_t *cnt,
+                             const int32_t *nbr, const int32_t *eid, const float *dt, const float *te_w,
+                             const float *te_b, float *X, float *S, hipStream_t stream) {
+  const Dims d{D, F, T, 1, D + F + T, D, fanout};
+  SGL_REQUIRE(D > 0 && F >= 0 && T >= 0 && d.C <= 64 * kMaxJ, "edge_rows: C = D+F+T = %d out of (0, %d]", d.C,
+              64 * kMaxJ);
+  SGL_REQUIRE(fanout >= 0 && fanout <= 4096, "edge_rows: fanout %d out of range", fanout);
+  SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX, "edge_rows: capacity %lld out of range", (long long)capacity);
+  const int64_t rows = capacity * fanout;
+  if (rows == 0) return SGL_OK;
+  SGL_REQUIRE(num_roots && memory && cnt && nbr && eid && dt && X && (F == 0 || efeat) &&
+                  (T == 0 || (te_w && te_b && S)),
+              "edge_rows: NULL array");
+  sgl::launch(&k_edge_rows, dim3(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
+              stream, d, rows, num_roots, memory, efeat, cnt, nbr, eid, dt, te_w, te_b, X, S);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
 extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int32_t fanout, int64_t capacity,
                                 const int32_t *num_roots, const int32_t *any_edges, const float *h_root,
-                                const float *memory, const float *efeat, const int32_t *cnt, const int32_t *nbr,
-                                const int32_t *eid, const float *dt, const float *w_q, const float *b_q,
+                                const int32_t *cnt, const float *X, const float *w_q, const float *b_q,
                                 const float *w_k, const float *b_k, const float *w_v, const float *b_v,
                                 const float *w_out, const float *b_out, const float *ln_g, const float *ln_b,
-                                const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
-                                float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
-                                float *sv_phi0, float *sv_trig, float *y, hipStream_t stream) {
+                                const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar, float *sv_score,
+                                float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats, float *sv_phi0, float *y,
+                                hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
-  SGL_REQUIRE(num_roots && any_edges && h_root && memory && cnt && w_q && b_q && w_k && b_k && w_v && b_v && w_out &&
-                  b_out && ln_g && ln_b && te_w && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z &&
-                  sv_stats && y && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score)),
+  SGL_REQUIRE(num_roots && any_edges && h_root && cnt && w_q && b_q && w_k && b_k && w_v && b_v && w_out && b_out &&
+                  ln_g && ln_b && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z && sv_stats && y &&
+                  (fanout == 0 || (X && sv_score)),
               "conv_forward: NULL array");
   const auto inst = pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
-  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
-  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_trig};
+  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, nullptr, te_b};
+  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
-              num_roots, any_edges, h_root, memory, efeat, cnt, nbr, eid, dt, p, sv, y);
+              num_roots, any_edges, h_root, cnt, X, p, sv, y);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
 
 extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int32_t fanout, int64_t capacity,
-                                 const int32_t *num_roots, const int32_t *any_edges, const float *memory,
-                                 const float *efeat, const int32_t *cnt, const int32_t *nbr, const int32_t *eid,
-                                 const float *dt, const float *w_q, const float *b_q, const float *w_k,
-                                 const float *b_k, const float *w_v, const float *b_v, const float *w_out,
-                                 const float *b_out, const float *ln_g, const float *ln_b, const float *te_w,
-                                 const float *te_b, const float *sv_Q, const float *sv_qt, const float *sv_xbar,
-                                 const float *sv_score, const float *sv_ml, const float *sv_agg, const float *sv_z,
-                                 const float *sv_stats, const float *sv_trig, const float *gy, int64_t *acc_src,
+                                 const int32_t *num_roots, const int32_t *any_edges, const int32_t *cnt,
+                                 const float *X, const float *S, const float *dt, const float *w_q,
+                                 const float *b_q, const float *w_k, const float *b_k, const float *w_v,
+                                 const float *b_v, const float *w_out, const float *b_out, const float *ln_g,
+                                 const float *ln_b, const float *te_b, const float *sv_Q, const float *sv_qt,
+                                 const float *sv_xbar, const float *sv_score, const float *sv_ml,
+                                 const float *sv_agg, const float *sv_z, const float *sv_stats, const float *gy,
+                                 int64_t *acc_src,
                                  int64_t *acc_dst, const float *w_s, const float *w_d, float *g_src, float *g_dst,
                                  float *gz, float *gagg, float *G, float *sigma, float *gQ, float *ln_part,
                                  float *te_part, hipStream_t stream) {
@@ -992,24 +1007,23 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
-  SGL_REQUIRE(num_roots && any_edges && memory && cnt && w_q && w_k && b_k && w_v && w_out && ln_g && te_w && te_b &&
-                  sv_qt && sv_xbar && sv_ml && sv_z && sv_stats &&
-                  (gy || (acc_src && acc_dst && w_s && w_d && g_src && g_dst)) && gz &&
-                  gagg && G && sigma && gQ && ln_part &&
-                  te_part && (F == 0 || efeat) && (fanout == 0 || (nbr && eid && dt && sv_score && sv_trig)),
+  SGL_REQUIRE(num_roots && any_edges && cnt && w_q && w_k && b_k && w_v && w_out && ln_g && te_b && sv_qt &&
+                  sv_xbar && sv_ml && sv_z && sv_stats && (gy || (acc_src && acc_dst && w_s && w_d && g_src && g_dst)) &&
+                  gz && gagg && G && sigma && gQ && ln_part && te_part &&
+                  (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_backward: NULL array");
   const auto inst = pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
   const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
-  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
+  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, nullptr, te_b};
   ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
                const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
-               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr, const_cast<float *>(sv_trig)};
+               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
-              num_roots, any_edges, memory, efeat, cnt, nbr, eid, dt, p, sv, gy,
+              num_roots, any_edges, cnt, X, S, dt, p, sv, gy,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst,
               g);
   SGL_CHECK_LAUNCH();

@@ -238,10 +238,11 @@ __device__ __forceinline__ void tile_gemm16(const float *__restrict__ A, int lda
   const int nblocks = (n_total + 15) >> 4;
   for (int nb = wave; nb < nblocks; nb += nwaves) {
     const int n0 = nb * 16;
-    f32x4 acc = mfma_block16<LAYOUT>(A, lda, W, ldw, n0, kd, n_total);
     const int col = n0 + (lane & 15);
+    // the bias is loaded before the block's k loop (one round trip less)
+    const float bv = bias != nullptr && col < n_total ? bias[col] : 0.f;
+    f32x4 acc = mfma_block16<LAYOUT>(A, lda, W, ldw, n0, kd, n_total);
     if (col < n_total) {
-      const float bv = bias != nullptr ? bias[col] : 0.f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 4 * (lane >> 4) + v;
@@ -289,10 +290,10 @@ __device__ __forceinline__ void tile_gemm16_jobs(const GemmJob (&jobs)[NJOBS], i
       first += nbj;
     }
     const int n0 = nb * 16;
-    f32x4 acc = mfma_block16<LAYOUT>(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
     const int col = n0 + (lane & 15);
+    const float bv = jb.bias != nullptr && col < jb.n_total ? jb.bias[col] : 0.f;
+    f32x4 acc = mfma_block16<LAYOUT>(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
     if (col < jb.n_total) {
-      const float bv = jb.bias != nullptr ? jb.bias[col] : 0.f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;
     }

@@ -100,10 +100,11 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     const int nblk = (D + 15) >> 4;
     for (int u = wave; u < 2 * nblk; u += kWaves) {
       const int nb = u < nblk ? u : u - nblk, n0 = nb * 16, col = n0 + (lane & 15);
+      // the bias is loaded before the block's k loop (one round trip less)
+      const float bv = col < D ? (u < nblk ? b_s[col] : b_d[col]) : 0.f;
       if (u < nblk) {
         const sgl::f32x4 acc = sgl::mfma_block16<sgl::kNT>(Es, ld, w_s, D, n0, D, D);
         if (col < D) {
-          const float bv = b_s[col];
 #pragma unroll
           for (int v = 0; v < 4; ++v) Hs[(4 * (lane >> 4) + v) * ld + col] = acc[v] + bv;
         }
@@ -111,7 +112,6 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
         sgl::f32x4 ad, an;
         sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
         if (col < D) {
-          const float bv = b_d[col];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             Hd[(4 * (lane >> 4) + v) * ld + col] = ad[v] + bv;

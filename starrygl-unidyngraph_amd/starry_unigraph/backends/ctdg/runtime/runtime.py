@@ -328,10 +328,13 @@ class CTDGOnlineRuntime:
 
     def _commit_body(self, step: DeviceStep, train: bool) -> None:
         """The memory commit (which also sets the step's "block has edges"
-        gate) and, in training, the Adam step-count advance and bias
-        corrections that the step's fused update reads."""
+        gate), the sampled edges' rows from the committed memory and, in
+        training, the Adam step-count advance and bias corrections that the
+        step's fused update reads."""
         if self._gru is not None:
             step.commit()
+        conv = self._core().conv
+        step.edge_rows(conv.time_enc.w.weight.detach(), conv.time_enc.w.bias.detach(), self._dev["edge_feat"])
         if train:
             self._param_update(step).advance()
 

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -46,8 +46,9 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
-    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 33),
-    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 44),
+    "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 12),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 27),
+    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 40),
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 21),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),

@@ -127,7 +127,10 @@ class StepBuffers:
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
         self.phi0 = z(max(dims.T, 1))
-        self.trig = z(max(c * k * 2 * dims.T, 1))   # each sampled edge's time-encoding cos, sin
+        # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)] and
+        # the sines of its time encoding (sgl_edge_rows)
+        self.X = z(max(c * k * C, 1))
+        self.S = z(max(c * k * dims.T, 1))
         self.gy = z(c, D)
         # per-root sums of the predictor's hidden-layer gradients (+ the
         # non-root-negatives row U): fixed-point accumulators the predictor
@@ -229,16 +232,25 @@ class DeviceStep:
             P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
 
     # -- attention ----------------------------------------------------------
-    def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
+    def edge_rows(self, te_w: torch.Tensor, te_b: torch.Tensor, efeat_all: torch.Tensor) -> None:
+        """The sampled edges' rows X and time-encoding sines S (sgl_edge_rows),
+        from the committed memory table: after commit(), before the attention."""
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
-        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
-        self._call("conv_forward", lambda: _capi.check(_capi.call("sgl_conv_forward", 
-            d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem), P(st.memory),
-            P(efeat_all), P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v),
-            P(b_v), P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar),
-            P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.phi0), P(b.trig), P(b.y), self._s()),
-            "sgl_conv_forward"))
+        self._call("edge_rows", lambda: _capi.check(_capi.call(
+            "sgl_edge_rows", d.D, d.F, d.T, d.fanout, b.cap, P(b.num_roots), P(st.memory), P(efeat_all),
+            P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(te_w), P(te_b), P(b.X), P(b.S), self._s()),
+            "sgl_edge_rows"))
+
+    def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
+        """The attention forward over the edge rows of the last edge_rows()."""
+        b, d, P = self.buf, self.dims, _capi.ptr
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
+        self._call("conv_forward", lambda: _capi.check(_capi.call(
+            "sgl_conv_forward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem),
+            P(b.hop.cnt), P(b.X), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out), P(ln_g),
+            P(ln_b), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats),
+            P(b.phi0), P(b.y), self._s()), "sgl_conv_forward"))
         return b.y
 
     def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None):
@@ -263,7 +275,7 @@ class DeviceStep:
         in the step buffers (the weight gradients are StepParamUpdate's).
         dL/dy is ``gy``, or (gy None) comes from the predictor's per-root rows
         with ``pred_w`` = (src_fc.weight, dst_fc.weight)."""
-        b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
+        b, d, P = self.buf, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
         if gy is not None:
@@ -272,14 +284,12 @@ class DeviceStep:
         else:
             acc_src, acc_dst, g_src, g_dst = b.acc_src, b.acc_dst, b.g_src, b.g_dst
             w_s, w_d = pred_w
-        self._call("conv_backward", lambda: _capi.check(_capi.call("sgl_conv_backward", 
-            d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(st.memory), P(efeat_all),
-            P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
-            P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score),
-            P(b.ml), P(b.agg), P(b.z), P(b.stats), P(b.trig), P(gy), P(acc_src), P(acc_dst), P(w_s), P(w_d),
-            P(g_src), P(g_dst), P(b.gz), P(b.gagg),
-            P(b.G), P(b.sigma), P(b.gQ),
-            P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
+        self._call("conv_backward", lambda: _capi.check(_capi.call(
+            "sgl_conv_backward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(hop.cnt),
+            P(b.X), P(b.S), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out), P(ln_g),
+            P(ln_b), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats),
+            P(gy), P(acc_src), P(acc_dst), P(w_s), P(w_d), P(g_src), P(g_dst), P(b.gz), P(b.gagg), P(b.G),
+            P(b.sigma), P(b.gQ), P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
 
     def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
         """The backward kernel plus the weight gradients as torch products (the
@@ -434,6 +444,7 @@ class ConvFunction(torch.autograd.Function):
         ctx.step = step
         ctx.efeat_all = efeat_all
         ctx.params = params
+        step.edge_rows(params[0], params[1], efeat_all)
         return step.conv_forward(list(params), efeat_all)
 
     @staticmethod
