@@ -154,6 +154,22 @@ __device__ __forceinline__ void load_row(const Dims &d, const float *__restrict_
   }
 }
 
+// A tile's products OUT = A * op(W) + bias: four-row MFMA strips for tiles
+// of 4 roots with k-major weights (sgl::tile_gemm4_jobs, partial sums in
+// `scratch`; a wave's weight loads are 64 consecutive floats per k), 16x16
+// blocks otherwise (for row-major weights a four-row strip would read 64
+// weight rows per load instruction). Called by every thread of the
+// workgroup.
+template <int LAYOUT, int RPW, int NJOBS>
+__device__ __forceinline__ void tile_products(const sgl::GemmJob (&jobs)[NJOBS], int nwaves, float *scratch) {
+  if constexpr (RPW == 4 && LAYOUT == sgl::kNN) {
+    sgl::tile_gemm4_jobs<LAYOUT>(jobs, nwaves, scratch);
+  } else {
+    (void)scratch;
+    sgl::tile_gemm16_jobs<LAYOUT>(jobs, nwaves);
+  }
+}
+
 // The slice [lo, hi) of a window of ne edges that slice `sub` of `nsub` takes.
 __device__ __forceinline__ void window_slice(int ne, int sub, int nsub, int &lo, int &hi) {
   const int per = (ne + nsub - 1) / nsub;
@@ -187,14 +203,15 @@ struct FwdLds {
   float *qb;    // [16][H]
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][2] a slice's running max and sum (slices only)
+  float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
 };
 
 __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bool slices) {
   FwdLds L;
-  L.ldh = d.D + d.T + 1;
-  L.ldr = d.D + 1;
-  L.lda = 2 * d.D + 1;
-  L.ldq = d.H * d.C + 1;
+  L.ldh = sgl::lds_ld(d.D + d.T);
+  L.ldr = sgl::lds_ld(d.D);
+  L.lda = sgl::lds_ld(2 * d.D);
+  L.ldq = sgl::lds_ld(d.H * d.C);
   L.HT = base;
   L.Qs = L.HT + kRows * L.ldh;
   L.AH = L.Qs + kRows * L.ldr;
@@ -203,13 +220,14 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.qb = L.QT + kRows * L.ldq;
   L.part = L.qb + kRows * d.H;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
+  L.scr = L.pml + (slices ? nw * d.H * 2 : 0);
   return L;
 }
 
 inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices) {
   float *base = reinterpret_cast<float *>(uintptr_t(4096));
   const FwdLds L = fwd_lds(d, base, nw, slices);
-  return size_t(L.pml + (slices ? nw * d.H * 2 : 0) - base);
+  return size_t(L.scr + (rows_for(nw) == 4 ? nw * 256 : 0) - base);
 }
 
 template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
@@ -220,7 +238,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
   const FwdLds L = fwd_lds(d, lds, NW, WPR > 1);
   __shared__ int s_cnt[kRows];
@@ -264,7 +282,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   __syncthreads();
   // Q = W_q [h | cos(b)] + b_q
-  sgl::tile_gemm16<sgl::kNT>(L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D, kWaves);
+  {
+    const sgl::GemmJob jobs[1] = {{L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D}};
+    tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
+  }
   __syncthreads();
   for (int idx = tid; idx < RPW * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
@@ -277,9 +298,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     L.qb[i * H + h] = acc;
   }
   // qt_h = Q_h W_k[h rows, :]  (kNN: rows of W_k are the reduction index)
-  for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNN>(L.Qs + h * dh, L.ldr, p.w_k + size_t(h) * dh * C, C, nullptr, L.QT + h * C, L.ldq,
-                               dh, C, kWaves);
+  {
+    sgl::GemmJob jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.Qs + h * dh, L.ldr, p.w_k + size_t(h) * dh * C, C, nullptr, L.QT + h * C, L.ldq, dh,
+                 h < H ? C : 0};
+    tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
+  }
   __syncthreads();
 
   // edge phase: wave w takes slice w % WPR of root w / WPR's window
@@ -426,7 +452,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     for (int h = 0; h < HM; ++h)
       jobs[h] = {L.QT + h * C, L.ldq, p.w_v + size_t(h) * dh * C, C, p.b_v + h * dh, L.AH + h * dh, L.lda, C,
                  h < H ? dh : 0};
-    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+    tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
@@ -436,7 +462,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   __syncthreads();
   // z = W_out [agg | h] + b_out
-  sgl::tile_gemm16<sgl::kNT>(L.AH, L.lda, p.w_out, 2 * D, p.b_out, L.Zs, L.ldr, 2 * D, D, kWaves);
+  {
+    const sgl::GemmJob jobs[1] = {{L.AH, L.lda, p.w_out, 2 * D, p.b_out, L.Zs, L.ldr, 2 * D, D}};
+    tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
+  }
   __syncthreads();
   // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance; one wave per row
   for (int i = wave; i < RPW; i += kWaves) {
@@ -483,12 +512,13 @@ struct BwdLds {
   float *TB;                      // [T] time-encoding bias
   float *part;                    // [NW][H*C]  a slice's G partial (slices only)
   float *psig;                    // [NW][H]    a slice's sigma partial (slices only)
+  float *scr;                     // [NW][4][64] four-row product partials (4-root tiles only)
 };
 
 __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bool slices) {
   BwdLds L;
-  L.ldr = d.D + 1;
-  L.ldq = d.H * d.C + 1;
+  L.ldr = sgl::lds_ld(d.D);
+  L.ldq = sgl::lds_ld(d.H * d.C);
   L.GZ = base;
   L.GA = L.GZ + kRows * L.ldr;
   L.GQ = L.GA + kRows * L.ldr;
@@ -499,13 +529,15 @@ __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bo
   L.TB = L.tep + nw * 2 * d.T;
   L.part = L.TB + d.T;
   L.psig = L.part + (slices ? nw * d.H * d.C : 0);
+  // 16-byte aligned for the product partials
+  L.scr = L.psig + (((slices ? nw * d.H : 0) + 3) & ~3);
   return L;
 }
 
 inline size_t bwd_lds_floats(const Dims &d, int nw, bool slices) {
   float *base = reinterpret_cast<float *>(uintptr_t(4096));
   const BwdLds L = bwd_lds(d, base, nw, slices);
-  return size_t(L.psig + (slices ? nw * d.H : 0) - base);
+  return size_t(L.scr + (rows_for(nw) == 4 ? nw * 256 : 0) - base);
 }
 
 // The edge predictor's per-root gradient rows r0 .. r0+nrows-1 (fixed-point
@@ -534,7 +566,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;
   static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
   const BwdLds L = bwd_lds(d, lds, NW, WPR > 1);
   __shared__ int s_cnt[kRows];
@@ -596,8 +628,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       L.GQ[i * L.ldr + j] = vd;
     }
     __syncthreads();
-    sgl::tile_gemm16<sgl::kNN>(L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D, kWaves / 2);
-    sgl::tile_gemm16<sgl::kNN>(L.GQ, L.ldr, w_d, D, nullptr, L.XH, L.ldr, D, D, kWaves / 2, kWaves / 2);
+    const sgl::GemmJob jobs[2] = {{L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D},
+                                  {L.GQ, L.ldr, w_d, D, nullptr, L.XH, L.ldr, D, D}};
+    tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
     __syncthreads();
   }
   // LayerNorm + ReLU backward; one wave per row (rows past the tile zeroed)
@@ -649,7 +682,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     g.gz[size_t(r0 + i) * D + j] = L.GZ[i * L.ldr + j];
   }
   // g_agg = gz W_out[:, :D]
-  sgl::tile_gemm16<sgl::kNN>(L.GZ, L.ldr, p.w_out, 2 * D, nullptr, L.GA, L.ldr, D, D, kWaves);
+  {
+    const sgl::GemmJob jobs[1] = {{L.GZ, L.ldr, p.w_out, 2 * D, nullptr, L.GA, L.ldr, D, D}};
+    tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
+  }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
@@ -658,9 +694,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
   __syncthreads();
   // g_xbar_h = g_agg_h W_v[h rows, :]
-  for (int h = 0; h < H; ++h)
-    sgl::tile_gemm16<sgl::kNN>(L.GA + h * dh, L.ldr, p.w_v + size_t(h) * dh * C, C, nullptr, L.GX + h * C, L.ldq,
-                               dh, C, kWaves);
+  {
+    sgl::GemmJob jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.GA + h * dh, L.ldr, p.w_v + size_t(h) * dh * C, C, nullptr, L.GX + h * C, L.ldq, dh,
+                 h < H ? C : 0};
+    tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
+  }
   __syncthreads();
 
   // edge backward phase: wave w takes slice w % WPR of root w / WPR's window
@@ -837,7 +878,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     for (int h = 0; h < HM; ++h)
       jobs[h] = {L.GX + h * C, L.ldq, p.w_k + size_t(h) * dh * C, C, nullptr, L.GQ + h * dh, L.ldr, C,
                  h < H ? dh : 0};
-    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kWaves);
+    tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
   __syncthreads();
   for (int idx = tid; idx < RPW * D; idx += kBlock) {

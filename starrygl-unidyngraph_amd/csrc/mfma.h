@@ -28,6 +28,13 @@ namespace sgl {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Leading dimension (floats) of an LDS row tile of x columns: a multiple of 4
+// with ld / 4 odd. 16-byte aligned rows let the MFMA blocks read A with one
+// 16-byte LDS read per k group, and the rows of a 16-row tile start in 16
+// distinct 4-bank groups, so those reads, column walks (one row per lane)
+// and the blocks' output stores are free of bank conflicts.
+__host__ __device__ constexpr int lds_ld(int x) { return ((x + 3) & ~3) | 4; }
+
 // Weight operand layouts for OUT = A * op(W):
 //   kNT: W is [N][ldw] row-major and OUT[i][n] = sum_k A[i][k] * W[n][k]   (nn.Linear weight)
 //   kNN: W is [K][ldw] row-major and OUT[i][n] = sum_k A[i][k] * W[k][n]
@@ -296,6 +303,151 @@ __device__ __forceinline__ void tile_gemm16_jobs(const GemmJob (&jobs)[NJOBS], i
     if (col < jb.n_total) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Four-row tiles (a workgroup's 4 live roots): v_mfma_f32_4x4x1_16b_f32 runs
+// 16 independent 4x4x1 blocks. With every block fed the same four A rows and
+// block b taking columns 4b..4b+3 of a 64-column strip, one instruction adds
+// a rank-1 update to 4 rows x 64 columns, so no MFMA work goes to padding
+// rows. Lane layout (16 blocks, K = 1): A[i][k] of block b comes from lane
+// 4b + i, B[k][j] from lane 4b + j, D[i][j] lands in lane 4b + j, element i.
+// So lane l supplies A[l % 4][k] and B[k][n0 + l], and holds column n0 + l of
+// the four output rows. Per 4 k a lane reads 16 bytes of A from LDS (four
+// distinct addresses per wave) and 16 bytes of its weight row (kNT) or four
+// values strided by ldw (kNN; 64 consecutive floats per k across the wave).
+// A strip's k range is split over several waves and the partial sums are
+// added through LDS, so each wave's MFMA chain is a fraction of the depth.
+
+// acc += A[0..3][k0 .. k1) * op(W)[k][n], k0 % 4 == 0; A rows past k1 read 0.
+template <int LAYOUT>
+__device__ __forceinline__ f32x4 mfma_strip4(const float *__restrict__ A, int lda, __amdgpu_buffer_rsrc_t wr,
+                                             int ldw, int n, int k0, int k1, bool wvec, bool avec) {
+  const int lane = threadIdx.x & 63;
+  const float *arow = A + (lane & 3) * lda;
+  constexpr int kG = 8;  // groups of 4 k per load batch
+  // A for the group at k (LDS; k past k1 reads 0)
+  auto load_a = [&](float (&a)[4], int k) {
+    if (avec && k + 4 <= k1) {
+      const f32x4 v = *reinterpret_cast<const f32x4 *>(arow + k);
+      a[0] = v[0]; a[1] = v[1]; a[2] = v[2]; a[3] = v[3];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float v = arow[min(k + t, k1 - 1)];
+        a[t] = k + t < k1 ? v : 0.f;
+      }
+    }
+  };
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  for (int kb = k0; kb < k1; kb += 4 * kG) {
+    // the batch's weights are loaded together, A one group ahead of its MFMAs
+    float w[kG][4];
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      const int k = kb + 4 * g;
+      if (k >= k1) break;  // uniform
+      if (LAYOUT == kNT && wvec) {
+        const f32x4 v = buf_load4(wr, uint32_t(n) * uint32_t(ldw) + uint32_t(k));
+        w[g][0] = v[0]; w[g][1] = v[1]; w[g][2] = v[2]; w[g][3] = v[3];
+      } else if (LAYOUT == kNT) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[g][t] = buf_load(wr, uint32_t(n) * uint32_t(ldw) + uint32_t(k + t));
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[g][t] = buf_load(wr, uint32_t(k + t) * uint32_t(ldw) + uint32_t(n));
+      }
+    }
+    float a0[4], a1[4];
+    load_a(a0, kb);
+#pragma unroll
+    for (int g = 0; g < kG; ++g) {
+      if (kb + 4 * g >= k1) break;
+      float (&cur)[4] = (g & 1) ? a1 : a0;
+      float (&nxt)[4] = (g & 1) ? a0 : a1;
+      if (g + 1 < kG && kb + 4 * (g + 1) < k1) load_a(nxt, kb + 4 * (g + 1));
+      acc0 = __builtin_amdgcn_mfma_f32_4x4x1f32(cur[0], w[g][0], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_4x4x1f32(cur[1], w[g][1], acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_4x4x1f32(cur[2], w[g][2], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_4x4x1f32(cur[3], w[g][3], acc1, 0, 0, 0);
+    }
+  }
+  return acc0 + acc1;
+}
+
+// OUT[0..3][n] (LDS, ldo) = A[0..3] * op(W) + bias for every job (GemmJob;
+// only rows 0..3 of A and OUT are touched). The jobs' 64-column strips are
+// dealt over the waves, each strip's k range split into `parts` slices of a
+// multiple of 4 (parts = nwaves / strips, at least 1); with parts > 1 the
+// slices' sums go through scratch (LDS, nwaves * 256 floats) and a barrier,
+// so all threads of the workgroup must call this. Without a barrier at the
+// end: the caller synchronises before reading OUT.
+template <int LAYOUT, int NJOBS>
+__device__ __forceinline__ void tile_gemm4_jobs(const GemmJob (&jobs)[NJOBS], int nwaves,
+                                                float *__restrict__ scratch) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int strips = 0;
+#pragma unroll
+  for (int j = 0; j < NJOBS; ++j) strips += (jobs[j].n_total + 63) >> 6;
+  const int parts = max(1, nwaves / max(strips, 1));
+  // Items (strip, part) are numbered job by job; wave w takes items w,
+  // w + nwaves, ... Each job is handled by its own unrolled code (constant
+  // indices into jobs[]: a dynamically indexed job table would live in
+  // scratch memory).
+  int first = 0;  // the job's first item
+#pragma unroll
+  for (int j = 0; j < NJOBS; ++j) {
+    const GemmJob &jb = jobs[j];
+    const int nitems = ((jb.n_total + 63) >> 6) * parts;
+    int it = wave;
+    if (it < first) it += ((first - it + nwaves - 1) / nwaves) * nwaves;
+    for (; it < first + nitems; it += nwaves) {
+      const int local = it - first, sl = local / parts, p = local - sl * parts;
+      const int n = sl * 64 + lane;
+      const int per = ((jb.kd + parts - 1) / parts + 3) & ~3;
+      const int k0 = min(jb.kd, p * per), k1 = min(jb.kd, k0 + per);
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (k0 < k1) {
+        const uint32_t span = LAYOUT == kNT ? uint32_t(jb.n_total - 1) * uint32_t(jb.ldw) + uint32_t(jb.kd)
+                                            : uint32_t(jb.kd - 1) * uint32_t(jb.ldw) + uint32_t(jb.n_total);
+        const __amdgpu_buffer_rsrc_t wr = weight_rsrc(jb.W, span);
+        const bool wvec = LAYOUT == kNT && (jb.kd & 3) == 0 && (jb.ldw & 3) == 0 && aligned16(jb.W);
+        const bool avec = (jb.lda & 3) == 0 && aligned16(jb.A);
+        acc = mfma_strip4<LAYOUT>(jb.A, jb.lda, wr, jb.ldw, n, k0, k1, wvec, avec);
+      }
+      if (parts == 1) {
+        if (n < jb.n_total) {
+          const float bv = jb.bias != nullptr ? jb.bias[n] : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) jb.OUT[i * jb.ldo + n] = acc[i] + bv;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) scratch[(it * 4 + i) * 64 + lane] = acc[i];
+      }
+    }
+    first += nitems;
+  }
+  if (parts > 1) {
+    __syncthreads();
+    int sfirst = 0;  // the job's first strip
+#pragma unroll
+    for (int j = 0; j < NJOBS; ++j) {
+      const GemmJob &jb = jobs[j];
+      const int sj = (jb.n_total + 63) >> 6;
+      for (int idx = threadIdx.x; idx < sj * 256; idx += nwaves * 64) {
+        const int sl = idx >> 8, i = (idx >> 6) & 3, l = idx & 63;
+        const int n = sl * 64 + l;
+        if (n < jb.n_total) {
+          float v = jb.bias != nullptr ? jb.bias[n] : 0.f;
+          for (int p = 0; p < parts; ++p) v += scratch[(((sfirst + sl) * parts + p) * 4 + i) * 64 + l];
+          jb.OUT[i * jb.ldo + n] = v;
+        }
+      }
+      sfirst += sj;
     }
   }
 }

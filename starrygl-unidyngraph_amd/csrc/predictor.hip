@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     long long *__restrict__ acc_src, long long *__restrict__ acc_dst, float *__restrict__ g_wo,
     float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done) {
   extern __shared__ __align__(16) float lds[];
-  const int ld = D + 1;
+  const int ld = sgl::lds_ld(D);
   long long *Nul = reinterpret_cast<long long *>(lds);  // [D] dL/dh_n of the tile's non-root negatives
   float *Es = lds + 2 * ((D + 1) & ~1);
   float *Ed = Es + kRows * ld;
@@ -227,7 +227,7 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
-  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * (D + 1) + 2 * ((D + 1) & ~1) + D);
+  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * sgl::lds_ld(D) + 2 * ((D + 1) & ~1) + D);
   SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
   sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,

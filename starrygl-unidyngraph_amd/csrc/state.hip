@@ -361,10 +361,10 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     const unsigned long long *__restrict__ win_src,
     const unsigned long long *__restrict__ win_dst, const int32_t *__restrict__ cnt_src,
     const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
-  extern __shared__ float lds[];
+  extern __shared__ __align__(16) float lds[];
   const int S = 2 * D + F;
   const int G = 3 * D;
-  const int ldx = S + 1, ldh = D + 1, ldg = G + 1;
+  const int ldx = sgl::lds_ld(S), ldh = sgl::lds_ld(D), ldg = sgl::lds_ld(G);
   float *xs = lds;
   float *hs = xs + kTileRows * ldx;
   float *ms = hs + kTileRows * ldh;
@@ -568,7 +568,7 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
 
 extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {
   const size_t S = size_t(2 * D + F), G = size_t(3 * D);
-  return sizeof(float) * kTileRows * ((S + 1) + 2 * (D + 1) + 2 * (G + 1));
+  return sizeof(float) * kTileRows * (sgl::lds_ld(int(S)) + 2 * sgl::lds_ld(D) + 2 * sgl::lds_ld(int(G)));
 }
 
 extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
