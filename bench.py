@@ -282,9 +282,9 @@ def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str,
     if name == "memory_commit":
         return "hbm", float(U) * (8 + 4 * D * 2 + 4)
     if name == "edge_rows":
-        # per sampled edge: nbr, eid, dt read, the memory row and edge feature gathered, X row and sines
-        # written; per root its count
-        return "hbm", float(E) * (12 + 4 * D + 4 * F + 4 * C + 4 * T) + float(U) * 4
+        # per sampled edge: nbr, eid read, the memory row and edge feature gathered and written into the
+        # edge's row; per root its count
+        return "hbm", float(E) * (8 + 8 * D + 8 * F) + float(U) * 4
     if name == "recent_sample":
         return "hbm", float(U) * (12 + 16 + 8 * 8 + 4) + float(E) * 28
     if name == "batch_prepare":

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 5
+#define SGL_ABI_VERSION 6
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -200,12 +200,14 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * build_dgl_block (models.py:144-197), one tile of sgl_conv_tile_rows()
  * roots per workgroup.
  * Inputs per root r < U: h_root[r] (its updated memory), its padded hop-0
- * window (cnt[r] sampled slots of fanout) and that window's edge rows from
- * sgl_edge_rows: X [cap][fanout][D+F+T] = [memory[nbr] | efeat[eid] |
- * cos(te_w * dt + te_b)] and (backward) S [cap][fanout][T] = the sines;
- * the backward also reads the sampler's dt rows [cap][fanout].
+ * window (cnt[r] sampled slots of fanout, the sampler's dt rows
+ * [cap][fanout]) and that window's edge rows X [cap][fanout][D+F+T], whose
+ * first D+F columns [memory[nbr] | efeat[eid]] come from sgl_edge_rows. The
+ * forward computes the time encodings cos(te_w * dt + te_b) (argument
+ * rounded as fl(fl(dt * w) + b)), writes them into the rows' last T columns
+ * and their sines into S [cap][fanout][T]; the backward reads X and S.
  * Parameters use nn.Linear layouts: w_q [D][D+T], w_k/w_v [D][D+F+T],
- * w_out [D][2D], ln_g/ln_b [D], te_b [T]. capacity % 16 == 0.
+ * w_out [D][2D], ln_g/ln_b [D], te_w/te_b [T]. capacity % 16 == 0.
  * Forward writes y [capacity][D] plus the saved state the backward needs
  * (sv_*: Q [cap][D], qt/xbar [cap][H][D+F+T], score [cap][fanout][H],
  * ml [cap][H][2], agg [cap][D], z [cap][D], stats [cap][2]); rows of y
@@ -226,20 +228,18 @@ int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
  * ------------------------------------------------------------------------- */
 /* Edge rows of the attention's neighbour windows, built once per step after
  * the memory commit: for every root r < U (device) and sampled slot e <
- * cnt[r], row r*fanout + e of X [capacity*fanout][D+F+T] becomes
- * [memory[nbr] | efeat[eid] | cos(te_w * dt + te_b)] and the same row of
- * S [capacity*fanout][T] sin(te_w * dt + te_b) (the argument rounded as
- * fl(fl(dt * w) + b), TimeEncode of runtime/modules/time_encode.py:41-58);
- * nbr, eid, dt are the sampler's padded rows. Padding slots are not
- * written. Replaces the per-edge feature assembly of
+ * cnt[r], row r*fanout + e of X [capacity*fanout][D+F+T] gets
+ * [memory[nbr] | efeat[eid]] in its first D+F columns (nbr, eid: the
+ * sampler's padded rows); the last T columns are the forward's. Padding
+ * slots are not written. Replaces the per-edge feature assembly of
  * TemporalTransformerConv.forward (models.py:77-137 over the block of
- * models.py:144-197). */
+ * models.py:144-197). It reads no trained parameter, so it may run beside
+ * the previous step's update. */
 int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
                   int64_t capacity, const int32_t *num_roots,
                   const float *memory, const float *efeat,
                   const int32_t *cnt, const int32_t *nbr, const int32_t *eid,
-                  const float *dt, const float *te_w, const float *te_b,
-                  float *X, float *S, hipStream_t stream);
+                  float *X, hipStream_t stream);
 /* Roots per attention workgroup for these dimensions (4 or 8; a divisor of
  * 16), i.e. the row count of one ln_part / te_part tile; 0 if the
  * dimensions are unsupported. */
@@ -247,15 +247,15 @@ int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
 int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      int32_t fanout, int64_t capacity,
                      const int32_t *num_roots, const int32_t *any_edges,
-                     const float *h_root, const int32_t *cnt, const float *X,
-                     const float *w_q, const float *b_q, const float *w_k,
-                     const float *b_k, const float *w_v, const float *b_v,
-                     const float *w_out, const float *b_out,
-                     const float *ln_g, const float *ln_b, const float *te_b,
-                     float *sv_Q, float *sv_qt, float *sv_xbar,
-                     float *sv_score, float *sv_ml, float *sv_agg,
-                     float *sv_z, float *sv_stats, float *sv_phi0, float *y,
-                     hipStream_t stream);
+                     const float *h_root, const int32_t *cnt, float *X,
+                     const float *dt, const float *w_q, const float *b_q,
+                     const float *w_k, const float *b_k, const float *w_v,
+                     const float *b_v, const float *w_out, const float *b_out,
+                     const float *ln_g, const float *ln_b, const float *te_w,
+                     const float *te_b, float *sv_Q, float *sv_qt,
+                     float *sv_xbar, float *sv_score, float *sv_ml,
+                     float *sv_agg, float *sv_z, float *sv_stats,
+                     float *sv_phi0, float *S, float *y, hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
@@ -396,34 +396,31 @@ int sgl_adam_coef(int32_t nseg, float *const *steps,
  * argument count without the trailing stream, a[i] argument i (pointers and
  * integers as their value, floats as their bit pattern in the low 32 bits).
  * sgl_plan_run enqueues, without blocking the host, ops [0, n_front) (the
- * step's front part: batch preparation, sampling, GRU), n_commit ops (the
- * memory commit), n_back ops (attention forward, predictor, backward) and
- * n_tail ops (the fused Adam), ordering the two streams through uint32
- * words in device memory (64 words, zero before the first run): sync[0] =
- * back (last back part done), sync[16] = fronted (last front part incl.
- * commit), sync[32] = bwd (last backward done), sync[48] = timeout. A write
- * is a one-lane kernel that stores the number once the stream's earlier
- * kernels are done; a wait is a one-lane kernel that polls the word and ends
- * when it reaches the value, or after about two seconds, setting timeout to
- * 1 (the ordering is then lost; the host checks that word):
- *   front stream: wait until back >= need_back, front ops,
- *                 wait until bwd >= need_bwd, commit ops, write fronted = seq
- *   back stream:  wait until fronted >= seq, back ops, write bwd = seq,
- *                 tail ops, write back = seq
+ * step's front part: batch preparation, sampling, GRU, memory commit, edge
+ * rows, Adam step counts) on the front stream and n_back ops (attention
+ * forward, predictor, backward, fused Adam) on the back stream, ordering the
+ * two streams through uint32 words in device memory (64 words, zero before
+ * the first run): sync[0] = back (last back part done), sync[16] = fronted
+ * (last front part done), sync[48] = timeout. A write is a one-lane kernel
+ * that stores the number once the stream's earlier kernels are done; a wait
+ * is a one-lane kernel that polls the word and ends when it reaches the
+ * value, or after about two seconds, setting timeout to 1 (the ordering is
+ * then lost; the host checks that word):
+ *   front stream: wait until back >= need_back, front ops, write fronted = seq
+ *   back stream:  wait until fronted >= seq, back ops, write back = seq
  * With two step-buffer sets used alternately, need_back is the sequence
  * number of the step before the previous one (its back part read this
- * step's buffers) and need_bwd that of the previous step (its backward
- * is the last reader of the memory table the commit writes): step t+1's
- * front part overlaps step t's back part and its commit step t's Adam.
- * Sequence numbers increase (from 1, need_* < seq). Work queued on the back
- * stream between runs that the next front part depends on is published by
- * writing a fresh number v to sync[0] and sync[32] on the back stream after
- * it and passing need_back = need_bwd = v (a fence). With n_commit == 0 every
- * op runs in order on the back stream (front, sync, seq, need_* unused).
- * An op's own checks run when it is replayed; the first failing op's error
- * is returned (ops before it are already enqueued). timed_op >= 0 has that
- * op's kernel record t_start and t_end at its own start and end (see
- * sgl_time_next_launch; -1: no timing).
+ * step's buffers): step t+1's front part overlaps step t's back part. A back
+ * part must not read the memory table (the edge rows carry the neighbours'
+ * memory). Sequence numbers increase (from 1, need_back < seq). Work queued
+ * on the back stream between runs that the next front part depends on is
+ * published by writing a fresh number v to sync[0] on the back stream after
+ * it and passing need_back = v (a fence). With front NULL every op runs in
+ * order on the back stream (sync, seq, need_back unused). An op's own checks
+ * run when it is replayed; the first failing op's error is returned (ops
+ * before it are already enqueued). timed_op >= 0 has that op's kernel record
+ * t_start and t_end at its own start and end (see sgl_time_next_launch; -1:
+ * no timing).
  * ------------------------------------------------------------------------- */
 /* Has the next kernel that the calling host thread launches through one of
  * the step entry points (batch_prepare, recent_sample, memory_update,
@@ -445,10 +442,9 @@ typedef struct sgl_op {
  * is not one; *nargs (may be NULL) receives its argument count without the
  * stream. */
 int32_t sgl_plan_op_kind(const char *name, int32_t *nargs);
-int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit,
-                 int32_t n_back, int32_t n_tail, hipStream_t front,
-                 hipStream_t back, uint32_t *sync, uint32_t seq,
-                 uint32_t need_back, uint32_t need_bwd, int32_t timed_op,
+int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_back,
+                 hipStream_t front, hipStream_t back, uint32_t *sync,
+                 uint32_t seq, uint32_t need_back, int32_t timed_op,
                  hipEvent_t t_start, hipEvent_t t_end);
 
 #ifdef __cplusplus

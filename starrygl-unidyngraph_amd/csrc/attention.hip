@@ -19,11 +19,12 @@
 // 2H dot/axpy passes over C floats remain.
 //
 // Latency structure: a step has a few hundred roots, and every phase is a
-// chain of L2 round trips. The edge rows X_e (and the sines of their time
-// encodings, for the backward) are built beforehand by k_edge_rows, one wave
-// per sampled edge, in the padded sampler layout [root][slot], so the
-// attention kernels read each edge's row contiguously instead of chasing
-// (nbr, eid) to the memory table. A workgroup takes few roots (RPW = 4 or 8;
+// chain of L2 round trips. The edge rows' gathered columns [memory[nbr] |
+// efeat[eid]] are copied beforehand by k_edge_rows, one wave per sampled
+// edge, in the padded sampler layout [root][slot], so the attention kernels
+// read each edge's row contiguously instead of chasing (nbr, eid) to the
+// memory table. The forward fills in the rows' time-encoding columns (they
+// depend on trained parameters) and saves the sines for the backward. A workgroup takes few roots (RPW = 4 or 8;
 // the MFMA tiles keep 16 rows, zero-padded), so a launch spreads over U/RPW
 // workgroups. The GEMMs issue all weight loads of a block at once (mfma.h).
 // In the edge phase WPR = waves / RPW waves share a root: each takes a
@@ -98,17 +99,17 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
   cs = q == 0 ? cp : q == 1 ? -sp : q == 2 ? -cp : sp;
 }
 
-// Edge rows: X[r*K + e] = [memory[nbr] | efeat[eid] | cos(w dt + b)] (C
-// floats) and S[r*K + e] = sin(w dt + b) (T floats) for every live root r <
-// U and sampled slot e < cnt[r]; padding slots are not written. One wave per
-// row, four rows per workgroup; the row's loads are issued together.
+// Edge rows: X[r*K + e][0, D+F) = [memory[nbr] | efeat[eid]] for every live
+// root r < U and sampled slot e < cnt[r] (rows of C = D+F+T floats; padding
+// slots are not written). The time-encoding columns depend on trained
+// parameters and are filled in by the attention forward. One wave per row,
+// four rows per workgroup; the row's loads are issued together.
 constexpr int kRowsPerBlock = 4;
 
 __global__ __launch_bounds__(64 * kRowsPerBlock) void k_edge_rows(
     Dims d, int64_t nrows_total, const int32_t *__restrict__ num_roots, const float *__restrict__ memory,
     const float *__restrict__ efeat, const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
-    const int32_t *__restrict__ eid, const float *__restrict__ dt, const float *__restrict__ te_w,
-    const float *__restrict__ te_b, float *__restrict__ X, float *__restrict__ S) {
+    const int32_t *__restrict__ eid, float *__restrict__ X) {
   const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= nrows_total) return;
@@ -117,29 +118,44 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void k_edge_rows(
   // issued together: the live-row test and the row's sampler entries
   const int U = *num_roots, ne = cnt[r];
   const int nb = nbr[row], ei = eid[row];
-  const float dtv = dt[row];
   if (r >= U || e >= ne) return;
   float v[kMaxJ];
 #pragma unroll
   for (int j = 0; j < kMaxJ; ++j) {
     const int c = lane + 64 * j;
     v[j] = 0.f;
-    if (c < d.D) {
-      v[j] = memory[size_t(nb) * d.D + c];
-    } else if (c < d.D + d.F) {
-      v[j] = efeat[size_t(ei) * d.F + (c - d.D)];
-    } else if (c < d.C) {
-      const int t = c - d.D - d.F;
-      float sn, cs;
-      te_sincos(te_arg(dtv, te_w[t], te_b[t]), sn, cs);
-      v[j] = cs;
-      S[size_t(row) * d.T + t] = sn;
-    }
+    if (c < d.D) v[j] = memory[size_t(nb) * d.D + c];
+    else if (c < d.D + d.F) v[j] = efeat[size_t(ei) * d.F + (c - d.D)];
   }
 #pragma unroll
   for (int j = 0; j < kMaxJ; ++j) {
     const int c = lane + 64 * j;
-    if (c < d.C) X[size_t(row) * d.C + c] = v[j];
+    if (c < d.D + d.F) X[size_t(row) * d.C + c] = v[j];
+  }
+}
+
+// This lane's slice of edge row `row` (c = lane + 64*j; zero past C) with
+// its time-encoding columns computed from dt and the time encoding's
+// parameters (te_w / te_b, staged in LDS): cos into x and into the row,
+// sin into S's row.
+template <int JM>
+__device__ __forceinline__ void fill_row(const Dims &d, float *__restrict__ X, float *__restrict__ S, size_t row,
+                                         const float *__restrict__ te_w, const float *__restrict__ te_b, float dtv,
+                                         int lane, float (&x)[JM]) {
+#pragma unroll
+  for (int j = 0; j < JM; ++j) {
+    const int c = lane + 64 * j;
+    float v = 0.f;
+    if (c < d.D + d.F) {
+      v = X[row * d.C + c];
+    } else if (c < d.C) {
+      const int t = c - d.D - d.F;
+      float sn;
+      te_sincos(te_arg(dtv, te_w[t], te_b[t]), sn, v);
+      X[row * d.C + c] = v;
+      S[row * d.T + t] = sn;
+    }
+    x[j] = v;
   }
 }
 
@@ -201,9 +217,11 @@ struct FwdLds {
   float *Zs;    // [16][ldr]
   float *QT;    // [16][ldq]  qt, then xbar
   float *qb;    // [16][H]
+  float *TW, *TB;  // [T] time-encoding weight / bias
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][2] a slice's running max and sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
+  float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
 
 __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bool slices) {
@@ -218,23 +236,29 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.Zs = L.AH + kRows * L.lda;
   L.QT = L.Zs + kRows * L.ldr;
   L.qb = L.QT + kRows * L.ldq;
-  L.part = L.qb + kRows * d.H;
+  L.TW = L.qb + kRows * d.H;
+  L.TB = L.TW + d.T;
+  L.part = L.TB + d.T;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   L.scr = L.pml + (slices ? nw * d.H * 2 : 0);
+  L.Ts = L.scr + (rows_for(nw) == 4 ? nw * 256 : 0);
   return L;
 }
 
-inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices) {
+// ts_rows: edges whose time encodings are staged in LDS (roots per tile *
+// fanout), 0 = computed in the edge loop instead.
+inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices, int ts_rows) {
   float *base = reinterpret_cast<float *>(uintptr_t(4096));
   const FwdLds L = fwd_lds(d, base, nw, slices);
-  return size_t(L.scr + (rows_for(nw) == 4 ? nw * 256 : 0) - base);
+  return size_t(L.Ts + size_t(ts_rows) * d.T - base);
 }
 
 template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
-    const float *__restrict__ h_root, const int32_t *__restrict__ cnt, const float *__restrict__ X,
-    ConvParams p, ConvSaved sv, float *__restrict__ y) {
+    const float *__restrict__ h_root, const int32_t *__restrict__ cnt, float *__restrict__ X,
+    const float *__restrict__ dt, float *__restrict__ S, ConvParams p, ConvSaved sv, float *__restrict__ y,
+    int ts_rows) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
@@ -267,6 +291,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
+  for (int t = tid; t < T; t += kBlock) {
+    L.TW[t] = p.te_w[t];
+    L.TB[t] = p.te_b[t];
+  }
   // HT = [h | cos(b)] (TimeEncode(0) = cos(0*w + b)); AH[:, D:] = h
   for (int idx = tid; idx < kRows * (D + T); idx += kBlock) {
     const int i = idx / (D + T), j = idx - i * (D + T);
@@ -281,10 +309,32 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     L.HT[i * L.ldh + j] = v;
   }
   __syncthreads();
-  // Q = W_q [h | cos(b)] + b_q
+  // Q = W_q [h | cos(b)] + b_q on the first (D+15)/16 waves (one 16x16
+  // block each). In 16-wave instances the other waves compute the tile's
+  // edges' cos / sin meanwhile: cos into the rows' time columns (and into
+  // LDS when staged, ts_rows == RPW * K), sin into S (the backward); the
+  // edge loop reads them after the barrier. 8-wave instances compute them
+  // in the edge loop.
+  constexpr bool kPre = NW == 16;
+  const bool staged = kPre && ts_rows > 0;
   {
     const sgl::GemmJob jobs[1] = {{L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D}};
     tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
+  }
+  if (kPre) {
+    const int qwaves = min(kWaves - 1, (D + 15) / 16);
+    const int nthr = (kWaves - qwaves) * 64;
+    for (int idx = tid - qwaves * 64; idx >= 0 && idx < RPW * K * T; idx += nthr) {
+      const int el = idx / T, t = idx - el * T, i = el / K, e = el - i * K;
+      if (e < s_cnt[i]) {
+        const size_t row = size_t(r0 + i) * K + e;
+        float sn, cs;
+        te_sincos(te_arg(dt[row], L.TW[t], L.TB[t]), sn, cs);
+        if (staged) L.Ts[el * T + t] = cs;
+        X[row * C + D + d.F + t] = cs;
+        S[row * T + t] = sn;
+      }
+    }
   }
   __syncthreads();
   for (int idx = tid; idx < RPW * D; idx += kBlock) {
@@ -331,49 +381,83 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       }
     }
     const size_t base = size_t(r) * K;
-    {
+    // one chunk of nv <= kEC edges from window position e: the scores first
+    // (independent reductions), then the online-softmax updates in edge order
+    auto consume = [&](const float (&x)[kEC][JM], int e, int nv) {
+      float sc[kEC][HM];
+#pragma unroll
+      for (int u = 0; u < kEC; ++u)
+#pragma unroll
+        for (int h = 0; h < HM; ++h) {
+          float part = 0.f;
+#pragma unroll
+          for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
+          sc[u][h] = u < nv ? wave_sum(part) + qbh[h] : 0.f;
+        }
+#pragma unroll
+      for (int u = 0; u < kEC; ++u) {
+        if (u >= nv) break;
+        const size_t idx = base + e + u;
+#pragma unroll
+        for (int h = 0; h < HM; ++h) {
+          if (h >= H) continue;
+          const float sh = sc[u][h];
+          const float a = sh > 0.f ? sh : 0.2f * sh;
+          const float mn = fmaxf(m[h], a);
+          const float scale = __expf(m[h] - mn);
+          const float pe = __expf(a - mn);
+          l[h] = l[h] * scale + pe;
+#pragma unroll
+          for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
+          m[h] = mn;
+          if (lane == 0) sv.score[idx * H + h] = a;
+        }
+      }
+    };
+    if (kPre) {
+      // gathered columns from the rows, time encodings from LDS (staged) or
+      // from the rows (written before the last barrier)
       for (int c0 = elo; c0 < ehi; c0 += kEC) {
-        // the chunk's rows past the window (uniform) are skipped
+        const int nv = min(kEC, ehi - c0);
         float x[kEC][JM];
 #pragma unroll
         for (int u = 0; u < kEC; ++u) {
-          if (c0 + u < ehi) {
-            load_row<JM>(d, X, base + c0 + u, lane, x[u]);
-          } else {
+          const int e = c0 + min(u, nv - 1);
+          const size_t row = base + e;
+          if (staged) {
+            const float *ts = L.Ts + (i * K + e) * T - (D + d.F);
 #pragma unroll
-            for (int j = 0; j < JM; ++j) x[u][j] = 0.f;
+            for (int j = 0; j < JM; ++j) {
+              const int c = lane + 64 * j;
+              x[u][j] = u < nv ? (c < D + d.F ? X[row * C + c] : c < C ? ts[c] : 0.f) : 0.f;
+            }
+          } else {
+            load_row<JM>(d, X, row, lane, x[u]);
+            if (u >= nv) {
+#pragma unroll
+              for (int j = 0; j < JM; ++j) x[u][j] = 0.f;
+            }
           }
         }
-        // the chunk's scores first (independent reductions), then the
-        // online-softmax updates in edge order
-        float sc[kEC][HM];
+        consume(x, c0, nv);
+      }
+    } else {
+      for (int e0 = elo; e0 < ehi; e0 += 64) {
+        const int wend = min(ehi, e0 + 64);
+        const float my_dt = e0 + lane < wend ? dt[base + e0 + lane] : 0.f;
+        for (int c0 = e0; c0 < wend; c0 += kEC) {
+          const int nv = min(kEC, wend - c0);
+          float x[kEC][JM];
 #pragma unroll
-        for (int u = 0; u < kEC; ++u)
+          for (int u = 0; u < kEC; ++u) {
+            if (u < nv) {
+              fill_row<JM>(d, X, S, base + c0 + u, L.TW, L.TB, __shfl(my_dt, c0 + u - e0, 64), lane, x[u]);
+            } else {
 #pragma unroll
-          for (int h = 0; h < HM; ++h) {
-            float part = 0.f;
-#pragma unroll
-            for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
-            sc[u][h] = c0 + u < ehi ? wave_sum(part) + qbh[h] : 0.f;
+              for (int j = 0; j < JM; ++j) x[u][j] = 0.f;
+            }
           }
-#pragma unroll
-        for (int u = 0; u < kEC; ++u) {
-          if (c0 + u >= ehi) break;
-          const size_t idx = base + c0 + u;
-#pragma unroll
-          for (int h = 0; h < HM; ++h) {
-            if (h >= H) continue;
-            const float s = sc[u][h];
-            const float a = s > 0.f ? s : 0.2f * s;
-            const float mn = fmaxf(m[h], a);
-            const float scale = __expf(m[h] - mn);
-            const float pe = __expf(a - mn);
-            l[h] = l[h] * scale + pe;
-#pragma unroll
-            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
-            m[h] = mn;
-            if (lane == 0) sv.score[idx * H + h] = a;
-          }
+          consume(x, c0, nv);
         }
       }
     }
@@ -983,8 +1067,7 @@ extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H
 
 extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, int64_t capacity,
                              const int32_t *num_roots, const float *memory, const float *efeat, const int32_t *cnt,
-                             const int32_t *nbr, const int32_t *eid, const float *dt, const float *te_w,
-                             const float *te_b, float *X, float *S, hipStream_t stream) {
+                             const int32_t *nbr, const int32_t *eid, float *X, hipStream_t stream) {
   const Dims d{D, F, T, 1, D + F + T, D, fanout};
   SGL_REQUIRE(D > 0 && F >= 0 && T >= 0 && d.C <= 64 * kMaxJ, "edge_rows: C = D+F+T = %d out of (0, %d]", d.C,
               64 * kMaxJ);
@@ -992,41 +1075,43 @@ extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, in
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX, "edge_rows: capacity %lld out of range", (long long)capacity);
   const int64_t rows = capacity * fanout;
   if (rows == 0) return SGL_OK;
-  SGL_REQUIRE(num_roots && memory && cnt && nbr && eid && dt && X && (F == 0 || efeat) &&
-                  (T == 0 || (te_w && te_b && S)),
-              "edge_rows: NULL array");
+  SGL_REQUIRE(num_roots && memory && cnt && nbr && eid && X && (F == 0 || efeat), "edge_rows: NULL array");
   sgl::launch(&k_edge_rows, dim3(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
-              stream, d, rows, num_roots, memory, efeat, cnt, nbr, eid, dt, te_w, te_b, X, S);
+              stream, d, rows, num_roots, memory, efeat, cnt, nbr, eid, X);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
 
 extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int32_t fanout, int64_t capacity,
                                 const int32_t *num_roots, const int32_t *any_edges, const float *h_root,
-                                const int32_t *cnt, const float *X, const float *w_q, const float *b_q,
+                                const int32_t *cnt, float *X, const float *dt, const float *w_q, const float *b_q,
                                 const float *w_k, const float *b_k, const float *w_v, const float *b_v,
                                 const float *w_out, const float *b_out, const float *ln_g, const float *ln_b,
-                                const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar, float *sv_score,
-                                float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats, float *sv_phi0, float *y,
-                                hipStream_t stream) {
+                                const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
+                                float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
+                                float *sv_phi0, float *S, float *y, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
   SGL_REQUIRE(num_roots && any_edges && h_root && cnt && w_q && b_q && w_k && b_k && w_v && b_v && w_out && b_out &&
-                  ln_g && ln_b && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z && sv_stats && y &&
-                  (fanout == 0 || (X && sv_score)),
+                  ln_g && ln_b && te_w && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z && sv_stats &&
+                  y && (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_forward: NULL array");
   const auto inst = pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
-  const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
+  // stage the tile's time encodings in LDS when they fit
+  const bool slices = inst.waves > inst.rows;
+  int ts_rows = fanout > 0 && T > 0 ? inst.rows * fanout : 0;
+  if (sizeof(float) * fwd_lds_floats(d, inst.waves, slices, ts_rows) > 160 * 1024) ts_rows = 0;
+  const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, slices, ts_rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
-  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, nullptr, te_b};
+  ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
-              num_roots, any_edges, h_root, cnt, X, p, sv, y);
+              num_roots, any_edges, h_root, cnt, X, dt, S, p, sv, y, ts_rows);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

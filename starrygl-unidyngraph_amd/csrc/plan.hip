@@ -2,22 +2,20 @@
 // arguments are fixed device pointers and sizes: events are read at a device
 // cursor) and replayed with plain kernel launches by one host call.
 //
-// A plan is four runs of ops: the front part of a step (batch preparation,
-// sampling, GRU memory update), the memory commit, and the back part split
-// after the backward (attention forward, edge predictor, backward | fused
-// Adam). Consecutive steps use different step buffers. Step t's front part
-// only needs the buffers that step t-2's back part read to be free, and its
-// commit only needs step t-1's backward (the last reader of the memory
-// table) to be done, so the front stream runs ahead, and the commit of step
-// t runs beside step t-1's Adam. The streams order themselves through three
-// device words (a one-lane signal kernel stores a number once the stream's
-// earlier kernels are done; a one-lane wait kernel holds the stream until
-// the word reaches a value):
+// A plan is two runs of ops: the front part of a step (batch preparation,
+// sampling, GRU memory update, memory commit, the edge rows, the Adam step
+// counts) and the back part (attention forward, edge predictor, backward,
+// fused Adam). Consecutive steps use different step buffers, and nothing in
+// a back part reads the memory table (the edge rows hold the neighbours'
+// memory), so step t's front part only needs the back part of step t-2
+// (the last reader of its buffers) to be done, and runs beside step t-1's
+// back part. The streams order themselves through two device words (a
+// one-lane signal kernel stores a number once the stream's earlier kernels
+// are done; a one-lane wait kernel holds the stream until the word reaches
+// a value):
 //
-//   front:  wait(back >= need_back) -> front ops -> wait(bwd >= need_bwd)
-//           -> commit -> write(fronted = seq)
-//   back:   wait(fronted >= seq) -> fwd, predictor, bwd -> write(bwd = seq)
-//           -> Adam -> write(back = seq)
+//   front:  wait(back >= need_back) -> front ops -> signal(fronted = seq)
+//   back:   wait(fronted >= seq) -> back ops -> signal(back = seq)
 //
 // Plain launches cost the GPU well under a microsecond between kernels; the
 // same kernels replayed as graphs cost several, and more at graph
@@ -154,31 +152,25 @@ extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
   return -1;
 }
 
-extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_commit, int32_t n_back,
-                            int32_t n_tail, hipStream_t front, hipStream_t back, uint32_t *sync, uint32_t seq,
-                            uint32_t need_back, uint32_t need_bwd, int32_t timed_op, hipEvent_t t_start,
-                            hipEvent_t t_end) {
-  SGL_REQUIRE(ops != nullptr || n_front + n_commit + n_back + n_tail == 0, "plan_run: NULL ops");
-  SGL_REQUIRE(n_front >= 0 && n_commit >= 0 && n_back >= 0 && n_tail >= 0, "plan_run: negative op count");
+extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_back, hipStream_t front,
+                            hipStream_t back, uint32_t *sync, uint32_t seq, uint32_t need_back, int32_t timed_op,
+                            hipEvent_t t_start, hipEvent_t t_end) {
+  SGL_REQUIRE(ops != nullptr || n_front + n_back == 0, "plan_run: NULL ops");
+  SGL_REQUIRE(n_front >= 0 && n_back >= 0, "plan_run: negative op count");
   SGL_REQUIRE(timed_op < 0 || (t_start && t_end), "plan_run: NULL timing event");
   const OpTimer t{timed_op, t_start, t_end};
-  if (n_commit == 0) {  // no split point: everything in order on the back stream
-    return run_ops(ops, n_front + n_back + n_tail, back, 0, t);
+  if (front == nullptr) {  // one stream: everything in order on the back stream
+    return run_ops(ops, n_front + n_back, back, 0, t);
   }
-  SGL_REQUIRE(sync != nullptr && seq > 0 && need_back < seq && need_bwd < seq,
+  SGL_REQUIRE(sync != nullptr && seq > 0 && need_back < seq,
               "plan_run: NULL sync words or inconsistent sequence numbers");
   SGL_REQUIRE(front != back, "plan_run: the front and back streams must differ");
-  // separate 64-byte lines; sync[48] is the gates' timeout word
-  uint32_t *w_back = sync, *w_front = sync + 16, *w_bwd = sync + 32, *timeout = sync + 48;
+  // separate 64-byte lines; sync[48] is the waits' timeout word
+  uint32_t *w_back = sync, *w_front = sync + 16, *timeout = sync + 48;
   if (int rc = gate(w_back, need_back, timeout, front)) return rc;
   if (int rc = run_ops(ops, n_front, front, 0, t)) return rc;
-  if (int rc = gate(w_bwd, need_bwd, timeout, front)) return rc;
-  if (int rc = run_ops(ops + n_front, n_commit, front, n_front, t)) return rc;
   if (int rc = signal(w_front, seq, front)) return rc;
   if (int rc = gate(w_front, seq, timeout, back)) return rc;
-  const int b0 = n_front + n_commit;
-  if (int rc = run_ops(ops + b0, n_back, back, b0, t)) return rc;
-  if (int rc = signal(w_bwd, seq, back)) return rc;
-  if (int rc = run_ops(ops + b0 + n_back, n_tail, back, b0 + n_back, t)) return rc;
+  if (int rc = run_ops(ops + n_front, n_back, back, n_front, t)) return rc;
   return signal(w_back, seq, back);
 }

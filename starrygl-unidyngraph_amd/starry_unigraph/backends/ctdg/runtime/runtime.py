@@ -95,18 +95,18 @@ class CTDGOnlineRuntime:
         self._views: dict[tuple[int, int], tuple] = {}
         self._updates: dict[int, StepParamUpdate] = {}
         # two-stream submission: the front stream runs batch preparation,
-        # sampling, the GRU and the memory commit; the caller's current stream
-        # the attention, predictor, backward and Adam. The streams order
-        # themselves through three device words (sgl_plan_run): _sync[0] the
-        # number of the last back part (or fence), _sync[16] of the last front
-        # part, _sync[32] of the last backward (or fence). _seq is the last
-        # number used; _need_back / _need_bwd what the next front part waits for.
+        # sampling, the GRU, the memory commit and the edge rows; the caller's
+        # current stream the attention, predictor, backward and Adam. The
+        # streams order themselves through two device words (sgl_plan_run):
+        # _sync[0] the number of the last back part (or fence), _sync[16] of
+        # the last front part. _seq is the last number used; _need_back what
+        # the next front part waits for.
         self._front_stream: torch.cuda.Stream | None = None
         self._sync = torch.zeros(64, dtype=torch.int32, device=self.device)
         self._sync_ptr = self._sync.data_ptr()
-        self._sync_back, self._sync_bwd = self._sync[0:1], self._sync[32:33]
+        self._sync_back = self._sync[0:1]
         self._seq = 0
-        self._need_back = self._need_bwd = self._prev_seq = 0
+        self._need_back = self._prev_seq = 0
         self._state_writes = memory.state.writes
 
     def _make_steps(self, max_batch: int) -> None:
@@ -125,8 +125,7 @@ class CTDGOnlineRuntime:
             self._seq += 1
             # on the current stream, after the work queued so far
             self._sync_back.fill_(self._seq)
-            self._sync_bwd.fill_(self._seq)
-            self._need_back = self._need_bwd = self._prev_seq = self._seq
+            self._need_back = self._prev_seq = self._seq
         self._state_writes = self.memory.state.writes
 
     def check_sync(self) -> None:
@@ -144,7 +143,7 @@ class CTDGOnlineRuntime:
         elif self._seq >= 0x7FFFFFF0:   # keep the sequence numbers in int32 range
             torch.cuda.synchronize(self.device)
             self._sync.zero_()
-            self._seq = self._need_back = self._need_bwd = self._prev_seq = 0
+            self._seq = self._need_back = self._prev_seq = 0
         return self._front_stream
 
     def _core(self):
@@ -270,15 +269,14 @@ class CTDGOnlineRuntime:
             if self.plan_timer is not None:   # (entry point name, callback giving this step's event pair or None)
                 evs = self.plan_timer[1]()
                 if evs is not None:
-                    top = plan[5].index(self.plan_timer[0])
+                    top = plan[3].index(self.plan_timer[0])
                     t0, t1 = evs[0].cuda_event, evs[1].cuda_event
             _capi.check(_capi.lib().sgl_plan_run(
-                plan[0], plan[1], plan[2], plan[3], plan[4], front.cuda_stream,
-                torch.cuda.current_stream(self.device).cuda_stream, self._sync_ptr, seq, self._need_back,
-                self._need_bwd, top, t0, t1), "sgl_plan_run")
+                plan[0], plan[1], plan[2], front.cuda_stream, torch.cuda.current_stream(self.device).cuda_stream,
+                self._sync_ptr, seq, self._need_back, top, t0, t1), "sgl_plan_run")
             # the next step's front part refills the buffers this step's
             # predecessor read; its commit follows this step's backward
-            self._need_back, self._need_bwd, self._prev_seq = self._prev_seq, seq, seq
+            self._need_back, self._prev_seq = self._prev_seq, seq
             self._seq = seq
         views = self._views.get((n, q))
         if views is None or views[0] is not b:
@@ -288,27 +286,32 @@ class CTDGOnlineRuntime:
 
     def _record(self, step: DeviceStep, split: str, train: bool, n: int) -> tuple:
         """Record a full step on ``step``'s buffers as a launch plan: (ops,
-        #front, #commit, #back, #tail, entry point names, recorded calls); in
-        training the commit part ends with the step's Adam count advance, the
-        tail is the fused gradient + Adam update. A plan with an empty commit
-        part (evaluation without a memory updater) runs in order on one
-        stream."""
+        #front, #back, entry point names, recorded calls). The front part is
+        the batch preparation, sampling, GRU, memory commit, edge rows and (in
+        training) the Adam step counts; the back part the attention, the
+        predictor and, in training, the backward and the fused update. No back
+        part reads the memory table, so a step's front part may run beside
+        the previous step's back part."""
         d = self._dev
         if train:
             self._param_update(step)   # any rebuild or host-side sync happens outside the recording
         with _capi.record() as front:
             self._front_body(step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"],
                              self._cursor)
-        with _capi.record() as commit:
             self._commit_body(step, train)
         with _capi.record() as back:
-            self._back_body(step, train, n, update=False)
-        with _capi.record() as tail:
-            if train:
-                self._param_update(step).run()
-        calls = front + commit + back + tail
-        return (_capi.pack_ops(calls), len(front), len(commit), len(back), len(tail), [c[0] for c in calls],
-                calls)
+            self._back_body(step, train, n)
+        # the front part runs beside the previous step's update: it must not
+        # read the trained parameters (every pointer argument outside them)
+        inner = getattr(self.optimizer, "inner", None)
+        if isinstance(inner, FusedAdam):
+            lo = inner.flat.data_ptr()
+            hi = lo + 4 * inner.flat.numel()
+            for name, args in front:
+                if any(isinstance(a, int) and lo <= a < hi for a in args):
+                    raise RuntimeError(f"launch plan: {name} in the front part reads the trained parameters")
+        calls = front + back
+        return (_capi.pack_ops(calls), len(front), len(back), [c[0] for c in calls], calls)
 
     def reset_plans(self) -> None:
         """Drop recorded plans (after buffers they reference change)."""
@@ -328,20 +331,19 @@ class CTDGOnlineRuntime:
 
     def _commit_body(self, step: DeviceStep, train: bool) -> None:
         """The memory commit (which also sets the step's "block has edges"
-        gate), the sampled edges' rows from the committed memory and, in
-        training, the Adam step-count advance and bias corrections that the
-        step's fused update reads."""
+        gate), the sampled edges' rows from the committed memory (no trained
+        parameter is read, so this may run beside the previous step's update)
+        and, in training, the Adam step-count advance and bias corrections
+        that the step's fused update reads."""
         if self._gru is not None:
             step.commit()
-        conv = self._core().conv
-        step.edge_rows(conv.time_enc.w.weight.detach(), conv.time_enc.w.bias.detach(), self._dev["edge_feat"])
+        step.edge_rows(self._dev["edge_feat"])
         if train:
             self._param_update(step).advance()
 
-    def _back_body(self, step: DeviceStep, train: bool, n: int, update: bool = True) -> None:
+    def _back_body(self, step: DeviceStep, train: bool, n: int) -> None:
         """Attention forward, edge predictor + BCE and, in training, the
-        backward and (with ``update``) the fused weight-gradient + Adam
-        update."""
+        backward and the fused weight-gradient + Adam update."""
         core = self._core()
         conv = core.conv
         efeat_all = self._dev["edge_feat"]
@@ -361,8 +363,7 @@ class CTDGOnlineRuntime:
         step.predictor(n, train, pdet, out_grads)
         if train:
             step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]))
-            if update:
-                upd.run()
+            upd.run()
 
     def _param_update(self, step: DeviceStep) -> StepParamUpdate:
         """The fused weight-gradient + Adam launch for a step's buffers and the

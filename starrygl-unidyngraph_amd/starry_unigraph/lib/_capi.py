@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -46,16 +46,15 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
-    "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 12),
-    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 27),
+    "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 8),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 30),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 40),
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 21),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
     "sgl_time_next_launch": (ctypes.c_int, [_vp, _vp]),
     "sgl_plan_op_kind": (_i32, [ctypes.c_char_p, _vp]),
-    "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp] + [ctypes.c_uint32] * 3
-                     + [_i32, _vp, _vp]),
+    "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp] + [ctypes.c_uint32] * 2 + [_i32, _vp, _vp]),
     "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 2 + [ctypes.c_float] * 4 + [_vp]),
     "sgl_adam_coef": (ctypes.c_int, [_i32] + [_vp] * 3 + [ctypes.c_float] * 3 + [_vp]),
 }

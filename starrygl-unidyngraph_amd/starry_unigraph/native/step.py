@@ -127,8 +127,8 @@ class StepBuffers:
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
         self.phi0 = z(max(dims.T, 1))
-        # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)] and
-        # the sines of its time encoding (sgl_edge_rows)
+        # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)]
+        # (sgl_edge_rows, then the forward) and the sines of its time encoding
         self.X = z(max(c * k * C, 1))
         self.S = z(max(c * k * dims.T, 1))
         self.gy = z(c, D)
@@ -232,25 +232,26 @@ class DeviceStep:
             P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
 
     # -- attention ----------------------------------------------------------
-    def edge_rows(self, te_w: torch.Tensor, te_b: torch.Tensor, efeat_all: torch.Tensor) -> None:
-        """The sampled edges' rows X and time-encoding sines S (sgl_edge_rows),
-        from the committed memory table: after commit(), before the attention."""
+    def edge_rows(self, efeat_all: torch.Tensor) -> None:
+        """The sampled edges' rows X (sgl_edge_rows: the neighbours' memory and
+        edge features) from the committed memory table: after commit(), before
+        the attention."""
         b, st, d, P = self.buf, self.state, self.dims, _capi.ptr
         hop = b.hop
         self._call("edge_rows", lambda: _capi.check(_capi.call(
             "sgl_edge_rows", d.D, d.F, d.T, d.fanout, b.cap, P(b.num_roots), P(st.memory), P(efeat_all),
-            P(hop.cnt), P(hop.nbr), P(hop.eid), P(hop.dt), P(te_w), P(te_b), P(b.X), P(b.S), self._s()),
-            "sgl_edge_rows"))
+            P(hop.cnt), P(hop.nbr), P(hop.eid), P(b.X), self._s()), "sgl_edge_rows"))
 
     def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
-        """The attention forward over the edge rows of the last edge_rows()."""
+        """The attention forward over the edge rows of the last edge_rows()
+        (it adds the rows' time encodings and their sines S)."""
         b, d, P = self.buf, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         self._call("conv_forward", lambda: _capi.check(_capi.call(
             "sgl_conv_forward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem),
-            P(b.hop.cnt), P(b.X), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out), P(ln_g),
-            P(ln_b), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats),
-            P(b.phi0), P(b.y), self._s()), "sgl_conv_forward"))
+            P(b.hop.cnt), P(b.X), P(b.hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out),
+            P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z),
+            P(b.stats), P(b.phi0), P(b.S), P(b.y), self._s()), "sgl_conv_forward"))
         return b.y
 
     def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None):
@@ -444,7 +445,7 @@ class ConvFunction(torch.autograd.Function):
         ctx.step = step
         ctx.efeat_all = efeat_all
         ctx.params = params
-        step.edge_rows(params[0], params[1], efeat_all)
+        step.edge_rows(efeat_all)
         return step.conv_forward(list(params), efeat_all)
 
     @staticmethod
