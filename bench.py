@@ -123,7 +123,8 @@ def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -
            "workload": "cfg3: 1e7 nodes, 1e8 edges, 4e6 degree-weighted queries, recent k=10, 1 hop",
            "roofline": {"bound": "hbm", "kernel": "k_recent_padded", "kernel_avg_ms": avg_ms,
                         "alg_bytes_per_launch": alg, "achieved": alg / (avg_ms * 1e-3) / 1e9,
-                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": alg / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": alg / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                        "traffic": HBM_TRAFFIC.get(("cfg3", "recent_sample"))}}
     del head
     if cases:
         res = {}
@@ -250,9 +251,13 @@ def _restore(rt, snap):
 
 # HBM bytes per launch (read + written) of a kernel on a workload, from the
 # rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
-# profiles/conv_backward_cfg4_hbm_traffic.md (counters scaled by a copy
-# kernel of known size); None where no counter run was made.
-HBM_TRAFFIC = {("cfg4", "conv_backward"): (2334 + 1801) * 1024}
+# profiles/tgn_cfg4_hbm_traffic.md and profiles/sampler_cfg3_hbm_traffic.md
+# (counters scaled by a copy kernel of known size); None where no counter run
+# was made.
+HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 1133.4 + 1504.5) * 1024),
+               ("cfg4", "edge_rows"): round((2 * 143.4 + 291.1) * 1024),
+               ("cfg4", "memory_commit"): round((2 * 63.8 + 93.9) * 1024),
+               ("cfg3", "recent_sample"): round((2 * 2384600 + 449830) * 1024)}
 
 # step stage name -> the C-ABI entry point that launches it
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
@@ -467,7 +472,7 @@ def main() -> None:
     ap.add_argument("--no-plans", action="store_true",
                     help="run steps eagerly (one library call at a time) instead of as recorded launch plans")
     ap.add_argument("--workload", default="tgn-large", choices=sorted(list(WORKLOADS) + ["sampler"]))
-    ap.add_argument("--roofline-kernel", default="conv_backward",
+    ap.add_argument("--roofline-kernel", default="conv_forward",
                     choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "edge_rows",
                              "conv_forward", "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
