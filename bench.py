@@ -251,12 +251,17 @@ def _restore(rt, snap):
 
 # HBM bytes per launch (read + written) of a kernel on a workload, from the
 # rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
-# profiles/tgn_cfg4_hbm_traffic.md and profiles/sampler_cfg3_hbm_traffic.md
+# profiles/tgn_cfg4_hbm_traffic.md, profiles/tgn_cfg4_mfma_utilisation.md and
+# profiles/sampler_cfg3_hbm_traffic.md
 # (counters scaled by a copy kernel of known size); None where no counter run
 # was made.
 HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 1133.4 + 1504.5) * 1024),
                ("cfg4", "edge_rows"): round((2 * 143.4 + 291.1) * 1024),
                ("cfg4", "memory_commit"): round((2 * 63.8 + 93.9) * 1024),
+               ("cfg4", "conv_forward"): round((2 * 1824.3 + 1880.2) * 1024),
+               ("cfg4", "memory_update"): round((2 * 2311.0 + 256.2) * 1024),
+               ("cfg4", "predictor"): round((2 * 564.4 + 1006.8) * 1024),
+               ("cfg4", "param_update"): round((2 * 8017.6 + 2070.6) * 1024),
                ("cfg3", "recent_sample"): round((2 * 2384600 + 449830) * 1024)}
 
 # step stage name -> the C-ABI entry point that launches it
