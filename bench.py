@@ -396,7 +396,8 @@ def run_tgn(args, wl: dict) -> dict:
         else:
             ach, peak, unit = wavg / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         breakdown[name] = {"avg_us": round(avg * 1e3, 2), "calls": len(ms), "bound": bound,
-                           "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5)}
+                           "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5),
+                           "traffic": HBM_TRAFFIC.get((wl["config"], name))}
     mean_U = sum(p[2] for p in per_step) / len(per_step)
     mean_E = sum(p[3] for p in per_step) / len(per_step)
     if not dom_ms:   # no timed launches in the timed region: the eager replay's
