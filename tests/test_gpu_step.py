@@ -153,10 +153,13 @@ def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
 
 # (D, F, T, H) cover both attention tile shapes: 16 waves sharing 4 roots
 # (slices of a window merged through LDS; k=3 leaves a slice empty) and 8
-# waves with one root each (H=4, or C = D+F+T above 256 with H=2); the last
-# two rows are the shapes of the benchmark configurations.
+# waves with one root each (H=4, or C = D+F+T above 256 with H=2); rows 4-5
+# are the shapes of the benchmark configurations. With k=120 and T=96 the
+# 16-wave forward's time encodings (4 roots x 120 edges x 96) do not fit in
+# LDS: its edge loop reads them from the rows the other waves wrote.
 @pytest.mark.parametrize("H,k,seed,D,F,T", [(2, 10, 0, 32, 6, 16), (4, 20, 1, 32, 6, 16), (1, 3, 2, 32, 6, 16),
-                                            (2, 10, 3, 100, 16, 100), (2, 10, 4, 100, 172, 100)])
+                                            (2, 10, 3, 100, 16, 100), (2, 10, 4, 100, 172, 100),
+                                            (2, 120, 5, 32, 6, 96)])
 def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T):
     from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
