@@ -12,6 +12,10 @@ Prints ONE JSON line. Workloads:
   tgn-stress config 5: the config-4 stream, D = 172, 4 heads, k = 20,
              2 sampled hops, 4 mailbox slots, batch 4,000.
   sampler    config 3 alone (temporal sampler microbench).
+  gather-scatter  the memory / mailbox gather-scatter microbench: config-5 state
+             (1,140,149 nodes, D = 172, K = 4, F = 16) under batches of 600, 4,000
+             and 1,048,576 events of the config-4 stream: batch preparation,
+             sampling (k = 20), GRU + mailbox, memory commit, edge-row gather.
 The default run also measures config 3 and reports it under "sampler".
 
 Timed region: W untimed warm-up steps, then K steps bracketed by
@@ -185,6 +189,123 @@ def sampler_cpu_baseline(g_np, nodes_np, qt_np) -> dict:
                 "cpu_model": cpu_model()}
     except Exception as e:  # reported, never required
         return {"value": None, "unit": "Mqueries/s", "cores": cores, "kind": "port", "sample": f"failed: {e}"}
+
+
+# --------------------------------------------------------------------------- gather / scatter
+GS_BATCHES = (600, 4000, 1 << 20)
+
+
+def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> float:
+    """Algorithmic HBM bytes of one launch of a front-part kernel."""
+    S = 2 * D + F
+    if name == "memory_commit":
+        # root id, new row read, memory row + memory_ts written, sample count, bitmap word
+        return U * (8 + 8 * D + 12)
+    if name == "edge_rows":
+        # per sampled edge: nbr, eid, the memory row and edge feature read and written into the edge's row
+        return E * (8 + 8 * (D + F)) + U * 4
+    if name == "memory_update":
+        # per root: memory row, K mailbox rows + times read, new row written, one message (S + ts) written;
+        # per event: src, dst, ts, edge feature read
+        return U * (8 * D + 4 * K * S + 4 * K + 4 * S + 4) + B * (8 + 8 + 4 + 4 * F)
+    if name == "batch_prepare":
+        return B * (8 + 8 + 8 + 4) + U * 8
+    return 0.0
+
+
+def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
+    """The gather / scatter microbench: config-5 node state (the config-4
+    stream's 1,140,149 nodes, D = 172, K = 4 mailbox slots, F = 16), batches of
+    B consecutive events of that stream for B in `batches`: batch
+    preparation, recent-k sampling (k = 20), the fused GRU + mailbox update
+    (the roots' memory and mailbox rows gathered, the new messages
+    scattered), the memory commit (scatter) and the edge-row gather, each
+    call timed by an event pair around it; algorithmic bytes per call against
+    HBM."""
+    import torch
+
+    from starry_unigraph import synth
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    es = synth.unipartite_stream(seed=0)
+    log(f"gather/scatter: stream generated in {time.time() - t0:.1f}s ({es.num_events} events)")
+    N, D, K, F, T, H, k = es.num_nodes, 172, 4, 16, 100, 4, 20
+    src = torch.from_numpy(es.src).to(dev)
+    dst = torch.from_numpy(es.dst).to(dev)
+    ts = torch.from_numpy(es.ts).to(dev)
+    ef = torch.from_numpy(es.edge_feat).to(dev)
+    # the sampler graph over the whole stream (row = src, col = dst, int64 times truncated from float32)
+    g = build_tcsr(N, src, dst, None, ts.to(torch.int64), device=dev)
+    sampler = RecentSampler(g)
+    state = NodeState(N, D, K, F, dev)
+    gen = torch.Generator().manual_seed(0)
+    S = 2 * D + F
+    rnd = lambda *shape: ((torch.rand(*shape, generator=gen) * 2 - 1) / D ** 0.5).to(dev)
+    gru = {"w_ih": rnd(3 * D, S), "w_hh": rnd(3 * D, D), "b_ih": rnd(3 * D), "b_hh": rnd(3 * D),
+           "wc_ih": rnd(3 * D, D), "wc_hh": rnd(3 * D, D), "bc_ih": rnd(3 * D), "bc_hh": rnd(3 * D)}
+    dims = ConvDims(D=D, F=F, T=T, H=H, fanout=k)
+    names = ("batch_prepare", "recent_sample", "memory_update", "memory_commit", "edge_rows")
+    cases = {}
+    for B in batches:
+        step = DeviceStep(state, dims, B, attention=False)
+        nb = es.num_events // B
+        agg = {n: [] for n in names}
+        shapes = []
+        # one event pair around each whole call (batch preparation and
+        # sampling launch several kernels each), all on the current stream
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        for i in range(warmup + steps):
+            # batches from the middle of the stream on, where the sampled windows are full
+            a = ((nb // 2 + i) % nb) * B
+            sb, db, tb = src[a:a + B], dst[a:a + B], ts[a:a + B]
+            neg = db.roll(1)
+            evs[0].record()
+            step.prepare(sb, db, neg, tb)
+            evs[1].record()
+            step.sample(sampler)
+            evs[2].record()
+            step.update_memory(gru, sb, db, ef[a:a + B], tb)
+            evs[3].record()
+            step.commit()
+            evs[4].record()
+            step.edge_rows(ef)
+            evs[5].record()
+            if i >= warmup:
+                torch.cuda.synchronize()
+                U = int(step.buf.num_roots.item())
+                E = int(step.buf.hop.cnt[:U].sum().item())
+                shapes.append((U, E))
+                for j, name in enumerate(names):
+                    agg[name].append((evs[j].elapsed_time(evs[j + 1]), U, E))
+        out = {}
+        for name in names:
+            ms = sum(x[0] for x in agg[name]) / len(agg[name])
+            alg = sum(gs_bytes(name, U, E, B, D, F, K) for _, U, E in agg[name]) / len(agg[name])
+            row = {"avg_us": round(ms * 1e3, 2), "calls": len(agg[name])}
+            if alg > 0:
+                gbs = alg / (ms * 1e-3) / 1e9
+                row.update({"alg_bytes": round(alg), "achieved": round(gbs, 1), "unit": "GB/s",
+                            "frac": round(gbs / HBM_PEAK_GBS, 4)})
+            out[name] = row
+        cases[str(B)] = {"mean_roots": round(sum(u for u, _ in shapes) / len(shapes), 1),
+                         "mean_sampled_edges": round(sum(e for _, e in shapes) / len(shapes), 1), "kernels": out}
+        log(f"gather/scatter B={B}: " + ", ".join(f"{n} {v['avg_us']} us" + (f" ({v['achieved']} GB/s)" if
+                                                                            "achieved" in v else "")
+                                                 for n, v in out.items()))
+        del step
+        torch.cuda.empty_cache()
+    big = cases[str(max(batches))]["kernels"]
+    gb = sum(big[n]["alg_bytes"] for n in ("memory_commit", "edge_rows"))
+    us = sum(big[n]["avg_us"] for n in ("memory_commit", "edge_rows"))
+    return {"value": gb / (us * 1e-6) / 1e9, "unit": "GB/s",
+            "workload": f"gather/scatter: cfg5 state (N={N}, D={D}, K={K}, F={F}), k={k}, batches {list(batches)}",
+            "cases": cases,
+            "roofline": {"bound": "hbm", "kernel": "k_memory_commit + k_edge_rows", "batch": max(batches),
+                         "achieved": gb / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None}}
 
 
 # --------------------------------------------------------------------------- TGN end to end
@@ -477,7 +598,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-plans", action="store_true",
                     help="run steps eagerly (one library call at a time) instead of as recorded launch plans")
-    ap.add_argument("--workload", default="tgn-large", choices=sorted(list(WORKLOADS) + ["sampler"]))
+    ap.add_argument("--workload", default="tgn-large",
+                    choices=sorted(list(WORKLOADS) + ["sampler", "gather-scatter"]))
     ap.add_argument("--roofline-kernel", default="conv_forward",
                     choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "edge_rows",
                              "conv_forward", "conv_backward"])
@@ -505,6 +627,13 @@ def main() -> None:
         del src, dst
     base = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded PCG64 generators, starry_unigraph.synth)"}
+    if args.workload == "gather-scatter":
+        r = run_gather_scatter(args.steps, args.warmup)
+        line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=None, dtype="fp32",
+                    config={"workload": r["workload"], "global_batch": max(GS_BATCHES), "parallelism": "single GPU"},
+                    roofline=r["roofline"], cpu_baseline=None, cases=r["cases"])
+        print(json.dumps(line), flush=True)
+        return
     if args.workload == "sampler":
         r = run_sampler(args.steps, args.warmup, cpu=not args.no_cpu)
         line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_pass"], dtype="int64",

@@ -102,35 +102,51 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
 // Edge rows: X[r*K + e][0, D+F) = [memory[nbr] | efeat[eid]] for every live
 // root r < U and sampled slot e < cnt[r] (rows of C = D+F+T floats; padding
 // slots are not written). The time-encoding columns depend on trained
-// parameters and are filled in by the attention forward. One wave per row,
-// four rows per workgroup; the row's loads are issued together.
-constexpr int kRowsPerBlock = 4;
+// parameters and are filled in by the attention forward. Rows are copied in
+// V-float vectors by 64/V lanes each (V = 4 when D, F and C are multiples of
+// four and the arrays 16-byte aligned: a wave then copies four rows at once),
+// each row's loads issued together; a bounded grid strides over the live
+// roots' rows.
+constexpr int kEdgeBlock = 256;
 
-__global__ __launch_bounds__(64 * kRowsPerBlock) void k_edge_rows(
+template <int V> struct EdgeVec;
+template <> struct EdgeVec<1> { using type = float; };
+template <> struct EdgeVec<4> { using type = float4; };
+
+template <int V>
+__global__ __launch_bounds__(kEdgeBlock) void k_edge_rows(
     Dims d, int64_t nrows_total, const int32_t *__restrict__ num_roots, const float *__restrict__ memory,
     const float *__restrict__ efeat, const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, float *__restrict__ X) {
-  const int64_t row = int64_t(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= nrows_total) return;
-  const int64_t r = row / d.k;
-  const int e = int(row - r * d.k);
-  // issued together: the live-row test and the row's sampler entries
-  const int U = *num_roots, ne = cnt[r];
-  const int nb = nbr[row], ei = eid[row];
-  if (r >= U || e >= ne) return;
-  float v[kMaxJ];
+  using vec = typename EdgeVec<V>::type;
+  constexpr int kLanes = sgl::kWave / V;            // lanes per row
+  constexpr int kRows = kEdgeBlock / kLanes;        // rows per workgroup pass
+  const int q = threadIdx.x & (kLanes - 1);
+  const int Dv = d.D / V, Fv = d.F / V, Wv = Dv + Fv, Cv = d.C / V;
+  const int64_t live = min(nrows_total, int64_t(*num_roots) * d.k);
+  for (int64_t row = int64_t(blockIdx.x) * kRows + threadIdx.x / kLanes; row < live;
+       row += int64_t(gridDim.x) * kRows) {
+    const int64_t r = row / d.k;
+    const int e = int(row - r * d.k);
+    // issued together: the row's count and sampler entries
+    const int ne = cnt[r];
+    const int nb = nbr[row], ei = eid[row];
+    if (e >= ne) continue;  // a padding slot
+    const vec *mrow = reinterpret_cast<const vec *>(memory) + size_t(nb) * Dv;
+    const vec *frow = reinterpret_cast<const vec *>(efeat) + size_t(ei) * Fv;
+    vec *xrow = reinterpret_cast<vec *>(X) + size_t(row) * Cv;
+    vec v[kMaxJ];
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
-    const int c = lane + 64 * j;
-    v[j] = 0.f;
-    if (c < d.D) v[j] = memory[size_t(nb) * d.D + c];
-    else if (c < d.D + d.F) v[j] = efeat[size_t(ei) * d.F + (c - d.D)];
-  }
+    for (int j = 0; j < kMaxJ; ++j) {
+      const int c = q + kLanes * j;
+      const vec *src = c < Dv ? mrow + c : frow + (c - Dv);
+      v[j] = c < Wv ? *src : vec{};
+    }
 #pragma unroll
-  for (int j = 0; j < kMaxJ; ++j) {
-    const int c = lane + 64 * j;
-    if (c < d.D + d.F) X[size_t(row) * d.C + c] = v[j];
+    for (int j = 0; j < kMaxJ; ++j) {
+      const int c = q + kLanes * j;
+      if (c < Wv) xrow[c] = v[j];
+    }
   }
 }
 
@@ -1076,8 +1092,16 @@ extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, in
   const int64_t rows = capacity * fanout;
   if (rows == 0) return SGL_OK;
   SGL_REQUIRE(num_roots && memory && cnt && nbr && eid && X && (F == 0 || efeat), "edge_rows: NULL array");
-  sgl::launch(&k_edge_rows, dim3(unsigned((rows + kRowsPerBlock - 1) / kRowsPerBlock)), dim3(64 * kRowsPerBlock), 0,
-              stream, d, rows, num_roots, memory, efeat, cnt, nbr, eid, X);
+  const auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool v4 = D % 4 == 0 && F % 4 == 0 && d.C % 4 == 0 && a16(memory) && a16(X) && (F == 0 || a16(efeat));
+  const int64_t per = v4 ? kEdgeBlock / (sgl::kWave / 4) : kEdgeBlock / sgl::kWave;
+  const unsigned grid = unsigned(std::min<int64_t>((rows + per - 1) / per, sgl::kMaxGrid));
+  if (v4)
+    sgl::launch(&k_edge_rows<4>, dim3(grid), dim3(kEdgeBlock), 0, stream, d, rows, num_roots, memory, efeat, cnt,
+                nbr, eid, X);
+  else
+    sgl::launch(&k_edge_rows<1>, dim3(grid), dim3(kEdgeBlock), 0, stream, d, rows, num_roots, memory, efeat, cnt,
+                nbr, eid, X);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -5,6 +5,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <type_traits>
@@ -12,6 +13,11 @@
 #include "../../include/starrygl_mi355x.h"
 
 namespace sgl {
+
+// Upper bound on the grids of the grid-stride kernels whose work is the live
+// part of a capacity-sized range (8 workgroups of 256 threads per CU): a
+// batch far below capacity then costs no idle workgroups.
+constexpr int64_t kMaxGrid = 2048;
 
 // Thread-local last error (read through sgl_last_error()).
 void set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));

@@ -37,66 +37,120 @@ __device__ __forceinline__ int32_t node_rank(const uint32_t *__restrict__ bits,
   return prefix[n >> 5] + __popc(w & below);
 }
 
-__global__ __launch_bounds__(kBlock) void k_step_mark(
+__device__ __forceinline__ float ts_from_order(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Multi-workgroup batch preparation (batches above kPrepMaxBatch events):
+// mark, scan, index. Each workgroup of the mark and index kernels takes
+// kAggEvents consecutive events and combines them per node (mark) or per
+// root (index) in a small LDS table before touching global memory: the hot
+// nodes of a skewed stream (a Zipf-distributed one has a node in a third of
+// all events) then cost one global atomic per workgroup instead of one per
+// event, as same-address atomics serialise in L2. A node whose table slot is
+// held by another goes to global memory directly. The running timestamp
+// maximum of the mark kernel lives in the first summary word of node_bits as
+// order(max ts), a word this path does not otherwise use; the scan reads it
+// and clears it again.
+constexpr int kAggBlock = 1024;
+constexpr int kAggPer = 4;
+constexpr int kAggEvents = kAggBlock * kAggPer;
+constexpr int kMarkLog2 = 12;  // node table of the mark kernel (4096 slots, 16 KB)
+constexpr int kMarkSlots = 1 << kMarkLog2;
+constexpr int kIdxLog2 = 10;   // per-role root table of the index kernel (1024 slots, 2 x 16 KB)
+constexpr int kIdxSlots = 1 << kIdxLog2;
+
+__device__ __forceinline__ uint32_t agg_slot(uint32_t key, int log2_slots) {
+  return (key * 2654435761u) >> (32 - log2_slots);
+}
+
+__global__ __launch_bounds__(kAggBlock) void k_step_mark(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
-    const int64_t *__restrict__ dst, const int64_t *__restrict__ cursor, int64_t *__restrict__ batch_start,
-    uint32_t *__restrict__ bits,
+    const int64_t *__restrict__ dst, const float *__restrict__ ts, const int64_t *__restrict__ cursor,
+    int64_t *__restrict__ batch_start, uint32_t *__restrict__ bits, uint32_t *__restrict__ ts_slot,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst,
     int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
-  const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (e == 0) *any_edges = 0;
-  for (int64_t r = 2 * e; r < 2 * e + 2 && r < cap; ++r) {
+  __shared__ int32_t s_node[kMarkSlots];
+  __shared__ float s_m[kAggBlock / sgl::kWave];
+  const int tid = threadIdx.x;
+  const int64_t g = int64_t(blockIdx.x) * kAggBlock + tid;
+  if (g == 0) *any_edges = 0;
+  for (int64_t r = g; r < cap; r += int64_t(gridDim.x) * kAggBlock) {
     win_src[r] = 0ull;
     win_dst[r] = 0ull;
     cnt_src[r] = 0;
     cnt_dst[r] = 0;
   }
+  for (int i = tid; i < kMarkSlots; i += kAggBlock) s_node[i] = -1;
   const int64_t off = cursor != nullptr ? *cursor : 0;
-  if (cursor != nullptr && e == 0) *batch_start = off;
-  if (e >= batch) return;
-  const int64_t s = src[off + e], d = dst[off + e];
-  if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
-    if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
-    return;
+  if (cursor != nullptr && g == 0) *batch_start = off;
+  __syncthreads();
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kAggPer; ++j) {
+    const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+    if (e >= batch) break;
+    const int64_t s = src[off + e], d = dst[off + e];
+    m = fmaxf(m, ts[off + e]);  // fmaxf ignores NaN
+    if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
+      if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
+      continue;
+    }
+#pragma unroll
+    for (int role = 0; role < 2; ++role) {
+      const int32_t n = int32_t(role == 0 ? s : d);
+      const int32_t old = atomicCAS(&s_node[agg_slot(uint32_t(n), kMarkLog2)], -1, n);
+      if (old == n) continue;  // this workgroup marks n already
+      // first in this workgroup (or its slot is taken): set the bit, with no
+      // atomic when another workgroup has set it already
+      const uint32_t mb = 1u << (n & 31);
+      if ((bits[n >> 5] & mb) == 0u) atomicOr(&bits[n >> 5], mb);
+    }
   }
-  atomicOr(&bits[s >> 5], 1u << (s & 31));
-  atomicOr(&bits[d >> 5], 1u << (d & 31));
+  // the block's timestamp maximum, then one atomic max per block, skipped
+  // when the slot already holds as much
+#pragma unroll
+  for (int dd = 32; dd > 0; dd >>= 1) m = fmaxf(m, __shfl_xor(m, dd, sgl::kWave));
+  if ((tid & 63) == 0) s_m[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) {
+    float mm = s_m[0];
+#pragma unroll
+    for (int w = 1; w < kAggBlock / sgl::kWave; ++w) mm = fmaxf(mm, s_m[w]);
+    if (mm > -INFINITY) {
+      const uint32_t k = ts_order(mm);
+      if (*ts_slot < k) atomicMax(ts_slot, k);
+    }
+  }
 }
 
 // One workgroup: exclusive scan of the bitmap word popcounts (-> root count)
-// and the batch's max timestamp (-> the sampler's query time).
+// in tiles of 4 words per thread (16-byte loads and stores), and the batch's
+// max timestamp from the mark kernel's slot (-> the sampler's query time).
 __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     int64_t nwords, const uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
-    const float *__restrict__ ts, int64_t *__restrict__ cursor, const int64_t *__restrict__ batch_start,
-    float *__restrict__ ts_max,
-    int64_t *__restrict__ t_query) {
-  if (cursor != nullptr) ts += *batch_start;
+    uint32_t *__restrict__ ts_slot, int64_t *__restrict__ cursor, const int64_t *__restrict__ batch_start,
+    float *__restrict__ ts_max, int64_t *__restrict__ t_query) {
   __shared__ int32_t s_w[kScanBlock / sgl::kWave];
-  __shared__ float s_m[kScanBlock / sgl::kWave];
-  const int64_t per = (nwords + kScanBlock - 1) / kScanBlock;
-  const int64_t b = int64_t(threadIdx.x) * per;
-  const int64_t e = b + per < nwords ? b + per : nwords;
-  int32_t sum = 0;
-  for (int64_t i = b; i < e; ++i) sum += __popc(bits[i]);
-  int32_t total;
-  int32_t run = sgl::block_exclusive_scan<int32_t, kScanBlock>(sum, s_w, total);
-  for (int64_t i = b; i < e; ++i) {
-    prefix[i] = run;
-    run += __popc(bits[i]);
+  int32_t carry = 0;
+  for (int64_t base = 0; base < nwords; base += 4 * kScanBlock) {
+    const int64_t i = base + 4 * int64_t(threadIdx.x);
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (i < nwords) w = *reinterpret_cast<const uint4 *>(bits + i);
+    const int32_t c0 = __popc(w.x), c1 = __popc(w.y), c2 = __popc(w.z), c3 = __popc(w.w);
+    int32_t total;
+    const int32_t run = carry + sgl::block_exclusive_scan<int32_t, kScanBlock>(c0 + c1 + c2 + c3, s_w, total);
+    if (i < nwords) *reinterpret_cast<int4 *>(prefix + i) = make_int4(run, run + c0, run + c0 + c1, run + c0 + c1 + c2);
+    carry += total;
   }
-  float m = -INFINITY;
-  for (int64_t i = threadIdx.x; i < batch; i += kScanBlock) m = fmaxf(m, ts[i]);
-#pragma unroll
-  for (int d = 32; d > 0; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, sgl::kWave));
-  if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
-  __syncthreads();
   if (threadIdx.x == 0) {
-    float mm = -INFINITY;
-    for (int w = 0; w < kScanBlock / sgl::kWave; ++w) mm = fmaxf(mm, s_m[w]);
-    *num_roots = total;
-    *num_roots64 = total;
+    const uint32_t k = *ts_slot;
+    *ts_slot = 0u;
+    const float mm = k != 0u ? ts_from_order(k) : -INFINITY;
+    *num_roots = carry;
+    *num_roots64 = carry;
     *ts_max = mm;
     // int(float max) truncates toward zero (runtime.py:142); the float32 round
     // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
@@ -105,7 +159,7 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
   }
 }
 
-__global__ __launch_bounds__(kBlock) void k_step_index(
+__global__ __launch_bounds__(kAggBlock) void k_step_index(
     int64_t batch, int64_t num_nodes, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
     const float *__restrict__ ts, const int64_t *__restrict__ batch_start, const uint32_t *__restrict__ bits,
@@ -115,8 +169,15 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
     int32_t *__restrict__ ridx_neg, unsigned long long *__restrict__ win_src,
     unsigned long long *__restrict__ win_dst, int32_t *__restrict__ cnt_src,
     int32_t *__restrict__ cnt_dst) {
-  const int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  if (e >= batch) return;
+  // per role: root rank, count and last-writer key of the table's roots
+  __shared__ int32_t s_root[2][kIdxSlots], s_cnt[2][kIdxSlots];
+  __shared__ unsigned long long s_win[2][kIdxSlots];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kIdxSlots; i += kAggBlock) {
+    s_root[0][i] = s_root[1][i] = -1;
+    s_cnt[0][i] = s_cnt[1][i] = 0;
+    s_win[0][i] = s_win[1][i] = 0ull;
+  }
   if (batch_start != nullptr) {
     const int64_t off = *batch_start;
     src += off;
@@ -124,34 +185,60 @@ __global__ __launch_bounds__(kBlock) void k_step_index(
     ts += off;
     if (neg != nullptr) neg += off;
   }
-  const int64_t s = src[e], d = dst[e];
-  if (neg != nullptr) {
-    const int64_t n = neg[e];
-    int32_t rn = -1;
-    if (n >= 0 && n < num_nodes && ((bits[n >> 5] >> (n & 31)) & 1u)) rn = node_rank(bits, prefix, n);
-    ridx_neg[e] = rn;
-  }
-  if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
-    ridx_src[e] = -1;
-    ridx_dst[e] = -1;
-    return;
-  }
-  const int32_t rs = node_rank(bits, prefix, s);
-  const int32_t rd = node_rank(bits, prefix, d);
   const int64_t tq = *t_query;
-  roots[rs] = s;
-  roots[rd] = d;
-  root_ts[rs] = tq;
-  root_ts[rd] = tq;
-  ridx_src[e] = rs;
-  ridx_dst[e] = rd;
-  // last writer per node and role = the largest (ts, event) pair (stable ts order)
-  const unsigned long long key = (static_cast<unsigned long long>(ts_order(ts[e])) << 32) |
-                                 static_cast<unsigned long long>(e);
-  atomicMax(&win_src[rs], key);
-  atomicMax(&win_dst[rd], key);
-  atomicAdd(&cnt_src[rs], 1);
-  atomicAdd(&cnt_dst[rd], 1);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kAggPer; ++j) {
+    const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+    if (e >= batch) break;
+    const int64_t s = src[e], d = dst[e];
+    if (neg != nullptr) {
+      const int64_t n = neg[e];
+      int32_t rn = -1;
+      if (n >= 0 && n < num_nodes && ((bits[n >> 5] >> (n & 31)) & 1u)) rn = node_rank(bits, prefix, n);
+      ridx_neg[e] = rn;
+    }
+    if (s < 0 || s >= num_nodes || d < 0 || d >= num_nodes) {
+      ridx_src[e] = -1;
+      ridx_dst[e] = -1;
+      continue;
+    }
+    const int32_t rs = node_rank(bits, prefix, s);
+    const int32_t rd = node_rank(bits, prefix, d);
+    ridx_src[e] = rs;
+    ridx_dst[e] = rd;
+    // last writer per root and role = the largest (order(ts), e) key (stable timestamp order)
+    const unsigned long long key = (static_cast<unsigned long long>(ts_order(ts[e])) << 32) |
+                                   static_cast<unsigned long long>(e);
+#pragma unroll
+    for (int role = 0; role < 2; ++role) {
+      const int32_t r = role == 0 ? rs : rd;
+      const int64_t node = role == 0 ? s : d;
+      const int slot = int(agg_slot(uint32_t(r), kIdxLog2));
+      const int32_t old = atomicCAS(&s_root[role][slot], -1, r);
+      if (old == -1 || old == r) {
+        if (old == -1) {  // the root's first event in this workgroup
+          roots[r] = node;
+          root_ts[r] = tq;
+        }
+        atomicAdd(&s_cnt[role][slot], 1);
+        atomicMax(&s_win[role][slot], key);
+      } else {  // the slot holds another root
+        roots[r] = node;
+        root_ts[r] = tq;
+        atomicAdd(role == 0 ? &cnt_src[r] : &cnt_dst[r], 1);
+        atomicMax(role == 0 ? &win_src[r] : &win_dst[r], key);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < 2 * kIdxSlots; i += kAggBlock) {
+    const int role = i / kIdxSlots, slot = i - role * kIdxSlots;
+    const int32_t r = s_root[role][slot];
+    if (r < 0) continue;
+    atomicAdd(role == 0 ? &cnt_src[r] : &cnt_dst[r], s_cnt[role][slot]);
+    atomicMax(role == 0 ? &win_src[r] : &win_dst[r], s_win[role][slot]);
+  }
 }
 
 // One-workgroup batch preparation for batches of up to kPrepMaxBatch events.
@@ -373,10 +460,6 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
   __shared__ int64_t s_root[kTileRows], s_e[2][kTileRows];
   __shared__ int32_t s_cnt[2][kTileRows];
   const int U = *num_roots;
-  const int r0 = blockIdx.x * kTileRows;
-  if (r0 >= U) return;  // uniform per workgroup
-  const int nrows = min(kTileRows, U - r0);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   if (batch_start != nullptr) {  // event arrays are the whole stream
     const int64_t off = *batch_start;
@@ -385,112 +468,123 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     ts += off;
     efeat += off * F;
   }
-  if (tid < kTileRows) {
-    const bool ok = tid < nrows;
-    s_root[tid] = ok ? roots[r0 + tid] : 0;
-    s_cnt[0][tid] = ok ? cnt_src[r0 + tid] : 0;
-    s_cnt[1][tid] = ok ? cnt_dst[r0 + tid] : 0;
-    s_e[0][tid] = ok ? int64_t(win_src[r0 + tid] & 0xffffffffull) : 0;
-    s_e[1][tid] = ok ? int64_t(win_dst[r0 + tid] & 0xffffffffull) : 0;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
-    const int i = idx / D, j = idx - i * D;
-    ms[i * ldh + j] = i < nrows ? memory[s_root[i] * D + j] : 0.f;
-    hs[i * ldh + j] = 0.f;
-  }
-  // Mailbox messages (memory.py:218-248): the src-role message of node u is
-  // [mem(u) || mem(other) || f_e] of its last src event e, the dst-role one
-  // the same for its last dst event. Prefetch the foreign parts.
-  const int i_msg = wave;
-  const bool msg_row = i_msg < nrows;
-  float part[2][kMaxMsgSlots];
-  float ts_e[2] = {0.f, 0.f};
-  int p_slot = 0;
-  if (msg_row) {
-    const int64_t u = s_root[i_msg];
-    p_slot = next_mail_pos[u];
-#pragma unroll
-    for (int role = 0; role < 2; ++role) {
-      const bool has = s_cnt[role][i_msg] > 0;
-      const int64_t e = s_e[role][i_msg];
-      const int64_t other = has ? (role == 0 ? dst[e] : src[e]) : 0;
-      if (has) ts_e[role] = ts[e];
-#pragma unroll
-      for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
-        const int c = lane + 64 * jj;
-        float v = 0.f;
-        if (has && c >= D && c < 2 * D) v = memory[other * D + (c - D)];
-        else if (has && c >= 2 * D && c < S) v = efeat[e * F + (c - 2 * D)];
-        part[role][jj] = v;
-      }
-    }
-  }
-  // GRU layer over the K mailbox slots in slot-index order, h0 = 0
-  for (int k = 0; k < K; ++k) {
-    for (int idx = tid; idx < kTileRows * S; idx += kGruBlock) {
-      const int i = idx / S, j = idx - (idx / S) * S;
-      xs[i * ldx + j] = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
-    }
-    __syncthreads();
-    {
-      sgl::GemmJob jobs[2] = {{xs, ldx, w_ih, S, b_ih, gi, ldg, S, G},
-                              {hs, ldh, w_hh, D, b_hh, gh, ldg, D, k > 0 ? G : 0}};
-      sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
+  // tiles of 16 roots, strided over a bounded grid (uniform per workgroup)
+  for (int r0 = blockIdx.x * kTileRows; r0 < U; r0 += gridDim.x * kTileRows) {
+    // the thread index is made opaque per tile so that the per-thread index
+    // arithmetic (divisions by D and S, message column masks) is recomputed
+    // in each tile rather than kept live across the loop
+    int t = int(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    const int tid = t, wave = t >> 6, lane = t & 63;
+    const int nrows = min(kTileRows, U - r0);
+    if (tid < kTileRows) {
+      const bool ok = tid < nrows;
+      s_root[tid] = ok ? roots[r0 + tid] : 0;
+      s_cnt[0][tid] = ok ? cnt_src[r0 + tid] : 0;
+      s_cnt[1][tid] = ok ? cnt_dst[r0 + tid] : 0;
+      s_e[0][tid] = ok ? int64_t(win_src[r0 + tid] & 0xffffffffull) : 0;
+      s_e[1][tid] = ok ? int64_t(win_dst[r0 + tid] & 0xffffffffull) : 0;
     }
     __syncthreads();
     for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
-      const int i = idx / D, j = idx - (idx / D) * D;
-      const float *g1 = gi + i * ldg;
-      float ghr, ghz, ghn;
-      if (k > 0) {
-        const float *g2 = gh + i * ldg;
-        ghr = g2[j]; ghz = g2[D + j]; ghn = g2[2 * D + j];
-      } else {  // W_hh h0 = 0
-        ghr = b_hh[j]; ghz = b_hh[D + j]; ghn = b_hh[2 * D + j];
+      const int i = idx / D, j = idx - i * D;
+      ms[i * ldh + j] = i < nrows ? memory[s_root[i] * D + j] : 0.f;
+      hs[i * ldh + j] = 0.f;
+    }
+    // Mailbox messages (memory.py:218-248): the src-role message of node u is
+    // [mem(u) || mem(other) || f_e] of its last src event e, the dst-role one
+    // the same for its last dst event. Prefetch the foreign parts.
+    const int i_msg = wave;
+    const bool msg_row = i_msg < nrows;
+    float part[2][kMaxMsgSlots];
+    float ts_e[2] = {0.f, 0.f};
+    int p_slot = 0;
+    if (msg_row) {
+      const int64_t u = s_root[i_msg];
+      p_slot = next_mail_pos[u];
+#pragma unroll
+      for (int role = 0; role < 2; ++role) {
+        const bool has = s_cnt[role][i_msg] > 0;
+        const int64_t e = s_e[role][i_msg];
+        const int64_t other = has ? (role == 0 ? dst[e] : src[e]) : 0;
+        if (has) ts_e[role] = ts[e];
+#pragma unroll
+        for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
+          const int c = lane + 64 * jj;
+          float v = 0.f;
+          if (has && c >= D && c < 2 * D) v = memory[other * D + (c - D)];
+          else if (has && c >= 2 * D && c < S) v = efeat[e * F + (c - 2 * D)];
+          part[role][jj] = v;
+        }
       }
-      hs[i * ldh + j] = gru_combine(g1[j], g1[D + j], g1[2 * D + j], ghr, ghz, ghn, hs[i * ldh + j]);
+    }
+    // GRU layer over the K mailbox slots in slot-index order, h0 = 0
+    for (int k = 0; k < K; ++k) {
+      for (int idx = tid; idx < kTileRows * S; idx += kGruBlock) {
+        const int i = idx / S, j = idx - (idx / S) * S;
+        xs[i * ldx + j] = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
+      }
+      __syncthreads();
+      {
+        sgl::GemmJob jobs[2] = {{xs, ldx, w_ih, S, b_ih, gi, ldg, S, G},
+                                {hs, ldh, w_hh, D, b_hh, gh, ldg, D, k > 0 ? G : 0}};
+        sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
+      }
+      __syncthreads();
+      for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
+        const int i = idx / D, j = idx - (idx / D) * D;
+        const float *g1 = gi + i * ldg;
+        float ghr, ghz, ghn;
+        if (k > 0) {
+          const float *g2 = gh + i * ldg;
+          ghr = g2[j]; ghz = g2[D + j]; ghn = g2[2 * D + j];
+        } else {  // W_hh h0 = 0
+          ghr = b_hh[j]; ghz = b_hh[D + j]; ghn = b_hh[2 * D + j];
+        }
+        hs[i * ldh + j] = gru_combine(g1[j], g1[D + j], g1[2 * D + j], ghr, ghz, ghn, hs[i * ldh + j]);
+      }
+      __syncthreads();
+    }
+    // GRUCell(agg = h, memory)
+    {
+      sgl::GemmJob jobs[2] = {{hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G}, {ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G}};
+      sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
     }
     __syncthreads();
-  }
-  // GRUCell(agg = h, memory)
-  {
-    sgl::GemmJob jobs[2] = {{hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G}, {ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G}};
-    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
-  }
-  __syncthreads();
-  for (int idx = tid; idx < nrows * D; idx += kGruBlock) {
-    const int i = idx / D, j = idx - (idx / D) * D;
-    const float *g1 = gi + i * ldg;
-    const float *g2 = gh + i * ldg;
-    new_mem[size_t(r0 + i) * D + j] =
-        gru_combine(g1[j], g1[D + j], g1[2 * D + j], g2[j], g2[D + j], g2[2 * D + j], ms[i * ldh + j]);
-  }
-
-  // Mailbox write: the src-role message goes to slot p = next_mail_pos[u],
-  // the dst-role one to (p + #src occurrences) % K, so with one slot the dst
-  // role wins; the pointer advances by both counts. Every read of this
-  // root's mailbox rows happened before the barriers above.
-  if (msg_row) {
-    const int64_t u = s_root[i_msg];
-    const int cs = s_cnt[0][i_msg], cd = s_cnt[1][i_msg];
-    const int p2 = (p_slot + cs) % K;
-    const bool write_src = cs > 0 && !(cd > 0 && p2 == p_slot);
-#pragma unroll
-    for (int role = 0; role < 2; ++role) {
-      if (role == 0 && !write_src) continue;
-      if (role == 1 && cd == 0) continue;
-      const int slot = role == 0 ? p_slot : p2;
-      float *out = mailbox + (u * K + slot) * S;
-#pragma unroll
-      for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
-        const int c = lane + 64 * jj;
-        if (c < D) out[c] = ms[i_msg * ldh + c];
-        else if (c < S) out[c] = part[role][jj];
-      }
-      if (lane == 0) mailbox_ts[u * K + slot] = ts_e[role];
+    for (int idx = tid; idx < nrows * D; idx += kGruBlock) {
+      const int i = idx / D, j = idx - (idx / D) * D;
+      const float *g1 = gi + i * ldg;
+      const float *g2 = gh + i * ldg;
+      new_mem[size_t(r0 + i) * D + j] =
+          gru_combine(g1[j], g1[D + j], g1[2 * D + j], g2[j], g2[D + j], g2[2 * D + j], ms[i * ldh + j]);
     }
-    if (lane == 0) next_mail_pos[u] = int32_t((int64_t(p_slot) + cs + cd) % K);
+
+    // Mailbox write: the src-role message goes to slot p = next_mail_pos[u],
+    // the dst-role one to (p + #src occurrences) % K, so with one slot the dst
+    // role wins; the pointer advances by both counts. Every read of this
+    // root's mailbox rows happened before the barriers above.
+    if (msg_row) {
+      const int64_t u = s_root[i_msg];
+      const int cs = s_cnt[0][i_msg], cd = s_cnt[1][i_msg];
+      const int p2 = (p_slot + cs) % K;
+      const bool write_src = cs > 0 && !(cd > 0 && p2 == p_slot);
+#pragma unroll
+      for (int role = 0; role < 2; ++role) {
+        if (role == 0 && !write_src) continue;
+        if (role == 1 && cd == 0) continue;
+        const int slot = role == 0 ? p_slot : p2;
+        float *out = mailbox + (u * K + slot) * S;
+#pragma unroll
+        for (int jj = 0; jj < kMaxMsgSlots; ++jj) {
+          const int c = lane + 64 * jj;
+          if (c < D) out[c] = ms[i_msg * ldh + c];
+          else if (c < S) out[c] = part[role][jj];
+        }
+        if (lane == 0) mailbox_ts[u * K + slot] = ts_e[role];
+      }
+      if (lane == 0) next_mail_pos[u] = int32_t((int64_t(p_slot) + cs + cd) % K);
+    }
+    __syncthreads();  // the next tile reuses the shared root table and LDS tiles
   }
 }
 
@@ -499,16 +593,20 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
     const float *__restrict__ new_mem, float *__restrict__ memory, float *__restrict__ memory_ts,
     const float *__restrict__ ts_max, uint32_t *__restrict__ bits,
     const int32_t *__restrict__ sample_cnt, int32_t *__restrict__ any_edges) {
-  const int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  const int64_t r = idx / D;
-  const int j = int(idx - r * D);
-  if (r >= cap || r >= *num_roots) return;
-  const int64_t u = roots[r];
-  memory[u * D + j] = new_mem[r * D + j];
-  if (j == 0) {
-    memory_ts[u] = *ts_max;
-    bits[u >> 5] = 0u;  // leave the bitmap clear for the next step
-    if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
+  // grid-stride over the live roots' elements (the grid is bounded, so a
+  // large capacity with few live roots costs no idle workgroups)
+  const int64_t live = min(cap, int64_t(*num_roots)) * D;
+  const float tmax = *ts_max;
+  for (int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x; idx < live; idx += int64_t(gridDim.x) * kBlock) {
+    const int64_t r = idx / D;
+    const int j = int(idx - r * D);
+    const int64_t u = roots[r];
+    memory[u * D + j] = new_mem[r * D + j];
+    if (j == 0) {
+      memory_ts[u] = tmax;
+      bits[u >> 5] = 0u;  // leave the bitmap clear for the next step
+      if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
+    }
   }
 }
 
@@ -546,18 +644,20 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
-  const int64_t nwords = (num_nodes + 31) / 32;
-  const unsigned grid = unsigned((cap / 2 + kBlock - 1) / kBlock + 1);
+  SGL_REQUIRE((reinterpret_cast<uintptr_t>(word_prefix) & 15u) == 0, "batch_prepare: word_prefix not 16-byte aligned");
+  const int64_t nwords = bitmap_words(num_nodes);  // a multiple of 4, padding words zero
+  uint32_t *ts_slot = node_bits + nwords;          // the first summary word
+  const unsigned grid = unsigned(std::max<int64_t>(1, (batch + kAggEvents - 1) / kAggEvents));
   auto *ws = reinterpret_cast<unsigned long long *>(win_src);
   auto *wd = reinterpret_cast<unsigned long long *>(win_dst);
-  k_step_mark<<<grid, kBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, cursor, batch_start, node_bits, ws, wd,
-                                           cnt_src, cnt_dst, any_edges, err_flag);
+  k_step_mark<<<grid, kAggBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, ts, cursor, batch_start, node_bits,
+                                           ts_slot, ws, wd, cnt_src, cnt_dst, any_edges, err_flag);
   SGL_CHECK_LAUNCH();
-  k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts,
+  k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts_slot,
                                             cursor, batch_start, ts_max, t_query);
   SGL_CHECK_LAUNCH();
   if (batch > 0) {
-    k_step_index<<<unsigned((batch + kBlock - 1) / kBlock), kBlock, 0, stream>>>(
+    k_step_index<<<grid, kAggBlock, 0, stream>>>(
         batch, num_nodes, src, dst, neg, ts, cursor != nullptr ? batch_start : nullptr, node_bits, word_prefix,
         t_query, roots, root_ts,
         ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
@@ -592,7 +692,7 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
   SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
               64 * kMaxMsgSlots);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox), lds));
-  const unsigned grid = unsigned((capacity + kTileRows - 1) / kTileRows);
+  const unsigned grid = unsigned(std::min<int64_t>((capacity + kTileRows - 1) / kTileRows, sgl::kMaxGrid));
   sgl::launch(&k_gru_mailbox, dim3(grid), dim3(kGruBlock), lds, stream, D, K, F, num_roots, roots, memory, mailbox,
               mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts,
               batch_start, reinterpret_cast<const unsigned long long *>(win_src),
@@ -611,7 +711,8 @@ extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num
   SGL_REQUIRE(num_roots && roots && new_mem && memory && memory_ts && ts_max && node_bits && any_edges,
               "memory_commit: NULL array");
   const int64_t total = capacity * D;
-  sgl::launch(&k_memory_commit, dim3(unsigned((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream, D, capacity,
+  const unsigned grid = unsigned(std::min<int64_t>((total + kBlock - 1) / kBlock, sgl::kMaxGrid));
+  sgl::launch(&k_memory_commit, dim3(grid), dim3(kBlock), 0, stream, D, capacity,
               num_roots, roots, new_mem, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

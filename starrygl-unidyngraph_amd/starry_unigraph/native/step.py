@@ -94,7 +94,9 @@ class StepBuffers:
     hold cap = round_up(2*max_batch, 16) rows (the most roots a batch can
     have), so launch shapes never depend on the batch."""
 
-    def __init__(self, max_batch: int, dims: ConvDims, device):
+    def __init__(self, max_batch: int, dims: ConvDims, device, attention: bool = True):
+        """``attention`` False: only the buffers of the front part (batch
+        preparation, sampling, memory / mailbox update, commit, edge rows)."""
         dev = torch.device(device)
         self.device = dev
         self.max_batch = int(max_batch)
@@ -121,16 +123,18 @@ class StepBuffers:
         self.new_mem = z(c, D)
         self.hop = PaddedHop(cnt=z(c, dt=i32), nbr=z(max(c * k, 1), dt=i32), eid=z(max(c * k, 1), dt=i32),
                              dt=z(max(c * k, 1)), ts=None, q_ts=self.root_ts, fanout=k)
+        # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)]
+        # (sgl_edge_rows, then the forward)
+        self.X = z(max(c * k * C, 1))
+        if not attention:
+            return
         # attention saved state and gradients
         self.Q, self.agg, self.z = z(c, D), z(c, D), z(c, D)
         self.y = z(c + TILE, D)          # rows >= cap stay zero (row U is read by the predictor's reductions)
         self.qt, self.xbar = z(c, H, C), z(c, H, C)
         self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
         self.phi0 = z(max(dims.T, 1))
-        # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)]
-        # (sgl_edge_rows, then the forward) and the sines of its time encoding
-        self.X = z(max(c * k * C, 1))
-        self.S = z(max(c * k * dims.T, 1))
+        self.S = z(max(c * k * dims.T, 1))   # the sines of the edges' time encodings
         self.gy = z(c, D)
         # per-root sums of the predictor's hidden-layer gradients (+ the
         # non-root-negatives row U): fixed-point accumulators the predictor
@@ -157,10 +161,10 @@ class StepBuffers:
 class DeviceStep:
     """The kernel sequence of one step over a NodeState (no host syncs)."""
 
-    def __init__(self, state: NodeState, dims: ConvDims, max_batch: int):
+    def __init__(self, state: NodeState, dims: ConvDims, max_batch: int, attention: bool = True):
         self.state = state
         self.dims = dims
-        self.buf = StepBuffers(max_batch, dims, state.device)
+        self.buf = StepBuffers(max_batch, dims, state.device, attention=attention)
         self.dev = state.device
         self.lib = _capi.lib()
         # optional per-launch timing: a list that receives (name, start, end)

@@ -48,18 +48,27 @@ def _small_batch(rng, n_nodes, B, sorted_ts=True):
     return src, dst, ts, neg
 
 
-@pytest.mark.parametrize("B,sorted_ts", [(600, True), (600, False), (4096, True), (5000, False)])
-def test_batch_prepare_matches_numpy(gpu, B, sorted_ts):
+@pytest.mark.parametrize("B,sorted_ts,skew", [(600, True, False), (600, False, False), (4096, True, False),
+                                               (5000, False, False), (600, False, True), (20000, True, True),
+                                               (20000, False, True)])
+def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew):
     """Roots, root indices, query time, per-role counts and last writers (in
-    stable timestamp order) against numpy: one-workgroup sort path (2B <=
-    8192) with sorted and unsorted timestamps, and the bitmap path."""
+    stable timestamp order) against numpy: the one-workgroup path (B <= 2048)
+    and the multi-workgroup path, with sorted and unsorted timestamps; skewed
+    batches (Zipf 1.5 node ids: a few roots in most events, many in each
+    wave, so the multi-workgroup path combines them per wave)."""
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
-    rng = np.random.default_rng(B)
+    rng = np.random.default_rng(B + skew)
     N = 5000
     st = NodeState(N, 8, 2, 4, gpu)
     step = DeviceStep(st, ConvDims(8, 4, 8, 2, 5), B)
     for _ in range(3):
         src, dst, ts, neg = _small_batch(rng, N, B, sorted_ts)
+        if skew:
+            src = np.minimum(rng.zipf(1.5, B) - 1, N - 1)
+            dst = np.minimum(rng.zipf(1.5, B) - 1, N - 1)
+            if not sorted_ts:   # negative and fractional times: t_query truncates toward zero
+                ts = ts - np.float32(25.5)
         T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
         step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
         b = step.buf
@@ -86,8 +95,12 @@ def test_batch_prepare_matches_numpy(gpu, B, sorted_ts):
             for r, node in enumerate(roots):
                 if c[r]:
                     assert got[r] == last[node], (role, node)
-        # leave the bitmap clear as the commit would
-        st.node_bits.zero_()
+        # the one-workgroup path leaves node_bits zero; the other leaves the
+        # roots' bits for the commit and its summary words (the timestamp slot) zero
+        W = ((N + 31) // 32 + 3) & ~3
+        left = st.node_bits[W:] if B > 2048 else st.node_bits
+        assert int(torch.count_nonzero(left).item()) == 0
+        st.node_bits.zero_()   # as the commit would
 
 
 def _state_pair(gpu, N, D, K, F, seed):
@@ -137,6 +150,58 @@ def test_memory_update_and_mailbox_teacher_forced(gpu, K):
         _close(st.memory, ref.memory, atol=2e-5, msg=f"memory step {it}")
         assert int(st.node_bits.abs().sum().item()) == 0
         st.memory.copy_(ref.memory)            # teacher forcing
+
+
+def test_bounded_grids_cover_large_batches(gpu):
+    """A batch whose roots outnumber one pass of the bounded grids (2048
+    workgroups: the GRU's tiles of 16 roots, the commit's elements, the edge
+    rows' rows loop): mailbox, pointers and memory times bit-exact and memory
+    within rtol 1e-3 against the oracle, and every live edge row equal to the
+    gather of its neighbour's committed memory row and its edge's features."""
+    from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
+    from starry_unigraph.native.step import ConvDims, DeviceStep
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    rng = np.random.default_rng(7)
+    N, D, K, F, T, B, k = 200_000, 16, 2, 4, 8, 30_000, 4
+    st, ref = _state_pair(gpu, N, D, K, F, seed=7)
+    up = CTDGMemoryUpdater(D, 2 * D + F, K).to(gpu)
+    up_ref = co.MemoryUpdaterO(D, 2 * D + F, K)
+    up_ref.load_state_dict({kk: v.cpu() for kk, v in up.state_dict().items()})
+    step = DeviceStep(st, ConvDims(D, F, T, 2, k), B)
+    src, dst, ts, neg = _small_batch(rng, N, B)
+    ef = rng.standard_normal((B, F)).astype(np.float32)
+    Td = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
+    s_d, d_d, t_d, e_d = Td(src), Td(dst), Td(ts, torch.float32), Td(ef, torch.float32)
+    step.prepare(s_d, d_d, Td(neg), t_d)
+    U = int(step.buf.num_roots.item())
+    assert U > 2048 * 16
+    step.update_memory(up.kernel_weights(), s_d, d_d, e_d, t_d)
+    step.commit()
+    co.memory_phase(ref, up_ref, torch.as_tensor(src), torch.as_tensor(dst), torch.as_tensor(ts),
+                    torch.as_tensor(ef))
+    assert torch.equal(st.mailbox.cpu(), ref.mailbox)
+    assert torch.equal(st.mailbox_ts.cpu(), ref.mailbox_ts)
+    assert torch.equal(st.next_mail_pos.cpu().long(), ref.next_mail_pos)
+    assert torch.equal(st.memory_ts.cpu(), ref.memory_ts)
+    _close(st.memory, ref.memory, atol=2e-5, msg="memory")
+    assert int(st.node_bits.abs().sum().item()) == 0
+    # edge rows over U * k > 2048 * 4 rows
+    E = 400_000
+    row, col = rng.integers(0, N, E), rng.integers(0, N, E)
+    g = build_tcsr(N, torch.as_tensor(row), torch.as_tensor(col), None,
+                   torch.as_tensor(np.sort(rng.integers(0, 40, E))))
+    step.sample(RecentSampler(g))
+    efall = torch.randn(E, F, device=gpu)
+    step.edge_rows(efall)
+    b = step.buf
+    cnt = b.hop.cnt[:U].long()
+    assert int(cnt.sum().item()) > 2048 * 4
+    live = (torch.arange(k, device=gpu)[None, :] < cnt[:, None]).reshape(-1)
+    nbr = b.hop.nbr[:U * k].long()[live]
+    eid = b.hop.eid[:U * k].long()[live]
+    X = b.X[:U * k * (D + F + T)].view(U * k, D + F + T)[live]
+    assert torch.equal(X[:, :D], st.memory[nbr])
+    assert torch.equal(X[:, D:D + F], efall[eid])
 
 
 def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
