@@ -16,7 +16,8 @@ Prints ONE JSON line. Workloads:
              (1,140,149 nodes, D = 172, K = 4, F = 16) under batches of 600, 4,000
              and 1,048,576 events of the config-4 stream: batch preparation,
              sampling (k = 20), GRU + mailbox, memory commit, edge-row gather.
-The default run also measures config 3 and reports it under "sampler".
+The default run also measures config 3 and reports it under "sampler", and the
+gather/scatter microbench under "gather_scatter".
 
 Timed region: W untimed warm-up steps, then K steps bracketed by
 torch.cuda.synchronize(); value = events / s over the K steps. Inputs (event
@@ -213,6 +214,11 @@ def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> f
     return 0.0
 
 
+# HBM bytes per launch of k_memory_commit + k_edge_rows at B = 1,048,576 (rocprofv3 FETCH_SIZE x 2.000 +
+# WRITE_SIZE x 1.000, profiles/gather_scatter_cfg5_hbm_traffic.md); None until measured
+GS_TRAFFIC_1M = None
+
+
 def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     """The gather / scatter microbench: config-5 node state (the config-4
     stream's 1,140,149 nodes, D = 172, K = 4 mailbox slots, F = 16), batches of
@@ -297,15 +303,21 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                                                  for n, v in out.items()))
         del step
         torch.cuda.empty_cache()
-    big = cases[str(max(batches))]["kernels"]
-    gb = sum(big[n]["alg_bytes"] for n in ("memory_commit", "edge_rows"))
-    us = sum(big[n]["avg_us"] for n in ("memory_commit", "edge_rows"))
+    big = cases[str(max(batches))]
+    gb = sum(big["kernels"][n]["alg_bytes"] for n in ("memory_commit", "edge_rows"))
+    us = sum(big["kernels"][n]["avg_us"] for n in ("memory_commit", "edge_rows"))
+    # the fused GRU + mailbox kernel is MFMA-bound at this state: 6DS K + 6D^2 (K-1) + 12D^2 flops per root
+    gru_flop = big["mean_roots"] * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
+    gru_tf = gru_flop / (big["kernels"]["memory_update"]["avg_us"] * 1e-6) / 1e12
     return {"value": gb / (us * 1e-6) / 1e9, "unit": "GB/s",
             "workload": f"gather/scatter: cfg5 state (N={N}, D={D}, K={K}, F={F}), k={k}, batches {list(batches)}",
             "cases": cases,
             "roofline": {"bound": "hbm", "kernel": "k_memory_commit + k_edge_rows", "batch": max(batches),
                          "achieved": gb / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None}}
+                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                         "traffic": GS_TRAFFIC_1M if max(batches) == 1 << 20 else None},
+            "gru_mfma": {"kernel": "k_gru_mailbox", "batch": max(batches), "flop_per_launch": round(gru_flop),
+                         "achieved": gru_tf, "peak": 157.3, "unit": "TFLOP/s", "frac": gru_tf / 157.3}}
 
 
 # --------------------------------------------------------------------------- TGN end to end
@@ -605,6 +617,8 @@ def main() -> None:
                              "conv_forward", "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-gather-scatter", action="store_true",
+                    help="skip the gather/scatter sub-benchmark of the default run")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="first run 3 device-to-device copies of this many MiB (a known-size kernel for "
                          "calibrating FETCH_SIZE / WRITE_SIZE counter runs)")
@@ -652,6 +666,9 @@ def main() -> None:
                 step_shape=r["step_shape"], final_train_loss=r["final_train_loss"])
     if args.workload == "tgn-large" and not args.no_sampler:
         line["sampler"] = run_sampler(20, 3, cases=False, cpu=not args.no_cpu)
+    if args.workload == "tgn-large" and not args.no_gather_scatter:
+        gs = run_gather_scatter(5, 1)
+        line["gather_scatter"] = {k: gs[k] for k in ("value", "unit", "workload", "roofline", "gru_mfma")}
     print(json.dumps(line), flush=True)
 
 

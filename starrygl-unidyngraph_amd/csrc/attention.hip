@@ -102,50 +102,74 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
 // Edge rows: X[r*K + e][0, D+F) = [memory[nbr] | efeat[eid]] for every live
 // root r < U and sampled slot e < cnt[r] (rows of C = D+F+T floats; padding
 // slots are not written). The time-encoding columns depend on trained
-// parameters and are filled in by the attention forward. Rows are copied in
-// V-float vectors by 64/V lanes each (V = 4 when D, F and C are multiples of
-// four and the arrays 16-byte aligned: a wave then copies four rows at once),
-// each row's loads issued together; a bounded grid strides over the live
-// roots' rows.
+// parameters and are filled in by the attention forward. A wave takes RW
+// consecutive roots (a bounded grid strides over the live roots) and copies
+// their live rows as one list, 64/L rows per pass, so padding slots cost
+// nothing and a pass is full whatever the per-root counts (RW = 8 when the
+// roots outnumber one pass of the grid; one root per wave below that, for
+// the shortest chain of dependent loads). Rows are copied in V-float vectors
+// by L lanes each, up to JM vectors per lane: V = 4 when D, F and C are
+// multiples of four and the arrays 16-byte aligned, with the fewest lanes per
+// row that keep JM <= 12 (4 lanes for D+F <= 192); otherwise a float per lane
+// and the whole wave per row. Each lane's loads are issued together.
 constexpr int kEdgeBlock = 256;
+constexpr int kEdgeWaves = kEdgeBlock / sgl::kWave;
 
 template <int V> struct EdgeVec;
 template <> struct EdgeVec<1> { using type = float; };
 template <> struct EdgeVec<4> { using type = float4; };
 
-template <int V>
+template <int V, int L, int JM, int RW>
 __global__ __launch_bounds__(kEdgeBlock) void k_edge_rows(
-    Dims d, int64_t nrows_total, const int32_t *__restrict__ num_roots, const float *__restrict__ memory,
+    Dims d, int64_t capacity, const int32_t *__restrict__ num_roots, const float *__restrict__ memory,
     const float *__restrict__ efeat, const int32_t *__restrict__ cnt, const int32_t *__restrict__ nbr,
     const int32_t *__restrict__ eid, float *__restrict__ X) {
+  static_assert(RW == 1 || RW == 2 || RW == 4 || RW == 8 || RW == 16, "RW: a power of two up to 16");
   using vec = typename EdgeVec<V>::type;
-  constexpr int kLanes = sgl::kWave / V;            // lanes per row
-  constexpr int kRows = kEdgeBlock / kLanes;        // rows per workgroup pass
-  const int q = threadIdx.x & (kLanes - 1);
+  constexpr int kPass = sgl::kWave / L;  // rows per pass
+  const int lane = threadIdx.x & 63;
+  const int q = lane & (L - 1), sub = lane / L;
   const int Dv = d.D / V, Fv = d.F / V, Wv = Dv + Fv, Cv = d.C / V;
-  const int64_t live = min(nrows_total, int64_t(*num_roots) * d.k);
-  for (int64_t row = int64_t(blockIdx.x) * kRows + threadIdx.x / kLanes; row < live;
-       row += int64_t(gridDim.x) * kRows) {
-    const int64_t r = row / d.k;
-    const int e = int(row - r * d.k);
-    // issued together: the row's count and sampler entries
-    const int ne = cnt[r];
-    const int nb = nbr[row], ei = eid[row];
-    if (e >= ne) continue;  // a padding slot
-    const vec *mrow = reinterpret_cast<const vec *>(memory) + size_t(nb) * Dv;
-    const vec *frow = reinterpret_cast<const vec *>(efeat) + size_t(ei) * Fv;
-    vec *xrow = reinterpret_cast<vec *>(X) + size_t(row) * Cv;
-    vec v[kMaxJ];
+  const int64_t live = min(capacity, int64_t(*num_roots));
+  for (int64_t r0 = (int64_t(blockIdx.x) * kEdgeWaves + (threadIdx.x >> 6)) * RW; r0 < live;
+       r0 += int64_t(gridDim.x) * kEdgeWaves * RW) {
+    // lanes 0..RW-1: the group's counts and their inclusive prefix
+    const int c = (lane < RW && r0 + lane < live) ? cnt[r0 + lane] : 0;
+    int incl = c;
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) {
-      const int c = q + kLanes * j;
-      const vec *src = c < Dv ? mrow + c : frow + (c - Dv);
-      v[j] = c < Wv ? *src : vec{};
+    for (int dd = 1; dd < RW; dd <<= 1) {
+      const int t = __shfl_up(incl, dd, sgl::kWave);
+      if (lane >= dd) incl += t;
     }
+    const int total = __shfl(incl, RW - 1, sgl::kWave);
+    for (int f0 = 0; f0 < total; f0 += kPass) {  // uniform trip count: every lane takes the shuffles
+      const int f = f0 + sub;
+      // the group's root j holding list entry f: the number of prefixes <= f
+      int j = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxJ; ++j) {
-      const int c = q + kLanes * j;
-      if (c < Wv) xrow[c] = v[j];
+      for (int st = RW / 2; st > 0; st >>= 1) {
+        const int p = __shfl(incl, j + st - 1, sgl::kWave);
+        if (p <= f) j += st;
+      }
+      const int e = f - __shfl(incl - c, j, sgl::kWave);
+      if (f >= total) continue;
+      const int64_t row = (r0 + j) * d.k + e;
+      const int nb = nbr[row], ei = eid[row];
+      const vec *mrow = reinterpret_cast<const vec *>(memory) + size_t(nb) * Dv;
+      const vec *frow = reinterpret_cast<const vec *>(efeat) + size_t(ei) * Fv;
+      vec *xrow = reinterpret_cast<vec *>(X) + size_t(row) * Cv;
+      vec v[JM];
+#pragma unroll
+      for (int jj = 0; jj < JM; ++jj) {
+        const int cc = q + L * jj;
+        const vec *src = cc < Dv ? mrow + cc : frow + (cc - Dv);
+        v[jj] = cc < Wv ? *src : vec{};
+      }
+#pragma unroll
+      for (int jj = 0; jj < JM; ++jj) {
+        const int cc = q + L * jj;
+        if (cc < Wv) xrow[cc] = v[jj];
+      }
     }
   }
 }
@@ -1094,14 +1118,15 @@ extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, in
   SGL_REQUIRE(num_roots && memory && cnt && nbr && eid && X && (F == 0 || efeat), "edge_rows: NULL array");
   const auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   const bool v4 = D % 4 == 0 && F % 4 == 0 && d.C % 4 == 0 && a16(memory) && a16(X) && (F == 0 || a16(efeat));
-  const int64_t per = v4 ? kEdgeBlock / (sgl::kWave / 4) : kEdgeBlock / sgl::kWave;
-  const unsigned grid = unsigned(std::min<int64_t>((rows + per - 1) / per, sgl::kMaxGrid));
-  if (v4)
-    sgl::launch(&k_edge_rows<4>, dim3(grid), dim3(kEdgeBlock), 0, stream, d, rows, num_roots, memory, efeat, cnt,
-                nbr, eid, X);
-  else
-    sgl::launch(&k_edge_rows<1>, dim3(grid), dim3(kEdgeBlock), 0, stream, d, rows, num_roots, memory, efeat, cnt,
-                nbr, eid, X);
+  const unsigned grid = unsigned(std::min<int64_t>((capacity + kEdgeWaves - 1) / kEdgeWaves, sgl::kMaxGrid));
+  // (with 8 roots per wave the bounded grid's waves still outnumber the roots' groups: capacity / 8 > 8192)
+  const int wv = (D + F) / 4;  // vectors per row of the V = 4 kernels (C <= 512: at most 128)
+  const bool group = capacity > sgl::kMaxGrid * kEdgeWaves;  // more roots than one pass of the grid
+  auto kern = group ? &k_edge_rows<1, 64, kMaxJ, 8> : &k_edge_rows<1, 64, kMaxJ, 1>;
+  if (v4 && wv <= 4 * 12) kern = group ? &k_edge_rows<4, 4, 12, 8> : &k_edge_rows<4, 4, 12, 1>;
+  else if (v4 && wv <= 8 * 12) kern = group ? &k_edge_rows<4, 8, 12, 8> : &k_edge_rows<4, 8, 12, 1>;
+  else if (v4) kern = group ? &k_edge_rows<4, 16, 8, 8> : &k_edge_rows<4, 16, 8, 1>;
+  sgl::launch(kern, dim3(grid), dim3(kEdgeBlock), 0, stream, d, capacity, num_roots, memory, efeat, cnt, nbr, eid, X);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -204,6 +204,49 @@ def test_bounded_grids_cover_large_batches(gpu):
     assert torch.equal(X[:, D:D + F], efall[eid])
 
 
+@pytest.mark.parametrize("D,F,T,misaligned,B", [(16, 4, 8, False, 700), (100, 172, 100, False, 700),
+                                                (256, 136, 8, False, 700), (30, 6, 8, False, 700),
+                                                (16, 4, 8, True, 700), (100, 172, 100, False, 5000),
+                                                (256, 136, 8, False, 5000), (30, 6, 8, False, 5000)])
+def test_edge_rows_match_gather(gpu, D, F, T, misaligned, B):
+    """The edge-row gather in each of its layouts (4, 8 or 16 lanes per row
+    with 16-byte vectors; a float per lane when a width is not a multiple of
+    four or the edge features are not 16-byte aligned), one root per wave
+    (capacity 1400) and eight roots' rows as one list (capacity 10000): every
+    live row equals its neighbour's memory row and its edge's features,
+    padding rows stay untouched."""
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    rng = np.random.default_rng(D + F + B)
+    N, k, E = 3000, 12, 40_000
+    st = NodeState(N, D, 1, F, gpu)
+    st.memory.normal_()
+    step = DeviceStep(st, ConvDims(D, F, T, 2, k), B)
+    src, dst, ts, neg = _small_batch(rng, N, B)
+    Td = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
+    step.prepare(Td(src), Td(dst), Td(neg), Td(ts + np.float32(60), torch.float32))
+    U = int(step.buf.num_roots.item())
+    g = build_tcsr(N, torch.as_tensor(rng.integers(0, N, E)), torch.as_tensor(rng.integers(0, N, E)), None,
+                   torch.as_tensor(np.sort(rng.integers(0, 60, E))))
+    step.sample(RecentSampler(g))
+    base = torch.randn(E * F + 2, device=gpu)
+    efall = (base[2:] if misaligned else base[:E * F]).view(E, F)
+    step.buf.X.fill_(-7.0)
+    step.edge_rows(efall)
+    b = step.buf
+    cnt = b.hop.cnt[:U].long()
+    live = (torch.arange(k, device=gpu)[None, :] < cnt[:, None]).reshape(-1)
+    assert int(live.sum().item()) > 0
+    X = b.X[:U * k * (D + F + T)].view(U * k, D + F + T)
+    nbr = b.hop.nbr[:U * k].long()[live]
+    eid = b.hop.eid[:U * k].long()[live]
+    assert torch.equal(X[live][:, :D], st.memory[nbr])
+    assert torch.equal(X[live][:, D:D + F], efall[eid])
+    assert bool((X[live][:, D + F:] == -7.0).all())
+    assert bool((X[~live] == -7.0).all())
+    st.node_bits.zero_()
+
+
 def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
     rng = np.random.default_rng(seed)
     row = rng.integers(0, N, E)
