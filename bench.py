@@ -215,8 +215,8 @@ def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> f
 
 
 # HBM bytes per launch of k_memory_commit + k_edge_rows at B = 1,048,576 (rocprofv3 FETCH_SIZE x 2.000 +
-# WRITE_SIZE x 1.000, profiles/gather_scatter_cfg5_hbm_traffic.md); None until measured
-GS_TRAFFIC_1M = None
+# WRITE_SIZE x 1.000, mean over four batches: profiles/gather_scatter_cfg5_B1M.md)
+GS_TRAFFIC_1M = 133_464_064
 
 
 def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
@@ -225,9 +225,9 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     B consecutive events of that stream for B in `batches`: batch
     preparation, recent-k sampling (k = 20), the fused GRU + mailbox update
     (the roots' memory and mailbox rows gathered, the new messages
-    scattered), the memory commit (scatter) and the edge-row gather, each
-    call timed by an event pair around it; algorithmic bytes per call against
-    HBM."""
+    scattered), the memory commit (scatter) and the edge-row gather; the
+    one-kernel calls timed at their dispatch, the others by an event pair
+    around the call; algorithmic bytes per call against HBM."""
     import torch
 
     from starry_unigraph import synth
@@ -260,10 +260,15 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
         nb = es.num_events // B
         agg = {n: [] for n in names}
         shapes = []
-        # one event pair around each whole call (batch preparation and
-        # sampling launch several kernels each), all on the current stream
+        # the one-kernel calls are timed at their own dispatch (sgl_time_next_launch:
+        # no launch gaps); batch preparation and sampling launch several kernels
+        # each and are timed by an event pair around the call, on the same stream
         evs = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+        single = {"memory_update", "memory_commit", "edge_rows"}
+        timer = []
+        step.timed = single
         for i in range(warmup + steps):
+            step.timer = timer if i >= warmup else None
             # batches from the middle of the stream on, where the sampled windows are full
             a = ((nb // 2 + i) % nb) * B
             sb, db, tb = src[a:a + B], dst[a:a + B], ts[a:a + B]
@@ -285,7 +290,12 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                 E = int(step.buf.hop.cnt[:U].sum().item())
                 shapes.append((U, E))
                 for j, name in enumerate(names):
-                    agg[name].append((evs[j].elapsed_time(evs[j + 1]), U, E))
+                    if name not in single:
+                        agg[name].append((evs[j].elapsed_time(evs[j + 1]), U, E))
+                for name, ev0, ev1 in timer:
+                    agg[name].append((ev0.elapsed_time(ev1), U, E))
+                timer.clear()
+        step.timer = step.timed = None
         out = {}
         for name in names:
             ms = sum(x[0] for x in agg[name]) / len(agg[name])
