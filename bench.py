@@ -295,11 +295,29 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                 for name, ev0, ev1 in timer:
                     agg[name].append((ev0.elapsed_time(ev1), U, E))
                 timer.clear()
+        # the same batches through the bf16-MFMA GRU (bf16 copies of the four weight matrices)
+        gru16 = dict(gru, **{w: gru[w].to(torch.bfloat16) for w in ("w_ih", "w_hh", "wc_ih", "wc_hh")})
+        agg["memory_update_bf16"] = []
+        step.timed = {"memory_update"}
+        for i in range(warmup + steps):
+            a = ((nb // 2 + i) % nb) * B
+            sb, db, tb = src[a:a + B], dst[a:a + B], ts[a:a + B]
+            step.timer = timer if i >= warmup else None
+            step.prepare(sb, db, db.roll(1), tb)
+            step.update_memory(gru16, sb, db, ef[a:a + B], tb)
+            step.timer = None
+            step.commit()
+            if i >= warmup:
+                torch.cuda.synchronize()
+                U = int(step.buf.num_roots.item())
+                for name, ev0, ev1 in timer:
+                    agg["memory_update_bf16"].append((ev0.elapsed_time(ev1), U, 0))
+                timer.clear()
         step.timer = step.timed = None
         out = {}
-        for name in names:
+        for name in names + ("memory_update_bf16",):
             ms = sum(x[0] for x in agg[name]) / len(agg[name])
-            alg = sum(gs_bytes(name, U, E, B, D, F, K) for _, U, E in agg[name]) / len(agg[name])
+            alg = sum(gs_bytes(name.replace("_bf16", ""), U, E, B, D, F, K) for _, U, E in agg[name]) / len(agg[name])
             row = {"avg_us": round(ms * 1e3, 2), "calls": len(agg[name])}
             if alg > 0:
                 gbs = alg / (ms * 1e-3) / 1e9
@@ -319,6 +337,7 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     # the fused GRU + mailbox kernel is MFMA-bound at this state: 6DS K + 6D^2 (K-1) + 12D^2 flops per root
     gru_flop = big["mean_roots"] * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
     gru_tf = gru_flop / (big["kernels"]["memory_update"]["avg_us"] * 1e-6) / 1e12
+    gru16_tf = gru_flop / (big["kernels"]["memory_update_bf16"]["avg_us"] * 1e-6) / 1e12
     return {"value": gb / (us * 1e-6) / 1e9, "unit": "GB/s",
             "workload": f"gather/scatter: cfg5 state (N={N}, D={D}, K={K}, F={F}), k={k}, batches {list(batches)}",
             "cases": cases,
@@ -326,8 +345,11 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                          "achieved": gb / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
                          "traffic": GS_TRAFFIC_1M if max(batches) == 1 << 20 else None},
-            "gru_mfma": {"kernel": "k_gru_mailbox", "batch": max(batches), "flop_per_launch": round(gru_flop),
-                         "achieved": gru_tf, "peak": 157.3, "unit": "TFLOP/s", "frac": gru_tf / 157.3}}
+            "gru_mfma": {"kernel": "k_gru_mailbox<float>", "batch": max(batches), "flop_per_launch": round(gru_flop),
+                         "achieved": gru_tf, "peak": 157.3, "unit": "TFLOP/s", "frac": gru_tf / 157.3},
+            "gru_mfma_bf16": {"kernel": "k_gru_mailbox<uint16_t> (bf16 GEMMs, fp32 accumulation)",
+                              "batch": max(batches), "flop_per_launch": round(gru_flop), "achieved": gru16_tf,
+                              "peak": 2500.0, "unit": "TFLOP/s", "frac": gru16_tf / 2500.0}}
 
 
 # --------------------------------------------------------------------------- TGN end to end
@@ -347,7 +369,7 @@ def build_session(wl: dict, stream):
            "data": {"name": f"bench_{wl['config']}", "format": "synthetic"},
            "train": {"batch_size": wl["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
            "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"], "dropout": 0.0,
-                    "att_dropout": 0.0},
+                    "att_dropout": 0.0, "memory_gemm_dtype": wl.get("gemm", "fp32")},
            "sampling": {"neighbor_limit": [wl["k"]] * wl["history"], "history": wl["history"],
                         "strategy": "recent"}}
     torch.manual_seed(0)
@@ -627,6 +649,9 @@ def main() -> None:
                              "conv_forward", "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--memory-gemm-dtype", default="fp32", choices=["fp32", "bf16"],
+                    help="the memory updater's GEMMs (TGN workloads): fp32 MFMA, or bf16 MFMA with fp32 "
+                         "accumulation (the mixed-precision setting; dtype reads fp32+bf16)")
     ap.add_argument("--no-gather-scatter", action="store_true",
                     help="skip the gather/scatter sub-benchmark of the default run")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -665,9 +690,10 @@ def main() -> None:
                     roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), cases=r.get("cases"))
         print(json.dumps(line), flush=True)
         return
-    wl = WORKLOADS[args.workload]
+    wl = dict(WORKLOADS[args.workload], gemm=args.memory_gemm_dtype)
     r = run_tgn(args, wl)
-    line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"], dtype="fp32",
+    line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"],
+                dtype="fp32" if args.memory_gemm_dtype == "fp32" else "fp32 (GRU GEMMs bf16)",
                 config={"workload": f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
                                     f"H={wl['H']} k={wl['k']} hops={wl['history']} K={wl['K']} B={wl['B']}, "
                                     "dropout 0",
@@ -678,7 +704,8 @@ def main() -> None:
         line["sampler"] = run_sampler(20, 3, cases=False, cpu=not args.no_cpu)
     if args.workload == "tgn-large" and not args.no_gather_scatter:
         gs = run_gather_scatter(5, 1)
-        line["gather_scatter"] = {k: gs[k] for k in ("value", "unit", "workload", "roofline", "gru_mfma")}
+        line["gather_scatter"] = {k: gs[k] for k in ("value", "unit", "workload", "roofline", "gru_mfma",
+                                                      "gru_mfma_bf16")}
     print(json.dumps(line), flush=True)
 
 

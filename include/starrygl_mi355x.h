@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 6
+#define SGL_ABI_VERSION 7
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -179,6 +179,27 @@ int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
                       const uint64_t *win_src, const uint64_t *win_dst,
                       const int32_t *cnt_src, const int32_t *cnt_dst,
                       float *new_mem, hipStream_t stream);
+/* The same update with the GRU's four weight matrices in bf16 (raw 16-bit
+ * patterns, the same layouts): its GEMMs run on bf16 MFMA with fp32
+ * accumulation, the mailbox rows, hidden state and memory rounded to bf16 as
+ * they enter a product; biases, gates, state and the mailbox stay fp32 (the
+ * mixed-precision setting: bf16 GEMMs, fp32 memory). The updater's weights
+ * never train (its output is detached, runtime.py:279), so the caller makes
+ * the bf16 copies once. Mailbox contents, slots and pointers are the same as
+ * sgl_memory_update's; new_mem within the bf16 tolerance (rtol 2e-2). */
+int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
+                           const int32_t *num_roots, const int64_t *roots,
+                           const float *memory, float *mailbox, float *mailbox_ts,
+                           int32_t *next_mail_pos, const uint16_t *w_ih,
+                           const uint16_t *w_hh, const float *b_ih, const float *b_hh,
+                           const uint16_t *wc_ih, const uint16_t *wc_hh,
+                           const float *bc_ih, const float *bc_hh,
+                           const int64_t *src, const int64_t *dst,
+                           const float *efeat, const float *ts,
+                           const int64_t *batch_start,
+                           const uint64_t *win_src, const uint64_t *win_dst,
+                           const int32_t *cnt_src, const int32_t *cnt_dst,
+                           float *new_mem, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * (5) Memory commit.

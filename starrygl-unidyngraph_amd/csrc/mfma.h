@@ -308,6 +308,124 @@ __device__ __forceinline__ void tile_gemm16_jobs(const GemmJob (&jobs)[NJOBS], i
 }
 
 // ---------------------------------------------------------------------------
+// bf16 products with fp32 accumulation: v_mfma_f32_16x16x32_bf16. Lane l
+// supplies eight k values of A row l % 16 and of op(W) column n0 + l % 16,
+// k = kb + 8 (l / 16) + j for j < 8; the hardware pairs A's and W's elements
+// by (lane group, element), so the product is the full sum over k whatever
+// order it assigns them. The result layout is the 16x16 f32 one above. A is
+// fp32 in LDS and rounded to bf16 (nearest even) as it is read; W is a bf16
+// weight matrix (raw 16-bit patterns) in global memory, row n holding op(W)
+// column n (kNT). k past kd and columns past n_total read 0.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ bf16x8 bf16x8_from_f32(const f32x4 &x0, const f32x4 &x1) {
+  bf16x8 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r[j] = static_cast<__bf16>(x0[j]);
+    r[4 + j] = static_cast<__bf16>(x1[j]);
+  }
+  return r;
+}
+
+__device__ __forceinline__ f32x4 mfma_block16_bf16(const float *__restrict__ A, int lda,
+                                                   const uint16_t *__restrict__ W, int ldw, int n0, int kd,
+                                                   int n_total) {
+  const int lane = threadIdx.x & 63;
+  const int i = lane & 15;
+  const int q = lane >> 4;
+  const int n = n0 + i;
+  const bool nok = n < n_total;
+  const uint16_t *wrow = W + size_t(nok ? n : 0) * size_t(ldw);
+  const float *arow = A + i * lda;
+  // 16-byte weight loads when row starts and k offsets are multiples of 8
+  // elements, else two 8-byte loads when they are multiples of 4 (D = 172)
+  const bool wvec = (ldw & 7) == 0 && (kd & 7) == 0 && aligned16(W);
+  const bool wvec4 = !wvec && (ldw & 3) == 0 && (kd & 3) == 0 && (reinterpret_cast<uintptr_t>(W) & 7u) == 0;
+  const bool avec = (lda & 3) == 0 && aligned16(A);
+  constexpr int kU = 8;  // k steps of 32 whose weights are loaded together
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  for (int kb = 0; kb < kd; kb += 32 * kU) {
+    bf16x8 b[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = kb + 32 * u + 8 * q;
+      if (wvec && nok && k + 8 <= kd) {
+        b[u] = *reinterpret_cast<const bf16x8 *>(wrow + k);
+      } else if (wvec4 && nok && k + 4 <= kd) {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(wrow + k);
+        const bf16x4 hi = k + 8 <= kd ? *reinterpret_cast<const bf16x4 *>(wrow + k + 4)
+                                      : bf16x4{static_cast<__bf16>(0.f), static_cast<__bf16>(0.f),
+                                               static_cast<__bf16>(0.f), static_cast<__bf16>(0.f)};
+        b[u] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          b[u][j] = (nok && k + j < kd) ? __builtin_bit_cast(__bf16, wrow[k + j]) : static_cast<__bf16>(0.f);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = kb + 32 * u + 8 * q;
+      if (kb + 32 * u >= kd) break;  // uniform
+      bf16x8 a;
+      if (avec && k + 8 <= kd) {
+        a = bf16x8_from_f32(*reinterpret_cast<const f32x4 *>(arow + k), *reinterpret_cast<const f32x4 *>(arow + k + 4));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(k + j < kd ? arow[min(k + j, kd - 1)] : 0.f);
+      }
+      if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc1, 0, 0, 0);
+      else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc0, 0, 0, 0);
+    }
+  }
+  return acc0 + acc1;
+}
+
+// The bf16 counterpart of GemmJob / tile_gemm16_jobs (kNT weights only).
+struct GemmJobBf16 {
+  const float *A;
+  int lda;
+  const uint16_t *W;
+  int ldw;
+  const float *bias;  // fp32, may be NULL
+  float *OUT;
+  int ldo;
+  int kd, n_total;
+};
+
+template <int NJOBS>
+__device__ __forceinline__ void tile_gemm16_jobs_bf16(const GemmJobBf16 (&jobs)[NJOBS], int nwaves) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < NJOBS; ++j) total += (jobs[j].n_total + 15) >> 4;
+  for (int blk = wave; blk < total; blk += nwaves) {
+    GemmJobBf16 jb = jobs[0];
+    int nb = blk, first = 0;
+#pragma unroll
+    for (int j = 0; j < NJOBS; ++j) {
+      const int nbj = (jobs[j].n_total + 15) >> 4;
+      if (blk >= first && blk < first + nbj) {
+        jb = jobs[j];
+        nb = blk - first;
+      }
+      first += nbj;
+    }
+    const int n0 = nb * 16;
+    const int col = n0 + (lane & 15);
+    const float bv = jb.bias != nullptr && col < jb.n_total ? jb.bias[col] : 0.f;
+    f32x4 acc = mfma_block16_bf16(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
+    if (col < jb.n_total) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Four-row tiles (a workgroup's 4 live roots): v_mfma_f32_4x4x1_16b_f32 runs
 // 16 independent 4x4x1 blocks. With every block fed the same four A rows and
 // block b taking columns 4b..4b+3 of a 64-column strip, one instruction adds

@@ -434,14 +434,33 @@ static_assert(kGruWaves == kTileRows, "the mailbox phase maps wave w to root w")
 // other endpoint's memory row and the edge's features) are loaded into
 // registers before the GEMMs and stored after them, so the loads overlap
 // the GRU arithmetic.
+// The GRU's weight matrices are fp32 (WT = float: fp32 MFMA) or bf16
+// (WT = uint16_t, raw bf16 patterns: bf16 MFMA with fp32 accumulation, the
+// LDS operands rounded to bf16 as they are read); biases, gates and state
+// stay fp32.
+template <typename WT>
+__device__ __forceinline__ void gru_products(const float *A0, int lda0, const WT *W0, int ldw0, const float *b0,
+                                             float *O0, int kd0, int n0, const float *A1, int lda1, const WT *W1,
+                                             int ldw1, const float *b1, float *O1, int kd1, int n1, int ldo) {
+  if constexpr (std::is_same_v<WT, float>) {
+    sgl::GemmJob jobs[2] = {{A0, lda0, W0, ldw0, b0, O0, ldo, kd0, n0}, {A1, lda1, W1, ldw1, b1, O1, ldo, kd1, n1}};
+    sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
+  } else {
+    sgl::GemmJobBf16 jobs[2] = {{A0, lda0, W0, ldw0, b0, O0, ldo, kd0, n0},
+                                {A1, lda1, W1, ldw1, b1, O1, ldo, kd1, n1}};
+    sgl::tile_gemm16_jobs_bf16(jobs, kGruWaves);
+  }
+}
+
+template <typename WT>
 __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     int D, int K, int F, const int32_t *__restrict__ num_roots,
     const int64_t *__restrict__ roots, const float *__restrict__ memory,
     float *__restrict__ mailbox, float *__restrict__ mailbox_ts,
-    int32_t *__restrict__ next_mail_pos, const float *__restrict__ w_ih,
-    const float *__restrict__ w_hh, const float *__restrict__ b_ih,
-    const float *__restrict__ b_hh, const float *__restrict__ wc_ih,
-    const float *__restrict__ wc_hh, const float *__restrict__ bc_ih,
+    int32_t *__restrict__ next_mail_pos, const WT *__restrict__ w_ih,
+    const WT *__restrict__ w_hh, const float *__restrict__ b_ih,
+    const float *__restrict__ b_hh, const WT *__restrict__ wc_ih,
+    const WT *__restrict__ wc_hh, const float *__restrict__ bc_ih,
     const float *__restrict__ bc_hh, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const float *__restrict__ efeat,
     const float *__restrict__ ts, const int64_t *__restrict__ batch_start,
@@ -525,11 +544,7 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
         xs[i * ldx + j] = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
       }
       __syncthreads();
-      {
-        sgl::GemmJob jobs[2] = {{xs, ldx, w_ih, S, b_ih, gi, ldg, S, G},
-                                {hs, ldh, w_hh, D, b_hh, gh, ldg, D, k > 0 ? G : 0}};
-        sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
-      }
+      gru_products<WT>(xs, ldx, w_ih, S, b_ih, gi, S, G, hs, ldh, w_hh, D, b_hh, gh, D, k > 0 ? G : 0, ldg);
       __syncthreads();
       for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
         const int i = idx / D, j = idx - (idx / D) * D;
@@ -546,10 +561,7 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
       __syncthreads();
     }
     // GRUCell(agg = h, memory)
-    {
-      sgl::GemmJob jobs[2] = {{hs, ldh, wc_ih, D, bc_ih, gi, ldg, D, G}, {ms, ldh, wc_hh, D, bc_hh, gh, ldg, D, G}};
-      sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
-    }
+    gru_products<WT>(hs, ldh, wc_ih, D, bc_ih, gi, D, G, ms, ldh, wc_hh, D, bc_hh, gh, D, G, ldg);
     __syncthreads();
     for (int idx = tid; idx < nrows * D; idx += kGruBlock) {
       const int i = idx / D, j = idx - (idx / D) * D;
@@ -689,15 +701,13 @@ extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {
   return sizeof(float) * kTileRows * (sgl::lds_ld(int(S)) + 2 * sgl::lds_ld(D) + 2 * sgl::lds_ld(int(G)));
 }
 
-extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
-                                 const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
-                                 int32_t *next_mail_pos, const float *w_ih, const float *w_hh, const float *b_ih,
-                                 const float *b_hh, const float *wc_ih, const float *wc_hh, const float *bc_ih,
-                                 const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
-                                 const float *ts, const int64_t *batch_start, const uint64_t *win_src,
-                                 const uint64_t *win_dst,
-                                 const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
-                                 hipStream_t stream) {
+template <typename WT>
+static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
+                  const float *memory, float *mailbox, float *mailbox_ts, int32_t *next_mail_pos, const WT *w_ih,
+                  const WT *w_hh, const float *b_ih, const float *b_hh, const WT *wc_ih, const WT *wc_hh,
+                  const float *bc_ih, const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
+                  const float *ts, const int64_t *batch_start, const uint64_t *win_src, const uint64_t *win_dst,
+                  const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem, hipStream_t stream) {
   SGL_REQUIRE(D > 0 && K > 0 && F >= 0, "memory_update: bad dims D=%d K=%d F=%d", D, K, F);
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX, "memory_update: capacity out of range");
   if (capacity == 0) return SGL_OK;
@@ -709,14 +719,42 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
   SGL_REQUIRE(lds <= 160 * 1024, "memory_update: D=%d F=%d needs %zu bytes of LDS (> 160 KiB)", D, F, lds);
   SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
               64 * kMaxMsgSlots);
-  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox), lds));
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox<WT>), lds));
   const unsigned grid = unsigned(std::min<int64_t>((capacity + kTileRows - 1) / kTileRows, sgl::kMaxGrid));
-  sgl::launch(&k_gru_mailbox, dim3(grid), dim3(kGruBlock), lds, stream, D, K, F, num_roots, roots, memory, mailbox,
-              mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts,
-              batch_start, reinterpret_cast<const unsigned long long *>(win_src),
+  sgl::launch(&k_gru_mailbox<WT>, dim3(grid), dim3(kGruBlock), lds, stream, D, K, F, num_roots, roots, memory,
+              mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst,
+              efeat, ts, batch_start, reinterpret_cast<const unsigned long long *>(win_src),
               reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
+}
+
+extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
+                                 const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
+                                 int32_t *next_mail_pos, const float *w_ih, const float *w_hh, const float *b_ih,
+                                 const float *b_hh, const float *wc_ih, const float *wc_hh, const float *bc_ih,
+                                 const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
+                                 const float *ts, const int64_t *batch_start, const uint64_t *win_src,
+                                 const uint64_t *win_dst,
+                                 const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
+                                 hipStream_t stream) {
+  return memory_update<float>(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih,
+                              w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts, batch_start,
+                              win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
+}
+
+extern "C" int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
+                                      const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
+                                      int32_t *next_mail_pos, const uint16_t *w_ih, const uint16_t *w_hh,
+                                      const float *b_ih, const float *b_hh, const uint16_t *wc_ih,
+                                      const uint16_t *wc_hh, const float *bc_ih, const float *bc_hh,
+                                      const int64_t *src, const int64_t *dst, const float *efeat, const float *ts,
+                                      const int64_t *batch_start, const uint64_t *win_src, const uint64_t *win_dst,
+                                      const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
+                                      hipStream_t stream) {
+  return memory_update<uint16_t>(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos,
+                                 w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts,
+                                 batch_start, win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
 }
 
 extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,

@@ -54,7 +54,8 @@ def build_ctdg_runtime(session_ctx: SessionContext, events=None) -> tuple[CTDGOn
                              edge_feat_dim=edge_feat_dim, dim_time=dim_time, num_head=num_head, dropout=dropout,
                              att_dropout=att_dropout).to(device)
     memory_updater = CTDGMemoryUpdater(hidden_dim=hidden_dim, mailbox_slot_dim=2 * hidden_dim + edge_feat_dim,
-                                       mailbox_slots=mailbox_slots).to(device)
+                                       mailbox_slots=mailbox_slots,
+                                       gemm_dtype=str(c.get("memory_gemm_dtype", "fp32"))).to(device)
     optimizer = make_optimizer(model, lr=float(cfg.get("train", {}).get("lr", 1e-3)))
     runtime = CTDGOnlineRuntime(dataset=dataset, sampler=sampler, memory=memory, model=model, optimizer=optimizer,
                                 route=_SingleRankRoute(str(cfg["graph"]["route"]), session_ctx.dist.world_size),

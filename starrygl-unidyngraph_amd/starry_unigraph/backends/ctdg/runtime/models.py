@@ -80,18 +80,43 @@ class CTDGModelOutput:
 class CTDGMemoryUpdater(nn.Module):
     """GRU over the K-slot mailbox, then GRUCell with the memory (models.py:214-254)."""
 
-    def __init__(self, hidden_dim: int, mailbox_slot_dim: int, mailbox_slots: int) -> None:
+    _MATRICES = ("w_ih", "w_hh", "wc_ih", "wc_hh")
+
+    def __init__(self, hidden_dim: int, mailbox_slot_dim: int, mailbox_slots: int, gemm_dtype: str = "fp32") -> None:
         super().__init__()
+        if gemm_dtype not in ("fp32", "bf16"):
+            raise ValueError(f"memory updater GEMM dtype {gemm_dtype!r}: expected 'fp32' or 'bf16'")
         self.hidden_dim = hidden_dim
         self.mailbox_slots = mailbox_slots
+        self.gemm_dtype = gemm_dtype
         self.mail_aggregator = nn.GRU(input_size=mailbox_slot_dim, hidden_size=hidden_dim, batch_first=True)
         self.memory_cell = nn.GRUCell(hidden_dim, hidden_dim)
+        self._bf16: dict[str, torch.Tensor] = {}
+        self._bf16_versions: tuple = ()
 
     def kernel_weights(self) -> dict[str, torch.Tensor]:
+        """The fused kernel's operands. With bf16 GEMMs the four weight
+        matrices are bf16 copies (round to nearest even) held in persistent
+        buffers: the weights never train (the update is detached,
+        runtime.py:279), and a changed weight (a loaded checkpoint) is copied
+        into the same buffers, so recorded launch plans stay valid."""
         g, c = self.mail_aggregator, self.memory_cell
-        return {"w_ih": g.weight_ih_l0.detach(), "w_hh": g.weight_hh_l0.detach(), "b_ih": g.bias_ih_l0.detach(),
-                "b_hh": g.bias_hh_l0.detach(), "wc_ih": c.weight_ih.detach(), "wc_hh": c.weight_hh.detach(),
-                "bc_ih": c.bias_ih.detach(), "bc_hh": c.bias_hh.detach()}
+        w = {"w_ih": g.weight_ih_l0.detach(), "w_hh": g.weight_hh_l0.detach(), "b_ih": g.bias_ih_l0.detach(),
+             "b_hh": g.bias_hh_l0.detach(), "wc_ih": c.weight_ih.detach(), "wc_hh": c.weight_hh.detach(),
+             "bc_ih": c.bias_ih.detach(), "bc_hh": c.bias_hh.detach()}
+        if self.gemm_dtype == "fp32":
+            return w
+        params = (g.weight_ih_l0, g.weight_hh_l0, c.weight_ih, c.weight_hh)
+        versions = tuple((p.data_ptr(), p._version) for p in params)
+        if versions != self._bf16_versions:
+            for name in self._MATRICES:
+                if name in self._bf16 and self._bf16[name].shape == w[name].shape:
+                    self._bf16[name].copy_(w[name])
+                else:
+                    self._bf16[name] = w[name].to(torch.bfloat16).contiguous()
+            self._bf16_versions = versions
+        w.update(self._bf16)
+        return w
 
     @torch.no_grad()
     def forward(self, mailbox_history: torch.Tensor, current_memory: torch.Tensor) -> torch.Tensor:
@@ -119,11 +144,12 @@ class CTDGMemoryUpdater(nn.Module):
         dummy_f = torch.zeros(max(Fd, 1), dtype=torch.float32, device=dev)
         mts = torch.zeros(M, K, dtype=torch.float32, device=dev)
         nmp = torch.zeros(M, dtype=torch.int32, device=dev)
-        _capi.check(_capi.lib().sgl_memory_update(
+        name = "sgl_memory_update_bf16" if self.gemm_dtype == "bf16" else "sgl_memory_update"
+        _capi.check(getattr(_capi.lib(), name)(
             D, K, Fd, cap, P(n), P(roots), P(mem), P(mail), P(mts), P(nmp), P(w["w_ih"]), P(w["w_hh"]),
             P(w["b_ih"]), P(w["b_hh"]), P(w["wc_ih"]), P(w["wc_hh"]), P(w["bc_ih"]), P(w["bc_hh"]), P(dummy_i64),
             P(dummy_i64), P(dummy_f), P(dummy_f), None, P(zeros_k), P(zeros_k), P(zeros_i), P(zeros_i), P(out),
-            _capi.stream_of(dev)), "sgl_memory_update")
+            _capi.stream_of(dev)), name)
         return out[:M]
 
 

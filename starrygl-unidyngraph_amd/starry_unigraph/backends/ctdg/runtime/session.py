@@ -74,3 +74,4 @@ class CTDGSession:
                 core.state_dict()[name].copy_(t)        # in place: parameters are views of the optimizer's buffer
             if self.online_runtime.memory_updater is not None and "memory_updater" in ckpt:
                 self.online_runtime.memory_updater.load_state_dict(ckpt["memory_updater"])
+                self.online_runtime.memory_updater.kernel_weights()   # refresh bf16 copies in place

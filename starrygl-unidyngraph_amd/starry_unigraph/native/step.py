@@ -222,12 +222,14 @@ class DeviceStep:
         span the stream and the batch starts at buf.batch_start."""
         event_offset = self.buf.batch_start if from_cursor else None
         b, st, P = self.buf, self.state, _capi.ptr
-        self._call("memory_update", lambda: _capi.check(_capi.call("sgl_memory_update", 
+        # bf16 weight matrices select the bf16-MFMA entry point
+        fn = "sgl_memory_update_bf16" if gru["w_ih"].dtype == torch.bfloat16 else "sgl_memory_update"
+        self._call("memory_update", lambda: _capi.check(_capi.call(fn, 
             st.D, st.K, st.F, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(st.mailbox), P(st.mailbox_ts),
             P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
             P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(event_offset),
             P(b.win_src),
-            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), "sgl_memory_update"))
+            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), fn))
 
     def commit(self) -> None:
         b, st, P = self.buf, self.state, _capi.ptr

@@ -21,12 +21,17 @@ def _close(got, want, rtol=RTOL, atol=1e-5, msg=""):
                                msg=msg)
 
 
-@pytest.mark.parametrize("K,D,F", [(1, 100, 16), (3, 32, 5), (4, 172, 16)])
-def test_gru_kernel_matches_torch(gpu, K, D, F):
+@pytest.mark.parametrize("K,D,F,dt", [(1, 100, 16, "fp32"), (3, 32, 5, "fp32"), (4, 172, 16, "fp32"),
+                                      (1, 100, 16, "bf16"), (3, 32, 5, "bf16"), (4, 172, 16, "bf16")])
+def test_gru_kernel_matches_torch(gpu, K, D, F, dt):
+    """The fused GRU + GRUCell against the oracle's torch modules: fp32 MFMA
+    within rtol 1e-3; bf16 MFMA (bf16 weights and operands, fp32
+    accumulation) within the bf16 tolerance rtol 2e-2, atol 2e-2 (outputs are
+    tanh-bounded, |h| < 1)."""
     from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
     torch.manual_seed(K)
     S = 2 * D + F
-    up = CTDGMemoryUpdater(D, S, K).to(gpu)
+    up = CTDGMemoryUpdater(D, S, K, gemm_dtype=dt).to(gpu)
     ref = co.MemoryUpdaterO(D, S, K)
     ref.load_state_dict({k: v.cpu() for k, v in up.state_dict().items()})
     M = 203
@@ -35,7 +40,12 @@ def test_gru_kernel_matches_torch(gpu, K, D, F):
     got = up(mail.to(gpu), mem.to(gpu))
     with torch.no_grad():
         want = ref(mail, mem)
-    _close(got, want, atol=2e-5)
+    if dt == "fp32":
+        _close(got, want, atol=2e-5)
+    else:
+        _close(got, want, rtol=2e-2, atol=2e-2)
+        # and not the fp32 result by accident: bf16 rounding leaves a visible difference
+        assert float((got.cpu() - want).abs().max()) > 1e-5
 
 
 def _small_batch(rng, n_nodes, B, sorted_ts=True):
@@ -119,16 +129,16 @@ def _state_pair(gpu, N, D, K, F, seed):
     return st, ref
 
 
-@pytest.mark.parametrize("K", [1, 2, 4])
-def test_memory_update_and_mailbox_teacher_forced(gpu, K):
+@pytest.mark.parametrize("K,dt", [(1, "fp32"), (2, "fp32"), (4, "fp32"), (1, "bf16"), (4, "bf16")])
+def test_memory_update_and_mailbox_teacher_forced(gpu, K, dt):
     """Each step starts from identical state: mailbox/ts/slot pointers bit-exact,
-    memory within rtol 1e-3."""
+    memory within rtol 1e-3 (fp32 GEMMs) or 2e-2 (bf16 GEMMs)."""
     from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
     from starry_unigraph.native.step import ConvDims, DeviceStep
     rng = np.random.default_rng(K)
     N, D, F, B = 700, 32, 6, 300
     st, ref = _state_pair(gpu, N, D, K, F, seed=K)
-    up = CTDGMemoryUpdater(D, 2 * D + F, K).to(gpu)
+    up = CTDGMemoryUpdater(D, 2 * D + F, K, gemm_dtype=dt).to(gpu)
     up_ref = co.MemoryUpdaterO(D, 2 * D + F, K)
     up_ref.load_state_dict({k: v.cpu() for k, v in up.state_dict().items()})
     step = DeviceStep(st, ConvDims(D, F, 8, 2, 4), B)
@@ -147,7 +157,10 @@ def test_memory_update_and_mailbox_teacher_forced(gpu, K):
         assert torch.equal(st.mailbox_ts.cpu(), ref.mailbox_ts)
         assert torch.equal(st.next_mail_pos.cpu().long(), ref.next_mail_pos)
         assert torch.equal(st.memory_ts.cpu(), ref.memory_ts)
-        _close(st.memory, ref.memory, atol=2e-5, msg=f"memory step {it}")
+        if dt == "fp32":
+            _close(st.memory, ref.memory, atol=2e-5, msg=f"memory step {it}")
+        else:
+            _close(st.memory, ref.memory, rtol=2e-2, atol=2e-2, msg=f"memory step {it}")
         assert int(st.node_bits.abs().sum().item()) == 0
         st.memory.copy_(ref.memory)            # teacher forcing
 
