@@ -105,8 +105,8 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
 // parameters and are filled in by the attention forward. A wave takes RW
 // consecutive roots (a bounded grid strides over the live roots) and copies
 // their live rows as one list, 64/L rows per pass, so padding slots cost
-// nothing and a pass is full whatever the per-root counts (RW = 8 when the
-// roots outnumber one pass of the grid; one root per wave below that, for
+// nothing and a pass is full whatever the per-root counts (RW = kEdgeGroup
+// when the roots outnumber one pass of the grid; one root per wave below that, for
 // the shortest chain of dependent loads). Rows are copied in V-float vectors
 // by L lanes each, up to JM vectors per lane: V = 4 when D, F and C are
 // multiples of four and the arrays 16-byte aligned, with the fewest lanes per
@@ -114,6 +114,7 @@ __device__ __forceinline__ void te_sincos(float x, float &sn, float &cs) {
 // and the whole wave per row. Each lane's loads are issued together.
 constexpr int kEdgeBlock = 256;
 constexpr int kEdgeWaves = kEdgeBlock / sgl::kWave;
+constexpr int kEdgeGroup = 4;  // roots per wave when the roots outnumber one pass of the grid
 
 template <int V> struct EdgeVec;
 template <> struct EdgeVec<1> { using type = float; };
@@ -1119,13 +1120,12 @@ extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, in
   const auto a16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   const bool v4 = D % 4 == 0 && F % 4 == 0 && d.C % 4 == 0 && a16(memory) && a16(X) && (F == 0 || a16(efeat));
   const unsigned grid = unsigned(std::min<int64_t>((capacity + kEdgeWaves - 1) / kEdgeWaves, sgl::kMaxGrid));
-  // (with 8 roots per wave the bounded grid's waves still outnumber the roots' groups: capacity / 8 > 8192)
   const int wv = (D + F) / 4;  // vectors per row of the V = 4 kernels (C <= 512: at most 128)
   const bool group = capacity > sgl::kMaxGrid * kEdgeWaves;  // more roots than one pass of the grid
-  auto kern = group ? &k_edge_rows<1, 64, kMaxJ, 8> : &k_edge_rows<1, 64, kMaxJ, 1>;
-  if (v4 && wv <= 4 * 12) kern = group ? &k_edge_rows<4, 4, 12, 8> : &k_edge_rows<4, 4, 12, 1>;
-  else if (v4 && wv <= 8 * 12) kern = group ? &k_edge_rows<4, 8, 12, 8> : &k_edge_rows<4, 8, 12, 1>;
-  else if (v4) kern = group ? &k_edge_rows<4, 16, 8, 8> : &k_edge_rows<4, 16, 8, 1>;
+  auto kern = group ? &k_edge_rows<1, 64, kMaxJ, kEdgeGroup> : &k_edge_rows<1, 64, kMaxJ, 1>;
+  if (v4 && wv <= 4 * 12) kern = group ? &k_edge_rows<4, 4, 12, kEdgeGroup> : &k_edge_rows<4, 4, 12, 1>;
+  else if (v4 && wv <= 8 * 12) kern = group ? &k_edge_rows<4, 8, 12, kEdgeGroup> : &k_edge_rows<4, 8, 12, 1>;
+  else if (v4) kern = group ? &k_edge_rows<4, 16, 8, kEdgeGroup> : &k_edge_rows<4, 16, 8, 1>;
   sgl::launch(kern, dim3(grid), dim3(kEdgeBlock), 0, stream, d, capacity, num_roots, memory, efeat, cnt, nbr, eid, X);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

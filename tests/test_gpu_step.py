@@ -225,7 +225,7 @@ def test_edge_rows_match_gather(gpu, D, F, T, misaligned, B):
     """The edge-row gather in each of its layouts (4, 8 or 16 lanes per row
     with 16-byte vectors; a float per lane when a width is not a multiple of
     four or the edge features are not 16-byte aligned), one root per wave
-    (capacity 1400) and eight roots' rows as one list (capacity 10000): every
+    (capacity 1400) and several roots' rows as one list (capacity 10000): every
     live row equals its neighbour's memory row and its edge's features,
     padding rows stay untouched."""
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
