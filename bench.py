@@ -176,7 +176,8 @@ def sampler_cpu_baseline(g_np, nodes_np, qt_np) -> dict:
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import numpy as np
     cores = host_cores()
-    nq = min(1_000_000, len(nodes_np))
+    nq = len(nodes_np)
+    nq1 = min(500_000, nq)
     try:
         import sampler_oracle as so
         so.set_threads(cores)
@@ -185,9 +186,17 @@ def sampler_cpu_baseline(g_np, nodes_np, qt_np) -> dict:
         t0 = time.perf_counter()
         so.sample_layer(og, nodes_np[:nq], qt_np[:nq], 10)
         dt = time.perf_counter() - t0
+        # one thread: the reference's own setting on one GPU (workers = 1)
+        so.set_threads(1)
+        t0 = time.perf_counter()
+        so.sample_layer(og, nodes_np[:nq1], qt_np[:nq1], 10)
+        dt1 = time.perf_counter() - t0
+        so.set_threads(cores)
         return {"value": nq / dt / 1e6, "unit": "Mqueries/s", "cores": cores, "kind": "port",
-                "sample": f"1-hop k=10 recent over the first {nq} config-3 queries (C oracle, OpenMP)",
-                "cpu_model": cpu_model()}
+                "sample": f"1-hop k=10 recent over the {nq} config-3 queries (C oracle, OpenMP)",
+                "cpu_model": cpu_model(),
+                "one_thread": {"value": nq1 / dt1 / 1e6, "cores": 1,
+                               "sample": f"the first {nq1} queries, 1 thread"}}
     except Exception as e:  # reported, never required
         return {"value": None, "unit": "Mqueries/s", "cores": cores, "kind": "port", "sample": f"failed: {e}"}
 
@@ -216,7 +225,7 @@ def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> f
 
 # HBM bytes per launch of k_memory_commit + k_edge_rows at B = 1,048,576 (rocprofv3 FETCH_SIZE x 2.000 +
 # WRITE_SIZE x 1.000, mean over four batches: profiles/gather_scatter_cfg5_B1M.md)
-GS_TRAFFIC_1M = 133_464_064
+GS_TRAFFIC_1M = 133_542_912
 
 
 def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
@@ -598,7 +607,8 @@ def tgn_cpu_baseline(wl: dict, stream, rt) -> dict:
     import numpy as np
     import torch
     cores = host_cores()
-    nsteps = 200 if wl["B"] <= 1000 else 20
+    nsteps = 2000 if wl["B"] <= 1000 else 100   # ~10 s of host work at config 4
+    nsteps1 = 200 if wl["B"] <= 1000 else 10    # the one-thread run
     try:
         import ctdg_oracle as co
         import sampler_oracle as so
@@ -626,10 +636,25 @@ def tgn_cpu_baseline(wl: dict, stream, rt) -> dict:
             co.train_step(model, updater, opt, mem, fn, b.src, b.dst, b.ts, b.edge_feat, neg, ds.edge_feat)
             n += b.size
         dt = time.perf_counter() - t0
+        # one thread (the reference's own setting on one GPU), the next batches
+        torch.set_num_threads(1)
+        so.set_threads(1)
+        t0 = time.perf_counter()
+        n1 = 0
+        for _ in range(nsteps1):
+            b = next(it)
+            neg = co.negative_sample(pool, b.dst, gen)
+            co.train_step(model, updater, opt, mem, fn, b.src, b.dst, b.ts, b.edge_feat, neg, ds.edge_feat)
+            n1 += b.size
+        dt1 = time.perf_counter() - t0
+        torch.set_num_threads(cores)
+        so.set_threads(cores)
         return {"value": n / dt, "unit": "events/s", "cores": cores, "kind": "port",
                 "sample": f"{nsteps} training steps (batches 2..{nsteps + 1} of the epoch, B={wl['B']}) of the "
                           f"torch-CPU oracle step incl. the C oracle sampler; {dt:.1f}s",
-                "cpu_model": cpu_model()}
+                "cpu_model": cpu_model(),
+                "one_thread": {"value": n1 / dt1, "cores": 1,
+                               "sample": f"the next {nsteps1} steps, 1 thread; {dt1:.1f}s"}}
     except Exception as e:  # reported, never required
         return {"value": None, "unit": "events/s", "cores": cores, "kind": "port", "sample": f"failed: {e!r}"}
 
