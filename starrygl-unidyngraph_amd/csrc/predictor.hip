@@ -57,7 +57,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     const float *__restrict__ b_d, const float *__restrict__ w_o, const float *__restrict__ b_o,
     float *__restrict__ pos_out, float *__restrict__ neg_out, float *__restrict__ loss,
     long long *__restrict__ acc_src, long long *__restrict__ acc_dst, float *__restrict__ g_wo,
-    float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done) {
+    float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done, int agg) {
   extern __shared__ __align__(16) float lds[];
   const int ld = sgl::lds_ld(D);
   long long *Nul = reinterpret_cast<long long *>(lds);  // [D] dL/dh_n of the tile's non-root negatives
@@ -68,8 +68,14 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   float *Hd = Hs + kRows * ld;   // h_d -> a_p
   float *Hn = Hd + kRows * ld;   // h_n -> a_n
   float *Wo = Hn + kRows * ld;   // [D] out_fc weight
+  // with agg: per-root sums of the tile's hidden-layer gradients (fixed
+  // point) before the global atomics, rows indexed by the root's first entry
+  // in the src list (16) and the dst list (32: (i, dst), (i, neg) of event i)
+  long long *Gs = reinterpret_cast<long long *>(Wo + ((D + 3) & ~3));
+  long long *Gd = Gs + kRows * D;
   __shared__ float s_gp[kRows], s_gn[kRows], s_sp[kRows];
   __shared__ int s_idx[3][kRows];
+  __shared__ int s_lead[3 * kRows];  // leader entry of src entry i, dst entries 2i / 2i+1
   __shared__ int s_last;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -85,7 +91,28 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     Nul[j] = 0;
     Wo[j] = w_o[j];
   }
+  if (agg && train)
+    for (int k = tid; k < 3 * kRows * D; k += kBlock) Gs[k] = 0;
   __syncthreads();
+  if (agg && train && tid < 3 * kRows) {
+    // the first entry of the same list with the same root (-1: no root)
+    if (tid < kRows) {
+      const int a = s_idx[0][tid];
+      int l = -1;
+      if (a >= 0)
+        for (int t = tid; t >= 0; --t)
+          if (s_idx[0][t] == a) l = t;
+      s_lead[tid] = l;
+    } else {
+      const int e = tid - kRows;
+      const int r = s_idx[1 + (e & 1)][e >> 1];
+      int l = -1;
+      if (r >= 0)
+        for (int t = e; t >= 0; --t)
+          if (s_idx[1 + (t & 1)][t >> 1] == r) l = t;
+      s_lead[tid] = l;
+    }
+  }
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
@@ -178,12 +205,36 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * Wo[j] : 0.f;
       const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
       const long long fp = sgl::to_fixed(ghp), fn = sgl::to_fixed(ghn);
+      if (agg) {  // LDS atomics into the roots' leader rows
+        auto add = [](long long *q, long long v) {
+          atomicAdd(reinterpret_cast<unsigned long long *>(q), static_cast<unsigned long long>(v));
+        };
+        if (a >= 0) add(&Gs[s_lead[i] * D + j], fp + fn);
+        if (b >= 0) add(&Gd[s_lead[kRows + 2 * i] * D + j], fp);
+        if (c >= 0) add(&Gd[s_lead[kRows + 2 * i + 1] * D + j], fn);
+        else if (fn != 0) add(&Nul[j], fn);
+        continue;
+      }
       if (a >= 0) sgl::atomic_add_fixed(&acc_src[size_t(a) * D + j], fp + fn);
       if (b >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(b) * D + j], fp);
       if (c >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(c) * D + j], fn);
       else if (fn != 0) atomicAdd(reinterpret_cast<unsigned long long *>(&Nul[j]), static_cast<unsigned long long>(fn));
     }
     __syncthreads();
+    if (agg) {  // one global atomic per (root in the tile, column)
+      for (int k = tid; k < 3 * kRows * D; k += kBlock) {
+        const int e = k / D, j = k - e * D;
+        if (s_lead[e] != (e < kRows ? e : e - kRows)) continue;  // not a leader, or no root
+        const long long v = Gs[k];
+        if (v == 0) continue;
+        if (e < kRows) {
+          sgl::atomic_add_fixed(&acc_src[size_t(s_idx[0][e]) * D + j], v);
+        } else {
+          const int t = e - kRows;
+          sgl::atomic_add_fixed(&acc_dst[size_t(s_idx[1 + (t & 1)][t >> 1]) * D + j], v);
+        }
+      }
+    }
     for (int j = tid; j < D; j += kBlock)
       if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_dst[size_t(U) * D + j], Nul[j]);
   }
@@ -227,13 +278,17 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
-  const size_t lds = sizeof(float) * (size_t(kRows) * 6 * sgl::lds_ld(D) + 2 * ((D + 1) & ~1) + D);
-  SGL_REQUIRE(lds <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds);
+  const size_t lds0 = sizeof(float) * (size_t(kRows) * 6 * sgl::lds_ld(D) + 2 * ((D + 1) & ~1) + ((D + 3) & ~3));
+  SGL_REQUIRE(lds0 <= 160 * 1024, "predictor: D=%d needs %zu bytes of LDS", D, lds0);
+  // the per-root gradient sums in LDS when they fit (otherwise one global atomic per event)
+  const size_t lds_agg = lds0 + sizeof(long long) * 3 * kRows * size_t(D);
+  const int agg = train && lds_agg <= 160 * 1024 ? 1 : 0;
+  const size_t lds = agg ? lds_agg : lds0;
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
   sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
               num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
-              reinterpret_cast<long long *>(acc_out), done);
+              reinterpret_cast<long long *>(acc_out), done, agg);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
