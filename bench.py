@@ -124,12 +124,17 @@ def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -
     wall = time.perf_counter() - w0
     avg_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     alg = sampler_bytes(deg[nodes], head.cnt)
+    traffic = HBM_TRAFFIC.get(("cfg3", "recent_sample"))
+    # diagnostics: the probe-free (compulsory) bytes, and the counter-measured bytes over the same time
+    compulsory = float((12 + 16 + 28 * head.cnt.double() + 4).sum().item())
     out = {"value": nq * steps / wall / 1e6, "unit": "Mqueries/s", "ms_per_pass": wall * 1e3 / steps,
            "workload": "cfg3: 1e7 nodes, 1e8 edges, 4e6 degree-weighted queries, recent k=10, 1 hop",
            "roofline": {"bound": "hbm", "kernel": "k_recent_padded", "kernel_avg_ms": avg_ms,
                         "alg_bytes_per_launch": alg, "achieved": alg / (avg_ms * 1e-3) / 1e9,
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": alg / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                        "traffic": HBM_TRAFFIC.get(("cfg3", "recent_sample"))}}
+                        "traffic": traffic,
+                        "compulsory_bytes_per_launch": compulsory,
+                        "traffic_rate_GBps": traffic / (avg_ms * 1e-3) / 1e9 if traffic else None}}
     del head
     if cases:
         res = {}
