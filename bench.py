@@ -493,6 +493,10 @@ def run_tgn(args, wl: dict) -> dict:
     rt.use_plans = not args.no_plans
     ep = Epochs(rt, wl["B"])
     dev = torch.device("cuda:0")
+    if args.epoch:  # the reference's definition: one warm-up epoch, then one timed epoch of train batches
+        n_train = -(-int(rt.dataset.split_event_ids("train").numel()) // wl["B"])
+        args.steps = args.warmup = n_train
+        log(f"epoch mode: {n_train} train batches per epoch")
     for _ in range(args.warmup):
         out = rt.train_step(ep.next())
     torch.cuda.synchronize()
@@ -679,6 +683,9 @@ def main() -> None:
                              "conv_forward", "conv_backward"])
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--epoch", action="store_true",
+                    help="TGN workloads: one warm-up epoch, then time one epoch of train batches (overrides "
+                         "--steps / --warmup)")
     ap.add_argument("--memory-gemm-dtype", default="fp32", choices=["fp32", "bf16"],
                     help="the memory updater's GEMMs (TGN workloads): fp32 MFMA, or bf16 MFMA with fp32 "
                          "accumulation (the mixed-precision setting; dtype reads fp32+bf16)")
@@ -722,6 +729,7 @@ def main() -> None:
         return
     wl = dict(WORKLOADS[args.workload], gemm=args.memory_gemm_dtype)
     r = run_tgn(args, wl)
+    base.update(steps=args.steps, warmup=args.warmup)  # --epoch sets them from the split
     line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"],
                 dtype="fp32" if args.memory_gemm_dtype == "fp32" else "fp32 (GRU GEMMs bf16)",
                 config={"workload": f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
