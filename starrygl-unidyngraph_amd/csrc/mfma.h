@@ -20,6 +20,8 @@
 // matrices are < 4 GiB, so element offsets are 32-bit.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -328,7 +330,10 @@ __device__ __forceinline__ bf16x8 bf16x8_from_f32(const f32x4 &x0, const f32x4 &
   return r;
 }
 
-__device__ __forceinline__ f32x4 mfma_block16_bf16(const float *__restrict__ A, int lda,
+// AT = float: A is fp32 in LDS, rounded as it is read; AT = uint16_t: A is
+// already bf16 in LDS (rows 16-byte aligned when lda % 8 == 0).
+template <typename AT>
+__device__ __forceinline__ f32x4 mfma_block16_bf16(const AT *__restrict__ A, int lda,
                                                    const uint16_t *__restrict__ W, int ldw, int n0, int kd,
                                                    int n_total) {
   const int lane = threadIdx.x & 63;
@@ -337,12 +342,12 @@ __device__ __forceinline__ f32x4 mfma_block16_bf16(const float *__restrict__ A, 
   const int n = n0 + i;
   const bool nok = n < n_total;
   const uint16_t *wrow = W + size_t(nok ? n : 0) * size_t(ldw);
-  const float *arow = A + i * lda;
+  const AT *arow = A + i * lda;
   // 16-byte weight loads when row starts and k offsets are multiples of 8
   // elements, else two 8-byte loads when they are multiples of 4 (D = 172)
   const bool wvec = (ldw & 7) == 0 && (kd & 7) == 0 && aligned16(W);
   const bool wvec4 = !wvec && (ldw & 3) == 0 && (kd & 3) == 0 && (reinterpret_cast<uintptr_t>(W) & 7u) == 0;
-  const bool avec = (lda & 3) == 0 && aligned16(A);
+  const bool avec = std::is_same_v<AT, float> ? (lda & 3) == 0 && aligned16(A) : (lda & 7) == 0 && aligned16(A);
   constexpr int kU = 8;  // k steps of 32 whose weights are loaded together
   f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   for (int kb = 0; kb < kd; kb += 32 * kU) {
@@ -370,11 +375,22 @@ __device__ __forceinline__ f32x4 mfma_block16_bf16(const float *__restrict__ A, 
       const int k = kb + 32 * u + 8 * q;
       if (kb + 32 * u >= kd) break;  // uniform
       bf16x8 a;
-      if (avec && k + 8 <= kd) {
-        a = bf16x8_from_f32(*reinterpret_cast<const f32x4 *>(arow + k), *reinterpret_cast<const f32x4 *>(arow + k + 4));
-      } else {
+      if constexpr (std::is_same_v<AT, float>) {
+        if (avec && k + 8 <= kd) {
+          a = bf16x8_from_f32(*reinterpret_cast<const f32x4 *>(arow + k),
+                              *reinterpret_cast<const f32x4 *>(arow + k + 4));
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(k + j < kd ? arow[min(k + j, kd - 1)] : 0.f);
+          for (int j = 0; j < 8; ++j) a[j] = static_cast<__bf16>(k + j < kd ? arow[min(k + j, kd - 1)] : 0.f);
+        }
+      } else {
+        if (avec && k + 8 <= kd) {
+          a = *reinterpret_cast<const bf16x8 *>(arow + k);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            a[j] = k + j < kd ? __builtin_bit_cast(__bf16, arow[min(k + j, kd - 1)]) : static_cast<__bf16>(0.f);
+        }
       }
       if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc1, 0, 0, 0);
       else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc0, 0, 0, 0);
@@ -383,9 +399,11 @@ __device__ __forceinline__ f32x4 mfma_block16_bf16(const float *__restrict__ A, 
   return acc0 + acc1;
 }
 
-// The bf16 counterpart of GemmJob / tile_gemm16_jobs (kNT weights only).
+// The bf16 counterpart of GemmJob / tile_gemm16_jobs (kNT weights only); A
+// fp32 (rounded on read) or bf16 (AT = uint16_t).
+template <typename AT>
 struct GemmJobBf16 {
-  const float *A;
+  const AT *A;
   int lda;
   const uint16_t *W;
   int ldw;
@@ -395,15 +413,15 @@ struct GemmJobBf16 {
   int kd, n_total;
 };
 
-template <int NJOBS>
-__device__ __forceinline__ void tile_gemm16_jobs_bf16(const GemmJobBf16 (&jobs)[NJOBS], int nwaves) {
+template <typename AT, int NJOBS>
+__device__ __forceinline__ void tile_gemm16_jobs_bf16(const GemmJobBf16<AT> (&jobs)[NJOBS], int nwaves) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   int total = 0;
 #pragma unroll
   for (int j = 0; j < NJOBS; ++j) total += (jobs[j].n_total + 15) >> 4;
   for (int blk = wave; blk < total; blk += nwaves) {
-    GemmJobBf16 jb = jobs[0];
+    GemmJobBf16<AT> jb = jobs[0];
     int nb = blk, first = 0;
 #pragma unroll
     for (int j = 0; j < NJOBS; ++j) {
@@ -417,7 +435,7 @@ __device__ __forceinline__ void tile_gemm16_jobs_bf16(const GemmJobBf16 (&jobs)[
     const int n0 = nb * 16;
     const int col = n0 + (lane & 15);
     const float bv = jb.bias != nullptr && col < jb.n_total ? jb.bias[col] : 0.f;
-    f32x4 acc = mfma_block16_bf16(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
+    f32x4 acc = mfma_block16_bf16<AT>(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
     if (col < jb.n_total) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;

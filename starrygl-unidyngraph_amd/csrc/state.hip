@@ -438,19 +438,26 @@ static_assert(kGruWaves == kTileRows, "the mailbox phase maps wave w to root w")
 // (WT = uint16_t, raw bf16 patterns: bf16 MFMA with fp32 accumulation, the
 // LDS operands rounded to bf16 as they are read); biases, gates and state
 // stay fp32.
-template <typename WT>
-__device__ __forceinline__ void gru_products(const float *A0, int lda0, const WT *W0, int ldw0, const float *b0,
-                                             float *O0, int kd0, int n0, const float *A1, int lda1, const WT *W1,
+// AT: the LDS operand type (fp32 tiles for fp32 weights, bf16 copies of the
+// tiles for bf16 weights).
+template <typename WT, typename AT>
+__device__ __forceinline__ void gru_products(const AT *A0, int lda0, const WT *W0, int ldw0, const float *b0,
+                                             float *O0, int kd0, int n0, const AT *A1, int lda1, const WT *W1,
                                              int ldw1, const float *b1, float *O1, int kd1, int n1, int ldo) {
   if constexpr (std::is_same_v<WT, float>) {
     sgl::GemmJob jobs[2] = {{A0, lda0, W0, ldw0, b0, O0, ldo, kd0, n0}, {A1, lda1, W1, ldw1, b1, O1, ldo, kd1, n1}};
     sgl::tile_gemm16_jobs<sgl::kNT>(jobs, kGruWaves);
   } else {
-    sgl::GemmJobBf16 jobs[2] = {{A0, lda0, W0, ldw0, b0, O0, ldo, kd0, n0},
-                                {A1, lda1, W1, ldw1, b1, O1, ldo, kd1, n1}};
+    sgl::GemmJobBf16<AT> jobs[2] = {{A0, lda0, W0, ldw0, b0, O0, ldo, kd0, n0},
+                                    {A1, lda1, W1, ldw1, b1, O1, ldo, kd1, n1}};
     sgl::tile_gemm16_jobs_bf16(jobs, kGruWaves);
   }
 }
+
+// Leading dimension (elements) of a bf16 LDS tile: a multiple of 8 (16-byte
+// rows) that is an odd multiple of 8, so that rows start in alternating
+// 16-byte bank groups.
+__host__ __device__ constexpr int lds_ld_bf16(int n) { return ((n + 7) & ~7) | 8; }
 
 template <typename WT>
 __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
@@ -476,6 +483,15 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
   float *ms = hs + kTileRows * ldh;
   float *gi = ms + kTileRows * ldh;
   float *gh = gi + kTileRows * ldg;
+  // bf16 weights: the products read bf16 copies of the tiles, written once
+  // per value (the mailbox rows go to LDS as bf16 only; h and memory keep
+  // their fp32 tiles for the gate combine)
+  constexpr bool kBf = !std::is_same_v<WT, float>;
+  const int lbx = lds_ld_bf16(S), lbh = lds_ld_bf16(D);
+  uint16_t *xb = reinterpret_cast<uint16_t *>(xs);
+  uint16_t *hb = reinterpret_cast<uint16_t *>(gh + kTileRows * ldg);
+  uint16_t *mb = hb + kTileRows * lbh;
+  auto to_bf = [](float v) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v)); };
   __shared__ int64_t s_root[kTileRows], s_e[2][kTileRows];
   __shared__ int32_t s_cnt[2][kTileRows];
   const int U = *num_roots;
@@ -507,8 +523,13 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     __syncthreads();
     for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
       const int i = idx / D, j = idx - i * D;
-      ms[i * ldh + j] = i < nrows ? memory[s_root[i] * D + j] : 0.f;
+      const float mv = i < nrows ? memory[s_root[i] * D + j] : 0.f;
+      ms[i * ldh + j] = mv;
       hs[i * ldh + j] = 0.f;
+      if constexpr (kBf) {
+        mb[i * lbh + j] = to_bf(mv);
+        hb[i * lbh + j] = 0;
+      }
     }
     // Mailbox messages (memory.py:218-248): the src-role message of node u is
     // [mem(u) || mem(other) || f_e] of its last src event e, the dst-role one
@@ -541,10 +562,15 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     for (int k = 0; k < K; ++k) {
       for (int idx = tid; idx < kTileRows * S; idx += kGruBlock) {
         const int i = idx / S, j = idx - (idx / S) * S;
-        xs[i * ldx + j] = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
+        const float xv = i < nrows ? mailbox[(s_root[i] * K + k) * S + j] : 0.f;
+        if constexpr (kBf) xb[i * lbx + j] = to_bf(xv);
+        else xs[i * ldx + j] = xv;
       }
       __syncthreads();
-      gru_products<WT>(xs, ldx, w_ih, S, b_ih, gi, S, G, hs, ldh, w_hh, D, b_hh, gh, D, k > 0 ? G : 0, ldg);
+      if constexpr (kBf)
+        gru_products<WT>(xb, lbx, w_ih, S, b_ih, gi, S, G, hb, lbh, w_hh, D, b_hh, gh, D, k > 0 ? G : 0, ldg);
+      else
+        gru_products<WT>(xs, ldx, w_ih, S, b_ih, gi, S, G, hs, ldh, w_hh, D, b_hh, gh, D, k > 0 ? G : 0, ldg);
       __syncthreads();
       for (int idx = tid; idx < kTileRows * D; idx += kGruBlock) {
         const int i = idx / D, j = idx - (idx / D) * D;
@@ -556,12 +582,17 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
         } else {  // W_hh h0 = 0
           ghr = b_hh[j]; ghz = b_hh[D + j]; ghn = b_hh[2 * D + j];
         }
-        hs[i * ldh + j] = gru_combine(g1[j], g1[D + j], g1[2 * D + j], ghr, ghz, ghn, hs[i * ldh + j]);
+        const float hv = gru_combine(g1[j], g1[D + j], g1[2 * D + j], ghr, ghz, ghn, hs[i * ldh + j]);
+        hs[i * ldh + j] = hv;
+        if constexpr (kBf) hb[i * lbh + j] = to_bf(hv);
       }
       __syncthreads();
     }
     // GRUCell(agg = h, memory)
-    gru_products<WT>(hs, ldh, wc_ih, D, bc_ih, gi, D, G, ms, ldh, wc_hh, D, bc_hh, gh, D, G, ldg);
+    if constexpr (kBf)
+      gru_products<WT>(hb, lbh, wc_ih, D, bc_ih, gi, D, G, mb, lbh, wc_hh, D, bc_hh, gh, D, G, ldg);
+    else
+      gru_products<WT>(hs, ldh, wc_ih, D, bc_ih, gi, D, G, ms, ldh, wc_hh, D, bc_hh, gh, D, G, ldg);
     __syncthreads();
     for (int idx = tid; idx < nrows * D; idx += kGruBlock) {
       const int i = idx / D, j = idx - (idx / D) * D;
@@ -715,7 +746,9 @@ static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, cons
                   b_hh && wc_ih && wc_hh && bc_ih && bc_hh && src && dst && ts && win_src && win_dst &&
                   cnt_src && cnt_dst && new_mem && (F == 0 || efeat),
               "memory_update: NULL array");
-  const size_t lds = sgl_memory_update_lds_bytes(D, F);
+  // the bf16 variant adds bf16 copies of the h and memory tiles (the mailbox tile's reuses the fp32 one)
+  const size_t lds = sgl_memory_update_lds_bytes(D, F) +
+                     (std::is_same_v<WT, float> ? 0 : sizeof(uint16_t) * 2 * kTileRows * size_t(lds_ld_bf16(D)));
   SGL_REQUIRE(lds <= 160 * 1024, "memory_update: D=%d F=%d needs %zu bytes of LDS (> 160 KiB)", D, F, lds);
   SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
               64 * kMaxMsgSlots);
