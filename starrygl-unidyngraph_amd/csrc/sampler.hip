@@ -28,12 +28,14 @@ constexpr int kTile = 256;      // queries per compaction tile
 constexpr int kScanBlock = 1024;
 constexpr int64_t kWaveModeMaxQueries = 1 << 15;  // below: one wavefront per query
 
-template <typename NodeT>
+// TsT: the CSR's timestamps as stored, int64 or (when every timestamp fits)
+// int32, compared with the int64 query times exactly.
+template <typename NodeT, typename TsT>
 __global__ __launch_bounds__(kBlock) void k_recent_padded(
     int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
     const int64_t *__restrict__ q_ts, const int32_t *__restrict__ q_valid_cnt, int q_stride,
     const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
-    const int32_t *__restrict__ eid, const int64_t *__restrict__ ts,
+    const int32_t *__restrict__ eid, const TsT *__restrict__ ts,
     int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
     int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
     float *__restrict__ out_dt, int64_t *__restrict__ out_ts,
@@ -59,7 +61,7 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
         while (len > 0) {  // std::lower_bound
           const int64_t half = len >> 1;
           const int64_t mid = first + half;
-          if (ts[mid] < t) {
+          if (int64_t(ts[mid]) < t) {
             first = mid + 1;
             len -= half + 1;
           } else {
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
     if (j < cq) {
       const int64_t src = bq + j;
       const int64_t o = obase + s;
-      const int64_t tv = ts[src];
+      const int64_t tv = int64_t(ts[src]);
       out_nbr[o] = nbr[src];
       out_eid[o] = eid[src];
       out_dt[o] = float(tq - tv);  // int64 -> f32, round to nearest even
@@ -106,12 +108,12 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
 // of 17 dependent probes. The window is then copied by the wave's lanes.
 constexpr int kWaveQueriesPerBlock = kBlock / sgl::kWave;
 
-template <typename NodeT>
+template <typename NodeT, typename TsT>
 __global__ __launch_bounds__(kBlock) void k_recent_wave(
     int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
     const int64_t *__restrict__ q_ts, const int32_t *__restrict__ q_valid_cnt, int q_stride,
     const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
-    const int32_t *__restrict__ eid, const int64_t *__restrict__ ts,
+    const int32_t *__restrict__ eid, const TsT *__restrict__ ts,
     int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
     int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
     float *__restrict__ out_dt, int64_t *__restrict__ out_ts,
@@ -145,7 +147,7 @@ __global__ __launch_bounds__(kBlock) void k_recent_wave(
             lh = half;
           }
         }
-        const bool below = h < sgl::kWave && lh > 0 && ts[fh + (lh >> 1)] < t;
+        const bool below = h < sgl::kWave && lh > 0 && int64_t(ts[fh + (lh >> 1)]) < t;
         const unsigned long long res = __ballot(below);
         int node = 1;
 #pragma unroll
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(kBlock) void k_recent_wave(
   const int64_t obase = i * k;
   for (int j = lane; j < c; j += sgl::kWave) {
     const int64_t src = b + j;
-    const int64_t tv = ts[src];
+    const int64_t tv = int64_t(ts[src]);
     out_nbr[obase + j] = nbr[src];
     out_eid[obase + j] = eid[src];
     out_dt[obase + j] = float(t - tv);  // int64 -> f32, round to nearest even
@@ -256,13 +258,12 @@ __global__ void k_write_zero_ptr(int64_t *out_ptr) { out_ptr[0] = 0; }
 
 }  // namespace
 
-extern "C" int sgl_recent_sample(
-    const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
-    const int64_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
-    const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
-    int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
-    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
-    hipStream_t stream) {
+template <typename TsT>
+static int recent_sample(const int64_t *indptr, const int32_t *nbr, const int32_t *eid, const TsT *ts,
+                         int64_t num_nodes, const void *q_node, int q_node_is_i64, const int64_t *q_ts,
+                         int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
+                         int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr, int32_t *out_eid,
+                         float *out_dt, int64_t *out_ts, int32_t *err_flag, hipStream_t stream) {
   SGL_REQUIRE(num_queries >= 0, "recent: num_queries < 0");
   SGL_REQUIRE(fanout >= 0 && fanout <= 4096, "recent: fanout %d outside [0, 4096]", fanout);
   SGL_REQUIRE(num_nodes >= 0, "recent: num_nodes < 0");
@@ -275,27 +276,51 @@ extern "C" int sgl_recent_sample(
   if (num_queries <= kWaveModeMaxQueries) {  // latency: one wavefront per query
     const unsigned wblocks = unsigned((num_queries + kWaveQueriesPerBlock - 1) / kWaveQueriesPerBlock);
     if (q_node_is_i64)
-      sgl::launch(&k_recent_wave<int64_t>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries, num_queries_dev,
-                  static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts, num_nodes,
-                  fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+      sgl::launch(&k_recent_wave<int64_t, TsT>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries,
+                  num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr,
+                  eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
     else
-      sgl::launch(&k_recent_wave<int32_t>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries, num_queries_dev,
-                  static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts, num_nodes,
-                  fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+      sgl::launch(&k_recent_wave<int32_t, TsT>, dim3(wblocks), dim3(kBlock), 0, stream, num_queries,
+                  num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr,
+                  eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
   if (q_node_is_i64) {
-    k_recent_padded<int64_t><<<unsigned(blocks), kBlock, 0, stream>>>(
-        num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
-        num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+    k_recent_padded<int64_t, TsT><<<unsigned(blocks), kBlock, 0, stream>>>(
+        num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
+        nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   } else {
-    k_recent_padded<int32_t><<<unsigned(blocks), kBlock, 0, stream>>>(
-        num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr, nbr, eid, ts,
-        num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+    k_recent_padded<int32_t, TsT><<<unsigned(blocks), kBlock, 0, stream>>>(
+        num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
+        nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   }
   SGL_CHECK_LAUNCH();
   return SGL_OK;
+}
+
+extern "C" int sgl_recent_sample(
+    const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
+    const int64_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
+    const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
+    int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
+    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
+    hipStream_t stream) {
+  return recent_sample<int64_t>(indptr, nbr, eid, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
+                                num_queries_dev, q_valid_cnt, q_stride, fanout, out_cnt, out_nbr, out_eid, out_dt,
+                                out_ts, err_flag, stream);
+}
+
+extern "C" int sgl_recent_sample_ts32(
+    const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
+    const int32_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
+    const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
+    int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
+    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
+    hipStream_t stream) {
+  return recent_sample<int32_t>(indptr, nbr, eid, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
+                                num_queries_dev, q_valid_cnt, q_stride, fanout, out_cnt, out_nbr, out_eid, out_dt,
+                                out_ts, err_flag, stream);
 }
 
 extern "C" size_t sgl_compact_workspace_bytes(int64_t num_queries) {

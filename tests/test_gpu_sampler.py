@@ -208,3 +208,31 @@ def _subset_oracle(g, nodes, qt, k):
                         nbr=g.nbr[idx].long().cpu().numpy(), eid=g.eid[idx].long().cpu().numpy(),
                         ts=g.ts[idx].cpu().numpy())
     return so.sample_layer(sub, np.searchsorted(uniq, nodes), qt, k)
+
+
+@pytest.mark.parametrize("nq", [2000, 100_000])
+def test_int32_timestamps_match_int64(gpu, nq):
+    """The narrowed-timestamp sampler (sgl_recent_sample_ts32, chosen when every
+    timestamp fits in int32) gives bit-identical windows to the int64 one, in
+    both kernel modes (one wave per query up to 32768 queries, one lane per
+    query above), with negative times and query times beyond int32's range;
+    a graph whose timestamps do not fit keeps the int64 path."""
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    rng = np.random.default_rng(nq)
+    N, E = 3000, 80_000
+    row, col = rng.integers(0, N, E), rng.integers(0, N, E)
+    ts = np.sort(rng.integers(-2 ** 31, 2 ** 31, E))
+    g = build_tcsr(N, torch.as_tensor(row), torch.as_tensor(col), None, torch.as_tensor(ts))
+    narrow, wide = RecentSampler(g), RecentSampler(g, narrow_ts=False)
+    assert narrow.ts32 is not None and wide.ts32 is None
+    nodes = torch.as_tensor(rng.integers(0, N, nq)).cuda()
+    qt = torch.as_tensor(rng.integers(-2 ** 32, 2 ** 32, nq)).cuda()
+    a = narrow.sample(nodes, qt, 10, want_ts=True)
+    b = wide.sample(nodes, qt, 10, want_ts=True)
+    assert torch.equal(a.cnt, b.cnt)
+    assert int(a.cnt.sum().item()) > 0
+    live = (torch.arange(10, device=a.cnt.device)[None, :] < a.cnt.long()[:, None]).reshape(-1)
+    for f in ("nbr", "eid", "dt", "ts"):
+        assert torch.equal(getattr(a, f)[live], getattr(b, f)[live]), f
+    g2 = build_tcsr(4, torch.tensor([0, 1]), torch.tensor([1, 1]), None, torch.tensor([1, 2 ** 31]))
+    assert RecentSampler(g2).ts32 is None
