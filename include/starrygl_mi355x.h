@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 8
+#define SGL_ABI_VERSION 9
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -95,20 +95,21 @@ int sgl_recent_sample(const int64_t *indptr, const int32_t *nbr,
                       int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
                       int32_t *out_eid, float *out_dt, int64_t *out_ts,
                       int32_t *err_flag, hipStream_t stream);
-/* The same with the CSR's timestamps as int32: a narrowed copy of ts_out of
- * sgl_tcsr_build that the caller makes when every timestamp fits in int32.
- * Each entry is compared with the int64 query time exactly as its int64
- * value would be, so the results are identical; a search probe and the
- * window's times read half the bytes (32 timestamps per 128-byte line). */
-int sgl_recent_sample_ts32(const int64_t *indptr, const int32_t *nbr,
-                           const int32_t *eid, const int32_t *ts, int64_t num_nodes,
-                           const void *q_node, int q_node_is_i64,
-                           const int64_t *q_ts, int64_t num_queries,
-                           const int64_t *num_queries_dev,
-                           const int32_t *q_valid_cnt, int32_t q_stride,
-                           int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
-                           int32_t *out_eid, float *out_dt, int64_t *out_ts,
-                           int32_t *err_flag, hipStream_t stream);
+/* The same over a packed copy of the CSR that the caller makes when every
+ * timestamp fits in int32: nbr_eid holds (nbr, eid) pairs ([num_edges][2],
+ * 8-byte aligned) and ts the int32 timestamps. Each entry is compared with the
+ * int64 query time exactly as its int64 value would be, so the results are
+ * identical; a search probe reads half the bytes (32 timestamps per 128-byte
+ * line) and a window's ids one contiguous run. */
+int sgl_recent_sample_packed(const int64_t *indptr, const int32_t *nbr_eid,
+                             const int32_t *ts, int64_t num_nodes,
+                             const void *q_node, int q_node_is_i64,
+                             const int64_t *q_ts, int64_t num_queries,
+                             const int64_t *num_queries_dev,
+                             const int32_t *q_valid_cnt, int32_t q_stride,
+                             int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
+                             int32_t *out_eid, float *out_dt, int64_t *out_ts,
+                             int32_t *err_flag, hipStream_t stream);
 
 /* Padded -> the reference's concatenated layout (TemporalGraphBlock order:
  * root order, each window oldest->newest; output.h:4-30). out_ptr[Q+1] is the

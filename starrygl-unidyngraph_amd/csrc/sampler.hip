@@ -18,6 +18,7 @@
 // reference's concatenated layout (a block scan of the counts, tile offsets
 // scanned by one workgroup, then a copy).
 #include <climits>
+#include <type_traits>
 
 #include "common.h"
 
@@ -29,7 +30,8 @@ constexpr int kScanBlock = 1024;
 constexpr int64_t kWaveModeMaxQueries = 1 << 15;  // below: one wavefront per query
 
 // TsT: the CSR's timestamps as stored, int64 or (when every timestamp fits)
-// int32, compared with the int64 query times exactly.
+// int32, compared with the int64 query times exactly. With int32 times the
+// ids come interleaved: nbr points at (nbr, eid) pairs and eid is unused.
 template <typename NodeT, typename TsT>
 __global__ __launch_bounds__(kBlock) void k_recent_padded(
     int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
@@ -90,8 +92,14 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
       const int64_t src = bq + j;
       const int64_t o = obase + s;
       const int64_t tv = int64_t(ts[src]);
-      out_nbr[o] = nbr[src];
-      out_eid[o] = eid[src];
+      if constexpr (std::is_same_v<TsT, int32_t>) {  // ids interleaved (nbr, eid) with int32 times
+        const int2 v = reinterpret_cast<const int2 *>(nbr)[src];
+        out_nbr[o] = v.x;
+        out_eid[o] = v.y;
+      } else {
+        out_nbr[o] = nbr[src];
+        out_eid[o] = eid[src];
+      }
       out_dt[o] = float(tq - tv);  // int64 -> f32, round to nearest even
       if (out_ts != nullptr) out_ts[o] = tv;
     }
@@ -176,8 +184,14 @@ __global__ __launch_bounds__(kBlock) void k_recent_wave(
   for (int j = lane; j < c; j += sgl::kWave) {
     const int64_t src = b + j;
     const int64_t tv = int64_t(ts[src]);
-    out_nbr[obase + j] = nbr[src];
-    out_eid[obase + j] = eid[src];
+    if constexpr (std::is_same_v<TsT, int32_t>) {
+      const int2 v = reinterpret_cast<const int2 *>(nbr)[src];
+      out_nbr[obase + j] = v.x;
+      out_eid[obase + j] = v.y;
+    } else {
+      out_nbr[obase + j] = nbr[src];
+      out_eid[obase + j] = eid[src];
+    }
     out_dt[obase + j] = float(t - tv);  // int64 -> f32, round to nearest even
     if (out_ts != nullptr) out_ts[obase + j] = tv;
   }
@@ -269,7 +283,10 @@ static int recent_sample(const int64_t *indptr, const int32_t *nbr, const int32_
   SGL_REQUIRE(num_nodes >= 0, "recent: num_nodes < 0");
   if (num_queries == 0) return SGL_OK;
   SGL_REQUIRE(indptr && q_node && q_ts && out_cnt, "recent: NULL graph, query or count array");
-  SGL_REQUIRE(fanout == 0 || (nbr && eid && ts && out_nbr && out_eid && out_dt), "recent: NULL output array");
+  constexpr bool kPacked = std::is_same_v<TsT, int32_t>;
+  SGL_REQUIRE(fanout == 0 || (nbr && (kPacked || eid) && ts && out_nbr && out_eid && out_dt),
+              "recent: NULL graph or output array");
+  SGL_REQUIRE(!kPacked || (reinterpret_cast<uintptr_t>(nbr) & 7u) == 0, "recent: nbr_eid not 8-byte aligned");
   SGL_REQUIRE(q_valid_cnt == nullptr || q_stride > 0, "recent: q_stride must be > 0 with q_valid_cnt");
   const int64_t blocks = (num_queries + kBlock - 1) / kBlock;
   SGL_REQUIRE(blocks < INT_MAX, "recent: too many queries");
@@ -311,14 +328,12 @@ extern "C" int sgl_recent_sample(
                                 out_ts, err_flag, stream);
 }
 
-extern "C" int sgl_recent_sample_ts32(
-    const int64_t *indptr, const int32_t *nbr, const int32_t *eid,
-    const int32_t *ts, int64_t num_nodes, const void *q_node, int q_node_is_i64,
-    const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
-    int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
-    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
-    hipStream_t stream) {
-  return recent_sample<int32_t>(indptr, nbr, eid, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
+extern "C" int sgl_recent_sample_packed(
+    const int64_t *indptr, const int32_t *nbr_eid, const int32_t *ts, int64_t num_nodes, const void *q_node,
+    int q_node_is_i64, const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev,
+    const int32_t *q_valid_cnt, int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
+    int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag, hipStream_t stream) {
+  return recent_sample<int32_t>(indptr, nbr_eid, nullptr, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
                                 num_queries_dev, q_valid_cnt, q_stride, fanout, out_cnt, out_nbr, out_eid, out_dt,
                                 out_ts, err_flag, stream);
 }

@@ -117,19 +117,22 @@ def build_tcsr(num_nodes: int, row, col, eid=None, ts=None, device=None, check: 
 
 class RecentSampler:
     """Recent-k sampler bound to one DeviceTCSR. When every timestamp of the
-    graph fits in int32 (checked once here), the sampler reads an int32 copy
-    (sgl_recent_sample_ts32: identical results, half the bytes per probe and
-    window time); ``narrow_ts=False`` keeps the int64 timestamps."""
+    graph fits in int32 (checked once here), the sampler reads a packed copy:
+    int32 timestamps and interleaved (nbr, eid) pairs (sgl_recent_sample_packed:
+    identical results, half the bytes per probe, one run of ids per window);
+    ``narrow_ts=False`` keeps the int64 arrays."""
 
     def __init__(self, graph: DeviceTCSR, narrow_ts: bool = True):
         self.g = graph
         self.dev = graph.device
         self.err = _capi.ErrorFlag(self.dev)
         self.ts32: torch.Tensor | None = None
+        self.ids: torch.Tensor | None = None
         if narrow_ts and graph.num_edges > 0:
             lo, hi = int(graph.ts.min().item()), int(graph.ts.max().item())
             if -2 ** 31 <= lo and hi < 2 ** 31:
                 self.ts32 = graph.ts.to(torch.int32)
+                self.ids = torch.stack([graph.nbr, graph.eid], dim=1).contiguous()
 
     def sample(self, nodes: torch.Tensor, q_ts: torch.Tensor, fanout: int, want_ts: bool = False,
                valid_cnt: torch.Tensor | None = None, stride: int = 0,
@@ -165,10 +168,14 @@ class RecentSampler:
                 ts=torch.empty(cap, dtype=torch.int64, device=dev) if want_ts else None,
                 q_ts=q_ts, fanout=fanout)
         g = self.g
-        fn, ts = ("sgl_recent_sample_ts32", self.ts32) if self.ts32 is not None else ("sgl_recent_sample", g.ts)
+        if self.ts32 is not None:
+            fn, graph_args = "sgl_recent_sample_packed", (_capi.ptr(g.indptr), _capi.ptr(self.ids),
+                                                          _capi.ptr(self.ts32))
+        else:
+            fn, graph_args = "sgl_recent_sample", (_capi.ptr(g.indptr), _capi.ptr(g.nbr), _capi.ptr(g.eid),
+                                                   _capi.ptr(g.ts))
         with torch.cuda.device(dev):
-            _capi.check(_capi.call(fn,
-                _capi.ptr(g.indptr), _capi.ptr(g.nbr), _capi.ptr(g.eid), _capi.ptr(ts), g.num_nodes,
+            _capi.check(_capi.call(fn, *graph_args, g.num_nodes,
                 _capi.ptr(nodes), 1 if nodes.dtype == torch.int64 else 0, _capi.ptr(q_ts), nq,
                 _capi.ptr(num_live), _capi.ptr(valid_cnt), int(stride), fanout,
                 _capi.ptr(hop.cnt), _capi.ptr(hop.nbr), _capi.ptr(hop.eid), _capi.ptr(hop.dt),

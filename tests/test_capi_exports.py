@@ -136,7 +136,7 @@ def test_plan_recording_and_packing():
     L = _capi.lib()
     plannable = ["sgl_batch_prepare", "sgl_recent_sample", "sgl_memory_update", "sgl_memory_commit",
                  "sgl_conv_forward", "sgl_predictor", "sgl_conv_backward", "sgl_grad_adam", "sgl_adam_coef",
-                 "sgl_edge_rows", "sgl_memory_update_bf16", "sgl_recent_sample_ts32"]
+                 "sgl_edge_rows", "sgl_memory_update_bf16", "sgl_recent_sample_packed"]
     for name in plannable:
         n = ctypes.c_int32(-1)
         assert L.sgl_plan_op_kind(name.encode(), ctypes.byref(n)) >= 0, name

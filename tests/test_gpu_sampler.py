@@ -212,8 +212,9 @@ def _subset_oracle(g, nodes, qt, k):
 
 @pytest.mark.parametrize("nq", [2000, 100_000])
 def test_int32_timestamps_match_int64(gpu, nq):
-    """The narrowed-timestamp sampler (sgl_recent_sample_ts32, chosen when every
-    timestamp fits in int32) gives bit-identical windows to the int64 one, in
+    """The packed sampler (sgl_recent_sample_packed: int32 timestamps and
+    interleaved ids, chosen when every timestamp fits in int32) gives
+    bit-identical windows to the int64 one, in
     both kernel modes (one wave per query up to 32768 queries, one lane per
     query above), with negative times and query times beyond int32's range;
     a graph whose timestamps do not fit keeps the int64 path."""
