@@ -441,7 +441,7 @@ HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 1133.4 + 1504.5) * 1024),
                ("cfg4", "memory_update"): round((2 * 2311.0 + 256.2) * 1024),
                ("cfg4", "predictor"): round((2 * 564.4 + 1006.8) * 1024),
                ("cfg4", "param_update"): round((2 * 8017.6 + 2070.6) * 1024),
-               ("cfg3", "recent_sample"): round((2 * 1943301 + 449830) * 1024)}
+               ("cfg3", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
 
 # step stage name -> the C-ABI entry point that launches it
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",

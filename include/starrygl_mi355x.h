@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 9
+#define SGL_ABI_VERSION 10
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -100,9 +100,13 @@ int sgl_recent_sample(const int64_t *indptr, const int32_t *nbr,
  * 8-byte aligned) and ts the int32 timestamps. Each entry is compared with the
  * int64 query time exactly as its int64 value would be, so the results are
  * identical; a search probe reads half the bytes (32 timestamps per 128-byte
- * line) and a window's ids one contiguous run. */
+ * line) and a window's ids one contiguous run. fence (may be NULL) holds
+ * ts[32 f] for f < ceil(num_edges / 32) and may be given only when every
+ * node's list is sorted by time: the queries of more than 32768-query
+ * launches then search the fences inside their list first (a small array
+ * that stays in cache) and one 32-entry line of ts after it. */
 int sgl_recent_sample_packed(const int64_t *indptr, const int32_t *nbr_eid,
-                             const int32_t *ts, int64_t num_nodes,
+                             const int32_t *ts, const int32_t *fence, int64_t num_nodes,
                              const void *q_node, int q_node_is_i64,
                              const int64_t *q_ts, int64_t num_queries,
                              const int64_t *num_queries_dev,

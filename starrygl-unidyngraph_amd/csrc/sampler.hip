@@ -28,6 +28,7 @@ constexpr int kBlock = 256;
 constexpr int kTile = 256;      // queries per compaction tile
 constexpr int kScanBlock = 1024;
 constexpr int64_t kWaveModeMaxQueries = 1 << 15;  // below: one wavefront per query
+constexpr int64_t kFence = 32;  // CSR entries per fence (one 128-byte line of int32 times)
 
 // TsT: the CSR's timestamps as stored, int64 or (when every timestamp fits)
 // int32, compared with the int64 query times exactly. With int32 times the
@@ -37,7 +38,7 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
     int64_t nq, const int64_t *__restrict__ nq_live_dev, const NodeT *__restrict__ q_node,
     const int64_t *__restrict__ q_ts, const int32_t *__restrict__ q_valid_cnt, int q_stride,
     const int64_t *__restrict__ indptr, const int32_t *__restrict__ nbr,
-    const int32_t *__restrict__ eid, const TsT *__restrict__ ts,
+    const int32_t *__restrict__ eid, const TsT *__restrict__ ts, const TsT *__restrict__ fence,
     int64_t num_nodes, int k, int32_t *__restrict__ out_cnt,
     int32_t *__restrict__ out_nbr, int32_t *__restrict__ out_eid,
     float *__restrict__ out_dt, int64_t *__restrict__ out_ts,
@@ -57,9 +58,26 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
       if (n < 0 || n >= num_nodes) {
         if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
       } else {
-        const int64_t lo = indptr[n];
-        int64_t len = indptr[n + 1] - lo;
-        int64_t first = lo;
+        const int64_t lo = indptr[n], hi = indptr[n + 1];
+        int64_t first = lo, len = hi - lo;
+        if (fence != nullptr && len > 2 * kFence) {
+          // every list time-sorted: lower_bound over the fences (ts[kFence * f],
+          // a small array that stays in cache) inside [lo, hi) first; the
+          // answer then lies in the one line (kFence * (f - 1), kFence * f]
+          const int64_t a = (lo + kFence - 1) / kFence, bf = (hi - 1) / kFence;
+          int64_t f = a, fl = bf - a + 1;
+          while (fl > 0) {
+            const int64_t half = fl >> 1;
+            if (int64_t(fence[f + half]) < t) {
+              f += half + 1;
+              fl -= half + 1;
+            } else {
+              fl = half;
+            }
+          }
+          first = f == a ? lo : kFence * (f - 1) + 1;
+          len = (f > bf ? hi : kFence * f) - first;
+        }
         while (len > 0) {  // std::lower_bound
           const int64_t half = len >> 1;
           const int64_t mid = first + half;
@@ -274,7 +292,7 @@ __global__ void k_write_zero_ptr(int64_t *out_ptr) { out_ptr[0] = 0; }
 
 template <typename TsT>
 static int recent_sample(const int64_t *indptr, const int32_t *nbr, const int32_t *eid, const TsT *ts,
-                         int64_t num_nodes, const void *q_node, int q_node_is_i64, const int64_t *q_ts,
+                         const TsT *fence, int64_t num_nodes, const void *q_node, int q_node_is_i64, const int64_t *q_ts,
                          int64_t num_queries, const int64_t *num_queries_dev, const int32_t *q_valid_cnt,
                          int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr, int32_t *out_eid,
                          float *out_dt, int64_t *out_ts, int32_t *err_flag, hipStream_t stream) {
@@ -306,11 +324,11 @@ static int recent_sample(const int64_t *indptr, const int32_t *nbr, const int32_
   if (q_node_is_i64) {
     k_recent_padded<int64_t, TsT><<<unsigned(blocks), kBlock, 0, stream>>>(
         num_queries, num_queries_dev, static_cast<const int64_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
-        nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+        nbr, eid, ts, fence, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   } else {
     k_recent_padded<int32_t, TsT><<<unsigned(blocks), kBlock, 0, stream>>>(
         num_queries, num_queries_dev, static_cast<const int32_t *>(q_node), q_ts, q_valid_cnt, q_stride, indptr,
-        nbr, eid, ts, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
+        nbr, eid, ts, fence, num_nodes, fanout, out_cnt, out_nbr, out_eid, out_dt, out_ts, err_flag);
   }
   SGL_CHECK_LAUNCH();
   return SGL_OK;
@@ -323,17 +341,19 @@ extern "C" int sgl_recent_sample(
     int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
     int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag,
     hipStream_t stream) {
-  return recent_sample<int64_t>(indptr, nbr, eid, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
+  return recent_sample<int64_t>(indptr, nbr, eid, ts, nullptr, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
                                 num_queries_dev, q_valid_cnt, q_stride, fanout, out_cnt, out_nbr, out_eid, out_dt,
                                 out_ts, err_flag, stream);
 }
 
 extern "C" int sgl_recent_sample_packed(
-    const int64_t *indptr, const int32_t *nbr_eid, const int32_t *ts, int64_t num_nodes, const void *q_node,
+    const int64_t *indptr, const int32_t *nbr_eid, const int32_t *ts, const int32_t *fence, int64_t num_nodes,
+    const void *q_node,
     int q_node_is_i64, const int64_t *q_ts, int64_t num_queries, const int64_t *num_queries_dev,
     const int32_t *q_valid_cnt, int32_t q_stride, int32_t fanout, int32_t *out_cnt, int32_t *out_nbr,
     int32_t *out_eid, float *out_dt, int64_t *out_ts, int32_t *err_flag, hipStream_t stream) {
-  return recent_sample<int32_t>(indptr, nbr_eid, nullptr, ts, num_nodes, q_node, q_node_is_i64, q_ts, num_queries,
+  return recent_sample<int32_t>(indptr, nbr_eid, nullptr, ts, fence, num_nodes, q_node, q_node_is_i64, q_ts,
+                                num_queries,
                                 num_queries_dev, q_valid_cnt, q_stride, fanout, out_cnt, out_nbr, out_eid, out_dt,
                                 out_ts, err_flag, stream);
 }

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -37,8 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_tcsr_build": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     "sgl_recent_sample": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _vp, _i32, _i32,
                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "sgl_recent_sample_packed": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _vp, _i32,
-                                                _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sgl_recent_sample_packed": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _vp,
+                                                _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "sgl_compact_workspace_bytes": (_sz, [_i64]),
     "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),

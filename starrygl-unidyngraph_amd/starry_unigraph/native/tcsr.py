@@ -120,7 +120,9 @@ class RecentSampler:
     graph fits in int32 (checked once here), the sampler reads a packed copy:
     int32 timestamps and interleaved (nbr, eid) pairs (sgl_recent_sample_packed:
     identical results, half the bytes per probe, one run of ids per window);
-    ``narrow_ts=False`` keeps the int64 arrays."""
+    ``narrow_ts=False`` keeps the int64 arrays. When moreover every node's
+    list is sorted by time, every 32nd timestamp goes into a fence array that
+    large query batches search first."""
 
     def __init__(self, graph: DeviceTCSR, narrow_ts: bool = True):
         self.g = graph
@@ -128,11 +130,16 @@ class RecentSampler:
         self.err = _capi.ErrorFlag(self.dev)
         self.ts32: torch.Tensor | None = None
         self.ids: torch.Tensor | None = None
+        self.fence: torch.Tensor | None = None
         if narrow_ts and graph.num_edges > 0:
             lo, hi = int(graph.ts.min().item()), int(graph.ts.max().item())
             if -2 ** 31 <= lo and hi < 2 ** 31:
                 self.ts32 = graph.ts.to(torch.int32)
                 self.ids = torch.stack([graph.nbr, graph.eid], dim=1).contiguous()
+                # sorted lists: every decrease of ts is at a list boundary
+                down = torch.nonzero(graph.ts[1:] < graph.ts[:-1]).flatten() + 1
+                if down.numel() == 0 or bool(torch.isin(down, graph.indptr).all()):
+                    self.fence = self.ts32[::32].contiguous()
 
     def sample(self, nodes: torch.Tensor, q_ts: torch.Tensor, fanout: int, want_ts: bool = False,
                valid_cnt: torch.Tensor | None = None, stride: int = 0,
@@ -170,7 +177,7 @@ class RecentSampler:
         g = self.g
         if self.ts32 is not None:
             fn, graph_args = "sgl_recent_sample_packed", (_capi.ptr(g.indptr), _capi.ptr(self.ids),
-                                                          _capi.ptr(self.ts32))
+                                                          _capi.ptr(self.ts32), _capi.ptr(self.fence))
         else:
             fn, graph_args = "sgl_recent_sample", (_capi.ptr(g.indptr), _capi.ptr(g.nbr), _capi.ptr(g.eid),
                                                    _capi.ptr(g.ts))

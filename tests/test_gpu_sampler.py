@@ -235,5 +235,32 @@ def test_int32_timestamps_match_int64(gpu, nq):
     live = (torch.arange(10, device=a.cnt.device)[None, :] < a.cnt.long()[:, None]).reshape(-1)
     for f in ("nbr", "eid", "dt", "ts"):
         assert torch.equal(getattr(a, f)[live], getattr(b, f)[live]), f
+    assert narrow.fence is not None   # sorted lists: the fence search runs in the one-lane-per-query mode
     g2 = build_tcsr(4, torch.tensor([0, 1]), torch.tensor([1, 1]), None, torch.tensor([1, 2 ** 31]))
     assert RecentSampler(g2).ts32 is None
+
+
+def test_unsorted_lists_skip_the_fences(gpu):
+    """Lists whose times are not sorted (event order is not time order) keep
+    std::lower_bound's probe sequence: no fences, and the packed sampler
+    equals the int64 one and the oracle."""
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    rng = np.random.default_rng(5)
+    N, E, nq = 500, 60_000, 50_000
+    row, col = rng.integers(0, N, E), rng.integers(0, N, E)
+    ts = rng.integers(0, 10 ** 6, E)          # unsorted
+    g = build_tcsr(N, torch.as_tensor(row), torch.as_tensor(col), None, torch.as_tensor(ts))
+    narrow, wide = RecentSampler(g), RecentSampler(g, narrow_ts=False)
+    assert narrow.ts32 is not None and narrow.fence is None
+    nodes, qt = rng.integers(0, N, nq), rng.integers(0, 10 ** 6, nq)
+    a = narrow.sample(torch.as_tensor(nodes).cuda(), torch.as_tensor(qt).cuda(), 7)
+    b = wide.sample(torch.as_tensor(nodes).cuda(), torch.as_tensor(qt).cuda(), 7)
+    assert torch.equal(a.cnt, b.cnt)
+    live = (torch.arange(7, device=a.cnt.device)[None, :] < a.cnt.long()[:, None]).reshape(-1)
+    for f in ("nbr", "eid", "dt"):
+        assert torch.equal(getattr(a, f)[live], getattr(b, f)[live]), f
+    og = so.build_tcsr(N, row, col, np.arange(E), ts)
+    want = so.sample_recent(og, nodes[:2000], qt[:2000], [7])[0]
+    got = narrow.compact(narrow.sample(torch.as_tensor(nodes[:2000]).cuda(), torch.as_tensor(qt[:2000]).cuda(), 7))
+    np.testing.assert_array_equal(got.nbr.cpu().numpy(), want["sample_nodes"])
+    np.testing.assert_array_equal(got.eid.cpu().numpy(), want["eid"])
