@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 10
+#define SGL_ABI_VERSION 11
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -230,6 +230,16 @@ int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
 int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
                       const int64_t *roots, const float *new_mem,
                       float *memory, float *memory_ts, const float *ts_max,
+                      uint32_t *node_bits, const int32_t *sample_cnt,
+                      int32_t *any_edges, hipStream_t stream);
+/* The same step point without a memory updater: rows[r] = memory[roots[r]]
+ * for r < U (the attention's root rows), node_bits cleared and any_edges set
+ * as above; memory and memory_ts are not written. Replaces the gather of
+ * CTDGMemoryBank.gather (memory.py:135-151) on the path of
+ * CTDGOnlineRuntime.train_step without an updater (runtime.py:283-285), which
+ * scores from the memory as it is. */
+int sgl_memory_gather(int32_t D, int64_t capacity, const int32_t *num_roots,
+                      const int64_t *roots, const float *memory, float *rows,
                       uint32_t *node_bits, const int32_t *sample_cnt,
                       int32_t *any_edges, hipStream_t stream);
 

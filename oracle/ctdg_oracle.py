@@ -297,12 +297,17 @@ def loss_from_logits(pos, neg):
 
 
 def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts, edge_feat, neg, edge_feat_all,
-               train=True):
+               train=True, after_memory=None):
     """runtime.py:225-297 for one batch (1 rank, dropout 0). ``sample_fn(roots,
-    tq)`` returns the hop-0 Block. Returns a dict of the step's tensors."""
+    tq)`` returns the hop-0 Block. ``after_memory(mem)`` (tests) runs between
+    the memory phase and the attention, e.g. to hand the attention another
+    implementation's updated memory. Returns a dict of the step's tensors."""
     roots, tq = prepare_roots(src, dst, ts)
     blk = sample_fn(roots, tq)
-    memory_phase(mem, updater, src, dst, ts, edge_feat)
+    if updater is not None:   # runtime.py:283-285: without one, memory and mailbox stay as they are
+        memory_phase(mem, updater, src, dst, ts, edge_feat)
+    if after_memory is not None:
+        after_memory(mem)
     if train:
         model.train()
     else:

@@ -632,39 +632,32 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
 }
 
 __global__ __launch_bounds__(kBlock) void k_memory_commit(
-    int D, bool vec4, int64_t cap, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ roots,
-    const float *__restrict__ new_mem, float *__restrict__ memory, float *__restrict__ memory_ts,
-    const float *__restrict__ ts_max, uint32_t *__restrict__ bits,
+    int D, bool vec4, bool gather, int64_t cap, const int32_t *__restrict__ num_roots,
+    const int64_t *__restrict__ roots, float *__restrict__ rows, float *__restrict__ memory,
+    float *__restrict__ memory_ts, const float *__restrict__ ts_max, uint32_t *__restrict__ bits,
     const int32_t *__restrict__ sample_cnt, int32_t *__restrict__ any_edges) {
   // grid-stride over the live roots' elements (the grid is bounded, so a
   // large capacity with few live roots costs no idle workgroups), four at a
-  // time when the rows allow 16-byte accesses
-  const float tmax = *ts_max;
+  // time when the rows allow 16-byte accesses. Commit: memory[roots[r]] =
+  // rows[r] and memory_ts = ts_max; gather (no memory updater): rows[r] =
+  // memory[roots[r]]. Both clear the roots' bitmap words and set the gate.
   const int64_t nr = min(cap, int64_t(*num_roots));
-  if (vec4) {
-    const int D4 = D >> 2;
-    const int64_t live = nr * D4;
-    for (int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x; idx < live; idx += int64_t(gridDim.x) * kBlock) {
-      const int64_t r = idx / D4;
-      const int j = int(idx - r * D4);
-      const int64_t u = roots[r];
-      reinterpret_cast<float4 *>(memory)[u * D4 + j] = reinterpret_cast<const float4 *>(new_mem)[r * D4 + j];
-      if (j == 0) {
-        memory_ts[u] = tmax;
-        bits[u >> 5] = 0u;
-        if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
-      }
-    }
-    return;
-  }
-  const int64_t live = nr * D;
+  const float tmax = gather ? 0.0f : *ts_max;
+  const int W = vec4 ? D >> 2 : D;
+  const int64_t live = nr * W;
   for (int64_t idx = int64_t(blockIdx.x) * kBlock + threadIdx.x; idx < live; idx += int64_t(gridDim.x) * kBlock) {
-    const int64_t r = idx / D;
-    const int j = int(idx - r * D);
+    const int64_t r = idx / W;
+    const int j = int(idx - r * W);
     const int64_t u = roots[r];
-    memory[u * D + j] = new_mem[r * D + j];
+    if (vec4) {
+      float4 *m4 = reinterpret_cast<float4 *>(memory) + u * W + j;
+      float4 *r4 = reinterpret_cast<float4 *>(rows) + r * W + j;
+      if (gather) *r4 = *m4; else *m4 = *r4;
+    } else {
+      if (gather) rows[r * D + j] = memory[u * D + j]; else memory[u * D + j] = rows[r * D + j];
+    }
     if (j == 0) {
-      memory_ts[u] = tmax;
+      if (!gather) memory_ts[u] = tmax;
       bits[u >> 5] = 0u;  // leave the bitmap clear for the next step
       if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
     }
@@ -790,20 +783,34 @@ extern "C" int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t c
                                  batch_start, win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
 }
 
+static int memory_rows(const char *what, bool gather, int32_t D, int64_t capacity, const int32_t *num_roots,
+                       const int64_t *roots, float *rows, float *memory, float *memory_ts, const float *ts_max,
+                       uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges, hipStream_t stream) {
+  SGL_REQUIRE(D > 0, "%s: D <= 0", what);
+  SGL_REQUIRE(capacity >= 0, "%s: capacity < 0", what);
+  if (capacity == 0) return SGL_OK;
+  SGL_REQUIRE(num_roots && roots && rows && memory && node_bits && any_edges && (gather || (memory_ts && ts_max)),
+              "%s: NULL array", what);
+  const bool vec4 = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(memory) | reinterpret_cast<uintptr_t>(rows)) & 15u) == 0;
+  const int64_t total = capacity * (vec4 ? D / 4 : D);
+  const unsigned grid = unsigned(std::min<int64_t>((total + kBlock - 1) / kBlock, sgl::kMaxGrid));
+  sgl::launch(&k_memory_commit, dim3(grid), dim3(kBlock), 0, stream, D, vec4, gather, capacity,
+              num_roots, roots, rows, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
 extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
                                  const float *new_mem, float *memory, float *memory_ts, const float *ts_max,
                                  uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges,
                                  hipStream_t stream) {
-  SGL_REQUIRE(D > 0, "memory_commit: D <= 0");
-  SGL_REQUIRE(capacity >= 0, "memory_commit: capacity < 0");
-  if (capacity == 0) return SGL_OK;
-  SGL_REQUIRE(num_roots && roots && new_mem && memory && memory_ts && ts_max && node_bits && any_edges,
-              "memory_commit: NULL array");
-  const bool vec4 = D % 4 == 0 && ((reinterpret_cast<uintptr_t>(memory) | reinterpret_cast<uintptr_t>(new_mem)) & 15u) == 0;
-  const int64_t total = capacity * (vec4 ? D / 4 : D);
-  const unsigned grid = unsigned(std::min<int64_t>((total + kBlock - 1) / kBlock, sgl::kMaxGrid));
-  sgl::launch(&k_memory_commit, dim3(grid), dim3(kBlock), 0, stream, D, vec4, capacity,
-              num_roots, roots, new_mem, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
-  SGL_CHECK_LAUNCH();
-  return SGL_OK;
+  return memory_rows("memory_commit", false, D, capacity, num_roots, roots, const_cast<float *>(new_mem), memory,
+                     memory_ts, ts_max, node_bits, sample_cnt, any_edges, stream);
+}
+
+extern "C" int sgl_memory_gather(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
+                                 const float *memory, float *rows, uint32_t *node_bits, const int32_t *sample_cnt,
+                                 int32_t *any_edges, hipStream_t stream) {
+  return memory_rows("memory_gather", true, D, capacity, num_roots, roots, rows, const_cast<float *>(memory),
+                     nullptr, nullptr, node_bits, sample_cnt, any_edges, stream);
 }

@@ -40,12 +40,13 @@ class CTDGDataBatch:
         (computed once: batches are immutable)."""
         st = self.__dict__.get("_start")
         if st is None:
-            n = self.event_ids.numel()
-            if n == 0:
+            ids = self.event_ids
+            if ids.numel() == 0:
                 st = 0
-            else:
-                a, b = int(self.event_ids[0]), int(self.event_ids[-1])
-                st = a if b - a + 1 == n else -1
+            elif ids.numel() == 1 or bool((ids[1:] - ids[:-1]).eq(1).all()):
+                st = int(ids[0])
+            else:   # out-of-order or gapped ids: the step gathers the batch's own events
+                st = -1
             self.__dict__["_start"] = st
         return st
 

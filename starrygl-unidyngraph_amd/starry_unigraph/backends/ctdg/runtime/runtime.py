@@ -78,6 +78,11 @@ class CTDGOnlineRuntime:
         self.plan_timer = None
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
+        # negatives are drawn inside the step, for neg_chunk consecutive
+        # batches of a contiguous split at a time (1: one draw per step);
+        # _neg_ahead[split] = (next unconsumed event, end of the drawn range)
+        self.neg_chunk = 32
+        self._neg_ahead: dict[str, tuple[int, int]] = {}
         core = self._core()
         conv = core.conv
         self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head,
@@ -110,7 +115,13 @@ class CTDGOnlineRuntime:
         self._state_writes = memory.state.writes
 
     def _make_steps(self, max_batch: int) -> None:
-        self.steps = [DeviceStep(self.memory.state, self.dims, max_batch) for _ in range(2)]
+        # every hop of the sampler (history layers, sampler.py:76-90) is
+        # sampled; the attention reads hop 0 (runtime.py:164-167)
+        hops = [int(f) for f in self.sampler.fanout[:max(1, int(self.sampler.history))]]
+        if len(hops) < int(self.sampler.history):
+            raise RuntimeError(f"ParallelSampler: num_layers {self.sampler.history} > len(fanouts) {len(hops)}")
+        self.steps = [DeviceStep(self.memory.state, self.dims, max_batch, more_fanouts=tuple(hops[1:]))
+                      for _ in range(2)]
         self._parity = 0
         self.step = self.steps[0]   # the step buffers of the latest step
 
@@ -198,7 +209,8 @@ class CTDGOnlineRuntime:
 
     def _negatives_at(self, batch: CTDGDataBatch) -> tuple[torch.Tensor, int]:
         """(buffer, offset) of the batch's negatives (offset -1: the buffer is
-        exactly the batch's negatives); consumes the split's precomputed queue."""
+        exactly the batch's negatives); consumes the split's precomputed queue,
+        else the negatives drawn ahead for consecutive batches."""
         q = self._neg_queue.get(batch.split)
         if q is not None:
             buf, off = q
@@ -207,7 +219,37 @@ class CTDGOnlineRuntime:
                 self._neg_queue[batch.split] = (buf, off + n)
                 return buf, off
             del self._neg_queue[batch.split]
+        s, n = batch.start, batch.size
+        if s >= 0 and self.neg_chunk > 1:
+            lo, hi = self._neg_ahead.get(batch.split, (-1, -1))
+            if s != lo or s + n > hi:
+                self._draw_ahead(batch)
+            self._neg_ahead[batch.split] = (s + n, self._neg_ahead[batch.split][1])
+            return self._neg_all, s
         return self._negative_sample(batch).to(self.device, non_blocking=True), -1
+
+    def _draw_ahead(self, batch: CTDGDataBatch) -> None:
+        """Negatives of this batch and the next neg_chunk - 1 batches of its
+        split in one draw on the CPU generator, written at their places in
+        the stream-wide array. torch.randint gives the same numbers in one
+        call as in one call per batch, so while batches come in order this
+        equals the reference's per-step draw (runtime.py:124-136); a batch out
+        of order discards what was drawn ahead (the generator has then moved
+        on past draws that no step used)."""
+        s, n = batch.start, batch.size
+        ids = self.dataset.split_event_ids("test" if batch.split == "predict" else batch.split)
+        end = int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
+        hi = max(s + n, min(end, s + self.neg_chunk * n))
+        pool = self._dst_pool()
+        idx = torch.randint(low=0, high=pool.numel(), size=(hi - s,), dtype=torch.long)
+        neg = pool[idx]
+        col = neg.eq(self.dataset.dst[s:hi])
+        if col.any():
+            idx[col] = (idx[col] + 1) % pool.numel()
+            neg = pool[idx]
+        self._neg_all[s:hi].copy_(neg.pin_memory(), non_blocking=True)
+        self._neg_ahead[batch.split] = (s, hi)
+        self.fence()   # the batch preparations read them on the other stream
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev
@@ -337,6 +379,8 @@ class CTDGOnlineRuntime:
         that the step's fused update reads."""
         if self._gru is not None:
             step.commit()
+        else:   # runtime.py:283-285: the conv reads the memory as it is
+            step.gather_memory()
         step.edge_rows(self._dev["edge_feat"])
         if train:
             self._param_update(step).advance()
@@ -396,16 +440,24 @@ class CTDGOnlineRuntime:
         return m
 
     def _sample_meta(self, n: int) -> dict[str, int]:
+        """CTDGSampleOutput.describe() (sampler.py:27-33, sampler.py:119-120):
+        roots, |unique(roots and every hop's nodes)|, |unique(every hop's
+        edge ids)|, the number of hops."""
         b = self.step.buf
         u = int(b.num_roots.item())
-        cnt = b.hop.cnt[:u]
-        k = self.dims.fanout
-        valid = torch.arange(k, device=cnt.device).unsqueeze(0) < cnt.unsqueeze(1)
-        nbr = b.hop.nbr[:u * k].view(u, k)[valid].long() if k > 0 else torch.empty(0, dtype=torch.long,
-                                                                                   device=cnt.device)
-        eid = b.hop.eid[:u * k].view(u, k)[valid] if k > 0 else nbr
-        return {"root_count": u, "sampled_node_count": int(torch.unique(torch.cat([b.roots[:u], nbr])).numel()),
-                "sampled_edge_count": int(torch.unique(eid).numel()), "num_layers": len(self.sampler.fanout[:1])}
+        nodes, eids = [b.roots[:u]], []
+        q = u
+        for hop in [b.hop] + b.more_hops:
+            k = hop.fanout
+            cnt = hop.cnt[:q]
+            if k > 0 and q > 0:
+                valid = torch.arange(k, device=cnt.device).unsqueeze(0) < cnt.unsqueeze(1)
+                nodes.append(hop.nbr[:q * k].view(q, k)[valid].long())
+                eids.append(hop.eid[:q * k].view(q, k)[valid].long())
+            q *= k
+        return {"root_count": u, "sampled_node_count": int(torch.unique(torch.cat(nodes)).numel()),
+                "sampled_edge_count": int(torch.unique(torch.cat(eids)).numel()) if eids else 0,
+                "num_layers": 1 + len(b.more_hops)}
 
     def _empty_result(self, batch: CTDGDataBatch, split: str) -> dict[str, Any]:
         return {"loss": 0.0, "predictions": [], "targets": [],

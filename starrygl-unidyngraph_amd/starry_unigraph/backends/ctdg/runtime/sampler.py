@@ -62,7 +62,7 @@ class NativeTemporalSampler:
                                '(the CTDG configs use "recent")')
         r = self._device.get(split)
         if r is None:
-            r = self._device[split] = RecentSampler(self._get(split).tnb.graph)
+            r = self._device[split] = RecentSampler.for_graph(self._get(split).tnb.graph)
         return r
 
     def sample(self, split: str, root_nodes: torch.Tensor, timestamps: torch.Tensor) -> CTDGSampleOutput:

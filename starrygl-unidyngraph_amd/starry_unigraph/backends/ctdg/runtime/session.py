@@ -65,13 +65,39 @@ class CTDGSession:
         torch.save(ckpt, str(path))
 
     def load_checkpoint(self, path: str | Path) -> None:
-        assert self.online_runtime is not None
+        """session.py:87-93: strict state-dict loads of the model and the
+        updater. The model's tensors are copied in place (its parameters are
+        views of the fused optimizer's flat buffer); the next step is ordered
+        after the copies."""
+        rt = self.online_runtime
+        assert rt is not None
         ckpt = torch.load(str(path), map_location="cpu", weights_only=True)
-        model = self.online_runtime.model
+        model = rt.model
         core = model.module if hasattr(model, "module") else model
+        _check_state_keys(type(core).__name__, core.state_dict(), ckpt["model"])
         with torch.no_grad():
+            own = core.state_dict()
             for name, t in ckpt["model"].items():
-                core.state_dict()[name].copy_(t)        # in place: parameters are views of the optimizer's buffer
-            if self.online_runtime.memory_updater is not None and "memory_updater" in ckpt:
-                self.online_runtime.memory_updater.load_state_dict(ckpt["memory_updater"])
-                self.online_runtime.memory_updater.kernel_weights()   # refresh bf16 copies in place
+                own[name].copy_(t)
+            if rt.memory_updater is not None and "memory_updater" in ckpt:
+                rt.memory_updater.load_state_dict(ckpt["memory_updater"])
+                rt.memory_updater.kernel_weights()   # refresh bf16 copies in place
+        rt.fence()
+
+
+def _check_state_keys(owner: str, own: dict, loaded: dict) -> None:
+    """The strict checks of nn.Module.load_state_dict (same message form):
+    missing and unexpected keys and shape mismatches raise RuntimeError."""
+    missing = [k for k in own if k not in loaded]
+    unexpected = [k for k in loaded if k not in own]
+    errs = []
+    if unexpected:
+        errs.append("Unexpected key(s) in state_dict: " + ", ".join(f'"{k}"' for k in unexpected) + ". ")
+    if missing:
+        errs.append("Missing key(s) in state_dict: " + ", ".join(f'"{k}"' for k in missing) + ". ")
+    for k, t in loaded.items():
+        if k in own and tuple(own[k].shape) != tuple(t.shape):
+            errs.append(f"size mismatch for {k}: copying a param with shape {tuple(t.shape)} from checkpoint, "
+                        f"the shape in current model is {tuple(own[k].shape)}.")
+    if errs:
+        raise RuntimeError(f"Error(s) in loading state_dict for {owner}:\n\t" + "\n\t".join(errs))

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_update_bf16": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
+    "sgl_memory_gather": (ctypes.c_int, [_i32, _i64] + [_vp] * 8),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
     "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 8),
     "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 30),

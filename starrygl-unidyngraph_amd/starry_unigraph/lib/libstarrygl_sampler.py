@@ -163,7 +163,7 @@ class ParallelSampler:
         self.boundery_probility = float(p)
         if self.num_layers > len(self.fanouts):
             raise RuntimeError(f"ParallelSampler: num_layers {self.num_layers} > len(fanouts) {len(self.fanouts)}")
-        self._sampler = RecentSampler(tnb.graph)
+        self._sampler = RecentSampler.for_graph(tnb.graph)
         self.ret: list[TemporalGraphBlock] = [TemporalGraphBlock() for _ in range(self.num_layers)]
 
     def reset(self) -> None:

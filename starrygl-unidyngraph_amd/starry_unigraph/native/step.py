@@ -94,9 +94,13 @@ class StepBuffers:
     hold cap = round_up(2*max_batch, 16) rows (the most roots a batch can
     have), so launch shapes never depend on the batch."""
 
-    def __init__(self, max_batch: int, dims: ConvDims, device, attention: bool = True):
+    def __init__(self, max_batch: int, dims: ConvDims, device, attention: bool = True,
+                 more_fanouts: tuple[int, ...] = ()):
         """``attention`` False: only the buffers of the front part (batch
-        preparation, sampling, memory / mailbox update, commit, edge rows)."""
+        preparation, sampling, memory / mailbox update, commit, edge rows).
+        ``more_fanouts``: the fanouts of the hops after hop 0 (history > 1):
+        hop l's queries are hop l-1's padded rows, so it holds
+        cap * fanout_0 * ... * fanout_l slots."""
         dev = torch.device(device)
         self.device = dev
         self.max_batch = int(max_batch)
@@ -121,8 +125,20 @@ class StepBuffers:
         self.cnt_src = z(c, dt=i32)
         self.cnt_dst = z(c, dt=i32)
         self.new_mem = z(c, D)
+        more = tuple(int(f) for f in more_fanouts)
         self.hop = PaddedHop(cnt=z(c, dt=i32), nbr=z(max(c * k, 1), dt=i32), eid=z(max(c * k, 1), dt=i32),
-                             dt=z(max(c * k, 1)), ts=None, q_ts=self.root_ts, fanout=k)
+                             dt=z(max(c * k, 1)), ts=z(max(c * k, 1), dt=i64) if more else None,
+                             q_ts=self.root_ts, fanout=k)
+        # hops 1.. (sampler.h:393-399): queried from the previous hop's rows,
+        # sampled for the step's result (the attention reads hop 0 only)
+        self.more_hops: list[PaddedHop] = []
+        q, prev = c * k, self.hop
+        for li, f in enumerate(more):
+            last = li == len(more) - 1
+            self.more_hops.append(PaddedHop(
+                cnt=z(max(q, 1), dt=i32), nbr=z(max(q * f, 1), dt=i32), eid=z(max(q * f, 1), dt=i32),
+                dt=z(max(q * f, 1)), ts=None if last else z(max(q * f, 1), dt=i64), q_ts=prev.ts, fanout=f))
+            prev, q = self.more_hops[-1], q * f
         # each sampled edge's row [memory[nbr] | efeat[eid] | cos(w dt + b)]
         # (sgl_edge_rows, then the forward)
         self.X = z(max(c * k * C, 1))
@@ -161,10 +177,11 @@ class StepBuffers:
 class DeviceStep:
     """The kernel sequence of one step over a NodeState (no host syncs)."""
 
-    def __init__(self, state: NodeState, dims: ConvDims, max_batch: int, attention: bool = True):
+    def __init__(self, state: NodeState, dims: ConvDims, max_batch: int, attention: bool = True,
+                 more_fanouts: tuple[int, ...] = ()):
         self.state = state
         self.dims = dims
-        self.buf = StepBuffers(max_batch, dims, state.device, attention=attention)
+        self.buf = StepBuffers(max_batch, dims, state.device, attention=attention, more_fanouts=more_fanouts)
         self.dev = state.device
         self.lib = _capi.lib()
         # optional per-launch timing: a list that receives (name, start, end)
@@ -212,9 +229,18 @@ class DeviceStep:
             self._s()), "sgl_batch_prepare"))
 
     def sample(self, sampler: RecentSampler) -> PaddedHop:
+        """Hop 0 of the roots at their query time, then every further hop
+        from the previous hop's padded rows (its entries' nodes and times,
+        masked by its counts); returns hop 0."""
         b = self.buf
-        return self._call("recent_sample", lambda: sampler.sample(b.roots, b.root_ts, self.dims.fanout, out=b.hop,
-                                                                   num_live=b.num_roots64))
+        want_ts = b.hop.ts is not None
+        hop = self._call("recent_sample", lambda: sampler.sample(b.roots, b.root_ts, self.dims.fanout, out=b.hop,
+                                                                  num_live=b.num_roots64, want_ts=want_ts))
+        prev = hop
+        for h in b.more_hops:
+            prev = sampler.sample(prev.nbr[:h.num_queries], prev.ts[:h.num_queries], h.fanout,
+                                  want_ts=h.ts is not None, valid_cnt=prev.cnt, stride=prev.fanout, out=h)
+        return hop
 
     # -- memory -------------------------------------------------------------
     def update_memory(self, gru: dict, src, dst, efeat, ts, from_cursor: bool = False) -> None:
@@ -236,6 +262,14 @@ class DeviceStep:
         self._call("memory_commit", lambda: _capi.check(_capi.call("sgl_memory_commit", 
             st.D, b.cap, P(b.num_roots), P(b.roots), P(b.new_mem), P(st.memory), P(st.memory_ts), P(b.ts_max),
             P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
+
+    def gather_memory(self) -> None:
+        """The commit's place without a memory updater: the roots' memory rows
+        into new_mem (the attention's root rows), memory left as it is."""
+        b, st, P = self.buf, self.state, _capi.ptr
+        self._call("memory_gather", lambda: _capi.check(_capi.call("sgl_memory_gather",
+            st.D, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(b.new_mem), P(st.node_bits), P(b.hop.cnt),
+            P(b.any_edges), self._s()), "sgl_memory_gather"))
 
     # -- attention ----------------------------------------------------------
     def edge_rows(self, efeat_all: torch.Tensor) -> None:

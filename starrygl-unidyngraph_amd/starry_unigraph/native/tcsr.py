@@ -141,6 +141,16 @@ class RecentSampler:
                 if down.numel() == 0 or bool(torch.isin(down, graph.indptr).all()):
                     self.fence = self.ts32[::32].contiguous()
 
+    @classmethod
+    def for_graph(cls, graph: DeviceTCSR) -> "RecentSampler":
+        """The one sampler of ``graph`` (made on first use, then kept on the
+        graph): its packed copy and fences are built once per CSR."""
+        r = getattr(graph, "_recent_sampler", None)
+        if r is None:
+            r = cls(graph)
+            graph._recent_sampler = r
+        return r
+
     def sample(self, nodes: torch.Tensor, q_ts: torch.Tensor, fanout: int, want_ts: bool = False,
                valid_cnt: torch.Tensor | None = None, stride: int = 0,
                out: PaddedHop | None = None, num_live: torch.Tensor | None = None) -> PaddedHop:

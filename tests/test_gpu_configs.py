@@ -1,0 +1,230 @@
+"""Full training and eval steps at the dimensions of every BASELINE
+configuration, teacher-forced against the CPU oracle (each step starts from
+the oracle's parameters and node state, so fp32 trajectories that the
+learnable time encoding would decorrelate are compared step by step):
+
+  cfg1  bipartite stream (the full 157,474-event stream), D = T = 100,
+        F = 172, H = 2, k = 10, K = 1, B = 200
+  cfg2  the same with the "jodie" family (the reference builds the same
+        model for it, models.py:337-338)
+  cfg4  unipartite Zipf(1.5) stream (30,000 nodes, 120,000 events of the
+        same generator), D = T = 100, F = 16, H = 2, k = 10, K = 1, B = 600
+  cfg5  unipartite Zipf(1.5) stream (30,000 nodes, 160,000 events), D = 172,
+        T = 100, F = 16, H = 4, k = 20 for 2 hops, K = 4, B = 4000
+
+each with the fp32 GRU and with bf16 GRU GEMMs. Tolerances: loss, logits
+and memory within rtol 1e-3, gradients within rtol 2e-3 (atol 1e-3 of the
+largest entry); with bf16 GEMMs in the GRU its memory update is held to
+rtol / atol 2e-2 against the fp32 oracle's, and the oracle's attention,
+predictor and backward are then run from the GPU's updated memory and held
+to the fp32 tolerances above.
+Mailbox contents, mailbox timestamps, slot pointers and memory timestamps
+are bit-exact in both (messages carry the memory from before the update).
+Also: the eval step against the oracle's no-grad step, the product's own
+negative draws against the oracle's under the same seed, the sample
+statistics of every hop against the oracle sampler, and the path without a
+memory updater."""
+import numpy as np
+import pytest
+import torch
+
+import ctdg_oracle as co
+import sampler_oracle as so
+
+pytestmark = pytest.mark.gpu
+
+CONFIGS = {
+    "cfg1": dict(stream="bipartite", gen={}, family="tgn", D=100, T=100, H=2, k=10, K=1, B=200, history=1,
+                 batches=(300, 301, 302)),
+    "cfg2": dict(stream="bipartite", gen={}, family="jodie", D=100, T=100, H=2, k=10, K=1, B=200, history=1,
+                 batches=(400, 401)),
+    "cfg4": dict(stream="unipartite", gen=dict(num_nodes=30000, num_events=120000), family="tgn", D=100, T=100,
+                 H=2, k=10, K=1, B=600, history=1, batches=(60, 61, 62)),
+    "cfg5": dict(stream="unipartite", gen=dict(num_nodes=30000, num_events=160000), family="tgn", D=172, T=100,
+                 H=4, k=20, K=4, B=4000, history=2, batches=(12, 13)),
+}
+
+_STREAMS: dict = {}
+
+
+def _stream(c):
+    from starry_unigraph import synth
+    key = (c["stream"], tuple(sorted(c["gen"].items())))
+    s = _STREAMS.get(key)
+    if s is None:
+        fn = synth.bipartite_stream if c["stream"] == "bipartite" else synth.unipartite_stream
+        s = _STREAMS[key] = fn(seed=0, **c["gen"])
+    return s
+
+
+def _pair(name, gemm="fp32", seed=0, updater=True):
+    """The product runtime for a configuration and the oracle with the same
+    weights; oracle node state drawn at random (memory in (-1, 1), mailbox
+    N(0, 1/4), slot pointers and timestamps random)."""
+    from starry_unigraph import SchedulerSession
+    from starry_unigraph.data import from_stream
+    c = CONFIGS[name]
+    s = _stream(c)
+    F = s.edge_feat.shape[1]
+    cfg = {"model": {"family": c["family"], "hidden_dim": c["D"]}, "data": {"name": f"p_{name}", "format": "synthetic"},
+           "train": {"batch_size": c["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
+           "ctdg": {"mailbox_slots": c["K"], "dim_time": c["T"], "num_head": c["H"], "dropout": 0.0,
+                    "att_dropout": 0.0, "memory_gemm_dtype": gemm},
+           "sampling": {"neighbor_limit": [c["k"]] * c["history"], "history": c["history"], "strategy": "recent"}}
+    torch.manual_seed(seed)
+    sess = SchedulerSession.from_config(cfg).with_events(from_stream(s))
+    sess.build_runtime()
+    rt = sess.ctdg_session.online_runtime
+    model, upd = co.build_models(c["D"], F, c["T"], c["H"], c["K"], seed=seed)
+    model.load_state_dict({k: v.cpu() for k, v in rt.model.state_dict().items()})
+    upd.load_state_dict({k: v.cpu() for k, v in rt.memory_updater.state_dict().items()})
+    if not updater:
+        rt.memory_updater, rt._gru, upd = None, None, None
+    opt = torch.optim.Adam(list(model.parameters()) + (list(upd.parameters()) if upd else []), lr=1e-3)
+    g = torch.Generator().manual_seed(seed + 1)
+    N, D, K = rt.dataset.num_nodes, c["D"], c["K"]
+    mem = co.MemoryO(N, D, K, F)
+    mem.memory = torch.rand(N, D, generator=g) * 2 - 1
+    mem.mailbox = torch.randn(N, K, 2 * D + F, generator=g) * 0.5
+    mem.mailbox_ts = torch.rand(N, K, generator=g) * 1e3
+    mem.memory_ts = torch.rand(N, generator=g) * 1e3
+    mem.next_mail_pos = torch.randint(0, K, (N,), generator=g)
+    return c, rt, model, upd, opt, mem
+
+
+def _oracle_graphs(rt):
+    out = {}
+    for split in ("train", "val"):
+        gr = rt.dataset.sampler_graph(split)
+        out[split] = so.build_tcsr(rt.dataset.num_nodes, gr["row"].numpy(), gr["col"].numpy(), gr["eid"].numpy(),
+                                   gr["ts"].numpy())
+    return out
+
+
+def _teacher_force(rt, model, mem):
+    with torch.no_grad():
+        for p, q in zip(rt.model.parameters(), model.parameters()):
+            p.copy_(q)
+    st = rt.memory.state
+    st.memory.copy_(mem.memory)
+    st.mailbox.copy_(mem.mailbox)
+    st.mailbox_ts.copy_(mem.mailbox_ts)
+    st.memory_ts.copy_(mem.memory_ts)
+    st.next_mail_pos.copy_(mem.next_mail_pos.to(torch.int32))
+    st.touched()
+
+
+def _close(got, want, rtol, atol, msg):
+    torch.testing.assert_close(got.detach().cpu().double(), want.detach().cpu().double(), rtol=rtol, atol=atol,
+                               msg=lambda m: f"{msg}: {m}")
+
+
+def _describe(og, roots, tq, fanouts):
+    """CTDGSampleOutput.describe() of the oracle sampler's hops."""
+    hops = so.sample_recent(og, roots.numpy(), tq.numpy(), fanouts)
+    nodes = np.unique(np.concatenate([roots.numpy()] + [h["sample_nodes"] for h in hops]))
+    eids = np.unique(np.concatenate([h["eid"] for h in hops])) if hops else np.empty(0)
+    return {"root_count": roots.numel(), "sampled_node_count": nodes.size, "sampled_edge_count": eids.size,
+            "num_layers": len(fanouts)}
+
+
+def _run_steps(name, gemm, train=True, updater=True):
+    c, rt, model, upd, opt, mem = _pair(name, gemm, updater=updater)
+    ogs = _oracle_graphs(rt)
+    split = "train" if train else "val"
+    og = ogs[split]
+    fan = c["k"]
+    batches = list(rt.iter_batches(split, c["B"]))
+    picks = c["batches"] if train else (len(batches) // 2,)
+    pool = rt.dataset.dst.unique()
+    gen = torch.Generator().manual_seed(5)
+    bf16 = gemm == "bf16"
+    tol = 1e-3
+    for i in picks:
+        batch = batches[i]
+        msg = f"{name} {gemm} {split} batch {i}"
+        print(msg, flush=True)
+        neg = co.negative_sample(pool, batch.dst, gen)
+        _teacher_force(rt, model, mem)
+        rt._neg_queue[split] = (neg.to(rt.device), 0)
+        out = rt.train_step(batch) if train else rt.eval_step(batch, split)
+        st = rt.memory.state
+        hook = None
+        if bf16:
+            # the bf16 GRU against the fp32 oracle's memory update (rtol /
+            # atol 2e-2); the oracle's attention, predictor and backward then
+            # run from the GPU's updated memory and must match at fp32 tolerance
+            m32 = mem.clone()
+            co.memory_phase(m32, upd, batch.src, batch.dst, batch.ts, batch.edge_feat)
+            _close(st.memory, m32.memory, 2e-2, 2e-2, f"bf16 GRU memory {msg}")
+            gpu_mem = st.memory.cpu()
+            hook = lambda m: m.memory.copy_(gpu_mem)
+        ref = co.train_step(model, upd, opt, mem, lambda r, t: co.block_from_oracle_sampler(og, r, t, fan),
+                            batch.src, batch.dst, batch.ts, batch.edge_feat, neg, rt.dataset.edge_feat, train=train,
+                            after_memory=hook)
+        assert int(ref["block"].nbr.numel()) > 0, msg
+        rl = float(ref["loss"])
+        assert abs(out["loss"] - rl) <= tol * abs(rl) + 1e-6, (msg, out["loss"], rl)
+        np.testing.assert_allclose(out["predictions"], torch.sigmoid(ref["pos"]).numpy(), rtol=tol, atol=tol * 1e-2,
+                                   err_msg=msg)
+        n = batch.size
+        _close(rt.step.buf.neg[:n], ref["neg"], tol, tol * float(ref["neg"].abs().max()), f"neg logits {msg}")
+        _close(st.memory, mem.memory, tol, 1e-5, f"memory {msg}")
+        assert torch.equal(st.mailbox.cpu(), mem.mailbox), f"mailbox {msg}"
+        assert torch.equal(st.mailbox_ts.cpu(), mem.mailbox_ts), msg
+        assert torch.equal(st.memory_ts.cpu(), mem.memory_ts), msg
+        assert torch.equal(st.next_mail_pos.cpu().long(), mem.next_mail_pos), msg
+        if train:
+            meta = out["meta"]["sample"]
+            want = _describe(og, ref["roots"], co.prepare_roots(batch.src, batch.dst, batch.ts)[1],
+                             [c["k"]] * c["history"])
+            assert meta == want, (msg, meta, want)
+            for (pn, p), (_, q) in zip(rt.model.named_parameters(), model.named_parameters()):
+                assert q.grad is not None, (pn, msg)
+                scale = float(q.grad.abs().max()) + 1e-12
+                _close(p.grad, q.grad, 2e-3, 1e-3 * scale, f"grad {pn} {msg}")
+    return rt
+
+
+@pytest.mark.parametrize("gemm", ["fp32", "bf16"])
+@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg4", "cfg5"])
+def test_train_steps_match_oracle_at_config_dims(gpu, name, gemm):
+    _run_steps(name, gemm)
+
+
+@pytest.mark.parametrize("name", ["cfg4", "cfg5"])
+def test_eval_step_matches_oracle(gpu, name):
+    _run_steps(name, "fp32", train=False)
+
+
+def test_step_without_memory_updater_matches_oracle(gpu):
+    """runtime.py:283-285: no updater -- the attention reads the memory as it
+    is, memory and mailbox stay untouched; cfg5's batches have > 2048 events
+    (the multi-workgroup batch preparation, whose node bitmap the step must
+    clear)."""
+    for name in ("cfg4", "cfg5"):
+        rt = _run_steps(name, "fp32", updater=False)
+        assert int(torch.count_nonzero(rt.memory.state.node_bits).item()) == 0
+
+
+def test_product_negatives_match_oracle_draws(gpu):
+    """The runtime's own negatives (drawn inside the step, a chunk of
+    consecutive batches per CPU draw, the last chunk cut at the split's end)
+    equal the oracle's per-batch draws (runtime.py:124-136) on the same
+    seeded global generator: a whole train epoch, then val batches."""
+    c, rt, *_ = _pair("cfg4", "fp32")
+    rt.neg_chunk = 8
+    rt.collect_results = False
+    pool = rt.dataset.dst.unique()
+    torch.manual_seed(1234)
+    gen = torch.Generator().manual_seed(1234)
+    for split, count in (("train", None), ("val", 5)):
+        batches = list(rt.iter_batches(split, c["B"]))[:count]
+        for batch in batches:
+            rt.train_step(batch) if split == "train" else rt.eval_step(batch, split)
+        torch.cuda.synchronize()
+        for batch in batches:
+            want = co.negative_sample(pool, batch.dst, gen)
+            got = rt._neg_all[batch.start:batch.start + batch.size].cpu()
+            assert torch.equal(got, want), (split, batch.index)
+    rt.check_sync()

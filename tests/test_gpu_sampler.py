@@ -195,6 +195,38 @@ def test_config3_scale_properties(gpu):
         np.testing.assert_array_equal(hop.eid[sel_t].cpu().numpy(), want["eid"])
         np.testing.assert_array_equal(hop.dt[sel_t].cpu().numpy(), want["delta_ts"].astype(np.float32))
         del hop, qi, ets, same
+    # 2 hops (sampler.h:393-399): hop-2 queries are every hop-1 entry (its
+    # node at its timestamp), in the padded layout (k = 20: 80M queries,
+    # 1.6e9 slots)
+    for k in (10, 20):
+        h1, h2 = s.sample_padded_hops(nd, td, [k, k])
+        q2 = h2.num_queries
+        assert q2 == len(nodes) * k
+        live1 = (torch.arange(k, device="cuda")[None, :] < h1.cnt[:, None]).reshape(-1)
+        assert torch.equal(h2.cnt[~live1], torch.zeros_like(h2.cnt[~live1]))   # padding slots: no query
+        assert int(h2.cnt.max()) <= k and int(h2.cnt.min()) >= 0
+        assert int(h2.cnt.sum()) > 0
+        step = 8_000_000
+        for a in range(0, q2, step):   # every live hop-2 entry is strictly before its query time
+            b = min(q2, a + step)
+            live2 = torch.arange(k, device="cuda")[None, :] < h2.cnt[a:b, None]
+            dt = h2.dt[a * k:b * k].view(b - a, k)
+            assert bool((dt[live2] >= 1.0).all()), a
+        # exact check of random live hop-2 queries against the oracle
+        live_idx = torch.nonzero(live1).flatten()
+        draw = torch.randint(0, live_idx.numel(), (2000,), generator=torch.Generator().manual_seed(k))
+        pick = live_idx[torch.unique(draw).to(live_idx.device)]
+        qn, qtt = h1.nbr[pick].long().cpu().numpy(), h1.ts[pick].cpu().numpy()
+        want = _subset_oracle(g, qn, qtt, k)
+        cnt = h2.cnt[pick].cpu().numpy()
+        np.testing.assert_array_equal(cnt, np.diff(want["ptr"]))
+        rows = pick.cpu().numpy()[:, None] * k + np.arange(k)[None, :]
+        live = np.arange(k)[None, :] < cnt[:, None]
+        sel = torch.from_numpy(rows[live]).cuda()
+        np.testing.assert_array_equal(h2.nbr[sel].cpu().numpy(), want["sample_nodes"])
+        np.testing.assert_array_equal(h2.eid[sel].cpu().numpy(), want["eid"])
+        np.testing.assert_array_equal(h2.dt[sel].cpu().numpy(), want["delta_ts"].astype(np.float32))
+        del h1, h2, live1, live_idx
 
 
 def _subset_oracle(g, nodes, qt, k):
@@ -264,3 +296,61 @@ def test_unsorted_lists_skip_the_fences(gpu):
     got = narrow.compact(narrow.sample(torch.as_tensor(nodes[:2000]).cuda(), torch.as_tensor(qt[:2000]).cuda(), 7))
     np.testing.assert_array_equal(got.nbr.cpu().numpy(), want["sample_nodes"])
     np.testing.assert_array_equal(got.eid.cpu().numpy(), want["eid"])
+
+
+def test_fence_search_matches_int64_and_oracle(gpu):
+    """The fence search of the one-lane-per-query mode (> 32768 queries on a
+    time-sorted packed CSR): lists of 65-5000 entries at unaligned offsets,
+    runs of tied timestamps across fence lines, and
+    query times equal to fence values, equal to list entries, below a list's
+    first entry and above its last. Windows equal the int64 sampler's and
+    the oracle's."""
+    from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
+    rng = np.random.default_rng(17)
+    N = 400
+    deg = rng.integers(65, 5001, N)
+    deg[deg % 32 == 0] += 1                          # list boundaries drift off the 32-entry lines
+    col = np.repeat(np.arange(N), deg)
+    E = col.size
+    # few distinct times: long tied runs within and across 32-entry lines
+    ts_per = [np.sort(rng.integers(0, max(2, d // 40), d)) * 1000 for d in deg]
+    ts = np.concatenate(ts_per)
+    row = rng.integers(0, N, E)
+    # event order = the lists' order (a stable sort by dst keeps it), so every list is time-sorted
+    g = build_tcsr(N, torch.as_tensor(row), torch.as_tensor(col), None, torch.as_tensor(ts))
+    narrow, wide = RecentSampler(g), RecentSampler(g, narrow_ts=False)
+    assert narrow.ts32 is not None and narrow.fence is not None
+    nq = 60_000
+    nodes = rng.integers(0, N, nq)
+    ip = g.indptr.cpu().numpy()
+    gts = g.ts.cpu().numpy()
+    kind = rng.integers(0, 5, nq)
+    qt = np.empty(nq, dtype=np.int64)
+    for i, (n, k) in enumerate(zip(nodes, kind)):
+        a, b = ip[n], ip[n + 1]
+        if k == 0:      # a fence value inside the list (every 32nd global entry)
+            f = np.arange((a + 31) // 32 * 32, b, 32)
+            qt[i] = gts[f[rng.integers(0, f.size)]] if f.size else gts[a]
+        elif k == 1:    # an entry of the list
+            qt[i] = gts[rng.integers(a, b)]
+        elif k == 2:    # below the first entry
+            qt[i] = gts[a] - rng.integers(0, 2)
+        elif k == 3:    # above the last entry
+            qt[i] = gts[b - 1] + rng.integers(0, 2)
+        else:
+            qt[i] = rng.integers(-5, int(gts[b - 1]) + 5)
+    for fan in (10, 25):
+        tn, tq = torch.as_tensor(nodes).cuda(), torch.as_tensor(qt).cuda()
+        a = narrow.sample(tn, tq, fan, want_ts=True)
+        b = wide.sample(tn, tq, fan, want_ts=True)
+        assert torch.equal(a.cnt, b.cnt), fan
+        live = (torch.arange(fan, device=a.cnt.device)[None, :] < a.cnt.long()[:, None]).reshape(-1)
+        for f in ("nbr", "eid", "dt", "ts"):
+            assert torch.equal(getattr(a, f)[live], getattr(b, f)[live]), (f, fan)
+        og = so.build_tcsr(N, row, col, np.arange(E), ts)
+        want = so.sample_recent(og, nodes, qt, [fan])[0]
+        got = narrow.compact(a)
+        np.testing.assert_array_equal(got.ptr.cpu().numpy(), want["ptr"])
+        np.testing.assert_array_equal(got.nbr.cpu().numpy(), want["sample_nodes"])
+        np.testing.assert_array_equal(got.eid.cpu().numpy(), want["eid"])
+        np.testing.assert_array_equal(got.dt.cpu().numpy(), want["delta_ts"].astype(np.float32))
