@@ -127,6 +127,23 @@ int sgl_recent_compact(int64_t num_queries, int32_t fanout, const int32_t *cnt,
                        int64_t *out_ptr, int32_t *out_nbr, int32_t *out_eid,
                        float *out_dt, int64_t *out_ts, void *workspace,
                        size_t workspace_bytes, hipStream_t stream);
+/* The same compaction without a workspace argument and without allocating:
+ * its scratch (the per-tile count sums and offsets) is a static device array
+ * of the library, 1 MiB per GPU, held until the process ends. No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Limit: num_queries <= SGL_COMPACT_NOALLOC_MAX_QUERIES (larger
+ * calls return SGL_ERR_INVALID). Every call on one GPU uses that GPU's one
+ * array, so calls that overlap on a GPU (other streams, other host threads)
+ * race; the stream must belong to the current device. Results are identical
+ * to sgl_recent_compact's. */
+#define SGL_COMPACT_NOALLOC_MAX_QUERIES (1LL << 24)
+int sgl_recent_compact_noalloc(int64_t num_queries, int32_t fanout,
+                               const int32_t *cnt, const int32_t *pad_nbr,
+                               const int32_t *pad_eid, const float *pad_dt,
+                               const int64_t *pad_ts, int64_t *out_ptr,
+                               int32_t *out_nbr, int32_t *out_eid,
+                               float *out_dt, int64_t *out_ts, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * (3) Batch preparation.

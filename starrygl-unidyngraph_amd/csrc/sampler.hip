@@ -18,6 +18,7 @@
 // reference's concatenated layout (a block scan of the counts, tile offsets
 // scanned by one workgroup, then a copy).
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -364,35 +365,36 @@ extern "C" size_t sgl_compact_workspace_bytes(int64_t num_queries) {
   return 2 * sgl::align_up(tiles * 8) + 256;
 }
 
-extern "C" int sgl_recent_compact(int64_t num_queries, int32_t fanout,
-                                  const int32_t *cnt, const int32_t *pad_nbr,
-                                  const int32_t *pad_eid, const float *pad_dt,
-                                  const int64_t *pad_ts, int64_t *out_ptr,
-                                  int32_t *out_nbr, int32_t *out_eid,
-                                  float *out_dt, int64_t *out_ts,
-                                  void *workspace, size_t workspace_bytes,
-                                  hipStream_t stream) {
+namespace {
+
+// The checks and launches shared by both compaction entry points; tile_sum
+// and tile_off hold ceil(num_queries / kTile) entries each. Every entry is
+// written before it is read, so the scratch needs no clearing.
+int compact_checks(int64_t num_queries, int32_t fanout, const int32_t *cnt, const int32_t *pad_nbr,
+                   const int32_t *pad_eid, const float *pad_dt, const int64_t *pad_ts, const int64_t *out_ptr,
+                   const int32_t *out_nbr, const int32_t *out_eid, const float *out_dt, const int64_t *out_ts) {
   SGL_REQUIRE(num_queries >= 0, "compact: num_queries < 0");
   SGL_REQUIRE(fanout >= 0 && fanout <= 4096, "compact: fanout %d outside [0, 4096]", fanout);
   SGL_REQUIRE(out_ptr != nullptr, "compact: out_ptr is NULL");
+  if (num_queries == 0) return SGL_OK;
+  SGL_REQUIRE(cnt != nullptr, "compact: cnt is NULL");
+  SGL_REQUIRE(fanout == 0 || (pad_nbr && pad_eid && pad_dt && out_nbr && out_eid && out_dt), "compact: NULL array");
+  SGL_REQUIRE(out_ts == nullptr || pad_ts != nullptr, "compact: out_ts needs pad_ts");
+  const size_t tiles = (size_t(num_queries) + kTile - 1) / kTile;
+  SGL_REQUIRE(tiles < size_t(INT_MAX), "compact: too many queries");
+  return SGL_OK;
+}
+
+int compact_run(int64_t num_queries, int32_t fanout, const int32_t *cnt, const int32_t *pad_nbr,
+                const int32_t *pad_eid, const float *pad_dt, const int64_t *pad_ts, int64_t *out_ptr,
+                int32_t *out_nbr, int32_t *out_eid, float *out_dt, int64_t *out_ts, int64_t *tile_sum,
+                int64_t *tile_off, hipStream_t stream) {
   if (num_queries == 0) {
     k_write_zero_ptr<<<1, 1, 0, stream>>>(out_ptr);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
-  SGL_REQUIRE(cnt != nullptr, "compact: cnt is NULL");
-  SGL_REQUIRE(fanout == 0 || (pad_nbr && pad_eid && pad_dt && out_nbr && out_eid && out_dt), "compact: NULL array");
-  SGL_REQUIRE(out_ts == nullptr || pad_ts != nullptr, "compact: out_ts needs pad_ts");
-  const size_t need = sgl_compact_workspace_bytes(num_queries);
-  if (workspace_bytes < need || workspace == nullptr) {
-    sgl::set_error("compact: workspace %zu bytes < required %zu", workspace_bytes, need);
-    return SGL_ERR_WORKSPACE;
-  }
   const size_t tiles = (size_t(num_queries) + kTile - 1) / kTile;
-  SGL_REQUIRE(tiles < size_t(INT_MAX), "compact: too many queries");
-  sgl::Carver c(workspace);
-  int64_t *tile_sum = c.take<int64_t>(tiles);
-  int64_t *tile_off = c.take<int64_t>(tiles);
   k_tile_sums<<<unsigned(tiles), kTile, 0, stream>>>(num_queries, cnt, tile_sum);
   SGL_CHECK_LAUNCH();
   k_scan_tiles<<<1, kScanBlock, 0, stream>>>(int64_t(tiles), tile_sum, tile_off);
@@ -401,4 +403,86 @@ extern "C" int sgl_recent_compact(int64_t num_queries, int32_t fanout,
                                                         pad_dt, pad_ts, out_ptr, out_nbr, out_eid, out_dt, out_ts);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
+}
+
+}  // namespace
+
+extern "C" int sgl_recent_compact(int64_t num_queries, int32_t fanout,
+                                  const int32_t *cnt, const int32_t *pad_nbr,
+                                  const int32_t *pad_eid, const float *pad_dt,
+                                  const int64_t *pad_ts, int64_t *out_ptr,
+                                  int32_t *out_nbr, int32_t *out_eid,
+                                  float *out_dt, int64_t *out_ts,
+                                  void *workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  int rc = compact_checks(num_queries, fanout, cnt, pad_nbr, pad_eid, pad_dt, pad_ts, out_ptr, out_nbr, out_eid,
+                          out_dt, out_ts);
+  if (rc != SGL_OK) return rc;
+  int64_t *tile_sum = nullptr, *tile_off = nullptr;
+  if (num_queries > 0) {
+    const size_t need = sgl_compact_workspace_bytes(num_queries);
+    if (workspace_bytes < need || workspace == nullptr) {
+      sgl::set_error("compact: workspace %zu bytes < required %zu", workspace_bytes, need);
+      return SGL_ERR_WORKSPACE;
+    }
+    const size_t tiles = (size_t(num_queries) + kTile - 1) / kTile;
+    sgl::Carver c(workspace);
+    tile_sum = c.take<int64_t>(tiles);
+    tile_off = c.take<int64_t>(tiles);
+  }
+  return compact_run(num_queries, fanout, cnt, pad_nbr, pad_eid, pad_dt, pad_ts, out_ptr, out_nbr, out_eid, out_dt,
+                     out_ts, tile_sum, tile_off, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free compaction: the tile sums and offsets live in `scratch`, a
+// static device array (each GPU holds its own copy for the life of the
+// process), so a caller that cannot allocate (HIP graph capture, a serving
+// loop) passes only its inputs and outputs. Calls that overlap on one GPU
+// share the array and race.
+static constexpr int64_t kNoAllocTiles = SGL_COMPACT_NOALLOC_MAX_QUERIES / kTile;
+static __device__ __align__(256) int64_t scratch[2 * kNoAllocTiles];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int64_t *g_scratch_dev[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (the
+// host-side name is a stand-in, not a device address).
+int scratch_of_current_device(int64_t **out) {
+  int dev = -1;
+  SGL_CHECK_HIP(hipGetDevice(&dev));
+  SGL_REQUIRE(dev >= 0 && dev < kMaxDevices, "compact_noalloc: device %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void *p = nullptr;
+    SGL_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    SGL_REQUIRE(p != nullptr, "compact_noalloc: no device address for the scratch array on device %d", dev);
+    g_scratch_dev[dev] = static_cast<int64_t *>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return SGL_OK;
+}
+
+}  // namespace
+
+extern "C" int sgl_recent_compact_noalloc(int64_t num_queries, int32_t fanout, const int32_t *cnt,
+                                          const int32_t *pad_nbr, const int32_t *pad_eid, const float *pad_dt,
+                                          const int64_t *pad_ts, int64_t *out_ptr, int32_t *out_nbr,
+                                          int32_t *out_eid, float *out_dt, int64_t *out_ts, hipStream_t stream) {
+  SGL_REQUIRE(num_queries <= SGL_COMPACT_NOALLOC_MAX_QUERIES,
+              "compact_noalloc: %lld queries exceed the static scratch limit of %lld (use sgl_recent_compact)",
+              (long long)num_queries, (long long)SGL_COMPACT_NOALLOC_MAX_QUERIES);
+  int rc = compact_checks(num_queries, fanout, cnt, pad_nbr, pad_eid, pad_dt, pad_ts, out_ptr, out_nbr, out_eid,
+                          out_dt, out_ts);
+  if (rc != SGL_OK) return rc;
+  int64_t *sc = nullptr;
+  if (num_queries > 0) {
+    rc = scratch_of_current_device(&sc);
+    if (rc != SGL_OK) return rc;
+  }
+  return compact_run(num_queries, fanout, cnt, pad_nbr, pad_eid, pad_dt, pad_ts, out_ptr, out_nbr, out_eid, out_dt,
+                     out_ts, sc, sc == nullptr ? nullptr : sc + kNoAllocTiles, stream);
 }

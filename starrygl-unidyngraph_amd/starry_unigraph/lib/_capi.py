@@ -23,6 +23,7 @@ SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
 SGL_FIXED_SHIFT = 40    # fractional bits of the predictor's int64 gradient accumulators
 SGL_DONE_WORDS = 1088   # int32 words of sgl_predictor's completion counter
+SGL_COMPACT_NOALLOC_MAX_QUERIES = 1 << 24   # sgl_recent_compact_noalloc's limit
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -42,6 +43,7 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_compact_workspace_bytes": (_sz, [_i64]),
     "sgl_recent_compact": (ctypes.c_int, [_i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
                                           _vp]),
+    "sgl_recent_compact_noalloc": (ctypes.c_int, [_i64, _i32] + [_vp] * 11),
     "sgl_node_bits_words": (_i64, [_i64]),
     "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 24),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),

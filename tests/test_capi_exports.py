@@ -110,7 +110,7 @@ def test_header_constants_match_binding(tmp_path):
     error bits, fixed-point scale, completion-counter size) are the header's."""
     from starry_unigraph.lib import _capi
     names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
-             "SGL_OP_MAX_ARGS"]
+             "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES"]
     src = tmp_path / "consts.cpp"
     src.write_text('#include <cstdio>\n#include "starrygl_mi355x.h"\nint main() {\n'
                    + "".join(f'  printf("%d ", int({n}));\n' for n in names) + "  return 0;\n}\n")
@@ -119,7 +119,7 @@ def test_header_constants_match_binding(tmp_path):
                     "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_FIXED_SHIFT,
-            _capi.SGL_DONE_WORDS, _capi.SGL_OP_MAX_ARGS]
+            _capi.SGL_DONE_WORDS, _capi.SGL_OP_MAX_ARGS, _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES]
     assert got == want
 
 
