@@ -125,6 +125,7 @@ def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -
     avg_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     alg = sampler_bytes(deg[nodes], head.cnt)
     traffic = HBM_TRAFFIC.get(("cfg3", "recent_sample"))
+    traffic_src = TRAFFIC_SOURCE["cfg3"] if traffic else None
     # diagnostics: the probe-free (compulsory) bytes, and the counter-measured bytes over the same time
     compulsory = float((12 + 16 + 28 * head.cnt.double() + 4).sum().item())
     out = {"value": nq * steps / wall / 1e6, "unit": "Mqueries/s", "ms_per_pass": wall * 1e3 / steps,
@@ -132,7 +133,7 @@ def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -
            "roofline": {"bound": "hbm", "kernel": "k_recent_padded", "kernel_avg_ms": avg_ms,
                         "alg_bytes_per_launch": alg, "achieved": alg / (avg_ms * 1e-3) / 1e9,
                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": alg / (avg_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                        "traffic": traffic,
+                        "traffic": traffic, "traffic_source": traffic_src,
                         "compulsory_bytes_per_launch": compulsory,
                         "traffic_rate_GBps": traffic / (avg_ms * 1e-3) / 1e9 if traffic else None}}
     del head
@@ -346,8 +347,13 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
         del step
         torch.cuda.empty_cache()
     big = cases[str(max(batches))]
-    gb = sum(big["kernels"][n]["alg_bytes"] for n in ("memory_commit", "edge_rows"))
-    us = sum(big["kernels"][n]["avg_us"] for n in ("memory_commit", "edge_rows"))
+    # the gather / scatter path of a step: the fused GRU + mailbox kernel (bf16 GEMMs, config 5's setting:
+    # memory and mailbox rows gathered, messages scattered), the memory commit and the edge-row gather
+    gs_names = ("memory_update_bf16", "memory_commit", "edge_rows")
+    gb = sum(big["kernels"][n]["alg_bytes"] for n in gs_names)
+    us = sum(big["kernels"][n]["avg_us"] for n in gs_names)
+    gb2 = sum(big["kernels"][n]["alg_bytes"] for n in ("memory_commit", "edge_rows"))
+    us2 = sum(big["kernels"][n]["avg_us"] for n in ("memory_commit", "edge_rows"))
     # the fused GRU + mailbox kernel is MFMA-bound at this state: 6DS K + 6D^2 (K-1) + 12D^2 flops per root
     gru_flop = big["mean_roots"] * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
     gru_tf = gru_flop / (big["kernels"]["memory_update"]["avg_us"] * 1e-6) / 1e12
@@ -355,10 +361,15 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     return {"value": gb / (us * 1e-6) / 1e9, "unit": "GB/s",
             "workload": f"gather/scatter: cfg5 state (N={N}, D={D}, K={K}, F={F}), k={k}, batches {list(batches)}",
             "cases": cases,
-            "roofline": {"bound": "hbm", "kernel": "k_memory_commit + k_edge_rows", "batch": max(batches),
+            "roofline": {"bound": "hbm", "kernel": "k_gru_mailbox<bf16> + k_memory_commit + k_edge_rows",
+                         "batch": max(batches), "alg_bytes_per_launch": gb,
                          "achieved": gb / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                         "traffic": GS_TRAFFIC_1M if max(batches) == 1 << 20 else None},
+                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                         "copy_kernels_only": {"kernel": "k_memory_commit + k_edge_rows",
+                                               "achieved": gb2 / (us2 * 1e-6) / 1e9,
+                                               "frac": gb2 / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                               "traffic": GS_TRAFFIC_1M if max(batches) == 1 << 20 else None,
+                                               "traffic_source": "profiles/gather_scatter_cfg5_B1M.md"}},
             "gru_mfma": {"kernel": "k_gru_mailbox<float>", "batch": max(batches), "flop_per_launch": round(gru_flop),
                          "achieved": gru_tf, "peak": 157.3, "unit": "TFLOP/s", "frac": gru_tf / 157.3},
             "gru_mfma_bf16": {"kernel": "k_gru_mailbox<uint16_t> (bf16 GEMMs, fp32 accumulation)",
@@ -394,7 +405,9 @@ def build_session(wl: dict, stream):
 
 class Epochs:
     """Training batches in order, epoch after epoch (memory is never reset
-    between epochs, as in the reference); negatives drawn per epoch."""
+    between epochs, as in the reference). The runtime draws each batch's
+    negatives inside its train_step (a few consecutive batches per CPU draw),
+    so the draws fall inside the timed region."""
 
     def __init__(self, rt, B):
         self.rt, self.B = rt, B
@@ -403,7 +416,6 @@ class Epochs:
     def next(self):
         while True:
             if self._it is None:
-                self.rt.precompute_negatives("train", self.B)
                 self._it = iter(self.rt.iter_batches("train", self.B))
             try:
                 return next(self._it)
@@ -442,6 +454,8 @@ HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 1133.4 + 1504.5) * 1024),
                ("cfg4", "predictor"): round((2 * 564.4 + 1006.8) * 1024),
                ("cfg4", "param_update"): round((2 * 8017.6 + 2070.6) * 1024),
                ("cfg3", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
+# the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
+TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
 
 # step stage name -> the C-ABI entry point that launches it
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
@@ -450,35 +464,70 @@ ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_rece
                 "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam"}
 
 
-def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float]:
-    """Algorithmic work of one launch: ("hbm", bytes) or ("mfma", flops)."""
+def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float, float]:
+    """Work of one launch: (bound, algorithmic, executed) -- ("hbm", bytes,
+    bytes) or ("mfma", flops, flops). The attention's algorithmic flops are
+    the reference algorithm's (per-edge K / V projections):
+    2U(D+T)D + 4E(D+F+T)D + 4UD^2 forward and twice that backward; the
+    executed count is what the re-associated kernels do (K / V projected
+    per root, q~ = W_k^T q per head)."""
     D, F, T, H, k, K = wl["D"], dims.F, wl["T"], wl["H"], wl["k"], wl["K"]
     C = D + F + T
     S = 2 * D + F
+    fwd_alg = float(U) * (2 * (D + T) * D + 4 * D * D) + float(E) * 4 * C * D
     if name == "memory_update":
         # GRU over K slots + GRUCell per updated root
-        return "mfma", float(U) * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
+        f = float(U) * (6 * D * S * K + 6 * D * D * (K - 1) + 12 * D * D)
+        return "mfma", f, f
     if name == "conv_forward":
-        # Q (2D*D), qt (2D*C), per edge 4HC (scores + weighted sum), agg (2CD), z (4D*D)
-        return "mfma", float(U) * (2 * D * D + 2 * D * C + 2 * C * D + 4 * D * D) + float(E) * 4 * H * C
+        # executed: Q (2D(D+T)), qt (2DC), per edge 4HC (scores + weighted sum), agg (2CD), z (4D*D)
+        return "mfma", fwd_alg, float(U) * (2 * D * (D + T) + 2 * D * C + 2 * C * D + 4 * D * D) + float(E) * 4 * H * C
     if name == "conv_backward":
-        # dL/dy from the predictor rows (4D*D), gagg (2D*D), gxbar (2D*C), per edge 8HC, gQ (2CD)
-        return "mfma", float(U) * (4 * D * D + 2 * D * D + 2 * D * C + 2 * C * D) + float(E) * 8 * H * C
+        # executed: dL/dy from the predictor rows (4D*D), gagg (2D*D), gxbar (2D*C), per edge 8HC, gQ (2CD)
+        return "mfma", 2 * fwd_alg, float(U) * (4 * D * D + 2 * D * D + 2 * D * C + 2 * C * D) + float(E) * 8 * H * C
+    if name == "predictor":
+        # per event: src_fc, dst_fc (positive and negative) 6D^2, out_fc and the logit gradients 12D
+        f = float(B) * (6 * D * D + 12 * D)
+        return "mfma", f, f
     if name == "param_update":
         # weight-gradient reductions over the roots: w_q (D x (D+T)), w_k, w_v (D x C), w_out (D x 2D),
         # src_fc / dst_fc (D x D over U + 1 rows); 2 flops per multiply-add
-        return "mfma", float(U) * 2 * (D * (D + T) + 2 * D * C + 2 * D * D) + float(U + 1) * 2 * 2 * D * D
+        f = float(U) * 2 * (D * (D + T) + 2 * D * C + 2 * D * D) + float(U + 1) * 2 * 2 * D * D
+        return "mfma", f, f
     if name == "memory_commit":
-        return "hbm", float(U) * (8 + 4 * D * 2 + 4)
-    if name == "edge_rows":
+        b = float(U) * (8 + 4 * D * 2 + 4)
+    elif name == "edge_rows":
         # per sampled edge: nbr, eid read, the memory row and edge feature gathered and written into the
         # edge's row; per root its count
-        return "hbm", float(E) * (8 + 8 * D + 8 * F) + float(U) * 4
-    if name == "recent_sample":
-        return "hbm", float(U) * (12 + 16 + 8 * 8 + 4) + float(E) * 28
-    if name == "batch_prepare":
-        return "hbm", float(B) * (8 + 8 + 8 + 4) + float(U) * 8
-    return "hbm", 0.0
+        b = float(E) * (8 + 8 * D + 8 * F) + float(U) * 4
+    elif name == "recent_sample":
+        b = float(U) * (12 + 16 + 8 * 8 + 4) + float(E) * 28
+    elif name == "batch_prepare":
+        b = float(B) * (8 + 8 + 8 + 4) + float(U) * 8
+    else:
+        b = 0.0
+    return "hbm", b, b
+
+
+def copy_bandwidth(mib: int = 2048, reps: int = 10) -> dict:
+    """A device-to-device copy of a known size (read + write), the measured
+    HBM bandwidth the roofline fractions can also be read against."""
+    import torch
+    n = mib * (1 << 18)
+    a = torch.ones(n, device="cuda")
+    b = torch.empty_like(a)
+    b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del a, b
+    torch.cuda.empty_cache()
+    return {"GBps": 2 * n * 4 / (ms * 1e-3) / 1e9, "bytes_per_copy": 2 * n * 4, "ms": ms,
+            "kernel": "torch copy_ (device to device)"}
 
 
 def run_tgn(args, wl: dict) -> dict:
@@ -504,7 +553,6 @@ def run_tgn(args, wl: dict) -> dict:
 
     batches = [ep.next() for _ in range(args.steps)]
     snap = _snapshot(rt)
-    neg_state = dict(rt._neg_queue)
     dom = args.roofline_kernel
     timer: list = []
     if args.no_plans:   # eager steps: time the dominant kernel inside the timed region
@@ -550,7 +598,6 @@ def run_tgn(args, wl: dict) -> dict:
 
     # replay the same steps eagerly with every library call timed + per-step counts
     _restore(rt, snap)
-    rt._neg_queue = dict(neg_state)
     for st in rt.steps:
         st.timer, st.timed = timer, None
     timer.clear()
@@ -568,12 +615,12 @@ def run_tgn(args, wl: dict) -> dict:
     for n0, n1, U, E, B in per_step:
         for name, a, b in timer[n0:n1]:
             agg.setdefault(name, []).append(a.elapsed_time(b))
-            work.setdefault(name, []).append(kernel_work(name, wl, U, E, B, rt.dims)[1])
+            work.setdefault(name, []).append(kernel_work(name, wl, U, E, B, rt.dims)[1:])
     breakdown = {}
     for name, ms in agg.items():
         avg = sum(ms) / len(ms)
         bound = kernel_work(name, wl, 1, 1, 1, rt.dims)[0]
-        wavg = sum(work[name]) / len(work[name])
+        wavg = sum(w[0] for w in work[name]) / len(work[name])
         if bound == "mfma":
             ach, peak, unit = wavg / (avg * 1e-3) / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
         else:
@@ -587,17 +634,23 @@ def run_tgn(args, wl: dict) -> dict:
         dom_ms = agg[dom]
     dom_avg = sum(dom_ms) / max(1, len(dom_ms))
     bound = kernel_work(dom, wl, 1, 1, 1, rt.dims)[0]
-    dwork = sum(work[dom]) / len(work[dom])
-    if bound == "mfma":
-        ach, peak, unit = dwork / (dom_avg * 1e-3) / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
-    else:
-        ach, peak, unit = dwork / (dom_avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+    dwork = sum(w[0] for w in work[dom]) / len(work[dom])
+    dexec = sum(w[1] for w in work[dom]) / len(work[dom])
+    scale = 1e12 if bound == "mfma" else 1e9
+    peak, unit = (FP32_PEAK_TFLOPS, "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
+    ach = dwork / (dom_avg * 1e-3) / scale
     res = {
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
         "final_train_loss": final_loss,
         "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "traffic": HBM_TRAFFIC.get((wl["config"], dom)), "kernel_avg_ms": dom_avg,
-                     "work_per_launch": dwork},
+                     "frac": ach / peak, "traffic": HBM_TRAFFIC.get((wl["config"], dom)),
+                     "traffic_source": TRAFFIC_SOURCE.get(wl["config"]) if (wl["config"], dom) in HBM_TRAFFIC
+                     else None,
+                     "kernel_avg_ms": dom_avg, "work_per_launch": dwork,
+                     "work_formula": "SURVEY 8(d) attention projections: 2U(D+T)D + 4E(D+F+T)D + 4UD^2 "
+                                     "(x2 backward)" if dom.startswith("conv_") else "see kernel_work()",
+                     "work_executed_per_launch": dexec,
+                     "frac_executed": dexec / (dom_avg * 1e-3) / scale / peak},
         "kernels": breakdown,
         "step_shape": {"mean_roots": round(mean_U, 1), "mean_sampled_edges": round(mean_E, 1)},
     }
@@ -738,8 +791,9 @@ def main() -> None:
                         "global_batch": wl["B"], "parallelism": "single GPU"},
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
                 step_shape=r["step_shape"], final_train_loss=r["final_train_loss"])
+    line["hbm_copy"] = copy_bandwidth()
     if args.workload == "tgn-large" and not args.no_sampler:
-        line["sampler"] = run_sampler(20, 3, cases=False, cpu=not args.no_cpu)
+        line["sampler"] = run_sampler(20, 3, cases=True, cpu=not args.no_cpu)
     if args.workload == "tgn-large" and not args.no_gather_scatter:
         gs = run_gather_scatter(5, 1)
         line["gather_scatter"] = {k: gs[k] for k in ("value", "unit", "workload", "roofline", "gru_mfma",

@@ -173,6 +173,16 @@ int sgl_recent_compact_noalloc(int64_t num_queries, int32_t fanout,
  * indices e above are relative to the batch start.
  * ------------------------------------------------------------------------- */
 int64_t sgl_node_bits_words(int64_t num_nodes);
+/* Negative destinations from uniform draws. Replaces the lookup and the
+ * collision rule of CTDGOnlineRuntime._negative_sample
+ * (backends/ctdg/runtime/runtime.py:124-136) after its torch.randint draw:
+ * neg[e] = pool[draw[e]], and when that equals dst[e], pool[(draw[e] + 1)
+ * mod pool_size] instead (once, as there). pool is the sorted unique dst
+ * pool; draws outside [0, pool_size) set SGL_DERR_NODE_RANGE. draw and neg
+ * may be the same array. */
+int sgl_negatives_from_draws(int64_t n, const int64_t *draw, const int64_t *pool,
+                             int64_t pool_size, const int64_t *dst, int64_t *neg,
+                             int32_t *err_flag, hipStream_t stream);
 int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
                       const int64_t *dst, const int64_t *neg, const float *ts,
                       int64_t *cursor, int64_t *batch_start, uint32_t *node_bits, int32_t *word_prefix,

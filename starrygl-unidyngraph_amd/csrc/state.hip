@@ -664,7 +664,41 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
   }
 }
 
+// Negative destinations from uniform draws over the sorted dst pool
+// (runtime.py:124-136): neg = pool[i]; when it equals the event's dst the
+// draw moves to the next pool entry (once, as there). In place: draw and neg
+// may be the same array (each element is read, then written by one thread).
+__global__ __launch_bounds__(kBlock) void k_negatives(int64_t n, const int64_t *draw, const int64_t *__restrict__ pool,
+                                                      int64_t pool_size, const int64_t *__restrict__ dst,
+                                                      int64_t *neg, int32_t *__restrict__ err) {
+  for (int64_t e = int64_t(blockIdx.x) * kBlock + threadIdx.x; e < n; e += int64_t(gridDim.x) * kBlock) {
+    int64_t i = draw[e];
+    if (i < 0 || i >= pool_size) {
+      if (err != nullptr) atomicOr(err, SGL_DERR_NODE_RANGE);
+      i = 0;
+    }
+    int64_t v = pool[i];
+    if (v == dst[e]) {
+      i = i + 1 == pool_size ? 0 : i + 1;
+      v = pool[i];
+    }
+    neg[e] = v;
+  }
+}
+
 }  // namespace
+
+extern "C" int sgl_negatives_from_draws(int64_t n, const int64_t *draw, const int64_t *pool, int64_t pool_size,
+                                        const int64_t *dst, int64_t *neg, int32_t *err_flag, hipStream_t stream) {
+  SGL_REQUIRE(n >= 0, "negatives: n < 0");
+  if (n == 0) return SGL_OK;
+  SGL_REQUIRE(pool_size > 0, "negatives: empty dst pool");
+  SGL_REQUIRE(draw && pool && dst && neg, "negatives: NULL array");
+  const unsigned grid = unsigned(std::min<int64_t>((n + kBlock - 1) / kBlock, sgl::kMaxGrid));
+  k_negatives<<<grid, kBlock, 0, stream>>>(n, draw, pool, pool_size, dst, neg, err_flag);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
 
 extern "C" int64_t sgl_node_bits_words(int64_t num_nodes) {
   return num_nodes > 0 ? bitmap_words(num_nodes) + summary_words(num_nodes) : 0;

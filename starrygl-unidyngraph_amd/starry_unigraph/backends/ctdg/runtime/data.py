@@ -108,8 +108,10 @@ class TGTemporalDataset:
                                     ts=self.ts[ev], edge_feat=self.edge_feat[ev])
             else:  # splits are contiguous event ranges: views, no copies
                 a, b = base + start, base + start + ev.numel()
-                yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[a:b], dst=self.dst[a:b],
-                                    ts=self.ts[a:b], edge_feat=self.edge_feat[a:b])
+                batch = CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[a:b], dst=self.dst[a:b],
+                                      ts=self.ts[a:b], edge_feat=self.edge_feat[a:b])
+                batch.__dict__["_start"] = a   # contiguous by construction (CTDGDataBatch.start)
+                yield batch
 
     def sampler_graph(self, split: str) -> dict[str, torch.Tensor]:
         """data.py:196-231: train = [0, train_end); val = [0, val_end);

@@ -81,8 +81,12 @@ class CTDGOnlineRuntime:
         # negatives are drawn inside the step, for neg_chunk consecutive
         # batches of a contiguous split at a time (1: one draw per step);
         # _neg_ahead[split] = (next unconsumed event, end of the drawn range)
-        self.neg_chunk = 32
+        self.neg_chunk = 8
         self._neg_ahead: dict[str, tuple[int, int]] = {}
+        self._draw_host: torch.Tensor | None = None   # pinned staging of the draws
+        self._draw_done = None                         # event: the last copy out of it
+        self._pool_dev: torch.Tensor | None = None
+        self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
         conv = core.conv
         self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head,
@@ -146,6 +150,7 @@ class CTDGOnlineRuntime:
         if self._front_stream is not None and int(self._sync[48].item()):
             raise RuntimeError("sgl_plan_run: a cross-stream wait timed out; the steps since the last check "
                                "ran out of order")
+        self._neg_err.raise_if_set("negative sampling (a draw outside the dst pool)")
 
     def _pipeline_streams(self):
         if self._front_stream is None:
@@ -240,16 +245,35 @@ class CTDGOnlineRuntime:
         ids = self.dataset.split_event_ids("test" if batch.split == "predict" else batch.split)
         end = int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
         hi = max(s + n, min(end, s + self.neg_chunk * n))
+        m = hi - s
         pool = self._dst_pool()
-        idx = torch.randint(low=0, high=pool.numel(), size=(hi - s,), dtype=torch.long)
-        neg = pool[idx]
-        col = neg.eq(self.dataset.dst[s:hi])
-        if col.any():
-            idx[col] = (idx[col] + 1) % pool.numel()
-            neg = pool[idx]
-        self._neg_all[s:hi].copy_(neg.pin_memory(), non_blocking=True)
+        if self._draw_host is None or self._draw_host.numel() < m:
+            self._draw_host = torch.empty(max(m, self.neg_chunk * n), dtype=torch.long, pin_memory=True)
+            self._draw_done = None
+        elif self._draw_done is not None:
+            self._draw_done.synchronize()   # the last copy out of the staging buffer (long finished)
+        host = self._draw_host[:m]
+        # the draw itself on the CPU generator; the lookup and the collision
+        # rule on the device (sgl_negatives_from_draws), in place
+        torch.randint(low=0, high=pool.numel(), size=(m,), dtype=torch.long, out=host)
+        if self._pool_dev is None:
+            self._pool_dev = pool.to(self.device)
+        front = self._front_stream
+        stream = front if front is not None else torch.cuda.current_stream(self.device)
+        # on the front stream, where the batch preparations read them; the
+        # current stream (eager steps) orders itself after it too
+        with torch.cuda.stream(stream):
+            out = self._neg_all[s:hi]
+            out.copy_(host, non_blocking=True)
+            self._draw_done = torch.cuda.Event()
+            self._draw_done.record(stream)
+            P = _capi.ptr
+            _capi.check(_capi.call("sgl_negatives_from_draws", m, P(out), P(self._pool_dev), self._pool_dev.numel(),
+                                   P(self._dev["dst"][s:hi]), P(out), P(self._neg_err.t), stream.cuda_stream),
+                        "sgl_negatives_from_draws")
+        if front is not None:
+            torch.cuda.current_stream(self.device).wait_stream(front)
         self._neg_ahead[batch.split] = (s, hi)
-        self.fence()   # the batch preparations read them on the other stream
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev

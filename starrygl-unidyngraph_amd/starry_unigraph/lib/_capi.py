@@ -45,6 +45,7 @@ SIGNATURES: dict[str, tuple] = {
                                           _vp]),
     "sgl_recent_compact_noalloc": (ctypes.c_int, [_i64, _i32] + [_vp] * 11),
     "sgl_node_bits_words": (_i64, [_i64]),
+    "sgl_negatives_from_draws": (ctypes.c_int, [_i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 24),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
