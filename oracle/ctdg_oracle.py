@@ -46,6 +46,11 @@ class TimeEncodeO(nn.Module):
         self.w.bias = nn.Parameter(torch.zeros(dim))
         self.w.weight = nn.Parameter((1.0 / 10 ** torch.linspace(0, 9, dim)).reshape(dim, 1))
 
+    # float64 copies only: keep the float32 rounding of the argument (its
+    # value), with the exact derivative of t*w + b (tests that compare float32
+    # gradients against float64 sums of the same float32 algorithm)
+    round_arg_f32 = False
+
     def forward(self, t: torch.Tensor) -> torch.Tensor:
         # The reference evaluates nn.Linear(1, T); a GPU GEMM with a bias
         # epilogue rounds the product, then adds the bias. CPU BLAS picks a fused
@@ -53,7 +58,12 @@ class TimeEncodeO(nn.Module):
         # two-rounding form elementwise. (t.float() in the reference; the
         # parameter dtype here so that a float64 copy can be checked in float64.)
         tt = t.to(self.w.weight.dtype).reshape(-1, 1)
-        return torch.cos(tt * self.w.weight.reshape(1, -1) + self.w.bias).reshape(*t.shape, self.dim)
+        arg = tt * self.w.weight.reshape(1, -1) + self.w.bias
+        if self.round_arg_f32 and arg.dtype == torch.float64:
+            with torch.no_grad():
+                a32 = (tt.float() * self.w.weight.float().reshape(1, -1)) + self.w.bias.float()
+            arg = arg + (a32.double() - arg).detach()
+        return torch.cos(arg).reshape(*t.shape, self.dim)
 
 
 class TemporalConvO(nn.Module):

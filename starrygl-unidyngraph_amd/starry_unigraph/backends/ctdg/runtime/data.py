@@ -8,6 +8,7 @@ from dataclasses import dataclass
 from pathlib import Path
 from typing import Iterator
 
+import numpy as np
 import torch
 
 from starry_unigraph.data import RawTemporalEvents, load_raw_temporal_events
@@ -68,8 +69,10 @@ class TGTemporalDataset:
         self.num_edges = int(raw.num_edges)
         self.edge_feat = raw.edge_feat.float()
         self.edge_feat_dim = int(self.edge_feat.size(-1))
-        self.node_temporal_features = None
-        self.node_feat_dim = 0
+        self.node_temporal_features = getattr(raw, "node_temporal_features", None)
+        nf = self.node_temporal_features
+        self.node_feat_dim = 0 if nf is None else nf.dim
+        self._node_hist = self._build_node_feat_history()
         self.split_ratio = normalize_split_ratio(cfg["data"].get("split_ratio"))
         self._split_cache: dict[str, torch.Tensor] = {}
         self._sampler_cache: dict[str, dict[str, torch.Tensor]] = {}
@@ -90,8 +93,45 @@ class TGTemporalDataset:
             ids = self._split_cache[split] = torch.arange(a, b, dtype=torch.long)
         return ids
 
-    def lookup_node_features(self, node_ids, ts):
-        return None
+    def _build_node_feat_history(self):
+        """data.py:128-140: each node's feature rows in time order (rows of a
+        node with equal times keep their order in the time-sorted table), as
+        one array sorted by (node, time)."""
+        nf = self.node_temporal_features
+        if nf is None or nf.size == 0 or nf.dim == 0:
+            return None
+        ids, ts = nf.node_ids.numpy(), nf.ts.float().numpy()
+        order = np.lexsort((ts, ids))   # stable: node, then time
+        return ids[order], ts[order], nf.values.float()[torch.from_numpy(order)]
+
+    def lookup_node_features(self, node_ids: torch.Tensor, ts: torch.Tensor) -> torch.Tensor | None:
+        """data.py:142-157: for each (node, t) the node's latest feature row
+        with time <= t (the last of equal times), zeros when it has none;
+        None without node features."""
+        if self.node_feat_dim <= 0 or self._node_hist is None:
+            return None
+        h_ids, h_ts, h_vals = self._node_hist
+        q = node_ids.long().numpy()
+        t = ts.float().numpy()
+        lo = np.searchsorted(h_ids, q, side="left")
+        hi = np.searchsorted(h_ids, q, side="right")
+        # upper_bound of t inside [lo, hi), all queries at once
+        a, b = lo.copy(), hi.copy()
+        while True:
+            act = a < b
+            if not act.any():
+                break
+            mid = (a + b) // 2
+            le = np.zeros_like(act)
+            le[act] = h_ts[mid[act]] <= t[act]
+            a = np.where(act & le, mid + 1, a)
+            b = np.where(act & ~le, mid, b)
+        idx = a - 1
+        out = torch.zeros(q.size, self.node_feat_dim, dtype=torch.float32)
+        hit = idx >= lo
+        if hit.any():
+            out[torch.from_numpy(np.nonzero(hit)[0])] = h_vals[torch.from_numpy(idx[hit])]
+        return out
 
     def iter_batches(self, split: str, batch_size: int) -> Iterator[CTDGDataBatch]:
         """data.py:161-194: consecutive slices of the split."""
@@ -104,12 +144,16 @@ class TGTemporalDataset:
             ev = ids[start:start + step]
             if sharded:
                 ev = ev[self.edge_parts[ev] == self.partition_rank]
-                yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[ev], dst=self.dst[ev],
-                                    ts=self.ts[ev], edge_feat=self.edge_feat[ev])
+                s, d, t = self.src[ev], self.dst[ev], self.ts[ev]
+                yield CTDGDataBatch(index=bi, split=split, event_ids=ev, src=s, dst=d, ts=t,
+                                    edge_feat=self.edge_feat[ev], src_node_feat=self.lookup_node_features(s, t),
+                                    dst_node_feat=self.lookup_node_features(d, t))
             else:  # splits are contiguous event ranges: views, no copies
                 a, b = base + start, base + start + ev.numel()
-                batch = CTDGDataBatch(index=bi, split=split, event_ids=ev, src=self.src[a:b], dst=self.dst[a:b],
-                                      ts=self.ts[a:b], edge_feat=self.edge_feat[a:b])
+                s, d, t = self.src[a:b], self.dst[a:b], self.ts[a:b]
+                batch = CTDGDataBatch(index=bi, split=split, event_ids=ev, src=s, dst=d, ts=t,
+                                      edge_feat=self.edge_feat[a:b], src_node_feat=self.lookup_node_features(s, t),
+                                      dst_node_feat=self.lookup_node_features(d, t))
                 batch.__dict__["_start"] = a   # contiguous by construction (CTDGDataBatch.start)
                 yield batch
 

@@ -29,14 +29,9 @@ from starry_unigraph.native.step import ConvDims, DeviceStep, FusedAdam, StepPar
 
 from .data import CTDGDataBatch, TGTemporalDataset
 from .memory import CTDGMemoryBank
+from .metrics import link_metrics
 from .models import CTDGMemoryUpdater
 from .sampler import NativeTemporalSampler
-
-try:
-    from sklearn.metrics import average_precision_score, roc_auc_score
-except Exception:  # pragma: no cover
-    average_precision_score = None
-    roc_auc_score = None
 
 
 @dataclass
@@ -450,18 +445,9 @@ class CTDGOnlineRuntime:
         return upd
 
     def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
-        """runtime.py:202-214."""
-        pp = torch.sigmoid(pos_logits).detach().cpu()
-        pn = torch.sigmoid(neg_logits).detach().cpu()
-        scores = torch.cat([pp, pn]).numpy()
-        labels = torch.cat([torch.ones_like(pp), torch.zeros_like(pn)]).numpy()
-        m: dict[str, float] = {}
-        if average_precision_score is not None:
-            m["ap"] = float(average_precision_score(labels, scores))
-        if roc_auc_score is not None:
-            m["auc"] = float(roc_auc_score(labels, scores))
-        m["mrr"] = float((pp.unsqueeze(1) > pn.unsqueeze(0)).float().mean().item())
-        return m
+        """runtime.py:202-214 (AP, AUC and the pairwise "mrr"), computed on
+        the logits' device (metrics.link_metrics)."""
+        return link_metrics(pos_logits, neg_logits)
 
     def _sample_meta(self, n: int) -> dict[str, int]:
         """CTDGSampleOutput.describe() (sampler.py:27-33, sampler.py:119-120):

@@ -1,0 +1,125 @@
+"""Session-level behaviour on the GPU: the checkpoint round trip of
+CTDGSession (backends/ctdg/runtime/session.py:78-93: model + updater state
+dicts, strict loading), a load queued between asynchronous steps, and the
+step's metric dict computed on the device against scikit-learn."""
+import numpy as np
+import pytest
+import torch
+
+import ctdg_oracle as co
+
+pytestmark = pytest.mark.gpu
+
+
+def _session(seed, B=200):
+    from starry_unigraph import SchedulerSession, synth
+    from starry_unigraph.data import from_stream
+    s = synth.bipartite_stream(num_src=300, num_dst=60, num_events=6000, edge_dim=16, seed=3)
+    cfg = {"model": {"family": "tgn", "hidden_dim": 32}, "data": {"name": "ckpt", "format": "synthetic"},
+           "train": {"batch_size": B, "lr": 1e-3}, "runtime": {"device": "cuda"},
+           "ctdg": {"mailbox_slots": 2, "dim_time": 16, "num_head": 2, "dropout": 0.0, "att_dropout": 0.0},
+           "sampling": {"neighbor_limit": [10], "history": 1, "strategy": "recent"}}
+    torch.manual_seed(seed)
+    sess = SchedulerSession.from_config(cfg).with_events(from_stream(s))
+    sess.build_runtime()
+    return sess.ctdg_session
+
+
+def test_checkpoint_round_trip(gpu, tmp_path):
+    """Save after training steps; a session built with other initial weights
+    loads it and then has bit-identical model and updater weights, and from
+    the same node state and negatives its next eval step is bit-identical."""
+    a, b = _session(0), _session(99)
+    rta, rtb = a.online_runtime, b.online_runtime
+    for batch in list(rta.iter_batches("train", 200))[:4]:
+        a.train_step(batch)
+    path = tmp_path / "ck.pt"
+    a.save_checkpoint(path)
+    b.load_checkpoint(path)
+    for (n, p), (_, q) in zip(rta.model.state_dict().items(), rtb.model.state_dict().items()):
+        assert torch.equal(p, q), n
+    for (n, p), (_, q) in zip(rta.memory_updater.state_dict().items(), rtb.memory_updater.state_dict().items()):
+        assert torch.equal(p, q), n
+    sa, sb = rta.memory.state, rtb.memory.state
+    for name in ("memory", "mailbox", "mailbox_ts", "memory_ts", "next_mail_pos"):
+        getattr(sb, name).copy_(getattr(sa, name))
+    sb.touched()
+    batch = list(rta.iter_batches("val", 200))[2]
+    neg = co.negative_sample(rta.dataset.dst.unique(), batch.dst, torch.Generator().manual_seed(4)).to(gpu)
+    outs = []
+    for rt in (rta, rtb):
+        rt._neg_queue["val"] = (neg, 0)
+        outs.append(rt.eval_step(batch, "val"))
+    assert outs[0]["loss"] == outs[1]["loss"]
+    assert outs[0]["predictions"] == outs[1]["predictions"]
+    assert outs[0]["meta"]["metrics"] == outs[1]["meta"]["metrics"]
+
+
+def test_checkpoint_loading_is_strict(gpu, tmp_path):
+    """Missing keys, unexpected keys and shape mismatches raise, as
+    nn.Module.load_state_dict does; the weights stay untouched."""
+    a = _session(0)
+    rt = a.online_runtime
+    path = tmp_path / "ck.pt"
+    a.save_checkpoint(path)
+    ck = torch.load(path, weights_only=True)
+    before = [p.clone() for p in rt.model.parameters()]
+    bad = []
+    m = dict(ck["model"])
+    m.pop("src_fc.bias")
+    bad.append(("Missing key", m))
+    m = dict(ck["model"], extra=torch.zeros(1))
+    bad.append(("Unexpected key", m))
+    m = dict(ck["model"])
+    m["out_fc.weight"] = torch.zeros(2, 32)
+    bad.append(("size mismatch", m))
+    for what, m in bad:
+        p = tmp_path / "bad.pt"
+        torch.save({"model": m, "memory_updater": ck["memory_updater"]}, p)
+        with pytest.raises(RuntimeError, match=what):
+            a.load_checkpoint(p)
+        for x, y in zip(before, rt.model.parameters()):
+            assert torch.equal(x, y)
+
+
+def test_load_between_async_steps_is_ordered(gpu, tmp_path):
+    """A checkpoint loaded right after asynchronous (pipelined) steps, with no
+    synchronisation, takes effect exactly as if the device had been
+    synchronised first: two identical runs end bit-identical."""
+    src = _session(5)
+    for batch in list(src.online_runtime.iter_batches("train", 200))[:3]:
+        src.train_step(batch)
+    path = tmp_path / "w.pt"
+    src.save_checkpoint(path)
+    runs = []
+    for sync_first in (False, True):
+        s = _session(0)
+        rt = s.online_runtime
+        rt.collect_results = False
+        batches = list(rt.iter_batches("train", 200))
+        torch.manual_seed(8)
+        for batch in batches[:3]:
+            rt.train_step(batch)
+        if sync_first:
+            torch.cuda.synchronize()
+        s.load_checkpoint(path)
+        for batch in batches[3:6]:
+            rt.train_step(batch)
+        torch.cuda.synchronize()
+        rt.check_sync()
+        runs.append([t.detach().clone() for t in (rt.optimizer.inner.flat, rt.memory.state.memory,
+                                                   rt.memory.state.mailbox)])
+    for x, y in zip(*runs):
+        assert torch.equal(x, y)
+
+
+def test_device_metrics_match_sklearn(gpu):
+    from starry_unigraph.backends.ctdg.runtime.metrics import link_metrics
+    rng = np.random.default_rng(3)
+    pos = torch.from_numpy(rng.normal(0.2, 1.5, 4000).astype(np.float32))
+    neg = torch.from_numpy(rng.normal(-0.2, 1.5, 4000).astype(np.float32))
+    pos[:500] = neg[:500]
+    got = link_metrics(pos.to(gpu), neg.to(gpu))
+    want = co.metric_dict(pos, neg)
+    for k, tol in (("ap", 1e-9), ("auc", 1e-9), ("mrr", 1e-6)):
+        assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])

@@ -343,3 +343,21 @@ def test_metric_dict_matches_definitions(seed):
     want = _brute_metrics(pos, neg)
     for k, tol in (("ap", 1e-9), ("auc", 1e-9), ("mrr", 1e-6)):   # "mrr" is a float32 mean
         assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_product_metrics_match_sklearn(seed):
+    """The runtime's metric dict (metrics.link_metrics, sorts on the logits'
+    device; here the CPU) against the oracle's scikit-learn metric_dict,
+    with ties within and across the classes."""
+    from starry_unigraph.backends.ctdg.runtime.metrics import link_metrics
+    rng = np.random.default_rng(seed)
+    pos = torch.from_numpy(rng.normal(0.3, 1.0, 257).astype(np.float32))
+    neg = torch.from_numpy(rng.normal(-0.1, 1.0, 257).astype(np.float32))
+    pos[:30] = neg[:30]
+    neg[30:40] = neg[40]
+    pos[50:60] = 40.0
+    got = link_metrics(pos, neg)
+    want = co.metric_dict(pos, neg)
+    for k, tol in (("ap", 1e-9), ("auc", 1e-9), ("mrr", 1e-6)):   # the reference's "mrr" is a float32 mean
+        assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])
