@@ -13,7 +13,8 @@
  *     outside the declared extents, whatever the ids say.
  *   - Scratch memory is supplied by the caller as `workspace` of at least the
  *     size returned by the matching *_workspace_bytes() query.
- *   - The library allocates no device memory of its own.
+ *   - The library allocates no device memory of its own (one static scratch
+ *     array, see sgl_recent_compact_noalloc).
  */
 #ifndef STARRYGL_MI355X_H
 #define STARRYGL_MI355X_H
@@ -27,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 11
+#define SGL_ABI_VERSION 12
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -291,12 +292,26 @@ int sgl_memory_gather(int32_t D, int64_t capacity, const int32_t *num_roots,
  * >= U are zero, rows of the saved state >= U are left unwritten. If
  * any_edges == 0 the whole output and saved state are zero (models.py:88-89).
  * sv_phi0 [T] (may be NULL) receives cos(te_b), the query's time encoding.
+ * Dropout (models.py:127,136; training only): p_att drops attention weights
+ * after the softmax, p_out the output projection before the ReLU, both
+ * inverted (kept entries scaled by 1/(1-p)); p = 0 turns either off, and
+ * with both 0 the masks, seed, rng_step, pass and sv_sdrop are unused and
+ * the results are those of the dropout-free kernels. The masks are drawn
+ * from a counter-based generator (Philox4x32-10) at (seed, *rng_step, pass,
+ * root row, edge slot / column), so the backward regenerates them; the
+ * reference runs the attention three times per step with independent masks
+ * (runtime.py:193-195), which the caller reproduces as passes 0, 1, 2 with
+ * their own saved state. sv_sdrop [cap][H] receives, with attention dropout,
+ * the sum of each row's kept and rescaled weights (agg = W_v xbar' + sdrop
+ * b_v; the backward reads it).
  * Backward takes dL/dy as gy [cap][D], or (gy NULL) as W_s^T g_src + W_d^T
  * g_dst from sgl_predictor's per-root rows and the predictor's src_fc /
  * dst_fc weights w_s, w_d [D][D]: it reads the fixed-point accumulators
  * acc_src / acc_dst [cap+1][D], writes their rows as floats to g_src / g_dst
  * [cap+1][D] (for the src_fc / dst_fc weight reductions) and clears them for
- * the next step. It writes gz, gagg [cap][D], G [cap][H][D+F+T],
+ * the next step. acc_dst may be NULL (a dropout pass: dL/dy = W_s^T g_src
+ * with the pass's own accumulator and weight in the src_* arguments). The
+ * dropout arguments are the forward's. It writes gz, gagg [cap][D], G [cap][H][D+F+T],
  * sigma [cap][H], gQ [cap][D] (inputs of the weight-gradient GEMMs; rows
  * >= U unwritten, all zero if any_edges == 0), and per
  * tile partial sums ln_part [cap/R][2][D] (gamma, beta) and
@@ -332,7 +347,9 @@ int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      const float *te_b, float *sv_Q, float *sv_qt,
                      float *sv_xbar, float *sv_score, float *sv_ml,
                      float *sv_agg, float *sv_z, float *sv_stats,
-                     float *sv_phi0, float *S, float *y, hipStream_t stream);
+                     float *sv_phi0, float *S, float *y, float p_att, float p_out,
+                     uint64_t seed, const uint64_t *rng_step, int32_t pass,
+                     float *sv_sdrop, hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
@@ -350,7 +367,17 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       float *g_src, float *g_dst,
                       float *gz, float *gagg, float *G,
                       float *sigma, float *gQ, float *ln_part, float *te_part,
-                      hipStream_t stream);
+                      float p_att, float p_out, uint64_t seed,
+                      const uint64_t *rng_step, int32_t pass,
+                      const float *sv_sdrop, hipStream_t stream);
+/* The attention's dropout masks for rows [0, rows) of a pass, as the
+ * kernels above draw them (values 0 or 1/(1-p)): att_mask [rows][fanout][H]
+ * and out_mask [rows][D] (either may be NULL). For tests and debugging; no
+ * reference counterpart (torch draws its masks from its own generator). */
+int sgl_dropout_masks(int64_t rows, int32_t fanout, int32_t H, int32_t D,
+                      float p_att, float p_out, uint64_t seed,
+                      const uint64_t *rng_step, int32_t pass, float *att_mask,
+                      float *out_mask, hipStream_t stream);
 
 /* Fractional bits of the fixed-point int64 accumulators (value = v * 2^-40)
  * that sgl_predictor scatters into and sgl_conv_backward consumes: integer
@@ -376,7 +403,11 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
  * entry, e.g. allocated zeroed and cleared by sgl_conv_backward, which
  * consumes them): acc_src[r] = sum over events with root r as src of dL/dh_s,
  * acc_dst[r] = the same for dst (dL/dh_d) and negatives (dL/dh_n); negatives
- * that are not roots add into row U = *num_roots. The src_fc / dst_fc
+ * that are not roots add into row U = *num_roots. With dropout (three
+ * attention passes, runtime.py:193-195) e_d and e_n come from the rows of
+ * y + y_pass_stride and y + 2 y_pass_stride (floats; 0: every role from y)
+ * and, when acc_neg is not NULL, the negatives' sums (row U included) go to
+ * acc_neg [capacity+1][D] instead of acc_dst. The src_fc / dst_fc
  * gradients follow as reductions over rows 0..U (sgl_grad_adam jobs) and
  * dL/dy through sgl_conv_backward. acc_out (int64 [D+2]) and done (int32
  * [SGL_DONE_WORDS]) are the launch's own accumulator and completion counter:
@@ -391,7 +422,7 @@ int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   const float *b_o, float *pos_logits, float *neg_logits,
                   float *loss, int64_t *acc_src, int64_t *acc_dst,
                   float *g_wo, float *g_bo, int64_t *acc_out, int32_t *done,
-                  hipStream_t stream);
+                  int64_t y_pass_stride, int64_t *acc_neg, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
@@ -416,10 +447,12 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * moments exp_avg / exp_avg_sq at the same offsets.
  *
  * A job (device array) is one of:
- *   kind 0: a gradient block G[a][b] = sum_{r<R} x1[r*s1 + a] * x2[r*s2 + b]
- *           for a < rows, b < cols, stored at grad[off + a*ldo + b]; R is
- *           r_fixed, or *num_roots + r_extra when r_fixed < 0. s1 >= rows (s2 may be 0:
- *           a broadcast row). Tiles: ceil(rows/16) * ceil(cols/16), tiles_b =
+ *   kind 0: a gradient block G[a][b] = sum_{p<npass} sum_{r<R}
+ *           x1[p*ps1 + r*s1 + a] * x2[p*ps2 + r*s2 + b] for a < rows,
+ *           b < cols, stored at grad[off + a*ldo + b]; R is r_fixed, or
+ *           *num_roots + r_extra when r_fixed < 0; npass 0 counts as 1 (the
+ *           passes of a dropout step). s1 >= rows (s2 may be 0: a broadcast
+ *           row). Tiles: ceil(rows/16) * ceil(cols/16), tiles_b =
  *           ceil(cols/16).
  *   kind 1: rows*cols contiguous elements from off whose gradient is already
  *           in grad (Adam only). Tiles: ceil(rows*cols/256).
@@ -438,7 +471,8 @@ typedef struct sgl_grad_job {
   const float *x2;
   int64_t s1, s2;
   int64_t off;
-  int32_t ldo, rows, cols, kind, seg, r_fixed, r_extra, tiles_b, tile0;
+  int64_t ps1, ps2;
+  int32_t ldo, rows, cols, kind, seg, r_fixed, r_extra, tiles_b, tile0, npass;
 } sgl_grad_job;
 
 int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
@@ -457,10 +491,14 @@ int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
  * the count after the advance (a closed segment: the count plus one), in
  * double as torch computes them. One lane. Enqueue it after the gates are
  * written and after the sgl_grad_adam launch that last read this coef;
- * steps and gates are host arrays of device pointers. */
+ * steps and gates are host arrays of device pointers. With step_counter
+ * (device uint64, may be NULL) it also advances the training-step counter
+ * and copies the new value to step_out (the dropout masks' step, kept with
+ * the step's buffers; no reference counterpart). */
 int sgl_adam_coef(int32_t nseg, float *const *steps,
                   const int32_t *const *gates, float *coef, float lr,
-                  float beta1, float beta2, hipStream_t stream);
+                  float beta1, float beta2, uint64_t *step_counter,
+                  uint64_t *step_out, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Launch plans: a training step's calls of the entry points above, recorded

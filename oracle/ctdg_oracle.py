@@ -17,7 +17,12 @@ Follows, function by function:
   negative_sample        backends/ctdg/runtime/runtime.py:124-136
   prepare_roots          runtime.py:138-144
   conv_output/_select    runtime.py:146-183
-  train_step             runtime.py:225-328 (dropout must be 0 for parity)
+  train_step             runtime.py:225-328 (dropout as explicit masks: the
+                         GPU kernels' masks are replayed, torch's own draws
+                         cannot be matched)
+  philox4x32_10          the counter-based generator of the kernels' dropout
+                         masks (Salmon et al., SC 2011), pinned by the
+                         published known-answer vectors
 
 Parity pins (tests/test_oracle_step.py): GRU/GRUCell against hand-written
 gate equations; the conv against a per-root brute-force attention loop and
@@ -84,9 +89,11 @@ class TemporalConvO(nn.Module):
         self.att_act = nn.LeakyReLU(0.2)
         self.layer_norm = nn.LayerNorm(dim_out)
 
-    def forward(self, h_dst, h_nbr, ef, dt, edge_dst):
+    def forward(self, h_dst, h_nbr, ef, dt, edge_dst, att_mask=None, out_mask=None):
         """h_dst [R,D] (memory of roots), h_nbr [E,D] (memory of sampled
-        neighbours), ef [E,F], dt [E] float32, edge_dst [E] in [0,R)."""
+        neighbours), ef [E,F], dt [E] float32, edge_dst [E] in [0,R).
+        att_mask [E,H] / out_mask [R,D] (values 0 or 1/(1-p)) replace the
+        dropout modules' own draws (models.py:127,136) when given."""
         n_dst = h_dst.shape[0]
         if edge_dst.numel() == 0:                                  # models.py:88-89
             return torch.zeros(n_dst, self.dim_out, dtype=h_dst.dtype)
@@ -104,11 +111,12 @@ class TemporalConvO(nn.Module):
         V = self.w_v(k_in).reshape(-1, H, self.dim_out // H)
         att_raw = self.att_act((Q * K).sum(dim=2))                 # [E,H]
         att = segment_softmax(att_raw, edge_dst, n_dst)
-        att = self.att_dropout(att)
+        att = att * att_mask.to(att.dtype) if att_mask is not None else self.att_dropout(att)
         vw = (V * att.unsqueeze(-1)).reshape(V.shape[0], -1)
         agg = torch.zeros(n_dst, self.dim_out, dtype=vw.dtype).index_add(0, edge_dst, vw)
         rst = self.w_out(torch.cat([agg, h_dst], dim=1))
-        return self.layer_norm(F.relu(self.dropout(rst)))
+        rst = rst * out_mask.to(rst.dtype) if out_mask is not None else self.dropout(rst)
+        return self.layer_norm(F.relu(rst))
 
 
 def segment_softmax(x: torch.Tensor, seg: torch.Tensor, n: int) -> torch.Tensor:
@@ -166,6 +174,43 @@ def build_models(hidden_dim, edge_feat_dim, dim_time, num_head, slots, seed=0, d
     model = LinkPredictorO(hidden_dim, f, dim_time, num_head, dropout, att_dropout)
     updater = MemoryUpdaterO(hidden_dim, 2 * hidden_dim + f, slots)
     return model, updater
+
+
+def philox4x32_10(ctr, key):
+    """Philox4x32-10 on uint32 numpy arrays: ctr [..., 4], key [..., 2]."""
+    c = [np.asarray(ctr[..., i], dtype=np.uint64) for i in range(4)]
+    k0 = np.asarray(key[..., 0], dtype=np.uint64)
+    k1 = np.asarray(key[..., 1], dtype=np.uint64)
+    m32 = np.uint64(0xFFFFFFFF)
+    for _ in range(10):
+        p0 = np.uint64(0xD2511F53) * c[0]
+        p1 = np.uint64(0xCD9E8D57) * c[2]
+        c = [((p1 >> np.uint64(32)) ^ c[1] ^ k0) & m32, p1 & m32, ((p0 >> np.uint64(32)) ^ c[3] ^ k1) & m32,
+             p0 & m32]
+        k0 = (k0 + np.uint64(0x9E3779B9)) & m32
+        k1 = (k1 + np.uint64(0xBB67AE85)) & m32
+    return np.stack(c, axis=-1).astype(np.uint32)
+
+
+def dropout_masks(seed, step, pass_, rows, fanout, H, D, p_att, p_out):
+    """The kernels' mask definition restated: attention [rows, fanout, H]
+    from counter (row, slot, 2 pass, step) lanes 0..H-1, output [rows, D]
+    from (row, col // 4, 2 pass + 1, step) lane col % 4, key (seed low,
+    seed high ^ step high); keep when (u >> 8) / 2^24 >= p, kept = 1/(1-p)."""
+    key = np.array([seed & 0xFFFFFFFF, ((seed >> 32) ^ (step >> 32)) & 0xFFFFFFFF], dtype=np.uint32)
+
+    def keep(u, p):
+        return np.where((u >> np.uint32(8)).astype(np.float64) * 2.0 ** -24 >= p, 1.0 / (1.0 - p), 0.0).astype(
+            np.float32)
+
+    r, e = np.meshgrid(np.arange(rows), np.arange(fanout), indexing="ij")
+    ctr = np.stack([r, e, np.full_like(r, 2 * pass_), np.full_like(r, step & 0xFFFFFFFF)], -1).astype(np.uint32)
+    att = keep(philox4x32_10(ctr, np.broadcast_to(key, ctr.shape[:-1] + (2,)))[..., :H], p_att)
+    g4 = (D + 3) // 4
+    r, cg = np.meshgrid(np.arange(rows), np.arange(g4), indexing="ij")
+    ctr = np.stack([r, cg, np.full_like(r, 2 * pass_ + 1), np.full_like(r, step & 0xFFFFFFFF)], -1).astype(np.uint32)
+    out = keep(philox4x32_10(ctr, np.broadcast_to(key, ctr.shape[:-1] + (2,))), p_out).reshape(rows, g4 * 4)[:, :D]
+    return att, np.ascontiguousarray(out)
 
 
 # --------------------------------------------------------------------------- memory bank
@@ -267,15 +312,18 @@ class Block:
     delta_ts: torch.Tensor    # int64 [E]
 
 
-def conv_all(model: LinkPredictorO, memory: torch.Tensor, roots, blk: Block, edge_feat_all) -> torch.Tensor:
-    """runtime.py:158-174 + build_dgl_block (models.py:170-195)."""
+def conv_all(model: LinkPredictorO, memory: torch.Tensor, roots, blk: Block, edge_feat_all,
+             masks=None) -> torch.Tensor:
+    """runtime.py:158-174 + build_dgl_block (models.py:170-195); ``masks`` =
+    (att_mask [E,H], out_mask [R,D]) for this call's dropout."""
     if blk.nbr.numel() == 0:
         return torch.zeros(roots.numel(), model.hidden_dim)
     h_dst = memory[roots].detach()
     h_nbr = memory[blk.nbr].detach()
     ef = edge_feat_all[blk.eid].float()
     dt = blk.delta_ts.float()
-    return model.conv(h_dst, h_nbr, ef, dt, blk.src_index.long())
+    am, om = masks if masks is not None else (None, None)
+    return model.conv(h_dst, h_nbr, ef, dt, blk.src_index.long(), am, om)
 
 
 def select_rows(conv: torch.Tensor, roots: torch.Tensor, nodes: torch.Tensor) -> torch.Tensor:
@@ -307,11 +355,15 @@ def loss_from_logits(pos, neg):
 
 
 def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts, edge_feat, neg, edge_feat_all,
-               train=True, after_memory=None):
-    """runtime.py:225-297 for one batch (1 rank, dropout 0). ``sample_fn(roots,
-    tq)`` returns the hop-0 Block. ``after_memory(mem)`` (tests) runs between
-    the memory phase and the attention, e.g. to hand the attention another
-    implementation's updated memory. Returns a dict of the step's tensors."""
+               train=True, after_memory=None, masks=None):
+    """runtime.py:225-297 for one batch (1 rank). ``sample_fn(roots, tq)``
+    returns the hop-0 Block. ``after_memory(mem)`` (tests) runs between the
+    memory phase and the attention, e.g. to hand the attention another
+    implementation's updated memory. Without ``masks`` the attention runs
+    once (dropout 0: the reference's three calls are identical); with
+    ``masks`` = three (att_mask, out_mask) pairs it runs three times, for
+    the src, dst and negative rows in that order (runtime.py:193-195).
+    Returns a dict of the step's tensors."""
     roots, tq = prepare_roots(src, dst, ts)
     blk = sample_fn(roots, tq)
     if updater is not None:   # runtime.py:283-285: without one, memory and mailbox stay as they are
@@ -323,10 +375,15 @@ def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts,
     else:
         model.eval()
     with torch.set_grad_enabled(train):
-        conv = conv_all(model, mem.memory, roots, blk, edge_feat_all)
-        e_s = select_rows(conv, roots, src)
-        e_d = select_rows(conv, roots, dst)
-        e_n = select_rows(conv, roots, neg)
+        if masks is None:
+            conv = conv_all(model, mem.memory, roots, blk, edge_feat_all)
+            convs = (conv, conv, conv)
+        else:
+            convs = tuple(conv_all(model, mem.memory, roots, blk, edge_feat_all, m) for m in masks)
+            conv = convs[0]
+        e_s = select_rows(convs[0], roots, src)
+        e_d = select_rows(convs[1], roots, dst)
+        e_n = select_rows(convs[2], roots, neg)
         pos, negl = model(e_s, e_d, e_n)
         loss = loss_from_logits(pos, negl)
     if train:
@@ -334,7 +391,7 @@ def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts,
         loss.backward()
         optimizer.step()
     return {"loss": loss.detach(), "pos": pos.detach(), "neg": negl.detach(), "conv": conv.detach(),
-            "roots": roots, "block": blk}
+            "convs": tuple(c.detach() for c in convs), "roots": roots, "block": blk}
 
 
 def metric_dict(pos_logits, neg_logits):

@@ -248,6 +248,7 @@ struct ConvSaved {
   float *z;      // [cap][D]     pre-ReLU output projection
   float *stats;  // [cap][2]     LayerNorm mean, rstd
   float *phi0;   // [T]          cos(b): the query's time encoding (may be NULL)
+  float *sdrop;  // [cap][H]     with attention dropout: sum of the kept, rescaled weights
 };
 
 struct FwdLds {
@@ -260,7 +261,7 @@ struct FwdLds {
   float *qb;    // [16][H]
   float *TW, *TB;  // [T] time-encoding weight / bias
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
-  float *pml;   // [NW][H][2] a slice's running max and sum (slices only)
+  float *pml;   // [NW][H][3] a slice's running max, sum and kept sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
   float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
@@ -281,7 +282,7 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.TB = L.TW + d.T;
   L.part = L.TB + d.T;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
-  L.scr = L.pml + (slices ? nw * d.H * 2 : 0);
+  L.scr = L.pml + (slices ? ((nw * d.H * 3 + 3) & ~3) : 0);
   L.Ts = L.scr + (rows_for(nw) == 4 ? nw * 256 : 0);
   return L;
 }
@@ -294,12 +295,12 @@ inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices, int ts_rows) {
   return size_t(L.Ts + size_t(ts_rows) * d.T - base);
 }
 
-template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+template <int HM, int JM, bool DROP, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ h_root, const int32_t *__restrict__ cnt, float *__restrict__ X,
     const float *__restrict__ dt, float *__restrict__ S, ConvParams p, ConvSaved sv, float *__restrict__ y,
-    int ts_rows) {
+    int ts_rows, sgl::DropCfg dc) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
@@ -307,12 +308,15 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
   const FwdLds L = fwd_lds(d, lds, NW, WPR > 1);
   __shared__ int s_cnt[kRows];
+  __shared__ float s_sd[kRows][kMaxH];  // with attention dropout: the rows' kept-weight sums
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int U = *num_roots;
   const int r0 = blockIdx.x * RPW;
   const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
+  const unsigned long long dstep = DROP ? *dc.step : 0ull;
+  const float sa = sgl::drop_scale(dc.p_att), so = sgl::drop_scale(dc.p_out);
   if (nrows == 0 || !live) {
     // rows outside the live set: zero output (y's row U is the null
     // embedding the predictor's reductions read); a block without edges:
@@ -329,6 +333,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       sv.xbar[size_t(r0) * H * C + idx] = 0.f;
     }
     for (int idx = tid; idx < RPW * 2; idx += kBlock) sv.stats[size_t(r0) * 2 + idx] = 0.f;
+    if (DROP)
+      for (int idx = tid; idx < RPW * H; idx += kBlock) sv.sdrop[size_t(r0) * H + idx] = 0.f;
     return;
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
@@ -407,10 +413,12 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     int elo, ehi;
     window_slice(ne, sub, WPR, elo, ehi);
     float q[HM][JM], acc[HM][JM], m[HM], l[HM], qbh[HM];
+    float ls[HM];  // with attention dropout: the running sum of the kept, rescaled weights
 #pragma unroll
     for (int h = 0; h < HM; ++h) {
       m[h] = -INFINITY;
       l[h] = 0.f;
+      ls[h] = 0.f;
       qbh[h] = h < H ? L.qb[i * H + h] : 0.f;
 #pragma unroll
       for (int j = 0; j < JM; ++j) {
@@ -439,6 +447,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       for (int u = 0; u < kEC; ++u) {
         if (u >= nv) break;
         const size_t idx = base + e + u;
+        sgl::U32x4 bits{};
+        if constexpr (DROP)
+          if (dc.p_att > 0.f) bits = sgl::drop_bits(dc, dstep, uint32_t(r), uint32_t(e + u), 0);
 #pragma unroll
         for (int h = 0; h < HM; ++h) {
           if (h >= H) continue;
@@ -448,8 +459,16 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
           const float scale = __expf(m[h] - mn);
           const float pe = __expf(a - mn);
           l[h] = l[h] * scale + pe;
+          if constexpr (DROP) {
+            // softmax over every edge (l), the kept weights rescaled (pk)
+            const float pk = pe * sgl::drop_keep(bits.v[h], dc.p_att, sa);
+            ls[h] = ls[h] * scale + pk;
 #pragma unroll
-          for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
+            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pk * x[u][j];
+          } else {
+#pragma unroll
+            for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
+          }
           m[h] = mn;
           if (lane == 0) sv.score[idx * H + h] = a;
         }
@@ -521,6 +540,11 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
         if (lane == 0) {
           sv.ml[(size_t(r) * H + h) * 2 + 0] = ne > 0 ? m[h] : 0.f;
           sv.ml[(size_t(r) * H + h) * 2 + 1] = ne > 0 ? l[h] : 1.f;
+          if (DROP) {
+            const float sd = ne > 0 ? ls[h] * inv : 0.f;
+            s_sd[i][h] = sd;
+            sv.sdrop[size_t(r) * H + h] = sd;
+          }
         }
       }
     } else {
@@ -535,8 +559,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
           if (c < C) L.part[(wave * H + h) * C + c] = acc[h][j];
         }
         if (lane == 0) {
-          L.pml[(wave * H + h) * 2 + 0] = m[h];
-          L.pml[(wave * H + h) * 2 + 1] = l[h];
+          L.pml[(wave * H + h) * 3 + 0] = m[h];
+          L.pml[(wave * H + h) * 3 + 1] = l[h];
+          L.pml[(wave * H + h) * 3 + 2] = ls[h];
         }
       }
     }
@@ -548,15 +573,16 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
       const int i = idx / (H * C), hc = idx - i * (H * C), h = hc / C, c = hc - h * C;
       const int r = r0 + i;
-      float v = 0.f, M = -INFINITY, Ls = 0.f;
+      float v = 0.f, M = -INFINITY, Ls = 0.f, Lk = 0.f;
       if (s_cnt[i] > 0) {
 #pragma unroll
-        for (int s = 0; s < WPR; ++s) M = fmaxf(M, L.pml[((i * WPR + s) * H + h) * 2]);
+        for (int s = 0; s < WPR; ++s) M = fmaxf(M, L.pml[((i * WPR + s) * H + h) * 3]);
 #pragma unroll
         for (int s = 0; s < WPR; ++s) {
           const int w = i * WPR + s;
-          const float f = __expf(L.pml[(w * H + h) * 2] - M);
-          Ls += L.pml[(w * H + h) * 2 + 1] * f;
+          const float f = __expf(L.pml[(w * H + h) * 3] - M);
+          Ls += L.pml[(w * H + h) * 3 + 1] * f;
+          if (DROP) Lk += L.pml[(w * H + h) * 3 + 2] * f;
           v += L.part[(w * H + h) * C + c] * f;
         }
         v /= Ls;
@@ -566,22 +592,29 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       if (c == 0) {
         sv.ml[(size_t(r) * H + h) * 2 + 0] = s_cnt[i] > 0 ? M : 0.f;
         sv.ml[(size_t(r) * H + h) * 2 + 1] = s_cnt[i] > 0 ? Ls : 1.f;
+        if (DROP) {
+          const float sd = s_cnt[i] > 0 ? Lk / Ls : 0.f;
+          s_sd[i][h] = sd;
+          sv.sdrop[size_t(r) * H + h] = sd;
+        }
       }
     }
     __syncthreads();
   }
-  // agg_h = W_v[h rows] xbar_h + b_v[h]  -> AH[:, :D]
+  // agg_h = W_v[h rows] xbar_h + b_v[h]  -> AH[:, :D]; with attention
+  // dropout the kept weights sum to s_h, not 1: agg_h = W_v xbar'_h + s_h b_v[h]
   {
     sgl::GemmJob jobs[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h)
-      jobs[h] = {L.QT + h * C, L.ldq, p.w_v + size_t(h) * dh * C, C, p.b_v + h * dh, L.AH + h * dh, L.lda, C,
-                 h < H ? dh : 0};
+      jobs[h] = {L.QT + h * C, L.ldq, p.w_v + size_t(h) * dh * C, C, DROP ? nullptr : p.b_v + h * dh,
+                 L.AH + h * dh, L.lda, C, h < H ? dh : 0};
     tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
   __syncthreads();
   for (int idx = tid; idx < kRows * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
+    if (DROP && i < RPW && s_cnt[i] > 0) L.AH[i * L.lda + j] += s_sd[i][j / dh] * p.b_v[j];
     if (s_cnt[i] == 0) L.AH[i * L.lda + j] = 0.f;  // no in-edges: the sum aggregator gives 0
     if (i < RPW) sv.agg[size_t(r0 + i) * D + j] = L.AH[i * L.lda + j];
   }
@@ -592,12 +625,19 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
   __syncthreads();
-  // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance; one wave per row
+  // y = LayerNorm(ReLU(z)), eps 1e-5, biased variance; one wave per row;
+  // with output dropout z is masked first (models.py:136: dropout, then
+  // ReLU) and saved masked
   for (int i = wave; i < RPW; i += kWaves) {
     const size_t ro = size_t(r0 + i) * D;
     float s1 = 0.f;
     for (int j = lane; j < D; j += 64) {
-      const float zz = L.Zs[i * L.ldr + j];
+      float zz = L.Zs[i * L.ldr + j];
+      if (DROP && dc.p_out > 0.f) {
+        zz *= sgl::drop_keep(sgl::drop_bits(dc, dstep, uint32_t(r0 + i), uint32_t(j >> 2), 1).v[j & 3],
+                             dc.p_out, so);
+        L.Zs[i * L.ldr + j] = zz;
+      }
       sv.z[ro + j] = i < nrows ? zz : 0.f;
       s1 += fmaxf(zz, 0.f);
     }
@@ -667,27 +707,29 @@ inline size_t bwd_lds_floats(const Dims &d, int nw, bool slices) {
 
 // The edge predictor's per-root gradient rows r0 .. r0+nrows-1 (fixed-point
 // accumulators): returned as floats in g_src / g_dst and cleared for the
-// next step.
+// next step (acc_dst may be NULL: one accumulator).
 __device__ __forceinline__ void consume_rows(long long *__restrict__ acc_src, long long *__restrict__ acc_dst,
                                              float *__restrict__ g_src, float *__restrict__ g_dst, int r0,
                                              int nrows, int D, int tid, int nthreads) {
   for (int idx = tid; idx < nrows * D; idx += nthreads) {
     const size_t o = size_t(r0) * D + idx;
     g_src[o] = sgl::from_fixed(acc_src[o]);
-    g_dst[o] = sgl::from_fixed(acc_dst[o]);
     acc_src[o] = 0;
-    acc_dst[o] = 0;
+    if (acc_dst != nullptr) {
+      g_dst[o] = sgl::from_fixed(acc_dst[o]);
+      acc_dst[o] = 0;
+    }
   }
 }
 
-template <int HM, int JM, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+template <int HM, int JM, bool DROP, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const int32_t *__restrict__ cnt, const float *__restrict__ X, const float *__restrict__ S,
     const float *__restrict__ dt, ConvParams p,
     ConvSaved sv, const float *__restrict__ gy, long long *__restrict__ acc_src,
     long long *__restrict__ acc_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
-    float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g) {
+    float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g, sgl::DropCfg dc) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;
   static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
@@ -702,6 +744,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   const int r0 = blockIdx.x * RPW;
   const int nrows = max(0, min(RPW, U - r0));
   const bool live = *any_edges != 0;
+  const unsigned long long dstep = DROP ? *dc.step : 0ull;
+  const float sa = sgl::drop_scale(dc.p_att), so = sgl::drop_scale(dc.p_out);
   // row U of the accumulators (the non-root negatives; row capacity when
   // every row is a root) belongs to the workgroup whose tile holds it, or
   // to the last one; the rows past U are never written by the predictor
@@ -719,6 +763,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       for (int idx = tid; idx < RPW * H * C; idx += kBlock) g.G[size_t(r0) * H * C + idx] = 0.f;
       for (int idx = tid; idx < RPW * H; idx += kBlock) g.sigma[size_t(r0) * H + idx] = 0.f;
     }
+    // rows past the live set: zero gradient rows (the weight reductions of
+    // dropout passes stop at U, but their products never read stale rows)
     for (int idx = tid; idx < 2 * D; idx += kBlock) g.ln_part[size_t(blockIdx.x) * 2 * D + idx] = 0.f;
     for (int idx = tid; idx < 2 * T; idx += kBlock) g.te_part[size_t(blockIdx.x) * 2 * T + idx] = 0.f;
     return;
@@ -737,24 +783,28 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     }
     __syncthreads();
   } else {
+    const bool two = acc_dst != nullptr;  // one accumulator: the pass of a dropout step
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
       float vs = 0.f, vd = 0.f;
       if (i < nrows) {  // the tile's live rows (row U is consumed above)
         const size_t o = size_t(r0 + i) * D + j;
         vs = sgl::from_fixed(acc_src[o]);
-        vd = sgl::from_fixed(acc_dst[o]);
         acc_src[o] = 0;
-        acc_dst[o] = 0;
         g_src[o] = vs;
-        g_dst[o] = vd;
+        if (two) {
+          vd = sgl::from_fixed(acc_dst[o]);
+          acc_dst[o] = 0;
+          g_dst[o] = vd;
+        }
       }
       L.GA[i * L.ldr + j] = vs;
       L.GQ[i * L.ldr + j] = vd;
+      if (!two) L.XH[i * L.ldr + j] = 0.f;
     }
     __syncthreads();
     const sgl::GemmJob jobs[2] = {{L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D},
-                                  {L.GQ, L.ldr, w_d, D, nullptr, L.XH, L.ldr, D, D}};
+                                  {L.GQ, L.ldr, two ? w_d : w_s, D, nullptr, L.XH, L.ldr, D, two ? D : 0}};
     tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
     __syncthreads();
   }
@@ -786,7 +836,11 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         const float zz = L.GZ[i * L.ldr + j];
         const float xh = L.XH[i * L.ldr + j];
         const float gx = rstd * (L.GY[i * L.ldr + j] * p.ln_g[j] - a1 - xh * a2);
-        L.GZ[i * L.ldr + j] = zz > 0.f ? gx : 0.f;
+        float gzv = zz > 0.f ? gx : 0.f;
+        if (DROP && dc.p_out > 0.f)  // through the output mask (z was saved masked)
+          gzv *= sgl::drop_keep(sgl::drop_bits(dc, dstep, uint32_t(r0 + i), uint32_t(j >> 2), 1).v[j & 3],
+                                dc.p_out, so);
+        L.GZ[i * L.ldr + j] = gzv;
       }
     }
   }
@@ -840,7 +894,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     int elo, ehi;
     window_slice(ne, sub, WPR, elo, ehi);
     float q[HM][JM], gx[HM][JM], G[HM][JM];
-    float dot[HM], sig[HM], mh[HM], lh[HM];
+    float dot[HM], sig[HM], mh[HM], lh[HM], cb[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h) {
       float pd = 0.f;
@@ -855,6 +909,18 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         pd += gx[h][j] * xb;
       }
       dot[h] = wave_sum(pd);
+      cb[h] = 0.f;
+      if constexpr (DROP) {
+        // with attention dropout the weights no longer sum to 1, so the
+        // value bias stays in: dL/dalpha'_e = <g_xbar_h, X_e> + c_h with
+        // c_h = <g_agg_h, b_v[h]>, and sum_e alpha_e dL/dalpha_e = dot + c_h s_h
+        if (h < H) {
+          float pc = 0.f;
+          for (int j = lane; j < dh; j += 64) pc += L.GA[i * L.ldr + h * dh + j] * p.b_v[h * dh + j];
+          cb[h] = wave_sum(pc);
+          dot[h] += cb[h] * sv.sdrop[size_t(r) * H + h];
+        }
+      }
       sig[h] = 0.f;
       mh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2] : 0.f;
       lh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2 + 1] : 1.f;
@@ -899,6 +965,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
           const int e = c0 + u;
           const float dtv = __shfl(my_dt, e, 64);
           float gsv[HM], al[HM];
+          sgl::U32x4 bits{};
+          if constexpr (DROP)
+            if (dc.p_att > 0.f) bits = sgl::drop_bits(dc, dstep, uint32_t(r), uint32_t(e0 + e), 0);
 #pragma unroll
           for (int h = 0; h < HM; ++h) {
             gsv[h] = 0.f;
@@ -907,10 +976,17 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
             const float t = tg[u][h];
             const float a = __shfl(my_sc[h], e, 64);
             const float alpha = __expf(a - mh[h]) / lh[h];
-            const float ga = alpha * (t - dot[h]);  // softmax backward
+            float ga, aw = alpha;
+            if constexpr (DROP) {
+              const float mk = sgl::drop_keep(bits.v[h], dc.p_att, sa);
+              ga = alpha * (mk * (t + cb[h]) - dot[h]);  // softmax backward through the mask
+              aw = alpha * mk;                           // the edge's weight in xbar'
+            } else {
+              ga = alpha * (t - dot[h]);  // softmax backward
+            }
             const float gs = ga * (a > 0.f ? 1.f : 0.2f);
             gsv[h] = gs;
-            al[h] = alpha;
+            al[h] = aw;
             sig[h] += gs;
 #pragma unroll
             for (int j = 0; j < JM; ++j) G[h][j] += gs * x[u][j];
@@ -1085,18 +1161,83 @@ auto pick_instance(const Dims &d) -> decltype(Pick<1, 2>::get()) {
   return {nullptr, 0, 0};
 }
 
-using FwdFn = decltype(&k_conv_fwd<1, 2>);
-using BwdFn = decltype(&k_conv_bwd<1, 2>);
+using FwdFn = decltype(&k_conv_fwd<1, 2, false>);
+using BwdFn = decltype(&k_conv_bwd<1, 2, false>);
 template <int HM, int JM>
 struct FwdPick {
-  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
 template <int HM, int JM>
 struct BwdPick {
-  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
+// the dropout instances (masks, kept-weight sums)
+template <int HM, int JM>
+struct FwdPickDrop {
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
+template <int HM, int JM>
+struct BwdPickDrop {
+  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
 
+int drop_cfg(float p_att, float p_out, uint64_t seed, const uint64_t *rng_step, int32_t pass, const float *sdrop,
+             sgl::DropCfg &dc, bool &drop) {
+  SGL_REQUIRE(p_att >= 0.f && p_att < 1.f && p_out >= 0.f && p_out < 1.f,
+              "conv: dropout probabilities must lie in [0, 1) (att %g, out %g)", p_att, p_out);
+  drop = p_att > 0.f || p_out > 0.f;
+  SGL_REQUIRE(!drop || (rng_step != nullptr && (p_att == 0.f || sdrop != nullptr)),
+              "conv: dropout needs the step counter and (attention dropout) the kept-weight sums");
+  SGL_REQUIRE(pass >= 0 && pass < (1 << 20), "conv: pass %d out of range", pass);
+  dc = sgl::DropCfg{p_att, p_out, uint32_t(seed), uint32_t(seed >> 32),
+                    reinterpret_cast<const unsigned long long *>(rng_step), pass};
+  return SGL_OK;
+}
+
 }  // namespace
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_dropout_masks(sgl::DropCfg dc, int64_t rows, int fanout, int H, int D,
+                                                       float *__restrict__ att, float *__restrict__ out) {
+  const unsigned long long step = *dc.step;
+  const float sa = sgl::drop_scale(dc.p_att), so = sgl::drop_scale(dc.p_out);
+  const int64_t na = att != nullptr ? rows * fanout : 0, no = out != nullptr ? rows * ((D + 3) / 4) : 0;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < na + no; i += int64_t(gridDim.x) * 256) {
+    if (i < na) {
+      const int64_t r = i / fanout;
+      const int e = int(i - r * fanout);
+      const sgl::U32x4 b = sgl::drop_bits(dc, step, uint32_t(r), uint32_t(e), 0);
+      for (int h = 0; h < H; ++h) att[i * H + h] = sgl::drop_keep(b.v[h], dc.p_att, sa);
+    } else {
+      const int64_t k = i - na, g4 = (D + 3) / 4;
+      const int64_t r = k / g4;
+      const int c4 = int(k - r * g4);
+      const sgl::U32x4 b = sgl::drop_bits(dc, step, uint32_t(r), uint32_t(c4), 1);
+      for (int q = 0; q < 4 && 4 * c4 + q < D; ++q) out[r * D + 4 * c4 + q] = sgl::drop_keep(b.v[q], dc.p_out, so);
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int sgl_dropout_masks(int64_t rows, int32_t fanout, int32_t H, int32_t D, float p_att, float p_out,
+                                 uint64_t seed, const uint64_t *rng_step, int32_t pass, float *att_mask,
+                                 float *out_mask, hipStream_t stream) {
+  SGL_REQUIRE(rows >= 0 && rows < INT_MAX && fanout >= 0 && fanout <= 4096 && H > 0 && H <= kMaxH && D > 0,
+              "dropout_masks: bad sizes");
+  SGL_REQUIRE(rng_step != nullptr, "dropout_masks: NULL step counter");
+  sgl::DropCfg dc;
+  bool drop;
+  if (int rc = drop_cfg(p_att, p_out, seed, rng_step, pass, reinterpret_cast<const float *>(rng_step), dc, drop))
+    return rc;
+  const int64_t n = (att_mask ? rows * fanout : 0) + (out_mask ? rows * ((D + 3) / 4) : 0);
+  if (n == 0) return SGL_OK;
+  const unsigned grid = unsigned(std::min<int64_t>((n + 255) / 256, sgl::kMaxGrid));
+  k_dropout_masks<<<grid, 256, 0, stream>>>(dc, rows, fanout, H, D, att_mask, out_mask);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
 
 extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H) {
   const Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, 0};
@@ -1138,9 +1279,13 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                                 const float *w_out, const float *b_out, const float *ln_g, const float *ln_b,
                                 const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
                                 float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
-                                float *sv_phi0, float *S, float *y, hipStream_t stream) {
+                                float *sv_phi0, float *S, float *y, float p_att, float p_out, uint64_t seed,
+                                const uint64_t *rng_step, int32_t pass, float *sv_sdrop, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
+  sgl::DropCfg dc;
+  bool drop;
+  if (int rc = drop_cfg(p_att, p_out, seed, rng_step, pass, sv_sdrop, dc, drop)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
@@ -1148,7 +1293,7 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                   ln_g && ln_b && te_w && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z && sv_stats &&
                   y && (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_forward: NULL array");
-  const auto inst = pick_instance<FwdPick>(d);
+  const auto inst = drop ? pick_instance<FwdPickDrop>(d) : pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   // stage the tile's time encodings in LDS when they fit
   const bool slices = inst.waves > inst.rows;
@@ -1158,9 +1303,9 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
   SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
-  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0};
+  ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_sdrop};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
-              num_roots, any_edges, h_root, cnt, X, dt, S, p, sv, y, ts_rows);
+              num_roots, any_edges, h_root, cnt, X, dt, S, p, sv, y, ts_rows, dc);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -1176,31 +1321,37 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                                  int64_t *acc_src,
                                  int64_t *acc_dst, const float *w_s, const float *w_d, float *g_src, float *g_dst,
                                  float *gz, float *gagg, float *G, float *sigma, float *gQ, float *ln_part,
-                                 float *te_part, hipStream_t stream) {
+                                 float *te_part, float p_att, float p_out, uint64_t seed, const uint64_t *rng_step,
+                                 int32_t pass, const float *sv_sdrop, hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
+  sgl::DropCfg dc;
+  bool drop;
+  if (int rc = drop_cfg(p_att, p_out, seed, rng_step, pass, sv_sdrop, dc, drop)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
   SGL_REQUIRE(num_roots && any_edges && cnt && w_q && w_k && b_k && w_v && w_out && ln_g && te_b && sv_qt &&
-                  sv_xbar && sv_ml && sv_z && sv_stats && (gy || (acc_src && acc_dst && w_s && w_d && g_src && g_dst)) &&
+                  sv_xbar && sv_ml && sv_z && sv_stats && (gy || (acc_src && w_s && g_src)) &&
+                  (acc_dst == nullptr || (w_d && g_dst)) && (!drop || b_v) &&
                   gz && gagg && G && sigma && gQ && ln_part && te_part &&
                   (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_backward: NULL array");
-  const auto inst = pick_instance<BwdPick>(d);
+  const auto inst = drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
   const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, nullptr, te_b};
-  ConvSaved sv{const_cast<float *>(sv_Q), const_cast<float *>(sv_qt), const_cast<float *>(sv_xbar),
-               const_cast<float *>(sv_score), const_cast<float *>(sv_ml), const_cast<float *>(sv_agg),
-               const_cast<float *>(sv_z), const_cast<float *>(sv_stats), nullptr};
+  ConvSaved sv{const_cast<float *>(sv_Q),     const_cast<float *>(sv_qt),   const_cast<float *>(sv_xbar),
+               const_cast<float *>(sv_score), const_cast<float *>(sv_ml),   const_cast<float *>(sv_agg),
+               const_cast<float *>(sv_z),     const_cast<float *>(sv_stats), nullptr,
+               const_cast<float *>(sv_sdrop)};
   ConvGrads g{gz, gagg, G, sigma, gQ, ln_part, te_part};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
               num_roots, any_edges, cnt, X, S, dt, p, sv, gy,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst,
-              g);
+              g, dc);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -136,6 +136,52 @@ __device__ inline bool last_block(int32_t *done) {
   return true;
 }
 
+// Counter-based random numbers: Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011): ten rounds of two
+// 32x32->64 multiplies with the published multipliers and Weyl key
+// increments. Four independent uint32 per (counter, key); no state.
+struct U32x4 {
+  uint32_t v[4];
+};
+__device__ __forceinline__ U32x4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                               uint32_t k1) {
+  constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u, kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = uint64_t(kM0) * c0, p1 = uint64_t(kM1) * c2;
+    const uint32_t n0 = uint32_t(p1 >> 32) ^ c1 ^ k0, n2 = uint32_t(p0 >> 32) ^ c3 ^ k1;
+    c0 = n0;
+    c1 = uint32_t(p1);
+    c2 = n2;
+    c3 = uint32_t(p0);
+    k0 += kW0;
+    k1 += kW1;
+  }
+  return U32x4{{c0, c1, c2, c3}};
+}
+
+// Dropout masks of the attention (inverted dropout: kept entries scale by
+// 1 / (1 - p)). A mask value is keep(u) ? scale : 0 for the uint32 u at the
+// element's place in the stream of (seed, step): attention weights draw
+// counter (row, slot, 2 * pass, step) and take lane h (head h < 4); output
+// entries draw (row, col / 4, 2 * pass + 1, step) and take lane col % 4.
+// Key = (seed low word, seed high word ^ step high word). u / 2^32 >= p keeps.
+struct DropCfg {
+  float p_att, p_out;          // drop probabilities (0: that dropout is off)
+  uint32_t seed_lo, seed_hi;
+  const unsigned long long *step;  // the step's counter (device)
+  int pass;
+};
+__device__ __forceinline__ float drop_scale(float p) { return p > 0.f ? 1.f / (1.f - p) : 1.f; }
+__device__ __forceinline__ float drop_keep(uint32_t u, float p, float scale) {
+  return float(u >> 8) * 0x1p-24f >= p ? scale : 0.f;
+}
+__device__ __forceinline__ U32x4 drop_bits(const DropCfg &c, unsigned long long step, uint32_t row, uint32_t col,
+                                           int out) {
+  return philox4x32_10(row, col, uint32_t(2 * c.pass + out), uint32_t(step), c.seed_lo,
+                       c.seed_hi ^ uint32_t(step >> 32));
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_reduce_sum(T v) {
 #pragma unroll

@@ -125,13 +125,14 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
     const int R = jb.r_fixed >= 0 ? jb.r_fixed : *num_roots + jb.r_extra;
     const int i16 = lane & 15, q = lane >> 4;
     sgl::f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if (R > 0) {
+    const int npass = jb.npass > 0 ? jb.npass : 1;
+    for (int ps = 0; R > 0 && ps < npass; ++ps) {
       // rows >= R read 0 through the buffer ranges (X1 rows are at least
       // `rows` wide, so row R starts past X1's span)
       const uint32_t span1 = uint32_t(R - 1) * uint32_t(jb.s1) + uint32_t(jb.rows);
       const uint32_t span2 = uint32_t(R - 1) * uint32_t(jb.s2) + uint32_t(jb.cols);
-      const __amdgpu_buffer_rsrc_t r1 = sgl::weight_rsrc(jb.x1, span1);
-      const __amdgpu_buffer_rsrc_t r2 = sgl::weight_rsrc(jb.x2, span2);
+      const __amdgpu_buffer_rsrc_t r1 = sgl::weight_rsrc(jb.x1 + ps * jb.ps1, span1);
+      const __amdgpu_buffer_rsrc_t r2 = sgl::weight_rsrc(jb.x2 + ps * jb.ps2, span2);
       const int ngroups = (R + 3) >> 2;
       for (int gb = wave; gb < ngroups; gb += 4 * kGaChunk) {
         float xa[kGaChunk], xb[kGaChunk];
@@ -178,8 +179,14 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
 // corrections of the step they are now at (torch.optim.Adam: the count is
 // incremented first, then lr / (1 - b1^t) and sqrt(1 - b2^t) in double).
 // A closed segment keeps its count; its coef (for the next count) is unused.
-__global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, float lr, float b1, float b2) {
+__global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, float lr, float b1, float b2,
+                            unsigned long long *step_counter, unsigned long long *step_out) {
   if (threadIdx.x != 0) return;
+  if (step_counter != nullptr) {
+    const unsigned long long n = *step_counter + 1ull;
+    *step_counter = n;
+    *step_out = n;
+  }
   for (int s = 0; s < nseg; ++s) {
     const float st = *segs.step[s];
     const bool open = segs.gate[s] == nullptr || *segs.gate[s] != 0;
@@ -216,12 +223,15 @@ extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, 
 }
 
 extern "C" int sgl_adam_coef(int32_t nseg, float *const *steps, const int32_t *const *gates, float *coef, float lr,
-                             float beta1, float beta2, hipStream_t stream) {
+                             float beta1, float beta2, uint64_t *step_counter, uint64_t *step_out,
+                             hipStream_t stream) {
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "adam_coef: nseg %d out of range", nseg);
   SGL_REQUIRE(steps != nullptr && coef != nullptr, "adam_coef: NULL array");
+  SGL_REQUIRE(step_counter == nullptr || step_out != nullptr, "adam_coef: step_counter without step_out");
   for (int s = 0; s < nseg; ++s) SGL_REQUIRE(steps[s] != nullptr, "adam_coef: NULL step counter %d", s);
   sgl::launch(&k_adam_coef, dim3(1), dim3(64), 0, stream, int(nseg), make_segs(nseg, steps, gates), coef, lr, beta1,
-              beta2);
+              beta2, reinterpret_cast<unsigned long long *>(step_counter),
+              reinterpret_cast<unsigned long long *>(step_out));
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

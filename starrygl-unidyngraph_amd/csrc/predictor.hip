@@ -15,6 +15,10 @@
 // these rows the attention backward gets dL/dy = W_s^T g_src + W_d^T g_dst,
 // and the src_fc / dst_fc gradients are reductions over the roots
 // (dW_s = sum_r g_src[r] y[r]^T, db_d = sum_{r <= U} g_dst[r], ...).
+// With dropout the reference runs the attention once per role with its own
+// masks (runtime.py:193-195): e_s, e_d and e_n then come from three passes'
+// outputs (y, y + y_pass_stride, y + 2 y_pass_stride) and the negatives'
+// gradients go to their own accumulator acc_neg (row U for non-roots).
 // Every sum over events is accumulated in fixed point with integer atomics
 // (exact, so independent of the workgroups' order): the per-root rows in the
 // caller's accumulators (consumed and cleared by the attention backward), the
@@ -57,7 +61,10 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     const float *__restrict__ b_d, const float *__restrict__ w_o, const float *__restrict__ b_o,
     float *__restrict__ pos_out, float *__restrict__ neg_out, float *__restrict__ loss,
     long long *__restrict__ acc_src, long long *__restrict__ acc_dst, float *__restrict__ g_wo,
-    float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done, int agg) {
+    float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done, int agg,
+    int64_t ystride, long long *__restrict__ acc_neg) {
+  const bool sep = acc_neg != nullptr;  // the negatives' rows apart from the dst rows
+  long long *acc_n = sep ? acc_neg : acc_dst;
   extern __shared__ __align__(16) float lds[];
   const int ld = sgl::lds_ld(D);
   long long *Nul = reinterpret_cast<long long *>(lds);  // [D] dL/dh_n of the tile's non-root negatives
@@ -109,7 +116,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       int l = -1;
       if (r >= 0)
         for (int t = e; t >= 0; --t)
-          if (s_idx[1 + (t & 1)][t >> 1] == r) l = t;
+          if (s_idx[1 + (t & 1)][t >> 1] == r && (!sep || ((t ^ e) & 1) == 0)) l = t;
       s_lead[tid] = l;
     }
   }
@@ -117,8 +124,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     const int i = idx / D, j = idx - i * D;
     const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
     Es[i * ld + j] = a >= 0 ? y[size_t(a) * D + j] : 0.f;
-    Ed[i * ld + j] = b >= 0 ? y[size_t(b) * D + j] : 0.f;
-    En[i * ld + j] = c >= 0 ? y[size_t(c) * D + j] : 0.f;
+    Ed[i * ld + j] = b >= 0 ? y[ystride + size_t(b) * D + j] : 0.f;
+    En[i * ld + j] = c >= 0 ? y[2 * ystride + size_t(c) * D + j] : 0.f;
   }
   __syncthreads();
   {
@@ -217,7 +224,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       }
       if (a >= 0) sgl::atomic_add_fixed(&acc_src[size_t(a) * D + j], fp + fn);
       if (b >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(b) * D + j], fp);
-      if (c >= 0) sgl::atomic_add_fixed(&acc_dst[size_t(c) * D + j], fn);
+      if (c >= 0) sgl::atomic_add_fixed(&acc_n[size_t(c) * D + j], fn);
       else if (fn != 0) atomicAdd(reinterpret_cast<unsigned long long *>(&Nul[j]), static_cast<unsigned long long>(fn));
     }
     __syncthreads();
@@ -231,12 +238,12 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
           sgl::atomic_add_fixed(&acc_src[size_t(s_idx[0][e]) * D + j], v);
         } else {
           const int t = e - kRows;
-          sgl::atomic_add_fixed(&acc_dst[size_t(s_idx[1 + (t & 1)][t >> 1]) * D + j], v);
+          sgl::atomic_add_fixed(&((t & 1) ? acc_n : acc_dst)[size_t(s_idx[1 + (t & 1)][t >> 1]) * D + j], v);
         }
       }
     }
     for (int j = tid; j < D; j += kBlock)
-      if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_dst[size_t(U) * D + j], Nul[j]);
+      if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_n[size_t(U) * D + j], Nul[j]);
   }
   // the last workgroup to finish turns the accumulated sums into the outputs
   // and clears the accumulator and the counter for the next launch. The sums
@@ -266,12 +273,13 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
                              const float *w_s, const float *b_s, const float *w_d, const float *b_d,
                              const float *w_o, const float *b_o, float *pos_logits, float *neg_logits, float *loss,
                              int64_t *acc_src, int64_t *acc_dst, float *g_wo, float *g_bo, int64_t *acc_out,
-                             int32_t *done, hipStream_t stream) {
+                             int32_t *done, int64_t y_pass_stride, int64_t *acc_neg, hipStream_t stream) {
   SGL_REQUIRE(batch >= 0 && batch < INT_MAX && D > 0 && capacity >= 0, "predictor: bad sizes");
   SGL_REQUIRE(num_roots && y && ridx_src && ridx_dst && ridx_neg && w_s && b_s && w_d && b_d && w_o && b_o &&
                   pos_logits && neg_logits && loss && acc_out && done,
               "predictor: NULL array");
   SGL_REQUIRE(!train || (acc_src && acc_dst && g_wo && g_bo), "predictor: NULL gradient array");
+  SGL_REQUIRE(y_pass_stride >= 0, "predictor: negative y_pass_stride");
   if (batch == 0) {  // no events: zero loss and out_fc gradients
     const ZeroSpans z{{loss, train ? g_wo : nullptr, train ? g_bo : nullptr, nullptr}, {1, train ? D : 0, train, 0}};
     k_zero<<<unsigned((D + 255) / 256), 256, 0, stream>>>(z);
@@ -288,7 +296,8 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
   sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
               num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
-              reinterpret_cast<long long *>(acc_out), done, agg);
+              reinterpret_cast<long long *>(acc_out), done, agg, y_pass_stride,
+              train ? reinterpret_cast<long long *>(acc_neg) : nullptr);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -13,8 +13,9 @@ interchangeable and a seeded construction draws the same initial weights:
   it never receives gradients in the reference (its output is detached,
   runtime.py:279), so it is forward-only here.
 * ``CTDGLinkPredictor`` (models.py:261-324) and ``build_ctdg_model``
-  (models.py:327-386). The edge predictor (three nn.Linear) and the BCE loss
-  run in torch.
+  (models.py:327-386). The runtime's step evaluates the edge predictor and
+  the BCE loss with the sgl_predictor kernel; the module's forward (torch)
+  serves callers outside the step.
 """
 from __future__ import annotations
 
@@ -55,20 +56,30 @@ class TemporalTransformerConv(nn.Module):
         self.att_dropout = nn.Dropout(att_dropout)
         self.att_act = nn.LeakyReLU(0.2)
         self.layer_norm = nn.LayerNorm(dim_out)
+        # dropout masks come from a counter-based generator keyed by this seed
+        # and the step buffers' counter (torch's generators are not consumed)
+        self.dropout_seed = int(torch.initial_seed()) & 0xFFFFFFFFFFFFFFFF
 
     def kernel_params(self) -> list[torch.Tensor]:
         return [self.time_enc.w.weight, self.time_enc.w.bias, self.w_q.weight, self.w_q.bias, self.w_k.weight,
                 self.w_k.bias, self.w_v.weight, self.w_v.bias, self.w_out.weight, self.w_out.bias,
                 self.layer_norm.weight, self.layer_norm.bias]
 
+    def drop_args(self):
+        """(p_att, p_out, seed) of the attention kernels in training, or None
+        when both dropouts are off (or in eval mode)."""
+        if not self.training or (self.dropout.p == 0 and self.att_dropout.p == 0):
+            return None
+        return float(self.att_dropout.p), float(self.dropout.p), self.dropout_seed
+
     def forward(self, step: DeviceStep, edge_feat_all: torch.Tensor) -> torch.Tensor:
         """Embeddings [capacity, D] of the step's roots (rows >= the live root
-        count are zero)."""
-        if self.training and (self.dropout.p > 0 or self.att_dropout.p > 0):
-            raise NotImplementedError(
-                "dropout > 0 is not implemented by the MI355X attention kernels; set ctdg.dropout and "
-                "ctdg.att_dropout to 0")
-        return ConvFunction.apply(step, edge_feat_all, *self.kernel_params())
+        count are zero). In training with dropout each call draws fresh masks
+        (the step buffers' counter advances)."""
+        drop = self.drop_args()
+        if drop is not None:
+            step.buf.rng_step.add_(1)
+        return ConvFunction.apply(step, edge_feat_all, drop, *self.kernel_params())
 
 
 @dataclass

@@ -4,16 +4,19 @@
 signatures and result dicts. Inside, a step is the device kernel sequence of
 starry_unigraph.native.step over the HBM-resident event stream:
 
-  negatives (CPU generator, runtime.py:124-136) -> sgl_batch_prepare ->
-  sgl_recent_sample (hop 0 of the split's sampler) -> sgl_memory_update ->
-  sgl_memory_commit -> attention forward -> edge predictor + BCE (torch) ->
-  backward -> Adam
+  negatives (CPU generator draws, device lookup; runtime.py:124-136) ->
+  sgl_batch_prepare -> sgl_recent_sample (every hop of the split's sampler)
+  -> sgl_memory_update (GRU + mailbox) -> sgl_memory_commit -> edge rows ->
+  attention forward -> sgl_predictor (edge predictor + BCE) -> attention
+  backward -> fused weight gradients + Adam
 
-Differences by design: the attention runs once per step and its rows are
-selected for src / dst / negatives (the reference runs it three times with
-three dropout masks, runtime.py:193-195 -- identical when dropout is 0, the
-only setting implemented here); no host synchronisation happens inside a step
-unless ``collect_results`` asks for the reference's Python-side result dict.
+The reference runs the attention three times per step, once per role (src,
+dst, negative) with three dropout masks (runtime.py:193-195). With dropout 0
+the three are identical, so the step runs it once and selects rows for the
+three roles; with dropout it runs three passes with independent masks (a
+counter-based generator, so the backward regenerates them). No host
+synchronisation happens inside a step unless ``collect_results`` asks for the
+reference's Python-side result dict.
 """
 from __future__ import annotations
 
@@ -112,6 +115,8 @@ class CTDGOnlineRuntime:
         self._seq = 0
         self._need_back = self._prev_seq = 0
         self._state_writes = memory.state.writes
+        # training steps so far (the dropout masks' step; sgl_adam_coef advances it)
+        self._rng_counter = torch.zeros(1, dtype=torch.int64, device=self.device)
 
     def _make_steps(self, max_batch: int) -> None:
         # every hop of the sampler (history layers, sampler.py:76-90) is
@@ -119,10 +124,17 @@ class CTDGOnlineRuntime:
         hops = [int(f) for f in self.sampler.fanout[:max(1, int(self.sampler.history))]]
         if len(hops) < int(self.sampler.history):
             raise RuntimeError(f"ParallelSampler: num_layers {self.sampler.history} > len(fanouts) {len(hops)}")
-        self.steps = [DeviceStep(self.memory.state, self.dims, max_batch, more_fanouts=tuple(hops[1:]))
-                      for _ in range(2)]
+        self._passes = self._dropout_passes()
+        self.steps = [DeviceStep(self.memory.state, self.dims, max_batch, more_fanouts=tuple(hops[1:]),
+                                 passes=self._passes) for _ in range(2)]
         self._parity = 0
         self.step = self.steps[0]   # the step buffers of the latest step
+
+    def _dropout_passes(self) -> int:
+        """3 attention passes per training step when a dropout is on
+        (runtime.py:193-195), else 1."""
+        conv = self._core().conv
+        return 3 if (conv.dropout.p > 0 or conv.att_dropout.p > 0) else 1
 
     def fence(self) -> None:
         """Order the next step after all work queued so far on the current
@@ -282,14 +294,9 @@ class CTDGOnlineRuntime:
     # ------------------------------------------------------------- the step
     def _forward(self, batch: CTDGDataBatch, split: str, train: bool) -> StepTensors:
         n = batch.size
-        if n > self.steps[0].buf.max_batch:
-            self._make_steps(n)
+        if n > self.steps[0].buf.max_batch or self._dropout_passes() != self._passes:
+            self._make_steps(max(n, self.steps[0].buf.max_batch))
             self.reset_plans()
-        if train:
-            conv = self._core().conv
-            if conv.dropout.p > 0 or conv.att_dropout.p > 0:
-                raise NotImplementedError("dropout > 0 is not implemented by the MI355X attention kernels; set "
-                                          "ctdg.dropout and ctdg.att_dropout to 0")
         q = self._parity
         self._parity = q ^ 1
         step = self.steps[q]
@@ -422,10 +429,12 @@ class CTDGOnlineRuntime:
         else:
             out_grads = None
         pdet = [p.detach() for p in pparams]
-        step.conv_forward(cparams, efeat_all)
-        step.predictor(n, train, pdet, out_grads)
+        drop = conv.drop_args() if train else None
+        passes = step.buf.passes if drop is not None else 1
+        step.conv_forward(cparams, efeat_all, drop=drop)
+        step.predictor(n, train, pdet, out_grads, passes=passes)
         if train:
-            step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]))
+            step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]), drop=drop)
             upd.run()
 
     def _param_update(self, step: DeviceStep) -> StepParamUpdate:
@@ -439,7 +448,8 @@ class CTDGOnlineRuntime:
             core = self._core()
             pred = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
                     core.out_fc.bias]
-            upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None])
+            upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None],
+                                  passes=step.buf.passes, counter=self._rng_counter)
             self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
             self._updates[id(step)] = upd
         return upd

@@ -95,12 +95,14 @@ class StepBuffers:
     have), so launch shapes never depend on the batch."""
 
     def __init__(self, max_batch: int, dims: ConvDims, device, attention: bool = True,
-                 more_fanouts: tuple[int, ...] = ()):
+                 more_fanouts: tuple[int, ...] = (), passes: int = 1):
         """``attention`` False: only the buffers of the front part (batch
         preparation, sampling, memory / mailbox update, commit, edge rows).
         ``more_fanouts``: the fanouts of the hops after hop 0 (history > 1):
         hop l's queries are hop l-1's padded rows, so it holds
-        cap * fanout_0 * ... * fanout_l slots."""
+        cap * fanout_0 * ... * fanout_l slots. ``passes``: 3 for training with
+        dropout (the attention runs once per role, runtime.py:193-195, each
+        pass with its own saved state, stacked along the rows), else 1."""
         dev = torch.device(device)
         self.device = dev
         self.max_batch = int(max_batch)
@@ -144,44 +146,56 @@ class StepBuffers:
         self.X = z(max(c * k * C, 1))
         if not attention:
             return
-        # attention saved state and gradients
-        self.Q, self.agg, self.z = z(c, D), z(c, D), z(c, D)
-        self.y = z(c + TILE, D)          # rows >= cap stay zero (row U is read by the predictor's reductions)
-        self.qt, self.xbar = z(c, H, C), z(c, H, C)
-        self.score, self.ml, self.stats = z(max(c * k * H, 1)), z(c, H, 2), z(c, 2)
+        # attention saved state and gradients, `passes` blocks of rows
+        P = self.passes = int(passes)
+        self.Q, self.agg, self.z = z(P * c, D), z(P * c, D), z(P * c, D)
+        # rows >= cap of each pass stay zero (row U is read by the predictor's reductions)
+        self.y_rows = c + TILE
+        self.y = z(P * self.y_rows, D)
+        self.qt, self.xbar = z(P * c, H, C), z(P * c, H, C)
+        self.score, self.ml, self.stats = z(max(P * c * k * H, 1)), z(P * c, H, 2), z(P * c, 2)
+        self.sdrop = z(P * c, H)                      # kept-weight sums of attention dropout
+        self.rng_step = z(1, dt=i64)                  # the dropout masks' step (sgl_adam_coef)
         self.phi0 = z(max(dims.T, 1))
         self.S = z(max(c * k * dims.T, 1))   # the sines of the edges' time encodings
         self.gy = z(c, D)
         # per-root sums of the predictor's hidden-layer gradients (+ the
         # non-root-negatives row U): fixed-point accumulators the predictor
         # adds into and the attention backward clears (zero between steps),
-        # and their float values for the weight reductions
-        self.acc_src, self.acc_dst = z(c + 1, D, dt=i64), z(c + 1, D, dt=i64)
-        self.g_src, self.g_dst = z(c + 1, D), z(c + 1, D)
+        # and their float values for the weight reductions; src, dst (and
+        # with dropout the negatives' own rows), one block of cap + 1 rows each
+        na = 3 if P > 1 else 2
+        self.acc_all, self.g_all = z(na, c + 1, D, dt=i64), z(na, c + 1, D)
+        self.acc_src, self.acc_dst = self.acc_all[0], self.acc_all[1]
+        self.g_src, self.g_dst = self.g_all[0], self.g_all[1]
+        self.acc_neg = self.acc_all[2] if P > 1 else None
+        self.g_neg = self.g_all[2] if P > 1 else None
         self.acc_out = z(D + 2, dt=i64)      # the predictor's loss / out_fc accumulator
         self.pred_done = z(_capi.SGL_DONE_WORDS, dt=i32)   # and its completion counter
         self.pos = z(max(B, 1))
         self.neg = z(max(B, 1))
         self.loss = z(1)
-        self.gz, self.gagg, self.gQ = z(c, D), z(c, D), z(c, D)
-        self.G, self.sigma = z(c, H, C), z(c, H)
+        self.gz, self.gagg, self.gQ = z(P * c, D), z(P * c, D), z(P * c, D)
+        self.G, self.sigma = z(P * c, H, C), z(P * c, H)
         # per-workgroup partial sums of the attention backward: one tile per
         # conv_rows roots
         self.conv_rows = int(_capi.lib().sgl_conv_tile_rows(D, dims.F, dims.T, H))
         if self.conv_rows <= 0 or TILE % self.conv_rows:
             raise RuntimeError(f"sgl_conv_tile_rows: unsupported attention dimensions {dims}")
-        self.ln_part = z(c // self.conv_rows, 2, D)
-        self.te_part = z(c // self.conv_rows, 2, max(dims.T, 1))
+        self.tiles = c // self.conv_rows
+        self.ln_part = z(P * self.tiles, 2, D)
+        self.te_part = z(P * self.tiles, 2, max(dims.T, 1))
 
 
 class DeviceStep:
     """The kernel sequence of one step over a NodeState (no host syncs)."""
 
     def __init__(self, state: NodeState, dims: ConvDims, max_batch: int, attention: bool = True,
-                 more_fanouts: tuple[int, ...] = ()):
+                 more_fanouts: tuple[int, ...] = (), passes: int = 1):
         self.state = state
         self.dims = dims
-        self.buf = StepBuffers(max_batch, dims, state.device, attention=attention, more_fanouts=more_fanouts)
+        self.buf = StepBuffers(max_batch, dims, state.device, attention=attention, more_fanouts=more_fanouts,
+                               passes=passes)
         self.dev = state.device
         self.lib = _capi.lib()
         # optional per-launch timing: a list that receives (name, start, end)
@@ -282,61 +296,91 @@ class DeviceStep:
             "sgl_edge_rows", d.D, d.F, d.T, d.fanout, b.cap, P(b.num_roots), P(st.memory), P(efeat_all),
             P(hop.cnt), P(hop.nbr), P(hop.eid), P(b.X), self._s()), "sgl_edge_rows"))
 
-    def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor) -> torch.Tensor:
+    def _at(self, t: torch.Tensor, p: int, rows: int | None = None) -> int:
+        """Pointer to pass p's block of a pass-stacked buffer (``rows``: the
+        block's element count when it is not the tensor's share)."""
+        n = t.numel() // self.buf.passes if rows is None else rows
+        return t.data_ptr() + p * n * t.element_size()
+
+    def conv_forward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, drop=None) -> torch.Tensor:
         """The attention forward over the edge rows of the last edge_rows()
-        (it adds the rows' time encodings and their sines S)."""
+        (it adds the rows' time encodings and their sines S). ``drop`` =
+        (p_att, p_out, seed): every pass of the buffers with its own dropout
+        masks; None: one pass without dropout."""
         b, d, P = self.buf, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
-        self._call("conv_forward", lambda: _capi.check(_capi.call(
-            "sgl_conv_forward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(b.new_mem),
-            P(b.hop.cnt), P(b.X), P(b.hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out),
-            P(ln_g), P(ln_b), P(te_w), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z),
-            P(b.stats), P(b.phi0), P(b.S), P(b.y), self._s()), "sgl_conv_forward"))
+        pa, po, seed = drop if drop is not None else (0.0, 0.0, 0)
+        for p in range(b.passes if drop is not None else 1):
+            a = lambda t: self._at(t, p)
+            self._call("conv_forward", lambda: _capi.check(_capi.call(
+                "sgl_conv_forward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges),
+                P(b.new_mem), P(b.hop.cnt), P(b.X), P(b.hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
+                P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), a(b.Q), a(b.qt), a(b.xbar), a(b.score),
+                a(b.ml), a(b.agg), a(b.z), a(b.stats), P(b.phi0), P(b.S), self._at(b.y, p, b.y_rows * d.D),
+                pa, po, seed, P(b.rng_step), p, a(b.sdrop), self._s()), "sgl_conv_forward"))
         return b.y
 
-    def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None):
+    def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None,
+                  passes: int = 1):
         """Edge predictor + BCE over the step's roots (sgl_predictor). ``pred``:
         src_fc.weight, src_fc.bias, dst_fc.weight, dst_fc.bias, out_fc.weight,
         out_fc.bias; ``out_grads``: the out_fc weight / bias gradient buffers
         (overwritten). In training the per-root gradient sums are added into
         the step's fixed-point accumulators, which the attention backward
-        (conv_backward_kernel) consumes and clears."""
+        (conv_backward_kernel) consumes and clears. ``passes`` 3: src, dst
+        and negative rows from the three dropout passes' outputs, the
+        negatives' sums in their own rows."""
         b, P = self.buf, _capi.ptr
         g = out_grads if (train and out_grads is not None) else [None, None]
+        ys = b.y_rows * self.dims.D if passes > 1 else 0
+        acc_neg = P(b.acc_neg) if (train and passes > 1) else None
         self._call("predictor", lambda: _capi.check(_capi.call(
             "sgl_predictor", n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src),
             P(b.ridx_dst), P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]),
             P(b.pos), P(b.neg), P(b.loss), P(b.acc_src) if train else None, P(b.acc_dst) if train else None,
-            P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), self._s()), "sgl_predictor"))
+            P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), ys, acc_neg, self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
     def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor,
-                             gy: torch.Tensor | None = None, pred_w: tuple | None = None) -> None:
+                             gy: torch.Tensor | None = None, pred_w: tuple | None = None, drop=None) -> None:
         """sgl_conv_backward only: per-root gradient rows and per-tile partials
         in the step buffers (the weight gradients are StepParamUpdate's).
         dL/dy is ``gy``, or (gy None) comes from the predictor's per-root rows
-        with ``pred_w`` = (src_fc.weight, dst_fc.weight)."""
+        with ``pred_w`` = (src_fc.weight, dst_fc.weight). With ``drop`` (the
+        forward's) every pass runs: pass 0 takes dL/dy from the src rows and
+        src_fc, pass 1 from the dst rows and dst_fc, pass 2 from the
+        negatives' rows and dst_fc."""
         b, d, P = self.buf, self.dims, _capi.ptr
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         hop = b.hop
+        pa, po, seed = drop if drop is not None else (0.0, 0.0, 0)
+        passes = b.passes if drop is not None else 1
         if gy is not None:
             gy = gy.contiguous()
-            acc_src = acc_dst = g_src = g_dst = w_s = w_d = None
-        else:
-            acc_src, acc_dst, g_src, g_dst = b.acc_src, b.acc_dst, b.g_src, b.g_dst
-            w_s, w_d = pred_w
-        self._call("conv_backward", lambda: _capi.check(_capi.call(
-            "sgl_conv_backward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges), P(hop.cnt),
-            P(b.X), P(b.S), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out), P(b_out), P(ln_g),
-            P(ln_b), P(te_b), P(b.Q), P(b.qt), P(b.xbar), P(b.score), P(b.ml), P(b.agg), P(b.z), P(b.stats),
-            P(gy), P(acc_src), P(acc_dst), P(w_s), P(w_d), P(g_src), P(g_dst), P(b.gz), P(b.gagg), P(b.G),
-            P(b.sigma), P(b.gQ), P(b.ln_part), P(b.te_part), self._s()), "sgl_conv_backward"))
+        for p in range(passes):
+            if gy is not None:
+                acc_a = acc_b = g_a = g_b = w_a = w_b = None
+            elif passes == 1:
+                acc_a, acc_b, g_a, g_b = b.acc_src, b.acc_dst, b.g_src, b.g_dst
+                w_a, w_b = pred_w
+            else:
+                acc_a, g_a, w_a = b.acc_all[p], b.g_all[p], pred_w[0 if p == 0 else 1]
+                acc_b = g_b = w_b = None
+            a = lambda t: self._at(t, p)
+            self._call("conv_backward", lambda: _capi.check(_capi.call(
+                "sgl_conv_backward", d.D, d.F, d.T, d.H, d.fanout, b.cap, P(b.num_roots), P(b.any_edges),
+                P(hop.cnt), P(b.X), P(b.S), P(hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v), P(w_out),
+                P(b_out), P(ln_g), P(ln_b), P(te_b), a(b.Q), a(b.qt), a(b.xbar), a(b.score), a(b.ml), a(b.agg),
+                a(b.z), a(b.stats), P(gy), P(acc_a), P(acc_b), P(w_a), P(w_b), P(g_a), P(g_b), a(b.gz), a(b.gagg),
+                a(b.G), a(b.sigma), a(b.gQ), a(b.ln_part), a(b.te_part), pa, po, seed, P(b.rng_step), p,
+                a(b.sdrop), self._s()), "sgl_conv_backward"))
 
-    def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor):
+    def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor, drop=None):
         """The backward kernel plus the weight gradients as torch products (the
-        autograd path). Returns the 12 parameter gradients (TimeEncode w, b;
-        w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln weight, ln bias)."""
-        self.conv_backward_kernel(params, efeat_all, gy)
+        autograd path, one pass). Returns the 12 parameter gradients
+        (TimeEncode w, b; w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln
+        weight, ln bias)."""
+        self.conv_backward_kernel(params, efeat_all, gy, drop=drop)
         b, d = self.buf, self.dims
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = params
         # weight gradients: per-root products reduced over the live root rows
@@ -349,7 +393,10 @@ class DeviceStep:
         g_b_out = gz.sum(0)
         ga = gagg.reshape(c, H, dh).permute(1, 2, 0).contiguous()          # [H, dh, U]
         g_w_v = torch.bmm(ga, b.xbar[:c].permute(1, 0, 2).contiguous()).reshape(D, C)
-        g_b_v = gagg.sum(0)
+        if drop is not None and drop[0] > 0:   # the kept weights sum to s_h, not 1
+            g_b_v = (gagg.reshape(c, H, dh) * b.sdrop[:c].unsqueeze(-1)).sum(0).reshape(D)
+        else:
+            g_b_v = gagg.sum(0)
         qh = b.Q[:c].reshape(c, H, dh)
         g_w_k = torch.bmm(qh.permute(1, 2, 0).contiguous(), b.G[:c].permute(1, 0, 2).contiguous()).reshape(D, C)
         g_b_k = (qh * b.sigma[:c].unsqueeze(-1)).sum(0).reshape(D)
@@ -374,13 +421,21 @@ class StepParamUpdate:
     edges" flag; segment 1 (the edge predictor) takes its gradients from
     sgl_predictor (Adam-only jobs). Each step-buffer set has its own bias
     corrections, so one step's advance may run while the previous step's
-    update still reads its own."""
+    update still reads its own. ``passes`` 3 (dropout): every attention
+    gradient sums the three passes' rows, dst_fc's the dst and negative
+    passes'; ``counter`` (device int64): the training-step counter the
+    advance increments and copies to the buffers' dropout step."""
 
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
-                 pred_params: list[torch.Tensor], gates: list[torch.Tensor | None]):
+                 pred_params: list[torch.Tensor], gates: list[torch.Tensor | None], passes: int = 1,
+                 counter: torch.Tensor | None = None):
         if len(opt.segments) != 2:
             raise ValueError("StepParamUpdate expects the attention and predictor segments")
+        if passes not in (1, step.buf.passes):
+            raise ValueError(f"StepParamUpdate: {passes} passes on buffers of {step.buf.passes}")
         self.step, self.opt = step, opt
+        self.passes = int(passes)
+        self.counter = counter
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
@@ -419,36 +474,56 @@ class StepParamUpdate:
             tiles.extend([len(jobs)] * ntile)
             jobs.append(job)
 
-        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0):
+        P = self.passes
+        c = b.cap
+
+        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0, npass=1, ps1=0, ps2=0):
             assert s1 >= rows
             tb = (cols + 15) // 16
-            add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ldo=ldo, rows=rows, cols=cols, kind=0, seg=seg,
-                              r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb), ((rows + 15) // 16) * tb)
+            add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ps1=ps1, ps2=ps2, ldo=ldo, rows=rows, cols=cols,
+                              kind=0, seg=seg, r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb, npass=npass),
+                ((rows + 15) // 16) * tb)
+
+        # the attention's reductions run over every pass's rows (rows of
+        # width w: pass stride c * w; the per-tile partials: ntiles * w)
+        def conv(x1, s1, x2, s2, o, ldo, rows, cols, x1w=None, x2w=None, r_fixed=-1):
+            gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=r_fixed, npass=P,
+                 ps1=0 if x1w is None else x1w, ps2=0 if x2w is None else x2w)
 
         one = at(self.one)
-        gemm(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, ntiles)
-        gemm(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, ntiles)
-        gemm(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D)
-        gemm(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T)
-        gemm(at(b.gQ), D, one, 0, off(b_q), 1, D, 1)
+        conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
+        conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
+        conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D)
+        conv(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T, x1w=c * D)
+        conv(at(b.gQ), D, one, 0, off(b_q), 1, D, 1, x1w=c * D)
         for h in range(H):
-            gemm(at(b.Q, h * dh), D, at(b.G, h * C), H * C, off(w_k) + h * dh * C, C, dh, C)
-            gemm(at(b.Q, h * dh), D, at(b.sigma, h), H, off(b_k) + h * dh, 1, dh, 1)
-            gemm(at(b.gagg, h * dh), D, at(b.xbar, h * C), H * C, off(w_v) + h * dh * C, C, dh, C)
-        gemm(at(b.gagg), D, one, 0, off(b_v), 1, D, 1)
-        gemm(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D)
-        gemm(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D)
-        gemm(at(b.gz), D, one, 0, off(b_out), 1, D, 1)
-        gemm(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, ntiles)
-        gemm(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, ntiles)
+            conv(at(b.Q, h * dh), D, at(b.G, h * C), H * C, off(w_k) + h * dh * C, C, dh, C, x1w=c * D,
+                 x2w=c * H * C)
+            conv(at(b.Q, h * dh), D, at(b.sigma, h), H, off(b_k) + h * dh, 1, dh, 1, x1w=c * D, x2w=c * H)
+            conv(at(b.gagg, h * dh), D, at(b.xbar, h * C), H * C, off(w_v) + h * dh * C, C, dh, C, x1w=c * D,
+                 x2w=c * H * C)
+        if P > 1:   # attention dropout: agg_h = W_v xbar'_h + s_h b_v[h]
+            for h in range(H):
+                conv(at(b.gagg, h * dh), D, at(b.sdrop, h), H, off(b_v) + h * dh, 1, dh, 1, x1w=c * D, x2w=c * H)
+        else:
+            conv(at(b.gagg), D, one, 0, off(b_v), 1, D, 1, x1w=c * D)
+        conv(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D, x1w=c * D, x2w=c * D)
+        conv(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D, x1w=c * D)
+        conv(at(b.gz), D, one, 0, off(b_out), 1, D, 1, x1w=c * D)
+        conv(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
+        conv(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
         # edge predictor: src_fc / dst_fc as reductions over roots 0..U (row U
         # of g_dst holds the non-root negatives; y's row U is zero); out_fc's
-        # gradients come from sgl_predictor (Adam only)
+        # gradients come from sgl_predictor (Adam only). With dropout dst_fc
+        # sums the dst pass's rows and the negatives' pass's rows
         w_s, b_s, w_d, b_d, w_o, b_o = pred_params
+        nd = 2 if P > 1 else 1
+        gs, ys = (c + 1) * D, b.y_rows * D
+        yd = at(b.y, ys) if P > 1 else at(b.y)
         gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, seg=1, r_extra=1)
         gemm(at(b.g_src), D, one, 0, off(b_s), 1, D, 1, seg=1, r_extra=1)
-        gemm(at(b.g_dst), D, at(b.y), D, off(w_d), D, D, D, seg=1, r_extra=1)
-        gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, seg=1, r_extra=1)
+        gemm(at(b.g_dst), D, yd, D, off(w_d), D, D, D, seg=1, r_extra=1, npass=nd, ps1=gs, ps2=ys)
+        gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, seg=1, r_extra=1, npass=nd, ps1=gs)
         if off(b_o) != off(w_o) + D:
             raise RuntimeError("StepParamUpdate: out_fc weight and bias are not contiguous in the flat buffer")
         add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=off(w_o), ldo=1, rows=D + 1, cols=1, kind=1, seg=1,
@@ -465,7 +540,8 @@ class StepParamUpdate:
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
         b1, b2 = opt.betas
         _capi.check(_capi.call("sgl_adam_coef", len(opt.segments), self._steps, self._gates, P(self.coef), opt.lr,
-                               b1, b2, s), "sgl_adam_coef")
+                               b1, b2, P(self.counter), P(self.step.buf.rng_step) if self.counter is not None else None,
+                               s), "sgl_adam_coef")
 
     def run(self) -> None:
         """Gradients + Adam with the bias corrections of the last advance()."""
@@ -481,17 +557,22 @@ class ConvFunction(torch.autograd.Function):
     """Autograd node for the attention: forward/backward are the HIP kernels."""
 
     @staticmethod
-    def forward(ctx, step: DeviceStep, efeat_all: torch.Tensor, *params):
+    def forward(ctx, step: DeviceStep, efeat_all: torch.Tensor, drop, *params):
+        """``drop``: (p_att, p_out, seed) for one dropout pass (pass 0, the
+        buffers' current step counter), or None."""
+        if drop is not None and step.buf.passes != 1:
+            raise RuntimeError("ConvFunction runs one pass; use step buffers made with passes=1")
         ctx.step = step
         ctx.efeat_all = efeat_all
         ctx.params = params
+        ctx.drop = drop
         step.edge_rows(efeat_all)
-        return step.conv_forward(list(params), efeat_all)
+        return step.conv_forward(list(params), efeat_all, drop=drop)
 
     @staticmethod
     def backward(ctx, gy):
-        grads = ctx.step.conv_backward(list(ctx.params), ctx.efeat_all, gy)
-        return (None, None, *grads)
+        grads = ctx.step.conv_backward(list(ctx.params), ctx.efeat_all, gy, drop=ctx.drop)
+        return (None, None, None, *grads)
 
 
 class FusedAdam:

@@ -190,9 +190,9 @@ def _hand_step():
 
     conv_fwd, model_fwd = model.conv.forward, model.forward
 
-    def conv_rec(h_dst, h_nbr, ef_, dt, edge_dst):
+    def conv_rec(h_dst, h_nbr, ef_, dt, edge_dst, *masks):
         seen["conv_in"] = (h_dst.detach().clone(), h_nbr.detach().clone(), ef_.clone(), dt.clone(), edge_dst.clone())
-        out = conv_fwd(h_dst, h_nbr, ef_, dt, edge_dst)
+        out = conv_fwd(h_dst, h_nbr, ef_, dt, edge_dst, *masks)
         seen["conv_out"] = out.detach().clone()
         return out
 
@@ -361,3 +361,23 @@ def test_product_metrics_match_sklearn(seed):
     want = co.metric_dict(pos, neg)
     for k, tol in (("ap", 1e-9), ("auc", 1e-9), ("mrr", 1e-6)):   # the reference's "mrr" is a float32 mean
         assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])
+
+
+def test_philox_known_answers():
+    """The oracle's Philox4x32-10 (the dropout masks' generator) against the
+    known-answer vectors published with Random123 (Salmon et al., SC 2011)."""
+    kat = [((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+           ((0xffffffff,) * 4, (0xffffffff, 0xffffffff), (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+           ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+            (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1))]
+    for ctr, key, want in kat:
+        got = co.philox4x32_10(np.array(ctr, dtype=np.uint32), np.array(key, dtype=np.uint32))
+        assert got.tolist() == list(want)
+
+
+def test_oracle_dropout_masks_scale_and_rate():
+    """Mask values are 0 or 1/(1-p); p = 0 keeps everything."""
+    att, out = co.dropout_masks(3, 7, 1, 500, 20, 4, 64, 0.2, 0.0)
+    assert set(np.unique(att).tolist()) == {0.0, np.float32(1 / 0.8)}
+    assert abs(float((att > 0).mean()) - 0.8) < 0.01
+    assert bool((out == 1.0).all())
