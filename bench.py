@@ -49,8 +49,9 @@ WORKLOADS = {
                       history=1),
     "tgn-small": dict(config="cfg1", stream="bipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=200,
                       history=1),
+    # config 2: memory + GRU + the JODIE time projection, no attention
     "jodie": dict(config="cfg2", stream="bipartite", family="jodie", D=100, T=100, H=2, k=10, K=1, B=200,
-                  history=1),
+                  history=1, embedding="time_projection"),
     "tgn-stress": dict(config="cfg5", stream="unipartite", family="tgn", D=172, T=100, H=4, k=20, K=4, B=4000,
                        history=2),
 }
@@ -394,7 +395,8 @@ def build_session(wl: dict, stream):
            "data": {"name": f"bench_{wl['config']}", "format": "synthetic"},
            "train": {"batch_size": wl["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
            "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"], "dropout": 0.0,
-                    "att_dropout": 0.0, "memory_gemm_dtype": wl.get("gemm", "fp32")},
+                    "att_dropout": 0.0, "memory_gemm_dtype": wl.get("gemm", "fp32"),
+                    "embedding": wl.get("embedding", "attention")},
            "sampling": {"neighbor_limit": [wl["k"]] * wl["history"], "history": wl["history"],
                         "strategy": "recent"}}
     torch.manual_seed(0)
@@ -461,7 +463,9 @@ TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/
 ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_recent_sample",
                 "memory_update": "sgl_memory_update", "memory_commit": "sgl_memory_commit",
                 "edge_rows": "sgl_edge_rows", "conv_forward": "sgl_conv_forward", "predictor": "sgl_predictor",
-                "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam"}
+                "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam",
+                "time_projection": "sgl_time_projection_forward",
+                "time_projection_backward": "sgl_time_projection_backward"}
 
 
 def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float, float]:

@@ -253,13 +253,16 @@ int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
  * Replaces CTDGMemoryBank._apply_memory_update (memory.py:254-269):
  * memory[roots[r]] = new_mem[r], memory_ts[roots[r]] = ts_max for r < U.
  * Also clears node_bits for the next batch and sets any_edges = 1 if some
- * root has sample_cnt[r] > 0 (sample_cnt may be NULL).
+ * root has sample_cnt[r] > 0 (sample_cnt may be NULL). root_dt (may be
+ * NULL) receives ts_max - memory_ts[roots[r]] as it was before the write:
+ * the time since the root's previous update (the time-projection
+ * embedding's input).
  * ------------------------------------------------------------------------- */
 int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots,
                       const int64_t *roots, const float *new_mem,
                       float *memory, float *memory_ts, const float *ts_max,
                       uint32_t *node_bits, const int32_t *sample_cnt,
-                      int32_t *any_edges, hipStream_t stream);
+                      int32_t *any_edges, float *root_dt, hipStream_t stream);
 /* The same step point without a memory updater: rows[r] = memory[roots[r]]
  * for r < U (the attention's root rows), node_bits cleared and any_edges set
  * as above; memory and memory_ts are not written. Replaces the gather of
@@ -378,6 +381,30 @@ int sgl_dropout_masks(int64_t rows, int32_t fanout, int32_t H, int32_t D,
                       float p_att, float p_out, uint64_t seed,
                       const uint64_t *rng_step, int32_t pass, float *att_mask,
                       float *out_mask, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Time-projection embedding (config 2's JODIE model: memory + GRU + a time
+ * projection, no attention). The reference builds its TGN model for family
+ * "jodie" (backends/ctdg/runtime/models.py:337-338); this embedding follows
+ * the JODIE paper (h(t + Delta) = (1 + W_p Delta) * h(t)) and is selected by
+ * ctdg.embedding = time_projection:
+ *   y[r] = h_root[r] * (1 + w * x_r + b),  x_r = (root_dt[r] - shift) * scale
+ * for r < U, y rows U .. rows-1 zero (rows >= capacity + 1). w, b [D]
+ * (nn.Linear(1, D) weight and bias). The backward takes dL/dy = W_s^T g_src +
+ * W_d^T g_dst from sgl_predictor's fixed-point rows (consumed, cleared and
+ * written as floats to g_src / g_dst [cap+1][D], as sgl_conv_backward does)
+ * and writes per-tile partial sums part [cap/16][2][D] of dL/dw and dL/db
+ * (reduced by sgl_grad_adam jobs). capacity % 16 == 0.
+ * ------------------------------------------------------------------------- */
+int sgl_time_projection_forward(int32_t D, int64_t rows, const int32_t *num_roots,
+                                const float *h_root, const float *root_dt, float shift,
+                                float scale, const float *w, const float *b, float *y,
+                                hipStream_t stream);
+int sgl_time_projection_backward(int32_t D, int64_t capacity, const int32_t *num_roots,
+                                 const float *h_root, const float *root_dt, float shift,
+                                 float scale, int64_t *acc_src, int64_t *acc_dst,
+                                 const float *w_s, const float *w_d, float *g_src,
+                                 float *g_dst, float *part, hipStream_t stream);
 
 /* Fractional bits of the fixed-point int64 accumulators (value = v * 2^-40)
  * that sgl_predictor scatters into and sgl_conv_backward consumes: integer

@@ -20,6 +20,9 @@ Follows, function by function:
   train_step             runtime.py:225-328 (dropout as explicit masks: the
                          GPU kernels' masks are replayed, torch's own draws
                          cannot be matched)
+  ProjectionPredictorO   config 2's JODIE time projection (the build's own
+                         definition: the reference has none), pinned by a
+                         closed form
   philox4x32_10          the counter-based generator of the kernels' dropout
                          masks (Salmon et al., SC 2011), pinned by the
                          published known-answer vectors
@@ -147,6 +150,34 @@ class LinkPredictorO(nn.Module):
         pos = self.out_fc(F.relu(h_src + h_dst)).squeeze(-1)
         neg = self.out_fc(F.relu(h_src + h_neg)).squeeze(-1)
         return pos, neg
+
+
+class ProjectionPredictorO(nn.Module):
+    """Config 2's JODIE model (no reference counterpart: the reference's
+    "jodie" is its TGN model, models.py:337-338): the updated memory h of a
+    root embedded as h * (1 + proj(x)), proj = nn.Linear(1, D), x = (dt -
+    shift) * scale with dt the time since the root's previous memory update
+    (JODIE, KDD 2019, eq. 3), then the edge predictor of LinkPredictorO."""
+
+    def __init__(self, hidden_dim, shift=0.0, scale=1.0):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.time_proj = nn.Module()
+        self.time_proj.proj = nn.Linear(1, hidden_dim)
+        nn.init.normal_(self.time_proj.proj.weight, 0.0, 0.1)
+        nn.init.zeros_(self.time_proj.proj.bias)
+        self.shift, self.scale = float(shift), float(scale)
+        self.src_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.dst_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.out_fc = nn.Linear(hidden_dim, 1)
+
+    def embed(self, h, dt):
+        """h [R, D] updated memory, dt [R] float32 time since the previous update."""
+        x = (dt - torch.tensor(self.shift, dtype=dt.dtype)) * torch.tensor(self.scale, dtype=dt.dtype)
+        lin = x.to(h.dtype).unsqueeze(1) * self.time_proj.proj.weight.reshape(1, -1) + self.time_proj.proj.bias
+        return h * (1.0 + lin)
+
+    forward = LinkPredictorO.forward
 
 
 class MemoryUpdaterO(nn.Module):
@@ -366,6 +397,7 @@ def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts,
     Returns a dict of the step's tensors."""
     roots, tq = prepare_roots(src, dst, ts)
     blk = sample_fn(roots, tq)
+    mts_prev = mem.memory_ts.clone()
     if updater is not None:   # runtime.py:283-285: without one, memory and mailbox stay as they are
         memory_phase(mem, updater, src, dst, ts, edge_feat)
     if after_memory is not None:
@@ -375,7 +407,12 @@ def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts,
     else:
         model.eval()
     with torch.set_grad_enabled(train):
-        if masks is None:
+        if isinstance(model, ProjectionPredictorO):
+            # time since the previous update: batch max time - memory_ts before the update (float32)
+            dt = torch.tensor(float(ts.max().item()), dtype=torch.float32) - mts_prev[roots]
+            conv = model.embed(mem.memory[roots].detach(), dt)
+            convs = (conv, conv, conv)
+        elif masks is None:
             conv = conv_all(model, mem.memory, roots, blk, edge_feat_all)
             convs = (conv, conv, conv)
         else:

@@ -80,7 +80,8 @@ const OpEntry kOps[] = {
     SGL_OP(sgl_batch_prepare), SGL_OP(sgl_recent_sample), SGL_OP(sgl_memory_update), SGL_OP(sgl_memory_commit),
     SGL_OP(sgl_conv_forward),  SGL_OP(sgl_predictor),     SGL_OP(sgl_conv_backward), SGL_OP(sgl_grad_adam),
     SGL_OP(sgl_adam_coef),     SGL_OP(sgl_edge_rows),     SGL_OP(sgl_memory_update_bf16),
-    SGL_OP(sgl_recent_sample_packed), SGL_OP(sgl_memory_gather),
+    SGL_OP(sgl_recent_sample_packed), SGL_OP(sgl_memory_gather), SGL_OP(sgl_negatives_from_draws),
+    SGL_OP(sgl_time_projection_forward), SGL_OP(sgl_time_projection_backward),
 };
 #undef SGL_OP
 constexpr int kNumOps = int(sizeof(kOps) / sizeof(kOps[0]));

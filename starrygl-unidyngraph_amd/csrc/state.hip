@@ -635,7 +635,7 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
     int D, bool vec4, bool gather, int64_t cap, const int32_t *__restrict__ num_roots,
     const int64_t *__restrict__ roots, float *__restrict__ rows, float *__restrict__ memory,
     float *__restrict__ memory_ts, const float *__restrict__ ts_max, uint32_t *__restrict__ bits,
-    const int32_t *__restrict__ sample_cnt, int32_t *__restrict__ any_edges) {
+    const int32_t *__restrict__ sample_cnt, int32_t *__restrict__ any_edges, float *__restrict__ root_dt) {
   // grid-stride over the live roots' elements (the grid is bounded, so a
   // large capacity with few live roots costs no idle workgroups), four at a
   // time when the rows allow 16-byte accesses. Commit: memory[roots[r]] =
@@ -657,7 +657,10 @@ __global__ __launch_bounds__(kBlock) void k_memory_commit(
       if (gather) rows[r * D + j] = memory[u * D + j]; else memory[u * D + j] = rows[r * D + j];
     }
     if (j == 0) {
-      if (!gather) memory_ts[u] = tmax;
+      if (!gather) {
+        if (root_dt != nullptr) root_dt[r] = tmax - memory_ts[u];  // time since the root's last update
+        memory_ts[u] = tmax;
+      }
       bits[u >> 5] = 0u;  // leave the bitmap clear for the next step
       if (sample_cnt != nullptr && sample_cnt[r] > 0) *any_edges = 1;
     }
@@ -819,7 +822,8 @@ extern "C" int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t c
 
 static int memory_rows(const char *what, bool gather, int32_t D, int64_t capacity, const int32_t *num_roots,
                        const int64_t *roots, float *rows, float *memory, float *memory_ts, const float *ts_max,
-                       uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges, hipStream_t stream) {
+                       uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges, float *root_dt,
+                       hipStream_t stream) {
   SGL_REQUIRE(D > 0, "%s: D <= 0", what);
   SGL_REQUIRE(capacity >= 0, "%s: capacity < 0", what);
   if (capacity == 0) return SGL_OK;
@@ -829,7 +833,7 @@ static int memory_rows(const char *what, bool gather, int32_t D, int64_t capacit
   const int64_t total = capacity * (vec4 ? D / 4 : D);
   const unsigned grid = unsigned(std::min<int64_t>((total + kBlock - 1) / kBlock, sgl::kMaxGrid));
   sgl::launch(&k_memory_commit, dim3(grid), dim3(kBlock), 0, stream, D, vec4, gather, capacity,
-              num_roots, roots, rows, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges);
+              num_roots, roots, rows, memory, memory_ts, ts_max, node_bits, sample_cnt, any_edges, root_dt);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -837,14 +841,14 @@ static int memory_rows(const char *what, bool gather, int32_t D, int64_t capacit
 extern "C" int sgl_memory_commit(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
                                  const float *new_mem, float *memory, float *memory_ts, const float *ts_max,
                                  uint32_t *node_bits, const int32_t *sample_cnt, int32_t *any_edges,
-                                 hipStream_t stream) {
+                                 float *root_dt, hipStream_t stream) {
   return memory_rows("memory_commit", false, D, capacity, num_roots, roots, const_cast<float *>(new_mem), memory,
-                     memory_ts, ts_max, node_bits, sample_cnt, any_edges, stream);
+                     memory_ts, ts_max, node_bits, sample_cnt, any_edges, root_dt, stream);
 }
 
 extern "C" int sgl_memory_gather(int32_t D, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
                                  const float *memory, float *rows, uint32_t *node_bits, const int32_t *sample_cnt,
                                  int32_t *any_edges, hipStream_t stream) {
   return memory_rows("memory_gather", true, D, capacity, num_roots, roots, rows, const_cast<float *>(memory),
-                     nullptr, nullptr, node_bits, sample_cnt, any_edges, stream);
+                     nullptr, nullptr, node_bits, sample_cnt, any_edges, nullptr, stream);
 }

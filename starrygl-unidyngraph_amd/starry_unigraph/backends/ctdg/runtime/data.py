@@ -93,6 +93,25 @@ class TGTemporalDataset:
             ids = self._split_cache[split] = torch.arange(a, b, dtype=torch.long)
         return ids
 
+    def inter_event_stats(self, split: str = "train") -> tuple[float, float]:
+        """(shift, scale) for the time-projection embedding: the mean of the
+        times between a node's consecutive events (either endpoint) within
+        the split, and 1 / their standard deviation (1 when undefined)."""
+        ids = self.split_event_ids(split)
+        if ids.numel() < 2:
+            return 0.0, 1.0
+        a, b = int(ids[0]), int(ids[-1]) + 1
+        nodes = torch.cat([self.src[a:b], self.dst[a:b]]).numpy()
+        ts = torch.cat([self.ts[a:b], self.ts[a:b]]).double().numpy()
+        order = np.lexsort((ts, nodes))
+        n, t = nodes[order], ts[order]
+        same = n[1:] == n[:-1]
+        gaps = (t[1:] - t[:-1])[same]
+        if gaps.size < 2:
+            return 0.0, 1.0
+        sd = float(gaps.std())
+        return float(gaps.mean()), (1.0 / sd if sd > 0 else 1.0)
+
     def _build_node_feat_history(self):
         """data.py:128-140: each node's feature rows in time order (rows of a
         node with equal times keep their order in the time-sorted table), as

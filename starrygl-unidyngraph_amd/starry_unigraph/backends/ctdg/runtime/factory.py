@@ -50,9 +50,12 @@ def build_ctdg_runtime(session_ctx: SessionContext, events=None) -> tuple[CTDGOn
                                 world_size=session_ctx.dist.world_size)
     memory = CTDGMemoryBank(num_nodes=dataset.num_nodes, hidden_dim=hidden_dim, device=device,
                             mailbox_slots=mailbox_slots, edge_feat_dim=edge_feat_dim)
+    embedding = str(c.get("embedding", "attention"))
+    shift, scale = dataset.inter_event_stats("train") if embedding == "time_projection" else (0.0, 1.0)
     model = build_ctdg_model(str(cfg["model"]["family"]), num_nodes=dataset.num_nodes, hidden_dim=hidden_dim,
                              edge_feat_dim=edge_feat_dim, dim_time=dim_time, num_head=num_head, dropout=dropout,
-                             att_dropout=att_dropout).to(device)
+                             att_dropout=att_dropout, embedding=embedding, time_shift=shift,
+                             time_scale=scale).to(device)
     memory_updater = CTDGMemoryUpdater(hidden_dim=hidden_dim, mailbox_slot_dim=2 * hidden_dim + edge_feat_dim,
                                        mailbox_slots=mailbox_slots,
                                        gemm_dtype=str(c.get("memory_gemm_dtype", "fp32"))).to(device)
@@ -61,7 +64,8 @@ def build_ctdg_runtime(session_ctx: SessionContext, events=None) -> tuple[CTDGOn
                                 route=_SingleRankRoute(str(cfg["graph"]["route"]), session_ctx.dist.world_size),
                                 device=device, dist_ctx=session_ctx.dist, memory_updater=memory_updater,
                                 max_batch=int(cfg["train"]["batch_size"]))
-    optimizer.gate_fn = lambda: runtime.step.buf.any_edges
+    if getattr(model, "conv", None) is not None:
+        optimizer.gate_fn = lambda: runtime.step.buf.any_edges
     optimizer.inner  # re-seat the parameters in the optimizer's flat buffers before any forward
     bundle = RuntimeBundle(model=model, optimizer=optimizer,
                            state={"pipeline": "ctdg_online_native", "dataset": dataset.describe(),
@@ -74,10 +78,11 @@ def make_optimizer(model: torch.nn.Module, lr: float) -> "GatedAdam":
 
 
 class GatedAdam:
-    """Adam over the link predictor's parameters (factory.py:122-128). The
-    attention's segment is gated by the step's "block has edges" flag (when
-    it is 0 those parameters have no gradient in the reference, and Adam
-    skips them). The memory updater gets no gradients in the reference
+    """Adam over the link predictor's parameters (factory.py:122-128), in two
+    segments: the embedding's (the attention, or the time projection) and
+    the edge predictor's. The attention's segment is gated by the step's
+    "block has edges" flag (when it is 0 those parameters have no gradient
+    in the reference, and Adam skips them). The memory updater gets no gradients in the reference
     (runtime.py:279) and is not optimised."""
 
     def __init__(self, model: torch.nn.Module, lr: float):
@@ -88,7 +93,7 @@ class GatedAdam:
 
     def _build(self) -> FusedAdam:
         core = self.model.module if hasattr(self.model, "module") else self.model
-        conv = list(core.conv.parameters())
+        conv = list(core.embedding_module().parameters())
         conv_ids = {id(p) for p in conv}
         rest = [p for p in core.parameters() if id(p) not in conv_ids]
         return FusedAdam([conv, rest], lr=self.lr)

@@ -178,12 +178,60 @@ class CTDGLinkPredictor(nn.Module):
         self.dst_fc = nn.Linear(hidden_dim, hidden_dim)
         self.out_fc = nn.Linear(hidden_dim, 1)
 
+    def embedding_module(self) -> nn.Module:
+        """The module that embeds the roots (its parameters are the
+        optimizer's first segment)."""
+        return self.conv
+
     def forward(self, src_conv: torch.Tensor, dst_conv: torch.Tensor, neg_conv: torch.Tensor) -> CTDGModelOutput:
         h_src = self.src_fc(src_conv)
         h_dst = self.dst_fc(dst_conv)
         h_neg = self.dst_fc(neg_conv)
         pos_logits = self.out_fc(F.relu(h_src + h_dst)).squeeze(-1)
         neg_logits = self.out_fc(F.relu(h_src + h_neg)).squeeze(-1)
+        return CTDGModelOutput(pos_logits=pos_logits, neg_logits=neg_logits)
+
+
+class TimeProjection(nn.Module):
+    """JODIE's time projection (Kumar, Zhang, Leskovec, KDD 2019, eq. 3):
+    h * (1 + proj(x)) with proj = nn.Linear(1, D) and x the time since the
+    node's previous memory update, normalised as (dt - shift) * scale
+    (shift / scale: the mean and the inverse spread of the training
+    split's per-node inter-event times). Evaluated by
+    sgl_time_projection_forward / _backward on the step's roots."""
+
+    def __init__(self, dim: int, shift: float = 0.0, scale: float = 1.0) -> None:
+        super().__init__()
+        self.proj = nn.Linear(1, dim)
+        nn.init.normal_(self.proj.weight, 0.0, 0.1)
+        nn.init.zeros_(self.proj.bias)
+        self.shift, self.scale = float(shift), float(scale)
+
+
+class CTDGTimeProjectionPredictor(nn.Module):
+    """Config 2's JODIE model: the node memory (GRU updater) embedded by a
+    time projection instead of the temporal attention, then the same edge
+    predictor (src_fc, dst_fc, out_fc; models.py:313-324). The reference has
+    no such embedding (its "jodie" builds CTDGLinkPredictor,
+    models.py:337-338); select it with ctdg.embedding = time_projection."""
+
+    def __init__(self, num_nodes: int, hidden_dim: int, time_shift: float = 0.0, time_scale: float = 1.0,
+                 **_unused) -> None:
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.conv = None
+        self.time_proj = TimeProjection(hidden_dim, time_shift, time_scale)
+        self.src_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.dst_fc = nn.Linear(hidden_dim, hidden_dim)
+        self.out_fc = nn.Linear(hidden_dim, 1)
+
+    def embedding_module(self) -> nn.Module:
+        return self.time_proj
+
+    def forward(self, src_emb: torch.Tensor, dst_emb: torch.Tensor, neg_emb: torch.Tensor) -> CTDGModelOutput:
+        h_src = self.src_fc(src_emb)
+        pos_logits = self.out_fc(F.relu(h_src + self.dst_fc(dst_emb))).squeeze(-1)
+        neg_logits = self.out_fc(F.relu(h_src + self.dst_fc(neg_emb))).squeeze(-1)
         return CTDGModelOutput(pos_logits=pos_logits, neg_logits=neg_logits)
 
 
@@ -199,9 +247,17 @@ CTDG_MODEL_SPECS: dict[str, CTDGModelSpec] = {
 
 
 def build_ctdg_model(model_family: str, *, num_nodes: int, hidden_dim: int, edge_feat_dim: int, dim_time: int = 100,
-                     num_head: int = 2, dropout: float = 0.1, att_dropout: float = 0.1) -> nn.Module:
+                     num_head: int = 2, dropout: float = 0.1, att_dropout: float = 0.1,
+                     embedding: str = "attention", time_shift: float = 0.0, time_scale: float = 1.0) -> nn.Module:
+    """models.py:345-386. ``embedding`` "attention" (the reference's model for
+    every family) or "time_projection" (config 2's JODIE embedding)."""
     spec = CTDG_MODEL_SPECS.get(model_family.lower())
     if spec is None:
         raise KeyError(f"Unsupported CTDG model family: {model_family}")
+    if embedding == "time_projection":
+        return CTDGTimeProjectionPredictor(num_nodes=num_nodes, hidden_dim=hidden_dim, time_shift=time_shift,
+                                           time_scale=time_scale)
+    if embedding != "attention":
+        raise KeyError(f"unknown ctdg.embedding {embedding!r}: expected 'attention' or 'time_projection'")
     return spec.model_cls(num_nodes=num_nodes, hidden_dim=hidden_dim, edge_feat_dim=edge_feat_dim,
                           dim_time=dim_time, num_head=num_head, dropout=dropout, att_dropout=att_dropout)

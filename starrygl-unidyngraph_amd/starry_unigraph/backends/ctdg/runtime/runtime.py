@@ -87,8 +87,16 @@ class CTDGOnlineRuntime:
         self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
         conv = core.conv
-        self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head,
-                             fanout=int(sampler.fanout[0]) if sampler.fanout else 0)
+        fan = int(sampler.fanout[0]) if sampler.fanout else 0
+        # the time-projection model (config 2's JODIE) has no attention: its
+        # back part is the projection, the predictor and their backward
+        self._proj = conv is None
+        if self._proj:
+            if memory_updater is None:
+                raise ValueError("the time-projection embedding needs the memory updater (it embeds updated memory)")
+            self.dims = ConvDims(D=memory.hidden_dim, F=max(1, dataset.edge_feat_dim), T=1, H=1, fanout=fan)
+        else:
+            self.dims = ConvDims(D=memory.hidden_dim, F=conv.dim_edge, T=conv.dim_time, H=conv.num_head, fanout=fan)
         self._make_steps(int(max_batch or 1))
         self._dev = dataset.device_arrays(self.device)
         self._gru = memory_updater.kernel_weights() if memory_updater is not None else None
@@ -134,7 +142,7 @@ class CTDGOnlineRuntime:
         """3 attention passes per training step when a dropout is on
         (runtime.py:193-195), else 1."""
         conv = self._core().conv
-        return 3 if (conv.dropout.p > 0 or conv.att_dropout.p > 0) else 1
+        return 3 if (conv is not None and (conv.dropout.p > 0 or conv.att_dropout.p > 0)) else 1
 
     def fence(self) -> None:
         """Order the next step after all work queued so far on the current
@@ -407,7 +415,8 @@ class CTDGOnlineRuntime:
             step.commit()
         else:   # runtime.py:283-285: the conv reads the memory as it is
             step.gather_memory()
-        step.edge_rows(self._dev["edge_feat"])
+        if not self._proj:
+            step.edge_rows(self._dev["edge_feat"])
         if train:
             self._param_update(step).advance()
 
@@ -417,9 +426,19 @@ class CTDGOnlineRuntime:
         core = self._core()
         conv = core.conv
         efeat_all = self._dev["edge_feat"]
-        cparams = [p.detach() for p in conv.kernel_params()]
         pparams = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
                    core.out_fc.bias]
+        if self._proj:
+            tp = core.time_proj
+            pdet = [p.detach() for p in pparams]
+            upd = self._param_update(step) if train else None
+            step.proj_forward(tp)
+            step.predictor(n, train, pdet, [core.out_fc.weight.grad, core.out_fc.bias.grad] if train else None)
+            if train:
+                step.proj_backward(tp, (pdet[0], pdet[2]))
+                upd.run()
+            return
+        cparams = [p.detach() for p in conv.kernel_params()]
         if train:
             # gradients are views of the optimizer's flat buffer (no torch
             # autograd on this path): sgl_predictor writes out_fc's, the fused
@@ -448,8 +467,12 @@ class CTDGOnlineRuntime:
             core = self._core()
             pred = [core.src_fc.weight, core.src_fc.bias, core.dst_fc.weight, core.dst_fc.bias, core.out_fc.weight,
                     core.out_fc.bias]
-            upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None],
-                                  passes=step.buf.passes, counter=self._rng_counter)
+            if self._proj:
+                tp = core.time_proj.proj
+                upd = StepParamUpdate(step, inner, [tp.weight, tp.bias], pred, [None, None], kind="projection")
+            else:
+                upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None],
+                                      passes=step.buf.passes, counter=self._rng_counter)
             self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
             self._updates[id(step)] = upd
         return upd

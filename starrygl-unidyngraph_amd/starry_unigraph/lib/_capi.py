@@ -53,7 +53,11 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
     "sgl_memory_update_bf16": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
-    "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 10),
+    "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 11),
+    "sgl_time_projection_forward": (ctypes.c_int, [_i32, _i64, _vp, _vp, _vp, ctypes.c_float, ctypes.c_float,
+                                                   _vp, _vp, _vp, _vp]),
+    "sgl_time_projection_backward": (ctypes.c_int, [_i32, _i64, _vp, _vp, _vp, ctypes.c_float, ctypes.c_float]
+                                     + [_vp] * 8),
     "sgl_memory_gather": (ctypes.c_int, [_i32, _i64] + [_vp] * 8),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
     "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 8),

@@ -127,6 +127,7 @@ class StepBuffers:
         self.cnt_src = z(c, dt=i32)
         self.cnt_dst = z(c, dt=i32)
         self.new_mem = z(c, D)
+        self.root_dt = z(c)   # time since each root's previous memory update (the commit writes it)
         more = tuple(int(f) for f in more_fanouts)
         self.hop = PaddedHop(cnt=z(c, dt=i32), nbr=z(max(c * k, 1), dt=i32), eid=z(max(c * k, 1), dt=i32),
                              dt=z(max(c * k, 1)), ts=z(max(c * k, 1), dt=i64) if more else None,
@@ -182,6 +183,7 @@ class StepBuffers:
         self.conv_rows = int(_capi.lib().sgl_conv_tile_rows(D, dims.F, dims.T, H))
         if self.conv_rows <= 0 or TILE % self.conv_rows:
             raise RuntimeError(f"sgl_conv_tile_rows: unsupported attention dimensions {dims}")
+        self.proj_part = z(c // TILE, 2, D)   # the time projection's per-tile gradient partials
         self.tiles = c // self.conv_rows
         self.ln_part = z(P * self.tiles, 2, D)
         self.te_part = z(P * self.tiles, 2, max(dims.T, 1))
@@ -275,7 +277,7 @@ class DeviceStep:
         b, st, P = self.buf, self.state, _capi.ptr
         self._call("memory_commit", lambda: _capi.check(_capi.call("sgl_memory_commit", 
             st.D, b.cap, P(b.num_roots), P(b.roots), P(b.new_mem), P(st.memory), P(st.memory_ts), P(b.ts_max),
-            P(st.node_bits), P(b.hop.cnt), P(b.any_edges), self._s()), "sgl_memory_commit"))
+            P(st.node_bits), P(b.hop.cnt), P(b.any_edges), P(b.root_dt), self._s()), "sgl_memory_commit"))
 
     def gather_memory(self) -> None:
         """The commit's place without a memory updater: the roots' memory rows
@@ -284,6 +286,27 @@ class DeviceStep:
         self._call("memory_gather", lambda: _capi.check(_capi.call("sgl_memory_gather",
             st.D, b.cap, P(b.num_roots), P(b.roots), P(st.memory), P(b.new_mem), P(st.node_bits), P(b.hop.cnt),
             P(b.any_edges), self._s()), "sgl_memory_gather"))
+
+    # -- time projection (config 2's JODIE embedding) ------------------------
+    def proj_forward(self, tp) -> torch.Tensor:
+        """y = h * (1 + proj(x)) for the live roots (sgl_time_projection_forward);
+        ``tp``: the model's TimeProjection."""
+        b, P = self.buf, _capi.ptr
+        w, bias = tp.proj.weight.detach(), tp.proj.bias.detach()
+        self._call("time_projection", lambda: _capi.check(_capi.call(
+            "sgl_time_projection_forward", self.dims.D, b.y_rows, P(b.num_roots), P(b.new_mem), P(b.root_dt),
+            tp.shift, tp.scale, P(w), P(bias), P(b.y), self._s()), "sgl_time_projection_forward"))
+        return b.y
+
+    def proj_backward(self, tp, pred_w: tuple) -> None:
+        """The projection's gradient partials from the predictor's per-root
+        rows (sgl_time_projection_backward); ``pred_w`` = (src_fc.weight,
+        dst_fc.weight)."""
+        b, P = self.buf, _capi.ptr
+        self._call("time_projection_backward", lambda: _capi.check(_capi.call(
+            "sgl_time_projection_backward", self.dims.D, b.cap, P(b.num_roots), P(b.new_mem), P(b.root_dt),
+            tp.shift, tp.scale, P(b.acc_src), P(b.acc_dst), P(pred_w[0]), P(pred_w[1]), P(b.g_src), P(b.g_dst),
+            P(b.proj_part), self._s()), "sgl_time_projection_backward"))
 
     # -- attention ----------------------------------------------------------
     def edge_rows(self, efeat_all: torch.Tensor) -> None:
@@ -428,7 +451,7 @@ class StepParamUpdate:
 
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
                  pred_params: list[torch.Tensor], gates: list[torch.Tensor | None], passes: int = 1,
-                 counter: torch.Tensor | None = None):
+                 counter: torch.Tensor | None = None, kind: str = "attention"):
         if len(opt.segments) != 2:
             raise ValueError("StepParamUpdate expects the attention and predictor segments")
         if passes not in (1, step.buf.passes):
@@ -436,6 +459,9 @@ class StepParamUpdate:
         self.step, self.opt = step, opt
         self.passes = int(passes)
         self.counter = counter
+        if kind not in ("attention", "projection"):
+            raise ValueError(f"StepParamUpdate: unknown kind {kind!r}")
+        self.kind = kind
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
@@ -456,7 +482,6 @@ class StepParamUpdate:
         dh = D // H
         ntiles = b.cap // b.conv_rows
         base = opt.flat.data_ptr()
-        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
 
         def off(p):
             o = p.data_ptr() - base
@@ -491,6 +516,16 @@ class StepParamUpdate:
                  ps1=0 if x1w is None else x1w, ps2=0 if x2w is None else x2w)
 
         one = at(self.one)
+        if self.kind == "projection":
+            # the time projection's weight [D, 1] and bias [D] from the
+            # per-tile partials of sgl_time_projection_backward
+            pw, pb = conv_params
+            nt = b.cap // TILE
+            gemm(at(b.proj_part), 2 * D, one, 0, off(pw), 1, D, 1, nt)
+            gemm(at(b.proj_part, D), 2 * D, one, 0, off(pb), 1, D, 1, nt)
+            self._pred_jobs(gemm, add, at, off, one, pred_params, 1)
+            return self._check(jobs, tiles, conv_params, pred_params)
+        te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
         conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
         conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
         conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D)
@@ -516,6 +551,12 @@ class StepParamUpdate:
         # of g_dst holds the non-root negatives; y's row U is zero); out_fc's
         # gradients come from sgl_predictor (Adam only). With dropout dst_fc
         # sums the dst pass's rows and the negatives' pass's rows
+        self._pred_jobs(gemm, add, at, off, one, pred_params, P)
+        return self._check(jobs, tiles, conv_params, pred_params)
+
+    def _pred_jobs(self, gemm, add, at, off, one, pred_params, P):
+        b, D = self.step.buf, self.step.dims.D
+        c = b.cap
         w_s, b_s, w_d, b_d, w_o, b_o = pred_params
         nd = 2 if P > 1 else 1
         gs, ys = (c + 1) * D, b.y_rows * D
@@ -528,8 +569,11 @@ class StepParamUpdate:
             raise RuntimeError("StepParamUpdate: out_fc weight and bias are not contiguous in the flat buffer")
         add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=off(w_o), ldo=1, rows=D + 1, cols=1, kind=1, seg=1,
                           r_fixed=0, tiles_b=1), (D + 1 + 255) // 256)
+
+    def _check(self, jobs, tiles, conv_params, pred_params):
+        opt = self.opt
         if sum(p.numel() for p in conv_params) != opt.segments[0][1]:
-            raise RuntimeError("StepParamUpdate: the attention segment holds parameters the jobs do not cover")
+            raise RuntimeError("StepParamUpdate: the embedding segment holds parameters the jobs do not cover")
         if sum(p.numel() for p in pred_params) != opt.segments[1][1]:
             raise RuntimeError("StepParamUpdate: the predictor segment holds parameters the jobs do not cover")
         return jobs, tiles

@@ -42,6 +42,9 @@ CONFIGS = {
                  batches=(300, 301, 302)),
     "cfg2": dict(stream="bipartite", gen={}, family="jodie", D=100, T=100, H=2, k=10, K=1, B=200, history=1,
                  batches=(400, 401)),
+    # config 2 as BASELINE.json describes it: memory + GRU + a time projection, no attention
+    "cfg2p": dict(stream="bipartite", gen={}, family="jodie", embedding="time_projection", D=100, T=100, H=2, k=10,
+                  K=1, B=200, history=1, batches=(400, 401, 402)),
     "cfg4": dict(stream="unipartite", gen=dict(num_nodes=30000, num_events=120000), family="tgn", D=100, T=100,
                  H=2, k=10, K=1, B=600, history=1, batches=(60, 61, 62)),
     "cfg5": dict(stream="unipartite", gen=dict(num_nodes=30000, num_events=160000), family="tgn", D=172, T=100,
@@ -73,13 +76,16 @@ def _pair(name, gemm="fp32", seed=0, updater=True):
     cfg = {"model": {"family": c["family"], "hidden_dim": c["D"]}, "data": {"name": f"p_{name}", "format": "synthetic"},
            "train": {"batch_size": c["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
            "ctdg": {"mailbox_slots": c["K"], "dim_time": c["T"], "num_head": c["H"], "dropout": 0.0,
-                    "att_dropout": 0.0, "memory_gemm_dtype": gemm},
+                    "att_dropout": 0.0, "memory_gemm_dtype": gemm, "embedding": c.get("embedding", "attention")},
            "sampling": {"neighbor_limit": [c["k"]] * c["history"], "history": c["history"], "strategy": "recent"}}
     torch.manual_seed(seed)
     sess = SchedulerSession.from_config(cfg).with_events(from_stream(s))
     sess.build_runtime()
     rt = sess.ctdg_session.online_runtime
     model, upd = co.build_models(c["D"], F, c["T"], c["H"], c["K"], seed=seed)
+    if c.get("embedding") == "time_projection":
+        tp = rt.model.time_proj
+        model = co.ProjectionPredictorO(c["D"], tp.shift, tp.scale)
     model.load_state_dict({k: v.cpu() for k, v in rt.model.state_dict().items()})
     upd.load_state_dict({k: v.cpu() for k, v in rt.memory_updater.state_dict().items()})
     if not updater:
@@ -164,6 +170,7 @@ def _run_steps(name, gemm, train=True, updater=True):
             gpu_mem = st.memory.cpu()
             hook = lambda m: m.memory.copy_(gpu_mem)
         model64 = copy.deepcopy(model).double() if train else None
+        mts_prev = mem.memory_ts.clone()
         ref = co.train_step(model, upd, opt, mem, lambda r, t: co.block_from_oracle_sampler(og, r, t, fan),
                             batch.src, batch.dst, batch.ts, batch.edge_feat, neg, rt.dataset.edge_feat, train=train,
                             after_memory=hook)
@@ -189,21 +196,25 @@ def _run_steps(name, gemm, train=True, updater=True):
             # time-encoding weight's gradient sums terms ~ sin(w dt) dt with dt
             # up to 1e8 that largely cancel, so its float32 value depends on
             # the order of the sum and only a float64 sum is a fixed yardstick
-            for g64, (pn, p) in zip(_grads64(model64, mem, ref, batch, neg, rt.dataset.edge_feat),
+            for g64, (pn, p) in zip(_grads64(model64, mem, ref, batch, neg, rt.dataset.edge_feat, mts_prev),
                                     rt.model.named_parameters()):
                 scale = float(g64.abs().max()) + 1e-12
                 _close(p.grad, g64, 2e-3, 1e-3 * scale, f"grad {pn} {msg}")
     return rt
 
 
-def _grads64(model64, mem, ref, batch, neg, edge_feat_all):
-    """The step's attention + predictor + loss gradients in float64, from the
-    oracle's updated memory and block."""
-    model64.conv.time_enc.round_arg_f32 = True
+def _grads64(model64, mem, ref, batch, neg, edge_feat_all, mts_prev):
+    """The step's embedding + predictor + loss gradients in float64, from the
+    oracle's updated memory and block (memory_ts before the step: mts_prev)."""
     blk, roots = ref["block"], ref["roots"]
     m = mem.memory.double()
-    conv = model64.conv(m[roots], m[blk.nbr], edge_feat_all[blk.eid].double(), blk.delta_ts.float(),
-                        blk.src_index.long())
+    if isinstance(model64, co.ProjectionPredictorO):
+        dt = torch.tensor(float(batch.ts.max()), dtype=torch.float32) - mts_prev[roots]
+        conv = model64.embed(m[roots], dt)
+    else:
+        model64.conv.time_enc.round_arg_f32 = True
+        conv = model64.conv(m[roots], m[blk.nbr], edge_feat_all[blk.eid].double(), blk.delta_ts.float(),
+                            blk.src_index.long())
     pos, ngl = model64(co.select_rows(conv, roots, batch.src), co.select_rows(conv, roots, batch.dst),
                        co.select_rows(conv, roots, neg))
     model64.zero_grad(set_to_none=True)
@@ -212,12 +223,12 @@ def _grads64(model64, mem, ref, batch, neg, edge_feat_all):
 
 
 @pytest.mark.parametrize("gemm", ["fp32", "bf16"])
-@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg4", "cfg5"])
+@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg2p", "cfg4", "cfg5"])
 def test_train_steps_match_oracle_at_config_dims(gpu, name, gemm):
     _run_steps(name, gemm)
 
 
-@pytest.mark.parametrize("name", ["cfg4", "cfg5"])
+@pytest.mark.parametrize("name", ["cfg2p", "cfg4", "cfg5"])
 def test_eval_step_matches_oracle(gpu, name):
     _run_steps(name, "fp32", train=False)
 

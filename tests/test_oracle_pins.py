@@ -381,3 +381,17 @@ def test_oracle_dropout_masks_scale_and_rate():
     assert set(np.unique(att).tolist()) == {0.0, np.float32(1 / 0.8)}
     assert abs(float((att > 0).mean()) - 0.8) < 0.01
     assert bool((out == 1.0).all())
+
+
+def test_time_projection_closed_form():
+    """Config 2's JODIE embedding in the oracle: y = h * (1 + w x + b) with
+    x = (dt - shift) * scale, written out for two roots."""
+    m = co.ProjectionPredictorO(3, shift=10.0, scale=0.5)
+    with torch.no_grad():
+        m.time_proj.proj.weight.copy_(torch.tensor([[1.0], [-2.0], [0.5]]))
+        m.time_proj.proj.bias.copy_(torch.tensor([0.0, 1.0, -1.0]))
+    h = torch.tensor([[1.0, 2.0, 3.0], [4.0, -1.0, 2.0]])
+    dt = torch.tensor([14.0, 10.0])   # x = 2, 0
+    y = m.embed(h, dt)
+    # root 0: 1+w*2+b = [3, -2, 1]; root 1: 1+b = [1, 2, 0]
+    assert y.tolist() == [[3.0, -4.0, 3.0], [4.0, -2.0, 0.0]]
