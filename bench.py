@@ -7,8 +7,8 @@ Prints ONE JSON line. Workloads:
              (Zipf 1.5), 16-d edge features, D = T = 100, 2 heads, k = 10,
              1 mailbox slot, batch 600. A step is one training batch.
   tgn-small  config 1: bipartite 8,227 + 1,000 nodes, 157,474 events, F = 172, B = 200.
-  jodie      config 2: the same stream with the "jodie" family (the reference
-             builds the same model for it, models.py:337-338).
+  jodie      config 2: the same stream, memory + GRU + the JODIE time
+             projection (ctdg.embedding = time_projection), no attention.
   tgn-stress config 5: the config-4 stream, D = 172, 4 heads, k = 20,
              2 sampled hops, 4 mailbox slots, batch 4,000.
   sampler    config 3 alone (temporal sampler microbench).
@@ -20,8 +20,10 @@ The default run also measures config 3 and reports it under "sampler", and the
 gather/scatter microbench under "gather_scatter".
 
 Timed region: W untimed warm-up steps, then K steps bracketed by
-torch.cuda.synchronize(); value = events / s over the K steps. Inputs (event
-stream, node state, negatives) are resident in HBM before the timed region.
+torch.cuda.synchronize(); value = events / s over the K steps. The event
+stream and node state are resident in HBM before the timed region; each
+step draws its negatives inside it (the runtime draws a few consecutive
+batches' negatives per CPU call and looks them up on the device).
 The node state and optimizer are then restored and the same K steps are
 replayed with HIP events around every library call (per-kernel breakdown and
 the algorithmic work of the dominant kernel); the dominant kernel's events are
