@@ -631,6 +631,416 @@ __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide-tile bf16 GRU + mailbox kernel. A workgroup takes 16*RB roots and
+// one wave per 16 hidden columns (a chunk; ceil(D/16) <= 12 waves). For its
+// chunk a wave computes the three gates for every row of the tile: the r and
+// z pre-activations of the input and hidden products share one accumulator
+// each (they are only ever summed), n keeps two (r scales the hidden part),
+// so a stage holds 4*RB MFMA accumulators and combines the gates in
+// registers: no gate tile goes through LDS. Each weight fragment loaded from
+// L2 feeds RB MFMAs (one per 16-row block), so the weight traffic per root
+// falls by RB against the 16-root kernel. A wave keeps its chunk's fp32
+// hidden state in registers across the K slots and publishes the bf16 copy
+// that the next hidden product reads after the barrier that ends the
+// products, together with the next slot's mailbox tile. Global reads are
+// issued in flat batches over the whole workgroup (the memory tile with the
+// first mailbox tile; the messages' parts for every root of the tile), so a
+// tile waits for few memory round trips.
+constexpr int kWideMaxChunks = 12;
+constexpr int kWideDepthSmall = 4;  // weight prefetch depth, 16-root tiles
+constexpr int kWideDepthLarge = 2;  // weight prefetch depth, 64-root tiles
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bf16_rsrc(const uint16_t *p, uint32_t elems) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  const uint32_t bytes = __builtin_amdgcn_readfirstlane(elems * 2u);
+  uint16_t *u = reinterpret_cast<uint16_t *>((uint64_t(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, int(bytes), 0x00020000);
+}
+
+// 8 consecutive bf16 weights at element e of the matrix behind r (e % 4 == 0;
+// e % 8 == 0 and a 16-byte aligned matrix when V16). Elements past the
+// matrix read 0; elements of the next row (k >= kd) meet zero A elements.
+template <bool V16>
+__device__ __forceinline__ bf16x8_t load_w8(__amdgpu_buffer_rsrc_t r, uint32_t e) {
+  sgl::u32x4 v;
+  if constexpr (V16) {
+    v = __builtin_amdgcn_raw_buffer_load_b128(r, int(e * 2u), 0, 0);
+  } else {
+    const u32x2_t lo = __builtin_amdgcn_raw_buffer_load_b64(r, int(e * 2u), 0, 0);
+    const u32x2_t hi = __builtin_amdgcn_raw_buffer_load_b64(r, int(e * 2u + 8u), 0, 0);
+    v = sgl::u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// A[row][k .. k+8) of a bf16 LDS row (lda % 8 == 0, lda >= kd) with the
+// elements at k >= kd zeroed: the 16 bytes at min(k, lda - 8) stay inside
+// the row (k > lda - 8 means k >= kd: every element is zeroed).
+__device__ __forceinline__ bf16x8_t load_a8_tail(const uint16_t *arow, int k, int kd, int lda) {
+  sgl::u32x4 w = *reinterpret_cast<const sgl::u32x4 *>(arow + min(k, lda - 8));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t keep = (k + 2 * t < kd ? 0x0000ffffu : 0u) | (k + 2 * t + 1 < kd ? 0xffff0000u : 0u);
+    w[t] &= keep;
+  }
+  return __builtin_bit_cast(bf16x8_t, w);
+}
+
+// acc_g[rb] += A[16 rb + i][0..kd) . W[g*D + n0 + i'][0..kd) for the three
+// gates g of a GRU weight matrix W ([3D][kd] row-major bf16) and the RB
+// 16-row blocks of the LDS tile A (lda % 8 == 0, lda >= kd). The gate
+// fragments of a k step are loaded once and multiplied into every row
+// block. The loads run P-1 steps ahead of the products through P register
+// sets (the loop unrolled by P, so that no set is copied): an L2 round trip
+// is long against one step's products, and each wave's steps are a serial
+// chain. Only the last step (k past kd) masks A.
+template <int RB, bool V16, int P>
+__device__ __forceinline__ void wide_gates(int lane, const uint16_t *A, int lda, int kd, const uint16_t *W, int D,
+                                           int n0, sgl::f32x4 (&a0)[RB], sgl::f32x4 (&a1)[RB],
+                                           sgl::f32x4 (&a2)[RB]) {
+  const int i = lane & 15, q = lane >> 4;
+  // columns past D read row D-1 (finite weights; their outputs are discarded)
+  const int n = min(n0 + i, D - 1);
+  const __amdgpu_buffer_rsrc_t wr = bf16_rsrc(W, uint32_t(3 * D) * uint32_t(kd));
+  const uint32_t gs = uint32_t(D) * uint32_t(kd);
+  const uint32_t wrow = uint32_t(n) * uint32_t(kd) + 8u * q;
+  const uint16_t *arow = A + i * lda + 8 * q;
+  const int nks = (kd + 31) >> 5, nfull = kd >> 5;
+  // loads are not guarded: past the matrix they read 0 (the descriptor's range)
+  auto load = [&](bf16x8_t (&b)[3], int ks) {
+    const uint32_t e = wrow + 32u * uint32_t(ks);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) b[g] = load_w8<V16>(wr, e + g * gs);
+  };
+  auto mma = [&](const bf16x8_t (&b)[3], const bf16x8_t (&a)[RB]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      a0[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b[0], a0[rb], 0, 0, 0);
+      a1[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b[1], a1[rb], 0, 0, 0);
+      a2[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[rb], b[2], a2[rb], 0, 0, 0);
+    }
+  };
+  auto step_full = [&](const bf16x8_t (&b)[3], int ks) {
+    bf16x8_t a[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) a[rb] = *reinterpret_cast<const bf16x8_t *>(arow + 16 * rb * lda + 32 * ks);
+    mma(b, a);
+  };
+  bf16x8_t b[P][3];
+#pragma unroll
+  for (int u = 0; u < P - 1; ++u) load(b[u], u);
+  int ks = 0;
+  // groups of P full steps; the scheduling barriers keep each load ahead of
+  // the products it overlaps
+  for (; ks + P <= nfull; ks += P) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      load(b[(u + P - 1) % P], ks + u + P - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      step_full(b[u], ks + u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // the remaining nks - ks <= P steps: sets 0 .. P-2 hold steps ks .. ks+P-2
+  load(b[P - 1], ks + P - 1);
+#pragma unroll
+  for (int u = 0; u < P; ++u) {
+    const int kk = ks + u;
+    if (kk < nfull) {
+      step_full(b[u], kk);
+    } else if (kk < nks) {
+      bf16x8_t a[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) a[rb] = load_a8_tail(A + (16 * rb + i) * lda, 32 * kk + 8 * q, kd, lda);
+      mma(b[u], a);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<__bf16>(a));
+  const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<__bf16>(b));
+  return lo | (hi << 16);
+}
+
+// One fp32 -> bf16 row-tile copy: rows [0, R) x columns [0, 4*n4) of the
+// rows at base + row_off(i) (16-byte aligned) into an LDS tile with leading
+// dimension ld; rows >= nrows read 0.
+template <typename RowOff>
+struct TileCopy {
+  uint16_t *tile;
+  int ld;
+  const float *base;
+  RowOff row_off;
+  int n4;
+};
+
+// Up to two tile copies as one flat index space, NB loads per thread issued
+// before their stores (one memory round trip per NB * blockDim.x vectors).
+// Branch-free: rows past nrows and positions past the end load the last live
+// row (their values land in padding rows whose outputs are discarded, or
+// nowhere), so the loads issue back to back (nrows > 0).
+template <int R, int NB, typename C0, typename C1>
+__device__ __forceinline__ void tiles_to_bf16(const C0 &c0, const C1 *c1, int nrows) {
+  const int nthr = blockDim.x;
+  const int t0 = R * c0.n4;
+  const int total = t0 + (c1 != nullptr ? R * c1->n4 : 0);
+  for (int f0 = threadIdx.x; f0 < total; f0 += NB * nthr) {
+    sgl::f32x4 v[NB];
+    int at[NB];  // LDS element offset within the region's tile, -1: none
+    bool second[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int f = min(f0 + u * nthr, total - 1);
+      const bool in1 = f >= t0;
+      const int g = in1 ? f - t0 : f;
+      const int n4 = in1 ? c1->n4 : c0.n4;
+      const int i = g / n4, c4 = g - i * n4;
+      const int il = min(i, nrows - 1);
+      const float *p = in1 ? c1->base + c1->row_off(il) + 4 * c4 : c0.base + c0.row_off(il) + 4 * c4;
+      v[u] = *reinterpret_cast<const sgl::f32x4 *>(p);
+      at[u] = f0 + u * nthr < total ? i * (in1 ? c1->ld : c0.ld) + 4 * c4 : -1;
+      second[u] = in1;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (at[u] < 0) continue;
+      uint16_t *tile = second[u] ? c1->tile : c0.tile;
+      *reinterpret_cast<u32x2_t *>(tile + at[u]) =
+          u32x2_t{pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3])};
+    }
+  }
+}
+
+template <typename RowOff>
+__device__ __forceinline__ TileCopy<RowOff> tile_copy(uint16_t *tile, int ld, const float *base, RowOff f, int n4) {
+  return TileCopy<RowOff>{tile, ld, base, f, n4};
+}
+
+// IH16 / HH16: 16-byte weight loads for W_ih / the D-wide matrices (rows of
+// a multiple of 8 elements, 16-byte aligned), else two 8-byte loads; P: the
+// weight prefetch depth.
+template <int RB, bool IH16, bool HH16, int P>
+__global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
+    int D, int K, int F, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ roots,
+    const float *__restrict__ memory, float *__restrict__ mailbox, float *__restrict__ mailbox_ts,
+    int32_t *__restrict__ next_mail_pos, const uint16_t *__restrict__ w_ih, const uint16_t *__restrict__ w_hh,
+    const float *__restrict__ b_ih, const float *__restrict__ b_hh, const uint16_t *__restrict__ wc_ih,
+    const uint16_t *__restrict__ wc_hh, const float *__restrict__ bc_ih, const float *__restrict__ bc_hh,
+    const int64_t *__restrict__ src, const int64_t *__restrict__ dst, const float *__restrict__ efeat,
+    const float *__restrict__ ts, const int64_t *__restrict__ batch_start,
+    const unsigned long long *__restrict__ win_src, const unsigned long long *__restrict__ win_dst,
+    const int32_t *__restrict__ cnt_src, const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
+  constexpr int R = 16 * RB;
+  // loads in flight per thread in the tile copies and the message copy: about
+  // one batch per copy at these tile sizes (the last batch repeats positions)
+  constexpr int NB = RB >= 4 ? 12 : 4;
+  constexpr int MB = RB >= 4 ? 8 : 4;
+  extern __shared__ __align__(16) float lds[];
+  const int S = 2 * D + F;
+  const int lbx = lds_ld_bf16(S), lbh = lds_ld_bf16(D);
+  const int ldf = sgl::lds_ld(D);
+  float *hf = lds;                                                     // fp32 hidden state
+  uint16_t *xb = reinterpret_cast<uint16_t *>(hf + R * ldf);          // mailbox tile
+  uint16_t *hb = xb + R * lbx;                                         // hidden tile (bf16)
+  uint16_t *mb = hb + R * lbh;                                         // memory tile
+  __shared__ int64_t s_root[R], s_e[2][R], s_other[2][R];
+  __shared__ int32_t s_cnt[2][R], s_pos[R], s_slot[2][R];
+  const int U = *num_roots;
+  const int nthr = blockDim.x;
+  const int S4 = S >> 2, D4 = D >> 2;
+  // The thread index is made opaque at the start of each stage, so that the
+  // stage's per-lane address arithmetic is recomputed there rather than
+  // hoisted out of the tile and slot loops and kept live (in registers the
+  // MFMA accumulators need) across the whole kernel.
+  auto opaque_tid = [] {
+    int t = int(threadIdx.x);
+    asm volatile("" : "+v"(t));
+    return t;
+  };
+
+  if (batch_start != nullptr) {  // event arrays are the whole stream
+    const int64_t off = *batch_start;
+    src += off;
+    dst += off;
+    ts += off;
+    efeat += off * F;
+  }
+  for (int r0 = blockIdx.x * R; r0 < U; r0 += gridDim.x * R) {
+    const int nrows = min(R, U - r0);
+    for (int t = threadIdx.x; t < R; t += nthr) {
+      const bool ok = t < nrows;
+      s_root[t] = ok ? roots[r0 + t] : 0;
+      s_cnt[0][t] = ok ? cnt_src[r0 + t] : 0;
+      s_cnt[1][t] = ok ? cnt_dst[r0 + t] : 0;
+      // the event of each role (0 for a role without events: a valid index)
+      s_e[0][t] = ok && cnt_src[r0 + t] > 0 ? int64_t(win_src[r0 + t] & 0xffffffffull) : 0;
+      s_e[1][t] = ok && cnt_dst[r0 + t] > 0 ? int64_t(win_dst[r0 + t] & 0xffffffffull) : 0;
+    }
+    __syncthreads();
+    // the memory tile and the first mailbox tile in one batch; the roots'
+    // slot pointers and the messages' other endpoints beside them
+    {
+      const int t = threadIdx.x;
+      int pos = 0;
+      int64_t oth[2] = {0, 0};
+      if (t < nrows) {  // s_e is a valid event index for a role without events
+        pos = next_mail_pos[s_root[t]];
+        const int64_t o0 = dst[s_e[0][t]], o1 = src[s_e[1][t]];
+        oth[0] = s_cnt[0][t] > 0 ? o0 : 0;
+        oth[1] = s_cnt[1][t] > 0 ? o1 : 0;
+      }
+      const auto cm = tile_copy(mb, lbh, memory, [&](int i) { return s_root[i] * D; }, D4);
+      const auto cx = tile_copy(xb, lbx, mailbox, [&](int i) { return s_root[i] * K * S; }, S4);
+      tiles_to_bf16<R, NB>(cm, &cx, nrows);
+      if (t < R) {
+        s_pos[t] = pos;
+        s_other[0][t] = oth[0];
+        s_other[1][t] = oth[1];
+      }
+    }
+    __syncthreads();
+    // The fp32 hidden state lives in LDS (hf): each wave reads and writes
+    // only its own chunk's columns, so it needs no barrier of its own, and
+    // the registers stay with the MFMA accumulators and weight loads.
+    // GRU layer over the K mailbox slots in slot-index order, h0 = 0
+    for (int k = 0; k < K; ++k) {
+      if (k > 0) {
+        // publish the hidden state (bf16), then the slot's mailbox tile
+        {
+          const int t = opaque_tid(), lane = t & 63;
+          const int j = 16 * (t >> 6) + (lane & 15);
+          if (j < D) {
+            for (int i = lane >> 4; i < R; i += 4)
+              hb[i * lbh + j] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(hf[i * ldf + j]));
+          }
+        }
+        const auto cx = tile_copy(xb, lbx, mailbox, [&](int i) { return (s_root[i] * K + k) * S; }, S4);
+        tiles_to_bf16<R, NB>(cx, static_cast<const decltype(cx) *>(nullptr), nrows);
+        __syncthreads();
+      }
+      const int t = opaque_tid(), lane = t & 63;
+      const int n0 = 16 * (t >> 6);
+      const int j = n0 + (lane & 15);
+      const bool jok = j < D;
+      const int jc = jok ? j : D - 1;
+      const int rq = 4 * (lane >> 4);
+      sgl::f32x4 ar[RB], az[RB], an[RB], ah[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) ar[rb] = az[rb] = an[rb] = ah[rb] = sgl::f32x4{0.f, 0.f, 0.f, 0.f};
+      wide_gates<RB, IH16, P>(lane, xb, lbx, S, w_ih, D, n0, ar, az, an);
+      if (k > 0) wide_gates<RB, HH16, P>(lane, hb, lbh, D, w_hh, D, n0, ar, az, ah);
+      const float br = b_ih[jc] + b_hh[jc], bz = b_ih[D + jc] + b_hh[D + jc];
+      const float bn = b_ih[2 * D + jc], bhn = b_hh[2 * D + jc];
+      if (jok) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float *hp = hf + (16 * rb + rq + v) * ldf + j;
+            const float hold = k > 0 ? *hp : 0.f;
+            const float r = 1.f / (1.f + expf(-(ar[rb][v] + br)));
+            const float z = 1.f / (1.f + expf(-(az[rb][v] + bz)));
+            const float nn = tanhf(an[rb][v] + bn + r * (ah[rb][v] + bhn));
+            *hp = (1.f - z) * nn + z * hold;
+          }
+        }
+      }
+      __syncthreads();  // the mailbox and hidden tiles are consumed
+    }
+    // GRUCell(agg = h, memory)
+    {
+      const int t = opaque_tid(), lane = t & 63;
+      const int j = 16 * (t >> 6) + (lane & 15);
+      if (j < D) {
+        for (int i = lane >> 4; i < R; i += 4)
+          hb[i * lbh + j] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(hf[i * ldf + j]));
+      }
+    }
+    __syncthreads();
+    {
+      const int t = opaque_tid(), lane = t & 63;
+      const int n0 = 16 * (t >> 6);
+      const int j = n0 + (lane & 15);
+      const bool jok = j < D;
+      const int jc = jok ? j : D - 1;
+      const int rq = 4 * (lane >> 4);
+      sgl::f32x4 ar[RB], az[RB], an[RB], ah[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) ar[rb] = az[rb] = an[rb] = ah[rb] = sgl::f32x4{0.f, 0.f, 0.f, 0.f};
+      wide_gates<RB, HH16, P>(lane, hb, lbh, D, wc_ih, D, n0, ar, az, an);
+      wide_gates<RB, HH16, P>(lane, mb, lbh, D, wc_hh, D, n0, ar, az, ah);
+      const float br = bc_ih[jc] + bc_hh[jc], bz = bc_ih[D + jc] + bc_hh[D + jc];
+      const float bn = bc_ih[2 * D + jc], bhn = bc_hh[2 * D + jc];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int i = 16 * rb + rq + v;
+          if (!jok || i >= nrows) continue;
+          const float m = memory[s_root[i] * D + j];
+          const float r = 1.f / (1.f + expf(-(ar[rb][v] + br)));
+          const float z = 1.f / (1.f + expf(-(az[rb][v] + bz)));
+          const float nn = tanhf(an[rb][v] + bn + r * (ah[rb][v] + bhn));
+          new_mem[size_t(r0 + i) * D + j] = (1.f - z) * nn + z * m;
+        }
+      }
+    }
+    // Mailbox write (memory.py:218-248), after every read of the tile's
+    // mailbox rows (the barriers ending the slots): the src-role message
+    // [mem(u) || mem(other) || f_e] of u's last src event goes to slot
+    // p = next_mail_pos[u], the dst-role one to (p + #src occurrences) % K,
+    // so with one slot the dst role wins; the pointer advances by both counts.
+    // Slot -1: the role writes nothing.
+    for (int t = threadIdx.x; t < nrows; t += nthr) {
+      const int64_t u = s_root[t];
+      const int p = s_pos[t], cs = s_cnt[0][t], cd = s_cnt[1][t];
+      const int p2 = (p + cs) % K;
+      const bool write_src = cs > 0 && !(cd > 0 && p2 == p);
+      s_slot[0][t] = write_src ? p : -1;
+      s_slot[1][t] = cd > 0 ? p2 : -1;
+      if (write_src) mailbox_ts[u * K + p] = ts[s_e[0][t]];
+      if (cd > 0) mailbox_ts[u * K + p2] = ts[s_e[1][t]];
+      next_mail_pos[u] = int32_t((int64_t(p) + cs + cd) % K);
+    }
+    __syncthreads();
+    {
+      // the messages' parts, all loads of a batch issued before its stores
+      // (a skipped role loads its root's own row and stores nothing)
+      const int total = nrows * 2 * S4;
+      for (int f0 = threadIdx.x; f0 < total; f0 += MB * nthr) {
+        sgl::f32x4 v[MB];
+        float *to[MB];
+#pragma unroll
+        for (int u = 0; u < MB; ++u) {
+          const int f = min(f0 + u * nthr, total - 1);
+          const int rt = f / S4, c4 = f - rt * S4;  // rt = 2 * root + role
+          const int t = rt >> 1, role = rt & 1;
+          const int slot = s_slot[role][t];
+          const int64_t uu = s_root[t];
+          const float *from = c4 < D4 ? memory + uu * D + 4 * c4
+                                      : (c4 < 2 * D4 ? memory + s_other[role][t] * D + 4 * (c4 - D4)
+                                                     : efeat + s_e[role][t] * F + 4 * (c4 - 2 * D4));
+          v[u] = *reinterpret_cast<const sgl::f32x4 *>(from);
+          to[u] = f0 + u * nthr < total && slot >= 0 ? mailbox + (uu * K + slot) * S + 4 * c4 : nullptr;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < MB; ++u)
+          if (to[u] != nullptr) *reinterpret_cast<sgl::f32x4 *>(to[u]) = v[u];
+      }
+    }
+    __syncthreads();  // the next tile reuses the shared root table and LDS tiles
+  }
+}
+
 __global__ __launch_bounds__(kBlock) void k_memory_commit(
     int D, bool vec4, bool gather, int64_t cap, const int32_t *__restrict__ num_roots,
     const int64_t *__restrict__ roots, float *__restrict__ rows, float *__restrict__ memory,
@@ -762,6 +1172,51 @@ extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {
   return sizeof(float) * kTileRows * (sgl::lds_ld(int(S)) + 2 * sgl::lds_ld(D) + 2 * sgl::lds_ld(int(G)));
 }
 
+// LDS of the wide-tile kernel: the fp32 hidden state and the bf16 mailbox,
+// hidden and memory tiles
+static size_t wide_lds_bytes(int D, int F, int rows) {
+  return sizeof(float) * size_t(rows) * size_t(sgl::lds_ld(D)) +
+         sizeof(uint16_t) * size_t(rows) * (size_t(lds_ld_bf16(2 * D + F)) + 2 * size_t(lds_ld_bf16(D)));
+}
+
+static bool host_aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rows per tile of the wide-tile kernel: 16 for batches that give fewer
+// tiles than CUs, 64 once a batch has 64-root tiles for every CU; 0 when the
+// shape does not fit it (float4 rows, at most 12 chunks, LDS).
+static int wide_rows(int D, int F, int64_t capacity, const float *memory, const float *mailbox,
+                     const float *new_mem, const float *efeat, const uint16_t *w_ih, const uint16_t *w_hh,
+                     const uint16_t *wc_ih, const uint16_t *wc_hh) {
+  if (D % 4 != 0 || F % 4 != 0 || (D + 15) / 16 > kWideMaxChunks) return 0;
+  if (!host_aligned16(memory) || !host_aligned16(mailbox) || !host_aligned16(new_mem) ||
+      (F > 0 && !host_aligned16(efeat)) || !host_aligned16(w_ih) || !host_aligned16(w_hh) ||
+      !host_aligned16(wc_ih) || !host_aligned16(wc_hh))
+    return 0;
+  const int rows = capacity >= 64 * 256 ? 64 : 16;
+  return wide_lds_bytes(D, F, rows) <= 160 * 1024 ? rows : 0;
+}
+
+template <int RB, bool IH16, bool HH16, int P>
+static int launch_wide(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
+                       const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
+                       int32_t *next_mail_pos, const uint16_t *w_ih, const uint16_t *w_hh, const float *b_ih,
+                       const float *b_hh, const uint16_t *wc_ih, const uint16_t *wc_hh, const float *bc_ih,
+                       const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
+                       const float *ts, const int64_t *batch_start, const uint64_t *win_src,
+                       const uint64_t *win_dst, const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
+                       hipStream_t stream) {
+  auto kern = &k_gru_mailbox_wide<RB, IH16, HH16, P>;
+  const size_t wl = wide_lds_bytes(D, F, 16 * RB);
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(kern), wl));
+  const unsigned grid = unsigned(std::min<int64_t>((capacity + 16 * RB - 1) / (16 * RB), sgl::kMaxGrid));
+  sgl::launch(kern, dim3(grid), dim3(sgl::kWave * ((D + 15) / 16)), wl, stream, D, K, F, num_roots, roots, memory,
+              mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst,
+              efeat, ts, batch_start, reinterpret_cast<const unsigned long long *>(win_src),
+              reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
 template <typename WT>
 static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots, const int64_t *roots,
                   const float *memory, float *mailbox, float *mailbox_ts, int32_t *next_mail_pos, const WT *w_ih,
@@ -782,6 +1237,25 @@ static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, cons
   SGL_REQUIRE(lds <= 160 * 1024, "memory_update: D=%d F=%d needs %zu bytes of LDS (> 160 KiB)", D, F, lds);
   SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
               64 * kMaxMsgSlots);
+  if constexpr (!std::is_same_v<WT, float>) {
+    const int rows = wide_rows(D, F, capacity, memory, mailbox, new_mem, efeat, w_ih, w_hh, wc_ih, wc_hh);
+    if (rows > 0) {
+      // 16-byte weight loads where rows are 16-byte multiples (the pointers are 16-byte aligned)
+      const bool ih16 = (2 * D + F) % 8 == 0, hh16 = D % 8 == 0;
+      decltype(&launch_wide<1, true, true, kWideDepthSmall>) fn;
+      if (rows == 64)
+        fn = ih16 ? (hh16 ? &launch_wide<4, true, true, kWideDepthLarge> : &launch_wide<4, true, false, kWideDepthLarge>)
+                  : (hh16 ? &launch_wide<4, false, true, kWideDepthLarge>
+                          : &launch_wide<4, false, false, kWideDepthLarge>);
+      else
+        fn = ih16 ? (hh16 ? &launch_wide<1, true, true, kWideDepthSmall> : &launch_wide<1, true, false, kWideDepthSmall>)
+                  : (hh16 ? &launch_wide<1, false, true, kWideDepthSmall>
+                          : &launch_wide<1, false, false, kWideDepthSmall>);
+      return fn(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih,
+                b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts, batch_start, win_src, win_dst, cnt_src,
+                cnt_dst, new_mem, stream);
+    }
+  }
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox<WT>), lds));
   const unsigned grid = unsigned(std::min<int64_t>((capacity + kTileRows - 1) / kTileRows, sgl::kMaxGrid));
   sgl::launch(&k_gru_mailbox<WT>, dim3(grid), dim3(kGruBlock), lds, stream, D, K, F, num_roots, roots, memory,
