@@ -564,9 +564,11 @@ def run_tgn(args, wl: dict) -> dict:
     if args.no_plans:   # eager steps: time the dominant kernel inside the timed region
         for st in rt.steps:
             st.timer, st.timed = timer, {dom}
-    else:   # planned steps: HIP events around the dominant kernel's launch in every 8th step
+    else:   # planned steps: HIP events at the dominant kernel's dispatch in steps 10, 74, 138, ...
+        # (a timed dispatch costs the host tens of microseconds: few samples, none at the cold start)
+        every, first = 64, min(10, args.steps - 1)
         pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                 for _ in range((args.steps + 7) // 8)]
+                 for _ in range((args.steps - first + every - 1) // every)]
         for a, b in pairs:   # torch creates the HIP event at its first record
             a.record()
             b.record()
@@ -575,9 +577,9 @@ def run_tgn(args, wl: dict) -> dict:
         def next_pair():
             i = count[0]
             count[0] += 1
-            if i % 8:
+            if i < first or (i - first) % every:
                 return None
-            p = pairs[i // 8]
+            p = pairs[(i - first) // every]
             timer.append((dom, p[0], p[1]))
             return p
 

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 12
+#define SGL_ABI_VERSION 13
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -42,6 +42,11 @@ extern "C" {
 /* (8) version / ABI query. */
 int sgl_abi_version(void);
 const char *sgl_last_error(void);
+/* The device-visible address of pinned host memory (hipHostGetDevicePointer),
+ * so that a kernel can read host-staged inputs in place instead of through a
+ * separate copy (the negatives' draws). No reference counterpart: the
+ * reference draws and looks up negatives on the host. */
+int sgl_host_device_pointer(const void *host, void **device);
 
 /* ---------------------------------------------------------------------------
  * (1) Temporal CSR build.
@@ -180,7 +185,8 @@ int64_t sgl_node_bits_words(int64_t num_nodes);
  * neg[e] = pool[draw[e]], and when that equals dst[e], pool[(draw[e] + 1)
  * mod pool_size] instead (once, as there). pool is the sorted unique dst
  * pool; draws outside [0, pool_size) set SGL_DERR_NODE_RANGE. draw and neg
- * may be the same array. */
+ * may be the same array; draw may be pinned host memory read in place
+ * (sgl_host_device_pointer). */
 int sgl_negatives_from_draws(int64_t n, const int64_t *draw, const int64_t *pool,
                              int64_t pool_size, const int64_t *dst, int64_t *neg,
                              int32_t *err_flag, hipStream_t stream);

@@ -46,3 +46,9 @@ extern "C" int sgl_time_next_launch(hipEvent_t start, hipEvent_t stop) {
 }
 
 extern "C" const char *sgl_last_error(void) { return sgl::g_last_error; }
+
+extern "C" int sgl_host_device_pointer(const void *host, void **device) {
+  SGL_REQUIRE(host != nullptr && device != nullptr, "host_device_pointer: NULL argument");
+  SGL_CHECK_HIP(hipHostGetDevicePointer(device, const_cast<void *>(host), 0));
+  return SGL_OK;
+}

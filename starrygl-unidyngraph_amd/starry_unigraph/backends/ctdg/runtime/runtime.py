@@ -47,6 +47,8 @@ class StepTensors:
 
 
 class CTDGOnlineRuntime:
+    kDrawRing = 4   # pinned staging buffers of the negative draws
+
     def __init__(self, dataset: TGTemporalDataset, sampler: NativeTemporalSampler, memory: CTDGMemoryBank,
                  model: torch.nn.Module, optimizer, route: Any, device: str, dist_ctx: Any,
                  memory_updater: CTDGMemoryUpdater | None = None, max_batch: int | None = None):
@@ -81,8 +83,11 @@ class CTDGOnlineRuntime:
         # _neg_ahead[split] = (next unconsumed event, end of the drawn range)
         self.neg_chunk = 8
         self._neg_ahead: dict[str, tuple[int, int]] = {}
-        self._draw_host: torch.Tensor | None = None   # pinned staging of the draws
-        self._draw_done = None                         # event: the last copy out of it
+        # pinned staging of the draws: a ring, so that the host waits only for
+        # the copy out of a buffer it filled kDrawRing draws ago (the host
+        # runs ahead of the GPU by up to that many chunks of steps)
+        self._draw_ring: list[list] = []   # [pinned buffer, event of the last lookup reading it, its device address]
+        self._draw_next = 0
         self._pool_dev: torch.Tensor | None = None
         self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
@@ -224,7 +229,10 @@ class CTDGOnlineRuntime:
         self.fence()   # the next batch preparation reads them
 
     def _negatives(self, batch: CTDGDataBatch) -> torch.Tensor:
+        """The batch's negatives, ready for work on the current stream."""
         buf, off = self._negatives_at(batch)
+        if self._front_stream is not None:   # drawn on the front stream
+            torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
         return buf[off:off + batch.size] if off >= 0 else buf
 
     def _negatives_at(self, batch: CTDGDataBatch) -> tuple[torch.Tensor, int]:
@@ -262,12 +270,19 @@ class CTDGOnlineRuntime:
         hi = max(s + n, min(end, s + self.neg_chunk * n))
         m = hi - s
         pool = self._dst_pool()
-        if self._draw_host is None or self._draw_host.numel() < m:
-            self._draw_host = torch.empty(max(m, self.neg_chunk * n), dtype=torch.long, pin_memory=True)
-            self._draw_done = None
-        elif self._draw_done is not None:
-            self._draw_done.synchronize()   # the last copy out of the staging buffer (long finished)
-        host = self._draw_host[:m]
+        if not self._draw_ring or self._draw_ring[0][0].numel() < m:
+            # the whole ring at once (pinned allocations are slow: none in later steps)
+            size = max(m, self.neg_chunk * n)
+            self._draw_ring = []
+            for _ in range(self.kDrawRing):
+                buf = torch.empty(size, dtype=torch.long, pin_memory=True)
+                self._draw_ring.append([buf, None, _capi.host_device_pointer(buf)])
+            self._draw_next = 0
+        slot = self._draw_ring[self._draw_next]
+        self._draw_next = (self._draw_next + 1) % len(self._draw_ring)
+        if slot[1] is not None:
+            slot[1].synchronize()   # the lookup that read this buffer, kDrawRing draws ago
+        host = slot[0][:m]
         # the draw itself on the CPU generator; the lookup and the collision
         # rule on the device (sgl_negatives_from_draws), in place
         torch.randint(low=0, high=pool.numel(), size=(m,), dtype=torch.long, out=host)
@@ -275,19 +290,17 @@ class CTDGOnlineRuntime:
             self._pool_dev = pool.to(self.device)
         front = self._front_stream
         stream = front if front is not None else torch.cuda.current_stream(self.device)
-        # on the front stream, where the batch preparations read them; the
-        # current stream (eager steps) orders itself after it too
+        # on the front stream, where the batch preparations read them (an
+        # eager step orders its stream after the front stream first); the
+        # lookup reads the pinned draws in place (no separate copy)
         with torch.cuda.stream(stream):
             out = self._neg_all[s:hi]
-            out.copy_(host, non_blocking=True)
-            self._draw_done = torch.cuda.Event()
-            self._draw_done.record(stream)
             P = _capi.ptr
-            _capi.check(_capi.call("sgl_negatives_from_draws", m, P(out), P(self._pool_dev), self._pool_dev.numel(),
+            _capi.check(_capi.call("sgl_negatives_from_draws", m, slot[2], P(self._pool_dev), self._pool_dev.numel(),
                                    P(self._dev["dst"][s:hi]), P(out), P(self._neg_err.t), stream.cuda_stream),
                         "sgl_negatives_from_draws")
-        if front is not None:
-            torch.cuda.current_stream(self.device).wait_stream(front)
+            slot[1] = torch.cuda.Event()
+            slot[1].record(stream)
         self._neg_ahead[batch.split] = (s, hi)
 
     def _device_batch(self, batch: CTDGDataBatch):
@@ -314,6 +327,8 @@ class CTDGOnlineRuntime:
         start = batch.start
         planned = self.use_plans and n == b.max_batch and start >= 0 and step.timer is None
         if not planned:
+            if self._front_stream is not None:   # negatives drawn on the front stream
+                torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
             src, dst, ts, ef = self._device_batch(batch)
             self._front_body(step, split, n, src, dst, buf[off:off + n] if off >= 0 else buf, ts, ef, None)
             self._commit_body(step, train)

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -37,6 +37,7 @@ _DROP = [ctypes.c_float, ctypes.c_float, ctypes.c_uint64, _vp, _i32, _vp]
 SIGNATURES: dict[str, tuple] = {
     "sgl_abi_version": (ctypes.c_int, []),
     "sgl_last_error": (ctypes.c_char_p, []),
+    "sgl_host_device_pointer": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]),
     "sgl_tcsr_workspace_bytes": (_sz, [_i64, _i64]),
     "sgl_tcsr_build": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
     "sgl_recent_sample": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _vp, ctypes.c_int, _vp, _i64, _vp, _vp, _i32, _i32,
@@ -123,6 +124,16 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = lib().sgl_last_error()
         raise RuntimeError(f"{what}: {msg.decode() if msg else 'error code %d' % rc}")
+
+
+def host_device_pointer(t: torch.Tensor) -> int:
+    """The device-visible address of a pinned host tensor's first element
+    (sgl_host_device_pointer), for a kernel that reads it in place."""
+    if not t.is_pinned():
+        raise RuntimeError("host_device_pointer: the tensor is not in pinned host memory")
+    out = ctypes.c_void_p()
+    check(lib().sgl_host_device_pointer(ctypes.c_void_p(t.data_ptr()), ctypes.byref(out)), "sgl_host_device_pointer")
+    return int(out.value)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -30,10 +30,11 @@ def test_gru_kernel_matches_torch(gpu, K, D, F, dt, M):
     """The fused GRU + GRUCell against the oracle's torch modules: fp32 MFMA
     within rtol 1e-3; bf16 MFMA (bf16 weights and operands, fp32
     accumulation) within the bf16 tolerance rtol 2e-2, atol 2e-2 (outputs are
-    tanh-bounded, |h| < 1). The bf16 cases cover the wide-tile kernel's 16-,
-    32- and 64-root tiles (by batch size: 203, 9,000, 20,000 roots), a
-    partial last tile and a hidden size that is not a multiple of 16, and the
-    16-root kernel where the wide one does not apply (F = 5)."""
+    tanh-bounded, |h| < 1). The bf16 cases cover the wide-tile kernel's 16-
+    and 64-root tiles (203 and 9,000 roots: 16-root tiles; 17,001 and 20,000
+    roots: 64-root tiles), a partial last tile and a hidden size that is not a
+    multiple of 16, and the 16-root kernel where the wide one does not apply
+    (F = 5)."""
     from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
     torch.manual_seed(K)
     S = 2 * D + F
