@@ -232,9 +232,11 @@ def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> f
     return 0.0
 
 
-# HBM bytes per launch of k_memory_commit + k_edge_rows at B = 1,048,576 (rocprofv3 FETCH_SIZE x 2.000 +
-# WRITE_SIZE x 1.000, mean over four batches: profiles/gather_scatter_cfg5_B1M.md)
-GS_TRAFFIC_1M = 133_542_912
+# HBM bytes per launch at B = 1,048,576 (rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, mean over
+# four batches: profiles/gather_scatter_cfg5_B1M.md): k_memory_commit + k_edge_rows, and the same with
+# the bf16 GRU + mailbox kernel (k_gru_mailbox_wide)
+GS_TRAFFIC_1M = 43_632_742 + 92_720_026
+GS_TRAFFIC_FULL_1M = GS_TRAFFIC_1M + 323_274_752
 
 
 def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
@@ -364,10 +366,12 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     return {"value": gb / (us * 1e-6) / 1e9, "unit": "GB/s",
             "workload": f"gather/scatter: cfg5 state (N={N}, D={D}, K={K}, F={F}), k={k}, batches {list(batches)}",
             "cases": cases,
-            "roofline": {"bound": "hbm", "kernel": "k_gru_mailbox<bf16> + k_memory_commit + k_edge_rows",
+            "roofline": {"bound": "hbm", "kernel": "k_gru_mailbox_wide<bf16> + k_memory_commit + k_edge_rows",
                          "batch": max(batches), "alg_bytes_per_launch": gb,
                          "achieved": gb / (us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                         "frac": gb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                         "traffic": GS_TRAFFIC_FULL_1M if max(batches) == 1 << 20 else None,
+                         "traffic_source": "profiles/gather_scatter_cfg5_B1M.md",
                          "copy_kernels_only": {"kernel": "k_memory_commit + k_edge_rows",
                                                "achieved": gb2 / (us2 * 1e-6) / 1e9,
                                                "frac": gb2 / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS,
@@ -375,7 +379,7 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                                                "traffic_source": "profiles/gather_scatter_cfg5_B1M.md"}},
             "gru_mfma": {"kernel": "k_gru_mailbox<float>", "batch": max(batches), "flop_per_launch": round(gru_flop),
                          "achieved": gru_tf, "peak": 157.3, "unit": "TFLOP/s", "frac": gru_tf / 157.3},
-            "gru_mfma_bf16": {"kernel": "k_gru_mailbox<uint16_t> (bf16 GEMMs, fp32 accumulation)",
+            "gru_mfma_bf16": {"kernel": "k_gru_mailbox_wide (bf16 GEMMs, fp32 accumulation, 64-root tiles)",
                               "batch": max(batches), "flop_per_launch": round(gru_flop), "achieved": gru16_tf,
                               "peak": 2500.0, "unit": "TFLOP/s", "frac": gru16_tf / 2500.0}}
 
@@ -446,17 +450,18 @@ def _restore(rt, snap):
 
 # HBM bytes per launch (read + written) of a kernel on a workload, from the
 # rocprofv3 FETCH_SIZE / WRITE_SIZE runs summarised in
-# profiles/tgn_cfg4_hbm_traffic.md, profiles/tgn_cfg4_mfma_utilisation.md and
-# profiles/sampler_cfg3_hbm_traffic.md
+# profiles/tgn_cfg4_hbm_traffic.md and profiles/sampler_cfg3_hbm_traffic.md
 # (counters scaled by a copy kernel of known size); None where no counter run
 # was made.
-HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 1133.4 + 1504.5) * 1024),
-               ("cfg4", "edge_rows"): round((2 * 143.4 + 291.1) * 1024),
-               ("cfg4", "memory_commit"): round((2 * 63.8 + 93.9) * 1024),
-               ("cfg4", "conv_forward"): round((2 * 1824.3 + 1880.2) * 1024),
-               ("cfg4", "memory_update"): round((2 * 2311.0 + 256.2) * 1024),
-               ("cfg4", "predictor"): round((2 * 564.4 + 1006.8) * 1024),
-               ("cfg4", "param_update"): round((2 * 8017.6 + 2070.6) * 1024),
+HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 2753.8 + 1506.1) * 1024),
+               ("cfg4", "edge_rows"): round((2 * 128.7 + 291.1) * 1024),
+               ("cfg4", "memory_commit"): round((2 * 78.0 + 94.3) * 1024),
+               ("cfg4", "conv_forward"): round((2 * 1834.4 + 1880.2) * 1024),
+               ("cfg4", "memory_update"): round((2 * 2344.5 + 256.2) * 1024),
+               ("cfg4", "predictor"): round((2 * 582.4 + 569.2) * 1024),
+               ("cfg4", "param_update"): round((2 * 8020.5 + 2070.6) * 1024),
+               ("cfg4", "batch_prepare"): round((2 * 63.3 + 128.2) * 1024),
+               ("cfg4", "recent_sample"): round((2 * 380.8 + 22.1) * 1024),
                ("cfg3", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
 # the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
 TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
