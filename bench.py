@@ -564,7 +564,7 @@ def run_tgn(args, wl: dict) -> dict:
 
     batches = [ep.next() for _ in range(args.steps)]
     snap = _snapshot(rt)
-    dom = args.roofline_kernel
+    dom = args.roofline_kernel or ("memory_update" if wl.get("embedding") == "time_projection" else "conv_forward")
     timer: list = []
     if args.no_plans:   # eager steps: time the dominant kernel inside the timed region
         for st in rt.steps:
@@ -744,9 +744,11 @@ def main() -> None:
                     help="run steps eagerly (one library call at a time) instead of as recorded launch plans")
     ap.add_argument("--workload", default="tgn-large",
                     choices=sorted(list(WORKLOADS) + ["sampler", "gather-scatter"]))
-    ap.add_argument("--roofline-kernel", default="conv_forward",
+    ap.add_argument("--roofline-kernel", default=None,
                     choices=["batch_prepare", "recent_sample", "memory_update", "memory_commit", "edge_rows",
-                             "conv_forward", "conv_backward"])
+                             "conv_forward", "conv_backward"],
+                    help="the kernel the roofline object measures (default: conv_forward, or memory_update "
+                         "for the time-projection workload, which has no attention)")
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--epoch", action="store_true",
@@ -798,9 +800,12 @@ def main() -> None:
     base.update(steps=args.steps, warmup=args.warmup)  # --epoch sets them from the split
     line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"],
                 dtype="fp32" if args.memory_gemm_dtype == "fp32" else "fp32 (GRU GEMMs bf16)",
-                config={"workload": f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
-                                    f"H={wl['H']} k={wl['k']} hops={wl['history']} K={wl['K']} B={wl['B']}, "
-                                    "dropout 0",
+                config={"workload": (f"{wl['config']} ({args.workload}): JODIE train step (memory + GRU + time "
+                                     f"projection, no attention), D={wl['D']} K={wl['K']} B={wl['B']}"
+                                     if wl.get("embedding") == "time_projection" else
+                                     f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
+                                     f"H={wl['H']} k={wl['k']} hops={wl['history']} K={wl['K']} B={wl['B']}, "
+                                     "dropout 0"),
                         "global_batch": wl["B"], "parallelism": "single GPU"},
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
                 step_shape=r["step_shape"], final_train_loss=r["final_train_loss"])
