@@ -421,6 +421,11 @@ int sgl_time_projection_backward(int32_t D, int64_t capacity, const int32_t *num
  * group words and a top word, 64 words apart, so that the workgroups of a
  * large launch do not all count themselves on one word. */
 #define SGL_DONE_WORDS 1088
+/* done[SGL_DONE_RANGE_WORD] (a word the counter never uses) becomes nonzero
+ * when sgl_predictor met a value outside the fixed-point range of its sums
+ * (|v| >= 2^23, or NaN; the value is clamped, so the sums are wrong); the
+ * caller reads and clears it. */
+#define SGL_DONE_RANGE_WORD 32
 
 /* ---------------------------------------------------------------------------
  * Edge predictor + BCE, forward and (train != 0) backward.

@@ -98,10 +98,16 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // Fixed-point accumulation (SGL_FIXED_SHIFT fractional bits in an int64):
 // integer atomics are exact, so sums scattered by many workgroups do not
 // depend on the order the additions happen in. Values are clamped to the
-// int64 range; magnitudes stay far below it for the gradients summed here.
+// int64 range (|x| < 2^23 fits); to_fixed_checked reports a value outside it.
 __device__ __forceinline__ long long to_fixed(float x) {
   const float s = x * 0x1p40f;
   return static_cast<long long>(rintf(fminf(fmaxf(s, -9.0e18f), 9.0e18f)));
+}
+// to_fixed, and *flag |= 1 when x lies outside the range (|x| >= 2^23, or
+// NaN): the clamped value no longer adds up to the sum the caller wanted.
+__device__ __forceinline__ long long to_fixed_checked(float x, int32_t *flag) {
+  if (!(fabsf(x) < 0x1p23f)) atomicOr(flag, 1);
+  return to_fixed(x);
 }
 __device__ __forceinline__ float from_fixed(long long v) { return float(double(v) * 0x1p-40); }
 __device__ __forceinline__ void atomic_add_fixed(long long *p, long long v) {

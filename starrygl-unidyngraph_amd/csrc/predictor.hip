@@ -64,6 +64,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done, int agg,
     int64_t ystride, long long *__restrict__ acc_neg) {
   const bool sep = acc_neg != nullptr;  // the negatives' rows apart from the dst rows
+  int32_t *range_flag = done + SGL_DONE_RANGE_WORD;  // a value outside the fixed-point range
   long long *acc_n = sep ? acc_neg : acc_dst;
   extern __shared__ __align__(16) float lds[];
   const int ld = sgl::lds_ld(D);
@@ -189,19 +190,19 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   if (tid == 0) {
     float sp = 0.f;
     for (int i = 0; i < kRows; ++i) sp += s_sp[i];
-    sgl::atomic_add_fixed(&acc_out[D + 1], sgl::to_fixed(sp));
+    sgl::atomic_add_fixed(&acc_out[D + 1], sgl::to_fixed_checked(sp, range_flag));
   }
   if (train) {  // uniform
     // out_fc gradients: this tile's sums
     for (int j = tid; j < D; j += kBlock) {
       float gw = 0.f;
       for (int i = 0; i < kRows; ++i) gw += s_gp[i] * Hd[i * ld + j] + s_gn[i] * Hn[i * ld + j];
-      sgl::atomic_add_fixed(&acc_out[j], sgl::to_fixed(gw));
+      sgl::atomic_add_fixed(&acc_out[j], sgl::to_fixed_checked(gw, range_flag));
     }
     if (tid == 64) {
       float gb = 0.f;
       for (int i = 0; i < kRows; ++i) gb += s_gp[i] + s_gn[i];
-      sgl::atomic_add_fixed(&acc_out[D], sgl::to_fixed(gb));
+      sgl::atomic_add_fixed(&acc_out[D], sgl::to_fixed_checked(gb, range_flag));
     }
     // hidden-layer gradients, summed into their roots' rows
     const int U = *num_roots;
@@ -211,7 +212,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       const float ghp = Hd[i * ld + j] > 0.f ? s_gp[i] * Wo[j] : 0.f;
       const float ghn = Hn[i * ld + j] > 0.f ? s_gn[i] * Wo[j] : 0.f;
       const int a = s_idx[0][i], b = s_idx[1][i], c = s_idx[2][i];
-      const long long fp = sgl::to_fixed(ghp), fn = sgl::to_fixed(ghn);
+      const long long fp = sgl::to_fixed_checked(ghp, range_flag), fn = sgl::to_fixed_checked(ghn, range_flag);
       if (agg) {  // LDS atomics into the roots' leader rows
         auto add = [](long long *q, long long v) {
           atomicAdd(reinterpret_cast<unsigned long long *>(q), static_cast<unsigned long long>(v));

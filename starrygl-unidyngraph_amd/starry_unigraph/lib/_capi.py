@@ -23,6 +23,7 @@ SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
 SGL_FIXED_SHIFT = 40    # fractional bits of the predictor's int64 gradient accumulators
 SGL_DONE_WORDS = 1088   # int32 words of sgl_predictor's completion counter
+SGL_DONE_RANGE_WORD = 32   # its word that flags a value outside the fixed-point range
 SGL_COMPACT_NOALLOC_MAX_QUERIES = 1 << 24   # sgl_recent_compact_noalloc's limit
 
 _vp = ctypes.c_void_p

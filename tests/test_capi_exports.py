@@ -107,10 +107,11 @@ def test_plan_op_struct_layout_matches_header(tmp_path):
 
 def test_header_constants_match_binding(tmp_path):
     """The binding's copies of the header's constants (ABI version, device
-    error bits, fixed-point scale, completion-counter size) are the header's."""
+    error bits, fixed-point scale, completion-counter size and range-flag
+    word) are the header's."""
     from starry_unigraph.lib import _capi
     names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
-             "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES"]
+             "SGL_DONE_RANGE_WORD", "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES"]
     src = tmp_path / "consts.cpp"
     src.write_text('#include <cstdio>\n#include "starrygl_mi355x.h"\nint main() {\n'
                    + "".join(f'  printf("%d ", int({n}));\n' for n in names) + "  return 0;\n}\n")
@@ -119,7 +120,8 @@ def test_header_constants_match_binding(tmp_path):
                     "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
     want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_FIXED_SHIFT,
-            _capi.SGL_DONE_WORDS, _capi.SGL_OP_MAX_ARGS, _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES]
+            _capi.SGL_DONE_WORDS, _capi.SGL_DONE_RANGE_WORD, _capi.SGL_OP_MAX_ARGS,
+            _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES]
     assert got == want
 
 

@@ -123,3 +123,22 @@ def test_device_metrics_match_sklearn(gpu):
     want = co.metric_dict(pos, neg)
     for k, tol in (("ap", 1e-9), ("auc", 1e-9), ("mrr", 1e-6)):
         assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])
+
+
+def test_fixed_point_range_is_reported(gpu):
+    """A term outside the predictor's fixed-point range (forced from the host:
+    out_fc weights of 1e10 make the per-event loss and hidden-layer gradient
+    terms exceed 2^23) sets the range flag, check_sync raises and clears it;
+    ordinary steps leave it clear."""
+    cs = _session(0)
+    rt = cs.online_runtime
+    batches = list(rt.iter_batches("train", 200))
+    cs.train_step(batches[0])
+    rt.check_sync()
+    with torch.no_grad():
+        rt._core().out_fc.weight.fill_(1e10)
+    rt.fence()
+    cs.train_step(batches[1])
+    with pytest.raises(RuntimeError, match="fixed-point range"):
+        rt.check_sync()
+    rt.check_sync()
