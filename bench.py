@@ -44,18 +44,21 @@ sys.path.insert(0, os.path.join(REPO, "starrygl-unidyngraph_amd"))
 
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
 METRIC = "TGN train events/sec on 1 MI355X; sampler Mqueries/s; % HBM roofline"
 
 WORKLOADS = {
+    # precision: BASELINE's GEMM precision of the configuration (configs 4 and 5:
+    # "bf16 GEMMs with fp32 memory"; configs 1 and 2: fp32)
     "tgn-large": dict(config="cfg4", stream="unipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=600,
-                      history=1),
+                      history=1, precision="bf16"),
     "tgn-small": dict(config="cfg1", stream="bipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=200,
                       history=1),
     # config 2: memory + GRU + the JODIE time projection, no attention
     "jodie": dict(config="cfg2", stream="bipartite", family="jodie", D=100, T=100, H=2, k=10, K=1, B=200,
                   history=1, embedding="time_projection"),
     "tgn-stress": dict(config="cfg5", stream="unipartite", family="tgn", D=172, T=100, H=4, k=20, K=4, B=4000,
-                       history=2),
+                       history=2, precision="bf16"),
 }
 
 
@@ -402,6 +405,8 @@ def build_session(wl: dict, stream):
            "train": {"batch_size": wl["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
            "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"], "dropout": 0.0,
                     "att_dropout": 0.0, "memory_gemm_dtype": wl.get("gemm", "fp32"),
+                    "attention_gemm_dtype": wl.get("gemm", "fp32") if wl.get("embedding", "attention") == "attention"
+                    else "fp32",
                     "embedding": wl.get("embedding", "attention")},
            "sampling": {"neighbor_limit": [wl["k"]] * wl["history"], "history": wl["history"],
                         "strategy": "recent"}}
@@ -473,6 +478,13 @@ ENTRY_POINTS = {"batch_prepare": "sgl_batch_prepare", "recent_sample": "sgl_rece
                 "conv_backward": "sgl_conv_backward", "param_update": "sgl_grad_adam",
                 "time_projection": "sgl_time_projection_forward",
                 "time_projection_backward": "sgl_time_projection_backward"}
+
+
+def mfma_peak(name: str, wl: dict) -> float:
+    """The dense MFMA peak of the precision a step kernel's products run in
+    (the fused Adam's weight-gradient products are fp32 in every mode)."""
+    bf = wl.get("gemm") == "bf16" and name in ("conv_forward", "conv_backward", "predictor", "memory_update")
+    return BF16_PEAK_TFLOPS if bf else FP32_PEAK_TFLOPS
 
 
 def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str, float, float]:
@@ -635,7 +647,7 @@ def run_tgn(args, wl: dict) -> dict:
         bound = kernel_work(name, wl, 1, 1, 1, rt.dims)[0]
         wavg = sum(w[0] for w in work[name]) / len(work[name])
         if bound == "mfma":
-            ach, peak, unit = wavg / (avg * 1e-3) / 1e12, FP32_PEAK_TFLOPS, "TFLOP/s"
+            ach, peak, unit = wavg / (avg * 1e-3) / 1e12, mfma_peak(name, wl), "TFLOP/s"
         else:
             ach, peak, unit = wavg / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         breakdown[name] = {"avg_us": round(avg * 1e3, 2), "calls": len(ms), "bound": bound,
@@ -650,7 +662,7 @@ def run_tgn(args, wl: dict) -> dict:
     dwork = sum(w[0] for w in work[dom]) / len(work[dom])
     dexec = sum(w[1] for w in work[dom]) / len(work[dom])
     scale = 1e12 if bound == "mfma" else 1e9
-    peak, unit = (FP32_PEAK_TFLOPS, "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
+    peak, unit = (mfma_peak(dom, wl), "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
     ach = dwork / (dom_avg * 1e-3) / scale
     res = {
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
@@ -754,9 +766,10 @@ def main() -> None:
     ap.add_argument("--epoch", action="store_true",
                     help="TGN workloads: one warm-up epoch, then time one epoch of train batches (overrides "
                          "--steps / --warmup)")
-    ap.add_argument("--memory-gemm-dtype", default="fp32", choices=["fp32", "bf16"],
-                    help="the memory updater's GEMMs (TGN workloads): fp32 MFMA, or bf16 MFMA with fp32 "
-                         "accumulation (the mixed-precision setting; dtype reads fp32+bf16)")
+    ap.add_argument("--gemm-dtype", default="auto", choices=["auto", "fp32", "bf16"],
+                    help="the GRU, attention and edge-predictor GEMMs of the TGN workloads: fp32 MFMA, or bf16 "
+                         "MFMA on bf16 weight copies with fp32 accumulation and fp32 memory; auto: the "
+                         "configuration's BASELINE precision (configs 4 and 5 bf16, configs 1 and 2 fp32)")
     ap.add_argument("--no-gather-scatter", action="store_true",
                     help="skip the gather/scatter sub-benchmark of the default run")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -795,11 +808,13 @@ def main() -> None:
                     roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), cases=r.get("cases"))
         print(json.dumps(line), flush=True)
         return
-    wl = dict(WORKLOADS[args.workload], gemm=args.memory_gemm_dtype)
+    wl = WORKLOADS[args.workload]
+    gemm = wl.get("precision", "fp32") if args.gemm_dtype == "auto" else args.gemm_dtype
+    wl = dict(wl, gemm=gemm)
     r = run_tgn(args, wl)
     base.update(steps=args.steps, warmup=args.warmup)  # --epoch sets them from the split
     line = dict(base, value=r["value"], unit=r["unit"], ms_per_step=r["ms_per_step"],
-                dtype="fp32" if args.memory_gemm_dtype == "fp32" else "fp32 (GRU GEMMs bf16)",
+                dtype="fp32" if gemm == "fp32" else "bf16 (GEMM operands; fp32 accumulation, memory and Adam)",
                 config={"workload": (f"{wl['config']} ({args.workload}): JODIE train step (memory + GRU + time "
                                      f"projection, no attention), D={wl['D']} K={wl['K']} B={wl['B']}"
                                      if wl.get("embedding") == "time_projection" else

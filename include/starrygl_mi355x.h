@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 13
+#define SGL_ABI_VERSION 14
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -345,6 +345,29 @@ int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
  * 16), i.e. the row count of one ln_part / te_part tile; 0 if the
  * dimensions are unsupported. */
 int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
+/* bf16 copies of the attention and edge-predictor weights, for the bf16
+ * GEMM variants of sgl_conv_forward, sgl_conv_backward and sgl_predictor
+ * (argument bw; NULL: the fp32 products). BASELINE configs 4 and 5 ask for
+ * bf16 GEMMs with fp32 memory; the reference runs these products in fp32
+ * torch (models.py:77-137, 313-324), so this has no reference counterpart.
+ * Every matrix is row-major raw bf16 with rows of ld elements (ld % 8 == 0,
+ * 16-byte aligned) and zero padding columns, kept equal to the rounded fp32
+ * parameters by sgl_grad_adam's shadow stores (sgl_grad_shadows rebuilds
+ * them). With H heads of dh = D/H rows and C = D+F+T:
+ *   wq [D][ld_q] = w_q (D+T columns); wk, wv [D][ld_c] = w_k, w_v (C);
+ *   wout [D][ld_o] = w_out (2D);
+ *   wkt, wvt [C][ld_h] = w_k^T, w_v^T, head h's dh columns from h*hp
+ *   (hp % 8 == 0, hp >= dh);
+ *   wot [D][ld_d] = w_out[:, :D]^T;
+ *   ws, wd [D][ld_d] = the predictor's src_fc / dst_fc weights, wst, wdt
+ *   [D][ld_d] their transposes.
+ * The bf16 variants take the fp32 arguments too (biases, LayerNorm, time
+ * encoding, the backward's query term) and need dropout 0. Products round
+ * their fp32 activations to bf16 and accumulate in fp32. */
+typedef struct sgl_bf16_weights {
+  const uint16_t *wq, *wk, *wv, *wout, *wkt, *wvt, *wot, *ws, *wd, *wst, *wdt;
+  int32_t ld_q, ld_c, ld_o, ld_h, hp, ld_d;
+} sgl_bf16_weights;
 int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      int32_t fanout, int64_t capacity,
                      const int32_t *num_roots, const int32_t *any_edges,
@@ -358,7 +381,8 @@ int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H,
                      float *sv_agg, float *sv_z, float *sv_stats,
                      float *sv_phi0, float *S, float *y, float p_att, float p_out,
                      uint64_t seed, const uint64_t *rng_step, int32_t pass,
-                     float *sv_sdrop, hipStream_t stream);
+                     float *sv_sdrop, const sgl_bf16_weights *bw,
+                     hipStream_t stream);
 int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       int32_t fanout, int64_t capacity,
                       const int32_t *num_roots, const int32_t *any_edges,
@@ -378,7 +402,8 @@ int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H,
                       float *sigma, float *gQ, float *ln_part, float *te_part,
                       float p_att, float p_out, uint64_t seed,
                       const uint64_t *rng_step, int32_t pass,
-                      const float *sv_sdrop, hipStream_t stream);
+                      const float *sv_sdrop, const sgl_bf16_weights *bw,
+                      hipStream_t stream);
 /* The attention's dropout masks for rows [0, rows) of a pass, as the
  * kernels above draw them (values 0 or 1/(1-p)): att_mask [rows][fanout][H]
  * and out_mask [rows][D] (either may be NULL). For tests and debugging; no
@@ -450,7 +475,9 @@ int sgl_time_projection_backward(int32_t D, int64_t capacity, const int32_t *num
  * dL/dy through sgl_conv_backward. acc_out (int64 [D+2]) and done (int32
  * [SGL_DONE_WORDS]) are the launch's own accumulator and completion counter:
  * zero before the first call, left zero by every call. All sums over events are exact integer
- * sums, so results do not depend on the order of the workgroups.
+ * sums, so results do not depend on the order of the workgroups. With bw
+ * (may be NULL; sgl_bf16_weights) the src_fc / dst_fc products run on its
+ * bf16 copies ws, wd (y_pass_stride 0).
  * ------------------------------------------------------------------------- */
 int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   const int32_t *num_roots, const float *y,
@@ -460,7 +487,8 @@ int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   const float *b_o, float *pos_logits, float *neg_logits,
                   float *loss, int64_t *acc_src, int64_t *acc_dst,
                   float *g_wo, float *g_bo, int64_t *acc_out, int32_t *done,
-                  int64_t y_pass_stride, int64_t *acc_neg, hipStream_t stream);
+                  int64_t y_pass_stride, int64_t *acc_neg,
+                  const sgl_bf16_weights *bw, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the
@@ -501,6 +529,10 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * beta1^t) and coef[2*seg+1] = sqrt(1 - beta2^t) of the segment's step t
  * (device floats, written by sgl_adam_coef). gates is a host array of
  * nseg <= SGL_MAX_ADAM_SEGMENTS device pointers (NULL: every segment open).
+ * With shadow (may be NULL; see sgl_bf16_weights) a kind-0 job also stores
+ * each element's parameter, rounded to bf16 (nearest even), at
+ * shadow[sh_off + a*sh_ld + b] when sh_off >= 0 and at
+ * shadow[sht_off + b*sht_ld + a] (the transpose) when sht_off >= 0.
  * ------------------------------------------------------------------------- */
 #define SGL_MAX_ADAM_SEGMENTS 8
 
@@ -511,14 +543,22 @@ typedef struct sgl_grad_job {
   int64_t off;
   int64_t ps1, ps2;
   int32_t ldo, rows, cols, kind, seg, r_fixed, r_extra, tiles_b, tile0, npass;
+  int64_t sh_off, sht_off;
+  int32_t sh_ld, sht_ld;
 } sgl_grad_job;
 
 int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job,
                   int32_t num_tiles, const int32_t *num_roots, float *param,
                   float *grad, float *exp_avg, float *exp_avg_sq, int32_t nseg,
                   const int32_t *const *gates, const float *coef, float beta1,
-                  float beta2, float eps, float weight_decay,
+                  float beta2, float eps, float weight_decay, uint16_t *shadow,
                   hipStream_t stream);
+/* The bf16 copies of sgl_grad_adam's kind-0 jobs from the current
+ * parameters (no update): after the parameters are set outside the fused
+ * update (initialisation, a loaded checkpoint). No reference counterpart. */
+int sgl_grad_shadows(const sgl_grad_job *jobs, const int32_t *tile_job,
+                     int32_t num_tiles, const float *param, uint16_t *shadow,
+                     hipStream_t stream);
 
 /* Step counts and bias corrections for one sgl_grad_adam launch. Replaces
  * torch.optim.Adam's per-step `step += 1` and bias corrections (the

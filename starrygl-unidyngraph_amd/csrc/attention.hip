@@ -295,15 +295,16 @@ inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices, int ts_rows) {
   return size_t(L.Ts + size_t(ts_rows) * d.T - base);
 }
 
-template <int HM, int JM, bool DROP, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ h_root, const int32_t *__restrict__ cnt, float *__restrict__ X,
     const float *__restrict__ dt, float *__restrict__ S, ConvParams p, ConvSaved sv, float *__restrict__ y,
-    int ts_rows, sgl::DropCfg dc) {
+    int ts_rows, sgl::DropCfg dc, sgl_bf16_weights bw) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
+  static_assert(!(BF && DROP), "the bf16 products run without dropout");
   extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
   const FwdLds L = fwd_lds(d, lds, NW, WPR > 1);
@@ -364,7 +365,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   // in the edge loop.
   constexpr bool kPre = NW == 16;
   const bool staged = kPre && ts_rows > 0;
-  {
+  if constexpr (BF) {
+    const sgl::GemmJobBw jobs[1] = {{L.HT, L.ldh, bw.wq, bw.ld_q, p.b_q, L.Qs, L.ldr, D + T, D}};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     const sgl::GemmJob jobs[1] = {{L.HT, L.ldh, p.w_q, D + T, p.b_q, L.Qs, L.ldr, D + T, D}};
     tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
@@ -394,8 +398,16 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     for (int j = 0; j < dh; ++j) acc += L.Qs[i * L.ldr + h * dh + j] * p.b_k[h * dh + j];
     L.qb[i * H + h] = acc;
   }
-  // qt_h = Q_h W_k[h rows, :]  (kNN: rows of W_k are the reduction index)
-  {
+  // qt_h = Q_h W_k[h rows, :]  (kNN: rows of W_k are the reduction index;
+  // the bf16 products read W_k^T)
+  if constexpr (BF) {
+    sgl::GemmJobBw jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.Qs + h * dh, L.ldr, bw.wkt + h * bw.hp, bw.ld_h, nullptr, L.QT + h * C, L.ldq, dh,
+                 h < H ? C : 0};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     sgl::GemmJob jobs[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h)
@@ -603,7 +615,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   // agg_h = W_v[h rows] xbar_h + b_v[h]  -> AH[:, :D]; with attention
   // dropout the kept weights sum to s_h, not 1: agg_h = W_v xbar'_h + s_h b_v[h]
-  {
+  if constexpr (BF) {
+    sgl::GemmJobBw jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.QT + h * C, L.ldq, bw.wv + size_t(h) * dh * bw.ld_c, bw.ld_c, p.b_v + h * dh, L.AH + h * dh,
+                 L.lda, C, h < H ? dh : 0};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     sgl::GemmJob jobs[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h)
@@ -620,7 +639,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   __syncthreads();
   // z = W_out [agg | h] + b_out
-  {
+  if constexpr (BF) {
+    const sgl::GemmJobBw jobs[1] = {{L.AH, L.lda, bw.wout, bw.ld_o, p.b_out, L.Zs, L.ldr, 2 * D, D}};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     const sgl::GemmJob jobs[1] = {{L.AH, L.lda, p.w_out, 2 * D, p.b_out, L.Zs, L.ldr, 2 * D, D}};
     tile_products<sgl::kNT, RPW>(jobs, kWaves, L.scr);
   }
@@ -722,17 +744,18 @@ __device__ __forceinline__ void consume_rows(long long *__restrict__ acc_src, lo
   }
 }
 
-template <int HM, int JM, bool DROP, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const int32_t *__restrict__ cnt, const float *__restrict__ X, const float *__restrict__ S,
     const float *__restrict__ dt, ConvParams p,
     ConvSaved sv, const float *__restrict__ gy, long long *__restrict__ acc_src,
     long long *__restrict__ acc_dst, const float *__restrict__ w_s, const float *__restrict__ w_d,
-    float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g, sgl::DropCfg dc) {
+    float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g, sgl::DropCfg dc, sgl_bf16_weights bw) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;
   static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
+  static_assert(!(BF && DROP), "the bf16 products run without dropout");
   extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
   const BwdLds L = bwd_lds(d, lds, NW, WPR > 1);
@@ -803,9 +826,15 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       if (!two) L.XH[i * L.ldr + j] = 0.f;
     }
     __syncthreads();
-    const sgl::GemmJob jobs[2] = {{L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D},
-                                  {L.GQ, L.ldr, two ? w_d : w_s, D, nullptr, L.XH, L.ldr, D, two ? D : 0}};
-    tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
+    if constexpr (BF) {
+      const sgl::GemmJobBw jobs[2] = {{L.GA, L.ldr, bw.wst, bw.ld_d, nullptr, L.GY, L.ldr, D, D},
+                                      {L.GQ, L.ldr, bw.wdt, bw.ld_d, nullptr, L.XH, L.ldr, D, two ? D : 0}};
+      sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+    } else {
+      const sgl::GemmJob jobs[2] = {{L.GA, L.ldr, w_s, D, nullptr, L.GY, L.ldr, D, D},
+                                    {L.GQ, L.ldr, two ? w_d : w_s, D, nullptr, L.XH, L.ldr, D, two ? D : 0}};
+      tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
+    }
     __syncthreads();
   }
   // LayerNorm + ReLU backward; one wave per row (rows past the tile zeroed)
@@ -861,7 +890,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     g.gz[size_t(r0 + i) * D + j] = L.GZ[i * L.ldr + j];
   }
   // g_agg = gz W_out[:, :D]
-  {
+  if constexpr (BF) {
+    const sgl::GemmJobBw jobs[1] = {{L.GZ, L.ldr, bw.wot, bw.ld_d, nullptr, L.GA, L.ldr, D, D}};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     const sgl::GemmJob jobs[1] = {{L.GZ, L.ldr, p.w_out, 2 * D, nullptr, L.GA, L.ldr, D, D}};
     tile_products<sgl::kNN, RPW>(jobs, kWaves, L.scr);
   }
@@ -873,7 +905,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
   __syncthreads();
   // g_xbar_h = g_agg_h W_v[h rows, :]
-  {
+  if constexpr (BF) {
+    sgl::GemmJobBw jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.GA + h * dh, L.ldr, bw.wvt + h * bw.hp, bw.ld_h, nullptr, L.GX + h * C, L.ldq, dh,
+                 h < H ? C : 0};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     sgl::GemmJob jobs[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h)
@@ -1073,7 +1112,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     __syncthreads();
   }
   // gQ_h = W_k[h rows] G_h + b_k[h] sigma_h
-  {
+  if constexpr (BF) {
+    sgl::GemmJobBw jobs[HM];
+#pragma unroll
+    for (int h = 0; h < HM; ++h)
+      jobs[h] = {L.GX + h * C, L.ldq, bw.wk + size_t(h) * dh * bw.ld_c, bw.ld_c, nullptr, L.GQ + h * dh, L.ldr, C,
+                 h < H ? dh : 0};
+    sgl::tile_gemm16_bw_jobs(jobs, kWaves);
+  } else {
     sgl::GemmJob jobs[HM];
 #pragma unroll
     for (int h = 0; h < HM; ++h)
@@ -1171,6 +1217,15 @@ template <int HM, int JM>
 struct BwdPick {
   static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
+// the bf16-product instances (no dropout)
+template <int HM, int JM>
+struct FwdPickBf {
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
+template <int HM, int JM>
+struct BwdPickBf {
+  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
 // the dropout instances (masks, kept-weight sums)
 template <int HM, int JM>
 struct FwdPickDrop {
@@ -1180,6 +1235,23 @@ template <int HM, int JM>
 struct BwdPickDrop {
   static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
+
+// The bf16 weight copies' shapes (sgl_bf16_weights): every pointer set,
+// leading dimensions multiples of 8 and wide enough, rows 16-byte aligned.
+int check_bf16_weights(const Dims &d, const sgl_bf16_weights &w, bool drop) {
+  SGL_REQUIRE(!drop, "conv: the bf16 products run without dropout");
+  SGL_REQUIRE(w.wq && w.wk && w.wv && w.wout && w.wkt && w.wvt && w.wot && w.ws && w.wd && w.wst && w.wdt,
+              "conv: NULL bf16 weight copy");
+  const uint16_t *ptrs[] = {w.wq, w.wk, w.wv, w.wout, w.wkt, w.wvt, w.wot, w.ws, w.wd, w.wst, w.wdt};
+  for (const uint16_t *q : ptrs)
+    SGL_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15u) == 0, "conv: bf16 weight copy not 16-byte aligned");
+  const int32_t lds[] = {w.ld_q, w.ld_c, w.ld_o, w.ld_h, w.hp, w.ld_d};
+  for (int32_t v : lds) SGL_REQUIRE(v > 0 && v % 8 == 0, "conv: bf16 leading dimension %d not a positive multiple of 8", v);
+  SGL_REQUIRE(w.ld_q >= d.D + d.T && w.ld_c >= d.C && w.ld_o >= 2 * d.D && w.hp >= d.dh && w.ld_h >= d.H * w.hp &&
+                  w.ld_d >= d.D,
+              "conv: bf16 weight copies narrower than the dimensions");
+  return SGL_OK;
+}
 
 int drop_cfg(float p_att, float p_out, uint64_t seed, const uint64_t *rng_step, int32_t pass, const float *sdrop,
              sgl::DropCfg &dc, bool &drop) {
@@ -1280,12 +1352,15 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                                 const float *te_w, const float *te_b, float *sv_Q, float *sv_qt, float *sv_xbar,
                                 float *sv_score, float *sv_ml, float *sv_agg, float *sv_z, float *sv_stats,
                                 float *sv_phi0, float *S, float *y, float p_att, float p_out, uint64_t seed,
-                                const uint64_t *rng_step, int32_t pass, float *sv_sdrop, hipStream_t stream) {
+                                const uint64_t *rng_step, int32_t pass, float *sv_sdrop, const sgl_bf16_weights *bw,
+                                hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   sgl::DropCfg dc;
   bool drop;
   if (int rc = drop_cfg(p_att, p_out, seed, rng_step, pass, sv_sdrop, dc, drop)) return rc;
+  if (bw != nullptr)
+    if (int rc = check_bf16_weights(d, *bw, drop)) return rc;
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
@@ -1293,7 +1368,8 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                   ln_g && ln_b && te_w && te_b && sv_Q && sv_qt && sv_xbar && sv_ml && sv_agg && sv_z && sv_stats &&
                   y && (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_forward: NULL array");
-  const auto inst = drop ? pick_instance<FwdPickDrop>(d) : pick_instance<FwdPick>(d);
+  const auto inst = bw != nullptr ? pick_instance<FwdPickBf>(d)
+                    : drop ? pick_instance<FwdPickDrop>(d) : pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   // stage the tile's time encodings in LDS when they fit
   const bool slices = inst.waves > inst.rows;
@@ -1305,7 +1381,8 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
   ConvSaved sv{sv_Q, sv_qt, sv_xbar, sv_score, sv_ml, sv_agg, sv_z, sv_stats, sv_phi0, sv_sdrop};
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
-              num_roots, any_edges, h_root, cnt, X, dt, S, p, sv, y, ts_rows, dc);
+              num_roots, any_edges, h_root, cnt, X, dt, S, p, sv, y, ts_rows, dc,
+              bw != nullptr ? *bw : sgl_bf16_weights{});
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -1322,12 +1399,17 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                                  int64_t *acc_dst, const float *w_s, const float *w_d, float *g_src, float *g_dst,
                                  float *gz, float *gagg, float *G, float *sigma, float *gQ, float *ln_part,
                                  float *te_part, float p_att, float p_out, uint64_t seed, const uint64_t *rng_step,
-                                 int32_t pass, const float *sv_sdrop, hipStream_t stream) {
+                                 int32_t pass, const float *sv_sdrop, const sgl_bf16_weights *bw,
+                                 hipStream_t stream) {
   Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, fanout};
   if (int rc = check_dims(d)) return rc;
   sgl::DropCfg dc;
   bool drop;
   if (int rc = drop_cfg(p_att, p_out, seed, rng_step, pass, sv_sdrop, dc, drop)) return rc;
+  if (bw != nullptr) {
+    if (int rc = check_bf16_weights(d, *bw, drop)) return rc;
+    SGL_REQUIRE(gy != nullptr || acc_dst != nullptr, "conv_backward: the bf16 products need both accumulators");
+  }
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX && capacity % kRows == 0,
               "conv: capacity %lld must be a multiple of %d", (long long)capacity, kRows);
   if (capacity == 0) return SGL_OK;
@@ -1337,7 +1419,8 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                   gz && gagg && G && sigma && gQ && ln_part && te_part &&
                   (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_backward: NULL array");
-  const auto inst = drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
+  const auto inst = bw != nullptr ? pick_instance<BwdPickBf>(d)
+                    : drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
   const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
@@ -1351,7 +1434,7 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   sgl::launch(inst.fn, dim3(unsigned(capacity / inst.rows)), dim3(unsigned(inst.waves * 64)), lds, stream, d,
               num_roots, any_edges, cnt, X, S, dt, p, sv, gy,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), w_s, w_d, g_src, g_dst,
-              g, dc);
+              g, dc, bw != nullptr ? *bw : sgl_bf16_weights{});
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

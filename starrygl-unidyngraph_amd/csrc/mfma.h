@@ -444,6 +444,139 @@ __device__ __forceinline__ void tile_gemm16_jobs_bf16(const GemmJobBf16<AT> (&jo
 }
 
 // ---------------------------------------------------------------------------
+// 16-row products against padded bf16 weight copies (v_mfma_f32_16x16x32_bf16,
+// fp32 accumulation). W is [n_total][ldw] row-major bf16 with ldw % 8 == 0 and
+// 16-byte aligned rows, so every lane's eight weights of a k step are one
+// 16-byte buffer load at row n, k = 32 s + 8 q, with no bounds logic: reads
+// past the copy's span return 0 (the descriptor's range) and k >= kd meets a
+// zeroed A element, so the weights there only need to be finite. A is an
+// fp32 LDS tile (16 rows, leading dim lda) rounded to bf16 (nearest even) as
+// it is read. Each block issues all of its weight loads (up to 8 k steps)
+// before the first MFMA: the products are short and latency-bound.
+struct GemmJobBw {
+  const float *A;
+  int lda;
+  const uint16_t *W;
+  int ldw;
+  const float *bias;  // fp32 [n_total] or NULL
+  float *OUT;
+  int ldo;
+  int kd, n_total;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bf16_weight_rsrc(const uint16_t *p, uint32_t elems) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(a >> 32));
+  const uint32_t bytes = __builtin_amdgcn_readfirstlane(elems * 2u);
+  uint16_t *u = reinterpret_cast<uint16_t *>((uint64_t(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, int(bytes), 0x00020000);
+}
+
+// A[row][k .. k+8) as bf16, elements at k >= kd zero. CLS: 2 = 16-byte
+// aligned rows (two 16-byte LDS reads), 1 = 8-byte aligned (four 8-byte
+// reads), 0 = 4-byte reads; the last, partial step clamps and masks.
+template <int CLS>
+__device__ __forceinline__ bf16x8 load_a_bf16(const float *__restrict__ arow, int k, int kd) {
+  bf16x8 a;
+  if (k + 8 <= kd) {
+    if constexpr (CLS == 2) {
+      return bf16x8_from_f32(*reinterpret_cast<const f32x4 *>(arow + k), *reinterpret_cast<const f32x4 *>(arow + k + 4));
+    } else if constexpr (CLS == 1) {
+      typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const f32x2 v = *reinterpret_cast<const f32x2 *>(arow + k + 2 * t);
+        a[2 * t] = static_cast<__bf16>(v[0]);
+        a[2 * t + 1] = static_cast<__bf16>(v[1]);
+      }
+      return a;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float v = arow[min(k + j, kd - 1)];
+    a[j] = static_cast<__bf16>(k + j < kd ? v : 0.f);
+  }
+  return a;
+}
+
+template <int CLS>
+__device__ __forceinline__ f32x4 mfma_block16_bw_cls(const float *__restrict__ A, int lda, __amdgpu_buffer_rsrc_t wr,
+                                                     uint32_t wrow, int kd) {
+  const int lane = threadIdx.x & 63;
+  const float *arow = A + (lane & 15) * lda;
+  const int q = lane >> 4;
+  const int nks = (kd + 31) >> 5;
+  constexpr int kU = 8;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+  for (int ks0 = 0; ks0 < nks; ks0 += kU) {
+    bf16x8 b[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (ks0 + u >= nks) break;  // uniform
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, int((wrow + 32u * uint32_t(ks0 + u)) * 2u), 0, 0);
+      b[u] = __builtin_bit_cast(bf16x8, v);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (ks0 + u >= nks) break;
+      const bf16x8 a = load_a_bf16<CLS>(arow, 32 * (ks0 + u) + 8 * q, kd);
+      if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc1, 0, 0, 0);
+      else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc0, 0, 0, 0);
+    }
+  }
+  return acc0 + acc1;
+}
+
+// One 16x16 output block (rows 0..15 of A, columns n0..n0+15 of W^T); this
+// lane's accumulators are rows 4*(lane/16)+v, column n0 + lane%16. Columns
+// past n_total read row n_total-1 (their outputs are discarded).
+__device__ __forceinline__ f32x4 mfma_block16_bw(const float *__restrict__ A, int lda, const uint16_t *__restrict__ W,
+                                                 int ldw, int n0, int kd, int n_total) {
+  const int lane = threadIdx.x & 63;
+  const int n = min(n0 + (lane & 15), n_total - 1);
+  const __amdgpu_buffer_rsrc_t wr = bf16_weight_rsrc(W, uint32_t(n_total) * uint32_t(ldw));
+  const uint32_t wrow = uint32_t(n) * uint32_t(ldw) + 8u * uint32_t(lane >> 4);
+  const uintptr_t ab = reinterpret_cast<uintptr_t>(A);
+  if ((ab & 15) == 0 && (lda & 3) == 0) return mfma_block16_bw_cls<2>(A, lda, wr, wrow, kd);
+  if ((ab & 7) == 0 && (lda & 1) == 0) return mfma_block16_bw_cls<1>(A, lda, wr, wrow, kd);
+  return mfma_block16_bw_cls<0>(A, lda, wr, wrow, kd);
+}
+
+// OUT (LDS, 16 x n_total) = A * W^T + bias for every job, the 16-column
+// blocks of all jobs dealt over the workgroup's waves. No barrier inside.
+template <int NJOBS>
+__device__ __forceinline__ void tile_gemm16_bw_jobs(const GemmJobBw (&jobs)[NJOBS], int nwaves) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < NJOBS; ++j) total += (jobs[j].n_total + 15) >> 4;
+  for (int blk = wave; blk < total; blk += nwaves) {
+    GemmJobBw jb = jobs[0];
+    int nb = blk, first = 0;
+#pragma unroll
+    for (int j = 0; j < NJOBS; ++j) {
+      const int nbj = (jobs[j].n_total + 15) >> 4;
+      if (blk >= first && blk < first + nbj) {
+        jb = jobs[j];
+        nb = blk - first;
+      }
+      first += nbj;
+    }
+    const int n0 = nb * 16;
+    const int col = n0 + (lane & 15);
+    const float bv = jb.bias != nullptr && col < jb.n_total ? jb.bias[col] : 0.f;
+    const f32x4 acc = mfma_block16_bw(jb.A, jb.lda, jb.W, jb.ldw, n0, jb.kd, jb.n_total);
+    if (col < jb.n_total) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) jb.OUT[(4 * (lane >> 4) + v) * jb.ldo + col] = acc[v] + bv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Four-row tiles (a workgroup's 4 live roots): v_mfma_f32_4x4x1_16b_f32 runs
 // 16 independent 4x4x1 blocks. With every block fed the same four A rows and
 // block b taking columns 4b..4b+3 of a 64-column strip, one instruction adds

@@ -81,7 +81,10 @@ extern "C" int sgl_adam_advance(float *step, const int32_t *active, hipStream_t 
 // this step, applies the Adam update to the parameter and moments with the
 // bias corrections in coef (k_adam_coef, enqueued earlier). No workgroup
 // reads a value another one of this launch writes, and none counts
-// completions: the step counts advance in k_adam_coef.
+// completions: the step counts advance in k_adam_coef. A kind-0 job may
+// also keep bf16 copies of its parameter block (as is and transposed, at
+// the job's shadow offsets) for the bf16 products of the attention and the
+// edge predictor; they are written from the parameter after the update.
 namespace {
 
 constexpr int kGaBlock = 256;
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
                                                        float *__restrict__ g, float *__restrict__ m,
                                                        float *__restrict__ v, AdamSegs segs,
                                                        const float *__restrict__ coef, float b1, float b2, float eps,
-                                                       float wd) {
+                                                       float wd, uint16_t *__restrict__ shadow) {
   __shared__ float red[4][16][17];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int t = blockIdx.x;
@@ -110,10 +113,13 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
   int64_t idx = 0;
   bool valid = false;
   float gv = 0.f, pv = 0.f, mv = 0.f, vv = 0.f;
+  int ea = 0, eb = 0;  // a kind-0 element's position in its block
   if (jb.kind == 0) {
     const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
     const int a0 = 16 * ta, b0 = 16 * tb;
     const int oa = tid >> 4, ob = tid & 15;
+    ea = a0 + oa;
+    eb = b0 + ob;
     valid = a0 + oa < jb.rows && b0 + ob < jb.cols;
     idx = jb.off + int64_t(a0 + oa) * jb.ldo + (b0 + ob);
     // this thread's Adam operands, loaded while the tile is reduced
@@ -171,8 +177,31 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
     m[idx] = mv;
     v[idx] = vv;
     const float denom = sqrtf(vv) / bc2_sqrt + eps;
-    p[idx] = pv - step_size * (mv / denom);
+    pv = pv - step_size * (mv / denom);
+    p[idx] = pv;
   }
+  if (shadow != nullptr && valid && jb.kind == 0) {
+    const uint16_t hv = __builtin_bit_cast(uint16_t, static_cast<__bf16>(pv));
+    if (jb.sh_off >= 0) shadow[jb.sh_off + int64_t(ea) * jb.sh_ld + eb] = hv;
+    if (jb.sht_off >= 0) shadow[jb.sht_off + int64_t(eb) * jb.sht_ld + ea] = hv;
+  }
+}
+
+// The bf16 copies of every kind-0 job's block from the parameters as they
+// are (one 16x16 tile per workgroup, as k_grad_adam deals them).
+__global__ __launch_bounds__(kGaBlock) void k_grad_shadows(const sgl_grad_job *__restrict__ jobs,
+                                                          const int32_t *__restrict__ tile_job,
+                                                          const float *__restrict__ p,
+                                                          uint16_t *__restrict__ shadow) {
+  const sgl_grad_job jb = jobs[tile_job[blockIdx.x]];
+  if (jb.kind != 0 || (jb.sh_off < 0 && jb.sht_off < 0)) return;
+  const int local = int(blockIdx.x) - jb.tile0;
+  const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
+  const int ea = 16 * ta + (threadIdx.x >> 4), eb = 16 * tb + (threadIdx.x & 15);
+  if (ea >= jb.rows || eb >= jb.cols) return;
+  const uint16_t hv = __builtin_bit_cast(uint16_t, static_cast<__bf16>(p[jb.off + int64_t(ea) * jb.ldo + eb]));
+  if (jb.sh_off >= 0) shadow[jb.sh_off + int64_t(ea) * jb.sh_ld + eb] = hv;
+  if (jb.sht_off >= 0) shadow[jb.sht_off + int64_t(eb) * jb.sht_ld + ea] = hv;
 }
 
 // One lane: advance the open segments' step counts and write the bias
@@ -211,13 +240,24 @@ AdamSegs make_segs(int nseg, float *const *steps, const int32_t *const *gates) {
 extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, int32_t num_tiles,
                              const int32_t *num_roots, float *param, float *grad, float *exp_avg, float *exp_avg_sq,
                              int32_t nseg, const int32_t *const *gates, const float *coef, float beta1, float beta2,
-                             float eps, float weight_decay, hipStream_t stream) {
+                             float eps, float weight_decay, uint16_t *shadow, hipStream_t stream) {
   SGL_REQUIRE(num_tiles >= 0, "grad_adam: num_tiles < 0");
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "grad_adam: nseg %d out of range", nseg);
   if (num_tiles == 0) return SGL_OK;
   SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && coef, "grad_adam: NULL array");
   sgl::launch(&k_grad_adam, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, num_roots, param,
-              grad, exp_avg, exp_avg_sq, make_segs(nseg, nullptr, gates), coef, beta1, beta2, eps, weight_decay);
+              grad, exp_avg, exp_avg_sq, make_segs(nseg, nullptr, gates), coef, beta1, beta2, eps, weight_decay,
+              shadow);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+extern "C" int sgl_grad_shadows(const sgl_grad_job *jobs, const int32_t *tile_job, int32_t num_tiles,
+                                const float *param, uint16_t *shadow, hipStream_t stream) {
+  SGL_REQUIRE(num_tiles >= 0, "grad_shadows: num_tiles < 0");
+  if (num_tiles == 0) return SGL_OK;
+  SGL_REQUIRE(jobs && tile_job && param && shadow, "grad_shadows: NULL array");
+  sgl::launch(&k_grad_shadows, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, param, shadow);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

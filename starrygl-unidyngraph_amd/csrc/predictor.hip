@@ -54,6 +54,7 @@ __global__ __launch_bounds__(256) void k_zero(ZeroSpans z) {
     if (i < z.n[k]) z.p[k][i] = 0.f;
 }
 
+template <bool BF>
 __global__ __launch_bounds__(kBlock) void k_predictor(
     int64_t batch, int D, int train, const int32_t *__restrict__ num_roots, const float *__restrict__ y,
     const int32_t *__restrict__ rs, const int32_t *__restrict__ rd, const int32_t *__restrict__ rn,
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     float *__restrict__ pos_out, float *__restrict__ neg_out, float *__restrict__ loss,
     long long *__restrict__ acc_src, long long *__restrict__ acc_dst, float *__restrict__ g_wo,
     float *__restrict__ g_bo, long long *__restrict__ acc_out, int32_t *__restrict__ done, int agg,
-    int64_t ystride, long long *__restrict__ acc_neg) {
+    int64_t ystride, long long *__restrict__ acc_neg, sgl_bf16_weights bw) {
   const bool sep = acc_neg != nullptr;  // the negatives' rows apart from the dst rows
   int32_t *range_flag = done + SGL_DONE_RANGE_WORD;  // a value outside the fixed-point range
   long long *acc_n = sep ? acc_neg : acc_dst;
@@ -138,14 +139,20 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       // the bias is loaded before the block's k loop (one round trip less)
       const float bv = col < D ? (u < nblk ? b_s[col] : b_d[col]) : 0.f;
       if (u < nblk) {
-        const sgl::f32x4 acc = sgl::mfma_block16<sgl::kNT>(Es, ld, w_s, D, n0, D, D);
+        const sgl::f32x4 acc = BF ? sgl::mfma_block16_bw(Es, ld, bw.ws, bw.ld_d, n0, D, D)
+                                  : sgl::mfma_block16<sgl::kNT>(Es, ld, w_s, D, n0, D, D);
         if (col < D) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) Hs[(4 * (lane >> 4) + v) * ld + col] = acc[v] + bv;
         }
       } else {
         sgl::f32x4 ad, an;
-        sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
+        if constexpr (BF) {
+          ad = sgl::mfma_block16_bw(Ed, ld, bw.wd, bw.ld_d, n0, D, D);
+          an = sgl::mfma_block16_bw(En, ld, bw.wd, bw.ld_d, n0, D, D);
+        } else {
+          sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
+        }
         if (col < D) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
@@ -274,13 +281,18 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
                              const float *w_s, const float *b_s, const float *w_d, const float *b_d,
                              const float *w_o, const float *b_o, float *pos_logits, float *neg_logits, float *loss,
                              int64_t *acc_src, int64_t *acc_dst, float *g_wo, float *g_bo, int64_t *acc_out,
-                             int32_t *done, int64_t y_pass_stride, int64_t *acc_neg, hipStream_t stream) {
+                             int32_t *done, int64_t y_pass_stride, int64_t *acc_neg, const sgl_bf16_weights *bw,
+                             hipStream_t stream) {
   SGL_REQUIRE(batch >= 0 && batch < INT_MAX && D > 0 && capacity >= 0, "predictor: bad sizes");
   SGL_REQUIRE(num_roots && y && ridx_src && ridx_dst && ridx_neg && w_s && b_s && w_d && b_d && w_o && b_o &&
                   pos_logits && neg_logits && loss && acc_out && done,
               "predictor: NULL array");
   SGL_REQUIRE(!train || (acc_src && acc_dst && g_wo && g_bo), "predictor: NULL gradient array");
   SGL_REQUIRE(y_pass_stride >= 0, "predictor: negative y_pass_stride");
+  SGL_REQUIRE(bw == nullptr || (bw->ws && bw->wd && bw->ld_d >= D && bw->ld_d % 8 == 0 && y_pass_stride == 0 &&
+                                (reinterpret_cast<uintptr_t>(bw->ws) & 15u) == 0 &&
+                                (reinterpret_cast<uintptr_t>(bw->wd) & 15u) == 0),
+              "predictor: bad bf16 weight copies (or a dropout pass stride with them)");
   if (batch == 0) {  // no events: zero loss and out_fc gradients
     const ZeroSpans z{{loss, train ? g_wo : nullptr, train ? g_bo : nullptr, nullptr}, {1, train ? D : 0, train, 0}};
     k_zero<<<unsigned((D + 255) / 256), 256, 0, stream>>>(z);
@@ -293,12 +305,13 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
   const size_t lds_agg = lds0 + sizeof(long long) * 3 * kRows * size_t(D);
   const int agg = train && lds_agg <= 160 * 1024 ? 1 : 0;
   const size_t lds = agg ? lds_agg : lds0;
-  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_predictor), lds));
-  sgl::launch(&k_predictor, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
+  auto kern = bw != nullptr ? &k_predictor<true> : &k_predictor<false>;
+  SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(kern), lds));
+  sgl::launch(kern, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
               num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
               reinterpret_cast<long long *>(acc_src), reinterpret_cast<long long *>(acc_dst), g_wo, g_bo,
               reinterpret_cast<long long *>(acc_out), done, agg, y_pass_stride,
-              train ? reinterpret_cast<long long *>(acc_neg) : nullptr);
+              train ? reinterpret_cast<long long *>(acc_neg) : nullptr, bw != nullptr ? *bw : sgl_bf16_weights{});
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

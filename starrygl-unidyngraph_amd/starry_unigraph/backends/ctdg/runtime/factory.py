@@ -55,7 +55,8 @@ def build_ctdg_runtime(session_ctx: SessionContext, events=None) -> tuple[CTDGOn
     model = build_ctdg_model(str(cfg["model"]["family"]), num_nodes=dataset.num_nodes, hidden_dim=hidden_dim,
                              edge_feat_dim=edge_feat_dim, dim_time=dim_time, num_head=num_head, dropout=dropout,
                              att_dropout=att_dropout, embedding=embedding, time_shift=shift,
-                             time_scale=scale).to(device)
+                             time_scale=scale,
+                             attention_gemm_dtype=str(c.get("attention_gemm_dtype", "fp32"))).to(device)
     memory_updater = CTDGMemoryUpdater(hidden_dim=hidden_dim, mailbox_slot_dim=2 * hidden_dim + edge_feat_dim,
                                        mailbox_slots=mailbox_slots,
                                        gemm_dtype=str(c.get("memory_gemm_dtype", "fp32"))).to(device)

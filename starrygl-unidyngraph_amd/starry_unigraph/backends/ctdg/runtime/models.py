@@ -59,6 +59,16 @@ class TemporalTransformerConv(nn.Module):
         # dropout masks come from a counter-based generator keyed by this seed
         # and the step buffers' counter (torch's generators are not consumed)
         self.dropout_seed = int(torch.initial_seed()) & 0xFFFFFFFFFFFFFFFF
+        # "bf16": the fused step runs the attention and edge-predictor
+        # products on bf16 weight copies (fp32 accumulation)
+        self.gemm_dtype = "fp32"
+
+    def set_gemm_dtype(self, dtype: str) -> None:
+        if dtype not in ("fp32", "bf16"):
+            raise ValueError(f"attention GEMM dtype {dtype!r}: expected 'fp32' or 'bf16'")
+        if dtype == "bf16" and (self.dropout.p != 0 or self.att_dropout.p != 0):
+            raise ValueError("the bf16 attention products run without dropout (set dropout and att_dropout to 0)")
+        self.gemm_dtype = dtype
 
     def kernel_params(self) -> list[torch.Tensor]:
         return [self.time_enc.w.weight, self.time_enc.w.bias, self.w_q.weight, self.w_q.bias, self.w_k.weight,
@@ -248,9 +258,12 @@ CTDG_MODEL_SPECS: dict[str, CTDGModelSpec] = {
 
 def build_ctdg_model(model_family: str, *, num_nodes: int, hidden_dim: int, edge_feat_dim: int, dim_time: int = 100,
                      num_head: int = 2, dropout: float = 0.1, att_dropout: float = 0.1,
-                     embedding: str = "attention", time_shift: float = 0.0, time_scale: float = 1.0) -> nn.Module:
+                     embedding: str = "attention", time_shift: float = 0.0, time_scale: float = 1.0,
+                     attention_gemm_dtype: str = "fp32") -> nn.Module:
     """models.py:345-386. ``embedding`` "attention" (the reference's model for
-    every family) or "time_projection" (config 2's JODIE embedding)."""
+    every family) or "time_projection" (config 2's JODIE embedding);
+    ``attention_gemm_dtype`` "bf16": the attention and edge-predictor products
+    on bf16 weight copies (BASELINE configs 4 and 5)."""
     spec = CTDG_MODEL_SPECS.get(model_family.lower())
     if spec is None:
         raise KeyError(f"Unsupported CTDG model family: {model_family}")
@@ -259,5 +272,10 @@ def build_ctdg_model(model_family: str, *, num_nodes: int, hidden_dim: int, edge
                                            time_scale=time_scale)
     if embedding != "attention":
         raise KeyError(f"unknown ctdg.embedding {embedding!r}: expected 'attention' or 'time_projection'")
-    return spec.model_cls(num_nodes=num_nodes, hidden_dim=hidden_dim, edge_feat_dim=edge_feat_dim,
-                          dim_time=dim_time, num_head=num_head, dropout=dropout, att_dropout=att_dropout)
+    model = spec.model_cls(num_nodes=num_nodes, hidden_dim=hidden_dim, edge_feat_dim=edge_feat_dim,
+                           dim_time=dim_time, num_head=num_head, dropout=dropout, att_dropout=att_dropout)
+    if getattr(model, "conv", None) is not None:
+        model.conv.set_gemm_dtype(attention_gemm_dtype)
+    elif attention_gemm_dtype != "fp32":
+        raise ValueError(f"model family {model_family!r} has no attention for ctdg.attention_gemm_dtype")
+    return model

@@ -28,7 +28,7 @@ import torch
 import torch.nn.functional as F
 
 from starry_unigraph.lib import _capi
-from starry_unigraph.native.step import ConvDims, DeviceStep, FusedAdam, StepParamUpdate
+from starry_unigraph.native.step import Bf16Shadow, ConvDims, DeviceStep, FusedAdam, StepParamUpdate
 
 from .data import CTDGDataBatch, TGTemporalDataset
 from .memory import CTDGMemoryBank
@@ -130,6 +130,11 @@ class CTDGOnlineRuntime:
         self._state_writes = memory.state.writes
         # training steps so far (the dropout masks' step; sgl_adam_coef advances it)
         self._rng_counter = torch.zeros(1, dtype=torch.int64, device=self.device)
+        # bf16 copies of the attention / predictor weights when the conv runs
+        # its products in bf16 (the fused update keeps them current; dirty:
+        # rebuild from the parameters before the next step)
+        self._bf16: Bf16Shadow | None = None
+        self._bf16_dirty = True
 
     def _make_steps(self, max_batch: int) -> None:
         # every hop of the sampler (history layers, sampler.py:76-90) is
@@ -322,11 +327,40 @@ class CTDGOnlineRuntime:
         return d["src"][ev], d["dst"][ev], d["ts"][ev], d["edge_feat"][ev].contiguous()
 
     # ------------------------------------------------------------- the step
+    def params_changed(self) -> None:
+        """Parameters were written outside the fused update (a loaded
+        checkpoint, user code): rebuild the bf16 weight copies before the
+        next step."""
+        self._bf16_dirty = True
+
+    def _bf16_sync(self) -> None:
+        """With bf16 attention products: the weight copies exist, every step
+        buffer set uses them and they match the parameters (rebuilt on the
+        current stream when marked dirty)."""
+        core = self._core()
+        conv = getattr(core, "conv", None)
+        if conv is None or getattr(conv, "gemm_dtype", "fp32") != "bf16":
+            return
+        if self._bf16 is None:
+            self._bf16 = Bf16Shadow(self.dims, self.device)
+            # the fused updates are rebuilt with the copies' stores (and the
+            # plans that point at their job tables dropped first)
+            self.reset_plans()
+            self._updates.clear()
+            self._bf16_dirty = True
+        for st in self.steps:
+            st.bf16 = self._bf16
+        if self._bf16_dirty:
+            self._bf16.refresh(conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight,
+                               core.src_fc.weight, core.dst_fc.weight)
+            self._bf16_dirty = False
+
     def _forward(self, batch: CTDGDataBatch, split: str, train: bool) -> StepTensors:
         n = batch.size
         if n > self.steps[0].buf.max_batch or self._dropout_passes() != self._passes:
             self._make_steps(max(n, self.steps[0].buf.max_batch))
             self.reset_plans()
+        self._bf16_sync()
         q = self._parity
         self._parity = q ^ 1
         step = self.steps[q]
@@ -496,7 +530,7 @@ class CTDGOnlineRuntime:
                 upd = StepParamUpdate(step, inner, [tp.weight, tp.bias], pred, [None, None], kind="projection")
             else:
                 upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None],
-                                      passes=step.buf.passes, counter=self._rng_counter)
+                                      passes=step.buf.passes, counter=self._rng_counter, shadow=self._bf16)
             self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
             self._updates[id(step)] = upd
         return upd

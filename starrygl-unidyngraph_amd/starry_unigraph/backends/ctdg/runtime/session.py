@@ -82,6 +82,7 @@ class CTDGSession:
             if rt.memory_updater is not None and "memory_updater" in ckpt:
                 rt.memory_updater.load_state_dict(ckpt["memory_updater"])
                 rt.memory_updater.kernel_weights()   # refresh bf16 copies in place
+        rt.params_changed()   # the attention's bf16 weight copies, before the next step
         rt.fence()
 
 

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -63,17 +63,19 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_memory_gather": (ctypes.c_int, [_i32, _i64] + [_vp] * 8),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
     "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 8),
-    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 29 + _DROP + [_vp]),
-    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 39 + _DROP + [_vp]),
+    "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 29 + _DROP + [_vp, _vp]),
+    "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 39 + _DROP + [_vp, _vp]),
     "sgl_dropout_masks": (ctypes.c_int, [_i64, _i32, _i32, _i32, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
                                          _vp, _i32, _vp, _vp, _vp]),
-    "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 20 + [_i64, _vp, _vp]),
+    "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 20 + [_i64, _vp, _vp, _vp]),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
     "sgl_time_next_launch": (ctypes.c_int, [_vp, _vp]),
     "sgl_plan_op_kind": (_i32, [ctypes.c_char_p, _vp]),
     "sgl_plan_run": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _vp] + [ctypes.c_uint32] * 2 + [_i32, _vp, _vp]),
-    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 2 + [ctypes.c_float] * 4 + [_vp]),
+    "sgl_grad_adam": (ctypes.c_int, [_vp, _vp, _i32] + [_vp] * 5 + [_i32] + [_vp] * 2 + [ctypes.c_float] * 4
+                      + [_vp, _vp]),
+    "sgl_grad_shadows": (ctypes.c_int, [_vp, _vp, _i32, _vp, _vp, _vp]),
     "sgl_adam_coef": (ctypes.c_int, [_i32] + [_vp] * 3 + [ctypes.c_float] * 3 + [_vp] * 3),
 }
 
@@ -153,10 +155,23 @@ def stream_of(device: torch.device) -> int:
 
 
 class GradJob(ctypes.Structure):
-    """struct sgl_grad_job of include/starrygl_mi355x.h."""
+    """struct sgl_grad_job of include/starrygl_mi355x.h (no bf16 copies
+    unless sh_off / sht_off are given)."""
     _fields_ = [("x1", _vp), ("x2", _vp), ("s1", _i64), ("s2", _i64), ("off", _i64), ("ps1", _i64), ("ps2", _i64),
                 ("ldo", _i32), ("rows", _i32), ("cols", _i32), ("kind", _i32), ("seg", _i32),
-                ("r_fixed", _i32), ("r_extra", _i32), ("tiles_b", _i32), ("tile0", _i32), ("npass", _i32)]
+                ("r_fixed", _i32), ("r_extra", _i32), ("tiles_b", _i32), ("tile0", _i32), ("npass", _i32),
+                ("sh_off", _i64), ("sht_off", _i64), ("sh_ld", _i32), ("sht_ld", _i32)]
+
+    def __init__(self, **kw):
+        kw.setdefault("sh_off", -1)
+        kw.setdefault("sht_off", -1)
+        super().__init__(**kw)
+
+
+class Bf16Weights(ctypes.Structure):
+    """struct sgl_bf16_weights of include/starrygl_mi355x.h."""
+    _fields_ = [(n, _vp) for n in ("wq", "wk", "wv", "wout", "wkt", "wvt", "wot", "ws", "wd", "wst", "wdt")] + \
+               [(n, _i32) for n in ("ld_q", "ld_c", "ld_o", "ld_h", "hp", "ld_d")]
 
 
 SGL_OP_MAX_ARGS = 64

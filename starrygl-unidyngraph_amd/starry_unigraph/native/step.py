@@ -189,6 +189,94 @@ class StepBuffers:
         self.te_part = z(P * self.tiles, 2, max(dims.T, 1))
 
 
+class Bf16Shadow:
+    """bf16 copies of the attention and edge-predictor weights for the bf16
+    products of sgl_conv_forward / sgl_conv_backward / sgl_predictor
+    (struct sgl_bf16_weights): padded row-major matrices in one zeroed device
+    buffer, kept current by the fused update's shadow stores
+    (StepParamUpdate) and rebuilt from the fp32 parameters by refresh()
+    after the parameters were written otherwise. ``offsets`` maps each
+    matrix to its element offset in ``buf``."""
+
+    NAMES = ("wq", "wk", "wv", "wout", "wkt", "wvt", "wot", "ws", "wd", "wst", "wdt")
+
+    def __init__(self, dims: "ConvDims", device: torch.device):
+        D, T, H, C = dims.D, dims.T, dims.H, dims.C
+        dh = D // H
+        r8 = lambda x: _round_up(x, 8)
+        self.dims = dims
+        self.ld = {"ld_q": r8(D + T), "ld_c": r8(C), "ld_o": r8(2 * D), "hp": r8(dh), "ld_d": r8(D)}
+        self.ld["ld_h"] = H * self.ld["hp"]
+        L = self.ld
+        rows = {"wq": (D, L["ld_q"]), "wk": (D, L["ld_c"]), "wv": (D, L["ld_c"]), "wout": (D, L["ld_o"]),
+                "wkt": (C, L["ld_h"]), "wvt": (C, L["ld_h"]), "wot": (D, L["ld_d"]), "ws": (D, L["ld_d"]),
+                "wd": (D, L["ld_d"]), "wst": (D, L["ld_d"]), "wdt": (D, L["ld_d"])}
+        self.offsets, n = {}, 0
+        for name in self.NAMES:
+            self.offsets[name] = n
+            n += rows[name][0] * rows[name][1]   # ld % 8 == 0: every matrix starts 16-byte aligned
+        self.buf = torch.zeros(n, dtype=torch.int16, device=device)
+        base = self.buf.data_ptr()
+        self.struct = _capi.Bf16Weights(**{k: base + 2 * o for k, o in self.offsets.items()}, **L)
+        self.ptr = ctypes.addressof(self.struct)
+        self._refresh = None
+
+    def jobs_for(self, which: str, head: int = 0, col0: int = 0) -> dict:
+        """The shadow fields of a StepParamUpdate job over a block of a
+        shadowed parameter: ``which`` in w_q (columns from col0), w_k / w_v
+        (head ``head``'s rows), w_out (columns from col0), w_s, w_d."""
+        o, L = self.offsets, self.ld
+        dh = self.dims.D // self.dims.H
+        if which == "w_q":
+            return dict(sh_off=o["wq"] + col0, sh_ld=L["ld_q"])
+        if which in ("w_k", "w_v"):
+            s = "wk" if which == "w_k" else "wv"
+            return dict(sh_off=o[s] + head * dh * L["ld_c"], sh_ld=L["ld_c"], sht_off=o[s + "t"] + head * L["hp"],
+                        sht_ld=L["ld_h"])
+        if which == "w_out":
+            if col0 == 0:
+                return dict(sh_off=o["wout"], sh_ld=L["ld_o"], sht_off=o["wot"], sht_ld=L["ld_d"])
+            return dict(sh_off=o["wout"] + col0, sh_ld=L["ld_o"])
+        if which in ("w_s", "w_d"):
+            s = "ws" if which == "w_s" else "wd"
+            return dict(sh_off=o[s], sh_ld=L["ld_d"], sht_off=o[s + "t"], sht_ld=L["ld_d"])
+        raise ValueError(which)
+
+    def refresh(self, w_q: torch.Tensor, w_k: torch.Tensor, w_v: torch.Tensor, w_out: torch.Tensor,
+                w_s: torch.Tensor, w_d: torch.Tensor) -> None:
+        """Rebuild every copy from the fp32 parameters (sgl_grad_shadows on
+        the current stream)."""
+        key = tuple(p.data_ptr() for p in (w_q, w_k, w_v, w_out, w_s, w_d))
+        if self._refresh is None or self._refresh[0] != key:
+            d = self.dims
+            D, T, H, C = d.D, d.T, d.H, d.C
+            dh = D // H
+            base = min(key)
+            jobs, tiles = [], []
+
+            def add(p, rows, cols, ldo, elem0, sh):
+                job = _capi.GradJob(off=(p.data_ptr() - base) // 4 + elem0, ldo=ldo, rows=rows, cols=cols, kind=0,
+                                    tiles_b=(cols + 15) // 16, tile0=len(tiles), **sh)
+                tiles.extend([len(jobs)] * (((rows + 15) // 16) * job.tiles_b))
+                jobs.append(job)
+
+            add(w_q, D, D + T, D + T, 0, self.jobs_for("w_q"))
+            for h in range(H):
+                add(w_k, dh, C, C, h * dh * C, self.jobs_for("w_k", h))
+                add(w_v, dh, C, C, h * dh * C, self.jobs_for("w_v", h))
+            add(w_out, D, D, 2 * D, 0, self.jobs_for("w_out"))
+            add(w_out, D, D, 2 * D, D, self.jobs_for("w_out", col0=D))
+            add(w_s, D, D, D, 0, self.jobs_for("w_s"))
+            add(w_d, D, D, D, 0, self.jobs_for("w_d"))
+            arr = (_capi.GradJob * len(jobs))(*jobs)
+            dev = self.buf.device
+            raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(dev)
+            self._refresh = (key, raw, torch.as_tensor(tiles, dtype=torch.int32, device=dev), len(tiles), base)
+        _, raw, tiles, nt, base = self._refresh
+        _capi.check(_capi.lib().sgl_grad_shadows(raw.data_ptr(), tiles.data_ptr(), nt, base, self.buf.data_ptr(),
+                                                 _capi.stream_of(self.buf.device)), "sgl_grad_shadows")
+
+
 class DeviceStep:
     """The kernel sequence of one step over a NodeState (no host syncs)."""
 
@@ -204,9 +292,14 @@ class DeviceStep:
         # HIP events around each library call, or None
         self.timer: list | None = None
         self.timed: set[str] | None = None   # names to time (None = all)
+        # bf16 weight copies for the attention / predictor products (Bf16Shadow), or None: fp32
+        self.bf16: Bf16Shadow | None = None
 
     def _s(self) -> int:
         return _capi.stream_of(self.dev)
+
+    def _bw(self) -> int | None:
+        return self.bf16.ptr if self.bf16 is not None else None
 
     def _call(self, name: str, fn):
         t = self.timer
@@ -340,7 +433,7 @@ class DeviceStep:
                 P(b.new_mem), P(b.hop.cnt), P(b.X), P(b.hop.dt), P(w_q), P(b_q), P(w_k), P(b_k), P(w_v), P(b_v),
                 P(w_out), P(b_out), P(ln_g), P(ln_b), P(te_w), P(te_b), a(b.Q), a(b.qt), a(b.xbar), a(b.score),
                 a(b.ml), a(b.agg), a(b.z), a(b.stats), P(b.phi0), P(b.S), self._at(b.y, p, b.y_rows * d.D),
-                pa, po, seed, P(b.rng_step), p, a(b.sdrop), self._s()), "sgl_conv_forward"))
+                pa, po, seed, P(b.rng_step), p, a(b.sdrop), self._bw(), self._s()), "sgl_conv_forward"))
         return b.y
 
     def predictor(self, n: int, train: bool, pred: list[torch.Tensor], out_grads: list[torch.Tensor] | None,
@@ -361,7 +454,7 @@ class DeviceStep:
             "sgl_predictor", n, self.dims.D, b.cap, 1 if train else 0, P(b.num_roots), P(b.y), P(b.ridx_src),
             P(b.ridx_dst), P(b.ridx_neg), P(pred[0]), P(pred[1]), P(pred[2]), P(pred[3]), P(pred[4]), P(pred[5]),
             P(b.pos), P(b.neg), P(b.loss), P(b.acc_src) if train else None, P(b.acc_dst) if train else None,
-            P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), ys, acc_neg, self._s()), "sgl_predictor"))
+            P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), ys, acc_neg, self._bw(), self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
     def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor,
@@ -396,7 +489,7 @@ class DeviceStep:
                 P(b_out), P(ln_g), P(ln_b), P(te_b), a(b.Q), a(b.qt), a(b.xbar), a(b.score), a(b.ml), a(b.agg),
                 a(b.z), a(b.stats), P(gy), P(acc_a), P(acc_b), P(w_a), P(w_b), P(g_a), P(g_b), a(b.gz), a(b.gagg),
                 a(b.G), a(b.sigma), a(b.gQ), a(b.ln_part), a(b.te_part), pa, po, seed, P(b.rng_step), p,
-                a(b.sdrop), self._s()), "sgl_conv_backward"))
+                a(b.sdrop), self._bw(), self._s()), "sgl_conv_backward"))
 
     def conv_backward(self, params: list[torch.Tensor], efeat_all: torch.Tensor, gy: torch.Tensor, drop=None):
         """The backward kernel plus the weight gradients as torch products (the
@@ -447,11 +540,13 @@ class StepParamUpdate:
     update still reads its own. ``passes`` 3 (dropout): every attention
     gradient sums the three passes' rows, dst_fc's the dst and negative
     passes'; ``counter`` (device int64): the training-step counter the
-    advance increments and copies to the buffers' dropout step."""
+    advance increments and copies to the buffers' dropout step; ``shadow``
+    (Bf16Shadow): the update also stores the bf16 copies of the weights it
+    holds."""
 
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
                  pred_params: list[torch.Tensor], gates: list[torch.Tensor | None], passes: int = 1,
-                 counter: torch.Tensor | None = None, kind: str = "attention"):
+                 counter: torch.Tensor | None = None, kind: str = "attention", shadow: Bf16Shadow | None = None):
         if len(opt.segments) != 2:
             raise ValueError("StepParamUpdate expects the attention and predictor segments")
         if passes not in (1, step.buf.passes):
@@ -462,6 +557,9 @@ class StepParamUpdate:
         if kind not in ("attention", "projection"):
             raise ValueError(f"StepParamUpdate: unknown kind {kind!r}")
         self.kind = kind
+        if shadow is not None and (kind != "attention" or self.passes != 1):
+            raise ValueError("StepParamUpdate: bf16 weight copies need the attention without dropout passes")
+        self.shadow = shadow
         self.lib = _capi.lib()
         dev = opt.flat.device
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
@@ -502,18 +600,24 @@ class StepParamUpdate:
         P = self.passes
         c = b.cap
 
-        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0, npass=1, ps1=0, ps2=0):
+        sh = self.shadow
+
+        def shf(*a, **k):   # a job's bf16-copy fields (none without a shadow)
+            return sh.jobs_for(*a, **k) if sh is not None else {}
+
+        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0, npass=1, ps1=0, ps2=0, shd=None):
             assert s1 >= rows
             tb = (cols + 15) // 16
             add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ps1=ps1, ps2=ps2, ldo=ldo, rows=rows, cols=cols,
-                              kind=0, seg=seg, r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb, npass=npass),
+                              kind=0, seg=seg, r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb, npass=npass,
+                              **(shd or {})),
                 ((rows + 15) // 16) * tb)
 
         # the attention's reductions run over every pass's rows (rows of
         # width w: pass stride c * w; the per-tile partials: ntiles * w)
-        def conv(x1, s1, x2, s2, o, ldo, rows, cols, x1w=None, x2w=None, r_fixed=-1):
+        def conv(x1, s1, x2, s2, o, ldo, rows, cols, x1w=None, x2w=None, r_fixed=-1, shd=None):
             gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=r_fixed, npass=P,
-                 ps1=0 if x1w is None else x1w, ps2=0 if x2w is None else x2w)
+                 ps1=0 if x1w is None else x1w, ps2=0 if x2w is None else x2w, shd=shd)
 
         one = at(self.one)
         if self.kind == "projection":
@@ -528,22 +632,22 @@ class StepParamUpdate:
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
         conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
         conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
-        conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D)
-        conv(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T, x1w=c * D)
+        conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D, shd=shf("w_q"))
+        conv(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T, x1w=c * D, shd=shf("w_q", col0=D))
         conv(at(b.gQ), D, one, 0, off(b_q), 1, D, 1, x1w=c * D)
         for h in range(H):
             conv(at(b.Q, h * dh), D, at(b.G, h * C), H * C, off(w_k) + h * dh * C, C, dh, C, x1w=c * D,
-                 x2w=c * H * C)
+                 x2w=c * H * C, shd=shf("w_k", h))
             conv(at(b.Q, h * dh), D, at(b.sigma, h), H, off(b_k) + h * dh, 1, dh, 1, x1w=c * D, x2w=c * H)
             conv(at(b.gagg, h * dh), D, at(b.xbar, h * C), H * C, off(w_v) + h * dh * C, C, dh, C, x1w=c * D,
-                 x2w=c * H * C)
+                 x2w=c * H * C, shd=shf("w_v", h))
         if P > 1:   # attention dropout: agg_h = W_v xbar'_h + s_h b_v[h]
             for h in range(H):
                 conv(at(b.gagg, h * dh), D, at(b.sdrop, h), H, off(b_v) + h * dh, 1, dh, 1, x1w=c * D, x2w=c * H)
         else:
             conv(at(b.gagg), D, one, 0, off(b_v), 1, D, 1, x1w=c * D)
-        conv(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D, x1w=c * D, x2w=c * D)
-        conv(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D, x1w=c * D)
+        conv(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D, x1w=c * D, x2w=c * D, shd=shf("w_out"))
+        conv(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D, x1w=c * D, shd=shf("w_out", col0=D))
         conv(at(b.gz), D, one, 0, off(b_out), 1, D, 1, x1w=c * D)
         conv(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
         conv(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
@@ -551,19 +655,19 @@ class StepParamUpdate:
         # of g_dst holds the non-root negatives; y's row U is zero); out_fc's
         # gradients come from sgl_predictor (Adam only). With dropout dst_fc
         # sums the dst pass's rows and the negatives' pass's rows
-        self._pred_jobs(gemm, add, at, off, one, pred_params, P)
+        self._pred_jobs(gemm, add, at, off, one, pred_params, P, shf)
         return self._check(jobs, tiles, conv_params, pred_params)
 
-    def _pred_jobs(self, gemm, add, at, off, one, pred_params, P):
+    def _pred_jobs(self, gemm, add, at, off, one, pred_params, P, shf=lambda *a, **k: {}):
         b, D = self.step.buf, self.step.dims.D
         c = b.cap
         w_s, b_s, w_d, b_d, w_o, b_o = pred_params
         nd = 2 if P > 1 else 1
         gs, ys = (c + 1) * D, b.y_rows * D
         yd = at(b.y, ys) if P > 1 else at(b.y)
-        gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, seg=1, r_extra=1)
+        gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, seg=1, r_extra=1, shd=shf("w_s"))
         gemm(at(b.g_src), D, one, 0, off(b_s), 1, D, 1, seg=1, r_extra=1)
-        gemm(at(b.g_dst), D, yd, D, off(w_d), D, D, D, seg=1, r_extra=1, npass=nd, ps1=gs, ps2=ys)
+        gemm(at(b.g_dst), D, yd, D, off(w_d), D, D, D, seg=1, r_extra=1, npass=nd, ps1=gs, ps2=ys, shd=shf("w_d"))
         gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, seg=1, r_extra=1, npass=nd, ps1=gs)
         if off(b_o) != off(w_o) + D:
             raise RuntimeError("StepParamUpdate: out_fc weight and bias are not contiguous in the flat buffer")
@@ -594,7 +698,8 @@ class StepParamUpdate:
         self.step._call("param_update", lambda: _capi.check(_capi.call(
             "sgl_grad_adam", P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots),
             P(opt.flat), P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._gates,
-            P(self.coef), b1, b2, opt.eps, opt.wd, s), "sgl_grad_adam"))
+            P(self.coef), b1, b2, opt.eps, opt.wd, P(self.shadow.buf) if self.shadow is not None else None, s),
+            "sgl_grad_adam"))
 
 
 class ConvFunction(torch.autograd.Function):

@@ -14,6 +14,12 @@ GOLDEN = os.path.join(REPO, "tests", "golden")
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP C-ABI library)")
+    # the CPU oracle on one thread: torch's multithreaded fp32 CPU kernels
+    # round differently from process to process, and the teacher-forced tests
+    # follow the oracle's own parameter trajectory, so its steps must be
+    # reproducible for the comparisons to be
+    import torch
+    torch.set_num_threads(1)
 
 
 @pytest.fixture(scope="session")

@@ -87,6 +87,25 @@ def test_grad_job_struct_layout_matches_header(tmp_path):
     assert got == want
 
 
+def test_bf16_weights_struct_layout_matches_header(tmp_path):
+    """ctypes' Bf16Weights has the size and field offsets of struct
+    sgl_bf16_weights."""
+    import ctypes
+    from starry_unigraph.lib import _capi
+    fields = [f for f, _ in _capi.Bf16Weights._fields_]
+    src = tmp_path / "layout.cpp"
+    src.write_text(
+        '#include <cstdio>\n#include <cstddef>\n#include "starrygl_mi355x.h"\nint main() {\n'
+        '  printf("%zu", sizeof(sgl_bf16_weights));\n'
+        + "".join(f'  printf(" %zu", offsetof(sgl_bf16_weights, {f}));\n' for f in fields) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                    "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(_capi.Bf16Weights)] + [getattr(_capi.Bf16Weights, f).offset for f in fields]
+    assert got == want
+
+
 def test_plan_op_struct_layout_matches_header(tmp_path):
     """ctypes' Op has the size and field offsets of struct sgl_op."""
     import ctypes

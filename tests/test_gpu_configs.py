@@ -12,7 +12,10 @@ learnable time encoding would decorrelate are compared step by step):
   cfg5  unipartite Zipf(1.5) stream (30,000 nodes, 160,000 events), D = 172,
         T = 100, F = 16, H = 4, k = 20 for 2 hops, K = 4, B = 4000
 
-each with the fp32 GRU and with bf16 GRU GEMMs. Tolerances: loss, logits
+each with the fp32 GRU and with bf16 GRU GEMMs, and (the attention
+configurations) with every GEMM in bf16 ("bf16all": the GRU and the
+attention and edge-predictor products on bf16 weight copies, BASELINE
+configs 4 and 5's precision). Tolerances: loss, logits
 and memory within rtol 1e-3 of the oracle; gradients within rtol 2e-3
 (atol 1e-3 of the largest entry) of the same step evaluated in float64
 (time-encoding arguments rounded as in float32); with bf16 GEMMs in the
@@ -20,8 +23,22 @@ GRU its memory update is held to
 rtol / atol 2e-2 against the fp32 oracle's, and the oracle's attention,
 predictor and backward are then run from the GPU's updated memory and held
 to the fp32 tolerances above.
+With bf16all the loss and logits are held to rtol 2e-2 (north_star's bf16
+tolerance) against the same fp32 oracle. Each gradient is held to the band
+that bf16 itself opens: the float64 gradient is evaluated a second time with
+the six weight matrices the bf16 path copies rounded to bf16, and the GPU's
+gradient must lie within 5x that distance plus 3 % of the gradient's norm
+(Frobenius norms) of the float64 one: the kernels also round every
+product's activation operand, which the band does not model (measured: the
+error is 0.3-7x the band, the largest for the key bias, where the rounded
+g_xbar and query enter a nearly cancelling sum). Several of these gradients are sums
+of nearly cancelling terms (the key bias's gradient vanishes but for the
+LeakyReLU slopes, as the softmax ignores a shift of a root's scores; the
+predictor's pos / neg terms cancel for untrained weights), so their bf16
+error ranges from 1 % to tens of per cent with the parameters, and one fixed
+bound would not measure the kernels.
 Mailbox contents, mailbox timestamps, slot pointers and memory timestamps
-are bit-exact in both (messages carry the memory from before the update).
+are bit-exact in every mode (messages carry the memory from before the update).
 Also: the eval step against the oracle's no-grad step, the product's own
 negative draws against the oracle's under the same seed, the sample
 statistics of every hop against the oracle sampler, and the path without a
@@ -76,7 +93,9 @@ def _pair(name, gemm="fp32", seed=0, updater=True):
     cfg = {"model": {"family": c["family"], "hidden_dim": c["D"]}, "data": {"name": f"p_{name}", "format": "synthetic"},
            "train": {"batch_size": c["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
            "ctdg": {"mailbox_slots": c["K"], "dim_time": c["T"], "num_head": c["H"], "dropout": 0.0,
-                    "att_dropout": 0.0, "memory_gemm_dtype": gemm, "embedding": c.get("embedding", "attention")},
+                    "att_dropout": 0.0, "memory_gemm_dtype": "fp32" if gemm == "fp32" else "bf16",
+                    "attention_gemm_dtype": "bf16" if gemm == "bf16all" else "fp32",
+                    "embedding": c.get("embedding", "attention")},
            "sampling": {"neighbor_limit": [c["k"]] * c["history"], "history": c["history"], "strategy": "recent"}}
     torch.manual_seed(seed)
     sess = SchedulerSession.from_config(cfg).with_events(from_stream(s))
@@ -122,6 +141,7 @@ def _teacher_force(rt, model, mem):
     st.memory_ts.copy_(mem.memory_ts)
     st.next_mail_pos.copy_(mem.next_mail_pos.to(torch.int32))
     st.touched()
+    rt.params_changed()   # parameters written outside the optimizer: rebuild the bf16 weight copies
 
 
 def _close(got, want, rtol, atol, msg):
@@ -148,8 +168,8 @@ def _run_steps(name, gemm, train=True, updater=True):
     picks = c["batches"] if train else (len(batches) // 2,)
     pool = rt.dataset.dst.unique()
     gen = torch.Generator().manual_seed(5)
-    bf16 = gemm == "bf16"
-    tol = 1e-3
+    bf16 = gemm != "fp32"
+    tol = 2e-2 if gemm == "bf16all" else 1e-3
     for i in picks:
         batch = batches[i]
         msg = f"{name} {gemm} {split} batch {i}"
@@ -170,6 +190,13 @@ def _run_steps(name, gemm, train=True, updater=True):
             gpu_mem = st.memory.cpu()
             hook = lambda m: m.memory.copy_(gpu_mem)
         model64 = copy.deepcopy(model).double() if train else None
+        model64b = None
+        if train and gemm == "bf16all":   # the same step with the bf16-copied weights rounded
+            model64b = copy.deepcopy(model64)
+            with torch.no_grad():
+                for lin in (model64b.conv.w_q, model64b.conv.w_k, model64b.conv.w_v, model64b.conv.w_out,
+                            model64b.src_fc, model64b.dst_fc):
+                    lin.weight.copy_(lin.weight.to(torch.bfloat16).double())
         mts_prev = mem.memory_ts.clone()
         ref = co.train_step(model, upd, opt, mem, lambda r, t: co.block_from_oracle_sampler(og, r, t, fan),
                             batch.src, batch.dst, batch.ts, batch.edge_feat, neg, rt.dataset.edge_feat, train=train,
@@ -196,8 +223,19 @@ def _run_steps(name, gemm, train=True, updater=True):
             # time-encoding weight's gradient sums terms ~ sin(w dt) dt with dt
             # up to 1e8 that largely cancel, so its float32 value depends on
             # the order of the sum and only a float64 sum is a fixed yardstick
-            for g64, (pn, p) in zip(_grads64(model64, mem, ref, batch, neg, rt.dataset.edge_feat, mts_prev),
-                                    rt.model.named_parameters()):
+            pairs = list(zip(_grads64(model64, mem, ref, batch, neg, rt.dataset.edge_feat, mts_prev),
+                             rt.model.named_parameters()))
+            bands = (_grads64(model64b, mem, ref, batch, neg, rt.dataset.edge_feat, mts_prev)
+                     if model64b is not None else [None] * len(pairs))
+            for (g64, (pn, p)), gb in zip(pairs, bands):
+                if gb is not None:
+                    err = float((p.grad.cpu().double() - g64).norm())
+                    band = float((gb - g64).norm())
+                    norm = float(g64.norm())
+                    print(f"  grad {pn}: error {err / (norm + 1e-30):.2e}, bf16 band {band / (norm + 1e-30):.2e} "
+                          f"(relative to the norm)", flush=True)
+                    assert err <= 5 * band + 3e-2 * norm, (msg, pn, err, band, norm)
+                    continue
                 scale = float(g64.abs().max()) + 1e-12
                 _close(p.grad, g64, 2e-3, 1e-3 * scale, f"grad {pn} {msg}")
     return rt
@@ -226,6 +264,61 @@ def _grads64(model64, mem, ref, batch, neg, edge_feat_all, mts_prev):
 @pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg2p", "cfg4", "cfg5"])
 def test_train_steps_match_oracle_at_config_dims(gpu, name, gemm):
     _run_steps(name, gemm)
+
+
+@pytest.mark.parametrize("name", ["cfg1", "cfg4", "cfg5"])
+def test_bf16_steps_match_oracle_at_config_dims(gpu, name):
+    _run_steps(name, "bf16all")
+
+
+@pytest.mark.parametrize("name", ["cfg4", "cfg5"])
+def test_bf16_eval_step_matches_oracle(gpu, name):
+    _run_steps(name, "bf16all", train=False)
+
+
+def _bf16_bits(x: torch.Tensor) -> torch.Tensor:
+    return x.detach().float().cpu().to(torch.bfloat16).view(torch.int16)
+
+
+def test_bf16_weight_copies_track_parameters(gpu):
+    """After planned bf16 training steps (the fused update stores the
+    copies), every bf16 weight copy equals its parameter rounded to bf16
+    (nearest even), transposes and head padding included, bit for bit; the
+    padding stays zero."""
+    c, rt, *_ = _pair("cfg4", "bf16all")
+    rt.collect_results = False
+    for batch in list(rt.iter_batches("train", c["B"]))[:6]:
+        rt.train_step(batch)
+    rt.fence()
+    torch.cuda.synchronize()
+    sh = rt._bf16
+    assert sh is not None
+    core = rt.model
+    conv = core.conv
+    D, T, H, C = rt.dims.D, rt.dims.T, rt.dims.H, rt.dims.C
+    dh, L, o = D // H, sh.ld, sh.offsets
+    buf = sh.buf.cpu()
+
+    def mat(name, rows, ld):
+        return buf[o[name]:o[name] + rows * ld].view(rows, ld)
+
+    def expect(name, rows, ld, blocks):
+        want = torch.zeros(rows, ld, dtype=torch.int16)
+        for r0, c0, m in blocks:
+            want[r0:r0 + m.shape[0], c0:c0 + m.shape[1]] = _bf16_bits(m)
+        assert torch.equal(mat(name, rows, ld), want), name
+
+    wk, wv, wout = conv.w_k.weight, conv.w_v.weight, conv.w_out.weight
+    expect("wq", D, L["ld_q"], [(0, 0, conv.w_q.weight)])
+    expect("wk", D, L["ld_c"], [(0, 0, wk)])
+    expect("wv", D, L["ld_c"], [(0, 0, wv)])
+    expect("wout", D, L["ld_o"], [(0, 0, wout)])
+    expect("wkt", C, L["ld_h"], [(0, h * L["hp"], wk[h * dh:(h + 1) * dh].t()) for h in range(H)])
+    expect("wvt", C, L["ld_h"], [(0, h * L["hp"], wv[h * dh:(h + 1) * dh].t()) for h in range(H)])
+    expect("wot", D, L["ld_d"], [(0, 0, wout[:, :D].t())])
+    for s, w in (("ws", core.src_fc.weight), ("wd", core.dst_fc.weight)):
+        expect(s, D, L["ld_d"], [(0, 0, w)])
+        expect(s + "t", D, L["ld_d"], [(0, 0, w.t())])
 
 
 @pytest.mark.parametrize("name", ["cfg2p", "cfg4", "cfg5"])

@@ -293,10 +293,23 @@ def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
 # are the shapes of the benchmark configurations. With k=120 and T=96 the
 # 16-wave forward's time encodings (4 roots x 120 edges x 96) do not fit in
 # LDS: its edge loop reads them from the rows the other waves wrote.
-@pytest.mark.parametrize("H,k,seed,D,F,T", [(2, 10, 0, 32, 6, 16), (4, 20, 1, 32, 6, 16), (1, 3, 2, 32, 6, 16),
-                                            (2, 10, 3, 100, 16, 100), (2, 10, 4, 100, 172, 100),
-                                            (2, 120, 5, 32, 6, 96)])
-def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T):
+@pytest.mark.parametrize("H,k,seed,D,F,T,bf16", [(2, 10, 0, 32, 6, 16, False), (4, 20, 1, 32, 6, 16, False),
+                                                 (1, 3, 2, 32, 6, 16, False), (2, 10, 3, 100, 16, 100, False),
+                                                 (2, 10, 4, 100, 172, 100, False), (2, 120, 5, 32, 6, 96, False),
+                                                 (2, 10, 3, 100, 16, 100, True), (4, 20, 6, 172, 16, 100, True),
+                                                 (2, 7, 7, 36, 6, 20, True)])
+def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T, bf16):
+    """fp32: embedding within atol 2e-4, gradients rtol 2e-3. bf16 (the
+    products on bf16 weight copies, Bf16Shadow; D = 36, H = 2: heads of 18
+    rows, so the head blocks of the transposed copies are padded): the
+    embedding within north_star's bf16 tolerance 2e-2 of its scale (max
+    error <= 2e-2 max|y|, relative Frobenius error <= 2e-2; measured 0.3-0.5 %
+    and 3e-3), each gradient within a relative Frobenius error of 1e-1
+    (measured 0.3-6 %), the time-encoding weight's within 1.5e-1 (measured
+    2.5-12 %): the softmax backward (t - sum alpha t) and the dt-weighted
+    time-encoding sums cancel, which amplifies bf16's ~0.3 % operand
+    rounding; a wrong weight copy (a transpose, a head block) gives errors
+    near 100 %."""
     from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
     from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
@@ -324,6 +337,12 @@ def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T):
     step.sample(RecentSampler(g))
     b.any_edges.fill_(int(int(b.hop.cnt[:R].sum().item()) > 0))
     efd = ef.to(gpu)
+    if bf16:
+        from starry_unigraph.native.step import Bf16Shadow
+        sh = Bf16Shadow(step.dims, gpu)
+        pred_w = [torch.randn(D, D, device=gpu) for _ in range(2)]   # src_fc / dst_fc copies (unused with gy)
+        sh.refresh(conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight, *pred_w)
+        step.bf16 = sh
     y = conv(step, efd)
     gy = torch.randn(R, D)
     loss = (y[:R] * gy.to(gpu)).sum()
@@ -333,8 +352,21 @@ def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T):
     blk = co.block_from_oracle_sampler(og, torch.as_tensor(roots), torch.as_tensor(tq), k)
     yr = co.conv_all(_Wrap(ref), mem, torch.as_tensor(roots), blk, ef)
     (yr * gy).sum().backward()
-    _close(y[:R], yr, atol=2e-4, msg="embedding")
     assert torch.count_nonzero(y[R:]) == 0
+    if bf16:
+        d = y[:R].detach().cpu().double() - yr.detach().double()
+        yn = yr.detach().double()
+        print(f"bf16 embedding: max abs err {float(d.abs().max()):.3e} (max |y| {float(yn.abs().max()):.3f}), "
+              f"relative Frobenius {float(d.norm() / yn.norm()):.3e}, "
+              f"elements beyond 2e-2 (rtol+atol): {int(((d.abs() > 2e-2 + 2e-2 * yn.abs())).sum())} / {d.numel()}",
+              flush=True)
+        assert float(d.abs().max()) <= 2e-2 * float(yn.abs().max()) and float(d.norm() / yn.norm()) <= 2e-2
+        for (name, p), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
+            err = float((p.grad.cpu().double() - pr.grad.double()).norm()) / (float(pr.grad.double().norm()) + 1e-30)
+            print(f"  grad {name}: relative Frobenius error {err:.3e}", flush=True)
+            assert err <= (1.5e-1 if name == "time_enc.w.weight" else 1e-1), (name, err)
+        return
+    _close(y[:R], yr, atol=2e-4, msg="embedding")
     for (name, p), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
         scale = float(pr.grad.abs().max()) + 1e-6
         _close(p.grad, pr.grad, rtol=2e-3, atol=2e-4 * scale, msg=f"grad {name}")
