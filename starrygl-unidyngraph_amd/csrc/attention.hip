@@ -260,6 +260,7 @@ struct FwdLds {
   float *QT;    // [16][ldq]  qt, then xbar
   float *qb;    // [16][H]
   float *TW, *TB;  // [T] time-encoding weight / bias
+  float *BK, *LG, *LB;  // [D] key bias, LayerNorm weight and bias (staged with the first loads)
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][3] a slice's running max, sum and kept sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
@@ -280,7 +281,10 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.qb = L.QT + kRows * L.ldq;
   L.TW = L.qb + kRows * d.H;
   L.TB = L.TW + d.T;
-  L.part = L.TB + d.T;
+  L.BK = L.TB + d.T;
+  L.LG = L.BK + d.D;
+  L.LB = L.LG + d.D;
+  L.part = L.LB + d.D;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   L.scr = L.pml + (slices ? ((nw * d.H * 3 + 3) & ~3) : 0);
   L.Ts = L.scr + (rows_for(nw) == 4 ? nw * 256 : 0);
@@ -343,6 +347,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     L.TW[t] = p.te_w[t];
     L.TB[t] = p.te_b[t];
   }
+  // the small parameter vectors of later phases, staged now so that no later
+  // phase waits on a global load for them
+  for (int j = tid; j < D; j += kBlock) {
+    L.BK[j] = p.b_k[j];
+    L.LG[j] = p.ln_g[j];
+    L.LB[j] = p.ln_b[j];
+  }
   // HT = [h | cos(b)] (TimeEncode(0) = cos(0*w + b)); AH[:, D:] = h
   for (int idx = tid; idx < kRows * (D + T); idx += kBlock) {
     const int i = idx / (D + T), j = idx - i * (D + T);
@@ -392,11 +403,13 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     const int i = idx / D, j = idx - i * D;
     sv.Q[size_t(r0 + i) * D + j] = i < nrows ? L.Qs[i * L.ldr + j] : 0.f;
   }
-  if (tid < kRows * H) {
-    const int i = tid / H, h = tid - (tid / H) * H;
+  // qb[i][h] = <Q_ih, b_k,h> for the live rows: one wave per (row, head)
+  for (int pr = wave; pr < RPW * H; pr += kWaves) {
+    const int i = pr / H, h = pr - (pr / H) * H;
     float acc = 0.f;
-    for (int j = 0; j < dh; ++j) acc += L.Qs[i * L.ldr + h * dh + j] * p.b_k[h * dh + j];
-    L.qb[i * H + h] = acc;
+    for (int j = lane; j < dh; j += 64) acc += L.Qs[i * L.ldr + h * dh + j] * L.BK[h * dh + j];
+    acc = wave_sum(acc);
+    if (lane == 0) L.qb[i * H + h] = acc;
   }
   // qt_h = Q_h W_k[h rows, :]  (kNN: rows of W_k are the reduction index;
   // the bf16 products read W_k^T)
@@ -672,7 +685,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     const float rstd = 1.f / sqrtf(wave_sum(s2) / D + 1e-5f);
     for (int j = lane; j < D; j += 64) {
       const float xh = (fmaxf(L.Zs[i * L.ldr + j], 0.f) - mean) * rstd;
-      y[ro + j] = i < nrows ? xh * p.ln_g[j] + p.ln_b[j] : 0.f;
+      y[ro + j] = i < nrows ? xh * L.LG[j] + L.LB[j] : 0.f;
     }
     if (lane == 0) {
       sv.stats[size_t(r0 + i) * 2 + 0] = i < nrows ? mean : 0.f;
@@ -697,6 +710,7 @@ struct BwdLds {
   float *GX;                      // [16][ldq]  g_xbar, then G
   float *tep;                     // [waves][2][T]
   float *TB;                      // [T] time-encoding bias
+  float *LG, *BK;                 // [D] LayerNorm weight, key bias (staged with the first loads)
   float *part;                    // [NW][H*C]  a slice's G partial (slices only)
   float *psig;                    // [NW][H]    a slice's sigma partial (slices only)
   float *scr;                     // [NW][4][64] four-row product partials (4-root tiles only)
@@ -714,7 +728,9 @@ __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bo
   L.GX = L.GY + kRows * L.ldr;
   L.tep = L.GX + kRows * L.ldq;
   L.TB = L.tep + nw * 2 * d.T;
-  L.part = L.TB + d.T;
+  L.LG = L.TB + d.T;
+  L.BK = L.LG + d.D;
+  L.part = L.BK + d.D;
   L.psig = L.part + (slices ? nw * d.H * d.C : 0);
   // 16-byte aligned for the product partials
   L.scr = L.psig + (((slices ? nw * d.H : 0) + 3) & ~3);
@@ -794,6 +810,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
   if (tid < kRows) s_cnt[tid] = tid < nrows ? cnt[r0 + tid] : 0;
   for (int t = tid; t < T; t += kBlock) L.TB[t] = p.te_b[t];
+  for (int j = tid; j < D; j += kBlock) {
+    L.LG[j] = p.ln_g[j];
+    L.BK[j] = p.b_k[j];
+  }
   // dL/dy of the tile: given, or W_s^T g_src + W_d^T g_dst from the edge
   // predictor's per-root rows (GA / GQ are free until later phases)
   // (the two products land in GY and XH in parallel; the LayerNorm pass
@@ -852,7 +872,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       for (int j = lane; j < D; j += 64) {
         const float zz = sv.z[ro + j], gv = L.GY[i * L.ldr + j] + L.XH[i * L.ldr + j];
         const float xh = (fmaxf(zz, 0.f) - mean) * rstd;
-        const float gxh = gv * p.ln_g[j];
+        const float gxh = gv * L.LG[j];
         L.GY[i * L.ldr + j] = gv;
         L.XH[i * L.ldr + j] = xh;
         L.GZ[i * L.ldr + j] = zz;
@@ -864,7 +884,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
       for (int j = lane; j < D; j += 64) {
         const float zz = L.GZ[i * L.ldr + j];
         const float xh = L.XH[i * L.ldr + j];
-        const float gx = rstd * (L.GY[i * L.ldr + j] * p.ln_g[j] - a1 - xh * a2);
+        const float gx = rstd * (L.GY[i * L.ldr + j] * L.LG[j] - a1 - xh * a2);
         float gzv = zz > 0.f ? gx : 0.f;
         if (DROP && dc.p_out > 0.f)  // through the output mask (z was saved masked)
           gzv *= sgl::drop_keep(sgl::drop_bits(dc, dstep, uint32_t(r0 + i), uint32_t(j >> 2), 1).v[j & 3],
@@ -1131,7 +1151,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   for (int idx = tid; idx < RPW * D; idx += kBlock) {
     const int i = idx / D, j = idx - i * D;
     const int h = j / dh;
-    const float v = i < nrows ? L.GQ[i * L.ldr + j] + p.b_k[j] * s_sig[i][h] : 0.f;
+    const float v = i < nrows ? L.GQ[i * L.ldr + j] + L.BK[j] * s_sig[i][h] : 0.f;
     L.GQ[i * L.ldr + j] = v;
     g.gQ[size_t(r0 + i) * D + j] = v;
   }
@@ -1147,13 +1167,32 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   // the query's cos(b) term of the time-encoding bias gradient,
   // -sin(b_t) * sum_j W_q[j][D+t] * colsum[j]: the j range split over the
   // waves, partial sums in GX (free by now), added in wave order
+  // (the weights of a batch of kQJ rows and two t columns are loaded
+  // together: one memory round trip per batch)
   {
+    constexpr int kQJ = 12;
     const int per = (D + kWaves - 1) / kWaves;
     const int j0 = wave * per, j1 = min(D, j0 + per);
-    for (int t = lane; t < T; t += 64) {
-      float acc = 0.f;
-      for (int j = j0; j < j1; ++j) acc += p.w_q[size_t(j) * (D + T) + D + t] * L.GA[j];
-      L.GX[wave * T + t] = acc;
+    for (int t0 = lane; t0 < T; t0 += 128) {
+      const int t1 = t0 + 64;
+      float acc0 = 0.f, acc1 = 0.f;
+      for (int jb = j0; jb < j1; jb += kQJ) {
+        float w0[kQJ], w1[kQJ];
+#pragma unroll
+        for (int u = 0; u < kQJ; ++u) {
+          const size_t row = size_t(min(jb + u, j1 - 1)) * (D + T) + D;
+          w0[u] = p.w_q[row + t0];
+          w1[u] = t1 < T ? p.w_q[row + t1] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kQJ; ++u) {
+          if (jb + u >= j1) break;
+          acc0 += w0[u] * L.GA[jb + u];
+          acc1 += w1[u] * L.GA[jb + u];
+        }
+      }
+      L.GX[wave * T + t0] = acc0;
+      if (t1 < T) L.GX[wave * T + t1] = acc1;
     }
   }
   __syncthreads();

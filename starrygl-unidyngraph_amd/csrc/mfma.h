@@ -531,17 +531,24 @@ __device__ __forceinline__ f32x4 mfma_block16_bw_cls(const float *__restrict__ A
 
 // One 16x16 output block (rows 0..15 of A, columns n0..n0+15 of W^T); this
 // lane's accumulators are rows 4*(lane/16)+v, column n0 + lane%16. Columns
-// past n_total read row n_total-1 (their outputs are discarded).
+// past n_total read row n_total-1 (their outputs are discarded). CLS >= 0
+// fixes the A read width for tiles known to be aligned (less code); -1
+// picks it from A and lda.
+template <int CLS = -1>
 __device__ __forceinline__ f32x4 mfma_block16_bw(const float *__restrict__ A, int lda, const uint16_t *__restrict__ W,
                                                  int ldw, int n0, int kd, int n_total) {
   const int lane = threadIdx.x & 63;
   const int n = min(n0 + (lane & 15), n_total - 1);
   const __amdgpu_buffer_rsrc_t wr = bf16_weight_rsrc(W, uint32_t(n_total) * uint32_t(ldw));
   const uint32_t wrow = uint32_t(n) * uint32_t(ldw) + 8u * uint32_t(lane >> 4);
-  const uintptr_t ab = reinterpret_cast<uintptr_t>(A);
-  if ((ab & 15) == 0 && (lda & 3) == 0) return mfma_block16_bw_cls<2>(A, lda, wr, wrow, kd);
-  if ((ab & 7) == 0 && (lda & 1) == 0) return mfma_block16_bw_cls<1>(A, lda, wr, wrow, kd);
-  return mfma_block16_bw_cls<0>(A, lda, wr, wrow, kd);
+  if constexpr (CLS >= 0) {
+    return mfma_block16_bw_cls<CLS>(A, lda, wr, wrow, kd);
+  } else {
+    const uintptr_t ab = reinterpret_cast<uintptr_t>(A);
+    if ((ab & 15) == 0 && (lda & 3) == 0) return mfma_block16_bw_cls<2>(A, lda, wr, wrow, kd);
+    if ((ab & 7) == 0 && (lda & 1) == 0) return mfma_block16_bw_cls<1>(A, lda, wr, wrow, kd);
+    return mfma_block16_bw_cls<0>(A, lda, wr, wrow, kd);
+  }
 }
 
 // OUT (LDS, 16 x n_total) = A * W^T + bias for every job, the 16-column

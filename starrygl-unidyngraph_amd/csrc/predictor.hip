@@ -82,10 +82,11 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   // in the src list (16) and the dst list (32: (i, dst), (i, neg) of event i)
   long long *Gs = reinterpret_cast<long long *>(Wo + ((D + 3) & ~3));
   long long *Gd = Gs + kRows * D;
-  __shared__ float s_gp[kRows], s_gn[kRows], s_sp[kRows];
+  __shared__ float s_gp[kRows], s_gn[kRows], s_sp[kRows], s_pp[kRows], s_pn[kRows];
   __shared__ int s_idx[3][kRows];
   __shared__ int s_lead[3 * kRows];  // leader entry of src entry i, dst entries 2i / 2i+1
   __shared__ int s_last;
+  __shared__ float s_bo;  // out_fc bias, staged with the first loads
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t e0 = int64_t(blockIdx.x) * kRows;
@@ -100,25 +101,27 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     Nul[j] = 0;
     Wo[j] = w_o[j];
   }
+  if (tid == kRows) s_bo = b_o[0];
   if (agg && train)
     for (int k = tid; k < 3 * kRows * D; k += kBlock) Gs[k] = 0;
   __syncthreads();
   if (agg && train && tid < 3 * kRows) {
-    // the first entry of the same list with the same root (-1: no root)
+    // the first entry of the same list with the same root (-1: no root);
+    // unrolled over the whole list, so its LDS reads issue together
     if (tid < kRows) {
       const int a = s_idx[0][tid];
       int l = -1;
-      if (a >= 0)
-        for (int t = tid; t >= 0; --t)
-          if (s_idx[0][t] == a) l = t;
+#pragma unroll
+      for (int t = kRows - 1; t >= 0; --t)
+        if (t <= tid && a >= 0 && s_idx[0][t] == a) l = t;
       s_lead[tid] = l;
     } else {
       const int e = tid - kRows;
       const int r = s_idx[1 + (e & 1)][e >> 1];
       int l = -1;
-      if (r >= 0)
-        for (int t = e; t >= 0; --t)
-          if (s_idx[1 + (t & 1)][t >> 1] == r && (!sep || ((t ^ e) & 1) == 0)) l = t;
+#pragma unroll
+      for (int t = 2 * kRows - 1; t >= 0; --t)
+        if (t <= e && r >= 0 && s_idx[1 + (t & 1)][t >> 1] == r && (!sep || ((t ^ e) & 1) == 0)) l = t;
       s_lead[tid] = l;
     }
   }
@@ -139,7 +142,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       // the bias is loaded before the block's k loop (one round trip less)
       const float bv = col < D ? (u < nblk ? b_s[col] : b_d[col]) : 0.f;
       if (u < nblk) {
-        const sgl::f32x4 acc = BF ? sgl::mfma_block16_bw(Es, ld, bw.ws, bw.ld_d, n0, D, D)
+        // (the tiles are 16-byte aligned with ld % 4 == 0: two 16-byte reads per k step)
+        const sgl::f32x4 acc = BF ? sgl::mfma_block16_bw<2>(Es, ld, bw.ws, bw.ld_d, n0, D, D)
                                   : sgl::mfma_block16<sgl::kNT>(Es, ld, w_s, D, n0, D, D);
         if (col < D) {
 #pragma unroll
@@ -148,8 +152,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       } else {
         sgl::f32x4 ad, an;
         if constexpr (BF) {
-          ad = sgl::mfma_block16_bw(Ed, ld, bw.wd, bw.ld_d, n0, D, D);
-          an = sgl::mfma_block16_bw(En, ld, bw.wd, bw.ld_d, n0, D, D);
+          ad = sgl::mfma_block16_bw<2>(Ed, ld, bw.wd, bw.ld_d, n0, D, D);
+          an = sgl::mfma_block16_bw<2>(En, ld, bw.wd, bw.ld_d, n0, D, D);
         } else {
           sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
         }
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     }
   }
   __syncthreads();
-  // logits, loss terms, logit gradients: one wave per event
+  // the two hidden-layer dot products: one wave per event
   for (int i = wave; i < kRows; i += kWaves) {
     float pp = 0.f, pn = 0.f;
     for (int j = lane; j < D; j += 64) {
@@ -179,19 +183,28 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     pp = sgl::wave_sum_dpp(pp);
     pn = sgl::wave_sum_dpp(pn);
     if (lane == 0) {
-      float gp = 0.f, gn = 0.f, sp = 0.f;
-      if (i < nrows) {
-        const float p = pp + b_o[0], n = pn + b_o[0];
-        pos_out[e0 + i] = p;
-        neg_out[e0 + i] = n;
-        sp = softplus(-p) + softplus(n);
-        gp = (sigmoid(p) - 1.f) / float(batch);
-        gn = sigmoid(n) / float(batch);
-      }
-      s_gp[i] = gp;
-      s_gn[i] = gn;
-      s_sp[i] = sp;
+      s_pp[i] = pp;
+      s_pn[i] = pn;
     }
+  }
+  __syncthreads();
+  // logits, loss terms and logit gradients of the tile's events on 16 lanes
+  // of one wave (the waves sharing a SIMD would run the branchy scalar tail
+  // one after another)
+  if (tid < kRows) {
+    const int i = tid;
+    float gp = 0.f, gn = 0.f, sp = 0.f;
+    if (i < nrows) {
+      const float p = s_pp[i] + s_bo, n = s_pn[i] + s_bo;
+      pos_out[e0 + i] = p;
+      neg_out[e0 + i] = n;
+      sp = softplus(-p) + softplus(n);
+      gp = (sigmoid(p) - 1.f) / float(batch);
+      gn = sigmoid(n) / float(batch);
+    }
+    s_gp[i] = gp;
+    s_gn[i] = gn;
+    s_sp[i] = sp;
   }
   __syncthreads();
   if (tid == 0) {
