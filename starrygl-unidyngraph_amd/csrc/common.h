@@ -39,6 +39,52 @@ struct LaunchTimer {
 };
 LaunchTimer &pending_timer();
 
+// A launch plan's cross-stream ordering handed to the first or last kernel
+// of one of its parts (sgl_plan_run, this host thread): the gate holds the
+// kernel's work until *word >= value (giving up after ~2 s and setting
+// *timeout); the signal stores value to *word once all of the launch's work
+// is done (release; counter is unused by the one-lane kernels that take
+// signals). An entry point that takes one either folds it into its kernel or
+// launches the one-lane gate / signal kernel itself (launch_gate /
+// launch_signal), so that each is issued exactly once and in order.
+struct PlanGate {
+  const uint32_t *word;
+  uint32_t value;
+  uint32_t *timeout;
+};
+struct PlanSignal {
+  uint32_t *word;
+  uint32_t value;
+  uint32_t *counter;
+};
+PlanGate &pending_gate();
+PlanSignal &pending_signal();
+inline PlanGate take_gate() {
+  const PlanGate g = pending_gate();
+  pending_gate() = PlanGate{nullptr, 0u, nullptr};
+  return g;
+}
+inline PlanSignal take_signal() {
+  const PlanSignal s = pending_signal();
+  pending_signal() = PlanSignal{nullptr, 0u, nullptr};
+  return s;
+}
+int launch_gate(const PlanGate &g, hipStream_t stream);
+int launch_signal(const PlanSignal &s, hipStream_t stream);
+
+// One thread: poll the gate word (acquire, agent scope) with s_sleep between
+// reads; after ~2 s (100 MHz clock) set the timeout word and give up.
+__device__ __forceinline__ void gate_wait(const uint32_t *word, uint32_t value, uint32_t *timeout) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  while (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < value) {
+    if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {
+      __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 template <typename F, typename... Args>
 inline void launch(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
   LaunchTimer &t = pending_timer();

@@ -35,6 +35,16 @@ LaunchTimer &pending_timer() {
   return t;
 }
 
+PlanGate &pending_gate() {
+  static thread_local PlanGate g{nullptr, 0u, nullptr};
+  return g;
+}
+
+PlanSignal &pending_signal() {
+  static thread_local PlanSignal s{nullptr, 0u, nullptr};
+  return s;
+}
+
 }  // namespace sgl
 
 extern "C" int sgl_abi_version(void) { return SGL_ABI_VERSION; }

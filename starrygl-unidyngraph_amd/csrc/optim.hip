@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_shadows(const sgl_grad_job *_
 // incremented first, then lr / (1 - b1^t) and sqrt(1 - b2^t) in double).
 // A closed segment keeps its count; its coef (for the next count) is unused.
 __global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, float lr, float b1, float b2,
-                            unsigned long long *step_counter, unsigned long long *step_out) {
+                            unsigned long long *step_counter, unsigned long long *step_out, uint32_t *sig_word,
+                            uint32_t sig_value) {
   if (threadIdx.x != 0) return;
   if (step_counter != nullptr) {
     const unsigned long long n = *step_counter + 1ull;
@@ -224,6 +225,9 @@ __global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, f
     coef[2 * s] = float(double(lr) / (1.0 - pow(double(b1), t)));
     coef[2 * s + 1] = float(sqrt(1.0 - pow(double(b2), t)));
   }
+  // a launch plan's signal: the earlier kernels of the stream are done
+  // (stream order), this lane's writes precede the release
+  if (sig_word != nullptr) __hip_atomic_store(sig_word, sig_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 AdamSegs make_segs(int nseg, float *const *steps, const int32_t *const *gates) {
@@ -269,9 +273,10 @@ extern "C" int sgl_adam_coef(int32_t nseg, float *const *steps, const int32_t *c
   SGL_REQUIRE(steps != nullptr && coef != nullptr, "adam_coef: NULL array");
   SGL_REQUIRE(step_counter == nullptr || step_out != nullptr, "adam_coef: step_counter without step_out");
   for (int s = 0; s < nseg; ++s) SGL_REQUIRE(steps[s] != nullptr, "adam_coef: NULL step counter %d", s);
+  const sgl::PlanSignal sig = sgl::take_signal();  // a launch plan's signal, folded
   sgl::launch(&k_adam_coef, dim3(1), dim3(64), 0, stream, int(nseg), make_segs(nseg, steps, gates), coef, lr, beta1,
               beta2, reinterpret_cast<unsigned long long *>(step_counter),
-              reinterpret_cast<unsigned long long *>(step_out));
+              reinterpret_cast<unsigned long long *>(step_out), sig.word, sig.value);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }

@@ -73,17 +73,21 @@ struct OpEntry {
   const char *name;
   int (*run)(const uint64_t *, hipStream_t);
   int slots;
+  bool takes_gate;    // as a part's first op it takes the part's gate (sgl::take_gate)
+  bool takes_signal;  // as a part's last op it takes the part's signal (sgl::take_signal)
 };
 
-#define SGL_OP(fn) {#fn, &run_op<&fn>, slots_of(&fn)}
+#define SGL_OP(fn) {#fn, &run_op<&fn>, slots_of(&fn), false, false}
+#define SGL_OP_GS(fn, g, s) {#fn, &run_op<&fn>, slots_of(&fn), g, s}
 const OpEntry kOps[] = {
-    SGL_OP(sgl_batch_prepare), SGL_OP(sgl_recent_sample), SGL_OP(sgl_memory_update), SGL_OP(sgl_memory_commit),
-    SGL_OP(sgl_conv_forward),  SGL_OP(sgl_predictor),     SGL_OP(sgl_conv_backward), SGL_OP(sgl_grad_adam),
-    SGL_OP(sgl_adam_coef),     SGL_OP(sgl_edge_rows),     SGL_OP(sgl_memory_update_bf16),
-    SGL_OP(sgl_recent_sample_packed), SGL_OP(sgl_memory_gather), SGL_OP(sgl_negatives_from_draws),
-    SGL_OP(sgl_time_projection_forward), SGL_OP(sgl_time_projection_backward),
+    SGL_OP_GS(sgl_batch_prepare, true, false), SGL_OP(sgl_recent_sample), SGL_OP(sgl_memory_update),
+    SGL_OP(sgl_memory_commit), SGL_OP(sgl_conv_forward), SGL_OP(sgl_predictor), SGL_OP(sgl_conv_backward),
+    SGL_OP(sgl_grad_adam), SGL_OP_GS(sgl_adam_coef, false, true), SGL_OP(sgl_edge_rows),
+    SGL_OP(sgl_memory_update_bf16), SGL_OP(sgl_recent_sample_packed), SGL_OP(sgl_memory_gather),
+    SGL_OP(sgl_negatives_from_draws), SGL_OP(sgl_time_projection_forward), SGL_OP(sgl_time_projection_backward),
 };
 #undef SGL_OP
+#undef SGL_OP_GS
 constexpr int kNumOps = int(sizeof(kOps) / sizeof(kOps[0]));
 static_assert(kNumOps > 0, "op table");
 
@@ -93,7 +97,10 @@ struct OpTimer {
   hipEvent_t start, end;
 };
 
-int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t) {
+// The ops of one part in order. `gate` (word NULL: none) is handed to the
+// first op, `sig` to the last; both must take theirs (their kinds say so).
+int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t, const sgl::PlanGate &gate,
+            const sgl::PlanSignal &sig) {
   for (int i = 0; i < n; ++i) {
     const sgl_op &op = ops[i];
     SGL_REQUIRE(op.kind >= 0 && op.kind < kNumOps, "plan op %d: unknown kind %d", base + i, op.kind);
@@ -102,9 +109,14 @@ int run_ops(const sgl_op *ops, int n, hipStream_t s, int base, const OpTimer &t)
                 op.nargs, e.slots);
     const bool timed = base + i == t.op;
     if (timed) sgl::pending_timer() = sgl::LaunchTimer{t.start, t.end};  // the op's (first) kernel records them
+    if (i == 0 && gate.word != nullptr) sgl::pending_gate() = gate;
+    if (i == n - 1 && sig.word != nullptr) sgl::pending_signal() = sig;
     const int rc = e.run(op.a, s);
     if (timed) sgl::pending_timer() = sgl::LaunchTimer{nullptr, nullptr};
+    // an op that failed before taking them leaves nothing pending
+    const bool left = sgl::take_gate().word != nullptr || sgl::take_signal().word != nullptr;
     if (rc) return rc;
+    SGL_REQUIRE(!left, "plan op %d (%s): the part's gate or signal was not taken", base + i, e.name);
   }
   return SGL_OK;
 }
@@ -119,15 +131,7 @@ __global__ void k_signal(uint32_t *word, uint32_t value) {
 }
 
 __global__ void k_gate(const uint32_t *word, uint32_t value, uint32_t *timeout) {
-  if (threadIdx.x != 0) return;
-  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();  // 100 MHz
-  while (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < value) {
-    if (__builtin_amdgcn_s_memrealtime() - t0 > 200000000ull) {
-      __hip_atomic_store(timeout, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
+  if (threadIdx.x == 0) sgl::gate_wait(word, value, timeout);
 }
 
 int signal(uint32_t *word, uint32_t value, hipStream_t s) {
@@ -143,6 +147,9 @@ int gate(const uint32_t *word, uint32_t value, uint32_t *timeout, hipStream_t s)
 }
 
 }  // namespace
+
+int sgl::launch_gate(const PlanGate &g, hipStream_t s) { return gate(g.word, g.value, g.timeout, s); }
+int sgl::launch_signal(const PlanSignal &sg, hipStream_t s) { return signal(sg.word, sg.value, s); }
 
 extern "C" int32_t sgl_plan_op_kind(const char *name, int32_t *nargs) {
   if (name == nullptr) return -1;
@@ -161,18 +168,35 @@ extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_back, 
   SGL_REQUIRE(n_front >= 0 && n_back >= 0, "plan_run: negative op count");
   SGL_REQUIRE(timed_op < 0 || (t_start && t_end), "plan_run: NULL timing event");
   const OpTimer t{timed_op, t_start, t_end};
+  const sgl::PlanGate no_gate{nullptr, 0u, nullptr};
+  const sgl::PlanSignal no_signal{nullptr, 0u, nullptr};
   if (front == nullptr) {  // one stream: everything in order on the back stream
-    return run_ops(ops, n_front + n_back, back, 0, t);
+    return run_ops(ops, n_front + n_back, back, 0, t, no_gate, no_signal);
   }
   SGL_REQUIRE(sync != nullptr && seq > 0 && need_back < seq,
               "plan_run: NULL sync words or inconsistent sequence numbers");
   SGL_REQUIRE(front != back, "plan_run: the front and back streams must differ");
   // separate 64-byte lines; sync[48] is the waits' timeout word
   uint32_t *w_back = sync, *w_front = sync + 16, *timeout = sync + 48;
-  if (int rc = gate(w_back, need_back, timeout, front)) return rc;
-  if (int rc = run_ops(ops, n_front, front, 0, t)) return rc;
-  if (int rc = signal(w_front, seq, front)) return rc;
+  // the gates and signals go into the parts' first and last kernels where
+  // those can take them (fewer launches), else into one-lane kernels
+  auto first_takes = [&](const sgl_op *p, int n) { return n > 0 && p[0].kind >= 0 && p[0].kind < kNumOps &&
+                                                          kOps[p[0].kind].takes_gate; };
+  auto last_takes = [&](const sgl_op *p, int n) { return n > 0 && p[n - 1].kind >= 0 && p[n - 1].kind < kNumOps &&
+                                                         kOps[p[n - 1].kind].takes_signal; };
+  const sgl::PlanGate g_front{w_back, need_back, timeout};
+  // (a signal is folded only into a one-lane kernel: a multi-workgroup one
+  // would need every workgroup to write back its XCD's L2 first)
+  const sgl::PlanSignal s_front{w_front, seq, nullptr}, s_back{w_back, seq, nullptr};
+  const bool fg = first_takes(ops, n_front), fs = last_takes(ops, n_front);
+  const bool bs = last_takes(ops + n_front, n_back);
+  if (!fg)
+    if (int rc = gate(w_back, need_back, timeout, front)) return rc;
+  if (int rc = run_ops(ops, n_front, front, 0, t, fg ? g_front : no_gate, fs ? s_front : no_signal)) return rc;
+  if (!fs)
+    if (int rc = signal(w_front, seq, front)) return rc;
   if (int rc = gate(w_front, seq, timeout, back)) return rc;
-  if (int rc = run_ops(ops + n_front, n_back, back, n_front, t)) return rc;
-  return signal(w_back, seq, back);
+  if (int rc = run_ops(ops + n_front, n_back, back, n_front, t, no_gate, bs ? s_back : no_signal)) return rc;
+  if (!bs) return signal(w_back, seq, back);
+  return SGL_OK;
 }

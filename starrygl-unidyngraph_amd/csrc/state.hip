@@ -269,12 +269,19 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst, int32_t *__restrict__ ridx_neg,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst, int32_t *__restrict__ any_edges,
-    int32_t *__restrict__ err) {
+    int32_t *__restrict__ err, const uint32_t *gate_word, uint32_t gate_value, uint32_t *gate_timeout) {
   extern __shared__ unsigned long long l_win[];                      // [2][cap]
   int32_t *l_cnt = reinterpret_cast<int32_t *>(l_win + 2 * cap);     // [2][cap]
   __shared__ int32_t s_scan[kPrepBlock / sgl::kWave];
   __shared__ float s_max[kPrepBlock / sgl::kWave];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (gate_word != nullptr) {
+    // a launch plan's cross-stream gate, before anything is read or written:
+    // thread 0's acquire loads invalidate this CU's L1 and the XCD's L2 for
+    // the whole workgroup (one CU), which the barrier then orders after
+    if (tid == 0) sgl::gate_wait(gate_word, gate_value, gate_timeout);
+    __syncthreads();
+  }
   uint32_t *summary = bits + bitmap_words(num_nodes);
   const int64_t off = cursor != nullptr ? *cursor : 0;
   src += off;
@@ -1135,16 +1142,20 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
                              cnt_src && cnt_dst && (neg == nullptr || ridx_neg)),
               "batch_prepare: NULL batch array");
   const int64_t cap = 2 * batch;
+  const sgl::PlanGate gate = sgl::take_gate();  // a launch plan's gate (folded, or its own kernel first)
   if (batch <= kPrepMaxBatch) {
     const size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
     SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_step_prepare_wg), lds));
     sgl::launch(&k_step_prepare_wg, dim3(1), dim3(kPrepBlock), lds, stream, batch, num_nodes, cap, src, dst, neg, ts,
                 cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64, ts_max, t_query, roots, root_ts,
                 ridx_src, ridx_dst, ridx_neg, reinterpret_cast<unsigned long long *>(win_src),
-                reinterpret_cast<unsigned long long *>(win_dst), cnt_src, cnt_dst, any_edges, err_flag);
+                reinterpret_cast<unsigned long long *>(win_dst), cnt_src, cnt_dst, any_edges, err_flag, gate.word,
+                gate.value, gate.timeout);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
+  if (gate.word != nullptr)
+    if (int rc = sgl::launch_gate(gate, stream)) return rc;
   SGL_REQUIRE((reinterpret_cast<uintptr_t>(word_prefix) & 15u) == 0, "batch_prepare: word_prefix not 16-byte aligned");
   const int64_t nwords = bitmap_words(num_nodes);  // a multiple of 4, padding words zero
   uint32_t *ts_slot = node_bits + nwords;          // the first summary word

@@ -88,6 +88,9 @@ class CTDGOnlineRuntime:
         # runs ahead of the GPU by up to that many chunks of steps)
         self._draw_ring: list[list] = []   # [pinned buffer, event of the last lookup reading it, its device address]
         self._draw_next = 0
+        # per split: [ring buffer, first event, count, drawn so far] of the
+        # next chunk, whose draws are taken during the current chunk's steps
+        self._pre_draw: dict[str, list] = {}
         self._pool_dev: torch.Tensor | None = None
         self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
@@ -148,11 +151,23 @@ class CTDGOnlineRuntime:
         self._parity = 0
         self.step = self.steps[0]   # the step buffers of the latest step
 
+    def _conv_mods(self) -> tuple:
+        """(core model, its conv or None, the conv's two dropout modules),
+        cached per core model (nn.Module attribute lookups cost microseconds
+        on every step)."""
+        core = self._core()
+        c = self.__dict__.get("_conv_mods_of")
+        if c is None or c[0] is not core:
+            conv = getattr(core, "conv", None)
+            c = self._conv_mods_of = (core, conv, conv.dropout if conv is not None else None,
+                                      conv.att_dropout if conv is not None else None)
+        return c
+
     def _dropout_passes(self) -> int:
         """3 attention passes per training step when a dropout is on
         (runtime.py:193-195), else 1."""
-        conv = self._core().conv
-        return 3 if (conv is not None and (conv.dropout.p > 0 or conv.att_dropout.p > 0)) else 1
+        _, conv, d, ad = self._conv_mods()
+        return 3 if (conv is not None and (d.p > 0 or ad.p > 0)) else 1
 
     def fence(self) -> None:
         """Order the next step after all work queued so far on the current
@@ -197,7 +212,13 @@ class CTDGOnlineRuntime:
         return self._front_stream
 
     def _core(self):
-        return self.model.module if hasattr(self.model, "module") else self.model
+        # (hasattr on an nn.Module without the attribute raises and catches
+        # inside __getattr__: cached per model object)
+        m = self.model
+        c = self.__dict__.get("_core_of")
+        if c is None or c[0] is not m:
+            c = self._core_of = (m, m.module if hasattr(m, "module") else m)
+        return c[1]
 
     # ------------------------------------------------------------- batching
     def iter_batches(self, split: str, batch_size: int) -> Iterable[CTDGDataBatch]:
@@ -263,59 +284,97 @@ class CTDGOnlineRuntime:
             del self._neg_queue[batch.split]
         s, n = batch.start, batch.size
         if s >= 0 and self.neg_chunk > 1:
-            lo, hi = self._neg_ahead.get(batch.split, (-1, -1))
+            split = batch.split
+            lo, hi = self._neg_ahead.get(split, (-1, -1))
             if s != lo or s + n > hi:
                 self._draw_ahead(batch)
-            self._neg_ahead[batch.split] = (s + n, self._neg_ahead[batch.split][1])
+            self._neg_ahead[split] = (s + n, self._neg_ahead[split][1])
+            # this step's share of the next chunk's draw
+            pre = self._pre_draw.get(split)
+            if pre is not None and pre[3] < pre[2]:
+                k = min(n, pre[2] - pre[3])
+                self._draw_into(pre[0], pre[3], k)
+                pre[3] += k
             return self._neg_all, s
         return self._negative_sample(batch).to(self.device, non_blocking=True), -1
 
-    def _draw_ahead(self, batch: CTDGDataBatch) -> None:
-        """Negatives of this batch and the next neg_chunk - 1 batches of its
-        split in one draw on the CPU generator, written at their places in
-        the stream-wide array. torch.randint gives the same numbers in one
-        call as in one call per batch, so while batches come in order this
-        equals the reference's per-step draw (runtime.py:124-136); a batch out
-        of order discards what was drawn ahead (the generator has then moved
-        on past draws that no step used)."""
-        s, n = batch.start, batch.size
-        ids = self.dataset.split_event_ids("test" if batch.split == "predict" else batch.split)
-        end = int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
-        hi = max(s + n, min(end, s + self.neg_chunk * n))
-        m = hi - s
-        pool = self._dst_pool()
+    def _draw_into(self, slot: list, at: int, k: int) -> None:
+        """k draws of the CPU generator into a ring buffer from position at."""
+        torch.randint(low=0, high=self._dst_pool().numel(), size=(k,), dtype=torch.long,
+                      out=slot[0][at:at + k])
+
+    def _ring_slot(self, m: int, n: int) -> list:
+        """The next pinned ring buffer (holding at least m draws), once the
+        lookup that read it kDrawRing chunks ago is done."""
         if not self._draw_ring or self._draw_ring[0][0].numel() < m:
-            # the whole ring at once (pinned allocations are slow: none in later steps)
+            # the whole ring at once (pinned allocations are slow: none in later
+            # steps), after every lookup that reads the old buffers
+            for old in self._draw_ring:
+                if old[1] is not None:
+                    old[1].synchronize()
             size = max(m, self.neg_chunk * n)
             self._draw_ring = []
             for _ in range(self.kDrawRing):
                 buf = torch.empty(size, dtype=torch.long, pin_memory=True)
                 self._draw_ring.append([buf, None, _capi.host_device_pointer(buf)])
             self._draw_next = 0
+            self._pre_draw.clear()
         slot = self._draw_ring[self._draw_next]
         self._draw_next = (self._draw_next + 1) % len(self._draw_ring)
         if slot[1] is not None:
-            slot[1].synchronize()   # the lookup that read this buffer, kDrawRing draws ago
-        host = slot[0][:m]
-        # the draw itself on the CPU generator; the lookup and the collision
-        # rule on the device (sgl_negatives_from_draws), in place
-        torch.randint(low=0, high=pool.numel(), size=(m,), dtype=torch.long, out=host)
+            slot[1].synchronize()
+        return slot
+
+    def _draw_ahead(self, batch: CTDGDataBatch) -> None:
+        """Negatives of this batch and the next neg_chunk - 1 batches of its
+        split, written at their places in the stream-wide array by one device
+        lookup of CPU draws. torch.randint gives the same numbers in one call
+        as in several consecutive calls, so the draws of a chunk are taken a
+        batch at a time during the previous chunk's steps (no step pays for a
+        whole chunk) and completed here when needed; while batches come in
+        order this equals the reference's per-step draw (runtime.py:124-136).
+        A batch out of order discards what was drawn ahead (the generator has
+        then moved on past draws that no step used)."""
+        s, n = batch.start, batch.size
+        split = batch.split
+        ids = self.dataset.split_event_ids("test" if split == "predict" else split)
+        end = int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
+        hi = max(s + n, min(end, s + self.neg_chunk * n))
+        m = hi - s
+        pre = self._pre_draw.pop(split, None)
+        if pre is not None and pre[1] == s and pre[2] == m and pre[0][0].numel() >= m:
+            slot = pre[0]
+            if pre[3] < m:
+                self._draw_into(slot, pre[3], m - pre[3])
+        else:
+            slot = self._ring_slot(m, n)
+            self._draw_into(slot, 0, m)
+        self._lookup(slot, s, m)
+        self._neg_ahead[split] = (s, hi)
+        if hi < end:   # the next chunk of the split, drawn during this chunk's steps
+            m2 = min(end, hi + self.neg_chunk * n) - hi
+            self._pre_draw[split] = [self._ring_slot(m2, n), hi, m2, 0]
+
+    def _lookup(self, slot: list, s: int, m: int) -> None:
+        """The pool lookup and collision rule of the m draws in a ring
+        buffer for events [s, s + m) (sgl_negatives_from_draws, in place in
+        the stream-wide array)."""
         if self._pool_dev is None:
-            self._pool_dev = pool.to(self.device)
+            self._pool_dev = self._dst_pool().to(self.device)
         front = self._front_stream
         stream = front if front is not None else torch.cuda.current_stream(self.device)
         # on the front stream, where the batch preparations read them (an
         # eager step orders its stream after the front stream first); the
         # lookup reads the pinned draws in place (no separate copy)
         with torch.cuda.stream(stream):
-            out = self._neg_all[s:hi]
+            out = self._neg_all[s:s + m]
             P = _capi.ptr
             _capi.check(_capi.call("sgl_negatives_from_draws", m, slot[2], P(self._pool_dev), self._pool_dev.numel(),
-                                   P(self._dev["dst"][s:hi]), P(out), P(self._neg_err.t), stream.cuda_stream),
+                                   P(self._dev["dst"][s:s + m]), P(out), P(self._neg_err.t), stream.cuda_stream),
                         "sgl_negatives_from_draws")
-            slot[1] = torch.cuda.Event()
+            if slot[1] is None:
+                slot[1] = torch.cuda.Event()
             slot[1].record(stream)
-        self._neg_ahead[batch.split] = (s, hi)
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev
@@ -337,9 +396,8 @@ class CTDGOnlineRuntime:
         """With bf16 attention products: the weight copies exist, every step
         buffer set uses them and they match the parameters (rebuilt on the
         current stream when marked dirty)."""
-        core = self._core()
-        conv = getattr(core, "conv", None)
-        if conv is None or getattr(conv, "gemm_dtype", "fp32") != "bf16":
+        core, conv, _, _ = self._conv_mods()
+        if conv is None or conv.gemm_dtype != "bf16":
             return
         if self._bf16 is None:
             self._bf16 = Bf16Shadow(self.dims, self.device)
@@ -406,7 +464,7 @@ class CTDGOnlineRuntime:
                     top = plan[3].index(self.plan_timer[0])
                     t0, t1 = evs[0].cuda_event, evs[1].cuda_event
             _capi.check(_capi.lib().sgl_plan_run(
-                plan[0], plan[1], plan[2], front.cuda_stream, torch.cuda.current_stream(self.device).cuda_stream,
+                plan[0], plan[1], plan[2], front.cuda_stream, _capi.stream_of(self.device),
                 self._sync_ptr, seq, self._need_back, top, t0, t1), "sgl_plan_run")
             # the next step's front part refills the buffers this step's
             # predecessor read; its commit follows this step's backward

@@ -150,8 +150,20 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_dev_index: dict = {}
+
+
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current HIP stream of ``device`` (its raw handle). torch's
+    current_stream() resolves the device through several Python layers on
+    every call; the index is resolved once per device here."""
+    if _raw_stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    idx = _dev_index.get(device)
+    if idx is None:
+        idx = _dev_index[device] = torch.cuda._get_device_index(device, optional=True)
+    return _raw_stream(idx)
 
 
 class GradJob(ctypes.Structure):
