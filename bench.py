@@ -130,7 +130,7 @@ def run_sampler(steps: int, warmup: int, cases: bool = True, cpu: bool = True) -
     wall = time.perf_counter() - w0
     avg_ms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
     alg = sampler_bytes(deg[nodes], head.cnt)
-    traffic = HBM_TRAFFIC.get(("cfg3", "recent_sample"))
+    traffic = HBM_TRAFFIC.get(("cfg3", "int64", "recent_sample"))
     traffic_src = TRAFFIC_SOURCE["cfg3"] if traffic else None
     # diagnostics: the probe-free (compulsory) bytes, and the counter-measured bytes over the same time
     compulsory = float((12 + 16 + 28 * head.cnt.double() + 4).sum().item())
@@ -458,16 +458,16 @@ def _restore(rt, snap):
 # profiles/tgn_cfg4_hbm_traffic.md and profiles/sampler_cfg3_hbm_traffic.md
 # (counters scaled by a copy kernel of known size); None where no counter run
 # was made.
-HBM_TRAFFIC = {("cfg4", "conv_backward"): round((2 * 2753.8 + 1506.1) * 1024),
-               ("cfg4", "edge_rows"): round((2 * 128.7 + 291.1) * 1024),
-               ("cfg4", "memory_commit"): round((2 * 78.0 + 94.3) * 1024),
-               ("cfg4", "conv_forward"): round((2 * 1834.4 + 1880.2) * 1024),
-               ("cfg4", "memory_update"): round((2 * 2344.5 + 256.2) * 1024),
-               ("cfg4", "predictor"): round((2 * 582.4 + 569.2) * 1024),
-               ("cfg4", "param_update"): round((2 * 8020.5 + 2070.6) * 1024),
-               ("cfg4", "batch_prepare"): round((2 * 63.3 + 128.2) * 1024),
-               ("cfg4", "recent_sample"): round((2 * 380.8 + 22.1) * 1024),
-               ("cfg3", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
+HBM_TRAFFIC = {("cfg4", "bf16", "conv_backward"): round((2 * 2109.8 + 1506.1) * 1024),
+               ("cfg4", "bf16", "edge_rows"): round((2 * 128.7 + 291.1) * 1024),
+               ("cfg4", "bf16", "memory_commit"): round((2 * 79.0 + 94.3) * 1024),
+               ("cfg4", "bf16", "conv_forward"): round((2 * 1253.8 + 1880.2) * 1024),
+               ("cfg4", "bf16", "memory_update"): round((2 * 1397.3 + 301.0) * 1024),
+               ("cfg4", "bf16", "predictor"): round((2 * 450.4 + 569.4) * 1024),
+               ("cfg4", "bf16", "param_update"): round((2 * 8026.5 + 2647.2) * 1024),
+               ("cfg4", "bf16", "batch_prepare"): round((2 * 63.6 + 128.2) * 1024),
+               ("cfg4", "bf16", "recent_sample"): round((2 * 380.8 + 22.1) * 1024),
+               ("cfg3", "int64", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
 # the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
 TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
 
@@ -652,7 +652,7 @@ def run_tgn(args, wl: dict) -> dict:
             ach, peak, unit = wavg / (avg * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         breakdown[name] = {"avg_us": round(avg * 1e3, 2), "calls": len(ms), "bound": bound,
                            "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5),
-                           "traffic": HBM_TRAFFIC.get((wl["config"], name))}
+                           "traffic": HBM_TRAFFIC.get((wl["config"], wl.get("gemm", "fp32"), name))}
     mean_U = sum(p[2] for p in per_step) / len(per_step)
     mean_E = sum(p[3] for p in per_step) / len(per_step)
     if not dom_ms:   # no timed launches in the timed region: the eager replay's
@@ -664,12 +664,13 @@ def run_tgn(args, wl: dict) -> dict:
     scale = 1e12 if bound == "mfma" else 1e9
     peak, unit = (mfma_peak(dom, wl), "TFLOP/s") if bound == "mfma" else (HBM_PEAK_GBS, "GB/s")
     ach = dwork / (dom_avg * 1e-3) / scale
+    tkey = (wl["config"], wl.get("gemm", "fp32"), dom)
     res = {
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
         "final_train_loss": final_loss,
         "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
-                     "frac": ach / peak, "traffic": HBM_TRAFFIC.get((wl["config"], dom)),
-                     "traffic_source": TRAFFIC_SOURCE.get(wl["config"]) if (wl["config"], dom) in HBM_TRAFFIC
+                     "frac": ach / peak, "traffic": HBM_TRAFFIC.get(tkey),
+                     "traffic_source": TRAFFIC_SOURCE.get(wl["config"]) if tkey in HBM_TRAFFIC
                      else None,
                      "kernel_avg_ms": dom_avg, "work_per_launch": dwork,
                      "work_formula": "SURVEY 8(d) attention projections: 2U(D+T)D + 4E(D+F+T)D + 4UD^2 "
