@@ -30,6 +30,7 @@ constexpr int kTile = 256;      // queries per compaction tile
 constexpr int kScanBlock = 1024;
 constexpr int64_t kWaveModeMaxQueries = 1 << 15;  // below: one wavefront per query
 constexpr int64_t kFence = 32;  // CSR entries per fence (one 128-byte line of int32 times)
+constexpr int kCopyBatch = 10;  // window-copy iterations per batch of loads (k = 10: one batch)
 
 // TsT: the CSR's timestamps as stored, int64 or (when every timestamp fits)
 // int32, compared with the int64 query times exactly. With int32 times the
@@ -98,29 +99,50 @@ __global__ __launch_bounds__(kBlock) void k_recent_padded(
     }
     out_cnt[i] = c;
   }
-  // Cooperative copy of the wave's 64 windows into its contiguous padded rows.
+  // Cooperative copy of the wave's 64 windows into its contiguous padded rows,
+  // kCopyBatch iterations at a time: every load of a batch is issued before
+  // its first store, so a batch costs one memory round trip (one per
+  // iteration when each load waited for the previous iteration's stores).
   const int64_t obase = q0 * k;
-  for (int it = 0; it < k; ++it) {
-    const int s = it * sgl::kWave + lane;
-    const int ql = s / k;
-    const int j = s - ql * k;
-    const int cq = __shfl(c, ql, sgl::kWave);
-    const int64_t bq = __shfl(b, ql, sgl::kWave);
-    const int64_t tq = __shfl(t, ql, sgl::kWave);
-    if (j < cq) {
-      const int64_t src = bq + j;
-      const int64_t o = obase + s;
-      const int64_t tv = int64_t(ts[src]);
-      if constexpr (std::is_same_v<TsT, int32_t>) {  // ids interleaved (nbr, eid) with int32 times
-        const int2 v = reinterpret_cast<const int2 *>(nbr)[src];
-        out_nbr[o] = v.x;
-        out_eid[o] = v.y;
-      } else {
-        out_nbr[o] = nbr[src];
-        out_eid[o] = eid[src];
+  for (int it0 = 0; it0 < k; it0 += kCopyBatch) {
+    TsT tv[kCopyBatch];
+    int32_t vn[kCopyBatch], ve[kCopyBatch];
+    bool ok[kCopyBatch];
+#pragma unroll
+    for (int u = 0; u < kCopyBatch; ++u) {
+      const int s = (it0 + u) * sgl::kWave + lane;
+      const int ql = s / k;  // < 64 while it0 + u < k
+      const int j = s - ql * k;
+      const int cq = __shfl(c, ql & (sgl::kWave - 1), sgl::kWave);
+      const int64_t bq = __shfl(b, ql & (sgl::kWave - 1), sgl::kWave);
+      ok[u] = it0 + u < k && j < cq;
+      tv[u] = 0;
+      vn[u] = ve[u] = 0;
+      if (ok[u]) {
+        const int64_t src = bq + j;
+        tv[u] = ts[src];
+        if constexpr (std::is_same_v<TsT, int32_t>) {  // ids interleaved (nbr, eid) with int32 times
+          const int2 v = reinterpret_cast<const int2 *>(nbr)[src];
+          vn[u] = v.x;
+          ve[u] = v.y;
+        } else {
+          vn[u] = nbr[src];
+          ve[u] = eid[src];
+        }
       }
-      out_dt[o] = float(tq - tv);  // int64 -> f32, round to nearest even
-      if (out_ts != nullptr) out_ts[o] = tv;
+    }
+#pragma unroll
+    for (int u = 0; u < kCopyBatch; ++u) {
+      const int s = (it0 + u) * sgl::kWave + lane;
+      const int ql = s / k;
+      const int64_t tq = __shfl(t, ql & (sgl::kWave - 1), sgl::kWave);
+      if (ok[u]) {
+        const int64_t o = obase + s;
+        out_nbr[o] = vn[u];
+        out_eid[o] = ve[u];
+        out_dt[o] = float(tq - int64_t(tv[u]));  // int64 -> f32, round to nearest even
+        if (out_ts != nullptr) out_ts[o] = int64_t(tv[u]);
+      }
     }
   }
 }
