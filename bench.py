@@ -569,13 +569,19 @@ def run_tgn(args, wl: dict) -> dict:
         n_train = -(-int(rt.dataset.split_event_ids("train").numel()) // wl["B"])
         args.steps = args.warmup = n_train
         log(f"epoch mode: {n_train} train batches per epoch")
-    for _ in range(args.warmup):
-        out = rt.train_step(ep.next())
+    # the eager per-kernel replay below starts from this snapshot and replays
+    # the warm-up steps first; taken (and the collector run) before the
+    # warm-up, so that neither the snapshot's copies nor a collection evict
+    # the GPU's and the host's caches just before the timed region
+    warm = [ep.next() for _ in range(args.warmup)]
+    snap = _snapshot(rt)
+    gc.collect()
+    for b in warm:
+        out = rt.train_step(b)
     torch.cuda.synchronize()
     log(f"warm-up done ({args.warmup} steps)")
 
     batches = [ep.next() for _ in range(args.steps)]
-    snap = _snapshot(rt)
     dom = args.roofline_kernel or ("memory_update" if wl.get("embedding") == "time_projection" else "conv_forward")
     timer: list = []
     if args.no_plans:   # eager steps: time the dominant kernel inside the timed region
@@ -602,7 +608,6 @@ def run_tgn(args, wl: dict) -> dict:
 
         rt.plan_timer = (ENTRY_POINTS[dom], next_pair)
     torch.cuda.synchronize()
-    gc.collect()
     gc.disable()   # no collector pauses on the host inside the timed region
     w0 = time.perf_counter()
     out = None
@@ -623,6 +628,8 @@ def run_tgn(args, wl: dict) -> dict:
 
     # replay the same steps eagerly with every library call timed + per-step counts
     _restore(rt, snap)
+    for b in warm:   # untimed: back to the state the timed region started from
+        rt.train_step(b)
     for st in rt.steps:
         st.timer, st.timed = timer, None
     timer.clear()
