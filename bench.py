@@ -467,7 +467,7 @@ HBM_TRAFFIC = {("cfg4", "bf16", "conv_backward"): round((2 * 2109.8 + 1506.1) * 
                ("cfg4", "bf16", "param_update"): round((2 * 8026.5 + 2647.2) * 1024),
                ("cfg4", "bf16", "batch_prepare"): round((2 * 63.6 + 128.2) * 1024),
                ("cfg4", "bf16", "recent_sample"): round((2 * 380.8 + 22.1) * 1024),
-               ("cfg3", "int64", "recent_sample"): round((2 * 1473203 + 449830) * 1024)}
+               ("cfg3", "int64", "recent_sample"): round((2 * 1342192 + 449830) * 1024)}
 # the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
 TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
 
