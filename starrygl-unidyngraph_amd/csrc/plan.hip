@@ -15,7 +15,10 @@
 // a value):
 //
 //   front:  wait(back >= need_back) -> front ops -> signal(fronted = seq)
-//   back:   wait(fronted >= seq) -> back ops -> signal(back = seq)
+//   back:   signal(back = seq - 1), wait(fronted >= seq) -> back ops
+//
+// (a back part's number is stored by the next back part's first kernel, once
+// every earlier kernel of the back stream is done)
 //
 // Plain launches cost the GPU well under a microsecond between kernels; the
 // same kernels replayed as graphs cost several, and more at graph
@@ -134,6 +137,19 @@ __global__ void k_gate(const uint32_t *word, uint32_t value, uint32_t *timeout) 
   if (threadIdx.x == 0) sgl::gate_wait(word, value, timeout);
 }
 
+// The back part's first kernel: the previous step's back part is done (it
+// precedes this kernel on the back stream), so its number is stored here
+// (release), then the kernel waits for this step's front part. One launch
+// where a signal at the end of each back part and a wait at the start of the
+// next took two on the critical stream.
+__global__ void k_signal_gate(uint32_t *sig_word, uint32_t sig_value, const uint32_t *word, uint32_t value,
+                              uint32_t *timeout) {
+  if (threadIdx.x == 0) {
+    if (sig_word != nullptr) __hip_atomic_store(sig_word, sig_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    sgl::gate_wait(word, value, timeout);
+  }
+}
+
 int signal(uint32_t *word, uint32_t value, hipStream_t s) {
   k_signal<<<1, 64, 0, s>>>(word, value);
   SGL_CHECK_LAUNCH();
@@ -142,6 +158,13 @@ int signal(uint32_t *word, uint32_t value, hipStream_t s) {
 
 int gate(const uint32_t *word, uint32_t value, uint32_t *timeout, hipStream_t s) {
   k_gate<<<1, 64, 0, s>>>(word, value, timeout);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
+}
+
+int signal_gate(uint32_t *sig_word, uint32_t sig_value, const uint32_t *word, uint32_t value, uint32_t *timeout,
+                hipStream_t s) {
+  k_signal_gate<<<1, 64, 0, s>>>(sig_word, sig_value, word, value, timeout);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
 }
@@ -187,16 +210,19 @@ extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_back, 
   const sgl::PlanGate g_front{w_back, need_back, timeout};
   // (a signal is folded only into a one-lane kernel: a multi-workgroup one
   // would need every workgroup to write back its XCD's L2 first)
-  const sgl::PlanSignal s_front{w_front, seq, nullptr}, s_back{w_back, seq, nullptr};
+  const sgl::PlanSignal s_front{w_front, seq, nullptr};
   const bool fg = first_takes(ops, n_front), fs = last_takes(ops, n_front);
-  const bool bs = last_takes(ops + n_front, n_back);
   if (!fg)
     if (int rc = gate(w_back, need_back, timeout, front)) return rc;
   if (int rc = run_ops(ops, n_front, front, 0, t, fg ? g_front : no_gate, fs ? s_front : no_signal)) return rc;
   if (!fs)
     if (int rc = signal(w_front, seq, front)) return rc;
-  if (int rc = gate(w_front, seq, timeout, back)) return rc;
-  if (int rc = run_ops(ops + n_front, n_back, back, n_front, t, no_gate, bs ? s_back : no_signal)) return rc;
-  if (!bs) return signal(w_back, seq, back);
-  return SGL_OK;
+  // The back part's number is stored when the next back part starts (every
+  // earlier back-stream kernel is done then): a front part waits for the back
+  // part two steps before it, whose number the back part one step before it
+  // (submitted earlier) stores. The number stored, seq - 1, is the last one
+  // issued before this step (a planned step's or a fence's; a fence stores its
+  // own as well).
+  if (int rc = signal_gate(seq > 1 ? w_back : nullptr, seq - 1, w_front, seq, timeout, back)) return rc;
+  return run_ops(ops + n_front, n_back, back, n_front, t, no_gate, no_signal);
 }
