@@ -551,6 +551,46 @@ __device__ __forceinline__ f32x4 mfma_block16_bw(const float *__restrict__ A, in
   }
 }
 
+// The weight fragments of one 16-column block of a bf16 W^T product (k steps
+// 0 .. ceil(kd/32)-1 <= KP; the rest zero), loaded ahead of the block's
+// products, e.g. before its A rows are gathered; lane layout and bounds as in
+// mfma_block16_bw.
+template <int KP>
+__device__ __forceinline__ void load_wfrag_bw(bf16x8 (&b)[KP], const uint16_t *__restrict__ W, int ldw, int n0, int kd,
+                                              int n_total) {
+  const int lane = threadIdx.x & 63;
+  const int n = min(n0 + (lane & 15), n_total - 1);
+  const __amdgpu_buffer_rsrc_t wr = bf16_weight_rsrc(W, uint32_t(n_total) * uint32_t(ldw));
+  const uint32_t wrow = uint32_t(n) * uint32_t(ldw) + 8u * uint32_t(lane >> 4);
+  const int nks = (kd + 31) >> 5;
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    b[u] = bf16x8{};
+    if (u < nks)
+      b[u] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, int((wrow + 32u * uint32_t(u)) * 2u), 0, 0));
+  }
+}
+
+// mfma_block16_bw with the weight fragments already in registers
+// (load_wfrag_bw): the same products in the same order (kd <= 32 KP).
+template <int CLS, int KP>
+__device__ __forceinline__ f32x4 mfma_block16_bw_pre(const float *__restrict__ A, int lda, const bf16x8 (&b)[KP],
+                                                     int kd) {
+  const int lane = threadIdx.x & 63;
+  const float *arow = A + (lane & 15) * lda;
+  const int q = lane >> 4;
+  const int nks = (kd + 31) >> 5;
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll
+  for (int u = 0; u < KP; ++u) {
+    if (u >= nks) break;  // uniform
+    const bf16x8 a = load_a_bf16<CLS>(arow, 32 * u + 8 * q, kd);
+    if (u & 1) acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc1, 0, 0, 0);
+    else acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[u], acc0, 0, 0, 0);
+  }
+  return acc0 + acc1;
+}
+
 // OUT (LDS, 16 x n_total) = A * W^T + bias for every job, the 16-column
 // blocks of all jobs dealt over the workgroup's waves. No barrier inside.
 template <int NJOBS>

@@ -54,7 +54,12 @@ __global__ __launch_bounds__(256) void k_zero(ZeroSpans z) {
     if (i < z.n[k]) z.p[k][i] = 0.f;
 }
 
-template <bool BF>
+// PRE (bf16 products with every 16-column block of W_s and W_d on a wave of
+// its own, D <= 32 kPreSteps): each wave loads its block's weight fragments
+// and bias first, so that their round trip overlaps the index loads and row
+// gathers, and holds them in registers for the products.
+constexpr int kPreSteps = 4;
+template <bool BF, bool PRE = false>
 __global__ __launch_bounds__(kBlock) void k_predictor(
     int64_t batch, int D, int train, const int32_t *__restrict__ num_roots, const float *__restrict__ y,
     const int32_t *__restrict__ rs, const int32_t *__restrict__ rd, const int32_t *__restrict__ rn,
@@ -88,9 +93,20 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
   __shared__ int s_last;
   __shared__ float s_bo;  // out_fc bias, staged with the first loads
 
+  static_assert(!PRE || BF, "held weights are the bf16 copies");
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t e0 = int64_t(blockIdx.x) * kRows;
   const int nrows = int(min<int64_t>(kRows, batch - e0));
+  const int nblk = (D + 15) >> 4;
+  sgl::bf16x8 wf[PRE ? kPreSteps : 1];
+  float bv0 = 0.f;
+  if constexpr (PRE) {
+    if (wave < 2 * nblk) {
+      const int nb = wave < nblk ? wave : wave - nblk, col = nb * 16 + (lane & 15);
+      sgl::load_wfrag_bw<kPreSteps>(wf, wave < nblk ? bw.ws : bw.wd, bw.ld_d, nb * 16, D, D);
+      bv0 = col < D ? (wave < nblk ? b_s[col] : b_d[col]) : 0.f;
+    }
+  }
   if (tid < kRows) {
     const bool ok = tid < nrows;
     s_idx[0][tid] = ok ? rs[e0 + tid] : -1;
@@ -133,10 +149,31 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
     En[i * ld + j] = c >= 0 ? y[2 * ystride + size_t(c) * D + j] : 0.f;
   }
   __syncthreads();
-  {
+  if constexpr (PRE) {
+    // the same products from the held fragments (one block per wave)
+    if (wave < 2 * nblk) {
+      const int nb = wave < nblk ? wave : wave - nblk, col = nb * 16 + (lane & 15);
+      if (wave < nblk) {
+        const sgl::f32x4 acc = sgl::mfma_block16_bw_pre<2, kPreSteps>(Es, ld, wf, D);
+        if (col < D) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) Hs[(4 * (lane >> 4) + v) * ld + col] = acc[v] + bv0;
+        }
+      } else {
+        const sgl::f32x4 ad = sgl::mfma_block16_bw_pre<2, kPreSteps>(Ed, ld, wf, D);
+        const sgl::f32x4 an = sgl::mfma_block16_bw_pre<2, kPreSteps>(En, ld, wf, D);
+        if (col < D) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            Hd[(4 * (lane >> 4) + v) * ld + col] = ad[v] + bv0;
+            Hn[(4 * (lane >> 4) + v) * ld + col] = an[v] + bv0;
+          }
+        }
+      }
+    }
+  } else {
     // h_s = W_s e_s + b_s on one set of waves; h_d and h_n (both W_d) on
     // another, each block's W_d loads shared by the two tiles
-    const int nblk = (D + 15) >> 4;
     for (int u = wave; u < 2 * nblk; u += kWaves) {
       const int nb = u < nblk ? u : u - nblk, n0 = nb * 16, col = n0 + (lane & 15);
       // the bias is loaded before the block's k loop (one round trip less)
@@ -318,7 +355,8 @@ extern "C" int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t
   const size_t lds_agg = lds0 + sizeof(long long) * 3 * kRows * size_t(D);
   const int agg = train && lds_agg <= 160 * 1024 ? 1 : 0;
   const size_t lds = agg ? lds_agg : lds0;
-  auto kern = bw != nullptr ? &k_predictor<true> : &k_predictor<false>;
+  const bool pre = bw != nullptr && 2 * ((D + 15) / 16) <= kWaves && D <= 32 * kPreSteps;
+  auto kern = bw == nullptr ? &k_predictor<false> : pre ? &k_predictor<true, true> : &k_predictor<true>;
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(kern), lds));
   sgl::launch(kern, dim3(unsigned((batch + kRows - 1) / kRows)), dim3(kBlock), lds, stream, batch, D, train,
               num_roots, y, ridx_src, ridx_dst, ridx_neg, w_s, b_s, w_d, b_d, w_o, b_o, pos_logits, neg_logits, loss,
