@@ -267,7 +267,7 @@ struct FwdLds {
   float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
 
-__host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bool slices) {
+__host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, int rows, bool slices) {
   FwdLds L;
   L.ldh = sgl::lds_ld(d.D + d.T);
   L.ldr = sgl::lds_ld(d.D);
@@ -287,19 +287,23 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, bo
   L.part = L.LB + d.D;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   L.scr = L.pml + (slices ? ((nw * d.H * 3 + 3) & ~3) : 0);
-  L.Ts = L.scr + (rows_for(nw) == 4 ? nw * 256 : 0);
+  L.Ts = L.scr + (rows == 4 ? nw * 256 : 0);
   return L;
 }
 
 // ts_rows: edges whose time encodings are staged in LDS (roots per tile *
 // fanout), 0 = computed in the edge loop instead.
-inline size_t fwd_lds_floats(const Dims &d, int nw, bool slices, int ts_rows) {
+inline size_t fwd_lds_floats(const Dims &d, int nw, int rows, bool slices, int ts_rows) {
   float *base = reinterpret_cast<float *>(uintptr_t(4096));
-  const FwdLds L = fwd_lds(d, base, nw, slices);
+  const FwdLds L = fwd_lds(d, base, nw, rows, slices);
   return size_t(L.Ts + size_t(ts_rows) * d.T - base);
 }
 
-template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+// HG: head groups per root in the edge phase. With HG = 2 the two waves of a
+// root each take half of its heads over the whole window (heads are
+// independent there: no merge), halving the per-lane [head][column] arrays,
+// so that wide rows with several heads fit 16-wave workgroups.
+template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW), int HG = 1>
 __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const float *__restrict__ h_root, const int32_t *__restrict__ cnt, float *__restrict__ X,
@@ -307,11 +311,14 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     int ts_rows, sgl::DropCfg dc, sgl_bf16_weights bw) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;  // waves per root in the edge phase
+  constexpr int NS = WPR / HG;   // window slices per root (merged through LDS when > 1)
+  constexpr int HL = HM / HG;    // heads per wave in the edge phase
   static_assert(RPW <= kRows && NW % RPW == 0, "tile shape");
+  static_assert(WPR % HG == 0 && HM % HG == 0 && (HG == 1 || NS == 1), "head groups");
   static_assert(!(BF && DROP), "the bf16 products run without dropout");
   extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const FwdLds L = fwd_lds(d, lds, NW, WPR > 1);
+  const FwdLds L = fwd_lds(d, lds, NW, RPW, NS > 1);
   __shared__ int s_cnt[kRows];
   __shared__ float s_sd[kRows][kMaxH];  // with attention dropout: the rows' kept-weight sums
 
@@ -430,27 +437,30 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   __syncthreads();
 
-  // edge phase: wave w takes slice w % WPR of root w / WPR's window
+  // edge phase: wave w takes window slice sl of root w / WPR's window for
+  // the heads of its head group hg (sub = w % WPR = hg * NS + sl)
   {
     const int i = wave / WPR, sub = wave % WPR;
+    const int hg = sub / NS, sl = sub - hg * NS;
     const int r = r0 + i;
     const int ne = s_cnt[i];
     int elo, ehi;
-    window_slice(ne, sub, WPR, elo, ehi);
-    float q[HM][JM], acc[HM][JM], m[HM], l[HM], qbh[HM];
-    float ls[HM];  // with attention dropout: the running sum of the kept, rescaled weights
+    window_slice(ne, sl, NS, elo, ehi);
+    float q[HL][JM], acc[HL][JM], m[HL], l[HL], qbh[HL];
+    float ls[HL];  // with attention dropout: the running sum of the kept, rescaled weights
 #pragma unroll
-    for (int h = 0; h < HM; ++h) {
+    for (int h = 0; h < HL; ++h) {
+      const int hh = hg * HL + h;
       m[h] = -INFINITY;
       l[h] = 0.f;
       ls[h] = 0.f;
-      qbh[h] = h < H ? L.qb[i * H + h] : 0.f;
+      qbh[h] = hh < H ? L.qb[i * H + hh] : 0.f;
 #pragma unroll
       for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
-        const bool ok = h < H && c < C;
-        q[h][j] = ok ? L.QT[i * L.ldq + h * C + c] : 0.f;
-        if (ok && sub == 0) sv.qt[size_t(r) * H * C + h * C + c] = i < nrows ? q[h][j] : 0.f;
+        const bool ok = hh < H && c < C;
+        q[h][j] = ok ? L.QT[i * L.ldq + hh * C + c] : 0.f;
+        if (ok && sl == 0) sv.qt[size_t(r) * H * C + hh * C + c] = i < nrows ? q[h][j] : 0.f;
         acc[h][j] = 0.f;
       }
     }
@@ -458,11 +468,11 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     // one chunk of nv <= kEC edges from window position e: the scores first
     // (independent reductions), then the online-softmax updates in edge order
     auto consume = [&](const float (&x)[kEC][JM], int e, int nv) {
-      float sc[kEC][HM];
+      float sc[kEC][HL];
 #pragma unroll
       for (int u = 0; u < kEC; ++u)
 #pragma unroll
-        for (int h = 0; h < HM; ++h) {
+        for (int h = 0; h < HL; ++h) {
           float part = 0.f;
 #pragma unroll
           for (int j = 0; j < JM; ++j) part += q[h][j] * x[u][j];
@@ -476,8 +486,9 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
         if constexpr (DROP)
           if (dc.p_att > 0.f) bits = sgl::drop_bits(dc, dstep, uint32_t(r), uint32_t(e + u), 0);
 #pragma unroll
-        for (int h = 0; h < HM; ++h) {
-          if (h >= H) continue;
+        for (int h = 0; h < HL; ++h) {
+          const int hh = hg * HL + h;
+          if (hh >= H) continue;
           const float sh = sc[u][h];
           const float a = sh > 0.f ? sh : 0.2f * sh;
           const float mn = fmaxf(m[h], a);
@@ -486,7 +497,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
           l[h] = l[h] * scale + pe;
           if constexpr (DROP) {
             // softmax over every edge (l), the kept weights rescaled (pk)
-            const float pk = pe * sgl::drop_keep(bits.v[h], dc.p_att, sa);
+            const float pk = pe * sgl::drop_keep(bits.v[hh], dc.p_att, sa);
             ls[h] = ls[h] * scale + pk;
 #pragma unroll
             for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pk * x[u][j];
@@ -495,7 +506,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
             for (int j = 0; j < JM; ++j) acc[h][j] = acc[h][j] * scale + pe * x[u][j];
           }
           m[h] = mn;
-          if (lane == 0) sv.score[idx * H + h] = a;
+          if (lane == 0) sv.score[idx * H + hh] = a;
         }
       }
     };
@@ -546,29 +557,30 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
         }
       }
     }
-    if (WPR == 1) {
-      // the wave owns its root: xbar overwrites qt in the root's LDS row
-      // (only this wave reads that row)
+    if constexpr (NS == 1) {
+      // the wave owns its root's heads of group hg: xbar overwrites their qt
+      // columns in the root's LDS row (only this wave reads them)
 #pragma unroll
-      for (int h = 0; h < HM; ++h) {
-        if (h >= H) continue;
+      for (int h = 0; h < HL; ++h) {
+        const int hh = hg * HL + h;
+        if (hh >= H) continue;
         const float inv = ne > 0 ? 1.f / l[h] : 0.f;
 #pragma unroll
         for (int j = 0; j < JM; ++j) {
           const int c = lane + 64 * j;
           if (c < C) {
             const float v = acc[h][j] * inv;
-            L.QT[i * L.ldq + h * C + c] = v;
-            sv.xbar[size_t(r) * H * C + h * C + c] = v;
+            L.QT[i * L.ldq + hh * C + c] = v;
+            sv.xbar[size_t(r) * H * C + hh * C + c] = v;
           }
         }
         if (lane == 0) {
-          sv.ml[(size_t(r) * H + h) * 2 + 0] = ne > 0 ? m[h] : 0.f;
-          sv.ml[(size_t(r) * H + h) * 2 + 1] = ne > 0 ? l[h] : 1.f;
+          sv.ml[(size_t(r) * H + hh) * 2 + 0] = ne > 0 ? m[h] : 0.f;
+          sv.ml[(size_t(r) * H + hh) * 2 + 1] = ne > 0 ? l[h] : 1.f;
           if (DROP) {
             const float sd = ne > 0 ? ls[h] * inv : 0.f;
-            s_sd[i][h] = sd;
-            sv.sdrop[size_t(r) * H + h] = sd;
+            s_sd[i][hh] = sd;
+            sv.sdrop[size_t(r) * H + hh] = sd;
           }
         }
       }
@@ -592,7 +604,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     }
   }
   __syncthreads();
-  if (WPR > 1) {
+  if constexpr (NS > 1) {
     // merge the slices: M = max_s m_s, Lsum = sum_s l_s e^(m_s - M),
     // xbar = sum_s acc_s e^(m_s - M) / Lsum (the whole window's softmax)
     for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
@@ -737,10 +749,10 @@ __host__ __device__ inline BwdLds bwd_lds(const Dims &d, float *base, int nw, bo
   return L;
 }
 
-inline size_t bwd_lds_floats(const Dims &d, int nw, bool slices) {
+inline size_t bwd_lds_floats(const Dims &d, int nw, int rows, bool slices) {
   float *base = reinterpret_cast<float *>(uintptr_t(4096));
   const BwdLds L = bwd_lds(d, base, nw, slices);
-  return size_t(L.scr + (rows_for(nw) == 4 ? nw * 256 : 0) - base);
+  return size_t(L.scr + (rows == 4 ? nw * 256 : 0) - base);
 }
 
 // The edge predictor's per-root gradient rows r0 .. r0+nrows-1 (fixed-point
@@ -760,7 +772,8 @@ __device__ __forceinline__ void consume_rows(long long *__restrict__ acc_src, lo
   }
 }
 
-template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW)>
+// HG: head groups per root in the edge phase, as in k_conv_fwd.
+template <int HM, int JM, bool DROP, bool BF = false, int NW = waves_for(HM, JM), int RPW = rows_for(NW), int HG = 1>
 __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     Dims d, const int32_t *__restrict__ num_roots, const int32_t *__restrict__ any_edges,
     const int32_t *__restrict__ cnt, const float *__restrict__ X, const float *__restrict__ S,
@@ -770,11 +783,15 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     float *__restrict__ g_src, float *__restrict__ g_dst, ConvGrads g, sgl::DropCfg dc, sgl_bf16_weights bw) {
   constexpr int kWaves = NW, kBlock = NW * 64;
   constexpr int WPR = NW / RPW;
+  constexpr int NS = WPR / HG;  // window slices per root (summed through LDS when > 1)
+  constexpr int HL = HM / HG;   // heads per wave in the edge phase
+  constexpr int EC = HG > 1 ? 2 : kEC;  // edges per round trip (fewer under the 1024-thread register cap)
   static_assert(RPW <= kRows && NW % RPW == 0 && NW <= kMaxWaves, "tile shape");
+  static_assert(WPR % HG == 0 && HM % HG == 0 && (HG == 1 || NS == 1), "head groups");
   static_assert(!(BF && DROP), "the bf16 products run without dropout");
   extern __shared__ __align__(16) float lds[];
   const int D = d.D, T = d.T, H = d.H, C = d.C, dh = d.dh, K = d.k;
-  const BwdLds L = bwd_lds(d, lds, NW, WPR > 1);
+  const BwdLds L = bwd_lds(d, lds, NW, NS > 1);
   __shared__ int s_cnt[kRows];
   __shared__ float s_sig[kRows][kMaxH];
 
@@ -942,28 +959,31 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
   }
   __syncthreads();
 
-  // edge backward phase: wave w takes slice w % WPR of root w / WPR's window
+  // edge backward phase: wave w takes window slice sl of root w / WPR's
+  // window for the heads of its head group hg (sub = w % WPR = hg * NS + sl)
   float twp[JM], tbp[JM];  // this lane's time-encoding weight / bias partials
 #pragma unroll
   for (int j = 0; j < JM; ++j) { twp[j] = 0.f; tbp[j] = 0.f; }
   {
     const int i = wave / WPR, sub = wave % WPR;
+    const int hg = sub / NS, sl = sub - hg * NS;
     const int r = r0 + i;
     const int ne = s_cnt[i];
     int elo, ehi;
-    window_slice(ne, sub, WPR, elo, ehi);
-    float q[HM][JM], gx[HM][JM], G[HM][JM];
-    float dot[HM], sig[HM], mh[HM], lh[HM], cb[HM];
+    window_slice(ne, sl, NS, elo, ehi);
+    float q[HL][JM], gx[HL][JM], G[HL][JM];
+    float dot[HL], sig[HL], mh[HL], lh[HL], cb[HL];
 #pragma unroll
-    for (int h = 0; h < HM; ++h) {
+    for (int h = 0; h < HL; ++h) {
+      const int hh = hg * HL + h;
       float pd = 0.f;
 #pragma unroll
       for (int j = 0; j < JM; ++j) {
         const int c = lane + 64 * j;
-        const bool ok = h < H && c < C;
-        q[h][j] = ok ? sv.qt[size_t(r) * H * C + h * C + c] : 0.f;
-        const float xb = ok ? sv.xbar[size_t(r) * H * C + h * C + c] : 0.f;
-        gx[h][j] = ok ? L.GX[i * L.ldq + h * C + c] : 0.f;
+        const bool ok = hh < H && c < C;
+        q[h][j] = ok ? sv.qt[size_t(r) * H * C + hh * C + c] : 0.f;
+        const float xb = ok ? sv.xbar[size_t(r) * H * C + hh * C + c] : 0.f;
+        gx[h][j] = ok ? L.GX[i * L.ldq + hh * C + c] : 0.f;
         G[h][j] = 0.f;
         pd += gx[h][j] * xb;
       }
@@ -973,33 +993,33 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         // with attention dropout the weights no longer sum to 1, so the
         // value bias stays in: dL/dalpha'_e = <g_xbar_h, X_e> + c_h with
         // c_h = <g_agg_h, b_v[h]>, and sum_e alpha_e dL/dalpha_e = dot + c_h s_h
-        if (h < H) {
+        if (hh < H) {
           float pc = 0.f;
-          for (int j = lane; j < dh; j += 64) pc += L.GA[i * L.ldr + h * dh + j] * p.b_v[h * dh + j];
+          for (int j = lane; j < dh; j += 64) pc += L.GA[i * L.ldr + hh * dh + j] * p.b_v[hh * dh + j];
           cb[h] = wave_sum(pc);
-          dot[h] += cb[h] * sv.sdrop[size_t(r) * H + h];
+          dot[h] += cb[h] * sv.sdrop[size_t(r) * H + hh];
         }
       }
       sig[h] = 0.f;
-      mh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2] : 0.f;
-      lh[h] = h < H ? sv.ml[(size_t(r) * H + h) * 2 + 1] : 1.f;
+      mh[h] = hh < H ? sv.ml[(size_t(r) * H + hh) * 2] : 0.f;
+      lh[h] = hh < H ? sv.ml[(size_t(r) * H + hh) * 2 + 1] : 1.f;
     }
     const size_t base = size_t(r) * K;
     for (int e0 = elo; e0 < ehi; e0 += 64) {
       const int mwin = min(64, ehi - e0);
-      float my_dt = 0.f, my_sc[HM];
+      float my_dt = 0.f, my_sc[HL];
 #pragma unroll
-      for (int h = 0; h < HM; ++h) my_sc[h] = 0.f;
+      for (int h = 0; h < HL; ++h) my_sc[h] = 0.f;
       if (lane < mwin) {
         my_dt = dt[base + e0 + lane];
 #pragma unroll
-        for (int h = 0; h < HM; ++h)
-          if (h < H) my_sc[h] = sv.score[(base + e0 + lane) * H + h];
+        for (int h = 0; h < HL; ++h)
+          if (hg * HL + h < H) my_sc[h] = sv.score[(base + e0 + lane) * H + hg * HL + h];
       }
-      for (int c0 = 0; c0 < mwin; c0 += kEC) {
-        float x[kEC][JM], sn[kEC][JM];
+      for (int c0 = 0; c0 < mwin; c0 += EC) {
+        float x[EC][JM], sn[EC][JM];
 #pragma unroll
-        for (int u = 0; u < kEC; ++u) {
+        for (int u = 0; u < EC; ++u) {
           const size_t row = base + e0 + min(c0 + u, mwin - 1);
           load_row<JM>(d, X, row, lane, x[u]);
 #pragma unroll
@@ -1008,36 +1028,37 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
             sn[u][j] = t >= 0 && t < d.T ? S[row * d.T + t] : 0.f;
           }
         }
-        float tg[kEC][HM];  // <g_xbar_h, X_e> for the chunk's edges
+        float tg[EC][HL];  // <g_xbar_h, X_e> for the chunk's edges
 #pragma unroll
-        for (int u = 0; u < kEC; ++u)
+        for (int u = 0; u < EC; ++u)
 #pragma unroll
-          for (int h = 0; h < HM; ++h) {
+          for (int h = 0; h < HL; ++h) {
             float part = 0.f;
 #pragma unroll
             for (int j = 0; j < JM; ++j) part += gx[h][j] * x[u][j];
             tg[u][h] = wave_sum(part);
           }
 #pragma unroll
-        for (int u = 0; u < kEC; ++u) {
+        for (int u = 0; u < EC; ++u) {
           if (c0 + u >= mwin) break;
           const int e = c0 + u;
           const float dtv = __shfl(my_dt, e, 64);
-          float gsv[HM], al[HM];
+          float gsv[HL], al[HL];
           sgl::U32x4 bits{};
           if constexpr (DROP)
             if (dc.p_att > 0.f) bits = sgl::drop_bits(dc, dstep, uint32_t(r), uint32_t(e0 + e), 0);
 #pragma unroll
-          for (int h = 0; h < HM; ++h) {
+          for (int h = 0; h < HL; ++h) {
+            const int hh = hg * HL + h;
             gsv[h] = 0.f;
             al[h] = 0.f;
-            if (h >= H) continue;
+            if (hh >= H) continue;
             const float t = tg[u][h];
             const float a = __shfl(my_sc[h], e, 64);
             const float alpha = __expf(a - mh[h]) / lh[h];
             float ga, aw = alpha;
             if constexpr (DROP) {
-              const float mk = sgl::drop_keep(bits.v[h], dc.p_att, sa);
+              const float mk = sgl::drop_keep(bits.v[hh], dc.p_att, sa);
               ga = alpha * (mk * (t + cb[h]) - dot[h]);  // softmax backward through the mask
               aw = alpha * mk;                           // the edge's weight in xbar'
             } else {
@@ -1055,10 +1076,10 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
           for (int j = 0; j < JM; ++j) {
             const int c = lane + 64 * j;
             if (c >= D + d.F && c < C) {
-              float gphi = 0.f;
+              float gphi = 0.f;  // this wave's heads (the waves' partials are summed below)
 #pragma unroll
-              for (int h = 0; h < HM; ++h)
-                if (h < H) gphi += gsv[h] * q[h][j] + al[h] * gx[h][j];
+              for (int h = 0; h < HL; ++h)
+                if (hg * HL + h < H) gphi += gsv[h] * q[h][j] + al[h] * gx[h][j];
               const float ds = -sn[u][j] * gphi;
               twp[j] += ds * dtv;
               tbp[j] += ds;
@@ -1067,28 +1088,29 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
         }
       }
     }
-    if (WPR == 1) {
-      // the wave owns its root: G overwrites g_xbar in the root's LDS row
-      // (only this wave reads that row)
+    if constexpr (NS == 1) {
+      // the wave owns its root's heads of group hg: G overwrites their
+      // g_xbar columns in the root's LDS row (only this wave reads them)
 #pragma unroll
-      for (int h = 0; h < HM; ++h) {
-        if (h >= H) continue;
+      for (int h = 0; h < HL; ++h) {
+        const int hh = hg * HL + h;
+        if (hh >= H) continue;
 #pragma unroll
         for (int j = 0; j < JM; ++j) {
           const int c = lane + 64 * j;
           if (c < C) {
-            L.GX[i * L.ldq + h * C + c] = G[h][j];
-            g.G[size_t(r) * H * C + h * C + c] = G[h][j];
+            L.GX[i * L.ldq + hh * C + c] = G[h][j];
+            g.G[size_t(r) * H * C + hh * C + c] = G[h][j];
           }
         }
         if (lane == 0) {
-          g.sigma[size_t(r) * H + h] = sig[h];
-          s_sig[i][h] = sig[h];
+          g.sigma[size_t(r) * H + hh] = sig[h];
+          s_sig[i][hh] = sig[h];
         }
       }
-    } else {
+    } else {  // one head group (HL == HM): the slice's partials of every head
 #pragma unroll
-      for (int h = 0; h < HM; ++h) {
+      for (int h = 0; h < HL; ++h) {
         if (h >= H) continue;
 #pragma unroll
         for (int j = 0; j < JM; ++j) {
@@ -1110,7 +1132,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_bwd(
     }
   }
   __syncthreads();
-  if (WPR > 1) {
+  if constexpr (NS > 1) {
     // sum the slices' partials into the root's row (every read of g_xbar is
     // behind the barrier above)
     for (int idx = tid; idx < RPW * H * C; idx += kBlock) {
@@ -1224,7 +1246,8 @@ template <typename Fn>
 struct Instance {
   Fn fn;
   int waves;
-  int rows;  // roots per workgroup
+  int rows;    // roots per workgroup
+  int hg = 1;  // head groups per root in the edge phase
 };
 
 inline void instance_shape(const Dims &d, int &hm, int &jm) {
@@ -1248,6 +1271,14 @@ auto pick_instance(const Dims &d) -> decltype(Pick<1, 2>::get()) {
 
 using FwdFn = decltype(&k_conv_fwd<1, 2, false>);
 using BwdFn = decltype(&k_conv_bwd<1, 2, false>);
+// bf16 instances whose whole-head arrays need the 8-wave instances'
+// registers split each root's heads over two waves of a 16-wave workgroup,
+// keeping the 8 roots per workgroup (the tile rows of sgl_conv_tile_rows).
+// The fp32 products' registers do not leave room for it; the backward's
+// widest shape (4 heads, 8 column blocks) would spill over 200 bytes a lane
+// under the 16-wave register cap and keeps the 8-wave instance.
+constexpr bool split_heads(int hm, int jm) { return waves_for(hm, jm) == 8 && hm >= 2; }
+constexpr bool split_heads_bwd(int hm, int jm) { return split_heads(hm, jm) && hm * jm <= 24; }
 template <int HM, int JM>
 struct FwdPick {
   static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
@@ -1259,11 +1290,17 @@ struct BwdPick {
 // the bf16-product instances (no dropout)
 template <int HM, int JM>
 struct FwdPickBf {
-  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<FwdFn> get() {
+    if constexpr (split_heads(HM, JM)) return {&k_conv_fwd<HM, JM, false, true, 16, 8, 2>, 16, 8, 2};
+    else return {&k_conv_fwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))};
+  }
 };
 template <int HM, int JM>
 struct BwdPickBf {
-  static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<BwdFn> get() {
+    if constexpr (split_heads_bwd(HM, JM)) return {&k_conv_bwd<HM, JM, false, true, 16, 8, 2>, 16, 8, 2};
+    else return {&k_conv_bwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))};
+  }
 };
 // the dropout instances (masks, kept-weight sums)
 template <int HM, int JM>
@@ -1411,10 +1448,10 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                     : drop ? pick_instance<FwdPickDrop>(d) : pick_instance<FwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   // stage the tile's time encodings in LDS when they fit
-  const bool slices = inst.waves > inst.rows;
+  const bool slices = inst.waves / inst.rows / inst.hg > 1;
   int ts_rows = fanout > 0 && T > 0 ? inst.rows * fanout : 0;
-  if (sizeof(float) * fwd_lds_floats(d, inst.waves, slices, ts_rows) > 160 * 1024) ts_rows = 0;
-  const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, slices, ts_rows);
+  if (sizeof(float) * fwd_lds_floats(d, inst.waves, inst.rows, slices, ts_rows) > 160 * 1024) ts_rows = 0;
+  const size_t lds = sizeof(float) * fwd_lds_floats(d, inst.waves, inst.rows, slices, ts_rows);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_forward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, te_w, te_b};
@@ -1461,7 +1498,10 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   const auto inst = bw != nullptr ? pick_instance<BwdPickBf>(d)
                     : drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
-  const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.waves > inst.rows);
+  // one ln_part / te_part tile per workgroup: the caller sized them by sgl_conv_tile_rows
+  SGL_REQUIRE(inst.rows == sgl_conv_tile_rows(D, F, T, H), "conv_backward: %d roots per workgroup, %d per tile",
+              inst.rows, sgl_conv_tile_rows(D, F, T, H));
+  const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.rows, inst.waves / inst.rows / inst.hg > 1);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));
   ConvParams p{w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b, nullptr, te_b};

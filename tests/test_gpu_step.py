@@ -292,12 +292,18 @@ def _conv_inputs(gpu, seed, N=400, D=32, F=6, T=16, H=2, k=10, R=150, E=3000):
 # waves with one root each (H=4, or C = D+F+T above 256 with H=2); rows 4-5
 # are the shapes of the benchmark configurations. With k=120 and T=96 the
 # 16-wave forward's time encodings (4 roots x 120 edges x 96) do not fit in
-# LDS: its edge loop reads them from the rows the other waves wrote.
+# LDS: its edge loop reads them from the rows the other waves wrote. The
+# bf16 rows after the first three cover every bf16 instance that splits a
+# root's heads over two waves of a 16-wave workgroup (H x 64-column blocks
+# 2x6, 2x8, 4x2, 4x4, 4x6 forward and backward; 4x8 forward, with the
+# 8-wave backward).
 @pytest.mark.parametrize("H,k,seed,D,F,T,bf16", [(2, 10, 0, 32, 6, 16, False), (4, 20, 1, 32, 6, 16, False),
                                                  (1, 3, 2, 32, 6, 16, False), (2, 10, 3, 100, 16, 100, False),
                                                  (2, 10, 4, 100, 172, 100, False), (2, 120, 5, 32, 6, 96, False),
                                                  (2, 10, 3, 100, 16, 100, True), (4, 20, 6, 172, 16, 100, True),
-                                                 (2, 7, 7, 36, 6, 20, True)])
+                                                 (2, 7, 7, 36, 6, 20, True), (2, 10, 8, 100, 172, 100, True),
+                                                 (2, 10, 9, 128, 172, 100, True), (4, 20, 10, 32, 6, 16, True),
+                                                 (4, 10, 11, 64, 16, 64, True), (4, 10, 12, 32, 300, 64, True)])
 def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T, bf16):
     """fp32: embedding within atol 2e-4, gradients rtol 2e-3. bf16 (the
     products on bf16 weight copies, Bf16Shadow; D = 36, H = 2: heads of 18
