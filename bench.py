@@ -254,7 +254,7 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
     import torch
 
     from starry_unigraph import synth
-    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState, gru_packed
     from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
 
     dev = torch.device("cuda:0")
@@ -319,7 +319,8 @@ def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
                     agg[name].append((ev0.elapsed_time(ev1), U, E))
                 timer.clear()
         # the same batches through the bf16-MFMA GRU (bf16 copies of the four weight matrices)
-        gru16 = dict(gru, **{w: gru[w].to(torch.bfloat16) for w in ("w_ih", "w_hh", "wc_ih", "wc_hh")})
+        gru16 = gru_packed(dict(gru, **{w: gru[w].to(torch.bfloat16).contiguous()
+                                        for w in ("w_ih", "w_hh", "wc_ih", "wc_hh")}))
         agg["memory_update_bf16"] = []
         step.timed = {"memory_update"}
         for i in range(warmup + steps):

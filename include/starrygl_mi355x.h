@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 14
+#define SGL_ABI_VERSION 15
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -239,7 +239,11 @@ int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
  * mixed-precision setting: bf16 GEMMs, fp32 memory). The updater's weights
  * never train (its output is detached, runtime.py:279), so the caller makes
  * the bf16 copies once. Mailbox contents, slots and pointers are the same as
- * sgl_memory_update's; new_mem within the bf16 tolerance (rtol 2e-2). */
+ * sgl_memory_update's; new_mem within the bf16 tolerance (rtol 2e-2).
+ * packed: the same four matrices in the wide-tile kernel's fragment order
+ * (sgl_gru_pack_bf16; 16-byte aligned), remade whenever the bf16 copies
+ * change. NULL runs the 16-root kernel on the row-major copies instead (same
+ * results, slower). */
 int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
                            const int32_t *num_roots, const int64_t *roots,
                            const float *memory, float *mailbox, float *mailbox_ts,
@@ -252,7 +256,19 @@ int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
                            const int64_t *batch_start,
                            const uint64_t *win_src, const uint64_t *win_dst,
                            const int32_t *cnt_src, const int32_t *cnt_dst,
-                           float *new_mem, hipStream_t stream);
+                           float *new_mem, const uint16_t *packed, hipStream_t stream);
+/* Elements (uint16) of the fragment-order copy of the four bf16 GRU weight
+ * matrices for hidden width D and edge-feature width F (0 if D <= 0 or F < 0).
+ * No reference counterpart: a layout of this build's bf16 copies. */
+int64_t sgl_gru_packed_elems(int32_t D, int32_t F);
+/* Writes that copy from the row-major bf16 matrices w_ih [3D][2D+F], w_hh,
+ * wc_ih, wc_hh [3D][D] (bit copies, zero padding), on `stream`. Element
+ * (((g*nc + c)*nks + s)*64 + l)*8 + t of a matrix's region (regions in that
+ * order, nc = ceil(D/16), nks = ceil(kd/32)) holds
+ * W[g*D + 16c + l%16][32s + 8(l/16) + t], or 0 past D or kd. */
+int sgl_gru_pack_bf16(int32_t D, int32_t F, const uint16_t *w_ih, const uint16_t *w_hh,
+                      const uint16_t *wc_ih, const uint16_t *wc_hh, uint16_t *packed,
+                      hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * (5) Memory commit.

@@ -670,20 +670,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t bf16_rsrc(const uint16_t *p, u
   return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, int(bytes), 0x00020000);
 }
 
-// 8 consecutive bf16 weights at element e of the matrix behind r (e % 4 == 0;
-// e % 8 == 0 and a 16-byte aligned matrix when V16). Elements past the
-// matrix read 0; elements of the next row (k >= kd) meet zero A elements.
-template <bool V16>
-__device__ __forceinline__ bf16x8_t load_w8(__amdgpu_buffer_rsrc_t r, uint32_t e) {
-  sgl::u32x4 v;
-  if constexpr (V16) {
-    v = __builtin_amdgcn_raw_buffer_load_b128(r, int(e * 2u), 0, 0);
-  } else {
-    const u32x2_t lo = __builtin_amdgcn_raw_buffer_load_b64(r, int(e * 2u), 0, 0);
-    const u32x2_t hi = __builtin_amdgcn_raw_buffer_load_b64(r, int(e * 2u + 8u), 0, 0);
-    v = sgl::u32x4{lo[0], lo[1], hi[0], hi[1]};
-  }
-  return __builtin_bit_cast(bf16x8_t, v);
+// Fragment-order copy of a bf16 GRU weight matrix W [3D][kd] (row-major,
+// gates r, z, n) for the wide-tile kernel: element
+//   (((g * nc + c) * nks + s) * 64 + l) * 8 + t,  nc = ceil(D/16), nks = ceil(kd/32),
+// holds W[g*D + 16c + l%16][32s + 8(l/16) + t] (0 past D or kd): the B
+// fragment of gate g, column chunk c and k step s for lane l of
+// v_mfma_f32_16x16x32_bf16. A wave's 16-byte loads of one fragment are then
+// one contiguous kilobyte (eight 128-byte lines) instead of sixteen row
+// segments that straddle lines; the vector-memory path (address, tag and
+// data cycles per line) is what the row-major loads were bound by.
+__host__ __device__ inline int64_t gru_packed_elems(int D, int kd) {
+  return 3ll * ((D + 15) / 16) * ((kd + 31) / 32) * 512;
 }
 
 // A[row][k .. k+8) of a bf16 LDS row (lda % 8 == 0, lda >= kd) with the
@@ -700,30 +697,30 @@ __device__ __forceinline__ bf16x8_t load_a8_tail(const uint16_t *arow, int k, in
 }
 
 // acc_g[rb] += A[16 rb + i][0..kd) . W[g*D + n0 + i'][0..kd) for the three
-// gates g of a GRU weight matrix W ([3D][kd] row-major bf16) and the RB
-// 16-row blocks of the LDS tile A (lda % 8 == 0, lda >= kd). The gate
-// fragments of a k step are loaded once and multiplied into every row
-// block. The loads run P-1 steps ahead of the products through P register
-// sets (the loop unrolled by P, so that no set is copied): an L2 round trip
-// is long against one step's products, and each wave's steps are a serial
-// chain. Only the last step (k past kd) masks A.
-template <int RB, bool V16, int P>
-__device__ __forceinline__ void wide_gates(int lane, const uint16_t *A, int lda, int kd, const uint16_t *W, int D,
+// gates g of a GRU weight matrix W (its fragment-order copy Wp, chunk
+// n0 / 16 of nc) and the RB 16-row blocks of the LDS tile A (lda % 8 == 0,
+// lda >= kd). The gate fragments of a k step are loaded once and multiplied
+// into every row block. The loads run P-1 steps ahead of the products
+// through P register sets (the loop unrolled by P, so that no set is
+// copied): an L2 round trip is long against one step's products, and each
+// wave's steps are a serial chain. Only the last step (k past kd) masks A.
+template <int RB, int P>
+__device__ __forceinline__ void wide_gates(int lane, const uint16_t *A, int lda, int kd, const uint16_t *Wp, int nc,
                                            int n0, sgl::f32x4 (&a0)[RB], sgl::f32x4 (&a1)[RB],
                                            sgl::f32x4 (&a2)[RB]) {
   const int i = lane & 15, q = lane >> 4;
-  // columns past D read row D-1 (finite weights; their outputs are discarded)
-  const int n = min(n0 + i, D - 1);
-  const __amdgpu_buffer_rsrc_t wr = bf16_rsrc(W, uint32_t(3 * D) * uint32_t(kd));
-  const uint32_t gs = uint32_t(D) * uint32_t(kd);
-  const uint32_t wrow = uint32_t(n) * uint32_t(kd) + 8u * q;
-  const uint16_t *arow = A + i * lda + 8 * q;
   const int nks = (kd + 31) >> 5, nfull = kd >> 5;
-  // loads are not guarded: past the matrix they read 0 (the descriptor's range)
+  const __amdgpu_buffer_rsrc_t wr = bf16_rsrc(Wp, uint32_t(3 * nc * nks) * 512u);
+  // byte offsets: this lane's 16 bytes of gate 0's fragment at k step 0, and
+  // the strides between k steps and gates
+  const uint32_t lane0 = ((uint32_t(n0 >> 4) * uint32_t(nks)) * 64u + uint32_t(lane)) * 16u;
+  const uint32_t gstride = uint32_t(nc * nks) * 1024u;
+  const uint16_t *arow = A + i * lda + 8 * q;
   auto load = [&](bf16x8_t (&b)[3], int ks) {
-    const uint32_t e = wrow + 32u * uint32_t(ks);
+    const uint32_t o = lane0 + 1024u * uint32_t(ks);
 #pragma unroll
-    for (int g = 0; g < 3; ++g) b[g] = load_w8<V16>(wr, e + g * gs);
+    for (int g = 0; g < 3; ++g)
+      b[g] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(wr, int(o + g * gstride), 0, 0));
   };
   auto mma = [&](const bf16x8_t (&b)[3], const bf16x8_t (&a)[RB]) {
 #pragma unroll
@@ -831,16 +828,15 @@ __device__ __forceinline__ TileCopy<RowOff> tile_copy(uint16_t *tile, int ld, co
   return TileCopy<RowOff>{tile, ld, base, f, n4};
 }
 
-// IH16 / HH16: 16-byte weight loads for W_ih / the D-wide matrices (rows of
-// a multiple of 8 elements, 16-byte aligned), else two 8-byte loads; P: the
-// weight prefetch depth.
-template <int RB, bool IH16, bool HH16, int P>
+// packed: the fragment-order copies of W_ih, W_hh, the cell's W_ih and W_hh
+// one after another (sgl_gru_pack_bf16); P: the weight prefetch depth.
+template <int RB, int P>
 __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
     int D, int K, int F, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ roots,
     const float *__restrict__ memory, float *__restrict__ mailbox, float *__restrict__ mailbox_ts,
-    int32_t *__restrict__ next_mail_pos, const uint16_t *__restrict__ w_ih, const uint16_t *__restrict__ w_hh,
-    const float *__restrict__ b_ih, const float *__restrict__ b_hh, const uint16_t *__restrict__ wc_ih,
-    const uint16_t *__restrict__ wc_hh, const float *__restrict__ bc_ih, const float *__restrict__ bc_hh,
+    int32_t *__restrict__ next_mail_pos, const uint16_t *__restrict__ packed,
+    const float *__restrict__ b_ih, const float *__restrict__ b_hh, const float *__restrict__ bc_ih,
+    const float *__restrict__ bc_hh,
     const int64_t *__restrict__ src, const int64_t *__restrict__ dst, const float *__restrict__ efeat,
     const float *__restrict__ ts, const int64_t *__restrict__ batch_start,
     const unsigned long long *__restrict__ win_src, const unsigned long long *__restrict__ win_dst,
@@ -863,6 +859,9 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
   const int U = *num_roots;
   const int nthr = blockDim.x;
   const int S4 = S >> 2, D4 = D >> 2;
+  const int nc = (D + 15) >> 4;
+  const uint16_t *pk_ih = packed, *pk_hh = pk_ih + gru_packed_elems(D, S);
+  const uint16_t *pkc_ih = pk_hh + gru_packed_elems(D, D), *pkc_hh = pkc_ih + gru_packed_elems(D, D);
   // The thread index is made opaque at the start of each stage, so that the
   // stage's per-lane address arithmetic is recomputed there rather than
   // hoisted out of the tile and slot loops and kept live (in registers the
@@ -942,8 +941,8 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
       sgl::f32x4 ar[RB], az[RB], an[RB], ah[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) ar[rb] = az[rb] = an[rb] = ah[rb] = sgl::f32x4{0.f, 0.f, 0.f, 0.f};
-      wide_gates<RB, IH16, P>(lane, xb, lbx, S, w_ih, D, n0, ar, az, an);
-      if (k > 0) wide_gates<RB, HH16, P>(lane, hb, lbh, D, w_hh, D, n0, ar, az, ah);
+      wide_gates<RB, P>(lane, xb, lbx, S, pk_ih, nc, n0, ar, az, an);
+      if (k > 0) wide_gates<RB, P>(lane, hb, lbh, D, pk_hh, nc, n0, ar, az, ah);
       const float br = b_ih[jc] + b_hh[jc], bz = b_ih[D + jc] + b_hh[D + jc];
       const float bn = b_ih[2 * D + jc], bhn = b_hh[2 * D + jc];
       if (jok) {
@@ -982,8 +981,8 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
       sgl::f32x4 ar[RB], az[RB], an[RB], ah[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) ar[rb] = az[rb] = an[rb] = ah[rb] = sgl::f32x4{0.f, 0.f, 0.f, 0.f};
-      wide_gates<RB, HH16, P>(lane, hb, lbh, D, wc_ih, D, n0, ar, az, an);
-      wide_gates<RB, HH16, P>(lane, mb, lbh, D, wc_hh, D, n0, ar, az, ah);
+      wide_gates<RB, P>(lane, hb, lbh, D, pkc_ih, nc, n0, ar, az, an);
+      wide_gates<RB, P>(lane, mb, lbh, D, pkc_hh, nc, n0, ar, az, ah);
       const float br = bc_ih[jc] + bc_hh[jc], bz = bc_ih[D + jc] + bc_hh[D + jc];
       const float bn = bc_ih[2 * D + jc], bhn = bc_hh[2 * D + jc];
 #pragma unroll
@@ -1194,34 +1193,32 @@ static bool host_aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(
 
 // Rows per tile of the wide-tile kernel: 16 for batches that give fewer
 // tiles than CUs, 64 once a batch has 64-root tiles for every CU; 0 when the
-// shape does not fit it (float4 rows, at most 12 chunks, LDS).
+// shape does not fit it (float4 rows, at most 12 chunks, LDS) or the caller
+// passed no fragment-order weight copy.
 static int wide_rows(int D, int F, int64_t capacity, const float *memory, const float *mailbox,
-                     const float *new_mem, const float *efeat, const uint16_t *w_ih, const uint16_t *w_hh,
-                     const uint16_t *wc_ih, const uint16_t *wc_hh) {
-  if (D % 4 != 0 || F % 4 != 0 || (D + 15) / 16 > kWideMaxChunks) return 0;
+                     const float *new_mem, const float *efeat, const uint16_t *packed) {
+  if (packed == nullptr || D % 4 != 0 || F % 4 != 0 || (D + 15) / 16 > kWideMaxChunks) return 0;
   if (!host_aligned16(memory) || !host_aligned16(mailbox) || !host_aligned16(new_mem) ||
-      (F > 0 && !host_aligned16(efeat)) || !host_aligned16(w_ih) || !host_aligned16(w_hh) ||
-      !host_aligned16(wc_ih) || !host_aligned16(wc_hh))
+      (F > 0 && !host_aligned16(efeat)) || !host_aligned16(packed))
     return 0;
   const int rows = capacity >= 64 * 256 ? 64 : 16;
   return wide_lds_bytes(D, F, rows) <= 160 * 1024 ? rows : 0;
 }
 
-template <int RB, bool IH16, bool HH16, int P>
+template <int RB, int P>
 static int launch_wide(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
                        const int64_t *roots, const float *memory, float *mailbox, float *mailbox_ts,
-                       int32_t *next_mail_pos, const uint16_t *w_ih, const uint16_t *w_hh, const float *b_ih,
-                       const float *b_hh, const uint16_t *wc_ih, const uint16_t *wc_hh, const float *bc_ih,
-                       const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
-                       const float *ts, const int64_t *batch_start, const uint64_t *win_src,
+                       int32_t *next_mail_pos, const uint16_t *packed, const float *b_ih, const float *b_hh,
+                       const float *bc_ih, const float *bc_hh, const int64_t *src, const int64_t *dst,
+                       const float *efeat, const float *ts, const int64_t *batch_start, const uint64_t *win_src,
                        const uint64_t *win_dst, const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
                        hipStream_t stream) {
-  auto kern = &k_gru_mailbox_wide<RB, IH16, HH16, P>;
+  auto kern = &k_gru_mailbox_wide<RB, P>;
   const size_t wl = wide_lds_bytes(D, F, 16 * RB);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(kern), wl));
   const unsigned grid = unsigned(std::min<int64_t>((capacity + 16 * RB - 1) / (16 * RB), sgl::kMaxGrid));
   sgl::launch(kern, dim3(grid), dim3(sgl::kWave * ((D + 15) / 16)), wl, stream, D, K, F, num_roots, roots, memory,
-              mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst,
+              mailbox, mailbox_ts, next_mail_pos, packed, b_ih, b_hh, bc_ih, bc_hh, src, dst,
               efeat, ts, batch_start, reinterpret_cast<const unsigned long long *>(win_src),
               reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
@@ -1234,7 +1231,8 @@ static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, cons
                   const WT *w_hh, const float *b_ih, const float *b_hh, const WT *wc_ih, const WT *wc_hh,
                   const float *bc_ih, const float *bc_hh, const int64_t *src, const int64_t *dst, const float *efeat,
                   const float *ts, const int64_t *batch_start, const uint64_t *win_src, const uint64_t *win_dst,
-                  const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem, hipStream_t stream) {
+                  const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem, const uint16_t *packed,
+                  hipStream_t stream) {
   SGL_REQUIRE(D > 0 && K > 0 && F >= 0, "memory_update: bad dims D=%d K=%d F=%d", D, K, F);
   SGL_REQUIRE(capacity >= 0 && capacity < INT_MAX, "memory_update: capacity out of range");
   if (capacity == 0) return SGL_OK;
@@ -1249,22 +1247,11 @@ static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, cons
   SGL_REQUIRE(2 * D + F <= 64 * kMaxMsgSlots, "memory_update: message width 2D+F = %d exceeds %d", 2 * D + F,
               64 * kMaxMsgSlots);
   if constexpr (!std::is_same_v<WT, float>) {
-    const int rows = wide_rows(D, F, capacity, memory, mailbox, new_mem, efeat, w_ih, w_hh, wc_ih, wc_hh);
+    const int rows = wide_rows(D, F, capacity, memory, mailbox, new_mem, efeat, packed);
     if (rows > 0) {
-      // 16-byte weight loads where rows are 16-byte multiples (the pointers are 16-byte aligned)
-      const bool ih16 = (2 * D + F) % 8 == 0, hh16 = D % 8 == 0;
-      decltype(&launch_wide<1, true, true, kWideDepthSmall>) fn;
-      if (rows == 64)
-        fn = ih16 ? (hh16 ? &launch_wide<4, true, true, kWideDepthLarge> : &launch_wide<4, true, false, kWideDepthLarge>)
-                  : (hh16 ? &launch_wide<4, false, true, kWideDepthLarge>
-                          : &launch_wide<4, false, false, kWideDepthLarge>);
-      else
-        fn = ih16 ? (hh16 ? &launch_wide<1, true, true, kWideDepthSmall> : &launch_wide<1, true, false, kWideDepthSmall>)
-                  : (hh16 ? &launch_wide<1, false, true, kWideDepthSmall>
-                          : &launch_wide<1, false, false, kWideDepthSmall>);
-      return fn(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih, w_hh, b_ih,
-                b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts, batch_start, win_src, win_dst, cnt_src,
-                cnt_dst, new_mem, stream);
+      const auto fn = rows == 64 ? &launch_wide<4, kWideDepthLarge> : &launch_wide<1, kWideDepthSmall>;
+      return fn(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, packed, b_ih, b_hh,
+                bc_ih, bc_hh, src, dst, efeat, ts, batch_start, win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
     }
   }
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_gru_mailbox<WT>), lds));
@@ -1288,7 +1275,7 @@ extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capaci
                                  hipStream_t stream) {
   return memory_update<float>(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos, w_ih,
                               w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts, batch_start,
-                              win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
+                              win_src, win_dst, cnt_src, cnt_dst, new_mem, nullptr, stream);
 }
 
 extern "C" int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,
@@ -1299,10 +1286,53 @@ extern "C" int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t c
                                       const int64_t *src, const int64_t *dst, const float *efeat, const float *ts,
                                       const int64_t *batch_start, const uint64_t *win_src, const uint64_t *win_dst,
                                       const int32_t *cnt_src, const int32_t *cnt_dst, float *new_mem,
-                                      hipStream_t stream) {
+                                      const uint16_t *packed, hipStream_t stream) {
   return memory_update<uint16_t>(D, K, F, capacity, num_roots, roots, memory, mailbox, mailbox_ts, next_mail_pos,
                                  w_ih, w_hh, b_ih, b_hh, wc_ih, wc_hh, bc_ih, bc_hh, src, dst, efeat, ts,
-                                 batch_start, win_src, win_dst, cnt_src, cnt_dst, new_mem, stream);
+                                 batch_start, win_src, win_dst, cnt_src, cnt_dst, new_mem, packed, stream);
+}
+
+namespace {
+// One thread per packed element: gather from the row-major bf16 matrix of its
+// region (W_ih [3D][2D+F], then W_hh, the cell's W_ih and W_hh [3D][D]).
+__global__ __launch_bounds__(kBlock) void k_gru_pack(int D, int S, const uint16_t *__restrict__ w_ih,
+                                                      const uint16_t *__restrict__ w_hh,
+                                                      const uint16_t *__restrict__ wc_ih,
+                                                      const uint16_t *__restrict__ wc_hh, uint16_t *__restrict__ out) {
+  const int64_t e_ih = gru_packed_elems(D, S), e_d = gru_packed_elems(D, D);
+  const int64_t total = e_ih + 3 * e_d;
+  const int nc = (D + 15) >> 4;
+  for (int64_t o = int64_t(blockIdx.x) * kBlock + threadIdx.x; o < total; o += int64_t(gridDim.x) * kBlock) {
+    const int m = o < e_ih ? 0 : int(1 + (o - e_ih) / e_d);
+    const int64_t r = m == 0 ? o : (o - e_ih) - int64_t(m - 1) * e_d;
+    const int kd = m == 0 ? S : D;
+    const uint16_t *w = m == 0 ? w_ih : m == 1 ? w_hh : m == 2 ? wc_ih : wc_hh;
+    const int nks = (kd + 31) >> 5;
+    const int t = int(r & 7), l = int((r >> 3) & 63);
+    const int64_t f = r >> 9;  // (g * nc + c) * nks + s
+    const int s = int(f % nks), gc = int(f / nks);
+    const int c = gc % nc, g = gc / nc;
+    const int n = 16 * c + (l & 15), k = 32 * s + 8 * (l >> 4) + t;
+    out[o] = n < D && k < kd ? w[(int64_t(g) * D + n) * kd + k] : uint16_t(0);
+  }
+}
+}  // namespace
+
+extern "C" int64_t sgl_gru_packed_elems(int32_t D, int32_t F) {
+  if (D <= 0 || F < 0) return 0;
+  return gru_packed_elems(D, 2 * D + F) + 3 * gru_packed_elems(D, D);
+}
+
+extern "C" int sgl_gru_pack_bf16(int32_t D, int32_t F, const uint16_t *w_ih, const uint16_t *w_hh,
+                                 const uint16_t *wc_ih, const uint16_t *wc_hh, uint16_t *packed,
+                                 hipStream_t stream) {
+  SGL_REQUIRE(D > 0 && F >= 0, "gru_pack: bad dims D=%d F=%d", D, F);
+  SGL_REQUIRE(w_ih && w_hh && wc_ih && wc_hh && packed, "gru_pack: NULL array");
+  const int64_t total = sgl_gru_packed_elems(D, F);
+  const unsigned grid = unsigned(std::min<int64_t>((total + kBlock - 1) / kBlock, sgl::kMaxGrid));
+  k_gru_pack<<<grid, kBlock, 0, stream>>>(D, 2 * D + F, w_ih, w_hh, wc_ih, wc_hh, packed);
+  SGL_CHECK_LAUNCH();
+  return SGL_OK;
 }
 
 static int memory_rows(const char *what, bool gather, int32_t D, int64_t capacity, const int32_t *num_roots,

@@ -135,6 +135,17 @@ class CTDGMemoryUpdater(nn.Module):
                     self._bf16[name].copy_(w[name])
                 else:
                     self._bf16[name] = w[name].to(torch.bfloat16).contiguous()
+            # the wide-tile kernel's fragment-order copy of the four matrices
+            D = self.hidden_dim
+            F = int(w["w_ih"].shape[1]) - 2 * D
+            n = int(_capi.lib().sgl_gru_packed_elems(D, F))
+            pk = self._bf16.get("packed")
+            if pk is None or pk.numel() != n or pk.device != w["w_ih"].device:
+                pk = self._bf16["packed"] = torch.empty(n, dtype=torch.bfloat16, device=w["w_ih"].device)
+            P = _capi.ptr
+            _capi.check(_capi.lib().sgl_gru_pack_bf16(
+                D, F, P(self._bf16["w_ih"]), P(self._bf16["w_hh"]), P(self._bf16["wc_ih"]), P(self._bf16["wc_hh"]),
+                P(pk), _capi.stream_of(pk.device)), "sgl_gru_pack_bf16")
             self._bf16_versions = versions
         w.update(self._bf16)
         return w
@@ -170,7 +181,7 @@ class CTDGMemoryUpdater(nn.Module):
             D, K, Fd, cap, P(n), P(roots), P(mem), P(mail), P(mts), P(nmp), P(w["w_ih"]), P(w["w_hh"]),
             P(w["b_ih"]), P(w["b_hh"]), P(w["wc_ih"]), P(w["wc_hh"]), P(w["bc_ih"]), P(w["bc_hh"]), P(dummy_i64),
             P(dummy_i64), P(dummy_f), P(dummy_f), None, P(zeros_k), P(zeros_k), P(zeros_i), P(zeros_i), P(out),
-            _capi.stream_of(dev)), name)
+            *([P(w["packed"])] if self.gemm_dtype == "bf16" else []), _capi.stream_of(dev)), name)
         return out[:M]
 
 

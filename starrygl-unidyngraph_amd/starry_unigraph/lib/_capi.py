@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -54,7 +54,9 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 24),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
-    "sgl_memory_update_bf16": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),
+    "sgl_memory_update_bf16": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 26),
+    "sgl_gru_packed_elems": (_i64, [_i32, _i32]),
+    "sgl_gru_pack_bf16": (ctypes.c_int, [_i32, _i32] + [_vp] * 6),
     "sgl_memory_commit": (ctypes.c_int, [_i32, _i64] + [_vp] * 11),
     "sgl_time_projection_forward": (ctypes.c_int, [_i32, _i64, _vp, _vp, _vp, ctypes.c_float, ctypes.c_float,
                                                    _vp, _vp, _vp, _vp]),

@@ -277,6 +277,21 @@ class Bf16Shadow:
                                                  _capi.stream_of(self.buf.device)), "sgl_grad_shadows")
 
 
+def gru_packed(gru: dict) -> dict:
+    """A copy of the GRU operand dict ``gru`` (bf16 weight matrices) with the
+    wide-tile kernel's fragment-order copy of its four matrices under
+    ``"packed"`` (sgl_gru_pack_bf16); the memory updater module keeps its own."""
+    w = gru["w_ih"]
+    D = int(gru["w_hh"].shape[1])
+    F = int(w.shape[1]) - 2 * D
+    pk = torch.empty(int(_capi.lib().sgl_gru_packed_elems(D, F)), dtype=torch.bfloat16, device=w.device)
+    P = _capi.ptr
+    _capi.check(_capi.lib().sgl_gru_pack_bf16(D, F, P(gru["w_ih"]), P(gru["w_hh"]), P(gru["wc_ih"]),
+                                              P(gru["wc_hh"]), P(pk), _capi.stream_of(w.device)),
+                "sgl_gru_pack_bf16")
+    return dict(gru, packed=pk)
+
+
 class DeviceStep:
     """The kernel sequence of one step over a NodeState (no host syncs)."""
 
@@ -364,7 +379,8 @@ class DeviceStep:
             P(st.next_mail_pos), P(gru["w_ih"]), P(gru["w_hh"]), P(gru["b_ih"]), P(gru["b_hh"]), P(gru["wc_ih"]),
             P(gru["wc_hh"]), P(gru["bc_ih"]), P(gru["bc_hh"]), P(src), P(dst), P(efeat), P(ts), P(event_offset),
             P(b.win_src),
-            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem), self._s()), fn))
+            P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.new_mem),
+            *([P(gru.get("packed"))] if fn == "sgl_memory_update_bf16" else []), self._s()), fn))
 
     def commit(self) -> None:
         b, st, P = self.buf, self.state, _capi.ptr
