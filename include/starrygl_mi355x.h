@@ -242,8 +242,8 @@ int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
  * sgl_memory_update's; new_mem within the bf16 tolerance (rtol 2e-2).
  * packed: the same four matrices in the wide-tile kernel's fragment order
  * (sgl_gru_pack_bf16; 16-byte aligned), remade whenever the bf16 copies
- * change. NULL runs the 16-root kernel on the row-major copies instead (same
- * results, slower). */
+ * change. NULL runs the 16-root kernel on the row-major copies instead
+ * (slower; the same tolerance). */
 int sgl_memory_update_bf16(int32_t D, int32_t K, int32_t F, int64_t capacity,
                            const int32_t *num_roots, const int64_t *roots,
                            const float *memory, float *mailbox, float *mailbox_ts,

@@ -417,7 +417,19 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   }
 }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// Gate nonlinearities of the bf16 wide-tile kernel from the hardware's base-2
+// exponential and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each):
+//   s(x) = 1 / (1 + 2^(-x log2 e)),  tanh(x) = 1 - 2 / (1 + 2^(2x log2 e)),
+// which saturate at the ends (2^+inf = inf, 1/inf = 0). Absolute error about
+// 1e-7, far inside the bf16 products' tolerance; at 16 gate values per lane
+// and slot the library expf / tanhf and divisions cost that kernel as much VALU
+// time as its products. The fp32 kernels keep expf / tanhf.
+__device__ __forceinline__ float gate_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504f * x));
+}
+__device__ __forceinline__ float gate_tanh(float x) {
+  return 1.f - 2.f * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(2.88539008f * x));
+}
 
 // GRU gate combination (PyTorch order r, z, n):
 //   r = s(gi_r + gh_r), z = s(gi_z + gh_z), n = tanh(gi_n + r * gh_n),
@@ -952,9 +964,9 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
           for (int v = 0; v < 4; ++v) {
             float *hp = hf + (16 * rb + rq + v) * ldf + j;
             const float hold = k > 0 ? *hp : 0.f;
-            const float r = 1.f / (1.f + expf(-(ar[rb][v] + br)));
-            const float z = 1.f / (1.f + expf(-(az[rb][v] + bz)));
-            const float nn = tanhf(an[rb][v] + bn + r * (ah[rb][v] + bhn));
+            const float r = gate_sigmoid(ar[rb][v] + br);
+            const float z = gate_sigmoid(az[rb][v] + bz);
+            const float nn = gate_tanh(an[rb][v] + bn + r * (ah[rb][v] + bhn));
             *hp = (1.f - z) * nn + z * hold;
           }
         }
@@ -992,9 +1004,9 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
           const int i = 16 * rb + rq + v;
           if (!jok || i >= nrows) continue;
           const float m = memory[s_root[i] * D + j];
-          const float r = 1.f / (1.f + expf(-(ar[rb][v] + br)));
-          const float z = 1.f / (1.f + expf(-(az[rb][v] + bz)));
-          const float nn = tanhf(an[rb][v] + bn + r * (ah[rb][v] + bhn));
+          const float r = gate_sigmoid(ar[rb][v] + br);
+          const float z = gate_sigmoid(az[rb][v] + bz);
+          const float nn = gate_tanh(an[rb][v] + bn + r * (ah[rb][v] + bhn));
           new_mem[size_t(r0 + i) * D + j] = (1.f - z) * nn + z * m;
         }
       }
