@@ -239,7 +239,7 @@ def gs_bytes(name: str, U: float, E: float, B: int, D: int, F: int, K: int) -> f
 # four batches: profiles/gather_scatter_cfg5_B1M.md): k_memory_commit + k_edge_rows, and the same with
 # the bf16 GRU + mailbox kernel (k_gru_mailbox_wide)
 GS_TRAFFIC_1M = 43_632_742 + 92_720_026
-GS_TRAFFIC_FULL_1M = GS_TRAFFIC_1M + 323_274_752
+GS_TRAFFIC_FULL_1M = GS_TRAFFIC_1M + 326_161_920
 
 
 def run_gather_scatter(steps: int, warmup: int, batches=GS_BATCHES) -> dict:
