@@ -264,6 +264,7 @@ struct FwdLds {
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][3] a slice's running max, sum and kept sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
+  float *DT;    // [rows][k] the tile's edges' dt (16-wave instances, which encode them beside Q)
   float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
 
@@ -287,7 +288,8 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, in
   L.part = L.LB + d.D;
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   L.scr = L.pml + (slices ? ((nw * d.H * 3 + 3) & ~3) : 0);
-  L.Ts = L.scr + (rows == 4 ? nw * 256 : 0);
+  L.DT = L.scr + (rows == 4 ? nw * 256 : 0);
+  L.Ts = L.DT + (nw == 16 ? ((rows * d.k + 3) & ~3) : 0);
   return L;
 }
 
@@ -354,6 +356,11 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     L.TW[t] = p.te_w[t];
     L.TB[t] = p.te_b[t];
   }
+  // the tile's dt rows (padding slots included: only live slots are encoded),
+  // so that the time-encoding loop below issues no global load per element
+  if constexpr (NW == 16)
+    if (T > 0)
+      for (int idx = tid; idx < RPW * K; idx += kBlock) L.DT[idx] = dt[size_t(r0) * K + idx];
   // the small parameter vectors of later phases, staged now so that no later
   // phase waits on a global load for them
   for (int j = tid; j < D; j += kBlock) {
@@ -398,7 +405,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       if (e < s_cnt[i]) {
         const size_t row = size_t(r0 + i) * K + e;
         float sn, cs;
-        te_sincos(te_arg(dt[row], L.TW[t], L.TB[t]), sn, cs);
+        te_sincos(te_arg(L.DT[el], L.TW[t], L.TB[t]), sn, cs);
         if (staged) L.Ts[el * T + t] = cs;
         X[row * C + D + d.F + t] = cs;
         S[row * T + t] = sn;
