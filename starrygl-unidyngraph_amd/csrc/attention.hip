@@ -264,9 +264,17 @@ struct FwdLds {
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][3] a slice's running max, sum and kept sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
-  float *DT;    // [rows][k] the tile's edges' dt (16-wave instances, which encode them beside Q)
+  float *DT;    // [rows][k] the tile's edges' dt (16-wave 8-root instances: stage_dt)
   float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
+
+// 16-wave instances encode the tile's edges' times beside the Q product, on
+// the waves Q leaves idle. With 8 roots a tile (the split-head instances:
+// 8 roots x k edges x T columns on five or so waves, tens of elements per
+// thread) the loop's per-element dt loads form a chain of dependent round
+// trips, so the tile's dt rows are staged in LDS with the setup loads; with
+// 4 roots the loop is a few elements per thread and its dt loads hit in L1.
+__host__ __device__ constexpr bool stage_dt(int nw, int rows) { return nw == 16 && rows == 8; }
 
 __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, int rows, bool slices) {
   FwdLds L;
@@ -289,7 +297,7 @@ __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, in
   L.pml = L.part + (slices ? nw * d.H * d.C : 0);
   L.scr = L.pml + (slices ? ((nw * d.H * 3 + 3) & ~3) : 0);
   L.DT = L.scr + (rows == 4 ? nw * 256 : 0);
-  L.Ts = L.DT + (nw == 16 ? ((rows * d.k + 3) & ~3) : 0);
+  L.Ts = L.DT + (stage_dt(nw, rows) ? ((rows * d.k + 3) & ~3) : 0);
   return L;
 }
 
@@ -356,9 +364,8 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
     L.TW[t] = p.te_w[t];
     L.TB[t] = p.te_b[t];
   }
-  // the tile's dt rows (padding slots included: only live slots are encoded),
-  // so that the time-encoding loop below issues no global load per element
-  if constexpr (NW == 16)
+  // the tile's dt rows (padding slots included: only live slots are encoded)
+  if constexpr (stage_dt(NW, RPW))
     if (T > 0)
       for (int idx = tid; idx < RPW * K; idx += kBlock) L.DT[idx] = dt[size_t(r0) * K + idx];
   // the small parameter vectors of later phases, staged now so that no later
@@ -405,7 +412,7 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
       if (e < s_cnt[i]) {
         const size_t row = size_t(r0 + i) * K + e;
         float sn, cs;
-        te_sincos(te_arg(L.DT[el], L.TW[t], L.TB[t]), sn, cs);
+        te_sincos(te_arg(stage_dt(NW, RPW) ? L.DT[el] : dt[row], L.TW[t], L.TB[t]), sn, cs);
         if (staged) L.Ts[el * T + t] = cs;
         X[row * C + D + d.F + t] = cs;
         S[row * T + t] = sn;
