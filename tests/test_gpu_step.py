@@ -21,6 +21,48 @@ def _close(got, want, rtol=RTOL, atol=1e-5, msg=""):
                                msg=msg)
 
 
+def _pack_fragments(w: np.ndarray, D: int) -> np.ndarray:
+    """Fragment order of one GRU matrix w [3D][kd] (uint16 bit patterns), written
+    from the definition: element (((g*nc + c)*nks + s)*64 + l)*8 + t holds
+    w[g*D + 16c + l%16][32s + 8(l//16) + t], zero past D or kd."""
+    kd = w.shape[1]
+    nc, nks = -(-D // 16), -(-kd // 32)
+    out = np.zeros((3, nc, nks, 64, 8), np.uint16)
+    for g in range(3):
+        for c in range(nc):
+            for s in range(nks):
+                for l in range(64):
+                    n = 16 * c + l % 16
+                    if n >= D:
+                        continue
+                    k0 = 32 * s + 8 * (l // 16)
+                    k1 = min(k0 + 8, kd)
+                    if k0 < kd:
+                        out[g, c, s, l, :k1 - k0] = w[g * D + n, k0:k1]
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("D,F", [(172, 16), (100, 0), (20, 4), (36, 172)])
+def test_gru_pack_matches_fragment_definition(gpu, D, F):
+    """sgl_gru_pack_bf16 is a bit copy into fragment order (D, kd not multiples
+    of 16 / 32 exercise the zero padding): bit-exact against the layout built
+    element by element on the host."""
+    from starry_unigraph.lib import _capi
+    rng = np.random.default_rng(D + F)
+    S = 2 * D + F
+    mats = [rng.integers(1, 1 << 16, size=(3 * D, kd), dtype=np.uint16) for kd in (S, D, D, D)]
+    dev = [torch.from_numpy(m.view(np.int16)).to(gpu) for m in mats]
+    n = int(_capi.lib().sgl_gru_packed_elems(D, F))
+    want = np.concatenate([_pack_fragments(m, D) for m in mats])
+    assert n == want.size
+    out = torch.full((n,), -1, dtype=torch.int16, device=gpu)
+    P = _capi.ptr
+    _capi.check(_capi.lib().sgl_gru_pack_bf16(D, F, *[P(t) for t in dev], P(out), _capi.stream_of(gpu)),
+                "sgl_gru_pack_bf16")
+    got = out.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("K,D,F,dt,M", [(1, 100, 16, "fp32", 203), (3, 32, 5, "fp32", 203),
                                         (4, 172, 16, "fp32", 203), (1, 100, 16, "bf16", 203),
                                         (3, 32, 5, "bf16", 203), (4, 172, 16, "bf16", 203),
