@@ -48,7 +48,7 @@ BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
 METRIC = "TGN train events/sec on 1 MI355X; sampler Mqueries/s; % HBM roofline"
 
 WORKLOADS = {
-    # precision: BASELINE's GEMM precision of the configuration (configs 4 and 5:
+    # precision: the benchmark's GEMM precision of the configuration (configs 4 and 5:
     # "bf16 GEMMs with fp32 memory"; configs 1 and 2: fp32)
     "tgn-large": dict(config="cfg4", stream="unipartite", family="tgn", D=100, T=100, H=2, k=10, K=1, B=600,
                       history=1, precision="bf16"),
@@ -681,7 +681,7 @@ def run_tgn(args, wl: dict) -> dict:
                      "traffic_source": TRAFFIC_SOURCE.get(wl["config"]) if tkey in HBM_TRAFFIC
                      else None,
                      "kernel_avg_ms": dom_avg, "work_per_launch": dwork,
-                     "work_formula": "SURVEY 8(d) attention projections: 2U(D+T)D + 4E(D+F+T)D + 4UD^2 "
+                     "work_formula": "attention projections, uncombined (models.py:77-137): 2U(D+T)D + 4E(D+F+T)D + 4UD^2 "
                                      "(x2 backward)" if dom.startswith("conv_") else "see kernel_work()",
                      "work_executed_per_launch": dexec,
                      "frac_executed": dexec / (dom_avg * 1e-3) / scale / peak},
@@ -778,7 +778,7 @@ def main() -> None:
     ap.add_argument("--gemm-dtype", default="auto", choices=["auto", "fp32", "bf16"],
                     help="the GRU, attention and edge-predictor GEMMs of the TGN workloads: fp32 MFMA, or bf16 "
                          "MFMA on bf16 weight copies with fp32 accumulation and fp32 memory; auto: the "
-                         "configuration's BASELINE precision (configs 4 and 5 bf16, configs 1 and 2 fp32)")
+                         "configuration's benchmark precision (configs 4 and 5 bf16, configs 1 and 2 fp32)")
     ap.add_argument("--no-gather-scatter", action="store_true",
                     help="skip the gather/scatter sub-benchmark of the default run")
     ap.add_argument("--copy-probe-mb", type=int, default=0,

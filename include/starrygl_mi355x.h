@@ -363,7 +363,7 @@ int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
 int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
 /* bf16 copies of the attention and edge-predictor weights, for the bf16
  * GEMM variants of sgl_conv_forward, sgl_conv_backward and sgl_predictor
- * (argument bw; NULL: the fp32 products). BASELINE configs 4 and 5 ask for
+ * (argument bw; NULL: the fp32 products). Benchmark configurations 4 and 5 ask for
  * bf16 GEMMs with fp32 memory; the reference runs these products in fp32
  * torch (models.py:77-137, 313-324), so this has no reference counterpart.
  * Every matrix is row-major raw bf16 with rows of ld elements (ld % 8 == 0,

@@ -274,7 +274,7 @@ def build_ctdg_model(model_family: str, *, num_nodes: int, hidden_dim: int, edge
     """models.py:345-386. ``embedding`` "attention" (the reference's model for
     every family) or "time_projection" (config 2's JODIE embedding);
     ``attention_gemm_dtype`` "bf16": the attention and edge-predictor products
-    on bf16 weight copies (BASELINE configs 4 and 5)."""
+    on bf16 weight copies (benchmark configurations 4 and 5)."""
     spec = CTDG_MODEL_SPECS.get(model_family.lower())
     if spec is None:
         raise KeyError(f"Unsupported CTDG model family: {model_family}")

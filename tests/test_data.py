@@ -1,5 +1,5 @@
 """The event-stream input pipeline on the CPU: split arithmetic at the
-BASELINE stream sizes, batching, the per-split sampler graph, and the
+Benchmark stream sizes, batching, the per-split sampler graph, and the
 on-disk formats of the reference's loader (data/raw_temporal.py:11-329):
 edges.csv + edge_features.pt, the edge-list fallback (<name>.edges /
 edges.txt: comments, separators, column layouts, stable time sort, id

@@ -1,4 +1,4 @@
-"""Full training and eval steps at the dimensions of every BASELINE
+"""Full training and eval steps at the dimensions of every benchmark
 configuration, teacher-forced against the CPU oracle (each step starts from
 the oracle's parameters and node state, so fp32 trajectories that the
 learnable time encoding would decorrelate are compared step by step):
@@ -14,7 +14,7 @@ learnable time encoding would decorrelate are compared step by step):
 
 each with the fp32 GRU and with bf16 GRU GEMMs, and (the attention
 configurations) with every GEMM in bf16 ("bf16all": the GRU and the
-attention and edge-predictor products on bf16 weight copies, BASELINE
+attention and edge-predictor products on bf16 weight copies, the benchmark
 configs 4 and 5's precision). Tolerances: loss, logits
 and memory within rtol 1e-3 of the oracle; gradients within rtol 2e-3
 (atol 1e-3 of the largest entry) of the same step evaluated in float64
@@ -59,7 +59,7 @@ CONFIGS = {
                  batches=(300, 301, 302)),
     "cfg2": dict(stream="bipartite", gen={}, family="jodie", D=100, T=100, H=2, k=10, K=1, B=200, history=1,
                  batches=(400, 401)),
-    # config 2 as BASELINE.json describes it: memory + GRU + a time projection, no attention
+    # config 2 as the benchmark defines it: memory + GRU + a time projection, no attention
     "cfg2p": dict(stream="bipartite", gen={}, family="jodie", embedding="time_projection", D=100, T=100, H=2, k=10,
                   K=1, B=200, history=1, batches=(400, 401, 402)),
     "cfg4": dict(stream="unipartite", gen=dict(num_nodes=30000, num_events=120000), family="tgn", D=100, T=100,
