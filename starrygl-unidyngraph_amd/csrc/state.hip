@@ -854,10 +854,13 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
     const unsigned long long *__restrict__ win_src, const unsigned long long *__restrict__ win_dst,
     const int32_t *__restrict__ cnt_src, const int32_t *__restrict__ cnt_dst, float *__restrict__ new_mem) {
   constexpr int R = 16 * RB;
-  // loads in flight per thread in the tile copies and the message copy: about
-  // one batch per copy at these tile sizes (the last batch repeats positions)
-  constexpr int NB = RB >= 4 ? 12 : 4;
-  constexpr int MB = RB >= 4 ? 8 : 4;
+  // loads in flight per thread in the tile copies and the message copy: one
+  // batch per copy at these tile sizes (the last batch repeats positions).
+  // With D = 172, F = 16 (11 waves): the memory and first mailbox tiles are
+  // 64 x (43 + 90) float4, 12.1 per thread; the messages 64 x 2 x 90, 16.4
+  // per thread. (17 tile loads per thread spill; 13 do not.)
+  constexpr int NB = RB >= 4 ? 13 : 4;
+  constexpr int MB = RB >= 4 ? 17 : 4;
   extern __shared__ __align__(16) float lds[];
   const int S = 2 * D + F;
   const int lbx = lds_ld_bf16(S), lbh = lds_ld_bf16(D);
