@@ -10,7 +10,9 @@ Prints ONE JSON line. Workloads:
   jodie      config 2: the same stream, memory + GRU + the JODIE time
              projection (ctdg.embedding = time_projection), no attention.
   tgn-stress config 5: the config-4 stream, D = 172, 4 heads, k = 20,
-             2 sampled hops, 4 mailbox slots, batch 4,000.
+             2 sampled hops and 1 attention layer (the reference's conv reads
+             only the first hop's block, runtime.py:164-167), 4 mailbox
+             slots, batch 4,000.
   sampler    config 3 alone (temporal sampler microbench).
   gather-scatter  the memory / mailbox gather-scatter microbench: config-5 state
              (1,140,149 nodes, D = 172, K = 4, F = 16) under batches of 600, 4,000
@@ -828,7 +830,8 @@ def main() -> None:
                                      f"projection, no attention), D={wl['D']} K={wl['K']} B={wl['B']}"
                                      if wl.get("embedding") == "time_projection" else
                                      f"{wl['config']} ({args.workload}): TGN train step, D={wl['D']} T={wl['T']} "
-                                     f"H={wl['H']} k={wl['k']} hops={wl['history']} K={wl['K']} B={wl['B']}, "
+                                     f"H={wl['H']} k={wl['k']} sampled_hops={wl['history']} attention_layers=1 K={wl['K']} "
+                                     f"B={wl['B']}, "
                                      "dropout 0"),
                         "global_batch": wl["B"], "parallelism": "single GPU"},
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 15
+#define SGL_ABI_VERSION 16
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -219,6 +219,13 @@ int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src,
  * cursor; src/dst/efeat/ts then span the whole stream.
  * ------------------------------------------------------------------------- */
 size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F);
+/* Roots per tile that sgl_memory_update_bf16 uses for these shapes when its
+ * arrays are 16-byte aligned and the fragment-order weight copy is passed:
+ * 64 or 16 (the wide-tile kernel, whose dynamic and static LDS must fit the
+ * CU's 160 KiB), or 0 (the 16-root kernel on row-major bf16 weights). Host
+ * arithmetic only (no device call). No counterpart in the reference: it
+ * tells a caller which kernel shape serves a configuration. */
+int32_t sgl_memory_update_bf16_tile_rows(int32_t D, int32_t F, int64_t capacity);
 int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity,
                       const int32_t *num_roots, const int64_t *roots,
                       const float *memory, float *mailbox, float *mailbox_ts,

@@ -1311,6 +1311,11 @@ struct FwdPickBf {
 };
 template <int HM, int JM>
 struct BwdPickBf {
+  // the backward's ln_part / te_part tiles are sized by sgl_conv_tile_rows
+  // (rows_for(waves_for(HM, JM))): a layout with other rows per workgroup
+  // would write past them
+  static_assert(!split_heads_bwd(HM, JM) || rows_for(waves_for(HM, JM)) == 8,
+                "a backward instance's rows per workgroup must equal sgl_conv_tile_rows");
   static Instance<BwdFn> get() {
     if constexpr (split_heads_bwd(HM, JM)) return {&k_conv_bwd<HM, JM, false, true, 16, 8, 2>, 16, 8, 2};
     else return {&k_conv_bwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))};

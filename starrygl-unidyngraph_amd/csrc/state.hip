@@ -478,6 +478,10 @@ __device__ __forceinline__ void gru_products(const AT *A0, int lda0, const WT *W
 // 16-byte bank groups.
 __host__ __device__ constexpr int lds_ld_bf16(int n) { return ((n + 7) & ~7) | 8; }
 
+// Static LDS of the wide-tile kernel at R rows per tile (its root tables:
+// three int64 and four int32 entries per row, two roles where they differ).
+__host__ __device__ constexpr size_t wide_static_lds(int R) { return size_t(R) * (5 * 8 + 5 * 4); }
+
 template <typename WT>
 __global__ __launch_bounds__(kGruBlock) void k_gru_mailbox(
     int D, int K, int F, const int32_t *__restrict__ num_roots,
@@ -871,6 +875,9 @@ __global__ __launch_bounds__(kWideMaxChunks * 64) void k_gru_mailbox_wide(
   uint16_t *mb = hb + R * lbh;                                         // memory tile
   __shared__ int64_t s_root[R], s_e[2][R], s_other[2][R];
   __shared__ int32_t s_cnt[2][R], s_pos[R], s_slot[2][R];
+  static_assert(sizeof(s_root) + sizeof(s_e) + sizeof(s_other) + sizeof(s_cnt) + sizeof(s_pos) + sizeof(s_slot) ==
+                    wide_static_lds(R),
+                "wide_static_lds must count the kernel's static LDS");
   const int U = *num_roots;
   const int nthr = blockDim.x;
   const int S4 = S >> 2, D4 = D >> 2;
@@ -1197,8 +1204,8 @@ extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {
   return sizeof(float) * kTileRows * (sgl::lds_ld(int(S)) + 2 * sgl::lds_ld(D) + 2 * sgl::lds_ld(int(G)));
 }
 
-// LDS of the wide-tile kernel: the fp32 hidden state and the bf16 mailbox,
-// hidden and memory tiles
+// Dynamic LDS of the wide-tile kernel: the fp32 hidden state and the bf16
+// mailbox, hidden and memory tiles
 static size_t wide_lds_bytes(int D, int F, int rows) {
   return sizeof(float) * size_t(rows) * size_t(sgl::lds_ld(D)) +
          sizeof(uint16_t) * size_t(rows) * (size_t(lds_ld_bf16(2 * D + F)) + 2 * size_t(lds_ld_bf16(D)));
@@ -1210,14 +1217,22 @@ static bool host_aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(
 // tiles than CUs, 64 once a batch has 64-root tiles for every CU; 0 when the
 // shape does not fit it (float4 rows, at most 12 chunks, LDS) or the caller
 // passed no fragment-order weight copy.
+static int wide_rows_for_shape(int D, int F, int64_t capacity) {
+  if (D <= 0 || F < 0 || D % 4 != 0 || F % 4 != 0 || (D + 15) / 16 > kWideMaxChunks) return 0;
+  // dynamic plus static LDS (the kernel's root tables) within the CU's 160 KiB;
+  // 64-root tiles that do not fit fall back to 16-root tiles
+  const auto fits = [&](int rows) { return wide_lds_bytes(D, F, rows) + wide_static_lds(rows) <= 160 * 1024; };
+  if (capacity >= 64 * 256 && fits(64)) return 64;
+  return fits(16) ? 16 : 0;
+}
+
 static int wide_rows(int D, int F, int64_t capacity, const float *memory, const float *mailbox,
                      const float *new_mem, const float *efeat, const uint16_t *packed) {
-  if (packed == nullptr || D % 4 != 0 || F % 4 != 0 || (D + 15) / 16 > kWideMaxChunks) return 0;
+  if (packed == nullptr) return 0;
   if (!host_aligned16(memory) || !host_aligned16(mailbox) || !host_aligned16(new_mem) ||
       (F > 0 && !host_aligned16(efeat)) || !host_aligned16(packed))
     return 0;
-  const int rows = capacity >= 64 * 256 ? 64 : 16;
-  return wide_lds_bytes(D, F, rows) <= 160 * 1024 ? rows : 0;
+  return wide_rows_for_shape(D, F, capacity);
 }
 
 template <int RB, int P>
@@ -1277,6 +1292,10 @@ static int memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, cons
               reinterpret_cast<const unsigned long long *>(win_dst), cnt_src, cnt_dst, new_mem);
   SGL_CHECK_LAUNCH();
   return SGL_OK;
+}
+
+extern "C" int32_t sgl_memory_update_bf16_tile_rows(int32_t D, int32_t F, int64_t capacity) {
+  return wide_rows_for_shape(D, F, capacity);
 }
 
 extern "C" int sgl_memory_update(int32_t D, int32_t K, int32_t F, int64_t capacity, const int32_t *num_roots,

@@ -34,6 +34,7 @@ from .data import CTDGDataBatch, TGTemporalDataset
 from .memory import CTDGMemoryBank
 from .metrics import link_metrics
 from .models import CTDGMemoryUpdater
+from .negatives import ChunkedDraws, DrawSlot
 from .sampler import NativeTemporalSampler
 
 
@@ -79,18 +80,13 @@ class CTDGOnlineRuntime:
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
         # negatives are drawn inside the step, for neg_chunk consecutive
-        # batches of a contiguous split at a time (1: one draw per step);
-        # _neg_ahead[split] = (next unconsumed event, end of the drawn range)
+        # batches of a contiguous split at a time (1: one draw per step),
+        # into a ring of kDrawRing pinned staging buffers (the host waits only
+        # for the lookup out of a buffer it filled that many draws ago); the
+        # schedule keeps the generator where per-step draws would leave it
         self.neg_chunk = 8
-        self._neg_ahead: dict[str, tuple[int, int]] = {}
-        # pinned staging of the draws: a ring, so that the host waits only for
-        # the copy out of a buffer it filled kDrawRing draws ago (the host
-        # runs ahead of the GPU by up to that many chunks of steps)
-        self._draw_ring: list[list] = []   # [pinned buffer, event of the last lookup reading it, its device address]
-        self._draw_next = 0
-        # per split: [ring buffer, first event, count, drawn so far] of the
-        # next chunk, whose draws are taken during the current chunk's steps
-        self._pre_draw: dict[str, list] = {}
+        self._draws = ChunkedDraws(lambda: self._dst_pool().numel(), self._split_end, self._alloc_draw_slot,
+                                   self._lookup, chunk=self.neg_chunk, ring=self.kDrawRing)
         self._pool_dev: torch.Tensor | None = None
         self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
@@ -138,6 +134,7 @@ class CTDGOnlineRuntime:
         # rebuild from the parameters before the next step)
         self._bf16: Bf16Shadow | None = None
         self._bf16_dirty = True
+        self._bf16_ver: tuple = ()
 
     def _make_steps(self, max_batch: int) -> None:
         # every hop of the sampler (history layers, sampler.py:76-90) is
@@ -233,6 +230,7 @@ class CTDGOnlineRuntime:
         """runtime.py:124-136: uniform over the sorted unique dst pool (global CPU
         generator), collisions with the true dst bumped to the next pool entry."""
         pool = self._dst_pool()
+        self._draws.release()   # the generator where the steps so far left it
         idx = torch.randint(low=0, high=pool.numel(), size=batch.dst.shape, dtype=torch.long)
         neg = pool[idx]
         col = neg.eq(batch.dst.cpu())
@@ -247,6 +245,7 @@ class CTDGOnlineRuntime:
         call as in per-batch calls, so this equals per-step sampling."""
         pool = self._dst_pool()
         ids = self.dataset.split_event_ids(split)
+        self._draws.release()
         idx = torch.randint(low=0, high=pool.numel(), size=(ids.numel(),), dtype=torch.long)
         dst = self.dataset.dst[ids]
         neg = pool[idx]
@@ -284,78 +283,25 @@ class CTDGOnlineRuntime:
             del self._neg_queue[batch.split]
         s, n = batch.start, batch.size
         if s >= 0 and self.neg_chunk > 1:
-            split = batch.split
-            lo, hi = self._neg_ahead.get(split, (-1, -1))
-            if s != lo or s + n > hi:
-                self._draw_ahead(batch)
-            self._neg_ahead[split] = (s + n, self._neg_ahead[split][1])
-            # this step's share of the next chunk's draw
-            pre = self._pre_draw.get(split)
-            if pre is not None and pre[3] < pre[2]:
-                k = min(n, pre[2] - pre[3])
-                self._draw_into(pre[0], pre[3], k)
-                pre[3] += k
+            self._draws.chunk = self.neg_chunk
+            self._draws.serve(batch.split, s, n)
             return self._neg_all, s
         return self._negative_sample(batch).to(self.device, non_blocking=True), -1
 
-    def _draw_into(self, slot: list, at: int, k: int) -> None:
-        """k draws of the CPU generator into a ring buffer from position at."""
-        torch.randint(low=0, high=self._dst_pool().numel(), size=(k,), dtype=torch.long,
-                      out=slot[0][at:at + k])
-
-    def _ring_slot(self, m: int, n: int) -> list:
-        """The next pinned ring buffer (holding at least m draws), once the
-        lookup that read it kDrawRing chunks ago is done."""
-        if not self._draw_ring or self._draw_ring[0][0].numel() < m:
-            # the whole ring at once (pinned allocations are slow: none in later
-            # steps), after every lookup that reads the old buffers
-            for old in self._draw_ring:
-                if old[1] is not None:
-                    old[1].synchronize()
-            size = max(m, self.neg_chunk * n)
-            self._draw_ring = []
-            for _ in range(self.kDrawRing):
-                buf = torch.empty(size, dtype=torch.long, pin_memory=True)
-                self._draw_ring.append([buf, None, _capi.host_device_pointer(buf)])
-            self._draw_next = 0
-            self._pre_draw.clear()
-        slot = self._draw_ring[self._draw_next]
-        self._draw_next = (self._draw_next + 1) % len(self._draw_ring)
-        if slot[1] is not None:
-            slot[1].synchronize()
-        return slot
-
-    def _draw_ahead(self, batch: CTDGDataBatch) -> None:
-        """Negatives of this batch and the next neg_chunk - 1 batches of its
-        split, written at their places in the stream-wide array by one device
-        lookup of CPU draws. torch.randint gives the same numbers in one call
-        as in several consecutive calls, so the draws of a chunk are taken a
-        batch at a time during the previous chunk's steps (no step pays for a
-        whole chunk) and completed here when needed; while batches come in
-        order this equals the reference's per-step draw (runtime.py:124-136).
-        A batch out of order discards what was drawn ahead (the generator has
-        then moved on past draws that no step used)."""
-        s, n = batch.start, batch.size
-        split = batch.split
+    def _split_end(self, split: str, s: int, n: int) -> int:
+        """One past the last event of the contiguous split holding batch
+        [s, s + n) (s + n when the batch lies outside it)."""
         ids = self.dataset.split_event_ids("test" if split == "predict" else split)
-        end = int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
-        hi = max(s + n, min(end, s + self.neg_chunk * n))
-        m = hi - s
-        pre = self._pre_draw.pop(split, None)
-        if pre is not None and pre[1] == s and pre[2] == m and pre[0][0].numel() >= m:
-            slot = pre[0]
-            if pre[3] < m:
-                self._draw_into(slot, pre[3], m - pre[3])
-        else:
-            slot = self._ring_slot(m, n)
-            self._draw_into(slot, 0, m)
-        self._lookup(slot, s, m)
-        self._neg_ahead[split] = (s, hi)
-        if hi < end:   # the next chunk of the split, drawn during this chunk's steps
-            m2 = min(end, hi + self.neg_chunk * n) - hi
-            self._pre_draw[split] = [self._ring_slot(m2, n), hi, m2, 0]
+        return int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
 
-    def _lookup(self, slot: list, s: int, m: int) -> None:
+    def _alloc_draw_slot(self, m: int) -> DrawSlot:
+        """A pinned staging buffer for at least m draws (a chunk of batches),
+        read in place by the device lookup through its device-visible
+        address."""
+        buf = torch.empty(max(m, 1), dtype=torch.long, pin_memory=True)
+        return DrawSlot(buf, None, _capi.host_device_pointer(buf))
+
+    def _lookup(self, slot: DrawSlot, s: int, m: int) -> None:
         """The pool lookup and collision rule of the m draws in a ring
         buffer for events [s, s + m) (sgl_negatives_from_draws, in place in
         the stream-wide array)."""
@@ -369,12 +315,12 @@ class CTDGOnlineRuntime:
         with torch.cuda.stream(stream):
             out = self._neg_all[s:s + m]
             P = _capi.ptr
-            _capi.check(_capi.call("sgl_negatives_from_draws", m, slot[2], P(self._pool_dev), self._pool_dev.numel(),
+            _capi.check(_capi.call("sgl_negatives_from_draws", m, slot.addr, P(self._pool_dev), self._pool_dev.numel(),
                                    P(self._dev["dst"][s:s + m]), P(out), P(self._neg_err.t), stream.cuda_stream),
                         "sgl_negatives_from_draws")
-            if slot[1] is None:
-                slot[1] = torch.cuda.Event()
-            slot[1].record(stream)
+            if slot.done is None:
+                slot.done = torch.cuda.Event()
+            slot.done.record(stream)
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev
@@ -387,15 +333,19 @@ class CTDGOnlineRuntime:
 
     # ------------------------------------------------------------- the step
     def params_changed(self) -> None:
-        """Parameters were written outside the fused update (a loaded
-        checkpoint, user code): rebuild the bf16 weight copies before the
-        next step."""
+        """Parameters were written outside the fused update in a way their
+        version counters do not show (through ``.data``, or by a kernel):
+        rebuild the bf16 weight copies before the next step. Writes through
+        torch (``load_state_dict``, ``nn.init``, in-place ops under
+        ``no_grad``) are detected without it."""
         self._bf16_dirty = True
 
     def _bf16_sync(self) -> None:
         """With bf16 attention products: the weight copies exist, every step
         buffer set uses them and they match the parameters (rebuilt on the
-        current stream when marked dirty)."""
+        current stream when marked dirty or when a shadowed weight's storage
+        or version counter changed: torch writes bump the counter, the fused
+        update's own stores keep the copies current and do not)."""
         core, conv, _, _ = self._conv_mods()
         if conv is None or conv.gemm_dtype != "bf16":
             return
@@ -408,10 +358,13 @@ class CTDGOnlineRuntime:
             self._bf16_dirty = True
         for st in self.steps:
             st.bf16 = self._bf16
-        if self._bf16_dirty:
-            self._bf16.refresh(conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight,
-                               core.src_fc.weight, core.dst_fc.weight)
+        ws = (conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight, core.src_fc.weight,
+              core.dst_fc.weight)
+        ver = tuple((w.data_ptr(), w._version) for w in ws)
+        if self._bf16_dirty or ver != self._bf16_ver:
+            self._bf16.refresh(*ws)
             self._bf16_dirty = False
+            self._bf16_ver = ver
 
     def _forward(self, batch: CTDGDataBatch, split: str, train: bool) -> StepTensors:
         n = batch.size

@@ -46,6 +46,37 @@ def test_host_side_queries_need_no_gpu():
     assert lib.sgl_compact_workspace_bytes(10 ** 6) >= 2 * 8 * (10 ** 6 // 256)
 
 
+def test_bf16_gru_tile_rows_fit_lds():
+    """The bf16 GRU's tile choice counts its static LDS (the root tables,
+    60 bytes a row) with the dynamic tiles against the CU's 160 KiB: shapes
+    whose 64-root tiles fit only without the static part take 16-root tiles."""
+    from starry_unigraph.lib import _capi
+    lib = _capi.load_library()
+
+    def ld_bf16(n):
+        return ((n + 7) & ~7) | 8
+
+    def ld_f32(n):
+        return ((n + 3) & ~3) | 4
+
+    def need(D, F, rows):
+        dyn = 4 * rows * ld_f32(D) + 2 * rows * (ld_bf16(2 * D + F) + 2 * ld_bf16(D))
+        return dyn + 60 * rows
+
+    big = 64 * 256
+    assert lib.sgl_memory_update_bf16_tile_rows(172, 16, big) == 64      # config 5
+    assert lib.sgl_memory_update_bf16_tile_rows(100, 16, 1200) == 16     # config 4's step
+    assert lib.sgl_memory_update_bf16_tile_rows(102, 16, big) == 0       # rows not float4
+    for D, F in ((192, 88), (192, 96)):
+        assert need(D, F, 64) - 60 * 64 <= 160 * 1024 < need(D, F, 64), (D, F)
+        assert lib.sgl_memory_update_bf16_tile_rows(D, F, big) == 16, (D, F)
+    for D in range(4, 197, 4):
+        for F in (0, 16, 96, 172):
+            want = 0 if (D + 15) // 16 > 12 else (64 if need(D, F, 64) <= 160 * 1024 else
+                                                   (16 if need(D, F, 16) <= 160 * 1024 else 0))
+            assert lib.sgl_memory_update_bf16_tile_rows(D, F, big) == want, (D, F)
+
+
 def test_argument_errors_are_reported_without_a_gpu():
     from starry_unigraph.lib import _capi
     lib = _capi.load_library()

@@ -289,6 +289,36 @@ def test_bf16_weight_copies_track_parameters(gpu):
     rt.collect_results = False
     for batch in list(rt.iter_batches("train", c["B"]))[:6]:
         rt.train_step(batch)
+    _check_bf16_copies(rt)
+
+
+def test_bf16_copies_follow_in_place_weight_writes(gpu):
+    """Weights written by torch between planned steps (in-place ops under
+    no_grad, load_state_dict), with no explicit params_changed(): the next
+    step rebuilds the bf16 copies (the weights' version counters moved), so
+    after it every copy again equals its parameter rounded to bf16."""
+    c, rt, *_ = _pair("cfg4", "bf16all")
+    rt.collect_results = False
+    batches = list(rt.iter_batches("train", c["B"]))[:9]
+    for batch in batches[:3]:
+        rt.train_step(batch)
+    core = rt.model
+    with torch.no_grad():
+        core.conv.w_q.weight.mul_(0.5)
+        core.src_fc.weight.add_(0.01)
+    for batch in batches[3:6]:
+        rt.train_step(batch)
+    _check_bf16_copies(rt)
+    sd = {k: v.clone() for k, v in core.state_dict().items()}
+    sd["conv.w_v.weight"].mul_(-1.0)
+    sd["dst_fc.weight"].mul_(2.0)
+    core.load_state_dict(sd)
+    for batch in batches[6:]:
+        rt.train_step(batch)
+    _check_bf16_copies(rt)
+
+
+def _check_bf16_copies(rt):
     rt.fence()
     torch.cuda.synchronize()
     sh = rt._bf16
