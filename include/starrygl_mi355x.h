@@ -38,6 +38,9 @@ extern "C" {
 /* bits OR-ed into err_flag by kernels */
 #define SGL_DERR_NODE_RANGE 1 /* a node id outside [0, num_nodes) */
 #define SGL_DERR_EID_RANGE 2  /* an edge id outside [0, 2^31) */
+#define SGL_DERR_STALE_NODE_BITS 4 /* sgl_batch_prepare found node bits set before it marked its batch
+                                    * (the previous preparation's commit did not run): the batch is
+                                    * given no roots and the bitmap is cleared */
 
 /* (8) version / ABI query. */
 int sgl_abi_version(void);

@@ -50,8 +50,8 @@ __device__ __forceinline__ float ts_from_order(uint32_t k) {
 // event, as same-address atomics serialise in L2. A node whose table slot is
 // held by another goes to global memory directly. The running timestamp
 // maximum of the mark kernel lives in the first summary word of node_bits as
-// order(max ts), a word this path does not otherwise use; the scan reads it
-// and clears it again.
+// order(max ts), and the number of bits the mark kernel set in the second
+// (words this path does not otherwise use); the scan reads and clears them.
 constexpr int kAggBlock = 1024;
 constexpr int kAggPer = 4;
 constexpr int kAggEvents = kAggBlock * kAggPer;
@@ -73,7 +73,9 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
     int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
   __shared__ int32_t s_node[kMarkSlots];
   __shared__ float s_m[kAggBlock / sgl::kWave];
+  __shared__ int32_t s_new;  // bits this workgroup set (summed into new_count)
   const int tid = threadIdx.x;
+  if (tid == 0) s_new = 0;
   const int64_t g = int64_t(blockIdx.x) * kAggBlock + tid;
   if (g == 0) *any_edges = 0;
   for (int64_t r = g; r < cap; r += int64_t(gridDim.x) * kAggBlock) {
@@ -105,7 +107,7 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
       // first in this workgroup (or its slot is taken): set the bit, with no
       // atomic when another workgroup has set it already
       const uint32_t mb = 1u << (n & 31);
-      if ((bits[n >> 5] & mb) == 0u) atomicOr(&bits[n >> 5], mb);
+      if ((bits[n >> 5] & mb) == 0u && (atomicOr(&bits[n >> 5], mb) & mb) == 0u) atomicAdd(&s_new, 1);
     }
   }
   // the block's timestamp maximum, then one atomic max per block, skipped
@@ -122,6 +124,7 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
       const uint32_t k = ts_order(mm);
       if (*ts_slot < k) atomicMax(ts_slot, k);
     }
+    if (s_new > 0) atomicAdd(ts_slot + 1, uint32_t(s_new));
   }
 }
 
@@ -129,11 +132,12 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
 // in tiles of 4 words per thread (16-byte loads and stores), and the batch's
 // max timestamp from the mark kernel's slot (-> the sampler's query time).
 __global__ __launch_bounds__(kScanBlock) void k_step_scan(
-    int64_t nwords, const uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
+    int64_t nwords, int64_t all_words, uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
     uint32_t *__restrict__ ts_slot, int64_t *__restrict__ cursor, const int64_t *__restrict__ batch_start,
-    float *__restrict__ ts_max, int64_t *__restrict__ t_query) {
+    float *__restrict__ ts_max, int64_t *__restrict__ t_query, int32_t *__restrict__ err) {
   __shared__ int32_t s_w[kScanBlock / sgl::kWave];
+  __shared__ int32_t s_stale;
   int32_t carry = 0;
   for (int64_t base = 0; base < nwords; base += 4 * kScanBlock) {
     const int64_t i = base + 4 * int64_t(threadIdx.x);
@@ -145,10 +149,21 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     if (i < nwords) *reinterpret_cast<int4 *>(prefix + i) = make_int4(run, run + c0, run + c0 + c1, run + c0 + c1 + c2);
     carry += total;
   }
+  // every set bit was set by this batch's mark kernel, unless a previous
+  // preparation's commit did not run: then its ranks could exceed the
+  // buffers; report it, clear the bitmap and give the batch no roots
+  if (threadIdx.x == 0) s_stale = carry != int32_t(ts_slot[1]);
+  __syncthreads();
+  const bool stale = s_stale != 0;
+  if (stale)
+    for (int64_t w = threadIdx.x; w < all_words; w += kScanBlock) bits[w] = 0u;
   if (threadIdx.x == 0) {
     const uint32_t k = *ts_slot;
     *ts_slot = 0u;
+    ts_slot[1] = 0u;
     const float mm = k != 0u ? ts_from_order(k) : -INFINITY;
+    if (stale && err != nullptr) atomicOr(err, SGL_DERR_STALE_NODE_BITS);
+    if (stale) carry = 0;
     *num_roots = carry;
     *num_roots64 = carry;
     *ts_max = mm;
@@ -160,7 +175,7 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
 }
 
 __global__ __launch_bounds__(kAggBlock) void k_step_index(
-    int64_t batch, int64_t num_nodes, const int64_t *__restrict__ src,
+    int64_t batch, int64_t num_nodes, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
     const float *__restrict__ ts, const int64_t *__restrict__ batch_start, const uint32_t *__restrict__ bits,
     const int32_t *__restrict__ prefix, const int64_t *__restrict__ t_query,
@@ -186,6 +201,17 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
     if (neg != nullptr) neg += off;
   }
   const int64_t tq = *t_query;
+  if (*num_roots == 0) {  // no valid event, or a stale bitmap (k_step_scan): no event has a root
+#pragma unroll
+    for (int j = 0; j < kAggPer; ++j) {
+      const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+      if (e >= batch) break;
+      ridx_src[e] = -1;
+      ridx_dst[e] = -1;
+      if (neg != nullptr) ridx_neg[e] = -1;
+    }
+    return;
+  }
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kAggPer; ++j) {
@@ -259,6 +285,28 @@ __host__ __device__ inline int64_t summary_words(int64_t num_nodes) {
   return ((bitmap_words(num_nodes) + 31) / 32 + 3) & ~int64_t(3);
 }
 
+// A batch preparation that found bits set before it marked its own: every
+// bitmap word cleared, no event mapped to a root, no counts (one workgroup
+// of nthr threads; the callers then report SGL_DERR_STALE_NODE_BITS and a
+// root count of 0).
+__device__ void stale_batch(int tid, int nthr, int64_t batch, int64_t cap, uint32_t *bits, int64_t words,
+                            int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
+                            unsigned long long *win_src, unsigned long long *win_dst, int32_t *cnt_src,
+                            int32_t *cnt_dst) {
+  for (int64_t w = tid; w < words; w += nthr) bits[w] = 0u;
+  for (int64_t e = tid; e < batch; e += nthr) {
+    ridx_src[e] = -1;
+    ridx_dst[e] = -1;
+    if (ridx_neg != nullptr) ridx_neg[e] = -1;
+  }
+  for (int64_t r = tid; r < cap; r += nthr) {
+    win_src[r] = 0ull;
+    win_dst[r] = 0ull;
+    cnt_src[r] = 0;
+    cnt_dst[r] = 0;
+  }
+}
+
 __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg, const float *__restrict__ ts,
@@ -292,6 +340,11 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     l_win[r] = 0ull;
     l_cnt[r] = 0;
   }
+  // bits this batch sets itself (a bit already set belongs to a previous
+  // batch whose commit did not run: checked against the root count below)
+  __shared__ int32_t s_new;
+  if (tid == 0) s_new = 0;
+  __syncthreads();
   // endpoints of events e = tid + c * kPrepBlock; mark their bits
   int64_t es[kPrepPer], ed[kPrepPer];
   bool ok[kPrepPer];
@@ -307,8 +360,10 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
       ok[c] = es[c] >= 0 && es[c] < num_nodes && ed[c] >= 0 && ed[c] < num_nodes;
       m = fmaxf(m, ts[e]);
       if (ok[c]) {
-        atomicOr(&bits[es[c] >> 5], 1u << (es[c] & 31));
-        atomicOr(&bits[ed[c] >> 5], 1u << (ed[c] & 31));
+        const uint32_t bs = 1u << (es[c] & 31), bd = 1u << (ed[c] & 31);
+        int fresh = (atomicOr(&bits[es[c] >> 5], bs) & bs) ? 0 : 1;
+        fresh += (atomicOr(&bits[ed[c] >> 5], bd) & bd) ? 0 : 1;
+        if (fresh) atomicAdd(&s_new, fresh);
         atomicOr(&summary[es[c] >> 10], 1u << ((es[c] >> 5) & 31));
         atomicOr(&summary[ed[c] >> 10], 1u << ((ed[c] >> 5) & 31));
       } else {
@@ -346,6 +401,26 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   }
   int32_t U;
   int32_t run = sgl::block_exclusive_scan<int32_t, kPrepBlock>(cnt_here, s_scan, U);
+  if (U != s_new) {
+    // the bitmap held bits before this batch (a previous preparation whose
+    // commit did not run): its ranks could exceed the buffers. Report it,
+    // clear both bitmaps and leave the batch without roots.
+    stale_batch(tid, kPrepBlock, batch, cap, bits, bitmap_words(num_nodes) + summary_words(num_nodes), ridx_src,
+                ridx_dst, neg != nullptr ? ridx_neg : nullptr, win_src, win_dst, cnt_src, cnt_dst);
+    if (tid == 0) {
+      if (err != nullptr) atomicOr(err, SGL_DERR_STALE_NODE_BITS);
+      *num_roots = 0;
+      *num_roots64 = 0;
+      *ts_max = mm;
+      *t_query = tq;
+      *any_edges = 0;
+      if (cursor != nullptr) {
+        *batch_start = off;
+        *cursor = off + batch;
+      }
+    }
+    return;
+  }
   for (int64_t sw = s0; sw < s1; ++sw) {
     uint32_t f = summary[sw];
     while (f != 0u) {
@@ -1186,12 +1261,13 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   k_step_mark<<<grid, kAggBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, ts, cursor, batch_start, node_bits,
                                            ts_slot, ws, wd, cnt_src, cnt_dst, any_edges, err_flag);
   SGL_CHECK_LAUNCH();
-  k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, node_bits, word_prefix, num_roots, num_roots64, batch, ts_slot,
-                                            cursor, batch_start, ts_max, t_query);
+  k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, nwords + summary_words(num_nodes), node_bits, word_prefix,
+                                            num_roots, num_roots64, batch, ts_slot, cursor, batch_start, ts_max,
+                                            t_query, err_flag);
   SGL_CHECK_LAUNCH();
   if (batch > 0) {
     k_step_index<<<grid, kAggBlock, 0, stream>>>(
-        batch, num_nodes, src, dst, neg, ts, cursor != nullptr ? batch_start : nullptr, node_bits, word_prefix,
+        batch, num_nodes, num_roots, src, dst, neg, ts, cursor != nullptr ? batch_start : nullptr, node_bits, word_prefix,
         t_query, roots, root_ts,
         ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
     SGL_CHECK_LAUNCH();

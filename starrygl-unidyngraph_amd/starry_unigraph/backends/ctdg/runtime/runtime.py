@@ -183,13 +183,16 @@ class CTDGOnlineRuntime:
     def check_sync(self) -> None:
         """Raise if a cross-stream wait of a planned step gave up (after about
         two seconds) instead of seeing its predecessor finish (results from
-        then on are unordered), or if the edge predictor met a gradient or loss
+        then on are unordered), if a batch preparation flagged its input (a
+        node id out of range, a node bitmap left set), or if the edge predictor met a gradient or loss
         term outside the range of its fixed-point sums (clamped: the sums since
         the last check are wrong). Synchronizes the device."""
         if self._front_stream is not None and int(self._sync[48].item()):
             raise RuntimeError("sgl_plan_run: a cross-stream wait timed out; the steps since the last check "
                                "ran out of order")
         self._neg_err.raise_if_set("negative sampling (a draw outside the dst pool)")
+        for st in self.steps:
+            st.buf.err.raise_if_set("sgl_batch_prepare")
         for st in self.steps:
             flag = st.buf.pred_done[_capi.SGL_DONE_RANGE_WORD]
             if int(flag.item()):

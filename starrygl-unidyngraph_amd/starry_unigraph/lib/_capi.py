@@ -21,6 +21,7 @@ ABI_VERSION = 16
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
+SGL_DERR_STALE_NODE_BITS = 4
 SGL_FIXED_SHIFT = 40    # fractional bits of the predictor's int64 gradient accumulators
 SGL_DONE_WORDS = 1088   # int32 words of sgl_predictor's completion counter
 SGL_DONE_RANGE_WORD = 32   # its word that flags a value outside the fixed-point range
@@ -277,6 +278,9 @@ class ErrorFlag:
                 parts.append("node id out of range [0, num_nodes)")
             if v & SGL_DERR_EID_RANGE:
                 parts.append("edge id out of range [0, 2^31)")
+            if v & SGL_DERR_STALE_NODE_BITS:
+                parts.append("node bitmap not clear at the batch preparation (a previous step's memory commit "
+                             "did not run); the batch was given no roots")
             self.reset()
             raise RuntimeError(f"{what}: " + "; ".join(parts))
 

@@ -160,7 +160,8 @@ def test_header_constants_match_binding(tmp_path):
     error bits, fixed-point scale, completion-counter size and range-flag
     word) are the header's."""
     from starry_unigraph.lib import _capi
-    names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
+    names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_DERR_STALE_NODE_BITS",
+             "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
              "SGL_DONE_RANGE_WORD", "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES"]
     src = tmp_path / "consts.cpp"
     src.write_text('#include <cstdio>\n#include "starrygl_mi355x.h"\nint main() {\n'
@@ -169,7 +170,8 @@ def test_header_constants_match_binding(tmp_path):
     subprocess.run(["g++", "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
                     "-I" + os.path.join(REPO, "include"), str(src), "-o", str(exe)], check=True)
     got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
-    want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_FIXED_SHIFT,
+    want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_DERR_STALE_NODE_BITS,
+            _capi.SGL_FIXED_SHIFT,
             _capi.SGL_DONE_WORDS, _capi.SGL_DONE_RANGE_WORD, _capi.SGL_OP_MAX_ARGS,
             _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES]
     assert got == want

@@ -161,6 +161,53 @@ def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew):
         st.node_bits.zero_()   # as the commit would
 
 
+@pytest.mark.parametrize("B1,B2", [(4096, 4096), (4096, 600)])
+def test_batch_prepare_reports_a_stale_bitmap(gpu, B1, B2):
+    """A preparation after one whose commit did not run (its node bits still
+    set; the multi-workgroup path leaves them for the commit) reports
+    SGL_DERR_STALE_NODE_BITS, gives the batch no roots (every root index -1,
+    no counts) and leaves the bitmap clear, so that the next preparation is
+    exact again. The batches draw from the same 700 nodes, so even a
+    preparation that missed the stale bits would rank within its buffers."""
+    from starry_unigraph.lib import _capi
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    rng = np.random.default_rng(B1 + B2)
+    N = 5000
+    nodes = rng.choice(N, 700, replace=False)
+    st = NodeState(N, 8, 2, 4, gpu)
+    step = DeviceStep(st, ConvDims(8, 4, 8, 2, 5), max(B1, B2))
+    T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
+
+    def batch(B):
+        src, dst = rng.choice(nodes, B), rng.choice(nodes, B)
+        ts = np.sort(rng.integers(0, 50, B)).astype(np.float32)
+        return src, dst, ts, rng.choice(nodes, B)
+
+    b = step.buf
+    b.err.reset()
+    src, dst, ts, neg = batch(B1)
+    step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))   # no commit follows
+    assert int(b.err.t.item()) == 0
+    assert int(torch.count_nonzero(st.node_bits).item()) > 0
+    src, dst, ts, neg = batch(B2)
+    step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
+    assert int(b.err.t.item()) == _capi.SGL_DERR_STALE_NODE_BITS
+    assert int(b.num_roots.item()) == 0
+    for r in (b.ridx_src, b.ridx_dst, b.ridx_neg):
+        assert bool((r[:B2] == -1).all())
+    assert int(b.cnt_src[:2 * B2].abs().sum().item()) == 0 and int(b.cnt_dst[:2 * B2].abs().sum().item()) == 0
+    assert int(torch.count_nonzero(st.node_bits).item()) == 0
+    with pytest.raises(RuntimeError, match="node bitmap not clear"):
+        b.err.raise_if_set("sgl_batch_prepare")
+    src, dst, ts, neg = batch(B2)
+    step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
+    roots = np.unique(np.concatenate([src, dst]))
+    assert int(b.err.t.item()) == 0
+    assert int(b.num_roots.item()) == len(roots)
+    np.testing.assert_array_equal(b.roots[:len(roots)].cpu().numpy(), roots)
+    np.testing.assert_array_equal(b.ridx_src[:B2].cpu().numpy(), np.searchsorted(roots, src))
+
+
 def _state_pair(gpu, N, D, K, F, seed):
     from starry_unigraph.native.step import NodeState
     torch.manual_seed(seed)
