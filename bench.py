@@ -624,6 +624,16 @@ def run_tgn(args, wl: dict) -> dict:
     rt.check_sync()
     log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
+    # every timed step's (loss, AP, AUC, "mrr"), computed on the device at the end
+    # of its back part (sgl_link_metrics) inside the timed region; read once here
+    met = rt.metrics_of_last_steps(args.steps) if rt.device_metrics else None
+    step_metrics = None
+    if met is not None and met.shape[0] == args.steps:
+        mean = met.mean(0).tolist()
+        step_metrics = {"steps": int(met.shape[0]), "mean_loss": mean[0], "mean_ap": mean[1], "mean_auc": mean[2],
+                        "mean_mrr": mean[3], "last": met[-1].tolist(),
+                        "computed": "per step on the device inside the timed region (sgl_link_metrics: "
+                                    "runtime.py:202-214's sklearn AP/AUC and pairwise mrr), no host sync"}
     dom_ms = [a.elapsed_time(b) for _, a, b in timer]
     # the step's loss is a view of a reused step buffer: read the last one
     final_loss = float(out["loss"].item()) if out is not None else float("nan")
@@ -678,6 +688,7 @@ def run_tgn(args, wl: dict) -> dict:
     res = {
         "value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / args.steps,
         "final_train_loss": final_loss,
+        "step_metrics": step_metrics,
         "roofline": {"bound": bound, "kernel": dom, "achieved": ach, "peak": peak, "unit": unit,
                      "frac": ach / peak, "traffic": HBM_TRAFFIC.get(tkey),
                      "traffic_source": TRAFFIC_SOURCE.get(wl["config"]) if tkey in HBM_TRAFFIC
@@ -835,7 +846,7 @@ def main() -> None:
                                      "dropout 0"),
                         "global_batch": wl["B"], "parallelism": "single GPU"},
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
-                step_shape=r["step_shape"], final_train_loss=r["final_train_loss"])
+                step_shape=r["step_shape"], final_train_loss=r["final_train_loss"], step_metrics=r["step_metrics"])
     line["hbm_copy"] = copy_bandwidth()
     if args.workload == "tgn-large" and not args.no_sampler:
         line["sampler"] = run_sampler(20, 3, cases=True, cpu=not args.no_cpu)

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 16
+#define SGL_ABI_VERSION 17
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -515,6 +515,30 @@ int sgl_predictor(int64_t batch, int32_t D, int64_t capacity, int32_t train,
                   float *g_wo, float *g_bo, int64_t *acc_out, int32_t *done,
                   int64_t y_pass_stride, int64_t *acc_neg,
                   const sgl_bf16_weights *bw, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * (9) Link-prediction metrics of a step on the device.
+ * Replaces CTDGOnlineRuntime._metric_dict (backends/ctdg/runtime/runtime.py:
+ * 202-214; scikit-learn on the host after a device-to-host copy): from the
+ * n_pos positive and n_neg negative logits, scores sigmoid(logit) in float32
+ * with labels 1 / 0, "ap" = average_precision_score, "auc" = roc_auc_score,
+ * "mrr" = mean over pairs of [pos score > neg score] (float32, as the
+ * reference's float mean). One launch, no host synchronisation.
+ * Writes (loss, ap, auc, mrr) as doubles to out[4] (may be NULL) and, with a
+ * ring, to ring[4 * (*seq % ring_slots)], then increments *seq (a device
+ * word the caller zeroes once): consecutive steps' metrics in stream order.
+ * loss may be NULL (NaN is written). n_pos + n_neg <= SGL_LINK_METRICS_MAX_SCORES;
+ * with no positive or no negative score every metric is NaN.
+ * work: sgl_link_metrics_work_doubles(n_pos) doubles of per-workgroup
+ * partial sums; done: a device word that is 0 before the first call (each
+ * call leaves it 0). Calls sharing work / done must be stream-ordered.
+ * ------------------------------------------------------------------------- */
+#define SGL_LINK_METRICS_MAX_SCORES 8192
+int64_t sgl_link_metrics_work_doubles(int32_t n_pos);
+int sgl_link_metrics(int32_t n_pos, int32_t n_neg, const float *pos_logits,
+                     const float *neg_logits, const float *loss, uint64_t *seq,
+                     double *ring, int32_t ring_slots, double *out,
+                     double *work, uint32_t *done, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the

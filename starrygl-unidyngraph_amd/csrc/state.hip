@@ -345,20 +345,28 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   __shared__ int32_t s_new;
   if (tid == 0) s_new = 0;
   __syncthreads();
-  // endpoints of events e = tid + c * kPrepBlock; mark their bits
-  int64_t es[kPrepPer], ed[kPrepPer];
+  // endpoints, times and negatives of events e = tid + c * kPrepBlock (one
+  // round of loads); mark the endpoints' bits
+  int64_t es[kPrepPer], ed[kPrepPer], en[kPrepPer];
+  float te[kPrepPer];
   bool ok[kPrepPer];
   float m = -INFINITY;
 #pragma unroll
   for (int c = 0; c < kPrepPer; ++c) {
     const int e = tid + c * kPrepBlock;
+    const bool live = e < batch;
+    es[c] = live ? src[e] : 0;
+    ed[c] = live ? dst[e] : 0;
+    te[c] = live ? ts[e] : 0.f;
+    en[c] = live && neg != nullptr ? neg[e] : -1;
+  }
+#pragma unroll
+  for (int c = 0; c < kPrepPer; ++c) {
+    const int e = tid + c * kPrepBlock;
     ok[c] = false;
-    es[c] = ed[c] = 0;
     if (e < batch) {
-      es[c] = src[e];
-      ed[c] = dst[e];
       ok[c] = es[c] >= 0 && es[c] < num_nodes && ed[c] >= 0 && ed[c] < num_nodes;
-      m = fmaxf(m, ts[e]);
+      m = fmaxf(m, te[c]);
       if (ok[c]) {
         const uint32_t bs = 1u << (es[c] & 31), bd = 1u << (ed[c] & 31);
         int fresh = (atomicOr(&bits[es[c] >> 5], bs) & bs) ? 0 : 1;
@@ -433,32 +441,45 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   }
   __syncthreads();
 
-  // ranks, roots, counts and last writers
+  // ranks, roots, counts and last writers; the bitmap and prefix words of
+  // every endpoint and negative are loaded in one round
+  uint32_t wb[kPrepPer][3];
+  int32_t wp[kPrepPer][3];
 #pragma unroll
   for (int c = 0; c < kPrepPer; ++c) {
     const int e = tid + c * kPrepBlock;
-    if (e >= batch || !ok[c]) continue;
-    const unsigned long long wkey =
-        (static_cast<unsigned long long>(ts_order(ts[e])) << 32) | static_cast<unsigned long long>(e);
+    const bool live = e < batch;
+    const int64_t nn = en[c] >= 0 && en[c] < num_nodes ? en[c] : 0;
+    const int64_t w[3] = {live && ok[c] ? es[c] >> 5 : 0, live && ok[c] ? ed[c] >> 5 : 0, live ? nn >> 5 : 0};
 #pragma unroll
-    for (int role = 0; role < 2; ++role) {
-      const int64_t n = role ? ed[c] : es[c];
-      const int32_t rank = node_rank(bits, prefix, n);
-      (role ? ridx_dst : ridx_src)[e] = rank;
-      roots[rank] = n;
-      root_ts[rank] = tq;
-      atomicAdd(&l_cnt[role * cap + rank], 1);
-      atomicMax(&l_win[role * cap + rank], wkey);
+    for (int r = 0; r < 3; ++r) {
+      wb[c][r] = bits[w[r]];
+      wp[c][r] = prefix[w[r]];
     }
   }
-  if (neg != nullptr) {
 #pragma unroll
-    for (int c = 0; c < kPrepPer; ++c) {
-      const int e = tid + c * kPrepBlock;
-      if (e >= batch) continue;
-      const int64_t n = neg[e];
+  for (int c = 0; c < kPrepPer; ++c) {
+    const int e = tid + c * kPrepBlock;
+    if (e >= batch) continue;
+    if (ok[c]) {
+      const unsigned long long wkey =
+          (static_cast<unsigned long long>(ts_order(te[c])) << 32) | static_cast<unsigned long long>(e);
+#pragma unroll
+      for (int role = 0; role < 2; ++role) {
+        const int64_t n = role ? ed[c] : es[c];
+        const int32_t rank = wp[c][role] + __popc(wb[c][role] & ((1u << (n & 31)) - 1u));
+        (role ? ridx_dst : ridx_src)[e] = rank;
+        roots[rank] = n;
+        root_ts[rank] = tq;
+        atomicAdd(&l_cnt[role * cap + rank], 1);
+        atomicMax(&l_win[role * cap + rank], wkey);
+      }
+    }
+    if (neg != nullptr) {
+      const int64_t n = en[c];
       int32_t rn = -1;
-      if (n >= 0 && n < num_nodes && ((bits[n >> 5] >> (n & 31)) & 1u)) rn = node_rank(bits, prefix, n);
+      if (n >= 0 && n < num_nodes && ((wb[c][2] >> (n & 31)) & 1u))
+        rn = wp[c][2] + __popc(wb[c][2] & ((1u << (n & 31)) - 1u));
       ridx_neg[e] = rn;
     }
   }

@@ -40,11 +40,15 @@ from .sampler import NativeTemporalSampler
 
 @dataclass
 class StepTensors:
-    """Device results of one step (no host sync)."""
+    """Device results of one step (no host sync). ``metrics``: the step's
+    row of the device metrics ring, (loss, AP, AUC, "mrr") as float64 (None
+    without device metrics; final once the step is done, overwritten
+    metric_slots steps later)."""
     loss: torch.Tensor
     pos_logits: torch.Tensor
     neg_logits: torch.Tensor
     batch_size: int
+    metrics: torch.Tensor | None = None
 
 
 class CTDGOnlineRuntime:
@@ -129,16 +133,45 @@ class CTDGOnlineRuntime:
         self._state_writes = memory.state.writes
         # training steps so far (the dropout masks' step; sgl_adam_coef advances it)
         self._rng_counter = torch.zeros(1, dtype=torch.int64, device=self.device)
+        # every step's (loss, AP, AUC, "mrr") (runtime.py:202-214, 314-328) computed
+        # on the device (sgl_link_metrics) into a ring of metric_slots rows in
+        # step order; _metrics_issued counts the steps submitted (the host's
+        # copy of the ring's device counter). Eager steps and steps whose
+        # results the host collects compute them at the end of their back part;
+        # in the asynchronous planned mode a step's metrics are computed by the
+        # front part of the next step on the same buffers (off the critical
+        # back stream; the logits stay until that step's back part), and
+        # _metrics_pending[q] holds the batch size of such a step on buffer set
+        # q (_metrics_order: the sets in step order), flushed whenever the
+        # ring is read
+        self.device_metrics = True
+        self._metrics_pending: list[int] = [0, 0]
+        self._metrics_order: list[int] = []
+        self.metric_slots = 8192
+        self.metrics_ring = torch.full((self.metric_slots, 4), float("nan"), dtype=torch.float64,
+                                       device=self.device)
+        self._metrics_seq = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self._metrics_issued = 0
+        self._metric_rows = self.metrics_ring.unbind(0)   # a view per slot (no tensor op per step)
+        # the kernel's per-workgroup partial sums and completion word (shared
+        # by the step buffer sets: the back parts are stream-ordered)
+        self._metrics_work = (
+            torch.zeros(int(_capi.lib().sgl_link_metrics_work_doubles(_capi.SGL_LINK_METRICS_MAX_SCORES // 2)),
+                        dtype=torch.float64, device=self.device),
+            torch.zeros(1, dtype=torch.int32, device=self.device))
         # bf16 copies of the attention / predictor weights when the conv runs
         # its products in bf16 (the fused update keeps them current; dirty:
         # rebuild from the parameters before the next step)
         self._bf16: Bf16Shadow | None = None
         self._bf16_dirty = True
         self._bf16_ver: tuple = ()
+        self._back_metrics = False
 
     def _make_steps(self, max_batch: int) -> None:
         # every hop of the sampler (history layers, sampler.py:76-90) is
         # sampled; the attention reads hop 0 (runtime.py:164-167)
+        if getattr(self, "steps", None):
+            self._flush_metrics()   # their logits are about to be dropped
         hops = [int(f) for f in self.sampler.fanout[:max(1, int(self.sampler.history))]]
         if len(hops) < int(self.sampler.history):
             raise RuntimeError(f"ParallelSampler: num_layers {self.sampler.history} > len(fanouts) {len(hops)}")
@@ -361,9 +394,12 @@ class CTDGOnlineRuntime:
             self._bf16_dirty = True
         for st in self.steps:
             st.bf16 = self._bf16
-        ws = (conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight, core.src_fc.weight,
-              core.dst_fc.weight)
-        ver = tuple((w.data_ptr(), w._version) for w in ws)
+        c = self.__dict__.get("_shadowed_of")
+        if c is None or c[0] is not core:   # nn.Module attribute lookups cost microseconds: once per model
+            c = self._shadowed_of = (core, (conv.w_q.weight, conv.w_k.weight, conv.w_v.weight, conv.w_out.weight,
+                                            core.src_fc.weight, core.dst_fc.weight))
+        ws = c[1]
+        ver = tuple([(w.data_ptr(), w._version) for w in ws])
         if self._bf16_dirty or ver != self._bf16_ver:
             self._bf16.refresh(*ws)
             self._bf16_dirty = False
@@ -382,7 +418,13 @@ class CTDGOnlineRuntime:
         buf, off = self._negatives_at(batch)
         b = step.buf
         start = batch.start
+        with_metrics = self.device_metrics and 0 < 2 * n <= _capi.SGL_LINK_METRICS_MAX_SCORES
         planned = self.use_plans and n == b.max_batch and start >= 0 and step.timer is None
+        # metrics at the end of the back part, or deferred to the next front part on these buffers
+        defer = planned and not self.collect_results
+        if not defer:
+            self._flush_metrics()   # ring rows in step order
+        self._back_metrics = with_metrics and not defer
         if not planned:
             if self._front_stream is not None:   # negatives drawn on the front stream
                 torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
@@ -405,10 +447,11 @@ class CTDGOnlineRuntime:
             # between steps, so its steps start after everything queued before
             if self.collect_results or self._state_writes != self.memory.state.writes:
                 self.fence()
-            key = ("test" if split == "predict" else split, bool(train), q)
+            front_metrics = self._metrics_pending[q] if defer else 0
+            key = ("test" if split == "predict" else split, bool(train), q, self._back_metrics, front_metrics)
             plan = self._plans.get(key)
             if plan is None:
-                plan = self._record(step, split, train, n)
+                plan = self._record(step, split, train, n, front_metrics)
                 self._plans[key] = plan
                 self.fence()   # state built on first use (a split's sampler graph) is queued here
             front = self._pipeline_streams()
@@ -426,13 +469,23 @@ class CTDGOnlineRuntime:
             # predecessor read; its commit follows this step's backward
             self._need_back, self._prev_seq = self._prev_seq, seq
             self._seq = seq
+            if defer:
+                if front_metrics:
+                    self._metrics_order.remove(q)
+                self._metrics_pending[q] = n if with_metrics else 0
+                if with_metrics:
+                    self._metrics_order.append(q)
         views = self._views.get((n, q))
         if views is None or views[0] is not b:
             views = (b, b.loss[0], b.pos[:n], b.neg[:n])
             self._views[(n, q)] = views
-        return StepTensors(views[1], views[2], views[3], n)
+        met = None
+        if with_metrics:
+            met = self._metric_rows[self._metrics_issued % self.metric_slots]
+            self._metrics_issued += 1
+        return StepTensors(views[1], views[2], views[3], n, met)
 
-    def _record(self, step: DeviceStep, split: str, train: bool, n: int) -> tuple:
+    def _record(self, step: DeviceStep, split: str, train: bool, n: int, front_metrics: int = 0) -> tuple:
         """Record a full step on ``step``'s buffers as a launch plan: (ops,
         #front, #back, entry point names, recorded calls). The front part is
         the batch preparation, sampling, GRU, memory commit, edge rows and (in
@@ -445,7 +498,7 @@ class CTDGOnlineRuntime:
             self._param_update(step)   # any rebuild or host-side sync happens outside the recording
         with _capi.record() as front:
             self._front_body(step, split, n, d["src"], d["dst"], self._neg_all, d["ts"], d["edge_feat"],
-                             self._cursor)
+                             self._cursor, front_metrics)
             self._commit_body(step, train)
         with _capi.record() as back:
             self._back_body(step, train, n)
@@ -467,12 +520,17 @@ class CTDGOnlineRuntime:
             torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
         self._plans.clear()
 
-    def _front_body(self, step: DeviceStep, split: str, n: int, src, dst, neg, ts, ef, cursor) -> None:
+    def _front_body(self, step: DeviceStep, split: str, n: int, src, dst, neg, ts, ef, cursor,
+                    prev_metrics: int = 0) -> None:
         """Batch preparation, sampling and the GRU memory update of one step.
         With ``cursor`` (device int64 [1]) the event and negative arrays are
         the whole stream and the batch starts at the cursor (which the step
-        advances)."""
+        advances). ``prev_metrics`` > 0: first the metrics of the previous
+        step on these buffers (that many events), whose back part the
+        preparation's wait has seen finish."""
         step.prepare(src, dst, neg, ts, n=n, cursor=cursor)
+        if prev_metrics:
+            step.link_metrics(prev_metrics, self._metrics_seq, self.metrics_ring, self._metrics_work)
         step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
         if self._gru is not None:
             step.update_memory(self._gru, src, dst, ef, ts, from_cursor=cursor is not None)
@@ -509,6 +567,7 @@ class CTDGOnlineRuntime:
             if train:
                 step.proj_backward(tp, (pdet[0], pdet[2]))
                 upd.run()
+            self._metrics_op(step, n)
             return
         cparams = [p.detach() for p in conv.kernel_params()]
         if train:
@@ -527,6 +586,41 @@ class CTDGOnlineRuntime:
         if train:
             step.conv_backward_kernel(cparams, efeat_all, pred_w=(pdet[0], pdet[2]), drop=drop)
             upd.run()
+        self._metrics_op(step, n)
+
+    def _metrics_op(self, step: DeviceStep, n: int) -> None:
+        """The step's metrics into the next ring slot as the last op of its
+        back part (the loss and logits are final there), unless they are
+        deferred to the next front part on these buffers (_forward decides)."""
+        if self._back_metrics:
+            step.link_metrics(n, self._metrics_seq, self.metrics_ring, self._metrics_work)
+
+    def _flush_metrics(self) -> None:
+        """Compute the deferred metrics of planned steps now, on the current
+        stream in step order (their logits are intact until the next back
+        part on their buffers, which is issued after this)."""
+        if not self._metrics_order:
+            return
+        if self._front_stream is not None:
+            torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
+        for q in self._metrics_order:
+            self.steps[q].link_metrics(self._metrics_pending[q], self._metrics_seq, self.metrics_ring,
+                                       self._metrics_work)
+            self._metrics_pending[q] = 0
+        self._metrics_order.clear()
+
+    def metrics_of_last_steps(self, count: int) -> torch.Tensor:
+        """(loss, AP, AUC, "mrr") of the last ``count`` steps submitted, one row
+        each in step order, from the device ring (float64 [count, 4]; rows of
+        steps without device metrics are NaN). Synchronizes the device."""
+        self._flush_metrics()
+        count = min(int(count), self._metrics_issued, self.metric_slots)
+        if self._front_stream is not None:
+            torch.cuda.current_stream(self.device).wait_stream(self._front_stream)
+        torch.cuda.synchronize(self.device)
+        end = int(self._metrics_seq.item())
+        idx = torch.arange(end - count, end, device=self.device) % self.metric_slots
+        return self.metrics_ring[idx].cpu()
 
     def _param_update(self, step: DeviceStep) -> StepParamUpdate:
         """The fused weight-gradient + Adam launch for a step's buffers and the
@@ -549,10 +643,15 @@ class CTDGOnlineRuntime:
             self._updates[id(step)] = upd
         return upd
 
-    def _metric_dict(self, pos_logits: torch.Tensor, neg_logits: torch.Tensor) -> dict[str, float]:
-        """runtime.py:202-214 (AP, AUC and the pairwise "mrr"), computed on
-        the logits' device (metrics.link_metrics)."""
-        return link_metrics(pos_logits, neg_logits)
+    def _metric_dict(self, st: StepTensors) -> dict[str, float]:
+        """runtime.py:202-214 (AP, AUC and the pairwise "mrr"): the step's row
+        of the device metrics ring (sgl_link_metrics), else computed on the
+        logits' device (metrics.link_metrics)."""
+        if st.metrics is not None:
+            self._flush_metrics()
+            _, ap, auc, mrr = st.metrics.tolist()
+            return {"ap": ap, "auc": auc, "mrr": mrr}
+        return link_metrics(st.pos_logits, st.neg_logits)
 
     def _sample_meta(self, n: int) -> dict[str, int]:
         """CTDGSampleOutput.describe() (sampler.py:27-33, sampler.py:119-120):
@@ -588,12 +687,12 @@ class CTDGOnlineRuntime:
         st = self._forward(batch, batch.split, train=True)
         if not self.collect_results:
             return {"loss": st.loss, "pos_logits": st.pos_logits, "neg_logits": st.neg_logits,
-                    "meta": {"split": batch.split, "batch_size": st.batch_size}}
+                    "metrics": st.metrics, "meta": {"split": batch.split, "batch_size": st.batch_size}}
         step_ms = (time.perf_counter() - t0) * 1000.0
         return {"loss": float(st.loss.item()), "predictions": torch.sigmoid(st.pos_logits).cpu().tolist(),
                 "targets": [1] * batch.size,
                 "meta": {"split": batch.split, "batch_size": batch.size, "sample": self._sample_meta(batch.size),
-                         "metrics": self._metric_dict(st.pos_logits, st.neg_logits),
+                         "metrics": self._metric_dict(st),
                          "memory": self.memory.describe(), "sync_wait_ms": 0.0, "sync_submit_ms": 0.0,
                          "step_ms": step_ms}}
 
@@ -607,11 +706,11 @@ class CTDGOnlineRuntime:
             st = self._forward(batch, split, train=False)
         if not self.collect_results:
             return {"loss": st.loss, "pos_logits": st.pos_logits, "neg_logits": st.neg_logits,
-                    "meta": {"split": split, "batch_size": st.batch_size}}
+                    "metrics": st.metrics, "meta": {"split": split, "batch_size": st.batch_size}}
         return {"loss": float(st.loss.item()), "predictions": torch.sigmoid(st.pos_logits).cpu().tolist(),
                 "targets": [1] * batch.size,
                 "meta": {"split": split, "batch_size": batch.size,
-                         "metrics": self._metric_dict(st.pos_logits, st.neg_logits),
+                         "metrics": self._metric_dict(st),
                          "memory": self.memory.describe()}}
 
     def predict_step(self, batch: CTDGDataBatch) -> dict[str, Any]:

@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -26,6 +26,7 @@ SGL_FIXED_SHIFT = 40    # fractional bits of the predictor's int64 gradient accu
 SGL_DONE_WORDS = 1088   # int32 words of sgl_predictor's completion counter
 SGL_DONE_RANGE_WORD = 32   # its word that flags a value outside the fixed-point range
 SGL_COMPACT_NOALLOC_MAX_QUERIES = 1 << 24   # sgl_recent_compact_noalloc's limit
+SGL_LINK_METRICS_MAX_SCORES = 8192   # sgl_link_metrics' limit on positive + negative scores
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -72,6 +73,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_dropout_masks": (ctypes.c_int, [_i64, _i32, _i32, _i32, ctypes.c_float, ctypes.c_float, ctypes.c_uint64,
                                          _vp, _i32, _vp, _vp, _vp]),
     "sgl_predictor": (ctypes.c_int, [_i64, _i32, _i64, _i32] + [_vp] * 20 + [_i64, _vp, _vp, _vp]),
+    "sgl_link_metrics_work_doubles": (_i64, [_i32]),
+    "sgl_link_metrics": (ctypes.c_int, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "sgl_adam_step": (ctypes.c_int, [_i64] + [_vp] * 6 + [ctypes.c_float] * 5 + [_vp]),
     "sgl_adam_advance": (ctypes.c_int, [_vp, _vp, _vp]),
     "sgl_time_next_launch": (ctypes.c_int, [_vp, _vp]),

@@ -473,6 +473,20 @@ class DeviceStep:
             P(g[0]), P(g[1]), P(b.acc_out), P(b.pred_done), ys, acc_neg, self._bw(), self._s()), "sgl_predictor"))
         return b.pos[:n], b.neg[:n], b.loss
 
+    def link_metrics(self, n: int, seq: torch.Tensor | None, ring: torch.Tensor | None,
+                     work: tuple[torch.Tensor, torch.Tensor], out: torch.Tensor | None = None) -> None:
+        """The step's (loss, AP, AUC, "mrr") from its n positive and n
+        negative logits on the device (sgl_link_metrics): into ``out``
+        (float64 [4]) and / or the next slot of ``ring`` (float64 [R, 4],
+        slot *seq % R; ``seq`` device int64 [1], incremented). ``work``: the
+        partial sums (float64, sgl_link_metrics_work_doubles(n)) and the
+        done word (int32 [1], zero)."""
+        b, P = self.buf, _capi.ptr
+        R = int(ring.shape[0]) if ring is not None else 0
+        self._call("link_metrics", lambda: _capi.check(_capi.call(
+            "sgl_link_metrics", n, n, P(b.pos), P(b.neg), P(b.loss), P(seq), P(ring), R, P(out), P(work[0]),
+            P(work[1]), self._s()), "sgl_link_metrics"))
+
     def conv_backward_kernel(self, params: list[torch.Tensor], efeat_all: torch.Tensor,
                              gy: torch.Tensor | None = None, pred_w: tuple | None = None, drop=None) -> None:
         """sgl_conv_backward only: per-root gradient rows and per-tile partials

@@ -162,7 +162,8 @@ def test_header_constants_match_binding(tmp_path):
     from starry_unigraph.lib import _capi
     names = ["SGL_ABI_VERSION", "SGL_DERR_NODE_RANGE", "SGL_DERR_EID_RANGE", "SGL_DERR_STALE_NODE_BITS",
              "SGL_FIXED_SHIFT", "SGL_DONE_WORDS",
-             "SGL_DONE_RANGE_WORD", "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES"]
+             "SGL_DONE_RANGE_WORD", "SGL_OP_MAX_ARGS", "SGL_COMPACT_NOALLOC_MAX_QUERIES",
+             "SGL_LINK_METRICS_MAX_SCORES"]
     src = tmp_path / "consts.cpp"
     src.write_text('#include <cstdio>\n#include "starrygl_mi355x.h"\nint main() {\n'
                    + "".join(f'  printf("%d ", int({n}));\n' for n in names) + "  return 0;\n}\n")
@@ -173,7 +174,7 @@ def test_header_constants_match_binding(tmp_path):
     want = [_capi.ABI_VERSION, _capi.SGL_DERR_NODE_RANGE, _capi.SGL_DERR_EID_RANGE, _capi.SGL_DERR_STALE_NODE_BITS,
             _capi.SGL_FIXED_SHIFT,
             _capi.SGL_DONE_WORDS, _capi.SGL_DONE_RANGE_WORD, _capi.SGL_OP_MAX_ARGS,
-            _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES]
+            _capi.SGL_COMPACT_NOALLOC_MAX_QUERIES, _capi.SGL_LINK_METRICS_MAX_SCORES]
     assert got == want
 
 

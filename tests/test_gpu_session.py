@@ -125,6 +125,63 @@ def test_device_metrics_match_sklearn(gpu):
         assert abs(got[k] - want[k]) <= tol, (k, got[k], want[k])
 
 
+@pytest.mark.parametrize("P,N,ties", [(600, 600, "dup"), (4000, 4000, "dup"), (4000, 4000, "sat"), (3, 5000, "dup"),
+                                       (1000, 1, "none"), (1, 1, "none"), (600, 600, "all")])
+def test_link_metrics_kernel_matches_sklearn(gpu, P, N, ties):
+    """sgl_link_metrics (per positive, counts of the scores below, equal and
+    above it over slices of the staged scores; a fixed-order sum of the
+    workgroups' partials) against scikit-learn's metrics
+    (runtime.py:202-214): AP and AUC to 1e-9, "mrr" to 1e-6; with tied
+    scores (logits on a coarse grid, as the non-root negatives' shared zero
+    embedding ties them; saturated logits whose sigmoids are all 1; every
+    score equal), unbalanced sizes and single elements. The
+    loss is copied through, and the ring takes consecutive calls in order."""
+    from starry_unigraph.lib import _capi
+    rng = np.random.default_rng(P + N)
+    if ties == "none":
+        pos = torch.from_numpy(rng.normal(0.2, 1.5, P).astype(np.float32))
+        neg = torch.from_numpy(rng.normal(-0.2, 1.5, N).astype(np.float32))
+    else:
+        # logits on a 1/64 grid: many exact ties, and distinct logits' sigmoids
+        # far apart (a sigmoid that differs from the host's in the last bit
+        # cannot tie or untie two of them)
+        pos = torch.from_numpy((rng.integers(-180, 220, P) / 64).astype(np.float32))
+        neg = torch.from_numpy((rng.integers(-220, 180, N) / 64).astype(np.float32))
+    if ties == "sat":   # sigmoid(x) rounds to exactly 1 for x >= 20
+        pos[: P // 4] = torch.from_numpy(rng.uniform(20.0, 40.0, P // 4).astype(np.float32))
+        neg[: N // 8] = torch.from_numpy(rng.uniform(20.0, 40.0, N // 8).astype(np.float32))
+    elif ties == "all":
+        pos.fill_(0.25)
+        neg.fill_(0.25)
+    loss = torch.tensor([1.25], device=gpu)
+    out = torch.zeros(4, dtype=torch.float64, device=gpu)
+    ring = torch.full((3, 4), -1.0, dtype=torch.float64, device=gpu)
+    seq = torch.zeros(1, dtype=torch.int64, device=gpu)
+    P_ = _capi.ptr
+    pg, ng = pos.to(gpu), neg.to(gpu)
+    work = torch.zeros(int(_capi.lib().sgl_link_metrics_work_doubles(P)), dtype=torch.float64, device=gpu)
+    done = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for _ in range(4):   # ring slots 0, 1, 2, 0
+        _capi.check(_capi.lib().sgl_link_metrics(P, N, P_(pg), P_(ng), P_(loss), P_(seq), P_(ring), 3, P_(out),
+                                                  P_(work), P_(done), _capi.stream_of(gpu)), "sgl_link_metrics")
+    torch.cuda.synchronize()
+    # the reference's scores: torch.sigmoid of the float32 logits on the device
+    # (runtime.py:203-204; torch's CPU sigmoid can give one logit two values,
+    # its vector and scalar paths rounding differently, which unties scores)
+    from sklearn.metrics import average_precision_score, roc_auc_score
+    sp, sn = torch.sigmoid(pg).cpu(), torch.sigmoid(ng).cpu()
+    scores = torch.cat([sp, sn]).numpy()
+    labels = np.concatenate([np.ones(P), np.zeros(N)])
+    want = {"ap": float(average_precision_score(labels, scores)), "auc": float(roc_auc_score(labels, scores)),
+            "mrr": float((sp.unsqueeze(1) > sn.unsqueeze(0)).float().mean().item())}
+    got = out.cpu().tolist()
+    assert got[0] == 1.25
+    for k, i, tol in (("ap", 1, 1e-9), ("auc", 2, 1e-9), ("mrr", 3, 1e-6)):
+        assert abs(got[i] - want[k]) <= tol, (k, got[i], want[k])
+    assert int(seq.item()) == 4 and int(done.item()) == 0
+    assert torch.equal(ring.cpu(), out.cpu().unsqueeze(0).expand(3, 4))
+
+
 def test_fixed_point_range_is_reported(gpu):
     """A term outside the predictor's fixed-point range (forced from the host:
     out_fc weights of 1e10 make the per-event loss and hidden-layer gradient

@@ -644,8 +644,11 @@ def test_planned_steps_match_eager(gpu):
                 assert torch.equal(getattr(se, name), getattr(sg, name)), (name, msg)
             _close(sg.memory, se.memory, rtol=1e-5, atol=1e-6, msg=f"memory {msg}")
             _close(rt_g.optimizer.inner.flat, rt_e.optimizer.inner.flat, rtol=0, atol=3 * lr, msg=f"params {msg}")
-    # one plan per (split, train/eval, step buffer)
-    assert set(rt_g._plans) == {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)}
+    # one plan per (split, train/eval, step buffer) (the device metrics op in
+    # the back part: the host collects every step's results)
+    assert {k[:3] for k in rt_g._plans} == {("train", True, 0), ("train", True, 1), ("val", False, 0),
+                                            ("val", False, 1)}
+    assert all(k[3] and not k[4] for k in rt_g._plans)
     assert not rt_e._plans
 
 
@@ -682,7 +685,16 @@ def test_pipelined_steps_match_eager(gpu):
         se, sg = rt_e.memory.state, rt_g.memory.state
         for name in ("mailbox", "mailbox_ts", "memory_ts", "next_mail_pos"):
             assert torch.equal(getattr(se, name), getattr(sg, name)), (name, split)
-    assert {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)} <= set(rt_g._plans)
+        # the device metrics ring: every step's (loss, AP, AUC, mrr) in step order
+        n = len(res[id(rt_e)])
+        me, mg = rt_e.metrics_of_last_steps(n), rt_g.metrics_of_last_steps(n)
+        assert me.shape == (n, 4) and torch.equal(me, mg), split
+        assert torch.equal(me[:, 0], torch.stack([r[0] for r in res[id(rt_e)]]).double().cpu())
+    # plans per (split, train/eval, step buffer); asynchronous steps compute the
+    # metrics of the previous step on their buffers in their front part
+    assert {("train", True, 0), ("train", True, 1), ("val", False, 0), ("val", False, 1)} <= \
+        {k[:3] for k in rt_g._plans}
+    assert any(k[4] for k in rt_g._plans) and not any(k[3] for k in rt_g._plans)
 
 
 def test_fused_update_matches_torch_adam(gpu):
