@@ -406,10 +406,11 @@ def build_session(wl: dict, stream):
     cfg = {"model": {"family": wl["family"], "hidden_dim": wl["D"]},
            "data": {"name": f"bench_{wl['config']}", "format": "synthetic"},
            "train": {"batch_size": wl["B"], "lr": 1e-3}, "runtime": {"device": "cuda"},
-           "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"], "dropout": 0.0,
-                    "att_dropout": 0.0, "memory_gemm_dtype": wl.get("gemm", "fp32"),
-                    "attention_gemm_dtype": wl.get("gemm", "fp32") if wl.get("embedding", "attention") == "attention"
-                    else "fp32",
+           "ctdg": {"mailbox_slots": wl["K"], "dim_time": wl["T"], "num_head": wl["H"],
+                    "dropout": wl.get("dropout", 0.0), "att_dropout": wl.get("dropout", 0.0),
+                    "memory_gemm_dtype": wl.get("gemm", "fp32"),
+                    "attention_gemm_dtype": wl.get("attention_gemm", wl.get("gemm", "fp32"))
+                    if wl.get("embedding", "attention") == "attention" else "fp32",
                     "embedding": wl.get("embedding", "attention")},
            "sampling": {"neighbor_limit": [wl["k"]] * wl["history"], "history": wl["history"],
                         "strategy": "recent"}}
@@ -533,6 +534,21 @@ def kernel_work(name: str, wl: dict, U: int, E: int, B: int, dims) -> tuple[str,
     else:
         b = 0.0
     return "hbm", b, b
+
+
+def param_update_bytes(wl: dict, U: float, dims, n_params: int, n_shadow: int, tile_rows: int) -> float:
+    """Algorithmic HBM bytes of one fused weight-gradient + Adam launch
+    (sgl_grad_adam): every per-root row its reductions read once -- gQ,
+    new_mem, Q, gagg, gz, agg [U][D], G, xbar [U][H][C], sigma [U][H]; y,
+    g_src, g_dst [U+1][D] for src_fc / dst_fc; the LayerNorm and
+    time-encoding partials [U/tile][2][D], [U/tile][2][T] -- plus Adam's
+    28 bytes per parameter (parameter, gradient and both moments read;
+    parameter and moments written) and the bf16 weight copies written."""
+    D, T, H = wl["D"], wl["T"], wl["H"]
+    C = D + dims.F + T
+    rows = U * 4.0 * (6 * D + 2 * H * C + H) + (U + 1) * 4.0 * 3 * D
+    parts = (U / max(1, tile_rows)) * 4.0 * 2 * (D + T)
+    return rows + parts + 28.0 * n_params + 2.0 * n_shadow
 
 
 def copy_bandwidth(mib: int = 2048, reps: int = 10) -> dict:
@@ -673,6 +689,18 @@ def run_tgn(args, wl: dict) -> dict:
         breakdown[name] = {"avg_us": round(avg * 1e3, 2), "calls": len(ms), "bound": bound,
                            "achieved": round(ach, 3), "unit": unit, "frac": round(ach / peak, 5),
                            "traffic": HBM_TRAFFIC.get((wl["config"], wl.get("gemm", "fp32"), name))}
+        if name == "param_update" and wl.get("embedding", "attention") == "attention":
+            # the fused launch is also a streaming kernel: its algorithmic bytes against HBM
+            from starry_unigraph.lib import _capi
+            U_avg = sum(p[2] for p in per_step) / len(per_step)
+            nb = param_update_bytes(wl, U_avg, rt.dims, rt.optimizer.inner.flat.numel(),
+                                    rt._bf16.buf.numel() if rt._bf16 is not None else 0,
+                                    int(_capi.lib().sgl_conv_tile_rows(rt.dims.D, rt.dims.F, rt.dims.T, rt.dims.H)))
+            gbs = nb / (avg * 1e-3) / 1e9
+            breakdown[name]["hbm"] = {"alg_bytes": round(nb), "achieved": round(gbs, 1), "unit": "GB/s",
+                                      "frac": round(gbs / HBM_PEAK_GBS, 5),
+                                      "formula": "param_update_bytes(): rows read once + 28 B per parameter "
+                                                 "+ the bf16 copies"}
     mean_U = sum(p[2] for p in per_step) / len(per_step)
     mean_E = sum(p[3] for p in per_step) / len(per_step)
     if not dom_ms:   # no timed launches in the timed region: the eager replay's
@@ -706,6 +734,53 @@ def run_tgn(args, wl: dict) -> dict:
     if not args.no_cpu:
         res["cpu_baseline"] = tgn_cpu_baseline(wl, stream, rt)
     return res
+
+
+def run_tgn_short(wl: dict, steps: int, warmup: int) -> dict:
+    """A configuration's training steps timed as the headline's are (W warm-up
+    steps, then K planned asynchronous steps between synchronizes, negatives
+    and per-step device metrics inside the timed region), without the
+    per-kernel replay: the driver-timed number of a configuration other than
+    the headline's."""
+    import torch
+
+    stream = make_stream(wl)
+    sess = build_session(wl, stream)
+    rt = sess.ctdg_session.online_runtime
+    rt.collect_results = False
+    ep = Epochs(rt, wl["B"])
+    for _ in range(warmup):
+        rt.train_step(ep.next())
+    torch.cuda.synchronize()
+    batches = [ep.next() for _ in range(steps)]
+    gc.collect()
+    gc.disable()
+    w0 = time.perf_counter()
+    for b in batches:
+        rt.train_step(b)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    gc.enable()
+    rt.check_sync()
+    met = rt.metrics_of_last_steps(steps).mean(0).tolist()
+    events = sum(b.size for b in batches)
+    gemm = wl.get("gemm", "fp32")
+    att = wl.get("attention_gemm", gemm) if wl.get("embedding", "attention") == "attention" else None
+    out = {"value": events / wall, "unit": "events/s", "ms_per_step": wall * 1e3 / steps, "steps": steps,
+           "warmup": warmup,
+           "config": {"workload": wl["config"], "model": wl["family"] + (" (time projection)"
+                                                                       if wl.get("embedding") == "time_projection"
+                                                                       else ""),
+                      "D": wl["D"], "T": wl["T"], "H": wl["H"], "k": wl["k"], "sampled_hops": wl["history"],
+                      "attention_layers": 1 if att is not None else 0, "K": wl["K"], "B": wl["B"],
+                      "dropout": wl.get("dropout", 0.0)},
+           "dtype": f"GRU {gemm}" + (f", attention and predictor {att}" if att is not None else "")
+                    + " GEMMs; fp32 memory and Adam",
+           "mean_step_metrics": {"loss": met[0], "ap": met[1], "auc": met[2], "mrr": met[3]}}
+    del rt, sess, stream
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
 
 
 def tgn_cpu_baseline(wl: dict, stream, rt) -> dict:
@@ -784,6 +859,8 @@ def main() -> None:
                     help="the kernel the roofline object measures (default: conv_forward, or memory_update "
                          "for the time-projection workload, which has no attention)")
     ap.add_argument("--no-sampler", action="store_true", help="skip the config-3 sampler sub-benchmark")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the short runs of configs 1, 2, 5 and config 4 with dropout")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--epoch", action="store_true",
                     help="TGN workloads: one warm-up epoch, then time one epoch of train batches (overrides "
@@ -848,6 +925,18 @@ def main() -> None:
                 roofline=r["roofline"], cpu_baseline=r.get("cpu_baseline"), kernels=r["kernels"],
                 step_shape=r["step_shape"], final_train_loss=r["final_train_loss"], step_metrics=r["step_metrics"])
     line["hbm_copy"] = copy_bandwidth()
+    if args.workload == "tgn-large" and not args.no_configs:
+        # every other configuration's training step, driver-timed (20 steps after 5 warm-up steps):
+        # configs 1, 2 and 5, and config 4 with the reference's default dropout 0.1
+        # (config/default.yaml:152-153; the dropout passes run the fp32 attention instances)
+        others = {"cfg1": WORKLOADS["tgn-small"], "cfg2": WORKLOADS["jodie"],
+                  "cfg5": dict(WORKLOADS["tgn-stress"], gemm=WORKLOADS["tgn-stress"]["precision"]),
+                  "cfg4_dropout": dict(WORKLOADS["tgn-large"], gemm="bf16", attention_gemm="fp32", dropout=0.1)}
+        line["configs"] = {}
+        for name, w in others.items():
+            r2 = run_tgn_short(w, 20, 5)
+            log(f"{name}: {r2['ms_per_step']:.3f} ms/step, {r2['value']:.0f} events/s")
+            line["configs"][name] = r2
     if args.workload == "tgn-large" and not args.no_sampler:
         line["sampler"] = run_sampler(20, 3, cases=True, cpu=not args.no_cpu)
     if args.workload == "tgn-large" and not args.no_gather_scatter:

@@ -96,6 +96,65 @@ def test_gru_kernel_matches_torch(gpu, K, D, F, dt, M):
         assert float((got.cpu() - want).abs().max()) > 1e-5
 
 
+def test_gather_scatter_at_config5_state_and_a_million_events(gpu):
+    """The gather / scatter path at the size its benchmark is quoted at:
+    config-5 node state (1,140,149 nodes, D = 172, K = 4 mailbox slots of
+    2D + F = 360 floats: a 6.6 GB mailbox, byte offsets past 2^32) and one
+    batch of 1,048,576 consecutive events of the config-4 stream from its
+    middle, through batch preparation, the bf16 GRU + mailbox kernel (its
+    64-root tiles) and the memory commit, against the oracle's memory phase
+    (runtime.py:268-282) from the same random state: every node's mailbox
+    timestamps, slot pointer and memory timestamp bit-exact; the touched
+    nodes' mailbox rows bit-exact and every other row unchanged; memory
+    within the bf16 tolerance (rtol / atol 2e-2)."""
+    from starry_unigraph import synth
+    from starry_unigraph.backends.ctdg.runtime.models import CTDGMemoryUpdater
+    from starry_unigraph.lib import _capi
+    from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
+    es = synth.unipartite_stream(seed=0)
+    N, D, K, F = es.num_nodes, 172, 4, 16
+    S = 2 * D + F
+    B = 1 << 20
+    a = (es.num_events // B // 2) * B
+    src, dst = torch.from_numpy(es.src[a:a + B]), torch.from_numpy(es.dst[a:a + B])
+    ts, ef = torch.from_numpy(es.ts[a:a + B]), torch.from_numpy(es.edge_feat[a:a + B])
+    assert _capi.lib().sgl_memory_update_bf16_tile_rows(D, F, 2 * B) == 64
+    g = torch.Generator(device=gpu).manual_seed(3)
+    st = NodeState(N, D, K, F, gpu)
+    st.memory.uniform_(-1, 1, generator=g)
+    st.mailbox.normal_(0, 0.5, generator=g)
+    st.mailbox_ts.uniform_(0, 1e3, generator=g)
+    st.next_mail_pos.random_(0, K, generator=g)
+    mem = co.MemoryO(N, D, K, F)
+    mem.memory, mem.mailbox = st.memory.cpu(), st.mailbox.cpu()
+    mem.mailbox_ts, mem.memory_ts = st.mailbox_ts.cpu(), st.memory_ts.cpu()
+    mem.next_mail_pos = st.next_mail_pos.cpu().long()
+    mailbox0 = st.mailbox.clone()
+    torch.manual_seed(5)
+    up = CTDGMemoryUpdater(D, S, K, gemm_dtype="bf16").to(gpu)
+    ref = co.MemoryUpdaterO(D, S, K)
+    ref.load_state_dict({k: v.cpu() for k, v in up.state_dict().items()})
+    step = DeviceStep(st, ConvDims(D=D, F=F, T=100, H=4, fanout=20), B, attention=False)
+    sg, dg, tg, fg = src.to(gpu), dst.to(gpu), ts.to(gpu), ef.to(gpu)
+    step.prepare(sg, dg, dg.roll(1), tg)
+    step.update_memory(up.kernel_weights(), sg, dg, fg, tg)
+    step.commit()
+    torch.cuda.synchronize()
+    U = int(step.buf.num_roots.item())
+    all_nodes, _ = co.memory_phase(mem, ref, src, dst, ts, ef)
+    assert U == all_nodes.numel() and U > 20000
+    assert int(torch.count_nonzero(st.node_bits).item()) == 0
+    assert torch.equal(st.mailbox_ts.cpu(), mem.mailbox_ts)
+    assert torch.equal(st.next_mail_pos.cpu().long(), mem.next_mail_pos)
+    assert torch.equal(st.memory_ts.cpu(), mem.memory_ts)
+    touched = torch.zeros(N, dtype=torch.bool, device=gpu)
+    touched[all_nodes.to(gpu)] = True
+    assert torch.equal(st.mailbox[touched].cpu(), mem.mailbox[all_nodes])
+    changed = (st.mailbox != mailbox0).flatten(1).any(1)
+    assert not bool(changed[~touched].any())
+    _close(st.memory, mem.memory, rtol=2e-2, atol=2e-2, msg="memory")
+
+
 def _small_batch(rng, n_nodes, B, sorted_ts=True):
     src = rng.integers(0, n_nodes, B)
     dst = rng.integers(0, n_nodes, B)
@@ -399,12 +458,11 @@ def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T, bf16):
     rows, so the head blocks of the transposed copies are padded): the
     embedding within north_star's bf16 tolerance 2e-2 of its scale (max
     error <= 2e-2 max|y|, relative Frobenius error <= 2e-2; measured 0.3-0.5 %
-    and 3e-3), each gradient within a relative Frobenius error of 1e-1
-    (measured 0.3-6 %), the time-encoding weight's within 1.5e-1 (measured
-    2.5-12 %): the softmax backward (t - sum alpha t) and the dt-weighted
-    time-encoding sums cancel, which amplifies bf16's ~0.3 % operand
-    rounding; a wrong weight copy (a transpose, a head block) gives errors
-    near 100 %."""
+    and 3e-3) and elementwise within rtol 2e-2 + atol 3e-2; each gradient
+    within BF16_CONV_GRAD_BOUND (its measured maximum and a margin): the
+    softmax backward (t - sum alpha t) and the dt-weighted time-encoding sums
+    cancel, which amplifies bf16's ~0.3 % operand rounding; a wrong weight
+    copy (a transpose, a head block) gives errors near 100 %."""
     from starry_unigraph.backends.ctdg.runtime.models import TemporalTransformerConv
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
     from starry_unigraph.native.tcsr import RecentSampler, build_tcsr
@@ -456,15 +514,40 @@ def test_conv_forward_backward_matches_oracle(gpu, H, k, seed, D, F, T, bf16):
               f"elements beyond 2e-2 (rtol+atol): {int(((d.abs() > 2e-2 + 2e-2 * yn.abs())).sum())} / {d.numel()}",
               flush=True)
         assert float(d.abs().max()) <= 2e-2 * float(yn.abs().max()) and float(d.norm() / yn.norm()) <= 2e-2
+        # elementwise: rtol 2e-2, atol 3e-2 on these unit-RMS LayerNorm outputs (measured over the
+        # shapes here: at most 2.8e-2 absolute, on outputs near 0 whose error scales with the row's
+        # RMS, not with |y|; 1 element in 5,400-25,800 exceeds 2e-2 + 2e-2 |y|)
+        assert int((d.abs() > 3e-2 + 2e-2 * yn.abs()).sum()) == 0
         for (name, p), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
             err = float((p.grad.cpu().double() - pr.grad.double()).norm()) / (float(pr.grad.double().norm()) + 1e-30)
             print(f"  grad {name}: relative Frobenius error {err:.3e}", flush=True)
-            assert err <= (1.5e-1 if name == "time_enc.w.weight" else 1e-1), (name, err)
+            assert err <= BF16_CONV_GRAD_BOUND[name], (name, err, BF16_CONV_GRAD_BOUND[name])
         return
     _close(y[:R], yr, atol=2e-4, msg="embedding")
     for (name, p), (_, pr) in zip(conv.named_parameters(), ref.named_parameters()):
         scale = float(pr.grad.abs().max()) + 1e-6
         _close(p.grad, pr.grad, rtol=2e-3, atol=2e-4 * scale, msg=f"grad {name}")
+
+
+# Relative Frobenius error bounds of the bf16 attention's gradients: the
+# largest error measured over the bf16 shapes of
+# test_conv_forward_backward_matches_oracle, times 1.25-1.5 (the time-encoding
+# weight's dt-weighted sums and the biases' near-cancelling sums amplify
+# bf16's operand rounding most).
+BF16_CONV_GRAD_BOUND = {   # measured maximum in the comment
+    "time_enc.w.weight": 0.15,   # 0.120
+    "time_enc.w.bias": 0.075,    # 0.057
+    "w_q.weight": 0.07,          # 0.051
+    "w_q.bias": 0.06,            # 0.046
+    "w_k.weight": 0.06,          # 0.047
+    "w_k.bias": 0.08,            # 0.061
+    "w_v.weight": 0.075,         # 0.057
+    "w_v.bias": 0.07,            # 0.051
+    "w_out.weight": 0.075,       # 0.057
+    "w_out.bias": 0.07,          # 0.051
+    "layer_norm.weight": 6e-3,   # 0.0041
+    "layer_norm.bias": 1e-5,     # 2.9e-7
+}
 
 
 class _Wrap:
