@@ -20,6 +20,8 @@ Follows, function by function:
   train_step             runtime.py:225-328 (dropout as explicit masks: the
                          GPU kernels' masks are replayed, torch's own draws
                          cannot be matched)
+  empty_train_step       runtime.py:248-253 with runtime.py:111-116, pinned
+                         by Adam's closed form with a zero gradient
   ProjectionPredictorO   config 2's JODIE time projection (the build's own
                          definition: the reference has none), pinned by a
                          closed form
@@ -292,10 +294,11 @@ class MemoryO:
         self.mailbox_ts[uniq, pos] = ts_o[last]
         self.next_mail_pos[uniq] = (pos + counts) % K
 
-    def apply_memory_update(self, ids, vals, ts_scalar):
-        """memory.py:254-269 (ids unique)."""
+    def apply_memory_update(self, ids, vals, ts):
+        """memory.py:254-269 (ids unique): ``ts`` one time per row, or one
+        for all rows (the training step's batch maximum)."""
         self.memory[ids] = vals.float()
-        self.memory_ts[ids] = float(ts_scalar)
+        self.memory_ts[ids] = torch.as_tensor(ts, dtype=torch.float32)
 
 
 def write_slots_serial(mem: MemoryO, ids, vals, ts):
@@ -429,6 +432,20 @@ def train_step(model, updater, optimizer, mem: MemoryO, sample_fn, src, dst, ts,
         optimizer.step()
     return {"loss": loss.detach(), "pos": pos.detach(), "neg": negl.detach(), "conv": conv.detach(),
             "convs": tuple(c.detach() for c in convs), "roots": roots, "block": blk}
+
+
+def empty_train_step(model, updater, optimizer):
+    """runtime.py:248-253 with runtime.py:111-116: on an empty batch the
+    backward of 0 * (sum of the model's first parameter) + 0 * (sum of the
+    updater's first parameter), then an optimizer step; those two
+    parameters alone have (zero) gradients."""
+    model.train()
+    zero = next(model.parameters()).sum() * 0.0
+    if updater is not None:
+        zero = zero + next(updater.parameters()).sum() * 0.0
+    optimizer.zero_grad(set_to_none=True)
+    zero.backward()
+    optimizer.step()
 
 
 def metric_dict(pos_logits, neg_logits):

@@ -79,12 +79,20 @@ def make_optimizer(model: torch.nn.Module, lr: float) -> "GatedAdam":
 
 
 class GatedAdam:
-    """Adam over the link predictor's parameters (factory.py:122-128), in two
-    segments: the embedding's (the attention, or the time projection) and
-    the edge predictor's. The attention's segment is gated by the step's
-    "block has edges" flag (when it is 0 those parameters have no gradient
-    in the reference, and Adam skips them). The memory updater gets no gradients in the reference
-    (runtime.py:279) and is not optimised."""
+    """Adam over the link predictor's parameters (factory.py:122-128), in
+    three segments: the embedding module's first parameter (the model's
+    first parameter), the rest of the embedding (the attention, or the time
+    projection) and the edge predictor. The first two are gated by the
+    step's "block has edges" flag (when it is 0 those parameters have no
+    gradient in the reference, and Adam skips them). The first parameter has
+    a segment of its own because the reference's empty-batch step
+    (runtime.py:248-253) gives it, alone among the model's parameters, a zero
+    gradient and an Adam step (its step count and moments advance).
+
+    The memory updater gets no gradients in the reference (runtime.py:279)
+    and is not optimised here. Its first parameter's zero-gradient steps on
+    empty batches (runtime.py:111-116) leave its values unchanged: its
+    moments start at zero and stay there, so each update is 0 / (0 + eps)."""
 
     def __init__(self, model: torch.nn.Module, lr: float):
         self.model = model
@@ -94,10 +102,13 @@ class GatedAdam:
 
     def _build(self) -> FusedAdam:
         core = self.model.module if hasattr(self.model, "module") else self.model
-        conv = list(core.embedding_module().parameters())
-        conv_ids = {id(p) for p in conv}
-        rest = [p for p in core.parameters() if id(p) not in conv_ids]
-        return FusedAdam([conv, rest], lr=self.lr)
+        emb = list(core.embedding_module().parameters())
+        first = next(core.parameters())
+        if emb[0] is not first:
+            raise RuntimeError("GatedAdam: the model's first parameter must open its embedding module")
+        emb_ids = {id(p) for p in emb}
+        rest = [p for p in core.parameters() if id(p) not in emb_ids]
+        return FusedAdam([emb[:1], emb[1:], rest], lr=self.lr)
 
     @property
     def inner(self) -> FusedAdam:
@@ -110,7 +121,16 @@ class GatedAdam:
 
     def step(self) -> None:
         gate = self.gate_fn() if self.gate_fn is not None else None
-        self.inner.step([gate, None])
+        self.inner.step([gate, gate, None])
+
+    def empty_step(self) -> None:
+        """The reference's step on an empty batch (runtime.py:248-253): the
+        model's first parameter takes an Adam step with a zero gradient;
+        every other parameter is untouched."""
+        inner = self.inner
+        start, n, _ = inner.segments[0]
+        inner.flat_grad[start:start + n].zero_()
+        inner.step([None], only=[0])
 
     def state_dict(self) -> dict:
         return self.inner.state_dict()

@@ -635,9 +635,11 @@ class CTDGOnlineRuntime:
                     core.out_fc.bias]
             if self._proj:
                 tp = core.time_proj.proj
-                upd = StepParamUpdate(step, inner, [tp.weight, tp.bias], pred, [None, None], kind="projection")
+                upd = StepParamUpdate(step, inner, [tp.weight, tp.bias], pred, [None, None, None],
+                                      kind="projection")
             else:
-                upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [step.buf.any_edges, None],
+                ae = step.buf.any_edges
+                upd = StepParamUpdate(step, inner, core.conv.kernel_params(), pred, [ae, ae, None],
                                       passes=step.buf.passes, counter=self._rng_counter, shadow=self._bf16)
             self._updates = {k: u for k, u in self._updates.items() if u.step in self.steps}
             self._updates[id(step)] = upd
@@ -683,7 +685,16 @@ class CTDGOnlineRuntime:
             self.model.train()
         t0 = time.perf_counter()
         if batch.is_empty:
-            return self._empty_result(batch, batch.split)
+            # runtime.py:248-258: a zero loss's backward and an optimizer
+            # step (the model's first parameter alone has a gradient); on the
+            # stream of the back parts, after the previous step's update
+            inner = getattr(self.optimizer, "inner", None)
+            if not isinstance(inner, FusedAdam):
+                raise RuntimeError("the fused step needs the runtime's optimizer (GatedAdam over a FusedAdam)")
+            self.optimizer.empty_step()
+            r = self._empty_result(batch, batch.split)
+            r["meta"].update(sync_wait_ms=0.0, sync_submit_ms=0.0, step_ms=(time.perf_counter() - t0) * 1000.0)
+            return r
         st = self._forward(batch, batch.split, train=True)
         if not self.collect_results:
             return {"loss": st.loss, "pos_logits": st.pos_logits, "neg_logits": st.neg_logits,

@@ -11,7 +11,7 @@ backends/ctdg/runtime/runtime.py:225-297):
   sgl_conv_forward    time encoding + temporal attention           (models.py:77-137)
   sgl_predictor       edge predictor + BCE, per-root gradient sums (models.py:313-324, runtime.py:290-292)
   sgl_conv_backward   attention backward                           (loss.backward(), runtime.py:296)
-  sgl_grad_adam       weight gradients + Adam, the attention segment
+  sgl_grad_adam       weight gradients + Adam, the attention segments
                       gated by "block has edges"                   (optimizer.step(), runtime.py:297)
 
 The first three are a step's front part, the memory commit its split point,
@@ -563,9 +563,11 @@ class StepParamUpdate:
     launch (sgl_grad_adam), preceded by the step-count advance and bias
     corrections (sgl_adam_coef). The job table points at the step buffers and
     at the optimizer's flat buffers, so it is rebuilt when either is
-    re-created. Segment 0 (the attention) is gated by the step's "block has
-    edges" flag; segment 1 (the edge predictor) takes its gradients from
-    sgl_predictor (Adam-only jobs). Each step-buffer set has its own bias
+    re-created. The optimizer's three segments are the embedding's first
+    parameter, the rest of the embedding (the attention, both gated by the
+    step's "block has edges" flag) and the edge predictor, whose out_fc
+    takes its gradients from sgl_predictor (Adam-only jobs); each job's
+    segment is the one holding its outputs. Each step-buffer set has its own bias
     corrections, so one step's advance may run while the previous step's
     update still reads its own. ``passes`` 3 (dropout): every attention
     gradient sums the three passes' rows, dst_fc's the dst and negative
@@ -577,8 +579,9 @@ class StepParamUpdate:
     def __init__(self, step: "DeviceStep", opt: "FusedAdam", conv_params: list[torch.Tensor],
                  pred_params: list[torch.Tensor], gates: list[torch.Tensor | None], passes: int = 1,
                  counter: torch.Tensor | None = None, kind: str = "attention", shadow: Bf16Shadow | None = None):
-        if len(opt.segments) != 2:
-            raise ValueError("StepParamUpdate expects the attention and predictor segments")
+        if len(opt.segments) != 3:
+            raise ValueError("StepParamUpdate expects three segments: the embedding's first parameter, the rest "
+                             "of the embedding and the predictor")
         if passes not in (1, step.buf.passes):
             raise ValueError(f"StepParamUpdate: {passes} passes on buffers of {step.buf.passes}")
         self.step, self.opt = step, opt
@@ -602,6 +605,8 @@ class StepParamUpdate:
         self.num_tiles = len(tiles)
         P = _capi.ptr
         self._steps = (ctypes.c_void_p * len(opt.segments))(*[P(seg[2]) for seg in opt.segments])
+        if len(gates) != len(opt.segments):
+            raise ValueError(f"StepParamUpdate: {len(gates)} gates for {len(opt.segments)} segments")
         self._gates = (ctypes.c_void_p * len(opt.segments))(*[P(g) for g in gates])
 
     def _jobs(self, conv_params, pred_params):
@@ -621,8 +626,16 @@ class StepParamUpdate:
             return t.data_ptr() + 4 * k
 
         jobs, tiles = [], []
+        bounds = [(st, st + k) for st, k, _ in opt.segments]
+
+        def seg_of(first, last):   # the segment holding a job's outputs
+            for i, (lo, hi) in enumerate(bounds):
+                if lo <= first and last < hi:
+                    return i
+            raise RuntimeError("StepParamUpdate: a job's outputs span optimizer segments")
 
         def add(job, ntile):
+            job.seg = seg_of(job.off, job.off + (job.rows - 1) * job.ldo + job.cols - 1)
             job.tile0 = len(tiles)
             tiles.extend([len(jobs)] * ntile)
             jobs.append(job)
@@ -635,11 +648,11 @@ class StepParamUpdate:
         def shf(*a, **k):   # a job's bf16-copy fields (none without a shadow)
             return sh.jobs_for(*a, **k) if sh is not None else {}
 
-        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, seg=0, r_extra=0, npass=1, ps1=0, ps2=0, shd=None):
+        def gemm(x1, s1, x2, s2, o, ldo, rows, cols, r_fixed=-1, r_extra=0, npass=1, ps1=0, ps2=0, shd=None):
             assert s1 >= rows
             tb = (cols + 15) // 16
             add(_capi.GradJob(x1=x1, x2=x2, s1=s1, s2=s2, off=o, ps1=ps1, ps2=ps2, ldo=ldo, rows=rows, cols=cols,
-                              kind=0, seg=seg, r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb, npass=npass,
+                              kind=0, r_fixed=r_fixed, r_extra=r_extra, tiles_b=tb, npass=npass,
                               **(shd or {})),
                 ((rows + 15) // 16) * tb)
 
@@ -695,20 +708,20 @@ class StepParamUpdate:
         nd = 2 if P > 1 else 1
         gs, ys = (c + 1) * D, b.y_rows * D
         yd = at(b.y, ys) if P > 1 else at(b.y)
-        gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, seg=1, r_extra=1, shd=shf("w_s"))
-        gemm(at(b.g_src), D, one, 0, off(b_s), 1, D, 1, seg=1, r_extra=1)
-        gemm(at(b.g_dst), D, yd, D, off(w_d), D, D, D, seg=1, r_extra=1, npass=nd, ps1=gs, ps2=ys, shd=shf("w_d"))
-        gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, seg=1, r_extra=1, npass=nd, ps1=gs)
+        gemm(at(b.g_src), D, at(b.y), D, off(w_s), D, D, D, r_extra=1, shd=shf("w_s"))
+        gemm(at(b.g_src), D, one, 0, off(b_s), 1, D, 1, r_extra=1)
+        gemm(at(b.g_dst), D, yd, D, off(w_d), D, D, D, r_extra=1, npass=nd, ps1=gs, ps2=ys, shd=shf("w_d"))
+        gemm(at(b.g_dst), D, one, 0, off(b_d), 1, D, 1, r_extra=1, npass=nd, ps1=gs)
         if off(b_o) != off(w_o) + D:
             raise RuntimeError("StepParamUpdate: out_fc weight and bias are not contiguous in the flat buffer")
-        add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=off(w_o), ldo=1, rows=D + 1, cols=1, kind=1, seg=1,
+        add(_capi.GradJob(x1=None, x2=None, s1=0, s2=0, off=off(w_o), ldo=1, rows=D + 1, cols=1, kind=1,
                           r_fixed=0, tiles_b=1), (D + 1 + 255) // 256)
 
     def _check(self, jobs, tiles, conv_params, pred_params):
         opt = self.opt
-        if sum(p.numel() for p in conv_params) != opt.segments[0][1]:
-            raise RuntimeError("StepParamUpdate: the embedding segment holds parameters the jobs do not cover")
-        if sum(p.numel() for p in pred_params) != opt.segments[1][1]:
+        if sum(p.numel() for p in conv_params) != opt.segments[0][1] + opt.segments[1][1]:
+            raise RuntimeError("StepParamUpdate: the embedding segments hold parameters the jobs do not cover")
+        if sum(p.numel() for p in pred_params) != opt.segments[2][1]:
             raise RuntimeError("StepParamUpdate: the predictor segment holds parameters the jobs do not cover")
         return jobs, tiles
 
@@ -787,13 +800,17 @@ class FusedAdam:
     def zero_grad(self, set_to_none: bool = False) -> None:
         self.flat_grad.zero_()
 
-    def step(self, gates: list[torch.Tensor | None] | None = None) -> None:
-        """``gates[i]``: device int32 gating segment i (None = always update)."""
+    def step(self, gates: list[torch.Tensor | None] | None = None, only: list[int] | None = None) -> None:
+        """``gates[i]``: device int32 gating the i-th stepped segment (None =
+        always update); ``only``: the segments to step (default all)."""
         lib, P = _capi.lib(), _capi.ptr
         s = _capi.stream_of(self.flat.device)
         b1, b2 = self.betas
-        gates = gates or [None] * len(self.segments)
-        for (start, n, stepc), gate in zip(self.segments, gates):
+        segs = self.segments if only is None else [self.segments[i] for i in only]
+        gates = gates or [None] * len(segs)
+        if len(gates) != len(segs):
+            raise ValueError(f"FusedAdam.step: {len(gates)} gates for {len(segs)} segments")
+        for (start, n, stepc), gate in zip(segs, gates):
             _capi.check(lib.sgl_adam_step(n, P(self.flat[start:start + n]), P(self.flat_grad[start:start + n]),
                                           P(self.exp_avg[start:start + n]), P(self.exp_avg_sq[start:start + n]),
                                           P(stepc), P(gate), self.lr, b1, b2, self.eps, self.wd, s), "sgl_adam_step")

@@ -663,7 +663,8 @@ def test_train_steps_match_oracle_teacher_forced(gpu, K):
 
 
 def test_fused_adam_matches_torch_adam(gpu):
-    """FusedAdam vs torch.optim.Adam, a gated segment skipped like a None grad."""
+    """FusedAdam vs torch.optim.Adam, a gated segment skipped like a None
+    grad, and one segment stepped alone (``only``)."""
     from starry_unigraph.native.step import FusedAdam
     torch.manual_seed(0)
     shapes = [(7, 3), (5,), (11, 2), (4,)]
@@ -672,19 +673,23 @@ def test_fused_adam_matches_torch_adam(gpu):
     opt_r = torch.optim.Adam(ref_p, lr=3e-3)
     opt_g = FusedAdam([gpu_p[:2], gpu_p[2:]], lr=3e-3)
     gate = torch.zeros(1, dtype=torch.int32, device=gpu)
-    for it, on in enumerate([1, 0, 1, 1, 0, 1]):
+    # on: 1 both segments, 0 the first gated off, -1 the second alone (only=)
+    for it, on in enumerate([1, 0, 1, -1, 1, 0, -1, 1]):
         grads = [torch.randn(s) * (10.0 ** (it % 3 - 1)) for s in shapes]
         opt_r.zero_grad(set_to_none=True)
         for i, (p, g) in enumerate(zip(ref_p, grads)):
-            if i < 2 and not on:
+            if i < 2 and on != 1:
                 continue
             p.grad = g.clone()
         opt_r.step()
         opt_g.zero_grad()
         for p, g in zip(gpu_p, grads):
             p.grad.copy_(g)
-        gate.fill_(on)
-        opt_g.step([gate, None])
+        if on == -1:
+            opt_g.step([None], only=[1])
+        else:
+            gate.fill_(on)
+            opt_g.step([gate, None])
         for a, b in zip(gpu_p, ref_p):
             _close(a, b, rtol=1e-5, atol=1e-6, msg=f"step {it}")
 
@@ -780,23 +785,77 @@ def test_pipelined_steps_match_eager(gpu):
     assert any(k[4] for k in rt_g._plans) and not any(k[3] for k in rt_g._plans)
 
 
+def _empty_batch(batch):
+    import dataclasses
+    e = lambda t: t[:0]
+    return dataclasses.replace(batch, event_ids=e(batch.event_ids), src=e(batch.src), dst=e(batch.dst),
+                               ts=e(batch.ts), edge_feat=e(batch.edge_feat))
+
+
+def _check_empty_step(rt, opt, msg):
+    """An empty-batch train step against the oracle's (runtime.py:248-253):
+    torch.optim.Adam over the oracle's model and updater, holding the
+    runtime's parameters and each parameter's moments and step count."""
+    core = rt._core()
+    model, updater = co.build_models(32, 16, 16, 2, 1, seed=0)
+    model.load_state_dict({k: v.cpu() for k, v in core.state_dict().items()})
+    updater.load_state_dict({k: v.cpu() for k, v in rt.memory_updater.state_dict().items()})
+    ref = torch.optim.Adam(list(model.parameters()) + list(updater.parameters()), lr=opt.lr, betas=opt.betas,
+                           eps=opt.eps)
+    base = opt.flat.data_ptr()
+    seg_of = lambda o: next(i for i, (st, n, _) in enumerate(opt.segments) if st <= o < st + n)
+    steps = [float(seg[2].item()) for seg in opt.segments]
+    slots = []
+    for q, p in zip(model.parameters(), core.parameters()):
+        o = (p.data_ptr() - base) // 4
+        sl, sg = slice(o, o + p.numel()), seg_of(o)
+        slots.append((q, p, sl, sg))
+        if steps[sg] > 0:
+            ref.state[q] = {"step": torch.tensor(steps[sg]), "exp_avg": opt.exp_avg[sl].cpu().view_as(q).clone(),
+                            "exp_avg_sq": opt.exp_avg_sq[sl].cpu().view_as(q).clone()}
+    upd_before = [t.detach().cpu().clone() for t in rt.memory_updater.parameters()]
+    r = rt.train_step(_empty_batch(next(iter(rt.iter_batches("train", 10)))))
+    assert r["loss"] == 0.0 and r["meta"]["empty_batch"] and r["meta"]["batch_size"] == 0
+    co.empty_train_step(model, updater, ref)
+    for q, p, sl, sg in slots:
+        torch.testing.assert_close(p.detach().cpu(), q.detach(), rtol=1e-6, atol=1e-8, msg=msg)
+        if q in ref.state:
+            torch.testing.assert_close(opt.exp_avg[sl].cpu().view_as(q), ref.state[q]["exp_avg"], rtol=1e-6,
+                                       atol=0, msg=msg)
+            torch.testing.assert_close(opt.exp_avg_sq[sl].cpu().view_as(q), ref.state[q]["exp_avg_sq"],
+                                       rtol=1e-6, atol=0, msg=msg)
+            assert float(opt.segments[sg][2].item()) == float(ref.state[q]["step"]), msg
+    assert [float(seg[2].item()) for seg in opt.segments] == [steps[0] + 1] + steps[1:], msg
+    for a, b in zip(rt.memory_updater.parameters(), upd_before):
+        assert torch.equal(a.detach().cpu(), b), msg
+
+
 def test_fused_update_matches_torch_adam(gpu):
     """sgl_adam_coef + sgl_grad_adam: the parameters after a runtime train
     step equal torch.optim.Adam applied (in fp32 on the CPU) to the parameters,
     moments and step count before it with the gradients the kernel wrote; the
-    attention segment is skipped when the block has no edges."""
+    attention segments are skipped when the block has no edges. Empty batches
+    between the steps take the reference's zero-gradient step (the model's
+    first parameter's segment alone advances), and the steps after them
+    keep the segments' step counts apart."""
     _, rt, *_ = _runtime_pair(gpu, K=1, seed=11)
     opt = rt.optimizer.inner
+    assert len(opt.segments) == 3 and opt.segments[0][1] == rt._core().conv.time_enc.w.weight.numel()
     gen = torch.Generator().manual_seed(3)
     pool = rt.dataset.dst.unique()
-    for i, batch in enumerate(list(rt.iter_batches("train", 200))[:4]):
+    batches = list(rt.iter_batches("train", 200))[:4]
+    _check_empty_step(rt, opt, "empty batch before any step")
+    for i, batch in enumerate(batches):
+        if i in (1, 3):
+            _check_empty_step(rt, opt, f"empty batch before step {i}")
         before = [t.detach().cpu().clone() for t in (opt.flat, opt.exp_avg, opt.exp_avg_sq)]
         steps = [float(seg[2].item()) for seg in opt.segments]
         rt._neg_queue["train"] = (co.negative_sample(pool, batch.dst, gen).to(gpu), 0)
         rt.train_step(batch)
         grad = opt.flat_grad.detach().cpu()
         after = opt.flat.detach().cpu()
-        active = [int(rt.step.buf.any_edges.item()) == 1, True]
+        ae = int(rt.step.buf.any_edges.item()) == 1
+        active = [ae, ae, True]
         for (start, n, stepc), st0, act in zip(opt.segments, steps, active):
             sl = slice(start, start + n)
             p = torch.nn.Parameter(before[0][sl].clone())

@@ -182,3 +182,38 @@ def test_prepare_roots_floor_time():
     src, dst = torch.tensor([4, 2, 4]), torch.tensor([7, 2, 1])
     roots, tq = co.prepare_roots(src, dst, torch.tensor([1.0, 5.75, 3.0]))
     assert roots.tolist() == [1, 2, 4, 7] and tq.tolist() == [5] * 4
+
+
+def test_empty_train_step_closed_form():
+    """The oracle's empty-batch step (runtime.py:248-253): the model's first
+    parameter moves by Adam's closed form with a zero gradient (moments
+    decay by beta1 and beta2, bias corrections at the advanced step count);
+    the updater's first parameter gets a step count and stays put; every
+    other parameter has neither gradient nor state."""
+    model, updater = co.build_models(8, 4, 6, 2, 2, seed=3)
+    params = list(model.parameters()) + list(updater.parameters())
+    lr, b1, b2, eps = 2e-3, 0.9, 0.999, 1e-8
+    opt = torch.optim.Adam(params, lr=lr, betas=(b1, b2), eps=eps)
+    first, ufirst = next(model.parameters()), next(updater.parameters())
+    gen = torch.Generator().manual_seed(5)
+    m0 = torch.randn(first.shape, generator=gen) * 1e-3
+    v0 = torch.rand(first.shape, generator=gen) * 1e-5 + 1e-7
+    t0 = 5
+    opt.state[first] = {"step": torch.tensor(float(t0)), "exp_avg": m0.clone(), "exp_avg_sq": v0.clone()}
+    before = [p.detach().clone() for p in params]
+    co.empty_train_step(model, updater, opt)
+    t = t0 + 1
+    m, v = b1 * m0.double(), b2 * v0.double()
+    want = (before[0].double() - lr / (1 - b1 ** t) * m / (v.sqrt() / math.sqrt(1 - b2 ** t) + eps)).float()
+    torch.testing.assert_close(first.detach(), want, rtol=1e-6, atol=1e-9)
+    assert not torch.equal(first.detach(), before[0])
+    st = opt.state[first]
+    assert float(st["step"]) == t
+    torch.testing.assert_close(st["exp_avg"], m.float(), rtol=1e-6, atol=0)
+    torch.testing.assert_close(st["exp_avg_sq"], v.float(), rtol=1e-6, atol=0)
+    assert float(opt.state[ufirst]["step"]) == 1
+    assert torch.equal(opt.state[ufirst]["exp_avg"], torch.zeros_like(ufirst))
+    for p, b in zip(params[1:], before[1:]):
+        assert torch.equal(p.detach(), b)
+        if p is not ufirst:
+            assert p.grad is None and p not in opt.state
