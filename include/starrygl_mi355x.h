@@ -573,6 +573,8 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  *   kind 1: rows*cols contiguous elements from off whose gradient is already
  *           in grad (Adam only). Tiles: ceil(rows*cols/256).
  * tile0 is the job's first tile; tile_job[t] the job of tile t (device).
+ * Which 16x16 block of its job a tile computes is the kernel's choice (the
+ * tiles that one XCD runs take a compact block of the grid).
  * Each gradient element is written once, then Adam-updated (torch.optim.Adam
  * arithmetic) if its segment `seg` is active: gates[seg] NULL or
  * *gates[seg] != 0, with the bias corrections coef[2*seg] = lr / (1 -

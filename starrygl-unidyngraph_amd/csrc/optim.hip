@@ -95,6 +95,26 @@ struct AdamSegs {
   const int32_t *gate[SGL_MAX_ADAM_SEGMENTS];
 };
 
+// The 16x16 tile (ta, tb) of an A x B tile grid that a job's tile `local`
+// computes. Workgroups are dealt to the XCDs in turn (workgroup w runs on
+// XCD w % 8), so a job's tiles with the same local % 8 share an XCD and its
+// L2: each such class takes a contiguous range of a banded order of the
+// grid (bands of h tile rows, column by column inside a band, h about
+// sqrt(A B / 8)), a compact block whose activation strips (one per tile row
+// and one per tile column) that XCD fetches once, instead of the scattered
+// tiles of the row-major order. A bijection for any A, B.
+__device__ __forceinline__ void grad_tile(int local, int A, int B, int &ta, int &tb) {
+  const int n = A * B, cls = local & 7, i = local >> 3;
+  int pos = i;
+  for (int c = 0; c < cls; ++c) pos += (n - c + 7) >> 3;   // the earlier classes' tiles
+  const int h = max(1, min(A, int(sqrtf(float(n) * 0.125f) + 0.5f)));
+  const int k = pos / (h * B);
+  const int p = pos - k * h * B;
+  const int hk = min(h, A - k * h);
+  ta = k * h + p % hk;
+  tb = p / hk;
+}
+
 __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__restrict__ jobs,
                                                        const int32_t *__restrict__ tile_job,
                                                        const int32_t *__restrict__ num_roots, float *__restrict__ p,
@@ -115,7 +135,8 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
   float gv = 0.f, pv = 0.f, mv = 0.f, vv = 0.f;
   int ea = 0, eb = 0;  // a kind-0 element's position in its block
   if (jb.kind == 0) {
-    const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
+    int ta, tb;
+    grad_tile(local, (jb.rows + 15) >> 4, jb.tiles_b, ta, tb);
     const int a0 = 16 * ta, b0 = 16 * tb;
     const int oa = tid >> 4, ob = tid & 15;
     ea = a0 + oa;

@@ -89,10 +89,8 @@ class ChunkedDraws:
     def _slot(self, m: int) -> DrawSlot:
         """The next ring buffer not reserved by the pending next-chunk draw,
         once the lookup that last read it is done (grown to m entries)."""
-        if len(self._ring) < self.ring_size:
-            slot = self.alloc(m)
-            self._ring.append(slot)
-            return slot
+        if not self._ring:   # the whole ring at once: a pinned allocation costs several steps' time
+            self._ring = [self.alloc(m) for _ in range(self.ring_size)]
         for _ in range(len(self._ring)):
             i = self._next
             self._next = (self._next + 1) % len(self._ring)

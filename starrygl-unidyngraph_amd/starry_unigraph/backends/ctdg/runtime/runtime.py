@@ -335,7 +335,9 @@ class CTDGOnlineRuntime:
         read in place by the device lookup through its device-visible
         address."""
         buf = torch.empty(max(m, 1), dtype=torch.long, pin_memory=True)
-        return DrawSlot(buf, None, _capi.host_device_pointer(buf))
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(self.device))   # created now, not on a later step
+        return DrawSlot(buf, done, _capi.host_device_pointer(buf))
 
     def _lookup(self, slot: DrawSlot, s: int, m: int) -> None:
         """The pool lookup and collision rule of the m draws in a ring

@@ -2,6 +2,8 @@
 CTDGSession (backends/ctdg/runtime/session.py:78-93: model + updater state
 dicts, strict loading), a load queued between asynchronous steps, and the
 step's metric dict computed on the device against scikit-learn."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -126,7 +128,9 @@ def test_device_metrics_match_sklearn(gpu):
 
 
 @pytest.mark.parametrize("P,N,ties", [(600, 600, "dup"), (4000, 4000, "dup"), (4000, 4000, "sat"), (3, 5000, "dup"),
-                                       (1000, 1, "none"), (1, 1, "none"), (600, 600, "all")])
+                                       (1000, 1, "none"), (1, 1, "none"), (600, 600, "all"), (2048, 2000, "dup"),
+                                       (2049, 150, "dup"), (600, 600, "narrow"), (3000, 1000, "tiny"),
+                                       (0, 10, "none"), (10, 0, "none")])
 def test_link_metrics_kernel_matches_sklearn(gpu, P, N, ties):
     """sgl_link_metrics (per positive, counts of the scores below, equal and
     above it over slices of the staged scores; a fixed-order sum of the
@@ -134,8 +138,10 @@ def test_link_metrics_kernel_matches_sklearn(gpu, P, N, ties):
     (runtime.py:202-214): AP and AUC to 1e-9, "mrr" to 1e-6; with tied
     scores (logits on a coarse grid, as the non-root negatives' shared zero
     embedding ties them; saturated logits whose sigmoids are all 1; every
-    score equal), unbalanced sizes and single elements. The
-    loss is copied through, and the ring takes consecutive calls in order."""
+    score equal), distinct scores packed close together (near 1, and below
+    2^-24), unbalanced sizes, single elements and an empty side (every
+    metric NaN). The loss is copied through, and the ring takes consecutive
+    calls in order."""
     from starry_unigraph.lib import _capi
     rng = np.random.default_rng(P + N)
     if ties == "none":
@@ -147,6 +153,12 @@ def test_link_metrics_kernel_matches_sklearn(gpu, P, N, ties):
         # cannot tie or untie two of them)
         pos = torch.from_numpy((rng.integers(-180, 220, P) / 64).astype(np.float32))
         neg = torch.from_numpy((rng.integers(-220, 180, N) / 64).astype(np.float32))
+    if ties == "narrow":   # sigmoids in (0.99995, 0.999994): one bucket, distinct values
+        pos = torch.from_numpy(rng.uniform(10.0, 12.0, P).astype(np.float32))
+        neg = torch.from_numpy(rng.uniform(10.0, 12.0, N).astype(np.float32))
+    elif ties == "tiny":   # sigmoids below 2^-24: one bucket, distinct values
+        pos = torch.from_numpy(rng.uniform(-30.0, -20.0, P).astype(np.float32))
+        neg = torch.from_numpy(rng.uniform(-31.0, -21.0, N).astype(np.float32))
     if ties == "sat":   # sigmoid(x) rounds to exactly 1 for x >= 20
         pos[: P // 4] = torch.from_numpy(rng.uniform(20.0, 40.0, P // 4).astype(np.float32))
         neg[: N // 8] = torch.from_numpy(rng.uniform(20.0, 40.0, N // 8).astype(np.float32))
@@ -165,6 +177,11 @@ def test_link_metrics_kernel_matches_sklearn(gpu, P, N, ties):
         _capi.check(_capi.lib().sgl_link_metrics(P, N, P_(pg), P_(ng), P_(loss), P_(seq), P_(ring), 3, P_(out),
                                                   P_(work), P_(done), _capi.stream_of(gpu)), "sgl_link_metrics")
     torch.cuda.synchronize()
+    if P == 0 or N == 0:
+        got = out.cpu().tolist()
+        assert got[0] == 1.25 and all(math.isnan(x) for x in got[1:]), got
+        assert int(seq.item()) == 4
+        return
     # the reference's scores: torch.sigmoid of the float32 logits on the device
     # (runtime.py:203-204; torch's CPU sigmoid can give one logit two values,
     # its vector and scalar paths rounding differently, which unties scores)
