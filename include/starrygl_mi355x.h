@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 17
+#define SGL_ABI_VERSION 18
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -539,6 +539,27 @@ int sgl_link_metrics(int32_t n_pos, int32_t n_neg, const float *pos_logits,
                      const float *neg_logits, const float *loss, uint64_t *seq,
                      double *ring, int32_t ring_slots, double *out,
                      double *work, uint32_t *done, hipStream_t stream);
+/* sgl_batch_prepare of a batch and sgl_link_metrics of an earlier step
+ * (its logits, loss and metric outputs: arrays the preparation neither
+ * reads nor writes) in one launch when the batch takes the one-workgroup
+ * preparation (up to 2048 events): the metrics' workgroups run beside the
+ * preparation's, after the same launch-plan gate. Larger batches make the
+ * two launches in order. Arguments: sgl_batch_prepare's, then
+ * sgl_link_metrics'. No counterpart in the reference (it computes the
+ * metrics on the host after every step); for callers that overlap a step's
+ * metrics with the next step's preparation. */
+int sgl_batch_prepare_metrics(int64_t num_nodes, int64_t batch, const int64_t *src,
+                              const int64_t *dst, const int64_t *neg, const float *ts,
+                              int64_t *cursor, int64_t *batch_start, uint32_t *node_bits,
+                              int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
+                              float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
+                              int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
+                              uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src,
+                              int32_t *cnt_dst, int32_t *any_edges, int32_t *err_flag,
+                              int32_t n_pos, int32_t n_neg, const float *pos_logits,
+                              const float *neg_logits, const float *loss, uint64_t *seq,
+                              double *ring, int32_t ring_slots, double *out, double *work,
+                              uint32_t *done, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Adam over a flat parameter segment (torch.optim.Adam arithmetic), for the

@@ -88,7 +88,7 @@ const OpEntry kOps[] = {
     SGL_OP(sgl_grad_adam), SGL_OP_GS(sgl_adam_coef, false, true), SGL_OP(sgl_edge_rows),
     SGL_OP(sgl_memory_update_bf16), SGL_OP(sgl_recent_sample_packed), SGL_OP(sgl_memory_gather),
     SGL_OP(sgl_negatives_from_draws), SGL_OP(sgl_time_projection_forward), SGL_OP(sgl_time_projection_backward),
-    SGL_OP(sgl_link_metrics),
+    SGL_OP(sgl_link_metrics), SGL_OP_GS(sgl_batch_prepare_metrics, true, false),
 };
 #undef SGL_OP
 #undef SGL_OP_GS

@@ -16,6 +16,7 @@
 #include <climits>
 
 #include "common.h"
+#include "metrics.h"
 #include "mfma.h"
 
 namespace {
@@ -317,7 +318,19 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     int32_t *__restrict__ ridx_src, int32_t *__restrict__ ridx_dst, int32_t *__restrict__ ridx_neg,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst, int32_t *__restrict__ any_edges,
-    int32_t *__restrict__ err, const uint32_t *gate_word, uint32_t gate_value, uint32_t *gate_timeout) {
+    int32_t *__restrict__ err, const uint32_t *gate_word, uint32_t gate_value, uint32_t *gate_timeout,
+    sgl::met::Args mr) {
+  if (blockIdx.x > 0) {
+    // the workgroups past the first: a previous step's link metrics
+    // (sgl_batch_prepare_metrics), which read only that step's logits and
+    // loss, after the same gate
+    if (gate_word != nullptr) {
+      if (threadIdx.x == 0) sgl::gate_wait(gate_word, gate_value, gate_timeout);
+      __syncthreads();
+    }
+    sgl::met::run(mr, blockIdx.x - 1, gridDim.x - 1);
+    return;
+  }
   extern __shared__ unsigned long long l_win[];                      // [2][cap]
   int32_t *l_cnt = reinterpret_cast<int32_t *>(l_win + 2 * cap);     // [2][cap]
   __shared__ int32_t s_scan[kPrepBlock / sgl::kWave];
@@ -1241,14 +1254,13 @@ extern "C" int64_t sgl_node_bits_words(int64_t num_nodes) {
   return num_nodes > 0 ? bitmap_words(num_nodes) + summary_words(num_nodes) : 0;
 }
 
-extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
-                                 const int64_t *neg, const float *ts, int64_t *cursor, int64_t *batch_start,
-                                 uint32_t *node_bits,
-                                 int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
-                                 float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
-                                 int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
-                                 uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src, int32_t *cnt_dst,
-                                 int32_t *any_edges, int32_t *err_flag, hipStream_t stream) {
+static int batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
+                         const int64_t *neg, const float *ts, int64_t *cursor, int64_t *batch_start,
+                         uint32_t *node_bits, int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
+                         float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts, int32_t *ridx_src,
+                         int32_t *ridx_dst, int32_t *ridx_neg, uint64_t *win_src, uint64_t *win_dst,
+                         int32_t *cnt_src, int32_t *cnt_dst, int32_t *any_edges, int32_t *err_flag,
+                         const sgl::met::Args *metrics, hipStream_t stream) {
   SGL_REQUIRE(num_nodes > 0 && num_nodes < INT_MAX, "batch_prepare: num_nodes %lld out of range", (long long)num_nodes);
   SGL_REQUIRE(batch >= 0 && batch < (INT_MAX / 2), "batch_prepare: batch %lld out of range", (long long)batch);
   SGL_REQUIRE(node_bits && word_prefix && num_roots && num_roots64 && ts_max && t_query && any_edges,
@@ -1261,16 +1273,21 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
   const int64_t cap = 2 * batch;
   const sgl::PlanGate gate = sgl::take_gate();  // a launch plan's gate (folded, or its own kernel first)
   if (batch <= kPrepMaxBatch) {
-    const size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
+    const sgl::met::Args none{};
+    const sgl::met::Args &mr = metrics != nullptr ? *metrics : none;
+    size_t lds = (2 * sizeof(unsigned long long) + 2 * sizeof(int32_t)) * size_t(cap > 0 ? cap : 1);
+    if (metrics != nullptr) lds = std::max(lds, sgl::met::lds_bytes(mr.P, mr.N));
+    const unsigned grid = 1u + (metrics != nullptr ? unsigned(sgl::met::blocks_for(mr.P)) : 0u);
     SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(&k_step_prepare_wg), lds));
-    sgl::launch(&k_step_prepare_wg, dim3(1), dim3(kPrepBlock), lds, stream, batch, num_nodes, cap, src, dst, neg, ts,
-                cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64, ts_max, t_query, roots, root_ts,
-                ridx_src, ridx_dst, ridx_neg, reinterpret_cast<unsigned long long *>(win_src),
+    sgl::launch(&k_step_prepare_wg, dim3(grid), dim3(kPrepBlock), lds, stream, batch, num_nodes, cap, src, dst, neg,
+                ts, cursor, batch_start, node_bits, word_prefix, num_roots, num_roots64, ts_max, t_query, roots,
+                root_ts, ridx_src, ridx_dst, ridx_neg, reinterpret_cast<unsigned long long *>(win_src),
                 reinterpret_cast<unsigned long long *>(win_dst), cnt_src, cnt_dst, any_edges, err_flag, gate.word,
-                gate.value, gate.timeout);
+                gate.value, gate.timeout, mr);
     SGL_CHECK_LAUNCH();
     return SGL_OK;
   }
+  SGL_REQUIRE(metrics == nullptr, "batch_prepare: metrics ride only on the one-workgroup preparation");
   if (gate.word != nullptr)
     if (int rc = sgl::launch_gate(gate, stream)) return rc;
   SGL_REQUIRE((reinterpret_cast<uintptr_t>(word_prefix) & 15u) == 0, "batch_prepare: word_prefix not 16-byte aligned");
@@ -1294,6 +1311,51 @@ extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t
     SGL_CHECK_LAUNCH();
   }
   return SGL_OK;
+}
+
+extern "C" int sgl_batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst,
+                                 const int64_t *neg, const float *ts, int64_t *cursor, int64_t *batch_start,
+                                 uint32_t *node_bits,
+                                 int32_t *word_prefix, int32_t *num_roots, int64_t *num_roots64,
+                                 float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts,
+                                 int32_t *ridx_src, int32_t *ridx_dst, int32_t *ridx_neg,
+                                 uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src, int32_t *cnt_dst,
+                                 int32_t *any_edges, int32_t *err_flag, hipStream_t stream) {
+  return batch_prepare(num_nodes, batch, src, dst, neg, ts, cursor, batch_start, node_bits, word_prefix, num_roots,
+                       num_roots64, ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg, win_src, win_dst,
+                       cnt_src, cnt_dst, any_edges, err_flag, nullptr, stream);
+}
+
+extern "C" int sgl_batch_prepare_metrics(
+    int64_t num_nodes, int64_t batch, const int64_t *src, const int64_t *dst, const int64_t *neg, const float *ts,
+    int64_t *cursor, int64_t *batch_start, uint32_t *node_bits, int32_t *word_prefix, int32_t *num_roots,
+    int64_t *num_roots64, float *ts_max, int64_t *t_query, int64_t *roots, int64_t *root_ts, int32_t *ridx_src,
+    int32_t *ridx_dst, int32_t *ridx_neg, uint64_t *win_src, uint64_t *win_dst, int32_t *cnt_src, int32_t *cnt_dst,
+    int32_t *any_edges, int32_t *err_flag, int32_t n_pos, int32_t n_neg, const float *pos_logits,
+    const float *neg_logits, const float *loss, uint64_t *seq, double *ring, int32_t ring_slots, double *out,
+    double *work, uint32_t *done, hipStream_t stream) {
+  SGL_REQUIRE(n_pos >= 0 && n_neg >= 0 && int64_t(n_pos) + n_neg <= SGL_LINK_METRICS_MAX_SCORES,
+              "batch_prepare_metrics: %d positive + %d negative scores (at most %d)", n_pos, n_neg,
+              SGL_LINK_METRICS_MAX_SCORES);
+  SGL_REQUIRE((n_pos == 0 || pos_logits) && (n_neg == 0 || neg_logits), "batch_prepare_metrics: NULL logits");
+  SGL_REQUIRE(ring == nullptr || (seq != nullptr && ring_slots > 0),
+              "batch_prepare_metrics: a ring needs seq and slots");
+  SGL_REQUIRE(ring != nullptr || out != nullptr, "batch_prepare_metrics: no metrics output");
+  SGL_REQUIRE(work != nullptr && done != nullptr, "batch_prepare_metrics: NULL work or done word");
+  if (batch > kPrepMaxBatch) {   // the multi-kernel preparation, then the metrics' own launch
+    if (int rc = batch_prepare(num_nodes, batch, src, dst, neg, ts, cursor, batch_start, node_bits, word_prefix,
+                               num_roots, num_roots64, ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg,
+                               win_src, win_dst, cnt_src, cnt_dst, any_edges, err_flag, nullptr, stream))
+      return rc;
+    return sgl_link_metrics(n_pos, n_neg, pos_logits, neg_logits, loss, seq, ring, ring_slots, out, work, done,
+                            stream);
+  }
+  const sgl::met::Args mr{int(n_pos), int(n_neg), pos_logits, neg_logits, loss,
+                          reinterpret_cast<unsigned long long *>(seq), ring, int(ring_slots), out, work,
+                          reinterpret_cast<unsigned int *>(done)};
+  return batch_prepare(num_nodes, batch, src, dst, neg, ts, cursor, batch_start, node_bits, word_prefix, num_roots,
+                       num_roots64, ts_max, t_query, roots, root_ts, ridx_src, ridx_dst, ridx_neg, win_src, win_dst,
+                       cnt_src, cnt_dst, any_edges, err_flag, &mr, stream);
 }
 
 extern "C" size_t sgl_memory_update_lds_bytes(int32_t D, int32_t F) {

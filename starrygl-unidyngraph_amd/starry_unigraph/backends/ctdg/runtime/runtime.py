@@ -530,9 +530,11 @@ class CTDGOnlineRuntime:
         advances). ``prev_metrics`` > 0: first the metrics of the previous
         step on these buffers (that many events), whose back part the
         preparation's wait has seen finish."""
-        step.prepare(src, dst, neg, ts, n=n, cursor=cursor)
-        if prev_metrics:
-            step.link_metrics(prev_metrics, self._metrics_seq, self.metrics_ring, self._metrics_work)
+        if prev_metrics:   # one launch (the metrics' workgroups beside the preparation's)
+            step.prepare_metrics(src, dst, neg, ts, n, cursor, prev_metrics, self._metrics_seq, self.metrics_ring,
+                                 self._metrics_work)
+        else:
+            step.prepare(src, dst, neg, ts, n=n, cursor=cursor)
         step.sample(self.sampler.device_sampler("test" if split == "predict" else split))
         if self._gru is not None:
             step.update_memory(self._gru, src, dst, ef, ts, from_cursor=cursor is not None)

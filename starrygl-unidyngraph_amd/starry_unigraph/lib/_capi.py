@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple] = {
     "sgl_node_bits_words": (_i64, [_i64]),
     "sgl_negatives_from_draws": (ctypes.c_int, [_i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
     "sgl_batch_prepare": (ctypes.c_int, [_i64, _i64] + [_vp] * 24),
+    "sgl_batch_prepare_metrics": (ctypes.c_int, [_i64, _i64] + [_vp] * 23 + [_i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                                                              _i32, _vp, _vp, _vp, _vp]),
     "sgl_memory_update_lds_bytes": (_sz, [_i32, _i32]),
     "sgl_memory_update_bf16_tile_rows": (_i32, [_i32, _i32, _i64]),
     "sgl_memory_update": (ctypes.c_int, [_i32, _i32, _i32, _i64] + [_vp] * 25),

@@ -352,6 +352,24 @@ class DeviceStep:
             P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
             self._s()), "sgl_batch_prepare"))
 
+    def prepare_metrics(self, src: torch.Tensor, dst: torch.Tensor, neg: torch.Tensor | None, ts: torch.Tensor,
+                        n: int, cursor: torch.Tensor | None, n_prev: int, seq: torch.Tensor, ring: torch.Tensor,
+                        work: tuple[torch.Tensor, torch.Tensor]) -> None:
+        """prepare() of this batch and, in the same launch, link_metrics() of
+        the step these buffers held before (its n_prev events' logits and
+        loss, which the preparation does not write): sgl_batch_prepare_metrics."""
+        b, st, P = self.buf, self.state, _capi.ptr
+        pb = b
+        if n > b.max_batch:
+            raise RuntimeError(f"batch of {n} events exceeds the step capacity {b.max_batch}")
+        self._call("batch_prepare", lambda: _capi.check(_capi.call("sgl_batch_prepare_metrics",
+            st.N, n, P(src), P(dst), P(neg), P(ts), P(cursor), P(b.batch_start) if cursor is not None else None,
+            P(st.node_bits), P(st.word_prefix), P(b.num_roots),
+            P(b.num_roots64), P(b.ts_max), P(b.t_query), P(b.roots), P(b.root_ts), P(b.ridx_src), P(b.ridx_dst),
+            P(b.ridx_neg), P(b.win_src), P(b.win_dst), P(b.cnt_src), P(b.cnt_dst), P(b.any_edges), P(b.err.t),
+            n_prev, n_prev, P(pb.pos), P(pb.neg), P(pb.loss), P(seq), P(ring), int(ring.shape[0]), None,
+            P(work[0]), P(work[1]), self._s()), "sgl_batch_prepare_metrics"))
+
     def sample(self, sampler: RecentSampler) -> PaddedHop:
         """Hop 0 of the roots at their query time, then every further hop
         from the previous hop's padded rows (its entries' nodes and times,

@@ -165,21 +165,32 @@ def _small_batch(rng, n_nodes, B, sorted_ts=True):
     return src, dst, ts, neg
 
 
-@pytest.mark.parametrize("B,sorted_ts,skew", [(600, True, False), (600, False, False), (4096, True, False),
-                                               (5000, False, False), (600, False, True), (20000, True, True),
-                                               (20000, False, True)])
-def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew):
+@pytest.mark.parametrize("B,sorted_ts,skew,metrics", [(600, True, False, False), (600, False, False, False),
+                                                       (4096, True, False, False), (5000, False, False, False),
+                                                       (600, False, True, False), (20000, True, True, False),
+                                                       (20000, False, True, False), (600, False, False, True),
+                                                       (2048, True, True, True), (5000, False, False, True)])
+def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew, metrics):
     """Roots, root indices, query time, per-role counts and last writers (in
     stable timestamp order) against numpy: the one-workgroup path (B <= 2048)
     and the multi-workgroup path, with sorted and unsorted timestamps; skewed
     batches (Zipf 1.5 node ids: a few roots in most events, many in each
-    wave, so the multi-workgroup path combines them per wave)."""
+    wave, so the multi-workgroup path combines them per wave). With
+    ``metrics`` the preparation carries the metrics of logits already in the
+    buffers (sgl_batch_prepare_metrics: one launch up to 2048 events, two
+    beyond): the same preparation, and the ring row equals sgl_link_metrics'
+    output on those logits."""
+    from starry_unigraph.lib import _capi
     from starry_unigraph.native.step import ConvDims, DeviceStep, NodeState
     rng = np.random.default_rng(B + skew)
     N = 5000
     st = NodeState(N, 8, 2, 4, gpu)
     step = DeviceStep(st, ConvDims(8, 4, 8, 2, 5), B)
-    for _ in range(3):
+    ring = torch.full((4, 4), float("nan"), dtype=torch.float64, device=gpu)
+    seq = torch.zeros(1, dtype=torch.int64, device=gpu)
+    work = (torch.zeros(int(_capi.lib().sgl_link_metrics_work_doubles(4096)), dtype=torch.float64, device=gpu),
+            torch.zeros(1, dtype=torch.int32, device=gpu))
+    for it in range(3):
         src, dst, ts, neg = _small_batch(rng, N, B, sorted_ts)
         if skew:
             src = np.minimum(rng.zipf(1.5, B) - 1, N - 1)
@@ -187,8 +198,24 @@ def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew):
             if not sorted_ts:   # negative and fractional times: t_query truncates toward zero
                 ts = ts - np.float32(25.5)
         T = lambda a, dt=torch.int64: torch.as_tensor(a, dtype=dt, device=gpu)
-        step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
         b = step.buf
+        if metrics:
+            n_prev = min(B, 3000) - 7 * it
+            b.pos[:n_prev].copy_(T(rng.normal(0.3, 1.0, n_prev), torch.float32))
+            b.neg[:n_prev].copy_(T((rng.integers(-100, 60, n_prev) / 32), torch.float32))   # ties
+            b.loss.fill_(0.5 + it)
+            step.prepare_metrics(T(src), T(dst), T(neg), T(ts, torch.float32), B, None, n_prev, seq, ring, work)
+            out = torch.zeros(4, dtype=torch.float64, device=gpu)
+            P_ = _capi.ptr
+            _capi.check(_capi.lib().sgl_link_metrics(n_prev, n_prev, P_(b.pos), P_(b.neg), P_(b.loss), None, None, 0,
+                                                      P_(out), P_(work[0]), P_(work[1]), _capi.stream_of(gpu)),
+                        "sgl_link_metrics")
+            torch.cuda.synchronize()
+            assert int(seq.item()) == it + 1 and int(work[1].item()) == 0
+            assert torch.equal(ring[it].cpu(), out.cpu()), (it, ring[it], out)
+            assert float(out[0].item()) == 0.5 + it
+        else:
+            step.prepare(T(src), T(dst), T(neg), T(ts, torch.float32))
         U = int(b.num_roots.item())
         roots = np.unique(np.concatenate([src, dst]))
         assert U == len(roots)
