@@ -181,7 +181,13 @@ __device__ __forceinline__ void run(const Args &a, unsigned b, unsigned nb) {
   const double ap = ok ? s_ap / double(P) : nan;
   const double auc = ok ? s_auc / pn : nan;
   const double mrr = ok ? double(float(s_mrr) / float(pn)) : nan;
-  const double l = a.loss != nullptr ? double(*a.loss) : nan;
+  // (the loss may come from another stream's work, ordered by a gate folded
+  // into the kernel: an atomic load, never a scalar load issued before the
+  // wait or served from the scalar cache)
+  const double l =
+      a.loss != nullptr ? double(__hip_atomic_load(const_cast<float *>(a.loss), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT))
+                        : nan;
   if (a.out != nullptr) {
     a.out[0] = l;
     a.out[1] = ap;

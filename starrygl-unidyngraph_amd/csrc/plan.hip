@@ -20,6 +20,11 @@
 // (a back part's number is stored by the next back part's first kernel, once
 // every earlier kernel of the back stream is done)
 //
+// A gate is folded only into a kernel of few workgroups (the batch
+// preparation): the workgroups of a large kernel waiting at a gate can hold
+// every CU, so that the other stream's work they wait for cannot run (a
+// folded gate in the attention forward timed out that way).
+//
 // Plain launches cost the GPU well under a microsecond between kernels; the
 // same kernels replayed as graphs cost several, and more at graph
 // boundaries; the signal / wait kernels cost less than ROCm's stream memory
