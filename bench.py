@@ -462,16 +462,18 @@ def _restore(rt, snap):
 # profiles/tgn_cfg4_hbm_traffic.md and profiles/sampler_cfg3_hbm_traffic.md
 # (counters scaled by a copy kernel of known size); None where no counter run
 # was made.
-HBM_TRAFFIC = {("cfg4", "bf16", "conv_backward"): round((2 * 2109.8 + 1506.1) * 1024),
-               ("cfg4", "bf16", "edge_rows"): round((2 * 128.7 + 291.1) * 1024),
-               ("cfg4", "bf16", "memory_commit"): round((2 * 79.0 + 94.3) * 1024),
-               ("cfg4", "bf16", "conv_forward"): round((2 * 1253.8 + 1880.2) * 1024),
-               ("cfg4", "bf16", "memory_update"): round((2 * 1397.3 + 301.0) * 1024),
-               ("cfg4", "bf16", "predictor"): round((2 * 450.4 + 569.4) * 1024),
-               ("cfg4", "bf16", "param_update"): round((2 * 8026.5 + 2647.2) * 1024),
-               ("cfg4", "bf16", "batch_prepare"): round((2 * 63.6 + 128.2) * 1024),
-               ("cfg4", "bf16", "recent_sample"): round((2 * 380.8 + 22.1) * 1024),
-               ("cfg3", "int64", "recent_sample"): round((2 * 1342192 + 449830) * 1024)}
+HBM_TRAFFIC = {  # cfg4: read requests x their sizes (32/64/128 B) + write requests x theirs (64/32 B)
+    ("cfg4", "bf16", "conv_backward"): 64 * 5457 + 128 * 27837 + 64 * 23700 + 32 * (24501 - 23700),
+    ("cfg4", "bf16", "edge_rows"): 64 * 347 + 128 * 1554 + 64 * 4203 + 32 * (4804 - 4203),
+    ("cfg4", "bf16", "memory_commit"): 64 * 291 + 128 * 872 + 64 * 1195 + 32 * (1823 - 1195),
+    ("cfg4", "bf16", "conv_forward"): 64 * 5314 + 128 * 14433 + 64 * 29426 + 32 * (30224 - 29426),
+    ("cfg4", "bf16", "memory_update"): 64 * 2679 + 128 * 23921 + 64 * 4519 + 32 * (5112 - 4519),
+    ("cfg4", "bf16", "predictor"): 64 * 2514 + 128 * 4294 + 64 * 8165 + 32 * (10028 - 8165),
+    ("cfg4", "bf16", "param_update"): 64 * 1267 + 128 * 83329 + 64 * 27770 + 32 * (44781 - 27770),
+    ("cfg4", "bf16", "batch_prepare"): 64 * 130 + 128 * 1307 + 64 * 692 + 32 * (3410 - 692),
+    ("cfg4", "bf16", "recent_sample"): 64 * 475 + 128 * 5557 + 64 * 119 + 32 * (584 - 119),
+    ("cfg4", "bf16", "link_metrics"): 64 * 1099 + 128 * 307 + 64 * 3 + 32 * (25 - 3),
+    ("cfg3", "int64", "recent_sample"): round((2 * 1342192 + 449830) * 1024)}
 # the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
 TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
 
@@ -628,17 +630,22 @@ def run_tgn(args, wl: dict) -> dict:
         rt.plan_timer = (ENTRY_POINTS[dom], next_pair)
     torch.cuda.synchronize()
     gc.disable()   # no collector pauses on the host inside the timed region
+    waited0 = rt._draws.wait_s
     w0 = time.perf_counter()
     out = None
     for b in batches:
         out = rt.train_step(b)
     host = time.perf_counter() - w0
+    # the host blocks only when it runs a full draw ring (32 steps) ahead of the GPU
+    waited = rt._draws.wait_s - waited0
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     gc.enable()
     rt.plan_timer = None
     rt.check_sync()
-    log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step (the rest is the GPU draining its queue)")
+    log(f"host-side loop {host * 1e6 / args.steps:.1f} us/step, of which {waited * 1e6 / args.steps:.1f} waiting "
+        f"for the GPU (a full draw ring ahead of it): {(host - waited) * 1e6 / args.steps:.1f} us/step of host "
+        f"work (the rest is the GPU draining its queue)")
     events = sum(b.size for b in batches)
     # every timed step's (loss, AP, AUC, "mrr"), computed on the device at the end
     # of its back part (sgl_link_metrics) inside the timed region; read once here

@@ -21,6 +21,7 @@ is reserved until its lookup is issued, so no other chunk is drawn into it.
 """
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass
 from typing import Any, Callable
 
@@ -79,6 +80,7 @@ class ChunkedDraws:
         self.ring_size = ring
         self._ring: list[DrawSlot] = []
         self._next = 0
+        self.wait_s = 0.0   # host seconds spent waiting for a ring buffer's lookup to finish
         self._cur: _Chunk | None = None
         self._pre: _PreDraw | None = None
 
@@ -97,7 +99,9 @@ class ChunkedDraws:
             slot = self._ring[i]
             if self._pre is not None and slot is self._pre.slot:
                 continue
+            t0 = time.perf_counter()
             slot.wait()
+            self.wait_s += time.perf_counter() - t0
             if slot.buf.numel() < m:
                 slot = self._ring[i] = self.alloc(m)
             return slot
