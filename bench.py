@@ -18,14 +18,16 @@ Prints ONE JSON line. Workloads:
              (1,140,149 nodes, D = 172, K = 4, F = 16) under batches of 600, 4,000
              and 1,048,576 events of the config-4 stream: batch preparation,
              sampling (k = 20), GRU + mailbox, memory commit, edge-row gather.
-The default run also measures config 3 and reports it under "sampler", and the
-gather/scatter microbench under "gather_scatter".
+The default run also measures config 3 and reports it under "sampler", the
+gather/scatter microbench under "gather_scatter", and short runs of configs 1,
+2, 5 and of config 4 with dropout 0.1 under "configs".
 
 Timed region: W untimed warm-up steps, then K steps bracketed by
 torch.cuda.synchronize(); value = events / s over the K steps. The event
 stream and node state are resident in HBM before the timed region; each
 step draws its negatives inside it (the runtime draws a few consecutive
-batches' negatives per CPU call and looks them up on the device).
+batches' negatives per CPU call and looks them up on the device) and
+computes its (loss, AP, AUC, "mrr") on the device ("step_metrics").
 The node state and optimizer are then restored and the same K steps are
 replayed with HIP events around every library call (per-kernel breakdown and
 the algorithmic work of the dominant kernel); the dominant kernel's events are
