@@ -264,17 +264,17 @@ struct FwdLds {
   float *part;  // [NW][H*C]  a slice's unnormalised sums (slices only)
   float *pml;   // [NW][H][3] a slice's running max, sum and kept sum (slices only)
   float *scr;   // [NW][4][64] partial sums of the four-row products (4-root tiles only)
-  float *DT;    // [rows][k] the tile's edges' dt (16-wave 8-root instances: stage_dt)
+  float *DT;    // [rows][k] the tile's edges' dt (16-wave instances: stage_dt)
   float *Ts;    // [ts_rows][T] the tile's edges' time encodings (cos), when staged
 };
 
 // 16-wave instances encode the tile's edges' times beside the Q product, on
-// the waves Q leaves idle. With 8 roots a tile (the split-head instances:
-// 8 roots x k edges x T columns on five or so waves, tens of elements per
-// thread) the loop's per-element dt loads form a chain of dependent round
-// trips, so the tile's dt rows are staged in LDS with the setup loads; with
-// 4 roots the loop is a few elements per thread and its dt loads hit in L1.
-__host__ __device__ constexpr bool stage_dt(int nw, int rows) { return nw == 16 && rows == 8; }
+// the waves Q leaves idle, one edge slot per wave at a time (lanes over the T
+// columns: the slot's index arithmetic is scalar, no per-element division).
+// The tile's dt rows are staged in LDS with the setup loads, so the loop
+// waits on no global load (each such wait would also wait for the loop's
+// earlier stores: loads and stores share one in-order counter).
+__host__ __device__ constexpr bool stage_dt(int nw, int rows) { return nw == 16 && rows > 0; }
 
 __host__ __device__ inline FwdLds fwd_lds(const Dims &d, float *base, int nw, int rows, bool slices) {
   FwdLds L;
@@ -406,16 +406,24 @@ __global__ __launch_bounds__(NW * 64) void k_conv_fwd(
   }
   if (kPre) {
     const int qwaves = min(kWaves - 1, (D + 15) / 16);
-    const int nthr = (kWaves - qwaves) * 64;
-    for (int idx = tid - qwaves * 64; idx >= 0 && idx < RPW * K * T; idx += nthr) {
-      const int el = idx / T, t = idx - el * T, i = el / K, e = el - i * K;
-      if (e < s_cnt[i]) {
-        const size_t row = size_t(r0 + i) * K + e;
-        float sn, cs;
-        te_sincos(te_arg(stage_dt(NW, RPW) ? L.DT[el] : dt[row], L.TW[t], L.TB[t]), sn, cs);
-        if (staged) L.Ts[el * T + t] = cs;
-        X[row * C + D + d.F + t] = cs;
-        S[row * T + t] = sn;
+    // wave tw takes edge slots el = tw, tw + ntw, ... (el = i * K + e)
+    const int ntw = kWaves - qwaves, tw = wave - qwaves;
+    if (tw >= 0 && K > 0) {
+      int i = tw / K, e = tw - (tw / K) * K;
+      for (int el = tw; el < RPW * K; el += ntw) {
+        if (e < s_cnt[i]) {
+          const size_t row = size_t(r0 + i) * K + e;
+          const float dtv = stage_dt(NW, RPW) ? L.DT[el] : dt[row];
+          for (int t = lane; t < T; t += 64) {
+            float sn, cs;
+            te_sincos(te_arg(dtv, L.TW[t], L.TB[t]), sn, cs);
+            if (staged) L.Ts[el * T + t] = cs;
+            X[row * C + D + d.F + t] = cs;
+            S[row * T + t] = sn;
+          }
+        }
+        e += ntw;
+        while (e >= K) { e -= K; ++i; }
       }
     }
   }
