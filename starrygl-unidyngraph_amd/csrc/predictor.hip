@@ -262,7 +262,6 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       sgl::atomic_add_fixed(&acc_out[D], sgl::to_fixed_checked(gb, range_flag));
     }
     // hidden-layer gradients, summed into their roots' rows
-    const int U = *num_roots;
     for (int idx = tid; idx < kRows * D; idx += kBlock) {
       const int i = idx / D, j = idx - i * D;
       if (i >= nrows) continue;
@@ -285,43 +284,48 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       if (c >= 0) sgl::atomic_add_fixed(&acc_n[size_t(c) * D + j], fn);
       else if (fn != 0) atomicAdd(reinterpret_cast<unsigned long long *>(&Nul[j]), static_cast<unsigned long long>(fn));
     }
-    __syncthreads();
-    if (agg) {  // one global atomic per (root in the tile, column)
-      for (int k = tid; k < 3 * kRows * D; k += kBlock) {
-        const int e = k / D, j = k - e * D;
-        if (s_lead[e] != (e < kRows ? e : e - kRows)) continue;  // not a leader, or no root
-        const long long v = Gs[k];
-        if (v == 0) continue;
-        if (e < kRows) {
-          sgl::atomic_add_fixed(&acc_src[size_t(s_idx[0][e]) * D + j], v);
-        } else {
-          const int t = e - kRows;
-          sgl::atomic_add_fixed(&((t & 1) ? acc_n : acc_dst)[size_t(s_idx[1 + (t & 1)][t >> 1]) * D + j], v);
-        }
-      }
-    }
-    for (int j = tid; j < D; j += kBlock)
-      if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_n[size_t(U) * D + j], Nul[j]);
   }
-  // the last workgroup to finish turns the accumulated sums into the outputs
-  // and clears the accumulator and the counter for the next launch. The sums
-  // only ever change by atomics, which are performed at the device's
-  // coherence point: a workgroup waits for its own atomics to complete
-  // before it counts itself done, and the last one reads the sums with
-  // atomics too, so no cache writeback is needed.
+  // The last workgroup to finish its loss and out_fc sums turns them into the
+  // outputs and clears the accumulator and the counter for the next launch.
+  // The sums only ever change by atomics, which are performed at the
+  // device's coherence point: a workgroup waits for its own atomics to
+  // complete before it counts itself done, and the last one reads the sums
+  // with atomics too, so no cache writeback is needed. With the per-root
+  // sums aggregated in LDS (agg), the wait comes before their global atomics
+  // (the attention backward, the next kernel, is their only reader), so the
+  // count and the conversion overlap them.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) s_last = sgl::last_block(done);
   __syncthreads();
-  if (!s_last) return;
-  auto take = [&](int k) {
-    return sgl::from_fixed(static_cast<long long>(atomicExch(reinterpret_cast<unsigned long long *>(&acc_out[k]), 0ull)));
-  };
-  if (train) {
-    for (int j = tid; j < D; j += kBlock) g_wo[j] = take(j);
-    if (tid == 64) g_bo[0] = take(D);
+  if (s_last) {
+    auto take = [&](int k) {
+      return sgl::from_fixed(static_cast<long long>(atomicExch(reinterpret_cast<unsigned long long *>(&acc_out[k]), 0ull)));
+    };
+    if (train) {
+      for (int j = tid; j < D; j += kBlock) g_wo[j] = take(j);
+      if (tid == 64) g_bo[0] = take(D);
+    }
+    if (tid == 0) *loss = float(double(take(D + 1)) / double(batch));
   }
-  if (tid == 0) *loss = float(double(take(D + 1)) / double(batch));
+  if (!train) return;  // uniform
+  if (agg) {  // one global atomic per (root in the tile, column)
+    for (int k = tid; k < 3 * kRows * D; k += kBlock) {
+      const int e = k / D, j = k - e * D;
+      if (s_lead[e] != (e < kRows ? e : e - kRows)) continue;  // not a leader, or no root
+      const long long v = Gs[k];
+      if (v == 0) continue;
+      if (e < kRows) {
+        sgl::atomic_add_fixed(&acc_src[size_t(s_idx[0][e]) * D + j], v);
+      } else {
+        const int t = e - kRows;
+        sgl::atomic_add_fixed(&((t & 1) ? acc_n : acc_dst)[size_t(s_idx[1 + (t & 1)][t >> 1]) * D + j], v);
+      }
+    }
+  }
+  const int U = *num_roots;
+  for (int j = tid; j < D; j += kBlock)
+    if (Nul[j] != 0) sgl::atomic_add_fixed(&acc_n[size_t(U) * D + j], Nul[j]);
 }
 
 }  // namespace
