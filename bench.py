@@ -471,7 +471,7 @@ HBM_TRAFFIC = {  # cfg4: read requests x their sizes (32/64/128 B) + write reque
     ("cfg4", "bf16", "conv_forward"): 64 * 5314 + 128 * 14433 + 64 * 29426 + 32 * (30224 - 29426),
     ("cfg4", "bf16", "memory_update"): 64 * 2679 + 128 * 23921 + 64 * 4519 + 32 * (5112 - 4519),
     ("cfg4", "bf16", "predictor"): 64 * 2514 + 128 * 4294 + 64 * 8165 + 32 * (10028 - 8165),
-    ("cfg4", "bf16", "param_update"): 64 * 1267 + 128 * 83329 + 64 * 27770 + 32 * (44781 - 27770),
+    ("cfg4", "bf16", "param_update"): 64 * 974 + 128 * 31057 + 64 * 30950 + 32 * (34587 - 30950),
     ("cfg4", "bf16", "batch_prepare"): 64 * 130 + 128 * 1307 + 64 * 692 + 32 * (3410 - 692),
     ("cfg4", "bf16", "recent_sample"): 64 * 475 + 128 * 5557 + 64 * 119 + 32 * (584 - 119),
     ("cfg4", "bf16", "link_metrics"): 64 * 1099 + 128 * 307 + 64 * 3 + 32 * (25 - 3),

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 18
+#define SGL_ABI_VERSION 19
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -586,16 +586,24 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * A job (device array) is one of:
  *   kind 0: a gradient block G[a][b] = sum_{p<npass} sum_{r<R}
  *           x1[p*ps1 + r*s1 + a] * x2[p*ps2 + r*s2 + b] for a < rows,
- *           b < cols, stored at grad[off + a*ldo + b]; R is r_fixed, or
- *           *num_roots + r_extra when r_fixed < 0; npass 0 counts as 1 (the
- *           passes of a dropout step). s1 >= rows (s2 may be 0: a broadcast
- *           row). Tiles: ceil(rows/16) * ceil(cols/16), tiles_b =
- *           ceil(cols/16).
+ *           b < cols, stored at grad[off + a*ldo + b]; R is r_fixed when
+ *           r_fixed >= 0, *num_roots + r_extra when r_fixed == -1, and
+ *           ceil(*num_roots / -r_fixed) when r_fixed <= -2 (per-tile partial
+ *           sums of tiles of -r_fixed roots: the tiles holding live roots);
+ *           npass 0 counts as 1 (the passes of a dropout step). s1 >= rows
+ *           (s2 may be 0: a broadcast row). Tiles: ceil(rows/16) *
+ *           ceil(cols/16), tiles_b = ceil(cols/16); the job's tile l is the
+ *           16x16 block (l / tiles_b, l % tiles_b).
  *   kind 1: rows*cols contiguous elements from off whose gradient is already
- *           in grad (Adam only). Tiles: ceil(rows*cols/256).
- * tile0 is the job's first tile; tile_job[t] the job of tile t (device).
- * Which 16x16 block of its job a tile computes is the kernel's choice (the
- * tiles that one XCD runs take a compact block of the grid).
+ *           in grad (Adam only). Tiles: ceil(rows*cols/256), tile l the
+ *           elements from l*256.
+ * tile_job (device, num_tiles entries, one workgroup each) holds for
+ * workgroup t the job index in bits 0-7 and the tile's index l within its
+ * job in bits 8-30, or -1 for no tile; every tile of every job appears
+ * once. Workgroup t runs on XCD t % 8, so the table decides which XCD's L2
+ * fetches a job's activation strips: starry_unigraph.native.step.xcd_tile_deal
+ * gives each job's tiles to one XCD where the per-XCD share allows. The
+ * jobs' tile0 field is not read.
  * Each gradient element is written once, then Adam-updated (torch.optim.Adam
  * arithmetic) if its segment `seg` is active: gates[seg] NULL or
  * *gates[seg] != 0, with the bias corrections coef[2*seg] = lr / (1 -

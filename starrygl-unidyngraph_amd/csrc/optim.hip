@@ -95,24 +95,23 @@ struct AdamSegs {
   const int32_t *gate[SGL_MAX_ADAM_SEGMENTS];
 };
 
-// The 16x16 tile (ta, tb) of an A x B tile grid that a job's tile `local`
-// computes. Workgroups are dealt to the XCDs in turn (workgroup w runs on
-// XCD w % 8), so a job's tiles with the same local % 8 share an XCD and its
-// L2: each such class takes a contiguous range of a banded order of the
-// grid (bands of h tile rows, column by column inside a band, h about
-// sqrt(A B / 8)), a compact block whose activation strips (one per tile row
-// and one per tile column) that XCD fetches once, instead of the scattered
-// tiles of the row-major order. A bijection for any A, B.
-__device__ __forceinline__ void grad_tile(int local, int A, int B, int &ta, int &tb) {
-  const int n = A * B, cls = local & 7, i = local >> 3;
-  int pos = i;
-  for (int c = 0; c < cls; ++c) pos += (n - c + 7) >> 3;   // the earlier classes' tiles
-  const int h = max(1, min(A, int(sqrtf(float(n) * 0.125f) + 0.5f)));
-  const int k = pos / (h * B);
-  const int p = pos - k * h * B;
-  const int hk = min(h, A - k * h);
-  ta = k * h + p % hk;
-  tb = p / hk;
+// A tile's entry of tile_job: its job in the low 8 bits and its index among
+// the job's tiles above them (-1: no tile). The host deals each job's tiles
+// to one XCD where it can (workgroup w runs on XCD w % 8) and splits the
+// larger ones into ranges of consecutive tiles, so that the activation
+// strips a job reads are fetched into few XCDs' L2s. A kind-0 job's tile l
+// computes the 16x16 block (l / tiles_b, l % tiles_b): a range of them is a
+// band of block rows, which shares the x1 strips of its rows.
+__device__ __forceinline__ int tile_entry_job(int32_t e) { return e & 0xFF; }
+__device__ __forceinline__ int tile_entry_local(int32_t e) { return e >> 8; }
+
+// The reduction length of a kind-0 job: r_fixed; *num_roots + r_extra when
+// r_fixed == -1; the tiles of -r_fixed rows that hold live rows when
+// r_fixed <= -2 (per-tile partial sums; the rest are zero).
+__device__ __forceinline__ int job_rows(const sgl_grad_job &jb, const int32_t *num_roots) {
+  if (jb.r_fixed >= 0) return jb.r_fixed;
+  if (jb.r_fixed == -1) return *num_roots + jb.r_extra;
+  return (*num_roots - jb.r_fixed - 1) / (-jb.r_fixed);
 }
 
 __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__restrict__ jobs,
@@ -124,9 +123,10 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
                                                        float wd, uint16_t *__restrict__ shadow) {
   __shared__ float red[4][16][17];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int t = blockIdx.x;
-  const sgl_grad_job jb = jobs[tile_job[t]];
-  const int local = t - jb.tile0;
+  const int32_t entry = tile_job[blockIdx.x];
+  if (entry < 0) return;  // uniform: a padding slot of the XCD deal
+  const sgl_grad_job jb = jobs[tile_entry_job(entry)];
+  const int local = tile_entry_local(entry);
   const bool active = segs.gate[jb.seg] == nullptr || *segs.gate[jb.seg] != 0;
   const float step_size = coef[2 * jb.seg], bc2_sqrt = coef[2 * jb.seg + 1];
 
@@ -135,8 +135,7 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
   float gv = 0.f, pv = 0.f, mv = 0.f, vv = 0.f;
   int ea = 0, eb = 0;  // a kind-0 element's position in its block
   if (jb.kind == 0) {
-    int ta, tb;
-    grad_tile(local, (jb.rows + 15) >> 4, jb.tiles_b, ta, tb);
+    const int ta = local / jb.tiles_b, tb = local - ta * jb.tiles_b;
     const int a0 = 16 * ta, b0 = 16 * tb;
     const int oa = tid >> 4, ob = tid & 15;
     ea = a0 + oa;
@@ -149,7 +148,7 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
       mv = m[idx];
       vv = v[idx];
     }
-    const int R = jb.r_fixed >= 0 ? jb.r_fixed : *num_roots + jb.r_extra;
+    const int R = job_rows(jb, num_roots);
     const int i16 = lane & 15, q = lane >> 4;
     sgl::f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const int npass = jb.npass > 0 ? jb.npass : 1;
@@ -214,9 +213,11 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_shadows(const sgl_grad_job *_
                                                           const int32_t *__restrict__ tile_job,
                                                           const float *__restrict__ p,
                                                           uint16_t *__restrict__ shadow) {
-  const sgl_grad_job jb = jobs[tile_job[blockIdx.x]];
+  const int32_t entry = tile_job[blockIdx.x];
+  if (entry < 0) return;
+  const sgl_grad_job jb = jobs[tile_entry_job(entry)];
   if (jb.kind != 0 || (jb.sh_off < 0 && jb.sht_off < 0)) return;
-  const int local = int(blockIdx.x) - jb.tile0;
+  const int local = tile_entry_local(entry);
   const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
   const int ea = 16 * ta + (threadIdx.x >> 4), eb = 16 * tb + (threadIdx.x & 15);
   if (ea >= jb.rows || eb >= jb.cols) return;

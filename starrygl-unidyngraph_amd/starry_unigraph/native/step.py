@@ -34,6 +34,35 @@ def _round_up(x: int, m: int) -> int:
     return (x + m - 1) // m * m
 
 
+def xcd_tile_deal(counts: list[int], xcds: int = 8) -> list[int]:
+    """The tile_job table of sgl_grad_adam / sgl_grad_shadows for jobs of
+    ``counts`` tiles: entry t (workgroup t, which runs on XCD t % xcds) is
+    job | (index among the job's tiles << 8), or -1 for a padding slot. Each
+    XCD takes at most ceil(total / xcds) tiles; the jobs go, largest first, to
+    the XCD with the fewest tiles, a job that does not fit split into ranges
+    of consecutive tiles, so that most jobs' activation strips are fetched by
+    one XCD's L2."""
+    if len(counts) > 256:
+        raise ValueError("xcd_tile_deal: more than 256 jobs")
+    total = sum(counts)
+    if total == 0:
+        return []
+    cap = -(-total // xcds)
+    bins: list[list[int]] = [[] for _ in range(xcds)]
+    for job in sorted(range(len(counts)), key=lambda k: (-counts[k], k)):
+        local, left = 0, counts[job]
+        if left >= 1 << 23:
+            raise ValueError("xcd_tile_deal: a job of more than 2^23 tiles")
+        while left > 0:
+            b = min(range(xcds), key=lambda k: (len(bins[k]), k))
+            take = min(left, cap - len(bins[b]))
+            bins[b].extend(job | (loc << 8) for loc in range(local, local + take))
+            local += take
+            left -= take
+    n = max(len(b) for b in bins)
+    return [bins[t % xcds][t // xcds] if t // xcds < len(bins[t % xcds]) else -1 for t in range(n * xcds)]
+
+
 class NodeState:
     """Per-node memory and K-slot mailbox in HBM (memory.py:98-102):
     memory [N,D] f32 = 0, mailbox [N,K,2D+F] f32 = 0, mailbox_ts [N,K] = 0,
@@ -271,7 +300,8 @@ class Bf16Shadow:
             arr = (_capi.GradJob * len(jobs))(*jobs)
             dev = self.buf.device
             raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8).to(dev)
-            self._refresh = (key, raw, torch.as_tensor(tiles, dtype=torch.int32, device=dev), len(tiles), base)
+            deal = xcd_tile_deal([tiles.count(k) for k in range(len(jobs))])
+            self._refresh = (key, raw, torch.as_tensor(deal, dtype=torch.int32, device=dev), len(deal), base)
         _, raw, tiles, nt, base = self._refresh
         _capi.check(_capi.lib().sgl_grad_shadows(raw.data_ptr(), tiles.data_ptr(), nt, base, self.buf.data_ptr(),
                                                  _capi.stream_of(self.buf.device)), "sgl_grad_shadows")
@@ -619,8 +649,9 @@ class StepParamUpdate:
         arr = (_capi.GradJob * len(jobs))(*jobs)
         raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
         self.jobs = raw.to(dev)
-        self.tile_job = torch.as_tensor(tiles, dtype=torch.int32, device=dev)
-        self.num_tiles = len(tiles)
+        deal = xcd_tile_deal([tiles.count(k) for k in range(len(jobs))])
+        self.tile_job = torch.as_tensor(deal, dtype=torch.int32, device=dev)
+        self.num_tiles = len(deal)
         P = _capi.ptr
         self._steps = (ctypes.c_void_p * len(opt.segments))(*[P(seg[2]) for seg in opt.segments])
         if len(gates) != len(opt.segments):
@@ -691,8 +722,10 @@ class StepParamUpdate:
             self._pred_jobs(gemm, add, at, off, one, pred_params, 1)
             return self._check(jobs, tiles, conv_params, pred_params)
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
-        conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
-        conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=ntiles)
+        # per-tile partials: the tiles holding live rows (the others' are zero)
+        rt = -b.conv_rows
+        conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=rt)
+        conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=rt)
         conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D, shd=shf("w_q"))
         conv(at(b.gQ), D, at(b.phi0), 0, off(w_q) + D, D + T, D, T, x1w=c * D, shd=shf("w_q", col0=D))
         conv(at(b.gQ), D, one, 0, off(b_q), 1, D, 1, x1w=c * D)
@@ -710,8 +743,8 @@ class StepParamUpdate:
         conv(at(b.gz), D, at(b.agg), D, off(w_out), 2 * D, D, D, x1w=c * D, x2w=c * D, shd=shf("w_out"))
         conv(at(b.gz), D, at(b.new_mem), D, off(w_out) + D, 2 * D, D, D, x1w=c * D, shd=shf("w_out", col0=D))
         conv(at(b.gz), D, one, 0, off(b_out), 1, D, 1, x1w=c * D)
-        conv(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
-        conv(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=ntiles)
+        conv(at(b.ln_part), 2 * D, one, 0, off(ln_g), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=rt)
+        conv(at(b.ln_part, D), 2 * D, one, 0, off(ln_b), 1, D, 1, x1w=ntiles * 2 * D, r_fixed=rt)
         # edge predictor: src_fc / dst_fc as reductions over roots 0..U (row U
         # of g_dst holds the non-root negatives; y's row U is zero); out_fc's
         # gradients come from sgl_predictor (Adam only). With dropout dst_fc
