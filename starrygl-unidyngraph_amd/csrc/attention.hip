@@ -1,5 +1,6 @@
 // TGN temporal attention (TimeEncode + TemporalTransformerConv), forward and
-// backward, one workgroup (8 or 16 waves) per tile of 4 or 8 roots.
+// backward, one workgroup (8 or 16 waves) per tile of 4 or 8 roots (the
+// 16-wave bf16 forward: one root).
 //
 // Reference: TemporalTransformerConv.forward  backends/ctdg/runtime/models.py:77-137,
 //            build_dgl_block                  models.py:144-197,
@@ -24,9 +25,9 @@
 // edge, in the padded sampler layout [root][slot], so the attention kernels
 // read each edge's row contiguously instead of chasing (nbr, eid) to the
 // memory table. The forward fills in the rows' time-encoding columns (they
-// depend on trained parameters) and saves the sines for the backward. A workgroup takes few roots (RPW = 4 or 8;
-// the MFMA tiles keep 16 rows, zero-padded), so a launch spreads over U/RPW
-// workgroups. The GEMMs issue all weight loads of a block at once (mfma.h).
+// depend on trained parameters) and saves the sines for the backward. A
+// workgroup takes few roots (RPW = 1, 4 or 8; the MFMA tiles keep 16 rows,
+// zero-padded), so a launch spreads over U/RPW workgroups. The GEMMs issue all weight loads of a block at once (mfma.h).
 // In the edge phase WPR = waves / RPW waves share a root: each takes a
 // contiguous slice of the window and reads the rows of 4 edges per round
 // trip, with its own online softmax (running max, running sum); the slices
@@ -1309,11 +1310,17 @@ template <int HM, int JM>
 struct BwdPick {
   static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
-// the bf16-product instances (no dropout)
+// the bf16-product instances (no dropout). The 16-wave forward takes one
+// root per workgroup (its 16 waves split the root's window): the products'
+// 16-row tiles cost the same for 1 root as for 4, and the per-root phases
+// (time encodings, edge windows, LayerNorm) shrink with the roots a
+// workgroup holds (config 4: 22.4 -> 20.2 us; 2 roots: 20.9). The forward
+// writes no per-tile partials, so its rows need not match the backward's.
 template <int HM, int JM>
 struct FwdPickBf {
   static Instance<FwdFn> get() {
     if constexpr (split_heads(HM, JM)) return {&k_conv_fwd<HM, JM, false, true, 16, 8, 2>, 16, 8, 2};
+    else if constexpr (waves_for(HM, JM) == 16) return {&k_conv_fwd<HM, JM, false, true, 16, 1, 1>, 16, 1};
     else return {&k_conv_fwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))};
   }
 };
