@@ -702,9 +702,10 @@ def run_tgn(args, wl: dict) -> dict:
             # the fused launch is also a streaming kernel: its algorithmic bytes against HBM
             from starry_unigraph.lib import _capi
             U_avg = sum(p[2] for p in per_step) / len(per_step)
+            d = rt.dims
+            tile_rows = int(_capi.lib().sgl_conv_backward_tile_rows(d.D, d.F, d.T, d.H, int(rt._bf16 is not None)))
             nb = param_update_bytes(wl, U_avg, rt.dims, rt.optimizer.inner.flat.numel(),
-                                    rt._bf16.buf.numel() if rt._bf16 is not None else 0,
-                                    int(_capi.lib().sgl_conv_tile_rows(rt.dims.D, rt.dims.F, rt.dims.T, rt.dims.H)))
+                                    rt._bf16.buf.numel() if rt._bf16 is not None else 0, tile_rows)
             gbs = nb / (avg * 1e-3) / 1e9
             breakdown[name]["hbm"] = {"alg_bytes": round(nb), "achieved": round(gbs, 1), "unit": "GB/s",
                                       "frac": round(gbs / HBM_PEAK_GBS, 5),

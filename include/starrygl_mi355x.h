@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 19
+#define SGL_ABI_VERSION 20
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -351,7 +351,8 @@ int sgl_memory_gather(int32_t D, int64_t capacity, const int32_t *num_roots,
  * >= U unwritten, all zero if any_edges == 0), and per
  * tile partial sums ln_part [cap/R][2][D] (gamma, beta) and
  * te_part [cap/R][2][T] (time-encoding w, b; the b part includes the
- * query's cos(b) term through w_q), R = sgl_conv_tile_rows(D, F, T, H).
+ * query's cos(b) term through w_q), R = sgl_conv_backward_tile_rows(D, F,
+ * T, H, bw != NULL).
  * ------------------------------------------------------------------------- */
 /* Edge rows of the attention's neighbour windows, built once per step after
  * the memory commit: for every root r < U (device) and sampled slot e <
@@ -367,10 +368,16 @@ int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
                   const float *memory, const float *efeat,
                   const int32_t *cnt, const int32_t *nbr, const int32_t *eid,
                   float *X, hipStream_t stream);
-/* Roots per attention workgroup for these dimensions (4 or 8; a divisor of
- * 16), i.e. the row count of one ln_part / te_part tile; 0 if the
- * dimensions are unsupported. */
+/* Roots per attention workgroup of the fp32 and dropout instances for these
+ * dimensions (4 or 8; a divisor of 16); 0 if the dimensions are
+ * unsupported. */
 int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
+/* Roots per workgroup of the backward instance sgl_conv_backward runs for
+ * these dimensions, with bf16 weight copies (bf16 != 0) or without: the row
+ * count of one ln_part / te_part tile (1, 4 or 8; a divisor of 16); 0 if the
+ * dimensions are unsupported. No reference counterpart (sizes this build's
+ * buffers). */
+int32_t sgl_conv_backward_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H, int32_t bf16);
 /* bf16 copies of the attention and edge-predictor weights, for the bf16
  * GEMM variants of sgl_conv_forward, sgl_conv_backward and sgl_predictor
  * (argument bw; NULL: the fp32 products). Benchmark configurations 4 and 5 ask for

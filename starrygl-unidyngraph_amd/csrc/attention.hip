@@ -1326,13 +1326,17 @@ struct FwdPickBf {
 };
 template <int HM, int JM>
 struct BwdPickBf {
-  // the backward's ln_part / te_part tiles are sized by sgl_conv_tile_rows
-  // (rows_for(waves_for(HM, JM))): a layout with other rows per workgroup
-  // would write past them
+  // the backward's ln_part / te_part tiles are sized by the rows per
+  // workgroup of the instance it runs (sgl_conv_backward_tile_rows, which
+  // asks this picker). The 16-wave instance takes one root per workgroup, as
+  // the forward does (config 4: 22.0 -> 20.9 us); the fp32 and dropout
+  // instances keep 4 (their four-row products; one root would make config 4
+  // with dropout 30 % slower).
   static_assert(!split_heads_bwd(HM, JM) || rows_for(waves_for(HM, JM)) == 8,
-                "a backward instance's rows per workgroup must equal sgl_conv_tile_rows");
+                "a split-head backward instance keeps the 8 rows of its 8-wave shape");
   static Instance<BwdFn> get() {
     if constexpr (split_heads_bwd(HM, JM)) return {&k_conv_bwd<HM, JM, false, true, 16, 8, 2>, 16, 8, 2};
+    else if constexpr (waves_for(HM, JM) == 16) return {&k_conv_bwd<HM, JM, false, true, 16, 1, 1>, 16, 1};
     else return {&k_conv_bwd<HM, JM, false, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))};
   }
 };
@@ -1427,6 +1431,13 @@ extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H
   int hm, jm;
   instance_shape(d, hm, jm);
   return rows_for(waves_for(hm, jm));
+}
+
+extern "C" int32_t sgl_conv_backward_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H, int32_t bf16) {
+  const Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, 0};
+  if (check_dims(d) != SGL_OK) return 0;
+  const auto inst = bf16 ? pick_instance<BwdPickBf>(d) : pick_instance<BwdPick>(d);
+  return inst.fn != nullptr ? inst.rows : 0;
 }
 
 extern "C" int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout, int64_t capacity,
@@ -1532,9 +1543,10 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
   const auto inst = bw != nullptr ? pick_instance<BwdPickBf>(d)
                     : drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
-  // one ln_part / te_part tile per workgroup: the caller sized them by sgl_conv_tile_rows
-  SGL_REQUIRE(inst.rows == sgl_conv_tile_rows(D, F, T, H), "conv_backward: %d roots per workgroup, %d per tile",
-              inst.rows, sgl_conv_tile_rows(D, F, T, H));
+  // one ln_part / te_part tile per workgroup: the caller sized them by
+  // sgl_conv_backward_tile_rows (the dropout instances' rows are the fp32 ones)
+  const int32_t tile_rows = sgl_conv_backward_tile_rows(D, F, T, H, bw != nullptr ? 1 : 0);
+  SGL_REQUIRE(inst.rows == tile_rows, "conv_backward: %d roots per workgroup, %d per tile", inst.rows, tile_rows);
   const size_t lds = sizeof(float) * bwd_lds_floats(d, inst.waves, inst.rows, inst.waves / inst.rows / inst.hg > 1);
   SGL_REQUIRE(lds <= 160 * 1024, "conv_backward: %zu bytes of LDS needed (> 160 KiB)", lds);
   SGL_CHECK_HIP(sgl::ensure_dynamic_lds(reinterpret_cast<const void *>(inst.fn), lds));

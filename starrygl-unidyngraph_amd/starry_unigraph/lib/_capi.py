@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2
@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple] = {
                                      + [_vp] * 8),
     "sgl_memory_gather": (ctypes.c_int, [_i32, _i64] + [_vp] * 8),
     "sgl_conv_tile_rows": (_i32, [_i32] * 4),
+    "sgl_conv_backward_tile_rows": (_i32, [_i32] * 5),
     "sgl_edge_rows": (ctypes.c_int, [_i32] * 4 + [_i64] + [_vp] * 8),
     "sgl_conv_forward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 29 + _DROP + [_vp, _vp]),
     "sgl_conv_backward": (ctypes.c_int, [_i32] * 5 + [_i64] + [_vp] * 39 + _DROP + [_vp, _vp]),

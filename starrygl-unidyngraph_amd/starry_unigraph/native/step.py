@@ -208,12 +208,16 @@ class StepBuffers:
         self.gz, self.gagg, self.gQ = z(P * c, D), z(P * c, D), z(P * c, D)
         self.G, self.sigma = z(P * c, H, C), z(P * c, H)
         # per-workgroup partial sums of the attention backward: one tile per
-        # conv_rows roots
-        self.conv_rows = int(_capi.lib().sgl_conv_tile_rows(D, dims.F, dims.T, H))
-        if self.conv_rows <= 0 or TILE % self.conv_rows:
-            raise RuntimeError(f"sgl_conv_tile_rows: unsupported attention dimensions {dims}")
+        # workgroup of the instance that runs, conv_rows roots (fp32 and
+        # dropout instances) or conv_rows_bf16 (with bf16 weight copies); the
+        # arrays hold the tiles of the smaller
+        lib = _capi.lib()
+        self.conv_rows = int(lib.sgl_conv_backward_tile_rows(D, dims.F, dims.T, H, 0))
+        self.conv_rows_bf16 = int(lib.sgl_conv_backward_tile_rows(D, dims.F, dims.T, H, 1))
+        if min(self.conv_rows, self.conv_rows_bf16) <= 0 or TILE % self.conv_rows or TILE % self.conv_rows_bf16:
+            raise RuntimeError(f"sgl_conv_backward_tile_rows: unsupported attention dimensions {dims}")
         self.proj_part = z(c // TILE, 2, D)   # the time projection's per-tile gradient partials
-        self.tiles = c // self.conv_rows
+        self.tiles = c // min(self.conv_rows, self.conv_rows_bf16)
         self.ln_part = z(P * self.tiles, 2, D)
         self.te_part = z(P * self.tiles, 2, max(dims.T, 1))
 
@@ -345,6 +349,13 @@ class DeviceStep:
 
     def _bw(self) -> int | None:
         return self.bf16.ptr if self.bf16 is not None else None
+
+    def bwd_tile_rows(self, bf16: bool | None = None) -> int:
+        """Roots per ln_part / te_part tile of the attention backward that
+        runs: with the bf16 weight copies (``bf16``, default: whether this
+        step has them) or the fp32 / dropout instances."""
+        use = self.bf16 is not None if bf16 is None else bf16
+        return self.buf.conv_rows_bf16 if use else self.buf.conv_rows
 
     def _call(self, name: str, fn):
         t = self.timer
@@ -598,9 +609,10 @@ class DeviceStep:
         phi0 = torch.cos(te_b)
         g_w_q = torch.cat([gQ.t() @ new_mem, torch.outer(sq, phi0)], dim=1)
         g_b_q = sq
-        g_ln_g = b.ln_part[:, 0].sum(0)
-        g_ln_b = b.ln_part[:, 1].sum(0)
-        te = b.te_part[:, :, :T].sum(0)
+        nt = b.cap // self.bwd_tile_rows(self.bf16 is not None and drop is None)
+        g_ln_g = b.ln_part[:nt, 0].sum(0)
+        g_ln_b = b.ln_part[:nt, 1].sum(0)
+        te = b.te_part[:nt, :, :T].sum(0)
         g_te_w = te[0].reshape(T, 1)
         g_te_b = te[1]   # includes the query's cos(b) term (folded in by the kernel)
         return [g_te_w, g_te_b, g_w_q, g_b_q, g_w_k, g_b_k, g_w_v, g_b_v, g_w_out, g_b_out, g_ln_g, g_ln_b]
@@ -662,7 +674,8 @@ class StepParamUpdate:
         b, d, opt = self.step.buf, self.step.dims, self.opt
         D, T, H, C = d.D, d.T, d.H, d.C
         dh = D // H
-        ntiles = b.cap // b.conv_rows
+        ntiles = b.tiles   # a pass's block of the per-tile partials
+        tile_rows = self.step.bwd_tile_rows(self.shadow is not None)
         base = opt.flat.data_ptr()
 
         def off(p):
@@ -723,7 +736,7 @@ class StepParamUpdate:
             return self._check(jobs, tiles, conv_params, pred_params)
         te_w, te_b, w_q, b_q, w_k, b_k, w_v, b_v, w_out, b_out, ln_g, ln_b = conv_params
         # per-tile partials: the tiles holding live rows (the others' are zero)
-        rt = -b.conv_rows
+        rt = -tile_rows
         conv(at(b.te_part), 2 * T, one, 0, off(te_w), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=rt)
         conv(at(b.te_part, T), 2 * T, one, 0, off(te_b), 1, T, 1, x1w=ntiles * 2 * T, r_fixed=rt)
         conv(at(b.gQ), D, at(b.new_mem), D, off(w_q), D + T, D, D, x1w=c * D, shd=shf("w_q"))

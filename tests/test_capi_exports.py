@@ -46,6 +46,32 @@ def test_host_side_queries_need_no_gpu():
     assert lib.sgl_compact_workspace_bytes(10 ** 6) >= 2 * 8 * (10 ** 6 // 256)
 
 
+def test_conv_backward_tile_rows():
+    """The ln_part / te_part tile of the attention backward is one workgroup
+    of the instance sgl_conv_backward runs; callers size those arrays (and the
+    fused update reduces them) by sgl_conv_backward_tile_rows, which asks the
+    same instance picker: 1 root for the 16-wave bf16 instances, the fp32 /
+    dropout instances' 4 or 8 (sgl_conv_tile_rows) otherwise."""
+    from starry_unigraph.lib import _capi
+    lib = _capi.load_library()
+    assert lib.sgl_conv_backward_tile_rows(100, 16, 100, 2, 1) == 1      # config 4, bf16 GEMMs
+    assert lib.sgl_conv_backward_tile_rows(100, 16, 100, 2, 0) == 4      # config 4, fp32 / dropout
+    assert lib.sgl_conv_backward_tile_rows(172, 16, 100, 4, 1) == 8      # config 5 (split heads)
+    assert lib.sgl_conv_backward_tile_rows(100, 16, 100, 3, 1) == 0      # D % H != 0
+    for D in (8, 32, 100, 172, 200):
+        for F in (0, 4, 16, 172):
+            for T in (0, 8, 100):
+                for H in (1, 2, 4):
+                    if D % H:
+                        continue
+                    fp, bf = (lib.sgl_conv_backward_tile_rows(D, F, T, H, b) for b in (0, 1))
+                    assert fp == lib.sgl_conv_tile_rows(D, F, T, H), (D, F, T, H)
+                    if D + F + T > 512:
+                        assert fp == bf == 0
+                        continue
+                    assert fp in (4, 8) and bf in (1, 8) and 16 % bf == 0 and bf <= fp, (D, F, T, H, fp, bf)
+
+
 def test_bf16_gru_tile_rows_fit_lds():
     """The bf16 GRU's tile choice counts its static LDS (the root tables,
     60 bytes a row) with the dynamic tiles against the CU's 160 KiB: shapes
