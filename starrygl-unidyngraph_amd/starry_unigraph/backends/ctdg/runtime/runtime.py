@@ -92,6 +92,7 @@ class CTDGOnlineRuntime:
         self._draws = ChunkedDraws(lambda: self._dst_pool().numel(), self._split_end, self._alloc_draw_slot,
                                    self._lookup, chunk=self.neg_chunk, ring=self.kDrawRing)
         self._pool_dev: torch.Tensor | None = None
+        self._split_bounds: dict[str, tuple[int, int]] = {}   # (first event, one past the last) of a split
         self._neg_err = _capi.ErrorFlag(self.device)
         core = self._core()
         conv = core.conv
@@ -327,8 +328,12 @@ class CTDGOnlineRuntime:
     def _split_end(self, split: str, s: int, n: int) -> int:
         """One past the last event of the contiguous split holding batch
         [s, s + n) (s + n when the batch lies outside it)."""
-        ids = self.dataset.split_event_ids("test" if split == "predict" else split)
-        return int(ids[-1]) + 1 if ids.numel() and int(ids[0]) <= s < int(ids[-1]) + 1 else s + n
+        key = "test" if split == "predict" else split
+        b = self._split_bounds.get(key)
+        if b is None:
+            ids = self.dataset.split_event_ids(key)
+            b = self._split_bounds[key] = (int(ids[0]), int(ids[-1]) + 1) if ids.numel() else (0, 0)
+        return b[1] if b[0] <= s < b[1] else s + n
 
     def _alloc_draw_slot(self, m: int) -> DrawSlot:
         """A pinned staging buffer for at least m draws (a chunk of batches),
@@ -345,20 +350,25 @@ class CTDGOnlineRuntime:
         the stream-wide array)."""
         if self._pool_dev is None:
             self._pool_dev = self._dst_pool().to(self.device)
+            for t in (self._dev["dst"], self._neg_all):
+                if t.dtype != torch.int64 or not t.is_contiguous():
+                    raise RuntimeError("negatives lookup: the dst and negative arrays must be contiguous int64")
         front = self._front_stream
         stream = front if front is not None else torch.cuda.current_stream(self.device)
         # on the front stream, where the batch preparations read them (an
         # eager step orders its stream after the front stream first); the
-        # lookup reads the pinned draws in place (no separate copy)
-        with torch.cuda.stream(stream):
-            out = self._neg_all[s:s + m]
-            P = _capi.ptr
-            _capi.check(_capi.call("sgl_negatives_from_draws", m, slot.addr, P(self._pool_dev), self._pool_dev.numel(),
-                                   P(self._dev["dst"][s:s + m]), P(out), P(self._neg_err.t), stream.cuda_stream),
-                        "sgl_negatives_from_draws")
-            if slot.done is None:
-                slot.done = torch.cuda.Event()
-            slot.done.record(stream)
+        # lookup reads the pinned draws in place (no separate copy). The
+        # launch and the event take the stream explicitly, and the int64
+        # arrays' pointers are offset directly (a draw boundary's host time
+        # counts in short runs)
+        P = _capi.ptr
+        dst, out = self._dev["dst"], self._neg_all
+        _capi.check(_capi.call("sgl_negatives_from_draws", m, slot.addr, P(self._pool_dev), self._pool_dev.numel(),
+                               dst.data_ptr() + 8 * s, out.data_ptr() + 8 * s, P(self._neg_err.t), stream.cuda_stream),
+                    "sgl_negatives_from_draws")
+        if slot.done is None:
+            slot.done = torch.cuda.Event()
+        slot.done.record(stream)
 
     def _device_batch(self, batch: CTDGDataBatch):
         d = self._dev
