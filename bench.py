@@ -465,16 +465,16 @@ def _restore(rt, snap):
 # (counters scaled by a copy kernel of known size); None where no counter run
 # was made.
 HBM_TRAFFIC = {  # cfg4: read requests x their sizes (32/64/128 B) + write requests x theirs (64/32 B)
-    ("cfg4", "bf16", "conv_backward"): 64 * 5457 + 128 * 27837 + 64 * 23700 + 32 * (24501 - 23700),
-    ("cfg4", "bf16", "edge_rows"): 64 * 347 + 128 * 1554 + 64 * 4203 + 32 * (4804 - 4203),
-    ("cfg4", "bf16", "memory_commit"): 64 * 291 + 128 * 872 + 64 * 1195 + 32 * (1823 - 1195),
-    ("cfg4", "bf16", "conv_forward"): 64 * 5314 + 128 * 14433 + 64 * 29426 + 32 * (30224 - 29426),
-    ("cfg4", "bf16", "memory_update"): 64 * 2679 + 128 * 23921 + 64 * 4519 + 32 * (5112 - 4519),
-    ("cfg4", "bf16", "predictor"): 64 * 2514 + 128 * 4294 + 64 * 8165 + 32 * (10028 - 8165),
-    ("cfg4", "bf16", "param_update"): 64 * 974 + 128 * 31057 + 64 * 30950 + 32 * (34587 - 30950),
-    ("cfg4", "bf16", "batch_prepare"): 64 * 130 + 128 * 1307 + 64 * 692 + 32 * (3410 - 692),
-    ("cfg4", "bf16", "recent_sample"): 64 * 475 + 128 * 5557 + 64 * 119 + 32 * (584 - 119),
-    ("cfg4", "bf16", "link_metrics"): 64 * 1099 + 128 * 307 + 64 * 3 + 32 * (25 - 3),
+    ("cfg4", "bf16", "conv_backward"): 64 * 5720 + 128 * 28901 + 64 * 44874 + 32 * (48862 - 44874),
+    ("cfg4", "bf16", "edge_rows"): 64 * 464 + 128 * 1622 + 64 * 4438 + 32 * (5072 - 4438),
+    ("cfg4", "bf16", "memory_commit"): 64 * 288 + 128 * 875 + 64 * 1197 + 32 * (1827 - 1197),
+    ("cfg4", "bf16", "conv_forward"): 64 * 5582 + 128 * 14860 + 64 * 29197 + 32 * (32231 - 29197),
+    ("cfg4", "bf16", "memory_update"): 64 * 2673 + 128 * 23921 + 64 * 4539 + 32 * (5134 - 4539),
+    ("cfg4", "bf16", "predictor"): 64 * 2512 + 128 * 4298 + 64 * 8194 + 32 * (10052 - 8194),
+    ("cfg4", "bf16", "param_update"): 64 * 988 + 128 * 35652 + 64 * 30950 + 32 * (34587 - 30950),
+    ("cfg4", "bf16", "batch_prepare"): 64 * 128 + 128 * 1305 + 64 * 691 + 32 * (3409 - 691),
+    ("cfg4", "bf16", "recent_sample"): 64 * 472 + 128 * 5531 + 64 * 123 + 32 * (585 - 123),
+    ("cfg4", "bf16", "link_metrics"): 64 * 1096 + 128 * 307 + 64 * 3 + 32 * (25 - 3),
     ("cfg3", "int64", "recent_sample"): round((2 * 1342192 + 449830) * 1024)}
 # the counter runs the HBM_TRAFFIC figures come from (the same kernels at the same workload)
 TRAFFIC_SOURCE = {"cfg4": "profiles/tgn_cfg4_hbm_traffic.md", "cfg3": "profiles/sampler_cfg3_hbm_traffic.md"}
