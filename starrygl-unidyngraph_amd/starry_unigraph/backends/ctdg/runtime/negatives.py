@@ -22,7 +22,7 @@ is reserved until its lookup is issued, so no other chunk is drawn into it.
 from __future__ import annotations
 
 import time
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Any, Callable
 
 import torch
@@ -36,6 +36,15 @@ class DrawSlot:
     buf: torch.Tensor
     done: Any = None
     addr: int = 0
+    views: dict = field(default_factory=dict)   # (at, k) -> buf[at:at + k], built once
+
+    def view(self, at: int, k: int) -> torch.Tensor:
+        v = self.views.get((at, k))
+        if v is None:
+            if len(self.views) >= 64:   # batch sizes that keep changing
+                self.views.clear()
+            v = self.views[(at, k)] = self.buf[at:at + k]
+        return v
 
     def wait(self) -> None:
         if self.done is not None:
@@ -86,7 +95,11 @@ class ChunkedDraws:
 
     # ------------------------------------------------------------ draws
     def _draw(self, slot: DrawSlot, at: int, k: int) -> None:
-        torch.randint(low=0, high=self.pool_size(), size=(k,), dtype=torch.long, out=slot.buf[at:at + k])
+        # the numbers of torch.randint(0, pool, (k,)) (randint fills its
+        # output with random_(low, high)), into a view made once per slot
+        # and range: a slice and randint's out= handling cost more host time
+        # per step than the draw itself
+        slot.view(at, k).random_(0, self.pool_size())
 
     def _slot(self, m: int) -> DrawSlot:
         """The next ring buffer not reserved by the pending next-chunk draw,
