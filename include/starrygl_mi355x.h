@@ -655,8 +655,9 @@ int sgl_grad_shadows(const sgl_grad_job *jobs, const int32_t *tile_job,
  * the completed-step count *steps[s] (device float) advances by one; coef[2s]
  * and coef[2s+1] become lr / (1 - beta1^t) and sqrt(1 - beta2^t) for t =
  * the count after the advance (a closed segment: the count plus one), in
- * double as torch computes them. One lane. Enqueue it after the gates are
- * written and after the sgl_grad_adam launch that last read this coef;
+ * double as torch computes them. One lane per segment; the steps[s] must be
+ * distinct counters (SGL_ERR_INVALID otherwise). Enqueue it after the gates
+ * are written and after the sgl_grad_adam launch that last read this coef;
  * steps and gates are host arrays of device pointers. With step_counter
  * (device uint64, may be NULL) it also advances the training-step counter
  * and copies the new value to step_out (the dropout masks' step, kept with

@@ -226,30 +226,51 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_shadows(const sgl_grad_job *_
   if (jb.sht_off >= 0) shadow[jb.sht_off + int64_t(eb) * jb.sht_ld + ea] = hv;
 }
 
-// One lane: advance the open segments' step counts and write the bias
-// corrections of the step they are now at (torch.optim.Adam: the count is
-// incremented first, then lr / (1 - b1^t) and sqrt(1 - b2^t) in double).
-// A closed segment keeps its count; its coef (for the next count) is unused.
+// One lane per segment: advance the open segments' step counts and write
+// the bias corrections of the step they are now at (torch.optim.Adam: the
+// count is incremented first, then lr / (1 - b1^t) and sqrt(1 - b2^t) in
+// double). A closed segment keeps its count; its coef (for the next count) is
+// unused. Every load is issued before the first store (one round trip; the
+// step counters are distinct words, sgl_adam_coef checks it).
 __global__ void k_adam_coef(int nseg, AdamSegs segs, float *__restrict__ coef, float lr, float b1, float b2,
                             unsigned long long *step_counter, unsigned long long *step_out, uint32_t *sig_word,
                             uint32_t sig_value) {
-  if (threadIdx.x != 0) return;
-  if (step_counter != nullptr) {
-    const unsigned long long n = *step_counter + 1ull;
-    *step_counter = n;
-    *step_out = n;
+  const int lane = threadIdx.x;
+  float *sp = nullptr;
+  const int32_t *gp = nullptr;
+#pragma unroll
+  for (int s = 0; s < SGL_MAX_ADAM_SEGMENTS; ++s)
+    if (lane == s) {
+      sp = segs.step[s];
+      gp = segs.gate[s];
+    }
+  const bool mine = lane < nseg;
+  const bool counts = lane == 0 && step_counter != nullptr;
+  unsigned long long n = 0ull;
+  if (counts) n = *step_counter;
+  float st = 0.f;
+  int32_t g = 1;
+  if (mine) {
+    st = *sp;
+    if (gp != nullptr) g = *gp;
   }
-  for (int s = 0; s < nseg; ++s) {
-    const float st = *segs.step[s];
-    const bool open = segs.gate[s] == nullptr || *segs.gate[s] != 0;
-    if (open) *segs.step[s] = st + 1.f;
+  if (counts) {
+    *step_counter = n + 1ull;
+    *step_out = n + 1ull;
+  }
+  if (mine) {
+    if (g != 0) *sp = st + 1.f;
     const double t = double(st) + 1.0;
-    coef[2 * s] = float(double(lr) / (1.0 - pow(double(b1), t)));
-    coef[2 * s + 1] = float(sqrt(1.0 - pow(double(b2), t)));
+    coef[2 * lane] = float(double(lr) / (1.0 - pow(double(b1), t)));
+    coef[2 * lane + 1] = float(sqrt(1.0 - pow(double(b2), t)));
   }
   // a launch plan's signal: the earlier kernels of the stream are done
-  // (stream order), this lane's writes precede the release
-  if (sig_word != nullptr) __hip_atomic_store(sig_word, sig_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  // (stream order); every lane's writes are released before lane 0's store
+  if (sig_word != nullptr) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __syncthreads();
+    if (lane == 0) __hip_atomic_store(sig_word, sig_value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 AdamSegs make_segs(int nseg, float *const *steps, const int32_t *const *gates) {
@@ -294,7 +315,10 @@ extern "C" int sgl_adam_coef(int32_t nseg, float *const *steps, const int32_t *c
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "adam_coef: nseg %d out of range", nseg);
   SGL_REQUIRE(steps != nullptr && coef != nullptr, "adam_coef: NULL array");
   SGL_REQUIRE(step_counter == nullptr || step_out != nullptr, "adam_coef: step_counter without step_out");
-  for (int s = 0; s < nseg; ++s) SGL_REQUIRE(steps[s] != nullptr, "adam_coef: NULL step counter %d", s);
+  for (int s = 0; s < nseg; ++s) {
+    SGL_REQUIRE(steps[s] != nullptr, "adam_coef: NULL step counter %d", s);
+    for (int r = 0; r < s; ++r) SGL_REQUIRE(steps[r] != steps[s], "adam_coef: segments %d and %d share a step counter", r, s);
+  }
   const sgl::PlanSignal sig = sgl::take_signal();  // a launch plan's signal, folded
   sgl::launch(&k_adam_coef, dim3(1), dim3(64), 0, stream, int(nseg), make_segs(nseg, steps, gates), coef, lr, beta1,
               beta2, reinterpret_cast<unsigned long long *>(step_counter),

@@ -214,8 +214,8 @@ extern "C" int sgl_plan_run(const sgl_op *ops, int32_t n_front, int32_t n_back, 
   auto last_takes = [&](const sgl_op *p, int n) { return n > 0 && p[n - 1].kind >= 0 && p[n - 1].kind < kNumOps &&
                                                          kOps[p[n - 1].kind].takes_signal; };
   const sgl::PlanGate g_front{w_back, need_back, timeout};
-  // (a signal is folded only into a one-lane kernel: a multi-workgroup one
-  // would need every workgroup to write back its XCD's L2 first)
+  // (a signal is folded only into a one-workgroup kernel: a multi-workgroup
+  // one would need every workgroup to write back its XCD's L2 first)
   const sgl::PlanSignal s_front{w_front, seq, nullptr};
   const bool fg = first_takes(ops, n_front), fs = last_takes(ops, n_front);
   if (!fg)
