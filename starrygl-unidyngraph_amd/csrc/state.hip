@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kScanBlock = 1024;
+constexpr int kScanUnroll = 4;  // 256-word rounds per wave in flight in k_step_scan
 constexpr int kTileRows = 16;
 
 __device__ __forceinline__ uint32_t ts_order(float x) {
@@ -44,7 +45,7 @@ __device__ __forceinline__ float ts_from_order(uint32_t k) {
 
 // Multi-workgroup batch preparation (batches above kPrepMaxBatch events):
 // mark, scan, index. Each workgroup of the mark and index kernels takes
-// kAggEvents consecutive events and combines them per node (mark) or per
+// kB * kPer consecutive events and combines them per node (mark) or per
 // root (index) in a small LDS table before touching global memory: the hot
 // nodes of a skewed stream (a Zipf-distributed one has a node in a third of
 // all events) then cost one global atomic per workgroup instead of one per
@@ -53,46 +54,57 @@ __device__ __forceinline__ float ts_from_order(uint32_t k) {
 // maximum of the mark kernel lives in the first summary word of node_bits as
 // order(max ts), and the number of bits the mark kernel set in the second
 // (words this path does not otherwise use); the scan reads and clears them.
+// Two workgroup shapes: batches of up to kAggSmallMax events take one event
+// per thread of 256-thread workgroups (config 5's 4,000 events: 16
+// workgroups, every event's dependent loads in flight at once, where
+// 4,096-event workgroups left the batch to one workgroup whose threads
+// walked four events each); larger batches 4,096 events per 1,024-thread
+// workgroup, where the per-workgroup aggregation of the hub nodes pays.
 constexpr int kAggBlock = 1024;
 constexpr int kAggPer = 4;
 constexpr int kAggEvents = kAggBlock * kAggPer;
 constexpr int kMarkLog2 = 12;  // node table of the mark kernel (4096 slots, 16 KB)
-constexpr int kMarkSlots = 1 << kMarkLog2;
 constexpr int kIdxLog2 = 10;   // per-role root table of the index kernel (1024 slots, 2 x 16 KB)
-constexpr int kIdxSlots = 1 << kIdxLog2;
+constexpr int kAggSmallBlock = 256;
+constexpr int64_t kAggSmallMax = 65536;
+constexpr int kMarkSmallLog2 = 10;  // at most 512 nodes per workgroup
+constexpr int kIdxSmallLog2 = 9;    // at most 256 roots per role and workgroup
+constexpr unsigned kFewGroups = 32;  // mark grids this small skip the read before each bit's atomic
 
 __device__ __forceinline__ uint32_t agg_slot(uint32_t key, int log2_slots) {
   return (key * 2654435761u) >> (32 - log2_slots);
 }
 
-__global__ __launch_bounds__(kAggBlock) void k_step_mark(
+template <int kB, int kPer, int kL2>
+__global__ __launch_bounds__(kB) void k_step_mark(
     int64_t batch, int64_t num_nodes, int64_t cap, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const float *__restrict__ ts, const int64_t *__restrict__ cursor,
     int64_t *__restrict__ batch_start, uint32_t *__restrict__ bits, uint32_t *__restrict__ ts_slot,
     unsigned long long *__restrict__ win_src, unsigned long long *__restrict__ win_dst,
     int32_t *__restrict__ cnt_src, int32_t *__restrict__ cnt_dst,
     int32_t *__restrict__ any_edges, int32_t *__restrict__ err) {
-  __shared__ int32_t s_node[kMarkSlots];
-  __shared__ float s_m[kAggBlock / sgl::kWave];
+  __shared__ int32_t s_node[(1 << kL2)];
+  __shared__ float s_m[kB / sgl::kWave];
   __shared__ int32_t s_new;  // bits this workgroup set (summed into new_count)
   const int tid = threadIdx.x;
+  const bool few = gridDim.x <= kFewGroups;
   if (tid == 0) s_new = 0;
-  const int64_t g = int64_t(blockIdx.x) * kAggBlock + tid;
+  const int64_t g = int64_t(blockIdx.x) * kB + tid;
   if (g == 0) *any_edges = 0;
-  for (int64_t r = g; r < cap; r += int64_t(gridDim.x) * kAggBlock) {
+  for (int64_t r = g; r < cap; r += int64_t(gridDim.x) * kB) {
     win_src[r] = 0ull;
     win_dst[r] = 0ull;
     cnt_src[r] = 0;
     cnt_dst[r] = 0;
   }
-  for (int i = tid; i < kMarkSlots; i += kAggBlock) s_node[i] = -1;
+  for (int i = tid; i < (1 << kL2); i += kB) s_node[i] = -1;
   const int64_t off = cursor != nullptr ? *cursor : 0;
   if (cursor != nullptr && g == 0) *batch_start = off;
   __syncthreads();
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kAggPer; ++j) {
-    const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t e = int64_t(blockIdx.x) * (kB * kPer) + j * kB + tid;
     if (e >= batch) break;
     const int64_t s = src[off + e], d = dst[off + e];
     m = fmaxf(m, ts[off + e]);  // fmaxf ignores NaN
@@ -103,12 +115,14 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
 #pragma unroll
     for (int role = 0; role < 2; ++role) {
       const int32_t n = int32_t(role == 0 ? s : d);
-      const int32_t old = atomicCAS(&s_node[agg_slot(uint32_t(n), kMarkLog2)], -1, n);
+      const int32_t old = atomicCAS(&s_node[agg_slot(uint32_t(n), kL2)], -1, n);
       if (old == n) continue;  // this workgroup marks n already
       // first in this workgroup (or its slot is taken): set the bit, with no
-      // atomic when another workgroup has set it already
+      // atomic when another workgroup has set it already (a grid of at most
+      // kFewGroups issues the atomic at once: one round trip less, and few
+      // same-address atomics on a hub's word)
       const uint32_t mb = 1u << (n & 31);
-      if ((bits[n >> 5] & mb) == 0u && (atomicOr(&bits[n >> 5], mb) & mb) == 0u) atomicAdd(&s_new, 1);
+      if ((few || (bits[n >> 5] & mb) == 0u) && (atomicOr(&bits[n >> 5], mb) & mb) == 0u) atomicAdd(&s_new, 1);
     }
   }
   // the block's timestamp maximum, then one atomic max per block, skipped
@@ -120,49 +134,100 @@ __global__ __launch_bounds__(kAggBlock) void k_step_mark(
   if (tid == 0) {
     float mm = s_m[0];
 #pragma unroll
-    for (int w = 1; w < kAggBlock / sgl::kWave; ++w) mm = fmaxf(mm, s_m[w]);
+    for (int w = 1; w < kB / sgl::kWave; ++w) mm = fmaxf(mm, s_m[w]);
     if (mm > -INFINITY) {
       const uint32_t k = ts_order(mm);
-      if (*ts_slot < k) atomicMax(ts_slot, k);
+      if (few || *ts_slot < k) atomicMax(ts_slot, k);
     }
     if (s_new > 0) atomicAdd(ts_slot + 1, uint32_t(s_new));
   }
 }
 
 // One workgroup: exclusive scan of the bitmap word popcounts (-> root count)
-// in tiles of 4 words per thread (16-byte loads and stores), and the batch's
-// max timestamp from the mark kernel's slot (-> the sampler's query time).
+// and the batch's max timestamp from the mark kernel's slot (-> the
+// sampler's query time). Each wave takes a contiguous range of the bitmap
+// (a multiple of 256 words): a first pass sums its popcounts (16-byte loads,
+// kScanUnroll rounds of 64 lanes in flight, every load instruction one
+// contiguous kilobyte), one barrier gives each wave the words before its
+// range, and a second pass re-reads the range (now in L2) and writes the
+// prefixes round by round, a wave scan per round. Threads holding many
+// consecutive words instead made each load touch 64 lines (a 16-word stride
+// per lane: 12-13 us for configs 4 and 5's 35,632 words, as slow as one
+// workgroup-wide scan per 4,096 words). Thread 0 reads the mark kernel's
+// words and the batch start first, so that their round trip overlaps the
+// bitmap's.
 __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     int64_t nwords, int64_t all_words, uint32_t *__restrict__ bits, int32_t *__restrict__ prefix,
     int32_t *__restrict__ num_roots, int64_t *__restrict__ num_roots64, int64_t batch,
     uint32_t *__restrict__ ts_slot, int64_t *__restrict__ cursor, const int64_t *__restrict__ batch_start,
     float *__restrict__ ts_max, int64_t *__restrict__ t_query, int32_t *__restrict__ err) {
-  __shared__ int32_t s_w[kScanBlock / sgl::kWave];
+  constexpr int kWaves = kScanBlock / sgl::kWave;
+  constexpr int kRound = 4 * sgl::kWave;  // words per wave and round
+  __shared__ int32_t s_w[kWaves];
   __shared__ int32_t s_stale;
-  int32_t carry = 0;
-  for (int64_t base = 0; base < nwords; base += 4 * kScanBlock) {
-    const int64_t i = base + 4 * int64_t(threadIdx.x);
-    uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if (i < nwords) w = *reinterpret_cast<const uint4 *>(bits + i);
-    const int32_t c0 = __popc(w.x), c1 = __popc(w.y), c2 = __popc(w.z), c3 = __popc(w.w);
-    int32_t total;
-    const int32_t run = carry + sgl::block_exclusive_scan<int32_t, kScanBlock>(c0 + c1 + c2 + c3, s_w, total);
-    if (i < nwords) *reinterpret_cast<int4 *>(prefix + i) = make_int4(run, run + c0, run + c0 + c1, run + c0 + c1 + c2);
-    carry += total;
+  uint32_t k_ts = 0u, n_set = 0u;
+  int64_t b_start = 0;
+  if (threadIdx.x == 0) {
+    k_ts = ts_slot[0];
+    n_set = ts_slot[1];
+    if (cursor != nullptr) b_start = *batch_start;
+  }
+  const int wave = threadIdx.x / sgl::kWave, lane = threadIdx.x & (sgl::kWave - 1);
+  // the wave's words [w0, w1): nwords is a multiple of 4, so every 16-byte
+  // group a lane takes is whole
+  const int64_t per = ((nwords + kWaves - 1) / kWaves + kRound - 1) / kRound * kRound;
+  const int64_t w0 = min(nwords, int64_t(wave) * per), w1 = min(nwords, w0 + per);
+  int32_t cnt = 0;
+  for (int64_t r0 = w0; r0 < w1; r0 += int64_t(kScanUnroll) * kRound) {
+    uint4 w[kScanUnroll];
+#pragma unroll
+    for (int u = 0; u < kScanUnroll; ++u) {
+      const int64_t i = r0 + int64_t(u) * kRound + 4 * lane;
+      w[u] = i < w1 ? *reinterpret_cast<const uint4 *>(bits + i) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kScanUnroll; ++u) cnt += __popc(w[u].x) + __popc(w[u].y) + __popc(w[u].z) + __popc(w[u].w);
+  }
+  const int32_t wave_total = __shfl(sgl::wave_inclusive_scan(cnt), sgl::kWave - 1, sgl::kWave);
+  if (lane == 0) s_w[wave] = wave_total;
+  __syncthreads();
+  int32_t run = 0, carry = 0;
+#pragma unroll
+  for (int v = 0; v < kWaves; ++v) {
+    const int32_t t = s_w[v];
+    run += v < wave ? t : 0;
+    carry += t;
+  }
+  for (int64_t r0 = w0; r0 < w1; r0 += int64_t(kScanUnroll) * kRound) {
+    uint4 w[kScanUnroll];
+#pragma unroll
+    for (int u = 0; u < kScanUnroll; ++u) {
+      const int64_t i = r0 + int64_t(u) * kRound + 4 * lane;
+      w[u] = i < w1 ? *reinterpret_cast<const uint4 *>(bits + i) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < kScanUnroll; ++u) {
+      const int64_t i = r0 + int64_t(u) * kRound + 4 * lane;
+      const int32_t c0 = __popc(w[u].x), c1 = __popc(w[u].y), c2 = __popc(w[u].z), c3 = __popc(w[u].w);
+      const int32_t sum = c0 + c1 + c2 + c3;
+      const int32_t inc = sgl::wave_inclusive_scan(sum);
+      const int32_t at = run + inc - sum;
+      if (i < w1) *reinterpret_cast<int4 *>(prefix + i) = make_int4(at, at + c0, at + c0 + c1, at + c0 + c1 + c2);
+      run += __shfl(inc, sgl::kWave - 1, sgl::kWave);
+    }
   }
   // every set bit was set by this batch's mark kernel, unless a previous
   // preparation's commit did not run: then its ranks could exceed the
   // buffers; report it, clear the bitmap and give the batch no roots
-  if (threadIdx.x == 0) s_stale = carry != int32_t(ts_slot[1]);
+  if (threadIdx.x == 0) s_stale = carry != int32_t(n_set);
   __syncthreads();
   const bool stale = s_stale != 0;
   if (stale)
     for (int64_t w = threadIdx.x; w < all_words; w += kScanBlock) bits[w] = 0u;
   if (threadIdx.x == 0) {
-    const uint32_t k = *ts_slot;
-    *ts_slot = 0u;
+    ts_slot[0] = 0u;
     ts_slot[1] = 0u;
-    const float mm = k != 0u ? ts_from_order(k) : -INFINITY;
+    const float mm = k_ts != 0u ? ts_from_order(k_ts) : -INFINITY;
     if (stale && err != nullptr) atomicOr(err, SGL_DERR_STALE_NODE_BITS);
     if (stale) carry = 0;
     *num_roots = carry;
@@ -171,11 +236,12 @@ __global__ __launch_bounds__(kScanBlock) void k_step_scan(
     // int(float max) truncates toward zero (runtime.py:142); the float32 round
     // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
     *t_query = batch > 0 ? (long long)truncf(mm) : 0;
-    if (cursor != nullptr) *cursor = *batch_start + batch;
+    if (cursor != nullptr) *cursor = b_start + batch;
   }
 }
 
-__global__ __launch_bounds__(kAggBlock) void k_step_index(
+template <int kB, int kPer, int kL2>
+__global__ __launch_bounds__(kB) void k_step_index(
     int64_t batch, int64_t num_nodes, const int32_t *__restrict__ num_roots, const int64_t *__restrict__ src,
     const int64_t *__restrict__ dst, const int64_t *__restrict__ neg,
     const float *__restrict__ ts, const int64_t *__restrict__ batch_start, const uint32_t *__restrict__ bits,
@@ -186,10 +252,10 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
     unsigned long long *__restrict__ win_dst, int32_t *__restrict__ cnt_src,
     int32_t *__restrict__ cnt_dst) {
   // per role: root rank, count and last-writer key of the table's roots
-  __shared__ int32_t s_root[2][kIdxSlots], s_cnt[2][kIdxSlots];
-  __shared__ unsigned long long s_win[2][kIdxSlots];
+  __shared__ int32_t s_root[2][(1 << kL2)], s_cnt[2][(1 << kL2)];
+  __shared__ unsigned long long s_win[2][(1 << kL2)];
   const int tid = threadIdx.x;
-  for (int i = tid; i < kIdxSlots; i += kAggBlock) {
+  for (int i = tid; i < (1 << kL2); i += kB) {
     s_root[0][i] = s_root[1][i] = -1;
     s_cnt[0][i] = s_cnt[1][i] = 0;
     s_win[0][i] = s_win[1][i] = 0ull;
@@ -204,8 +270,8 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
   const int64_t tq = *t_query;
   if (*num_roots == 0) {  // no valid event, or a stale bitmap (k_step_scan): no event has a root
 #pragma unroll
-    for (int j = 0; j < kAggPer; ++j) {
-      const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+    for (int j = 0; j < kPer; ++j) {
+      const int64_t e = int64_t(blockIdx.x) * (kB * kPer) + j * kB + tid;
       if (e >= batch) break;
       ridx_src[e] = -1;
       ridx_dst[e] = -1;
@@ -215,8 +281,8 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kAggPer; ++j) {
-    const int64_t e = int64_t(blockIdx.x) * kAggEvents + j * kAggBlock + tid;
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t e = int64_t(blockIdx.x) * (kB * kPer) + j * kB + tid;
     if (e >= batch) break;
     const int64_t s = src[e], d = dst[e];
     if (neg != nullptr) {
@@ -241,7 +307,7 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
     for (int role = 0; role < 2; ++role) {
       const int32_t r = role == 0 ? rs : rd;
       const int64_t node = role == 0 ? s : d;
-      const int slot = int(agg_slot(uint32_t(r), kIdxLog2));
+      const int slot = int(agg_slot(uint32_t(r), kL2));
       const int32_t old = atomicCAS(&s_root[role][slot], -1, r);
       if (old == -1 || old == r) {
         if (old == -1) {  // the root's first event in this workgroup
@@ -259,8 +325,8 @@ __global__ __launch_bounds__(kAggBlock) void k_step_index(
     }
   }
   __syncthreads();
-  for (int i = tid; i < 2 * kIdxSlots; i += kAggBlock) {
-    const int role = i / kIdxSlots, slot = i - role * kIdxSlots;
+  for (int i = tid; i < 2 * (1 << kL2); i += kB) {
+    const int role = i / (1 << kL2), slot = i - role * (1 << kL2);
     const int32_t r = s_root[role][slot];
     if (r < 0) continue;
     atomicAdd(role == 0 ? &cnt_src[r] : &cnt_dst[r], s_cnt[role][slot]);
@@ -1293,21 +1359,34 @@ static int batch_prepare(int64_t num_nodes, int64_t batch, const int64_t *src, c
   SGL_REQUIRE((reinterpret_cast<uintptr_t>(word_prefix) & 15u) == 0, "batch_prepare: word_prefix not 16-byte aligned");
   const int64_t nwords = bitmap_words(num_nodes);  // a multiple of 4, padding words zero
   uint32_t *ts_slot = node_bits + nwords;          // the first summary word
-  const unsigned grid = unsigned(std::max<int64_t>(1, (batch + kAggEvents - 1) / kAggEvents));
+  const bool small = batch <= kAggSmallMax;
+  const int64_t per_wg = small ? kAggSmallBlock : kAggEvents;
+  const unsigned grid = unsigned(std::max<int64_t>(1, (batch + per_wg - 1) / per_wg));
   auto *ws = reinterpret_cast<unsigned long long *>(win_src);
   auto *wd = reinterpret_cast<unsigned long long *>(win_dst);
-  k_step_mark<<<grid, kAggBlock, 0, stream>>>(batch, num_nodes, cap, src, dst, ts, cursor, batch_start, node_bits,
-                                           ts_slot, ws, wd, cnt_src, cnt_dst, any_edges, err_flag);
+  if (small)
+    k_step_mark<kAggSmallBlock, 1, kMarkSmallLog2><<<grid, kAggSmallBlock, 0, stream>>>(
+        batch, num_nodes, cap, src, dst, ts, cursor, batch_start, node_bits, ts_slot, ws, wd, cnt_src, cnt_dst,
+        any_edges, err_flag);
+  else
+    k_step_mark<kAggBlock, kAggPer, kMarkLog2><<<grid, kAggBlock, 0, stream>>>(
+        batch, num_nodes, cap, src, dst, ts, cursor, batch_start, node_bits, ts_slot, ws, wd, cnt_src, cnt_dst,
+        any_edges, err_flag);
   SGL_CHECK_LAUNCH();
   k_step_scan<<<1, kScanBlock, 0, stream>>>(nwords, nwords + summary_words(num_nodes), node_bits, word_prefix,
                                             num_roots, num_roots64, batch, ts_slot, cursor, batch_start, ts_max,
                                             t_query, err_flag);
   SGL_CHECK_LAUNCH();
   if (batch > 0) {
-    k_step_index<<<grid, kAggBlock, 0, stream>>>(
-        batch, num_nodes, num_roots, src, dst, neg, ts, cursor != nullptr ? batch_start : nullptr, node_bits, word_prefix,
-        t_query, roots, root_ts,
-        ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
+    const int64_t *bs = cursor != nullptr ? batch_start : nullptr;
+    if (small)
+      k_step_index<kAggSmallBlock, 1, kIdxSmallLog2><<<grid, kAggSmallBlock, 0, stream>>>(
+          batch, num_nodes, num_roots, src, dst, neg, ts, bs, node_bits, word_prefix, t_query, roots, root_ts,
+          ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
+    else
+      k_step_index<kAggBlock, kAggPer, kIdxLog2><<<grid, kAggBlock, 0, stream>>>(
+          batch, num_nodes, num_roots, src, dst, neg, ts, bs, node_bits, word_prefix, t_query, roots, root_ts,
+          ridx_src, ridx_dst, ridx_neg, ws, wd, cnt_src, cnt_dst);
     SGL_CHECK_LAUNCH();
   }
   return SGL_OK;

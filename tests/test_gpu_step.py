@@ -169,11 +169,13 @@ def _small_batch(rng, n_nodes, B, sorted_ts=True):
                                                        (4096, True, False, False), (5000, False, False, False),
                                                        (600, False, True, False), (20000, True, True, False),
                                                        (20000, False, True, False), (600, False, False, True),
-                                                       (2048, True, True, True), (5000, False, False, True)])
+                                                       (2048, True, True, True), (5000, False, False, True),
+                                                       (100000, False, True, False)])
 def test_batch_prepare_matches_numpy(gpu, B, sorted_ts, skew, metrics):
     """Roots, root indices, query time, per-role counts and last writers (in
     stable timestamp order) against numpy: the one-workgroup path (B <= 2048)
-    and the multi-workgroup path, with sorted and unsorted timestamps; skewed
+    and the multi-workgroup path (256-event workgroups up to 65,536 events,
+    4,096-event ones above), with sorted and unsorted timestamps; skewed
     batches (Zipf 1.5 node ids: a few roots in most events, many in each
     wave, so the multi-workgroup path combines them per wave). With
     ``metrics`` the preparation carries the metrics of logits already in the
