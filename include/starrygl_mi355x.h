@@ -369,8 +369,8 @@ int sgl_edge_rows(int32_t D, int32_t F, int32_t T, int32_t fanout,
                   const int32_t *cnt, const int32_t *nbr, const int32_t *eid,
                   float *X, hipStream_t stream);
 /* Roots per attention workgroup of the fp32 and dropout instances for these
- * dimensions (4 or 8; a divisor of 16); 0 if the dimensions are
- * unsupported. */
+ * dimensions (4, or 8 where the 4-root layouts of the 8-wave instances do
+ * not fit in LDS; a divisor of 16); 0 if the dimensions are unsupported. */
 int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H);
 /* Roots per workgroup of the backward instance sgl_conv_backward runs for
  * these dimensions, with bf16 weight copies (bf16 != 0) or without: the row

@@ -55,6 +55,14 @@ constexpr int waves_for(int hm, int jm) { return hm * jm <= 6 || (hm == 2 && jm 
 // Roots per workgroup: 16 waves share 4 roots (4 waves a root, merged
 // through LDS); 8 waves take 8 roots (one wave each, no merge).
 constexpr int rows_for(int nw) { return nw == 16 ? 4 : 8; }
+// The fp32 and dropout instances take 4 roots with either wave count (the
+// 8-wave ones two waves a root, merged through LDS) where both 4-root
+// layouts fit in LDS (fp32_four_fits): a 16-row product tile of 4 roots costs
+// about what one of 8 does, and twice the workgroups share the step's roots
+// (config 1, 8 waves: forward 44.0 -> 37.8 us, backward 41.3 -> 33.9 us;
+// 2 roots 37.4 / 35.4). Wider shapes (config 5's 4 heads of 288 columns:
+// the merge partials need 184 KB) keep 8 roots, one wave each.
+constexpr int kFp32Rows = 4;
 
 struct Dims {
   int D, F, T, H, C, dh, k;
@@ -1296,18 +1304,33 @@ using FwdFn = decltype(&k_conv_fwd<1, 2, false>);
 using BwdFn = decltype(&k_conv_bwd<1, 2, false>);
 // bf16 instances whose whole-head arrays need the 8-wave instances'
 // registers split each root's heads over two waves of a 16-wave workgroup,
-// keeping the 8 roots per workgroup (the tile rows of sgl_conv_tile_rows).
+// keeping the 8 roots per workgroup of the 8-wave shape.
 // The fp32 products' registers do not leave room for it; the backward's
 // widest shape (4 heads, 8 column blocks) would spill over 200 bytes a lane
 // under the 16-wave register cap and keeps the 8-wave instance.
 constexpr bool split_heads(int hm, int jm) { return waves_for(hm, jm) == 8 && hm >= 2; }
 constexpr bool split_heads_bwd(int hm, int jm) { return split_heads(hm, jm) && hm * jm <= 24; }
+// fp32 and dropout instances: FwdPick / BwdPick (/ ...Drop) with kFp32Rows
+// roots, the ...Wide twins with the wave count's own rows (rows_for), taken
+// where fp32_four_fits says the 4-root layouts do not fit.
 template <int HM, int JM>
 struct FwdPick {
-  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<FwdFn> get() {
+    return {&k_conv_fwd<HM, JM, false, false, waves_for(HM, JM), kFp32Rows>, waves_for(HM, JM), kFp32Rows};
+  }
 };
 template <int HM, int JM>
 struct BwdPick {
+  static Instance<BwdFn> get() {
+    return {&k_conv_bwd<HM, JM, false, false, waves_for(HM, JM), kFp32Rows>, waves_for(HM, JM), kFp32Rows};
+  }
+};
+template <int HM, int JM>
+struct FwdPickWide {
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
+template <int HM, int JM>
+struct BwdPickWide {
   static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, false>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
 // the bf16-product instances (no dropout). The 16-wave forward takes one
@@ -1343,12 +1366,40 @@ struct BwdPickBf {
 // the dropout instances (masks, kept-weight sums)
 template <int HM, int JM>
 struct FwdPickDrop {
-  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+  static Instance<FwdFn> get() {
+    return {&k_conv_fwd<HM, JM, true, false, waves_for(HM, JM), kFp32Rows>, waves_for(HM, JM), kFp32Rows};
+  }
 };
 template <int HM, int JM>
 struct BwdPickDrop {
+  static Instance<BwdFn> get() {
+    return {&k_conv_bwd<HM, JM, true, false, waves_for(HM, JM), kFp32Rows>, waves_for(HM, JM), kFp32Rows};
+  }
+};
+template <int HM, int JM>
+struct FwdPickDropWide {
+  static Instance<FwdFn> get() { return {&k_conv_fwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
+};
+template <int HM, int JM>
+struct BwdPickDropWide {
   static Instance<BwdFn> get() { return {&k_conv_bwd<HM, JM, true>, waves_for(HM, JM), rows_for(waves_for(HM, JM))}; }
 };
+
+// Whether the fp32 / dropout instances of these dimensions take kFp32Rows
+// roots: always with 16 waves (their own rows), with 8 waves when the
+// forward's (time encodings not staged) and the backward's 4-root layouts,
+// two waves a root, fit in the CU's LDS. A function of (D, F, T, H) alone, so
+// the forward, the backward and sgl_conv_backward_tile_rows agree.
+bool fp32_four_fits(const Dims &d, int nw) {
+  if (nw == 16) return true;
+  const bool slices = nw / kFp32Rows > 1;
+  return sizeof(float) * fwd_lds_floats(d, nw, kFp32Rows, slices, 0) <= 160 * 1024 &&
+         sizeof(float) * bwd_lds_floats(d, nw, kFp32Rows, slices) <= 160 * 1024;
+}
+template <class Fn>
+Instance<Fn> fp32_or_wide(const Dims &d, Instance<Fn> four, Instance<Fn> (*wide)(const Dims &)) {
+  return four.fn == nullptr || fp32_four_fits(d, four.waves) ? four : wide(d);
+}
 
 // The bf16 weight copies' shapes (sgl_bf16_weights): every pointer set,
 // leading dimensions multiples of 8 and wide enough, rows 16-byte aligned.
@@ -1428,15 +1479,15 @@ extern "C" int sgl_dropout_masks(int64_t rows, int32_t fanout, int32_t H, int32_
 extern "C" int32_t sgl_conv_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H) {
   const Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, 0};
   if (check_dims(d) != SGL_OK) return 0;
-  int hm, jm;
-  instance_shape(d, hm, jm);
-  return rows_for(waves_for(hm, jm));
+  const auto inst = fp32_or_wide(d, pick_instance<BwdPick>(d), &pick_instance<BwdPickWide>);
+  return inst.fn != nullptr ? inst.rows : 0;
 }
 
 extern "C" int32_t sgl_conv_backward_tile_rows(int32_t D, int32_t F, int32_t T, int32_t H, int32_t bf16) {
   const Dims d{D, F, T, H, D + F + T, H > 0 ? D / H : 0, 0};
   if (check_dims(d) != SGL_OK) return 0;
-  const auto inst = bf16 ? pick_instance<BwdPickBf>(d) : pick_instance<BwdPick>(d);
+  const auto inst = bf16 ? pick_instance<BwdPickBf>(d)
+                         : fp32_or_wide(d, pick_instance<BwdPick>(d), &pick_instance<BwdPickWide>);
   return inst.fn != nullptr ? inst.rows : 0;
 }
 
@@ -1490,7 +1541,8 @@ extern "C" int sgl_conv_forward(int32_t D, int32_t F, int32_t T, int32_t H, int3
                   y && (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_forward: NULL array");
   const auto inst = bw != nullptr ? pick_instance<FwdPickBf>(d)
-                    : drop ? pick_instance<FwdPickDrop>(d) : pick_instance<FwdPick>(d);
+                    : drop ? fp32_or_wide(d, pick_instance<FwdPickDrop>(d), &pick_instance<FwdPickDropWide>)
+                           : fp32_or_wide(d, pick_instance<FwdPick>(d), &pick_instance<FwdPickWide>);
   SGL_REQUIRE(inst.fn != nullptr, "conv_forward: no kernel instance for H=%d C=%d", H, d.C);
   // stage the tile's time encodings in LDS when they fit
   const bool slices = inst.waves / inst.rows / inst.hg > 1;
@@ -1541,7 +1593,8 @@ extern "C" int sgl_conv_backward(int32_t D, int32_t F, int32_t T, int32_t H, int
                   (fanout == 0 || (X && dt && sv_score && (T == 0 || S))),
               "conv_backward: NULL array");
   const auto inst = bw != nullptr ? pick_instance<BwdPickBf>(d)
-                    : drop ? pick_instance<BwdPickDrop>(d) : pick_instance<BwdPick>(d);
+                    : drop ? fp32_or_wide(d, pick_instance<BwdPickDrop>(d), &pick_instance<BwdPickDropWide>)
+                           : fp32_or_wide(d, pick_instance<BwdPick>(d), &pick_instance<BwdPickWide>);
   SGL_REQUIRE(inst.fn != nullptr, "conv_backward: no kernel instance for H=%d C=%d", H, d.C);
   // one ln_part / te_part tile per workgroup: the caller sized them by
   // sgl_conv_backward_tile_rows (the dropout instances' rows are the fp32 ones)
