@@ -337,15 +337,20 @@ __global__ __launch_bounds__(kB) void k_step_index(
 // One-workgroup batch preparation for batches of up to kPrepMaxBatch events.
 // The node bitmap gives the roots in ascending order without a sort. Marking
 // also sets a summary bitmap (bit w: word w of the node bitmap is nonzero),
-// so the popcount prefix only visits the nonzero words: scan the summary,
-// popcount the flagged words, block-scan, and rank(n) = prefix[n / 32] +
-// popc(word & below(n)). Per-(root, role) counts and last writers are LDS
+// so on large graphs the popcount prefix only visits the nonzero words: scan
+// the summary, popcount the flagged words, block-scan, and rank(n) =
+// prefix[n / 32] + popc(word & below(n)); a bitmap of at most
+// kPrepDirectWords words is read whole instead, a few words per thread in
+// one round (configs 1 and 2: 289 words, where the summary walk left ten
+// threads each loading about 29 flagged words one after another). Per-(root, role) counts and last writers are LDS
 // atomics (64-bit max of order(ts) << 32 | e: the last event in stable
 // timestamp order); negatives need one bit test. The workgroup clears the
 // bits it set, leaving both bitmaps zero.
 constexpr int kPrepBlock = 1024;
 constexpr int kPrepMaxBatch = 2048;
 constexpr int kPrepPer = kPrepMaxBatch / kPrepBlock;
+constexpr int kPrepDirectPer = 4;  // bitmap words per thread of the direct prefix
+constexpr int64_t kPrepDirectWords = int64_t(kPrepDirectPer) * kPrepBlock;
 
 __host__ __device__ inline int64_t bitmap_words(int64_t num_nodes) { return ((num_nodes + 31) / 32 + 3) & ~int64_t(3); }
 __host__ __device__ inline int64_t summary_words(int64_t num_nodes) {
@@ -471,19 +476,36 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
   // trip of sampler.py:113 then bts_sampler.py:81 is exact for that value.
   const int64_t tq = batch > 0 ? (long long)truncf(mm) : 0;
 
-  // popcount prefix over the nonzero words, in word order: thread t owns
-  // summary words [s0, s0 + cs)
-  const int64_t nsum = (bitmap_words(num_nodes) + 31) / 32;
+  // popcount prefix over the nonzero words, in word order. A bitmap of at
+  // most kPrepDirectWords words (graphs up to 131,072 nodes): thread t owns
+  // words [t * per, t * per + per), all loaded in one round. Larger ones:
+  // thread t owns summary words [s0, s0 + cs) and visits the bitmap words
+  // they flag (a small graph's few summary words would leave a handful of
+  // threads each loading tens of flagged words one after another).
+  const int64_t nbw = bitmap_words(num_nodes);
+  const bool direct = nbw <= kPrepDirectWords;
+  const int per = int((nbw + kPrepBlock - 1) / kPrepBlock);  // <= kPrepDirectPer when direct
+  const int64_t nsum = (nbw + 31) / 32;
   const int64_t cs = (nsum + kPrepBlock - 1) / kPrepBlock;
   const int64_t s0 = int64_t(tid) * cs;
   const int64_t s1 = s0 + cs < nsum ? s0 + cs : nsum;
   int32_t cnt_here = 0;
-  for (int64_t sw = s0; sw < s1; ++sw) {
-    uint32_t f = summary[sw];
-    while (f != 0u) {
-      const int b = __ffs(f) - 1;
-      f &= f - 1u;
-      cnt_here += __popc(bits[(sw << 5) + b]);
+  uint32_t dw[kPrepDirectPer];
+  if (direct) {
+#pragma unroll
+    for (int q = 0; q < kPrepDirectPer; ++q) {
+      const int64_t w = int64_t(tid) * per + q;
+      dw[q] = q < per && w < nbw ? bits[w] : 0u;
+      cnt_here += __popc(dw[q]);
+    }
+  } else {
+    for (int64_t sw = s0; sw < s1; ++sw) {
+      uint32_t f = summary[sw];
+      while (f != 0u) {
+        const int b = __ffs(f) - 1;
+        f &= f - 1u;
+        cnt_here += __popc(bits[(sw << 5) + b]);
+      }
     }
   }
   int32_t U;
@@ -508,14 +530,25 @@ __global__ __launch_bounds__(kPrepBlock) void k_step_prepare_wg(
     }
     return;
   }
-  for (int64_t sw = s0; sw < s1; ++sw) {
-    uint32_t f = summary[sw];
-    while (f != 0u) {
-      const int b = __ffs(f) - 1;
-      f &= f - 1u;
-      const int64_t w = (sw << 5) + b;
-      prefix[w] = run;
-      run += __popc(bits[w]);
+  if (direct) {
+#pragma unroll
+    for (int q = 0; q < kPrepDirectPer; ++q) {
+      const int64_t w = int64_t(tid) * per + q;
+      if (q < per && w < nbw) {
+        prefix[w] = run;
+        run += __popc(dw[q]);
+      }
+    }
+  } else {
+    for (int64_t sw = s0; sw < s1; ++sw) {
+      uint32_t f = summary[sw];
+      while (f != 0u) {
+        const int b = __ffs(f) - 1;
+        f &= f - 1u;
+        const int64_t w = (sw << 5) + b;
+        prefix[w] = run;
+        run += __popc(bits[w]);
+      }
     }
   }
   __syncthreads();
