@@ -529,6 +529,58 @@ __device__ __forceinline__ f32x4 mfma_block16_bw_cls(const float *__restrict__ A
   return acc0 + acc1;
 }
 
+// mfma_block16_bw_cls for two A tiles against the same weight block: each
+// weight fragment is loaded once and feeds both tiles' products, which keep
+// the single-tile order (bit-identical to two separate calls).
+template <int CLS>
+__device__ __forceinline__ void mfma_block16_bw_pair_cls(const float *__restrict__ A0, const float *__restrict__ A1,
+                                                         int lda, __amdgpu_buffer_rsrc_t wr, uint32_t wrow, int kd,
+                                                         f32x4 &out0, f32x4 &out1) {
+  const int lane = threadIdx.x & 63;
+  const float *arow0 = A0 + (lane & 15) * lda;
+  const float *arow1 = A1 + (lane & 15) * lda;
+  const int q = lane >> 4;
+  const int nks = (kd + 31) >> 5;
+  constexpr int kU = 8;
+  f32x4 a00 = {0.f, 0.f, 0.f, 0.f}, a01 = a00, a10 = a00, a11 = a00;
+  for (int ks0 = 0; ks0 < nks; ks0 += kU) {
+    bf16x8 b[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (ks0 + u >= nks) break;  // uniform
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(wr, int((wrow + 32u * uint32_t(ks0 + u)) * 2u), 0, 0);
+      b[u] = __builtin_bit_cast(bf16x8, v);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (ks0 + u >= nks) break;
+      const bf16x8 x0 = load_a_bf16<CLS>(arow0, 32 * (ks0 + u) + 8 * q, kd);
+      const bf16x8 x1 = load_a_bf16<CLS>(arow1, 32 * (ks0 + u) + 8 * q, kd);
+      if (u & 1) {
+        a01 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b[u], a01, 0, 0, 0);
+        a11 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b[u], a11, 0, 0, 0);
+      } else {
+        a00 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, b[u], a00, 0, 0, 0);
+        a10 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, b[u], a10, 0, 0, 0);
+      }
+    }
+  }
+  out0 = a00 + a01;
+  out1 = a10 + a11;
+}
+
+// The pair product of mfma_block16_bw's block (A0, A1 aligned as CLS 2: rows
+// 16-byte aligned, lda % 4 == 0).
+__device__ __forceinline__ void mfma_block16_bw_pair(const float *__restrict__ A0, const float *__restrict__ A1,
+                                                     int lda, const uint16_t *__restrict__ W, int ldw, int n0, int kd,
+                                                     int n_total, f32x4 &out0, f32x4 &out1) {
+  const int lane = threadIdx.x & 63;
+  const int n = min(n0 + (lane & 15), n_total - 1);
+  const __amdgpu_buffer_rsrc_t wr = bf16_weight_rsrc(W, uint32_t(n_total) * uint32_t(ldw));
+  const uint32_t wrow = uint32_t(n) * uint32_t(ldw) + 8u * uint32_t(lane >> 4);
+  mfma_block16_bw_pair_cls<2>(A0, A1, lda, wr, wrow, kd, out0, out1);
+}
+
 // One 16x16 output block (rows 0..15 of A, columns n0..n0+15 of W^T); this
 // lane's accumulators are rows 4*(lane/16)+v, column n0 + lane%16. Columns
 // past n_total read row n_total-1 (their outputs are discarded). CLS >= 0

@@ -189,8 +189,8 @@ __global__ __launch_bounds__(kBlock) void k_predictor(
       } else {
         sgl::f32x4 ad, an;
         if constexpr (BF) {
-          ad = sgl::mfma_block16_bw<2>(Ed, ld, bw.wd, bw.ld_d, n0, D, D);
-          an = sgl::mfma_block16_bw<2>(En, ld, bw.wd, bw.ld_d, n0, D, D);
+          // the block's W_d fragments loaded once for both tiles
+          sgl::mfma_block16_bw_pair(Ed, En, ld, bw.wd, bw.ld_d, n0, D, D, ad, an);
         } else {
           sgl::mfma_block16_pair<sgl::kNT>(Ed, En, ld, w_d, D, n0, D, D, ad, an);
         }
