@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SGL_ABI_VERSION 21
+#define SGL_ABI_VERSION 22
 
 #define SGL_OK 0
 #define SGL_ERR_INVALID 1   /* bad argument (host-checked) */
@@ -610,7 +610,12 @@ int sgl_adam_advance(float *step, const int32_t *active, hipStream_t stream);
  * once. Workgroup t runs on XCD t % 8, so the table decides which XCD's L2
  * fetches a job's activation strips: starry_unigraph.native.step.xcd_tile_deal
  * gives each job's tiles to one XCD where the per-XCD share allows. The
- * jobs' tile0 field is not read.
+ * jobs' tile0 field is not read then. With tile_job NULL, jobs holds
+ * num_tiles entries instead, one per workgroup: a copy of the workgroup's job
+ * with tile0 the tile's index l within it, or kind -1 for an empty slot
+ * (starry_unigraph.native.step.per_workgroup_jobs builds it from the same
+ * deal; the workgroup then loads its job in one round trip instead of two).
+ * sgl_grad_shadows reads either form the same way.
  * Each gradient element is written once, then Adam-updated (torch.optim.Adam
  * arithmetic) if its segment `seg` is active: gates[seg] NULL or
  * *gates[seg] != 0, with the bias corrections coef[2*seg] = lr / (1 -

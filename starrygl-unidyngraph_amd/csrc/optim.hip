@@ -105,6 +105,24 @@ struct AdamSegs {
 __device__ __forceinline__ int tile_entry_job(int32_t e) { return e & 0xFF; }
 __device__ __forceinline__ int tile_entry_local(int32_t e) { return e >> 8; }
 
+// Workgroup blockIdx.x's job and tile (false: a padding slot, nothing to do;
+// uniform). With tile_job, its entry names the job and the tile; without,
+// jobs holds one copy per workgroup with the tile's index in tile0 (kind < 0
+// marks padding), which takes the entry's load off the front of the chain.
+__device__ __forceinline__ bool workgroup_tile(const sgl_grad_job *__restrict__ jobs,
+                                               const int32_t *__restrict__ tile_job, sgl_grad_job &jb, int &local) {
+  if (tile_job != nullptr) {
+    const int32_t entry = tile_job[blockIdx.x];
+    if (entry < 0) return false;
+    jb = jobs[tile_entry_job(entry)];
+    local = tile_entry_local(entry);
+    return true;
+  }
+  jb = jobs[blockIdx.x];
+  local = jb.tile0;
+  return jb.kind >= 0;
+}
+
 // The reduction length of a kind-0 job: r_fixed; *num_roots + r_extra when
 // r_fixed == -1; the tiles of -r_fixed rows that hold live rows when
 // r_fixed <= -2 (per-tile partial sums; the rest are zero).
@@ -123,10 +141,9 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_adam(const sgl_grad_job *__re
                                                        float wd, uint16_t *__restrict__ shadow) {
   __shared__ float red[4][16][17];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int32_t entry = tile_job[blockIdx.x];
-  if (entry < 0) return;  // uniform: a padding slot of the XCD deal
-  const sgl_grad_job jb = jobs[tile_entry_job(entry)];
-  const int local = tile_entry_local(entry);
+  sgl_grad_job jb;
+  int local;
+  if (!workgroup_tile(jobs, tile_job, jb, local)) return;  // uniform: a padding slot of the XCD deal
   const bool active = segs.gate[jb.seg] == nullptr || *segs.gate[jb.seg] != 0;
   const float step_size = coef[2 * jb.seg], bc2_sqrt = coef[2 * jb.seg + 1];
 
@@ -213,11 +230,10 @@ __global__ __launch_bounds__(kGaBlock) void k_grad_shadows(const sgl_grad_job *_
                                                           const int32_t *__restrict__ tile_job,
                                                           const float *__restrict__ p,
                                                           uint16_t *__restrict__ shadow) {
-  const int32_t entry = tile_job[blockIdx.x];
-  if (entry < 0) return;
-  const sgl_grad_job jb = jobs[tile_entry_job(entry)];
+  sgl_grad_job jb;
+  int local;
+  if (!workgroup_tile(jobs, tile_job, jb, local)) return;
   if (jb.kind != 0 || (jb.sh_off < 0 && jb.sht_off < 0)) return;
-  const int local = tile_entry_local(entry);
   const int ta = local / jb.tiles_b, tb = local - (local / jb.tiles_b) * jb.tiles_b;
   const int ea = 16 * ta + (threadIdx.x >> 4), eb = 16 * tb + (threadIdx.x & 15);
   if (ea >= jb.rows || eb >= jb.cols) return;
@@ -291,7 +307,7 @@ extern "C" int sgl_grad_adam(const sgl_grad_job *jobs, const int32_t *tile_job, 
   SGL_REQUIRE(num_tiles >= 0, "grad_adam: num_tiles < 0");
   SGL_REQUIRE(nseg > 0 && nseg <= SGL_MAX_ADAM_SEGMENTS, "grad_adam: nseg %d out of range", nseg);
   if (num_tiles == 0) return SGL_OK;
-  SGL_REQUIRE(jobs && tile_job && param && grad && exp_avg && exp_avg_sq && coef, "grad_adam: NULL array");
+  SGL_REQUIRE(jobs && param && grad && exp_avg && exp_avg_sq && coef, "grad_adam: NULL array");
   sgl::launch(&k_grad_adam, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, num_roots, param,
               grad, exp_avg, exp_avg_sq, make_segs(nseg, nullptr, gates), coef, beta1, beta2, eps, weight_decay,
               shadow);
@@ -303,7 +319,7 @@ extern "C" int sgl_grad_shadows(const sgl_grad_job *jobs, const int32_t *tile_jo
                                 const float *param, uint16_t *shadow, hipStream_t stream) {
   SGL_REQUIRE(num_tiles >= 0, "grad_shadows: num_tiles < 0");
   if (num_tiles == 0) return SGL_OK;
-  SGL_REQUIRE(jobs && tile_job && param && shadow, "grad_shadows: NULL array");
+  SGL_REQUIRE(jobs && param && shadow, "grad_shadows: NULL array");
   sgl::launch(&k_grad_shadows, dim3(unsigned(num_tiles)), dim3(kGaBlock), 0, stream, jobs, tile_job, param, shadow);
   SGL_CHECK_LAUNCH();
   return SGL_OK;

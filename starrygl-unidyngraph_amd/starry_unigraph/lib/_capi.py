@@ -17,7 +17,7 @@ import torch  # loads the HIP runtime first, so the library binds to the same on
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libstarrygl_mi355x.so"
 LIB_PATH = os.path.join(_HERE, LIB_NAME)
-ABI_VERSION = 21
+ABI_VERSION = 22
 
 SGL_DERR_NODE_RANGE = 1
 SGL_DERR_EID_RANGE = 2

@@ -34,6 +34,23 @@ def _round_up(x: int, m: int) -> int:
     return (x + m - 1) // m * m
 
 
+def per_workgroup_jobs(jobs: list, deal: list[int]) -> list:
+    """sgl_grad_adam's job table without tile_job: one copy of its job per
+    entry of ``deal`` (xcd_tile_deal), the tile's index within the job in
+    tile0, and a job of kind -1 for a padding slot (workgroup t reads entry t,
+    one load where the indexed form takes two in a row)."""
+    out = []
+    for e in deal:
+        if e < 0:
+            j = _capi.GradJob()
+            j.kind = -1
+        else:
+            j = _capi.GradJob.from_buffer_copy(jobs[e & 0xFF])
+            j.tile0 = e >> 8
+        out.append(j)
+    return out
+
+
 def xcd_tile_deal(counts: list[int], xcds: int = 8) -> list[int]:
     """The tile_job table of sgl_grad_adam / sgl_grad_shadows for jobs of
     ``counts`` tiles: entry t (workgroup t, which runs on XCD t % xcds) is
@@ -658,11 +675,12 @@ class StepParamUpdate:
         self.one = torch.ones(1, dtype=torch.float32, device=dev)
         self.coef = torch.zeros(2 * len(opt.segments), dtype=torch.float32, device=dev)
         jobs, tiles = self._jobs(conv_params, pred_params)
-        arr = (_capi.GradJob * len(jobs))(*jobs)
+        deal = xcd_tile_deal([tiles.count(k) for k in range(len(jobs))])
+        # one job copy per workgroup (no tile_job table: one load less at the
+        # front of every workgroup's chain)
+        arr = (_capi.GradJob * len(deal))(*per_workgroup_jobs(jobs, deal))
         raw = torch.frombuffer(bytearray(bytes(arr)), dtype=torch.uint8)
         self.jobs = raw.to(dev)
-        deal = xcd_tile_deal([tiles.count(k) for k in range(len(jobs))])
-        self.tile_job = torch.as_tensor(deal, dtype=torch.int32, device=dev)
         self.num_tiles = len(deal)
         P = _capi.ptr
         self._steps = (ctypes.c_void_p * len(opt.segments))(*[P(seg[2]) for seg in opt.segments])
@@ -803,7 +821,7 @@ class StepParamUpdate:
         opt, P, s = self.opt, _capi.ptr, _capi.stream_of(self.opt.flat.device)
         b1, b2 = opt.betas
         self.step._call("param_update", lambda: _capi.check(_capi.call(
-            "sgl_grad_adam", P(self.jobs), P(self.tile_job), self.num_tiles, P(self.step.buf.num_roots),
+            "sgl_grad_adam", P(self.jobs), None, self.num_tiles, P(self.step.buf.num_roots),
             P(opt.flat), P(opt.flat_grad), P(opt.exp_avg), P(opt.exp_avg_sq), len(opt.segments), self._gates,
             P(self.coef), b1, b2, opt.eps, opt.wd, P(self.shadow.buf) if self.shadow is not None else None, s),
             "sgl_grad_adam"))

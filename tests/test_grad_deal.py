@@ -6,7 +6,7 @@ import random
 
 import pytest
 
-from starry_unigraph.native.step import xcd_tile_deal
+from starry_unigraph.native.step import per_workgroup_jobs, xcd_tile_deal
 
 
 def _decode(table):
@@ -66,3 +66,30 @@ def test_limits():
     assert xcd_tile_deal([]) == [] and xcd_tile_deal([0, 0]) == []
     with pytest.raises(ValueError):
         xcd_tile_deal([1] * 257)
+
+
+def test_per_workgroup_jobs_match_the_deal():
+    """sgl_grad_adam's table without tile_job: workgroup t's entry is a copy
+    of the job the deal's entry t names, tile0 = the tile's index within it,
+    kind -1 for a padding slot; the other fields are the job's."""
+    from starry_unigraph.lib import _capi
+    counts = [7, 0, 49, 3, 56, 1]
+    jobs = []
+    for k, c in enumerate(counts):
+        j = _capi.GradJob()
+        j.kind = k % 2
+        j.rows, j.cols, j.seg, j.r_fixed, j.off = 16 * c + 1, 3 + k, k % 3, -k, 1000 * k
+        j.tile0 = 12345   # replaced in the copies
+        jobs.append(j)
+    deal = xcd_tile_deal(counts)
+    table = per_workgroup_jobs(jobs, deal)
+    assert len(table) == len(deal)
+    for e, t in zip(deal, table):
+        if e < 0:
+            assert t.kind == -1
+            continue
+        src = jobs[e & 0xFF]
+        assert t.tile0 == e >> 8
+        for f in ("kind", "rows", "cols", "seg", "r_fixed", "off"):
+            assert getattr(t, f) == getattr(src, f), f
+    assert jobs[0].tile0 == 12345   # the source jobs are not modified
