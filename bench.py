@@ -638,7 +638,7 @@ def run_tgn(args, wl: dict) -> dict:
     for b in batches:
         out = rt.train_step(b)
     host = time.perf_counter() - w0
-    # the host blocks only when it runs a full draw ring (32 steps) ahead of the GPU
+    # the host blocks only when it runs a full draw ring (four chunks of draws) ahead of the GPU
     waited = rt._draws.wait_s - waited0
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0

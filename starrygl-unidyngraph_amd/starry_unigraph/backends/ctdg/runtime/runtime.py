@@ -53,6 +53,7 @@ class StepTensors:
 
 class CTDGOnlineRuntime:
     kDrawRing = 4   # pinned staging buffers of the negative draws
+    kDrawChunkNumbers = 1 << 17   # draws per chunk at most (1 MB of int64 per staging buffer)
 
     def __init__(self, dataset: TGTemporalDataset, sampler: NativeTemporalSampler, memory: CTDGMemoryBank,
                  model: torch.nn.Module, optimizer, route: Any, device: str, dist_ctx: Any,
@@ -84,11 +85,14 @@ class CTDGOnlineRuntime:
         self._dst_node_pool: torch.Tensor | None = None
         self._neg_queue: dict[str, tuple[torch.Tensor, int]] = {}
         # negatives are drawn inside the step, for neg_chunk consecutive
-        # batches of a contiguous split at a time (1: one draw per step),
+        # batches of a contiguous split at a time (1: one draw per step; at
+        # most kDrawChunkNumbers numbers a chunk, so large batches take fewer),
         # into a ring of kDrawRing pinned staging buffers (the host waits only
         # for the lookup out of a buffer it filled that many draws ago); the
-        # schedule keeps the generator where per-step draws would leave it
-        self.neg_chunk = 8
+        # schedule keeps the generator where per-step draws would leave it.
+        # A chunk boundary costs the host a lookup launch and the next chunk's
+        # set-up (≈20-40 us), so longer chunks spread it over more steps
+        self.neg_chunk = 32
         self._draws = ChunkedDraws(lambda: self._dst_pool().numel(), self._split_end, self._alloc_draw_slot,
                                    self._lookup, chunk=self.neg_chunk, ring=self.kDrawRing)
         self._pool_dev: torch.Tensor | None = None
@@ -320,7 +324,7 @@ class CTDGOnlineRuntime:
             del self._neg_queue[batch.split]
         s, n = batch.start, batch.size
         if s >= 0 and self.neg_chunk > 1:
-            self._draws.chunk = self.neg_chunk
+            self._draws.chunk = max(1, min(self.neg_chunk, self.kDrawChunkNumbers // max(n, 1)))
             self._draws.serve(batch.split, s, n)
             return self._neg_all, s
         return self._negative_sample(batch).to(self.device, non_blocking=True), -1
