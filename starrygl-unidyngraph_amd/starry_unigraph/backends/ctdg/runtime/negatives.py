@@ -41,9 +41,14 @@ class DrawSlot:
     def view(self, at: int, k: int) -> torch.Tensor:
         v = self.views.get((at, k))
         if v is None:
-            if len(self.views) >= 64:   # batch sizes that keep changing
+            if len(self.views) >= 256:   # batch sizes that keep changing
                 self.views.clear()
-            v = self.views[(at, k)] = self.buf[at:at + k]
+            if at % k == 0:   # every batch-aligned view of the buffer at once, at its first use
+                for a in range(0, self.buf.numel() - k + 1, k):
+                    self.views[(a, k)] = self.buf[a:a + k]
+            v = self.views.get((at, k))
+            if v is None:
+                v = self.views[(at, k)] = self.buf[at:at + k]
         return v
 
     def wait(self) -> None:
